@@ -1,0 +1,261 @@
+"""MoE-layer forward benchmark on one MI355X.
+
+Default workload: Mixtral-8x7B-shaped single MoE layer,
+d=4096, expert hidden 14336, 8 gated silu experts, top-2, 4096 tokens, bf16
+weights ~N(0, 0.02), activations ~N(0, 1), fp32 router ~N(0, 0.02) plus a
+per-expert logit bias ~N(0, 1).  Inputs and weights are generated on the GPU
+and are resident in HBM before the timed region.
+
+One step = one MoE-layer forward over the 4096-token batch, issued as its five
+stages (router, permute, expert up GEMM, expert down GEMM, combine) with HIP
+events between them on the launch stream, so the per-kernel times come from
+the timed region itself.  Prints one JSON line.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "MoE-layer tokens/s at 1 GPU, Mixtral-8x7B shape; % of MFMA/HBM roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+CONFIGS = {
+    # name: T, D, H, E, k, gate, shared, expert type, activation, weight dtype
+    "mixtral": dict(T=4096, D=4096, H=14336, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="bf16",
+                    workload="mixtral-8x7b-moe-layer"),
+    "deepseek": dict(T=8192, D=2048, H=1408, E=66, k=6, gate="shared", ns=2, etype="gated", act="silu", w="fp8",
+                     workload="deepseek-fine-grained-moe-layer"),
+    "switch": dict(T=16384, D=768, H=3072, E=128, k=1, gate="switch", ns=0, etype="standard", act="gelu", w="bf16",
+                   workload="switch-k1-moe-layer"),
+    "readme": dict(T=32, D=512, H=2048, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="f32",
+                   workload="readme-moe-layer"),
+}
+
+
+def build_workload(cfg, seed=1234):
+    import numpy as np
+    import torch
+
+    from mixtureofexperts_amd import _lib
+    from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+    T, D, H, E, k = cfg["T"], cfg["D"], cfg["H"], cfg["E"], cfg["k"]
+    kt = k + cfg["ns"]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    dev_bf16 = cfg["w"] != "f32"
+    spec = {"topk": GateSpec(_lib.MOE_GATE_TOPK, k, 0), "switch": GateSpec(_lib.MOE_GATE_SWITCH, 1, 0),
+            "shared": GateSpec(_lib.MOE_GATE_SHARED, k, cfg["ns"])}[cfg["gate"]]
+    wcode = {"f32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3}[cfg["w"]]
+    gated = cfg["etype"] == "gated"
+    layer = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED if gated else _lib.MOE_EXPERT_STANDARD,
+                        input_dim=D, hidden_dim=H, output_dim=D,
+                        activation=_lib.MOE_ACT_SILU if cfg["act"] == "silu" else _lib.MOE_ACT_GELU, gate=spec,
+                        weight_dtype=wcode, balance_alpha=0.01, z_loss_weight=0.001, capacity_factor=1.25,
+                        drop_tokens=False, max_tokens=T)
+    xdt = torch.bfloat16 if dev_bf16 else torch.float32
+    x = torch.randn(T, D, generator=gen, device="cuda").to(xdt)
+    if cfg["workload"].startswith("mixtral"):
+        wr = torch.randn(E, D, generator=gen, device="cuda") * 0.02
+        rbias = torch.randn(E, generator=gen, device="cuda")
+    elif cfg["workload"].startswith("deepseek"):
+        wr = torch.randn(E, D, generator=gen, device="cuda") * 0.02
+        r = torch.arange(1, E - cfg["ns"] + 1, device="cuda", dtype=torch.float32)
+        rbias = torch.cat([torch.zeros(cfg["ns"], device="cuda"), -1.1 * torch.log(r)])  # Zipf(1.1) routed load
+    else:
+        wr = torch.randn(E, D, generator=gen, device="cuda") / (D ** 0.5)  # logits ~ N(0, 1)
+        rbias = None
+    wr_mem = wr.t().contiguous()  # Flux (E, D) weight memory = [D][E]
+    _lib.check(_lib.lib().moe_set_router(layer.h, wr_mem.data_ptr(), None if rbias is None else rbias.data_ptr()),
+               layer.h)
+    host_w = []
+    wsrc = _lib.MOE_BF16 if dev_bf16 else _lib.MOE_F32
+    std = 0.02 if dev_bf16 else (2.0 / D) ** 0.5
+    for e in range(E):
+        mats = []
+        shapes = [(H, D), (D, H), (H, D)] if gated else [(H, D), (D, H)]
+        for shp in shapes:
+            w = (torch.randn(*shp, generator=gen, device="cuda") * std).to(torch.bfloat16 if dev_bf16 else torch.float32)
+            mats.append(w.contiguous())
+        b1 = b2 = None
+        if not gated:
+            b1 = (torch.randn(H, generator=gen, device="cuda") * 0.02).contiguous()
+            b2 = (torch.randn(D, generator=gen, device="cuda") * 0.02).contiguous()
+        w1, w2 = mats[0], mats[1]
+        w3 = mats[2] if gated else None
+        _lib.check(_lib.lib().moe_set_expert(layer.h, e, _lib.MOE_LAYOUT_LLAMA_IN_OUT, wsrc, w1.data_ptr(),
+                                             w2.data_ptr(), None if w3 is None else w3.data_ptr(),
+                                             None if b1 is None else b1.data_ptr(),
+                                             None if b2 is None else b2.data_ptr(), None, None, None), layer.h)
+        host_w.append(dict(w1=w1, w2=w2, w3=w3, b1=b1, b2=b2))
+    torch.cuda.synchronize()
+    out = torch.empty(T, D, dtype=torch.float32, device="cuda")
+    loss = torch.zeros(1, dtype=torch.float32, device="cuda")
+    return dict(layer=layer, x=x, xcode=_lib.MOE_BF16 if dev_bf16 else _lib.MOE_F32, out=out, loss=loss, wr=wr,
+                rbias=rbias, weights=host_w, kt=kt)
+
+
+def cpu_baseline(cfg, wl, sample_tokens):
+    """Time the oracle (CPU restatement of the reference path: fp32 router,
+    softmax/top-k, per-expert gather + 3 OpenBLAS sgemm, scatter-add in
+    expert order, Switch + z loss) on the first `sample_tokens` tokens of the
+    same workload, weights dequantised to fp32."""
+    import numpy as np
+    import torch
+
+    from oracle import moe_oracle as oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("internal_api") == "openblas"]
+                      or [os.cpu_count() or 1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    S = min(sample_tokens, cfg["T"])
+    x = wl["x"][:S].float().cpu().numpy()
+    wr = wl["wr"].float().cpu().numpy()
+    rb = None if wl["rbias"] is None else wl["rbias"].float().cpu().numpy()
+    ex = []
+    for w in wl["weights"]:
+        ex.append({k: (None if v is None else v.float().cpu().numpy()) for k, v in w.items()})
+    logits = (x @ wr.T).astype(np.float32)
+    if rb is not None:
+        logits = (logits + rb).astype(np.float32)
+    kwargs = dict(gate=cfg["gate"], k=cfg["k"], num_shared=cfg["ns"], expert_type=cfg["etype"], act=cfg["act"],
+                  training=True)
+    oracle.moe_forward(x[: min(8, S)], wr, ex, router_bias=rb, **kwargs)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.moe_forward(x, wr, ex, router_bias=rb, **kwargs)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": S / t, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"first {S} of {cfg['T']} tokens of the same workload, full layer forward (router GEMM, "
+                      f"gating, per-expert OpenBLAS sgemm FFN on fp32-dequantised weights, combine, losses); "
+                      f"median of 3 runs, {t:.2f} s each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="mixtral", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-sample", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from mixtureofexperts_amd import _lib
+
+    cfg = CONFIGS[args.config]
+    T, D, H, E, k = cfg["T"], cfg["D"], cfg["H"], cfg["E"], cfg["k"]
+    wl = build_workload(cfg)
+    L = _lib.lib()
+    h = wl["layer"].h
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    xp, op, lp = wl["x"].data_ptr(), wl["out"].data_ptr(), wl["loss"].data_ptr()
+    xcode = wl["xcode"]
+
+    def forward():
+        _lib.check(L.moe_forward_async(h, xp, xcode, T, 1, op, lp, sp), h)
+
+    stage_names = ["router", "permute", "expert_up", "expert_down", "combine"]
+
+    def staged(ev):
+        ev[0].record(stream)
+        _lib.check(L.moe_stage_router_async(h, xp, xcode, T, 1, sp), h)
+        ev[1].record(stream)
+        _lib.check(L.moe_stage_permute_async(h, xp, xcode, T, sp), h)
+        ev[2].record(stream)
+        _lib.check(L.moe_stage_expert_up_async(h, T, sp), h)
+        ev[3].record(stream)
+        _lib.check(L.moe_stage_expert_down_async(h, T, sp), h)
+        ev[4].record(stream)
+        _lib.check(L.moe_stage_combine_async(h, T, op, sp), h)
+        ev[5].record(stream)
+
+    for _ in range(max(1, args.warmup)):
+        forward()
+    torch.cuda.synchronize()
+    counts = np.zeros(E, np.int32)
+    _lib.check(L.moe_read_counts(h, counts.ctypes.data), h)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        staged(events[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stage_ms = {n: float(np.mean([ev[j].elapsed_time(ev[j + 1]) for ev in events])) for j, n in enumerate(stage_names)}
+    assert bool(torch.isfinite(wl["out"]).all()), "non-finite output"
+
+    ms_step = elapsed * 1000.0 / args.steps
+    tokens_s = T * args.steps / elapsed
+    kt = wl["kt"]
+    rows = T * kt
+    gated = cfg["etype"] == "gated"
+    up_flops = (4 if gated else 2) * rows * D * H
+    down_flops = 2 * rows * D * H
+    peak = PEAK_F32_TFLOPS if cfg["w"] == "f32" else PEAK_BF16_TFLOPS
+    up_tflops = up_flops / (stage_ms["expert_up"] * 1e-3) / 1e12
+    down_tflops = down_flops / (stage_ms["expert_down"] * 1e-3) / 1e12
+    xs = 2 if cfg["w"] != "f32" else 4
+    # algorithmic HBM bytes of the memory-bound stages (per launch)
+    router_bytes = T * D * xs + E * D * 4 + T * E * 4 * 2 + T * kt * (4 + 4 + 4)
+    permute_bytes = T * D * xs + rows * D * xs + rows * 16
+    combine_bytes = rows * D * 4 + T * D * 4 + T * kt * 12
+    gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg["w"] != "f32" else "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "tokens": T, "d_model": D, "d_expert_hidden": H, "experts": E,
+                   "top_k": k, "shared_experts": cfg["ns"], "expert_type": cfg["etype"], "activation": cfg["act"],
+                   "weights": cfg["w"], "output": "f32"},
+        "tflops": round((up_flops + down_flops) / (ms_step * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_kernel (expert up: gate+up GEMM, silu*mul epilogue)",
+                     "achieved": round(up_tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(up_tflops / peak, 4), "traffic": None},
+        "stages": {
+            "router": {"ms": round(stage_ms["router"], 4), "GB/s": round(gbs(router_bytes, stage_ms["router"]), 1)},
+            "permute": {"ms": round(stage_ms["permute"], 4), "GB/s": round(gbs(permute_bytes, stage_ms["permute"]), 1)},
+            "expert_up": {"ms": round(stage_ms["expert_up"], 4), "TFLOP/s": round(up_tflops, 1)},
+            "expert_down": {"ms": round(stage_ms["expert_down"], 4), "TFLOP/s": round(down_tflops, 1)},
+            "combine": {"ms": round(stage_ms["combine"], 4), "GB/s": round(gbs(combine_bytes, stage_ms["combine"]), 1)},
+        },
+        "expert_counts": counts.tolist(),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, wl, args.cpu_sample)
+    print(json.dumps(line), flush=True)
+    wl["layer"].close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,199 @@
+/*
+ * moe_mi355x.h -- C ABI of libmoe_mi355x.so, the MI355X (gfx950) MoE-layer
+ * forward path behind MixtureOfExperts.jl's API.
+ *
+ * The reference has no FFI boundary; its seams are Julia multiple-dispatch
+ * points.  Each entry point below names the reference function it replaces
+ * (paths relative to the MixtureOfExperts.jl repository).  A host shim (Julia
+ * via ccall, Python via ctypes) keeps the reference API and calls these.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  Every array is dense and row-major in the
+ *    token-major order that Julia's column-major matrices already have:
+ *    a Julia matrix of size (D, T) is passed as its own memory, [T][D].
+ *  - Expert ids are 1-based, as in the reference; 0 marks an entry dropped by
+ *    the capacity constraint.  Entry ids are 0-based: entry = t*k + slot.
+ *    Positions, counts and offsets are 0-based.
+ *  - Every function returns a moe_status; on failure moe_last_error() holds a
+ *    message.  Host-pointer entry points block until results are in host
+ *    memory.  *_async entry points take device pointers and a hipStream_t
+ *    (passed as void*, NULL = the handle's own stream) and only enqueue.
+ *  - Calls on one handle are serialised by the library; distinct handles may
+ *    be used from distinct threads.
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_ABI_VERSION 1
+#define MOE_MAX_TOPK 8        /* maximum slots per token (shared + routed) */
+#define MOE_MAX_EXPERTS 128   /* maximum experts seen by one router */
+
+typedef enum {
+    MOE_OK = 0,
+    MOE_EINVAL = -1,       /* bad argument (shape, range, null pointer) */
+    MOE_EOOM = -2,         /* device allocation failed */
+    MOE_EHIP = -3,         /* a HIP runtime call failed */
+    MOE_ENOTREADY = -4,    /* router or an expert has no weights yet */
+    MOE_EUNSUPPORTED = -5  /* valid in the reference, not implemented here */
+} moe_status;
+
+typedef enum { MOE_F32 = 0, MOE_BF16 = 1, MOE_FP8_E4M3 = 2 } moe_dtype;
+
+/* Memory order of a weight matrix as the reference holds it.
+ * FLUX_OUT_IN: Flux Dense weight of size (out, in), column-major, i.e. memory
+ *              [in][out] (src/experts/gated.jl:15-27, src/core/router.jl:18).
+ * LLAMA_IN_OUT: Llama2 weight of size (in, out), column-major, i.e. memory
+ *              [out][in] (src/llama2/types.jl:207-210). */
+typedef enum { MOE_LAYOUT_FLUX_OUT_IN = 0, MOE_LAYOUT_LLAMA_IN_OUT = 1 } moe_layout;
+
+typedef enum { MOE_EXPERT_GATED = 0, MOE_EXPERT_STANDARD = 1 } moe_expert_type;
+
+/* Elementwise activation of the expert FFN (MoEConfig.activation,
+ * src/core/moe_layer.jl:10).  GELU is NNlib's tanh form. */
+typedef enum { MOE_ACT_GELU = 0, MOE_ACT_SILU = 1, MOE_ACT_RELU = 2, MOE_ACT_IDENTITY = 3 } moe_activation;
+
+/* Gating mechanism (src/gating/topk.jl:16-22, switch.jl:7-11,
+ * advanced.jl:74-108). */
+typedef enum { MOE_GATE_TOPK = 0, MOE_GATE_SWITCH = 1, MOE_GATE_SHARED = 2 } moe_gate_kind;
+
+/* Mirror of MoEConfig (src/core/moe_layer.jl:4-29) plus device sizing. */
+typedef struct {
+    int32_t num_experts;        /* E: experts held by the layer */
+    int32_t expert_type;        /* moe_expert_type */
+    int32_t input_dim;          /* D */
+    int32_t hidden_dim;         /* H */
+    int32_t output_dim;         /* D_out */
+    int32_t activation;         /* moe_activation */
+    int32_t gate_kind;          /* moe_gate_kind */
+    int32_t top_k;              /* k of the (base) top-k gate */
+    int32_t gate_num_shared;    /* SharedExpertGating.num_shared (gate_kind SHARED) */
+    int32_t weight_dtype;       /* moe_dtype the expert GEMMs run on */
+    float balance_alpha;        /* SwitchTransformerLoss.alpha */
+    float z_loss_weight;        /* MoEConfig.z_loss_weight */
+    float capacity_factor;      /* MoEConfig.capacity_factor */
+    int32_t drop_tokens;        /* MoEConfig.drop_tokens */
+    int32_t max_tokens;         /* largest T a call may pass (workspace size) */
+    int32_t reserved[7];        /* zero */
+} moe_config;
+
+typedef struct moe_handle moe_handle;
+
+/* Optional per-call outputs of moe_forward (any pointer may be NULL). */
+typedef struct {
+    float *logits;          /* [T][E_router] fp32 router logits */
+    float *probs;           /* [T][E] router probabilities */
+    int32_t *indices;       /* [T][k_total] 1-based expert ids (0 = dropped) */
+    float *gates;           /* [T][k_total] */
+    int32_t *counts;        /* [E] entries per expert this call */
+    int32_t *offsets;       /* [E+1] exclusive prefix sum of counts */
+    int32_t *perm;          /* [T*k_total] entry id at each position */
+    float *switch_loss;     /* scalar, training only */
+    float *z_loss;          /* scalar, training only */
+    float *mean_entropy;    /* scalar: update_stats! entropy of this call */
+} moe_forward_aux;
+
+/* ---- lifecycle -------------------------------------------------------- */
+
+/* MoELayer(config) -- src/core/moe_layer.jl:44-63.  Allocates the device
+ * state for one layer on the current HIP device. */
+int moe_create(const moe_config *cfg, moe_handle **out);
+int moe_destroy(moe_handle *h);
+/* Last error message of h (or of the last failed moe_create when h is NULL). */
+const char *moe_last_error(const moe_handle *h);
+int moe_abi_version(void);
+/* Number of router outputs: E for TopK/Switch/Shared gating. */
+int moe_router_outputs(const moe_handle *h);
+/* Slots per token: k, 1 (Switch) or num_shared + k (Shared). */
+int moe_slots_per_token(const moe_handle *h);
+
+/* ---- weights (uploaded once, prepacked, device resident) --------------- */
+
+/* Router weight -- src/core/router.jl:18 Dense(in, E, bias=false):
+ * weight (E_router, D) column-major = memory [D][E_router] fp32.  bias may be
+ * NULL (the reference router has none; a bias is Dense(W, b)). */
+int moe_set_router(moe_handle *h, const float *weight, const float *bias);
+
+/* Expert e (0-based) weights -- GatedExpert (src/experts/gated.jl:6-27):
+ * w1 (H,D), w3 (H,D), w2 (D_out,H); StandardExpert (src/experts/standard.jl):
+ * w1 (H,D), w2 (D_out,H), b1 (H), b2 (D_out), w3 NULL.
+ * src_dtype: F32 (converted to cfg.weight_dtype; FP8 quantises per output
+ * channel), BF16, or FP8_E4M3 with per-output-channel fp32 scales s1/s2/s3
+ * (value = fp8 * scale[out]); scales are ignored for other dtypes. */
+int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dtype,
+                   const void *w1, const void *w2, const void *w3,
+                   const float *b1, const float *b2,
+                   const float *s1, const float *s2, const float *s3);
+
+/* ---- host-buffer entry points (blocking) -------------------------------- */
+
+/* compute_gates(gate, logits) -- src/gating/topk.jl:24-44,
+ * src/gating/switch.jl:9-11, src/gating/advanced.jl:80-108.
+ * logits [T][E_router] -> indices/gates [T][k_total], probs [T][E]. */
+int moe_compute_gates(moe_handle *h, const float *logits, int32_t T,
+                      int32_t *indices, float *gates, float *probs);
+
+/* compute_gates + the bucketing of process_expert_forward!
+ * (src/core/moe_layer.jl:192-203), with the capacity constraint
+ * (src/core/moe_layer.jl:221-248) when cfg.drop_tokens && training.
+ * counts [E], offsets [E+1], perm [T*k_total] (valid prefix offsets[E]). */
+int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t training,
+                          int32_t *indices, float *gates, float *probs,
+                          int32_t *counts, int32_t *offsets, int32_t *perm);
+
+/* (moe::MoELayer)(x; training) -- src/core/moe_layer.jl:107-156.
+ * x [T][D] in x_dtype (F32 or BF16); out [T][D_out] fp32; *loss = Switch
+ * loss + z-loss when training, else 0. */
+int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
+                float *out, float *loss, moe_forward_aux *aux);
+
+/* (e::Expert)(x) on a block of tokens -- src/experts/gated.jl:29-34,
+ * src/experts/standard.jl:38-55.  x [n][D] fp32 -> y [n][D_out] fp32 through
+ * the device expert path of expert e (0-based). */
+int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n, float *y);
+
+/* compute_loss(::SwitchTransformerLoss, indices, probs) --
+ * src/balancing/losses.jl:15-36.  indices [T][k] 1-based (entries outside
+ * 1..E are not counted), probs [T][E]; no handle needed.  Host pointers. */
+int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *probs, int32_t E, float alpha,
+                    float *loss);
+
+/* compute_loss(::ZLoss, logits) -- src/balancing/losses.jl:103-114.
+ * logits [T][E]; *loss = beta * mean_t(logsumexp_t^2).  Host pointers. */
+int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *loss);
+
+/* ---- device-buffer entry points (enqueue only) -------------------------- */
+
+/* moe_forward on device buffers: x_dev [T][D], out_dev [T][D_out] fp32,
+ * loss_dev (1 float) may be NULL.  Runs on `stream` (hipStream_t). */
+int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T,
+                      int32_t training, float *out_dev, float *loss_dev, void *stream);
+
+/* Stage-level entry points for profiling: together they issue exactly the
+ * kernels of moe_forward_async, one stage per call, on device buffers owned
+ * by the handle.  Call them in forward order (router, permute, expert_up,
+ * expert_down, combine) after a moe_forward_async on the same handle with the
+ * same T.  router = logits GEMM + gating + scan; permute = gather into
+ * expert-contiguous rows; expert_up/down = the two grouped GEMMs; combine =
+ * the weighted scatter back to token order. */
+int moe_stage_router_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T,
+                           int32_t training, void *stream);
+int moe_stage_permute_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T,
+                            void *stream);
+int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream);
+int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream);
+int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stream);
+
+/* Copy the per-expert counts of the last call to host memory (int32 [E]). */
+int moe_read_counts(moe_handle *h, int32_t *counts);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

@@ -1,0 +1,124 @@
+"""Owner of one libmoe_mi355x handle: device-resident weights and workspace.
+
+All array arguments are host numpy arrays in the ABI's token-major memory
+order (a Julia (D, T) matrix is passed as its (T, D) row-major memory).
+"""
+import ctypes
+from collections import namedtuple
+
+import numpy as np
+
+from . import _lib
+
+GateSpec = namedtuple("GateSpec", "kind k num_shared")
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class DeviceLayer:
+    def __init__(self, *, num_experts, expert_type, input_dim, hidden_dim, output_dim, activation, gate,
+                 weight_dtype, balance_alpha, z_loss_weight, capacity_factor, drop_tokens, max_tokens):
+        c = _lib.MoeConfigC()
+        c.num_experts = num_experts
+        c.expert_type = expert_type
+        c.input_dim = input_dim
+        c.hidden_dim = hidden_dim
+        c.output_dim = output_dim
+        c.activation = activation
+        c.gate_kind = gate.kind
+        c.top_k = gate.k
+        c.gate_num_shared = gate.num_shared
+        c.weight_dtype = weight_dtype
+        c.balance_alpha = balance_alpha
+        c.z_loss_weight = z_loss_weight
+        c.capacity_factor = capacity_factor
+        c.drop_tokens = int(bool(drop_tokens))
+        c.max_tokens = max_tokens
+        self.cfg = c
+        self.max_tokens = max_tokens
+        self.num_experts = num_experts
+        self.output_dim = output_dim
+        self.input_dim = input_dim
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().moe_create(ctypes.byref(c), ctypes.byref(h)), None)
+        self.h = h
+        self.router_outputs = _lib.lib().moe_router_outputs(h)
+        self.slots = _lib.lib().moe_slots_per_token(h)
+
+    @classmethod
+    def gating_only(cls, spec, E, T, capacity_factor=None):
+        return cls(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED, input_dim=1, hidden_dim=1, output_dim=1,
+                   activation=_lib.MOE_ACT_IDENTITY, gate=spec, weight_dtype=_lib.MOE_BF16, balance_alpha=0.0,
+                   z_loss_weight=0.0, capacity_factor=1.25 if capacity_factor is None else capacity_factor,
+                   drop_tokens=capacity_factor is not None, max_tokens=T)
+
+    def close(self):
+        if getattr(self, "h", None) is not None and self.h.value is not None:
+            _lib.lib().moe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- weights --------------------------------------------------------
+    def set_router(self, weight_mem_DE, bias=None):
+        w = np.ascontiguousarray(weight_mem_DE, dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        _lib.check(_lib.lib().moe_set_router(self.h, _ptr(w), _ptr(b)), self.h)
+
+    def set_expert(self, e, w1, w2, w3=None, b1=None, b2=None, *, src_dtype=_lib.MOE_F32,
+                   layout=_lib.MOE_LAYOUT_LLAMA_IN_OUT, s1=None, s2=None, s3=None):
+        """Matrices in memory order of ``layout`` (LLAMA_IN_OUT = [out][in],
+        i.e. a numpy (out, in) C-contiguous array)."""
+        dt = {_lib.MOE_F32: np.float32, _lib.MOE_BF16: np.uint16, _lib.MOE_FP8_E4M3: np.uint8}[src_dtype]
+        conv = lambda a: None if a is None else np.ascontiguousarray(a, dtype=dt)
+        convf = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+        arrs = [conv(w1), conv(w2), conv(w3), convf(b1), convf(b2), convf(s1), convf(s2), convf(s3)]
+        _lib.check(
+            _lib.lib().moe_set_expert(self.h, int(e), int(layout), int(src_dtype), *[_ptr(a) for a in arrs]),
+            self.h,
+        )
+
+    # ---- calls ------------------------------------------------------------
+    def forward(self, x_TD, x_dtype, training, want_aux=False):
+        T = x_TD.shape[0]
+        out = np.zeros((T, self.output_dim), dtype=np.float32)
+        loss = ctypes.c_float(0.0)
+        aux = _lib.MoeForwardAux()
+        res = {}
+        counts = np.zeros(self.num_experts, dtype=np.int32)
+        ent = np.zeros(1, dtype=np.float32)
+        sw = np.zeros(1, dtype=np.float32)
+        zl = np.zeros(1, dtype=np.float32)
+        aux.counts = counts.ctypes.data
+        aux.mean_entropy = ent.ctypes.data
+        aux.switch_loss = sw.ctypes.data
+        aux.z_loss = zl.ctypes.data
+        if want_aux:
+            res["logits"] = np.zeros((T, self.router_outputs), dtype=np.float32)
+            res["probs"] = np.zeros((T, self.num_experts), dtype=np.float32)
+            res["indices"] = np.zeros((T, self.slots), dtype=np.int32)
+            res["gates"] = np.zeros((T, self.slots), dtype=np.float32)
+            res["offsets"] = np.zeros(self.num_experts + 1, dtype=np.int32)
+            res["perm"] = np.zeros(T * self.slots, dtype=np.int32)
+            for k in ("logits", "probs", "indices", "gates", "offsets", "perm"):
+                setattr(aux, k, res[k].ctypes.data)
+        _lib.check(
+            _lib.lib().moe_forward(self.h, x_TD.ctypes.data, int(x_dtype), T, int(bool(training)), out.ctypes.data,
+                                   ctypes.byref(loss), ctypes.byref(aux)),
+            self.h,
+        )
+        res.update(counts=counts, mean_entropy=float(ent[0]), switch_loss=float(sw[0]), z_loss=float(zl[0]))
+        return out, float(np.float32(loss.value)), res
+
+    def expert_forward(self, e, x_nD):
+        x = np.ascontiguousarray(x_nD, dtype=np.float32)
+        n = x.shape[0]
+        y = np.zeros((n, self.output_dim), dtype=np.float32)
+        _lib.check(_lib.lib().moe_expert_forward(self.h, int(e), x.ctypes.data, n, y.ctypes.data), self.h)
+        return y

@@ -1,0 +1,865 @@
+// moe_api.hip -- the C ABI of libmoe_mi355x.so (declared in moe_mi355x.h):
+// handle lifecycle, weight upload/prepack on the device, and the stage
+// orchestration of the MoE-layer forward pass on one HIP stream.
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "moe_internal.h"
+
+using namespace moe;
+
+namespace {
+thread_local std::string g_create_error;
+inline long long round_up(long long v, long long m) { return (v + m - 1) / m * m; }
+}  // namespace
+
+struct moe_handle {
+    moe_config cfg{};
+    int E = 0, Er = 0, Er_pad = 0, D = 0, H = 0, Dout = 0, k = 0, ns = 0, kt = 0;
+    int D_pad = 0, H_pad = 0, Dout_npad = 0;
+    int ct = CT_BF16, wt = WT_BF16;
+    bool gated = true;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    std::string err;
+
+    // weights
+    float *wr = nullptr, *br = nullptr;
+    bool router_set = false, has_bias = false;
+    std::vector<char> expert_set;
+    void *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
+    float *s1 = nullptr, *s3 = nullptr, *s2 = nullptr;
+    float *b1 = nullptr, *b2 = nullptr;
+    long long w1_stride = 0, w2_stride = 0;  // elements per expert
+
+    // workspace
+    int T_max = 0, nblk_max = 0, rows_max = 0, max_tiles = 0;
+    float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
+    int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
+    double *blk_stats = nullptr;
+    int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
+    int2 *tiles = nullptr;
+    int *num_tiles = nullptr;
+    float *scalars = nullptr;
+    int *perm = nullptr, *pos_of = nullptr;
+    void *xp = nullptr, *hbuf = nullptr;
+    float *y = nullptr;
+    void *x_dev = nullptr;
+    float *out_dev = nullptr;
+
+    int last_T = -1, last_training = 0, last_x_bf16 = 0;
+    std::vector<void *> allocs;
+};
+
+static int fail(moe_handle *h, int code, const std::string &msg) {
+    if (h) h->err = msg; else g_create_error = msg;
+    return code;
+}
+
+#define HIP_TRY(h, call)                                                                   \
+    do {                                                                                   \
+        hipError_t _e = (call);                                                            \
+        if (_e != hipSuccess)                                                              \
+            return fail((h), MOE_EHIP, std::string(#call) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+static int dalloc(moe_handle *h, void **p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(h, MOE_EOOM, "hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+    }
+    h->allocs.push_back(*p);
+    return MOE_OK;
+}
+
+static void free_all(moe_handle *h) {
+    for (void *p : h->allocs) (void)hipFree(p);
+    h->allocs.clear();
+}
+
+static int validate_config(const moe_config *c, std::string &why) {
+    if (c->num_experts < 1 || c->num_experts > MOE_MAX_EXPERTS) { why = "num_experts out of range [1,128]"; return 0; }
+    if (c->input_dim < 1 || c->hidden_dim < 1 || c->output_dim < 1) { why = "dimensions must be positive"; return 0; }
+    if (c->expert_type != MOE_EXPERT_GATED && c->expert_type != MOE_EXPERT_STANDARD) { why = "unknown expert_type"; return 0; }
+    if (c->activation < MOE_ACT_GELU || c->activation > MOE_ACT_IDENTITY) { why = "unknown activation"; return 0; }
+    if (c->weight_dtype < MOE_F32 || c->weight_dtype > MOE_FP8_E4M3) { why = "unknown weight_dtype"; return 0; }
+    if (c->max_tokens < 1) { why = "max_tokens must be >= 1"; return 0; }
+    if (c->drop_tokens && !(c->capacity_factor > 0.0f)) { why = "capacity_factor must be > 0"; return 0; }
+    const int k = (c->gate_kind == MOE_GATE_SWITCH) ? 1 : c->top_k;
+    if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH) {
+        if (k < 1 || k > c->num_experts) { why = "top_k must be in [1, num_experts]"; return 0; }
+        if (k > MOE_MAX_TOPK) { why = "top_k above MOE_MAX_TOPK (8)"; return 0; }
+    } else if (c->gate_kind == MOE_GATE_SHARED) {
+        const int ns = c->gate_num_shared;
+        if (ns < 0 || ns >= c->num_experts) { why = "gate_num_shared must be in [0, num_experts)"; return 0; }
+        if (k < 1 || k > c->num_experts - ns) { why = "top_k must be in [1, num_experts - num_shared]"; return 0; }
+        if (ns + k > MOE_MAX_TOPK) { why = "num_shared + top_k above MOE_MAX_TOPK (8)"; return 0; }
+    } else {
+        why = "unknown gate_kind";
+        return 0;
+    }
+    const long long rows = (long long)c->max_tokens * (k + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0));
+    if (rows > INT_MAX / 2) { why = "max_tokens * slots too large"; return 0; }
+    return 1;
+}
+
+// ============================================================================
+// Weight packing kernels (run once per upload).
+// ============================================================================
+namespace {
+
+// Source element (o, i) of an (out N, in K) matrix as fp32 (fp8 dequantised by
+// the per-output-channel scale).
+template <int SRC>
+__device__ inline float src_elem(const void *src, long long off, const float *scales, int o) {
+    if (SRC == MOE_F32) return ((const float *)src)[off];
+    if (SRC == MOE_BF16) return bf16_to_f32(((const uint16_t *)src)[off]);
+    return fp8e4m3_to_f32(((const uint8_t *)src)[off]) * scales[o];
+}
+
+// src (any layout / dtype) -> fp32 [N][K] row-major (K contiguous).
+template <int SRC>
+__global__ void to_f32_rows_kernel(const void *src, int layout, int N, int K, const float *scales,
+                                   float *dst) {
+    __shared__ float tile[32][33];
+    const int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
+    const int o0 = blockIdx.x * 32, i0 = blockIdx.y * 32;
+    if (layout == MOE_LAYOUT_FLUX_OUT_IN) {  // memory [K][N]
+        for (int j = ty; j < 32; j += 8) {
+            const int i = i0 + j, o = o0 + tx;
+            if (i < K && o < N) tile[j][tx] = src_elem<SRC>(src, (long long)i * N + o, scales, o);
+        }
+        __syncthreads();
+        for (int j = ty; j < 32; j += 8) {
+            const int o = o0 + j, i = i0 + tx;
+            if (i < K && o < N) dst[(long long)o * K + i] = tile[tx][j];
+        }
+    } else {  // memory [N][K]
+        for (int j = ty; j < 32; j += 8) {
+            const int o = o0 + j, i = i0 + tx;
+            if (i < K && o < N) dst[(long long)o * K + i] = src_elem<SRC>(src, (long long)o * K + i, scales, o);
+        }
+    }
+}
+
+__device__ inline uint8_t f32_to_fp8e4m3_dev(float v) {
+    const uint8_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+    const float a = fabsf(v);
+    if (!(a < 448.0f)) return sign | 0x7e;  // saturate (and NaN) to max finite
+    if (a < 0.015625f) {
+        int m = (int)rintf(a * 512.0f);
+        return m >= 8 ? (uint8_t)(sign | 0x08) : (uint8_t)(sign | m);
+    }
+    int ex;
+    const float fr = frexpf(a, &ex);
+    int e = ex - 1;
+    int m = (int)rintf((2.0f * fr - 1.0f) * 8.0f);
+    if (m == 8) { m = 0; ++e; }
+    if (e > 8 || (e == 8 && m > 6)) return sign | 0x7e;
+    return sign | (uint8_t)(((e + 7) << 3) | m);
+}
+
+// fp32 [N][K] -> packed [Npad][Kpad] of DST (row o of this expert), one block
+// per row.  fp8 rows get scale = max|w| / 448 (1 for an all-zero row).
+template <int DST>
+__global__ __launch_bounds__(256) void pack_rows_kernel(const float *src, int K, int Kpad, void *dst,
+                                                        float *scales) {
+    const int o = blockIdx.x;
+    const float *row = src + (long long)o * K;
+    float inv = 1.0f;
+    if (DST == WT_FP8) {
+        __shared__ float red[256];
+        float m = 0.0f;
+        for (int i = threadIdx.x; i < K; i += 256) m = fmaxf(m, fabsf(row[i]));
+        red[threadIdx.x] = m;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+            __syncthreads();
+        }
+        const float amax = red[0];
+        const float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
+        if (threadIdx.x == 0) scales[o] = sc;
+        inv = sc;
+    }
+    for (int i = threadIdx.x; i < Kpad; i += 256) {
+        const float v = (i < K) ? row[i] : 0.0f;
+        if (DST == WT_F32) ((float *)dst)[(long long)o * Kpad + i] = v;
+        else if (DST == WT_BF16) ((uint16_t *)dst)[(long long)o * Kpad + i] = f32_to_bf16(v);
+        else ((uint8_t *)dst)[(long long)o * Kpad + i] = f32_to_fp8e4m3_dev(v / inv);
+    }
+}
+
+// fp8 source kept bit-exact when the packed type is fp8 too.
+__global__ void fp8_rows_kernel(const uint8_t *src, int layout, int N, int K, int Kpad, uint8_t *dst) {
+    const long long total = (long long)N * Kpad;
+    for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
+         t += (long long)gridDim.x * blockDim.x) {
+        const int o = (int)(t / Kpad), i = (int)(t % Kpad);
+        uint8_t v = 0;
+        if (i < K) v = (layout == MOE_LAYOUT_FLUX_OUT_IN) ? src[(long long)i * N + o] : src[(long long)o * K + i];
+        dst[t] = v;
+    }
+}
+
+// rows [n][D] of fp32/bf16 -> compute type with row stride ld (pads untouched)
+__global__ void convert_rows_kernel(const void *src, int src_bf16, int n, int D, int ct, void *dst, int ld) {
+    const long long total = (long long)n * D;
+    for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
+         t += (long long)gridDim.x * blockDim.x) {
+        const long long r = t / D, c = t % D;
+        const float v = src_bf16 ? bf16_to_f32(((const uint16_t *)src)[t]) : ((const float *)src)[t];
+        if (ct == CT_F32) ((float *)dst)[r * ld + c] = v;
+        else ((uint16_t *)dst)[r * ld + c] = f32_to_bf16(v);
+    }
+}
+
+}  // namespace
+
+static bool is_device_ptr(const void *p) {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
+// Make a device copy of `bytes` at p unless p already is device memory.
+static int stage_to_device(moe_handle *h, const void *p, size_t bytes, const void **dptr, void **owned) {
+    *owned = nullptr;
+    if (is_device_ptr(p)) {
+        *dptr = p;
+        return MOE_OK;
+    }
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, bytes);
+    if (e != hipSuccess) return fail(h, MOE_EOOM, std::string("staging allocation failed: ") + hipGetErrorString(e));
+    e = hipMemcpy(d, p, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(h, MOE_EHIP, std::string("staging copy failed: ") + hipGetErrorString(e));
+    }
+    *dptr = d;
+    *owned = d;
+    return MOE_OK;
+}
+
+// Pack one (N out, K in) matrix of expert e into dst [Npad][Kpad] (+ scales).
+static int pack_matrix(moe_handle *h, int layout, int src_dtype, const void *src, const float *src_scales,
+                       int N, int K, int Kpad, void *dst_expert, float *dst_scales) {
+    const size_t esz = src_dtype == MOE_F32 ? 4 : (src_dtype == MOE_BF16 ? 2 : 1);
+    const void *dsrc = nullptr;
+    void *own_src = nullptr, *own_sc = nullptr;
+    const void *dsc = nullptr;
+    int r = stage_to_device(h, src, esz * (size_t)N * K, &dsrc, &own_src);
+    if (r != MOE_OK) return r;
+    if (src_dtype == MOE_FP8_E4M3) {
+        r = stage_to_device(h, src_scales, sizeof(float) * (size_t)N, &dsc, &own_sc);
+        if (r != MOE_OK) { if (own_src) (void)hipFree(own_src); return r; }
+    }
+    hipError_t e = hipSuccess;
+    if (src_dtype == MOE_FP8_E4M3 && h->wt == WT_FP8) {
+        hipLaunchKernelGGL(fp8_rows_kernel, dim3(1024), dim3(256), 0, h->stream, (const uint8_t *)dsrc, layout, N,
+                           K, Kpad, (uint8_t *)dst_expert);
+        e = hipGetLastError();
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(dst_scales, dsc, sizeof(float) * N, hipMemcpyDeviceToDevice, h->stream);
+    } else {
+        float *tmp = nullptr;
+        e = hipMalloc(&tmp, sizeof(float) * (size_t)N * K);
+        if (e == hipSuccess) {
+            dim3 grid((N + 31) / 32, (K + 31) / 32), block(32, 8);
+            if (src_dtype == MOE_F32)
+                hipLaunchKernelGGL(to_f32_rows_kernel<MOE_F32>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                                   (const float *)dsc, tmp);
+            else if (src_dtype == MOE_BF16)
+                hipLaunchKernelGGL(to_f32_rows_kernel<MOE_BF16>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                                   (const float *)dsc, tmp);
+            else
+                hipLaunchKernelGGL(to_f32_rows_kernel<MOE_FP8_E4M3>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                                   (const float *)dsc, tmp);
+            e = hipGetLastError();
+            if (e == hipSuccess) {
+                if (h->wt == WT_F32)
+                    hipLaunchKernelGGL(pack_rows_kernel<WT_F32>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
+                                       dst_expert, dst_scales);
+                else if (h->wt == WT_BF16)
+                    hipLaunchKernelGGL(pack_rows_kernel<WT_BF16>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
+                                       dst_expert, dst_scales);
+                else
+                    hipLaunchKernelGGL(pack_rows_kernel<WT_FP8>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
+                                       dst_expert, dst_scales);
+                e = hipGetLastError();
+            }
+            hipError_t e2 = hipStreamSynchronize(h->stream);
+            if (e == hipSuccess) e = e2;
+            (void)hipFree(tmp);
+        }
+    }
+    hipError_t e3 = hipStreamSynchronize(h->stream);
+    if (e == hipSuccess) e = e3;
+    if (own_src) (void)hipFree(own_src);
+    if (own_sc) (void)hipFree(own_sc);
+    if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("weight packing failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+// ============================================================================
+// Forward orchestration
+// ============================================================================
+static int check_ready(moe_handle *h) {
+    if (!h->router_set) return fail(h, MOE_ENOTREADY, "router weights not set (moe_set_router)");
+    for (int e = 0; e < h->E; ++e)
+        if (!h->expert_set[e]) return fail(h, MOE_ENOTREADY, "expert " + std::to_string(e) + " has no weights");
+    return MOE_OK;
+}
+
+static int m_tiles_for(const moe_handle *h, int T) {
+    long long mt = (long long)T * h->kt / kGemmBM + h->E;
+    if (mt > h->max_tiles) mt = h->max_tiles;
+    return (int)mt;
+}
+
+enum { PERMUTE_NONE = 0, PERMUTE_INDEX = 1, PERMUTE_ROWS = 2 };
+
+static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
+    PermuteArgs pa{};
+    pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kt; pa.E = h->E;
+    pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base;
+    pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && h->cfg.drop_tokens) ? 1 : 0;
+    pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
+    pa.copy_rows = mode == PERMUTE_ROWS ? 1 : 0;
+    HIP_TRY(h, launch_permute(pa, s));
+    return MOE_OK;
+}
+
+// logits -> gating -> scan -> permute (mode PERMUTE_*)
+static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
+                       int permute_mode, float *loss_dev, hipStream_t s) {
+    if (compute_logits)
+        HIP_TRY(h, launch_router_logits(x_dev, x_bf16, T, h->D, h->Er, h->Er_pad, h->wr,
+                                        h->has_bias ? h->br : nullptr, h->logits, s));
+    RouteArgs ra{};
+    ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->E; ra.gate_kind = h->cfg.gate_kind;
+    ra.k = h->k; ra.ns = h->ns; ra.kt = h->kt; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
+    ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
+    HIP_TRY(h, launch_route(ra, s));
+    ScanArgs sa{};
+    sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
+    sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kt;
+    sa.training = training; sa.drop = h->cfg.drop_tokens; sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
+    sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
+    sa.bm = kGemmBM; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
+    sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
+    sa.loss_out = loss_dev;
+    HIP_TRY(h, launch_scan(sa, s));
+    if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
+    return MOE_OK;
+}
+
+static GemmArgs up_args(moe_handle *h, int mt_grid) {
+    GemmArgs g{};
+    g.A = h->xp; g.lda = h->D_pad;
+    g.B0 = h->w1; g.B1 = h->gated ? h->w3 : nullptr;
+    g.b_stride = h->w1_stride; g.ldb = h->D_pad;
+    g.s0 = h->s1; g.s1 = h->s3; g.bias = h->gated ? nullptr : h->b1; g.s_stride = h->H_pad;
+    g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
+    g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
+    g.m_tiles_grid = mt_grid; g.n_tiles = h->H_pad / kGemmBN; g.act = h->cfg.activation;
+    return g;
+}
+
+static GemmArgs down_args(moe_handle *h, int mt_grid) {
+    GemmArgs g{};
+    g.A = h->hbuf; g.lda = h->H_pad;
+    g.B0 = h->w2; g.B1 = nullptr;
+    g.b_stride = h->w2_stride; g.ldb = h->H_pad;
+    g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
+    g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
+    g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
+    g.m_tiles_grid = mt_grid; g.n_tiles = h->Dout_npad / kGemmBN; g.act = h->cfg.activation;
+    return g;
+}
+
+static int run_experts(moe_handle *h, int T, hipStream_t s) {
+    const int mt = m_tiles_for(h, T);
+    HIP_TRY(h, launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0,
+                                   up_args(h, mt), s));
+    HIP_TRY(h, launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt), s));
+    return MOE_OK;
+}
+
+static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
+    CombineArgs c{};
+    c.y = h->y; c.ld_y = h->Dout; c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
+    c.T = T; c.D = h->Dout; c.kt = h->kt; c.out = out_dev;
+    HIP_TRY(h, launch_combine(c, s));
+    return MOE_OK;
+}
+
+static int forward_locked(moe_handle *h, const void *x_dev, int x_dtype, int T, int training, float *out_dev,
+                          float *loss_dev, hipStream_t s) {
+    int r = check_ready(h);
+    if (r != MOE_OK) return r;
+    if (x_dtype != MOE_F32 && x_dtype != MOE_BF16) return fail(h, MOE_EINVAL, "x_dtype must be F32 or BF16");
+    if (T < 1 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [1, max_tokens]");
+    if (!x_dev || !out_dev) return fail(h, MOE_EINVAL, "null buffer");
+    const int xb = x_dtype == MOE_BF16;
+    r = run_routing(h, x_dev, xb, T, training, true, PERMUTE_ROWS, loss_dev, s);
+    if (r != MOE_OK) return r;
+    r = run_experts(h, T, s);
+    if (r != MOE_OK) return r;
+    r = run_combine(h, T, out_dev, s);
+    if (r != MOE_OK) return r;
+    h->last_T = T;
+    h->last_training = training;
+    h->last_x_bf16 = xb;
+    return MOE_OK;
+}
+
+static int ensure_io_buffers(moe_handle *h) {
+    if (!h->x_dev) {
+        int r = dalloc(h, &h->x_dev, sizeof(float) * (size_t)h->T_max * h->D);
+        if (r != MOE_OK) return r;
+    }
+    if (!h->out_dev) {
+        int r = dalloc(h, (void **)&h->out_dev, sizeof(float) * (size_t)h->T_max * h->Dout);
+        if (r != MOE_OK) return r;
+    }
+    return MOE_OK;
+}
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+const char *moe_last_error(const moe_handle *h) { return h ? h->err.c_str() : g_create_error.c_str(); }
+
+int moe_router_outputs(const moe_handle *h) { return h ? h->Er : -1; }
+int moe_slots_per_token(const moe_handle *h) { return h ? h->kt : -1; }
+
+int moe_create(const moe_config *cfg, moe_handle **out) {
+    if (!cfg || !out) return fail(nullptr, MOE_EINVAL, "null argument");
+    *out = nullptr;
+    std::string why;
+    if (!validate_config(cfg, why)) return fail(nullptr, MOE_EINVAL, why);
+    moe_handle *h = new moe_handle();
+    h->cfg = *cfg;
+    h->E = cfg->num_experts;
+    h->Er = cfg->num_experts;
+    h->Er_pad = (int)round_up(h->Er, 8);
+    h->D = cfg->input_dim;
+    h->H = cfg->hidden_dim;
+    h->Dout = cfg->output_dim;
+    h->k = (cfg->gate_kind == MOE_GATE_SWITCH) ? 1 : cfg->top_k;
+    h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
+    h->kt = h->ns + h->k;
+    h->D_pad = (int)round_up(h->D, kKPad);
+    h->H_pad = (int)round_up(h->H, kNPad);  // N of the up GEMM, K of the down GEMM
+    h->Dout_npad = (int)round_up(h->Dout, kNPad);
+    h->ct = (cfg->weight_dtype == MOE_F32) ? CT_F32 : CT_BF16;
+    h->wt = (cfg->weight_dtype == MOE_F32) ? WT_F32 : (cfg->weight_dtype == MOE_BF16 ? WT_BF16 : WT_FP8);
+    h->gated = cfg->expert_type == MOE_EXPERT_GATED;
+    h->expert_set.assign(h->E, 0);
+    (void)hipGetDevice(&h->device);
+
+    auto cleanup = [&](int code) {
+        g_create_error = h->err;
+        free_all(h);
+        if (h->stream) (void)hipStreamDestroy(h->stream);
+        delete h;
+        return code;
+    };
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        h->err = "hipStreamCreate failed";
+        return cleanup(MOE_EHIP);
+    }
+    int r = MOE_OK;
+    auto A = [&](void **p, size_t bytes) {
+        if (r == MOE_OK) r = dalloc(h, p, bytes);
+    };
+    const size_t wsz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
+    const size_t asz = (h->ct == CT_F32) ? 4 : 2;
+    h->w1_stride = (long long)h->H_pad * h->D_pad;
+    h->w2_stride = (long long)h->Dout_npad * h->H_pad;
+    const size_t wr_bytes = sizeof(float) * (size_t)h->D * h->Er_pad;
+    A((void **)&h->wr, wr_bytes);
+    A((void **)&h->br, sizeof(float) * (size_t)h->Er_pad);
+    A(&h->w1, wsz * (size_t)h->E * h->w1_stride);
+    if (h->gated) A(&h->w3, wsz * (size_t)h->E * h->w1_stride);
+    A(&h->w2, wsz * (size_t)h->E * h->w2_stride);
+    if (h->wt == WT_FP8) {
+        A((void **)&h->s1, sizeof(float) * (size_t)h->E * h->H_pad);
+        if (h->gated) A((void **)&h->s3, sizeof(float) * (size_t)h->E * h->H_pad);
+        A((void **)&h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    }
+    if (!h->gated) {
+        A((void **)&h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
+        A((void **)&h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    }
+    h->T_max = cfg->max_tokens;
+    h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
+    h->rows_max = h->T_max * h->kt;
+    h->max_tiles = h->rows_max / kGemmBM + h->E + 1;
+    const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
+    A((void **)&h->logits, sizeof(float) * T * h->Er);
+    A((void **)&h->probs, sizeof(float) * T * E);
+    A((void **)&h->idx, sizeof(int) * T * kt);
+    A((void **)&h->gates, sizeof(float) * T * kt);
+    A((void **)&h->rank, sizeof(int) * T * kt);
+    A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * E);
+    A((void **)&h->blk_stats, sizeof(double) * (size_t)h->nblk_max * (E + 2));
+    A((void **)&h->counts, sizeof(int) * E);
+    A((void **)&h->offsets, sizeof(int) * (E + 1));
+    A((void **)&h->rank_base, sizeof(int) * (size_t)h->nblk_max * E);
+    A((void **)&h->cap, sizeof(int));
+    A((void **)&h->tiles, sizeof(int2) * (size_t)h->max_tiles);
+    A((void **)&h->num_tiles, sizeof(int));
+    A((void **)&h->scalars, sizeof(float) * 8);
+    A((void **)&h->perm, sizeof(int) * T * kt);
+    A((void **)&h->pos_of, sizeof(int) * T * kt);
+    A((void **)&h->gate_sorted, sizeof(float) * T * kt);
+    A(&h->xp, asz * (size_t)h->rows_max * h->D_pad);
+    A(&h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
+    A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout);
+    if (r != MOE_OK) return cleanup(r);
+    // Pads of the packed weights and of the activation rows must read as 0.
+    hipError_t ze = hipSuccess;
+    auto Z = [&](void *p, size_t bytes) {
+        if (ze == hipSuccess && p) ze = hipMemsetAsync(p, 0, bytes, h->stream);
+    };
+    Z(h->wr, wr_bytes);
+    Z(h->br, sizeof(float) * (size_t)h->Er_pad);
+    Z(h->w1, wsz * (size_t)h->E * h->w1_stride);
+    Z(h->w3, wsz * (size_t)h->E * h->w1_stride);
+    Z(h->w2, wsz * (size_t)h->E * h->w2_stride);
+    Z(h->s1, sizeof(float) * (size_t)h->E * h->H_pad);
+    Z(h->s3, sizeof(float) * (size_t)h->E * h->H_pad);
+    Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    Z(h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
+    Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    Z(h->xp, asz * (size_t)h->rows_max * h->D_pad);
+    Z(h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
+    if (ze == hipSuccess) ze = hipStreamSynchronize(h->stream);
+    if (ze != hipSuccess) {
+        h->err = std::string("initialising device memory failed: ") + hipGetErrorString(ze);
+        return cleanup(MOE_EHIP);
+    }
+    *out = h;
+    return MOE_OK;
+}
+
+int moe_destroy(moe_handle *h) {
+    if (!h) return MOE_OK;
+    {
+        std::lock_guard<std::mutex> lk(h->mu);
+        if (h->stream) (void)hipStreamSynchronize(h->stream);
+        free_all(h);
+        if (h->stream) (void)hipStreamDestroy(h->stream);
+        h->stream = nullptr;
+    }
+    delete h;
+    return MOE_OK;
+}
+
+int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (!weight) return fail(h, MOE_EINVAL, "null router weight");
+    const bool dev_w = is_device_ptr(weight);
+    const bool dev_b = bias && is_device_ptr(bias);
+    // memory [D][Er] -> [D][Er_pad]
+    HIP_TRY(h, hipMemcpy2DAsync(h->wr, sizeof(float) * h->Er_pad, weight, sizeof(float) * h->Er,
+                                sizeof(float) * h->Er, h->D, dev_w ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                h->stream));
+    if (bias)
+        HIP_TRY(h, hipMemcpyAsync(h->br, bias, sizeof(float) * h->Er, dev_b ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                  h->stream));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    h->has_bias = bias != nullptr;
+    h->router_set = true;
+    return MOE_OK;
+}
+
+int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dtype, const void *w1, const void *w2,
+                   const void *w3, const float *b1, const float *b2, const float *s1, const float *s2,
+                   const float *s3) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (expert < 0 || expert >= h->E) return fail(h, MOE_EINVAL, "expert index out of range");
+    if (layout != MOE_LAYOUT_FLUX_OUT_IN && layout != MOE_LAYOUT_LLAMA_IN_OUT) return fail(h, MOE_EINVAL, "bad layout");
+    if (src_dtype < MOE_F32 || src_dtype > MOE_FP8_E4M3) return fail(h, MOE_EINVAL, "bad src_dtype");
+    if (!w1 || !w2 || (h->gated && !w3)) return fail(h, MOE_EINVAL, "missing expert weight matrix");
+    if (src_dtype == MOE_FP8_E4M3 && (!s1 || !s2 || (h->gated && !s3)))
+        return fail(h, MOE_EINVAL, "fp8 weights need per-output-channel scales");
+    const size_t wsz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
+    uint8_t *w1d = (uint8_t *)h->w1 + wsz * (size_t)expert * h->w1_stride;
+    uint8_t *w2d = (uint8_t *)h->w2 + wsz * (size_t)expert * h->w2_stride;
+    float *s1d = h->s1 ? h->s1 + (size_t)expert * h->H_pad : nullptr;
+    float *s2d = h->s2 ? h->s2 + (size_t)expert * h->Dout_npad : nullptr;
+    int r = pack_matrix(h, layout, src_dtype, w1, s1, h->H, h->D, h->D_pad, w1d, s1d);
+    if (r != MOE_OK) return r;
+    if (h->gated) {
+        uint8_t *w3d = (uint8_t *)h->w3 + wsz * (size_t)expert * h->w1_stride;
+        float *s3d = h->s3 ? h->s3 + (size_t)expert * h->H_pad : nullptr;
+        r = pack_matrix(h, layout, src_dtype, w3, s3, h->H, h->D, h->D_pad, w3d, s3d);
+        if (r != MOE_OK) return r;
+    }
+    r = pack_matrix(h, layout, src_dtype, w2, s2, h->Dout, h->H, h->H_pad, w2d, s2d);
+    if (r != MOE_OK) return r;
+    if (!h->gated) {
+        if (b1)
+            HIP_TRY(h, hipMemcpy(h->b1 + (size_t)expert * h->H_pad, b1, sizeof(float) * h->H,
+                                 is_device_ptr(b1) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice));
+        if (b2)
+            HIP_TRY(h, hipMemcpy(h->b2 + (size_t)expert * h->Dout_npad, b2, sizeof(float) * h->Dout,
+                                 is_device_ptr(b2) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice));
+    }
+    h->expert_set[expert] = 1;
+    return MOE_OK;
+}
+
+int moe_compute_gates(moe_handle *h, const float *logits, int32_t T, int32_t *indices, float *gates, float *probs) {
+    return moe_route_from_logits(h, logits, T, 0, indices, gates, probs, nullptr, nullptr, nullptr);
+}
+
+int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t training, int32_t *indices,
+                          float *gates, float *probs, int32_t *counts, int32_t *offsets, int32_t *perm) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (T < 0 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [0, max_tokens]");
+    if (T > 0 && !logits) return fail(h, MOE_EINVAL, "null logits");
+    if (T == 0) {
+        if (counts) memset(counts, 0, sizeof(int32_t) * h->E);
+        if (offsets) memset(offsets, 0, sizeof(int32_t) * (h->E + 1));
+        return MOE_OK;
+    }
+    hipStream_t s = h->stream;
+    h->last_T = -1;  // routing state no longer matches a forward call
+    HIP_TRY(h, hipMemcpyAsync(h->logits, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
+    int r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
+    if (r != MOE_OK) return r;
+    const size_t nk = (size_t)T * h->kt;
+    if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
+    if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * nk, hipMemcpyDeviceToHost, s));
+    if (probs) HIP_TRY(h, hipMemcpyAsync(probs, h->probs, sizeof(float) * (size_t)T * h->E, hipMemcpyDeviceToHost, s));
+    if (counts) HIP_TRY(h, hipMemcpyAsync(counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost, s));
+    if (offsets) HIP_TRY(h, hipMemcpyAsync(offsets, h->offsets, sizeof(int) * (h->E + 1), hipMemcpyDeviceToHost, s));
+    if (perm) HIP_TRY(h, hipMemcpyAsync(perm, h->perm, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    return MOE_OK;
+}
+
+int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training, float *out, float *loss,
+                moe_forward_aux *aux) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (T < 0 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [0, max_tokens]");
+    if (T == 0) {
+        // empty batch: zero-size output; loss 0 (inference) or NaN (means over no tokens)
+        if (loss) *loss = training ? NAN : 0.0f;
+        if (aux) {
+            if (aux->counts) memset(aux->counts, 0, sizeof(int32_t) * h->E);
+            if (aux->offsets) memset(aux->offsets, 0, sizeof(int32_t) * (h->E + 1));
+            if (aux->mean_entropy) *aux->mean_entropy = NAN;
+            if (aux->switch_loss) *aux->switch_loss = training ? NAN : 0.0f;
+            if (aux->z_loss) *aux->z_loss = training ? NAN : 0.0f;
+        }
+        return MOE_OK;
+    }
+    if (!x || !out) return fail(h, MOE_EINVAL, "null x or out");
+    int r = ensure_io_buffers(h);
+    if (r != MOE_OK) return r;
+    hipStream_t s = h->stream;
+    const size_t xbytes = (x_dtype == MOE_BF16 ? 2 : 4) * (size_t)T * h->D;
+    HIP_TRY(h, hipMemcpyAsync(h->x_dev, x, xbytes, hipMemcpyHostToDevice, s));
+    r = forward_locked(h, h->x_dev, x_dtype, T, training, h->out_dev, nullptr, s);
+    if (r != MOE_OK) return r;
+    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, sizeof(float) * (size_t)T * h->Dout, hipMemcpyDeviceToHost, s));
+    float sc[4] = {0, 0, 0, 0};
+    HIP_TRY(h, hipMemcpyAsync(sc, h->scalars, sizeof(float) * 4, hipMemcpyDeviceToHost, s));
+    const size_t nk = (size_t)T * h->kt;
+    if (aux) {
+        if (aux->logits) HIP_TRY(h, hipMemcpyAsync(aux->logits, h->logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
+        if (aux->probs) HIP_TRY(h, hipMemcpyAsync(aux->probs, h->probs, sizeof(float) * (size_t)T * h->E, hipMemcpyDeviceToHost, s));
+        if (aux->indices) HIP_TRY(h, hipMemcpyAsync(aux->indices, h->idx, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
+        if (aux->gates) HIP_TRY(h, hipMemcpyAsync(aux->gates, h->gates, sizeof(float) * nk, hipMemcpyDeviceToHost, s));
+        if (aux->counts) HIP_TRY(h, hipMemcpyAsync(aux->counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost, s));
+        if (aux->offsets) HIP_TRY(h, hipMemcpyAsync(aux->offsets, h->offsets, sizeof(int) * (h->E + 1), hipMemcpyDeviceToHost, s));
+        if (aux->perm) HIP_TRY(h, hipMemcpyAsync(aux->perm, h->perm, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
+    }
+    HIP_TRY(h, hipStreamSynchronize(s));
+    if (loss) *loss = sc[2];
+    if (aux) {
+        if (aux->switch_loss) *aux->switch_loss = sc[0];
+        if (aux->z_loss) *aux->z_loss = sc[1];
+        if (aux->mean_entropy) *aux->mean_entropy = sc[3];
+    }
+    return MOE_OK;
+}
+
+int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n, float *y) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (expert < 0 || expert >= h->E) return fail(h, MOE_EINVAL, "expert index out of range");
+    if (!h->expert_set[expert]) return fail(h, MOE_ENOTREADY, "expert has no weights");
+    if (n < 0 || n > h->rows_max) return fail(h, MOE_EINVAL, "n must be in [0, max_tokens * slots]");
+    if (n == 0) return MOE_OK;
+    if (!x || !y) return fail(h, MOE_EINVAL, "null buffer");
+    hipStream_t s = h->stream;
+    // single segment: counts[expert] = n, all others 0
+    std::vector<int> cnt(h->E, 0), off(h->E + 1, 0);
+    cnt[expert] = n;
+    for (int e = 0; e < h->E; ++e) off[e + 1] = off[e] + cnt[e];
+    const int nt = (n + kGemmBM - 1) / kGemmBM;
+    std::vector<int2> tl(nt);
+    for (int i = 0; i < nt; ++i) tl[i] = make_int2(expert, i * kGemmBM);
+    void *xs = nullptr;
+    HIP_TRY(h, hipMalloc(&xs, sizeof(float) * (size_t)n * h->D));
+    hipError_t e = hipMemcpyAsync(xs, x, sizeof(float) * (size_t)n * h->D, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(h->counts, cnt.data(), sizeof(int) * h->E, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(h->offsets, off.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(h->tiles, tl.data(), sizeof(int2) * nt, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(h->num_tiles, &nt, sizeof(int), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(convert_rows_kernel, dim3(1024), dim3(256), 0, s, (const void *)xs, 0, n, h->D, h->ct,
+                           h->xp, h->D_pad);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt,
+                                                 h->ct == CT_BF16 ? 1 : 0, up_args(h, nt), s);
+    if (e == hipSuccess) e = launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, nt), s);
+    if (e == hipSuccess) e = hipMemcpyAsync(y, h->y, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s);
+    hipError_t e2 = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = e2;
+    (void)hipFree(xs);
+    h->last_T = -1;  // routing state no longer matches a forward call
+    if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("expert forward failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, int32_t training, float *out_dev,
+                      float *loss_dev, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    return forward_locked(h, x_dev, x_dtype, T, training, out_dev, loss_dev, s);
+}
+
+static int stage_check(moe_handle *h, int T) {
+    if (h->last_T != T) return fail(h, MOE_EINVAL, "stage call must follow a moe_forward_async with the same T");
+    return MOE_OK;
+}
+
+int moe_stage_router_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, int32_t training,
+                           void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = stage_check(h, T);
+    if (r != MOE_OK) return r;
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    h->last_training = training;
+    return run_routing(h, x_dev, x_dtype == MOE_BF16, T, training, true, PERMUTE_NONE, nullptr, s);
+}
+
+int moe_stage_permute_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = stage_check(h, T);
+    if (r != MOE_OK) return r;
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    return run_permute(h, x_dev, x_dtype == MOE_BF16, T, h->last_training, PERMUTE_ROWS, s);
+}
+
+int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = stage_check(h, T);
+    if (r != MOE_OK) return r;
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    HIP_TRY(h, launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0,
+                                   up_args(h, m_tiles_for(h, T)), s));
+    return MOE_OK;
+}
+
+int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = stage_check(h, T);
+    if (r != MOE_OK) return r;
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    HIP_TRY(h, launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, m_tiles_for(h, T)), s));
+    return MOE_OK;
+}
+
+int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = stage_check(h, T);
+    if (r != MOE_OK) return r;
+    if (!out_dev) return fail(h, MOE_EINVAL, "null out");
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    return run_combine(h, T, out_dev, s);
+}
+
+int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *probs, int32_t E, float alpha,
+                    float *loss) {
+    if (!loss || T < 0 || k < 1 || E < 1) return fail(nullptr, MOE_EINVAL, "bad switch-loss arguments");
+    if (T > 0 && (!indices || !probs)) return fail(nullptr, MOE_EINVAL, "null indices or probs");
+    if (T == 0) { *loss = NAN; return MOE_OK; }
+    const size_t ni = (size_t)T * k, np_ = (size_t)T * E;
+    void *buf = nullptr;
+    const size_t bytes = sizeof(int) * ni + sizeof(float) * np_ + sizeof(int) * E + 16;
+    if (hipMalloc(&buf, bytes) != hipSuccess) return fail(nullptr, MOE_EOOM, "hipMalloc failed");
+    int *di = (int *)buf;
+    float *dp = (float *)(di + ni);
+    int *dc = (int *)(dp + np_);
+    float *dout = (float *)(dc + E);
+    hipError_t e = hipMemcpy(di, indices, sizeof(int) * ni, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dp, probs, sizeof(float) * np_, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_switch_loss(di, T, k, dp, E, alpha, dc, dout, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(loss, dout, sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("switch loss failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *loss) {
+    if (!loss || T < 0 || E < 1) return fail(nullptr, MOE_EINVAL, "bad z-loss arguments");
+    if (T > 0 && !logits) return fail(nullptr, MOE_EINVAL, "null logits");
+    if (T == 0) { *loss = NAN; return MOE_OK; }
+    void *buf = nullptr;
+    const size_t n = (size_t)T * E;
+    if (hipMalloc(&buf, sizeof(float) * (n + 4)) != hipSuccess) return fail(nullptr, MOE_EOOM, "hipMalloc failed");
+    float *dl = (float *)buf;
+    float *dout = dl + n;
+    hipError_t e = hipMemcpy(dl, logits, sizeof(float) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_z_loss(dl, T, E, beta, dout, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(loss, dout, sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("z loss failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+int moe_read_counts(moe_handle *h, int32_t *counts) {
+    if (!h || !counts) return fail(h, MOE_EINVAL, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    HIP_TRY(h, hipMemcpy(counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost));
+    return MOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// moe_internal.h -- device helpers and launcher declarations shared by the
+// translation units of libmoe_mi355x.so.  gfx950 (CDNA4) only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_mi355x.h"
+
+namespace moe {
+
+constexpr int kRouteBlock = 256;   // tokens per routing block (one per thread)
+constexpr int kGemmBM = 128;       // grouped-GEMM tile rows (token rows)
+constexpr int kGemmBN = 128;       // grouped-GEMM tile columns
+constexpr int kKPad = 64;          // K (and H) padding of packed weights
+constexpr int kNPad = 128;         // N padding of packed weights
+
+enum ComputeType { CT_F32 = 0, CT_BF16 = 1 };
+enum WeightType { WT_F32 = 0, WT_BF16 = 1, WT_FP8 = 2 };
+enum GemmMode { MODE_GATED_UP = 0, MODE_STD_UP = 1, MODE_DOWN = 2 };
+
+// ---- scalar conversions (host and device) -----------------------------------
+
+// fp32 -> bf16, round to nearest even; NaN stays NaN.
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+}
+
+// OCP fp8 e4m3fn -> fp32, exact.  Encodings 0x7f/0xff (NaN) are never
+// produced by the library's quantiser (it saturates at +-448).
+__host__ __device__ inline float fp8e4m3_to_f32(uint8_t b) {
+    uint32_t em = b & 0x7fu;
+    float v;
+    if (em >= 8u) {
+        uint32_t u = (em << 20) + (120u << 23);
+        __builtin_memcpy(&v, &u, 4);
+    } else {
+        v = (float)em * 0.001953125f;  // subnormal: m * 2^-9
+    }
+    return (b & 0x80u) ? -v : v;
+}
+
+// Julia `isless` total order as an unsigned key: every NaN is largest,
+// -0.0 < +0.0 (src/gating/topk.jl:35 partialsortperm, rev=true).
+__host__ __device__ inline uint32_t isless_key(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---- kernel argument blocks --------------------------------------------------
+
+struct RouteArgs {
+    const float *logits;   // [T][Er]
+    int T, Er, E, gate_kind, k, ns, kt;
+    float *probs;          // [T][E]
+    int *idx;              // [T][kt]
+    float *gates;          // [T][kt]
+    int *rank;             // [T][kt] rank of the entry inside its block & expert
+    int *blk_counts;       // [nblk][E]
+    double *blk_stats;     // [nblk][E+2]: prob sums, sum lse^2, sum entropy
+};
+
+struct ScanArgs {
+    const int *blk_counts;
+    const double *blk_stats;
+    int nblk, T, E, kt;
+    int training, drop, z_enabled;
+    float capacity_factor, alpha, beta;
+    int bm;                // GEMM tile rows
+    int *counts;           // [E]   (after capacity)
+    int *offsets;          // [E+1]
+    int *rank_base;        // [nblk][E] rank of the block's first entry per expert
+    int *cap_out;          // [1] capacity (INT_MAX when unused)
+    int2 *tiles;           // [max_tiles] (expert, m0)
+    int *num_tiles;        // [1]
+    float *scalars;        // [4]: switch, z, loss, mean entropy
+    float *loss_out;       // optional extra destination of the loss
+};
+
+struct PermuteArgs {
+    const void *x; int x_bf16;   // [T][D]
+    int T, D, ld_xp, kt, E;
+    int ct;                      // compute type of xp
+    int *idx; float *gates;      // [T][kt] (rewritten under capacity)
+    const int *rank;             // [T][kt]
+    const int *rank_base;        // [nblk][E]
+    const int *offsets;          // [E+1]
+    const int *cap;              // [1]
+    int renorm;                  // capacity active: renormalise gates
+    int *perm;                   // [T*kt]
+    int *pos_of;                 // [T*kt] (-1 = dropped)
+    float *gate_sorted;          // [T*kt]
+    void *xp;                    // [rows][ld_xp]
+    int copy_rows;               // 0: only the index arrays
+};
+
+struct CombineArgs {
+    const float *y; int ld_y;    // [rows][ld_y]
+    const int *idx; const int *pos_of; const float *gates;
+    int T, D, kt;
+    float *out;                  // [T][D]
+};
+
+struct GemmArgs {
+    const void *A; long long lda;        // activations [rows][lda] (elements)
+    const void *B0; const void *B1;      // packed weights [E][Npad][ldb]
+    long long b_stride;                  // elements per expert
+    long long ldb;                       // = padded K
+    const float *s0; const float *s1;    // per-output-channel scales [E][Npad] or null
+    const float *bias;                   // [E][Npad] or null
+    long long s_stride;                  // = Npad
+    int N;                               // real N (store bound)
+    int K;                               // padded K (multiple of the tile K)
+    void *C; long long ldc;              // output [rows][ldc]
+    const int2 *tiles; const int *num_tiles; const int *counts; const int *offsets;
+    int m_tiles_grid; int n_tiles;
+    int act;
+};
+
+// ---- launchers ----------------------------------------------------------------
+hipError_t launch_router_logits(const void *x, int x_bf16, int T, int D, int Er, int Er_pad,
+                                const float *wr, const float *bias, float *logits, hipStream_t s);
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
+hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
+hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
+hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,
+                              float *out, hipStream_t s);
+hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *out, hipStream_t s);
+hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const GemmArgs &g,
+                               hipStream_t s);
+
+}  // namespace moe

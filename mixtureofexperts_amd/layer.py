@@ -1,0 +1,196 @@
+"""MoEConfig, Router and MoELayer -- src/core/moe_layer.jl, src/core/router.jl.
+
+The layer keeps the reference's call signature, ``layer(x, training=...,
+return_stats=...) -> (output, balance_loss[, stats])`` with ``x`` of Julia
+shape (input_dim, T) and ``output`` (output_dim, T) float32.  The whole
+forward (router GEMM, gating, permute, grouped expert GEMMs, combine, losses,
+statistics) runs in libmoe_mi355x.so on the GPU.
+"""
+from dataclasses import dataclass, field
+from typing import Any, Optional
+
+import numpy as np
+
+from . import _lib
+from ._device import DeviceLayer
+from .activations import activation_code, gelu
+from .balancing import LoadBalancingLoss, SwitchTransformerLoss, balance_alpha
+from .experts import GatedExpert, StandardExpert
+from .gating import GatingMechanism, TopKGating, gate_spec
+
+_DTYPES = {"f32": _lib.MOE_F32, "fp32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3,
+           "fp8_e4m3": _lib.MOE_FP8_E4M3}
+
+
+@dataclass
+class MoEConfig:
+    """Base.@kwdef MoEConfig -- src/core/moe_layer.jl:4-29 (same fields and
+    defaults), plus ``weight_dtype`` (device GEMM precision: "f32" is the
+    reference precision, "bf16" and "fp8" the MI355X paths) and
+    ``max_tokens`` (largest batch the device workspace is sized for)."""
+
+    num_experts: int = 8
+    expert_type: str = "standard"
+    input_dim: int = 768
+    hidden_dim: int = 3072
+    output_dim: int = 768
+    activation: Any = gelu
+    expert_dropout: float = 0.0
+    gate_type: GatingMechanism = field(default_factory=lambda: TopKGating(2))
+    top_k: int = 2
+    noise_scale: float = 0.0
+    use_noise_network: bool = False
+    use_fp32_router: bool = True
+    balance_loss: LoadBalancingLoss = field(default_factory=lambda: SwitchTransformerLoss(0.01))
+    z_loss_weight: float = 0.001
+    capacity_factor: float = 1.25
+    drop_tokens: bool = False
+    use_cur: bool = False
+    cur_rank: Optional[int] = None
+    num_shared_experts: int = 0
+    weight_dtype: str = "f32"
+    max_tokens: int = 4096
+
+
+def create_moe_config(**kwargs):
+    """create_moe_config(; kwargs...) -- src/core/moe_layer.jl:281-283."""
+    return MoEConfig(**kwargs)
+
+
+class Router:
+    """Router -- src/core/router.jl:4-46: ``weight`` (E, input_dim) float32 as
+    Flux Dense(in, E, bias=false) with its default glorot-uniform init
+    (:18); an optional ``bias`` (E,) makes it Dense(W, b)."""
+
+    def __init__(self, input_dim, num_experts, gate_type, *, noise_scale=0.0, use_noise_network=False,
+                 use_fp32=True, rng=None, weight=None, bias=None):
+        rng = np.random.default_rng() if rng is None else rng
+        if weight is None:
+            a = np.sqrt(6.0 / (input_dim + num_experts))
+            weight = rng.uniform(-a, a, size=(num_experts, input_dim)).astype(np.float32)
+        self.weight = np.asarray(weight, dtype=np.float32)
+        self.bias = None if bias is None else np.asarray(bias, dtype=np.float32)
+        self.gate_type = gate_type
+        self.noise_scale = float(noise_scale)
+        self.use_noise_network = bool(use_noise_network)
+        self.use_fp32 = bool(use_fp32)
+
+
+def create_experts(config, rng=None):
+    """create_experts(config) -- src/core/moe_layer.jl:65-102 (full hidden_dim
+    per expert)."""
+    if config.use_cur:
+        raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "CUR experts have no device path")
+    rng = np.random.default_rng() if rng is None else rng
+    wdt = _DTYPES[config.weight_dtype]
+    experts = []
+    for _ in range(config.num_experts):
+        if config.expert_type == "gated":
+            experts.append(GatedExpert(config.input_dim, config.hidden_dim, config.output_dim, config.activation,
+                                       rng=rng, weight_dtype=wdt))
+        else:
+            experts.append(StandardExpert(config.input_dim, config.hidden_dim, config.output_dim, config.activation,
+                                          dropout=config.expert_dropout, rng=rng, weight_dtype=wdt))
+    return experts
+
+
+class MoELayer:
+    """MoELayer(config) -- src/core/moe_layer.jl:34-63."""
+
+    def __init__(self, config, *, rng=None, experts=None, router=None):
+        self.config = config
+        rng = np.random.default_rng() if rng is None else rng
+        self.experts = experts if experts is not None else create_experts(config, rng)
+        self.router = router if router is not None else Router(
+            config.input_dim, config.num_experts - config.num_shared_experts, config.gate_type,
+            noise_scale=config.noise_scale, use_noise_network=config.use_noise_network,
+            use_fp32=config.use_fp32_router, rng=rng)
+        self.balance_loss = config.balance_loss
+        self.training_stats = {
+            "tokens_per_expert": np.zeros(config.num_experts, dtype=np.int64),
+            "routing_entropy": [],
+            "capacity_overflow": 0,
+        }
+        self._dev = None
+
+    # ---- device state ----------------------------------------------------
+    def _check_supported(self, training):
+        c = self.config
+        if c.num_shared_experts > 0:
+            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED,
+                                "MoEConfig.num_shared_experts > 0 (forward_with_shared_experts) has no device path; "
+                                "use SharedExpertGating")
+        if training and c.noise_scale > 0:
+            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "router noise in training has no device path")
+        if training and c.expert_dropout > 0 and c.expert_type != "gated":
+            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "expert dropout in training has no device path")
+
+    def sync_weights(self):
+        """(Re)build the device handle and upload router and expert weights."""
+        c = self.config
+        if self._dev is not None:
+            self._dev.close()
+        spec = gate_spec(self.router.gate_type, self.router.weight.shape[0])
+        self._dev = DeviceLayer(
+            num_experts=c.num_experts, expert_type=(_lib.MOE_EXPERT_GATED if c.expert_type == "gated"
+                                                    else _lib.MOE_EXPERT_STANDARD),
+            input_dim=c.input_dim, hidden_dim=c.hidden_dim, output_dim=c.output_dim,
+            activation=activation_code(c.activation), gate=spec, weight_dtype=_DTYPES[c.weight_dtype],
+            balance_alpha=balance_alpha(self.balance_loss), z_loss_weight=c.z_loss_weight,
+            capacity_factor=c.capacity_factor, drop_tokens=c.drop_tokens, max_tokens=c.max_tokens)
+        self._dev.set_router(np.ascontiguousarray(self.router.weight.T), self.router.bias)
+        for e, ex in enumerate(self.experts):
+            ex.upload(self._dev, e)
+        return self._dev
+
+    def close(self):
+        if self._dev is not None:
+            self._dev.close()
+            self._dev = None
+
+    # ---- forward -----------------------------------------------------------
+    def __call__(self, x, training=False, return_stats=False, x_dtype="f32", _aux=None):
+        """(moe::MoELayer)(x; training, return_stats) -- src/core/moe_layer.jl:107-156.
+
+        x: (input_dim, T) float32, or uint16 bf16 bit patterns with
+        ``x_dtype="bf16"``.  Returns (output (output_dim, T) float32,
+        balance_loss float32[, training_stats])."""
+        self._check_supported(training)
+        xa = np.asarray(x)
+        if xa.ndim != 2 or xa.shape[0] != self.config.input_dim:
+            raise _lib.MoeError(_lib.MOE_EINVAL, f"x must be ({self.config.input_dim}, T), got {xa.shape}")
+        T = xa.shape[1]
+        if T > self.config.max_tokens:
+            raise _lib.MoeError(_lib.MOE_EINVAL, f"batch of {T} tokens exceeds max_tokens={self.config.max_tokens}")
+        if x_dtype == "bf16":
+            xt = np.ascontiguousarray(xa.T, dtype=np.uint16)
+            xcode = _lib.MOE_BF16
+        else:
+            xt = np.ascontiguousarray(xa.T, dtype=np.float32)
+            xcode = _lib.MOE_F32
+        dev = self._dev if self._dev is not None else self.sync_weights()
+        out, loss, res = dev.forward(xt, xcode, training, want_aux=_aux is not None)
+        if _aux is not None:
+            _aux.update(res)
+        # update_stats! -- src/core/moe_layer.jl:250-264
+        self.training_stats["tokens_per_expert"] += res["counts"].astype(np.int64)
+        self.training_stats["routing_entropy"].append(np.float32(res["mean_entropy"]))
+        output = out.T
+        loss = np.float32(loss)
+        if return_stats:
+            return output, loss, self.training_stats
+        return output, loss
+
+
+def reset_stats(moe):
+    """reset_stats!(moe) -- src/core/moe_layer.jl:271-276."""
+    moe.training_stats["tokens_per_expert"][:] = 0
+    moe.training_stats["routing_entropy"].clear()
+    moe.training_stats["capacity_overflow"] = 0
+
+
+def create_moe_layer(input_dim, hidden_dim, output_dim, **kwargs):
+    """create_moe_layer(input_dim, hidden_dim, output_dim; kwargs...) --
+    src/core/moe_layer.jl:285-293."""
+    rng = kwargs.pop("rng", None)
+    return MoELayer(MoEConfig(input_dim=input_dim, hidden_dim=hidden_dim, output_dim=output_dim, **kwargs), rng=rng)

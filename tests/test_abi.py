@@ -1,0 +1,132 @@
+"""CPU checks of the C ABI boundary: the library loads, exports every symbol
+include/moe_mi355x.h declares, and rejects bad configurations before touching
+the device.  No compute call is made (no GPU here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "moe_mi355x.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|char\s*\*|const char\s*\*)\s*\*?\s*(moe_\w+)\s*\(",
+                                 text, flags=re.M)))
+
+
+def test_header_parses():
+    fns = header_functions()
+    assert "moe_forward" in fns and "moe_create" in fns and len(fns) >= 20
+
+
+def test_library_exports_every_declared_symbol(moe):
+    from mixtureofexperts_amd import _lib
+
+    L = _lib.lib()
+    for name in header_functions():
+        assert hasattr(L, name), name
+    assert sorted(_lib.EXPORTED_SYMBOLS) == header_functions()
+
+
+def test_abi_version(moe):
+    from mixtureofexperts_amd import _lib
+
+    assert _lib.lib().moe_abi_version() == 1
+
+
+def _cfg(**kw):
+    from mixtureofexperts_amd import _lib
+
+    c = _lib.MoeConfigC()
+    c.num_experts, c.expert_type, c.input_dim, c.hidden_dim, c.output_dim = 8, 0, 64, 128, 64
+    c.activation, c.gate_kind, c.top_k, c.gate_num_shared, c.weight_dtype = 1, 0, 2, 0, 1
+    c.balance_alpha, c.z_loss_weight, c.capacity_factor, c.drop_tokens, c.max_tokens = 0.01, 0.001, 1.25, 0, 64
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(num_experts=0), "num_experts"),
+    (dict(num_experts=129), "num_experts"),
+    (dict(top_k=9), "top_k"),
+    (dict(top_k=0), "top_k"),
+    (dict(top_k=9, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(gate_kind=2, gate_num_shared=8), "gate_num_shared"),
+    (dict(gate_kind=2, gate_num_shared=2, top_k=7, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(gate_kind=7), "gate_kind"),
+    (dict(weight_dtype=5), "weight_dtype"),
+    (dict(max_tokens=0), "max_tokens"),
+    (dict(input_dim=0), "dimensions"),
+    (dict(drop_tokens=1, capacity_factor=0.0), "capacity_factor"),
+])
+def test_create_rejects_bad_config(moe, bad, msg):
+    from mixtureofexperts_amd import _lib
+
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    rc = L.moe_create(ctypes.byref(_cfg(**bad)), ctypes.byref(h))
+    assert rc == _lib.MOE_EINVAL
+    assert h.value is None
+    assert msg in L.moe_last_error(None).decode()
+
+
+def test_null_handle_calls_fail_cleanly(moe):
+    from mixtureofexperts_amd import _lib
+
+    L = _lib.lib()
+    assert L.moe_forward(None, None, 0, 1, 0, None, None, None) == _lib.MOE_EINVAL
+    assert L.moe_set_router(None, None, None) == _lib.MOE_EINVAL
+    assert L.moe_destroy(None) == _lib.MOE_OK
+    assert L.moe_router_outputs(None) == -1
+
+
+def test_loss_argument_checks(moe):
+    from mixtureofexperts_amd import _lib
+
+    L = _lib.lib()
+    out = ctypes.c_float(0)
+    assert L.moe_switch_loss(None, 4, 0, None, 8, 0.01, ctypes.byref(out)) == _lib.MOE_EINVAL
+    assert L.moe_z_loss(None, 4, 8, 0.001, ctypes.byref(out)) == _lib.MOE_EINVAL
+    # T = 0: means over no tokens are NaN, as Julia's mean of an empty array
+    assert L.moe_z_loss(None, 0, 8, 0.001, ctypes.byref(out)) == _lib.MOE_OK and np.isnan(out.value)
+
+
+def test_host_mirror_config_defaults(moe):
+    # MoEConfig defaults mirror src/core/moe_layer.jl:4-29
+    c = moe.MoEConfig()
+    assert (c.num_experts, c.expert_type, c.input_dim, c.hidden_dim, c.output_dim) == (8, "standard", 768, 3072, 768)
+    assert c.activation is moe.gelu and isinstance(c.gate_type, moe.TopKGating) and c.gate_type.k == 2
+    assert c.z_loss_weight == 0.001 and c.capacity_factor == 1.25 and c.drop_tokens is False
+    assert isinstance(c.balance_loss, moe.SwitchTransformerLoss) and abs(c.balance_loss.alpha - 0.01) < 1e-9
+    assert c.num_shared_experts == 0 and c.use_fp32_router is True
+
+
+def test_host_mirror_rejects_unsupported_before_device(moe):
+    from mixtureofexperts_amd import _lib
+
+    layer = moe.MoELayer(moe.MoEConfig(input_dim=8, hidden_dim=16, output_dim=8, num_shared_experts=2))
+    with pytest.raises(moe.MoeError) as ei:
+        layer(np.zeros((8, 4), np.float32))
+    assert ei.value.status == _lib.MOE_EUNSUPPORTED
+    layer = moe.MoELayer(moe.MoEConfig(input_dim=8, hidden_dim=16, output_dim=8, noise_scale=0.1))
+    with pytest.raises(moe.MoeError):
+        layer(np.zeros((8, 4), np.float32), training=True)
+    with pytest.raises(moe.MoeError):
+        moe.gating.gate_spec(object(), 8)
+    with pytest.raises(moe.MoeError):
+        moe.activations.activation_code(lambda v: v)
+
+
+def test_gate_spec_mapping(moe):
+    from mixtureofexperts_amd import _lib
+
+    assert tuple(moe.gating.gate_spec(moe.TopKGating(3), 8)) == (_lib.MOE_GATE_TOPK, 3, 0)
+    assert tuple(moe.gating.gate_spec(moe.SwitchGating(), 8)) == (_lib.MOE_GATE_SWITCH, 1, 0)
+    g = moe.SharedExpertGating(2, moe.TopKGating(6), 66)
+    assert tuple(moe.gating.gate_spec(g, 66)) == (_lib.MOE_GATE_SHARED, 6, 2)

@@ -1,0 +1,270 @@
+"""GPU parity of the full MoE-layer forward (router GEMM, gating, permute,
+grouped expert GEMMs, combine, losses, statistics) through the C ABI against
+the oracle on identical seeded inputs.
+
+Tolerances (north star): layer output relative error (Frobenius) <= 1e-4 at
+fp32, 2e-2 at bf16, 5e-2 at fp8 weights; balance loss within 1e-5; routing
+bit-exact given identical router logits (the oracle is run on the GPU's
+logits; the logits themselves are checked against the oracle's fp32 GEMM)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "bf16": 2e-2, "fp8": 5e-2}
+
+
+def rel_err(a, b):
+    return float(np.linalg.norm((a - b).astype(np.float64)) / max(np.linalg.norm(b.astype(np.float64)), 1e-30))
+
+
+class Case:
+    """Seeded weights + inputs, uploaded to a device handle and kept as the
+    fp32 values the oracle sees (bf16 / fp8 weights dequantised)."""
+
+    def __init__(self, moe, oracle, *, T, D, H, Dout=None, E, k, gate="topk", ns=0, expert_type="gated", act="silu",
+                 wdtype="f32", xdtype="f32", seed=0, router_bias=None, alpha=0.01, z=0.001, drop=False, cf=1.25,
+                 max_tokens=None, wscale=None):
+        from mixtureofexperts_amd import _lib
+        from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+        self.oracle = oracle
+        Dout = D if Dout is None else Dout
+        rng = np.random.default_rng(seed)
+        self.T, self.D, self.H, self.Dout, self.E, self.k = T, D, H, Dout, E, k
+        self.gate, self.ns, self.expert_type, self.act = gate, ns, expert_type, act
+        self.alpha, self.z, self.drop, self.cf = alpha, z, drop, cf
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        if xdtype == "bf16":
+            self.x_dev = oracle.f32_to_bf16_bits(x)
+            self.x = oracle.bf16_bits_to_f32(self.x_dev)
+            self.xcode = _lib.MOE_BF16
+        else:
+            self.x_dev = self.x = x
+            self.xcode = _lib.MOE_F32
+        self.wr = (rng.standard_normal((E, D)) * (1.0 / np.sqrt(D))).astype(np.float32)
+        self.rb = router_bias
+        s_in = np.sqrt(2.0 / D) if wscale is None else wscale
+        s_h = np.sqrt(2.0 / H) if wscale is None else wscale
+        self.ex, dev_ex = [], []
+        for _ in range(E):
+            w1 = (rng.standard_normal((H, D)) * s_in).astype(np.float32)
+            w2 = (rng.standard_normal((Dout, H)) * (s_in if expert_type == "gated" else s_h)).astype(np.float32)
+            w3 = (rng.standard_normal((H, D)) * s_in).astype(np.float32) if expert_type == "gated" else None
+            b1 = (rng.standard_normal(H) * 0.1).astype(np.float32) if expert_type != "gated" else None
+            b2 = (rng.standard_normal(Dout) * 0.1).astype(np.float32) if expert_type != "gated" else None
+            mats = [w1, w2, w3]
+            if wdtype == "bf16":
+                dv = [None if m is None else oracle.f32_to_bf16_bits(m) for m in mats]
+                ov = [None if m is None else oracle.bf16_bits_to_f32(b) for m, b in zip(mats, dv)]
+                dev_ex.append(dict(src=_lib.MOE_BF16, w=dv, s=[None] * 3))
+            elif wdtype == "fp8":
+                q = [None if m is None else oracle.quantize_fp8_rows(m) for m in mats]
+                ov = [None if c is None else oracle.dequantize_fp8_rows(*c) for c in q]
+                dev_ex.append(dict(src=_lib.MOE_FP8_E4M3, w=[None if c is None else c[0] for c in q],
+                                   s=[None if c is None else c[1] for c in q]))
+            else:
+                ov = mats
+                dev_ex.append(dict(src=_lib.MOE_F32, w=mats, s=[None] * 3))
+            self.ex.append(dict(w1=ov[0], w2=ov[1], w3=ov[2], b1=b1, b2=b2))
+            dev_ex[-1]["b"] = (b1, b2)
+        spec = {"topk": GateSpec(_lib.MOE_GATE_TOPK, k, 0), "switch": GateSpec(_lib.MOE_GATE_SWITCH, 1, 0),
+                "shared": GateSpec(_lib.MOE_GATE_SHARED, k, ns)}[gate]
+        acts = {"silu": _lib.MOE_ACT_SILU, "gelu": _lib.MOE_ACT_GELU, "relu": _lib.MOE_ACT_RELU,
+                "identity": _lib.MOE_ACT_IDENTITY}
+        wcode = {"f32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3}[wdtype]
+        print(f"layer case T={T} D={D} H={H} E={E} k={k} gate={gate} ns={ns} type={expert_type} w={wdtype} "
+              f"x={xdtype}", flush=True)
+        self.dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED if expert_type == "gated"
+                               else _lib.MOE_EXPERT_STANDARD, input_dim=D, hidden_dim=H, output_dim=Dout,
+                               activation=acts[act], gate=spec, weight_dtype=wcode, balance_alpha=alpha,
+                               z_loss_weight=z, capacity_factor=cf, drop_tokens=drop,
+                               max_tokens=max_tokens or T)
+        self.dev.set_router(np.ascontiguousarray(self.wr.T), router_bias)
+        for e, d in enumerate(dev_ex):
+            self.dev.set_expert(e, d["w"][0], d["w"][1], d["w"][2], d["b"][0], d["b"][1], src_dtype=d["src"],
+                                s1=d["s"][0], s2=d["s"][1], s3=d["s"][2])
+
+    def run(self, training=True, T=None):
+        T = self.T if T is None else T
+        out, loss, res = self.dev.forward(np.ascontiguousarray(self.x_dev[:T]), self.xcode, training, want_aux=True)
+        return out, loss, res
+
+    def oracle_forward(self, logits, training=True, T=None):
+        T = self.T if T is None else T
+        return self.oracle.moe_forward(self.x[:T], self.wr, self.ex, gate=self.gate, k=self.k, num_shared=self.ns,
+                                       expert_type=self.expert_type, act=self.act, alpha=self.alpha,
+                                       z_weight=self.z, training=training, drop_tokens=self.drop,
+                                       capacity_factor=self.cf, logits=logits)
+
+
+def check_case(case, tol, training=True, T=None):
+    out, loss, res = case.run(training, T)
+    # logits: fp32 GEMM vs the oracle's OpenBLAS sgemm
+    T = case.T if T is None else T
+    ref_logits = (case.x[:T] @ case.wr.T).astype(np.float32)
+    if case.rb is not None:
+        ref_logits = ref_logits + case.rb
+    assert np.max(np.abs(res["logits"] - ref_logits)) <= 1e-5 * max(1.0, np.max(np.abs(ref_logits)))
+    # routing bit-exact given the GPU's logits
+    ref_out, ref_loss, aux = case.oracle_forward(res["logits"], training, T)
+    assert np.array_equal(res["indices"], aux["idx"])
+    assert np.array_equal(res["gates"].view(np.uint32), aux["gates"].view(np.uint32))
+    assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32))
+    assert np.array_equal(res["counts"], aux["counts"])
+    assert np.array_equal(res["offsets"], aux["offsets"])
+    n = int(aux["offsets"][-1])
+    assert np.array_equal(res["perm"][:n], aux["perm"])
+    # layer output and losses
+    err = rel_err(out, ref_out)
+    assert err <= tol, f"relative error {err:.3e} > {tol}"
+    assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (loss, ref_loss)
+    assert abs(res["mean_entropy"] - aux["mean_entropy"]) <= 1e-5 * max(1.0, abs(float(aux["mean_entropy"])))
+    if not training:
+        assert loss == 0.0
+    return out, err
+
+
+def test_readme_config_fp32(moe, oracle):
+    # README MoELayer, 8 gated silu experts, 512/2048/512,
+    # TopKGating(2), SwitchTransformerLoss(0.01), x randn(512, 32), fp32
+    c = Case(moe, oracle, T=32, D=512, H=2048, E=8, k=2, wdtype="f32", seed=1)
+    check_case(c, TOL["f32"], training=True)
+    check_case(c, TOL["f32"], training=False)
+
+
+@pytest.mark.parametrize("wdtype,xdtype", [("f32", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("fp8", "bf16")])
+def test_gated_dtypes(moe, oracle, wdtype, xdtype):
+    c = Case(moe, oracle, T=700, D=256, H=384, E=8, k=2, wdtype=wdtype, xdtype=xdtype, seed=2)
+    check_case(c, TOL[wdtype])
+
+
+def test_mixtral_shape_scaled(moe, oracle):
+    # C3 structure at reduced size: bf16, skewed router bias
+    rng = np.random.default_rng(3)
+    bias = rng.standard_normal(8).astype(np.float32)
+    c = Case(moe, oracle, T=1024, D=1024, H=1792, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=3,
+             router_bias=bias, wscale=0.02)
+    check_case(c, TOL["bf16"])
+
+
+def test_standard_experts_gelu(moe, oracle):
+    # C5 structure at reduced size: StandardExpert + gelu + biases, SwitchGating
+    for wd in ("f32", "bf16"):
+        c = Case(moe, oracle, T=2048, D=192, H=384, E=32, k=1, gate="switch", expert_type="standard",
+                 act="gelu", wdtype=wd, xdtype="bf16" if wd == "bf16" else "f32", seed=4)
+        check_case(c, TOL[wd])
+
+
+def test_shared_expert_gating_fp8(moe, oracle):
+    # C4 structure at reduced size: SharedExpertGating(2, TopKGating(6), 18), fp8 weights
+    c = Case(moe, oracle, T=1500, D=256, H=192, E=18, k=6, gate="shared", ns=2, wdtype="fp8", xdtype="bf16",
+             seed=5)
+    check_case(c, TOL["fp8"])
+
+
+def test_capacity_drop_tokens(moe, oracle):
+    rng = np.random.default_rng(6)
+    c = Case(moe, oracle, T=600, D=128, H=256, E=8, k=2, wdtype="f32", seed=6, drop=True, cf=0.75,
+             router_bias=(rng.standard_normal(8) * 2).astype(np.float32))
+    out, _ = check_case(c, TOL["f32"], training=True)
+    check_case(c, TOL["f32"], training=False)
+
+
+def test_other_activations_and_odd_sizes(moe, oracle):
+    # dims that are not multiples of the tiles (padding paths)
+    c = Case(moe, oracle, T=77, D=100, H=150, Dout=90, E=5, k=3, act="relu", wdtype="f32", seed=7)
+    check_case(c, TOL["f32"])
+    c = Case(moe, oracle, T=77, D=100, H=150, Dout=90, E=5, k=3, act="identity", wdtype="bf16", seed=8)
+    check_case(c, TOL["bf16"])
+
+
+def test_varying_batch_on_one_handle(moe, oracle):
+    c = Case(moe, oracle, T=300, D=128, H=256, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=9)
+    for T in (300, 1, 7, 129, 300):
+        check_case(c, TOL["bf16"], T=T)
+
+
+def test_forward_is_deterministic(moe, oracle):
+    c = Case(moe, oracle, T=512, D=256, H=512, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=10)
+    a = c.run()[0]
+    b = c.run()[0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_expert_known_answer_dense_llama_ffn(moe, oracle):
+    # the reference's known-answer check (test_moeLlama2_integration.jl:132-164):
+    # a gated expert equals the dense Llama FFN w2(silu(w1 x) .* (w3 x)) (< 1e-5)
+    from mixtureofexperts_amd import _lib
+    from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+    rng = np.random.default_rng(11)
+    dim, hid = 256, 688
+    x = rng.standard_normal((5, dim)).astype(np.float32)
+    w1 = (rng.standard_normal((dim, hid)) * 0.02).astype(np.float32)  # Llama (in, out)
+    w2 = (rng.standard_normal((hid, dim)) * 0.02).astype(np.float32)
+    w3 = (rng.standard_normal((dim, hid)) * 0.02).astype(np.float32)
+    dev = DeviceLayer(num_experts=1, expert_type=_lib.MOE_EXPERT_GATED, input_dim=dim, hidden_dim=hid,
+                      output_dim=dim, activation=_lib.MOE_ACT_SILU, gate=GateSpec(_lib.MOE_GATE_SWITCH, 1, 0),
+                      weight_dtype=_lib.MOE_F32, balance_alpha=0.0, z_loss_weight=0.0, capacity_factor=1.0,
+                      drop_tokens=False, max_tokens=8)
+    # Llama (in, out) column-major == Flux-layout memory [in][out]... pass as FLUX_OUT_IN memory
+    dev.set_expert(0, np.ascontiguousarray(w1), np.ascontiguousarray(w2), np.ascontiguousarray(w3),
+                   src_dtype=_lib.MOE_F32, layout=_lib.MOE_LAYOUT_FLUX_OUT_IN)
+    y = dev.expert_forward(0, x)
+    for t in range(5):
+        hb1 = w1.T @ x[t]
+        hb2 = w3.T @ x[t]
+        h = hb1 * (np.float32(1) / (np.float32(1) + np.exp(-hb1))) * hb2
+        dense = w2.T @ h
+        assert np.max(np.abs(dense - y[t])) < 1e-5
+    dev.close()
+
+
+def test_python_api_readme_flow(moe, oracle):
+    # README usage: MoELayer(config)(x; training=true) with silu passed explicitly
+    rng = np.random.default_rng(12)
+    cfg = moe.MoEConfig(num_experts=8, expert_type="gated", input_dim=512, hidden_dim=2048, output_dim=512,
+                        activation=moe.silu, gate_type=moe.TopKGating(2),
+                        balance_loss=moe.SwitchTransformerLoss(0.01), max_tokens=64)
+    layer = moe.MoELayer(cfg, rng=rng)
+    x = rng.standard_normal((512, 32)).astype(np.float32)
+    aux = {}
+    out, loss = layer(x, training=True, _aux=aux)
+    assert out.shape == (512, 32) and out.dtype == np.float32 and np.all(np.isfinite(out))
+    assert loss >= 0
+    ex = [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]
+    ref, ref_loss, oa = oracle.moe_forward(x.T, layer.router.weight, ex, k=2, training=True, logits=aux["logits"])
+    assert rel_err(out.T, ref) <= 1e-4
+    assert abs(loss - ref_loss) <= 1e-5
+    assert layer.training_stats["tokens_per_expert"].sum() == 64
+    assert len(layer.training_stats["routing_entropy"]) == 1
+    out2, loss2, stats = layer(x, training=False, return_stats=True)
+    assert loss2 == 0.0 and stats["tokens_per_expert"].sum() == 128
+    moe.reset_stats(layer)
+    assert layer.training_stats["tokens_per_expert"].sum() == 0
+    # expert functor on the device: (e::Expert)(x)
+    y = layer.experts[3](x[:, :4])
+    yref = oracle.gated_expert(x[:, :4].T, layer.experts[3].w1, layer.experts[3].w2, layer.experts[3].w3,
+                               oracle.act_silu).T
+    assert rel_err(y, yref) <= 1e-4
+    layer.close()
+
+
+def test_async_device_path_matches_host(moe, oracle):
+    torch = pytest.importorskip("torch")
+    import ctypes
+
+    from mixtureofexperts_amd import _lib
+
+    c = Case(moe, oracle, T=640, D=256, H=512, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=13)
+    ref, ref_loss, _ = c.run(training=True)
+    x = torch.from_numpy(c.x_dev.view(np.int16)).cuda().view(torch.bfloat16)
+    out = torch.empty((c.T, c.Dout), dtype=torch.float32, device="cuda")
+    loss = torch.zeros(1, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    _lib.check(_lib.lib().moe_forward_async(c.dev.h, x.data_ptr(), _lib.MOE_BF16, c.T, 1, out.data_ptr(),
+                                            loss.data_ptr(), ctypes.c_void_p(stream.cuda_stream)), c.dev.h)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert float(loss.item()) == ref_loss
