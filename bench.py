@@ -165,11 +165,17 @@ def main():
 
     cfg = CONFIGS[args.config]
     T, D, H, E, k = cfg["T"], cfg["D"], cfg["H"], cfg["E"], cfg["k"]
+    # A dedicated (default-priority) stream: every kernel of the step and every
+    # timing event go to it, so the events bracket exactly the launched kernels.
+    # (torch's current stream is the null stream, which the ABI reads as "the
+    # handle's own stream".)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     wl = build_workload(cfg)
     L = _lib.lib()
     h = wl["layer"].h
-    stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
+    assert sp.value, "bench stream must not be the null stream"
     xp, op, lp = wl["x"].data_ptr(), wl["out"].data_ptr(), wl["loss"].data_ptr()
     xcode = wl["xcode"]
 

@@ -113,6 +113,9 @@ int moe_router_outputs(const moe_handle *h);
 int moe_slots_per_token(const moe_handle *h);
 
 /* ---- weights (uploaded once, prepacked, device resident) --------------- */
+/* Weight sources may be host or device memory.  When any source is device
+ * memory the call first waits for the whole device (hipDeviceSynchronize), so
+ * kernels that produced it on any stream have finished before it is read. */
 
 /* Router weight -- src/core/router.jl:18 Dense(in, E, bias=false):
  * weight (E_router, D) column-major = memory [D][E_router] fp32.  bias may be

@@ -97,6 +97,16 @@ def lib():
             f"{LIB_PATH} is missing: build it with `python -m mixtureofexperts_amd.build` "
             "(there is no CPU fallback)"
         )
+    # One HIP runtime per process.  The torch wheel bundles its own
+    # libamdhip64 / libhsa-runtime64 (SONAMEs libamdhip64.so.7 and
+    # libhsa-runtime64.so.1) but its own libraries ask for them under other
+    # names.  Loading torch first makes this library's dependencies resolve to
+    # those already-loaded copies; loading this library first would make torch
+    # bring in a second HSA runtime, which then finds no GPU.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, f32p = ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_float)
     L.moe_create.argtypes = [ctypes.POINTER(MoeConfigC), ctypes.POINTER(vp)]

@@ -581,6 +581,9 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     if (!weight) return fail(h, MOE_EINVAL, "null router weight");
     const bool dev_w = is_device_ptr(weight);
     const bool dev_b = bias && is_device_ptr(bias);
+    // device sources may still be in flight on another stream (this handle's
+    // stream does not order with the caller's): wait for the whole device
+    if (dev_w || dev_b) HIP_TRY(h, hipDeviceSynchronize());
     // memory [D][Er] -> [D][Er_pad]
     HIP_TRY(h, hipMemcpy2DAsync(h->wr, sizeof(float) * h->Er_pad, weight, sizeof(float) * h->Er,
                                 sizeof(float) * h->Er, h->D, dev_w ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
@@ -605,6 +608,15 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
     if (!w1 || !w2 || (h->gated && !w3)) return fail(h, MOE_EINVAL, "missing expert weight matrix");
     if (src_dtype == MOE_FP8_E4M3 && (!s1 || !s2 || (h->gated && !s3)))
         return fail(h, MOE_EINVAL, "fp8 weights need per-output-channel scales");
+    // device sources may still be in flight on another stream (this handle's
+    // stream does not order with the caller's): wait for the whole device
+    {
+        const void *srcs[8] = {w1, w2, w3, b1, b2, s1, s2, s3};
+        bool any_dev = false;
+        for (const void *p : srcs)
+            if (p && is_device_ptr(p)) any_dev = true;
+        if (any_dev) HIP_TRY(h, hipDeviceSynchronize());
+    }
     const size_t wsz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
     uint8_t *w1d = (uint8_t *)h->w1 + wsz * (size_t)expert * h->w1_stride;
     uint8_t *w2d = (uint8_t *)h->w2 + wsz * (size_t)expert * h->w2_stride;

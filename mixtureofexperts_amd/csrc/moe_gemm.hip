@@ -99,8 +99,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
     const long long lda_b = g.lda * ESZ;
     constexpr int WSZ = (WT == WT_FP8) ? 1 : ESZ;  // stored weight element size
     const long long ldb_b = g.ldb * WSZ;
-    const uint8_t *Bb0 = (const uint8_t *)g.B0 + ((long long)e * g.b_stride + n0) * WSZ;
-    const uint8_t *Bb1 = (NB == 2) ? (const uint8_t *)g.B1 + ((long long)e * g.b_stride + n0) * WSZ : Bb0;
+    // packed weights [E][Npad][ldb]: this tile's first row is n0 of expert e
+    const uint8_t *Bb0 = (const uint8_t *)g.B0 + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * WSZ;
+    const uint8_t *Bb1 =
+        (NB == 2) ? (const uint8_t *)g.B1 + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * WSZ : Bb0;
 
 #define MOE_LOAD_TILES(KT_)                                                                            \
     do {                                                                                              \
