@@ -41,12 +41,15 @@ struct moe_handle {
 
     // workspace
     int T_max = 0, nblk_max = 0, rows_max = 0, max_tiles = 0;
+    int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
+    bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
     double *blk_stats = nullptr;
     int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
     int2 *tiles = nullptr;
     int *num_tiles = nullptr;
+    int *tile_start = nullptr;
     float *scalars = nullptr;
     int *perm = nullptr, *pos_of = nullptr;
     void *xp = nullptr, *hbuf = nullptr;
@@ -325,7 +328,7 @@ static int check_ready(moe_handle *h) {
 }
 
 static int m_tiles_for(const moe_handle *h, int T) {
-    long long mt = (long long)T * h->kt / kGemmBM + h->E;
+    long long mt = (long long)T * h->kt / h->bm + h->E;
     if (mt > h->max_tiles) mt = h->max_tiles;
     return (int)mt;
 }
@@ -359,7 +362,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kt;
     sa.training = training; sa.drop = h->cfg.drop_tokens; sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
-    sa.bm = kGemmBM; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
+    sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
     sa.loss_out = loss_dev;
     HIP_TRY(h, launch_scan(sa, s));
@@ -375,7 +378,10 @@ static GemmArgs up_args(moe_handle *h, int mt_grid) {
     g.s0 = h->s1; g.s1 = h->s3; g.bias = h->gated ? nullptr : h->b1; g.s_stride = h->H_pad;
     g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
-    g.m_tiles_grid = mt_grid; g.n_tiles = h->H_pad / kGemmBN; g.act = h->cfg.activation;
+    g.tile_start = h->tile_start; g.E = h->E;
+    g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
+    // bf16 kernel: 128 h columns (gated, W1 and W3 rows) or 256 rows per tile
+    g.n_tiles = h->bf16_gemm ? h->H_pad / (h->gated ? 128 : 256) : h->H_pad / kGemmBN;
     return g;
 }
 
@@ -387,15 +393,30 @@ static GemmArgs down_args(moe_handle *h, int mt_grid) {
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
-    g.m_tiles_grid = mt_grid; g.n_tiles = h->Dout_npad / kGemmBN; g.act = h->cfg.activation;
+    g.tile_start = h->tile_start; g.E = h->E;
+    g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
+    g.n_tiles = h->bf16_gemm ? h->Dout_npad / 256 : h->Dout_npad / kGemmBN;
     return g;
+}
+
+// The expert up GEMM (W1/W3 or W1 + activation) and the down GEMM (W2) over
+// mt_grid M tiles: the LDS-DMA bf16 kernel for bf16 weights, the
+// register-staged kernel for fp32 and fp8 weights.
+static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
+    const int mode = h->gated ? MODE_GATED_UP : MODE_STD_UP;
+    if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, up_args(h, mt_grid), s);
+    return launch_grouped_gemm(mode, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0, up_args(h, mt_grid), s);
+}
+
+static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s) {
+    if (h->bf16_gemm) return launch_grouped_gemm_bf16(MODE_DOWN, h->bm, down_args(h, mt_grid), s);
+    return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid), s);
 }
 
 static int run_experts(moe_handle *h, int T, hipStream_t s) {
     const int mt = m_tiles_for(h, T);
-    HIP_TRY(h, launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0,
-                                   up_args(h, mt), s));
-    HIP_TRY(h, launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt), s));
+    HIP_TRY(h, launch_up(h, mt, s));
+    HIP_TRY(h, launch_down(h, mt, s));
     return MOE_OK;
 }
 
@@ -468,7 +489,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
     h->kt = h->ns + h->k;
     h->D_pad = (int)round_up(h->D, kKPad);
-    h->H_pad = (int)round_up(h->H, kNPad);  // N of the up GEMM, K of the down GEMM
+    // N of the up GEMM, K of the down GEMM: a whole number of up-GEMM tiles
+    h->H_pad = (int)round_up(h->H, cfg->expert_type == MOE_EXPERT_GATED ? kNPadGated : kNPad);
     h->Dout_npad = (int)round_up(h->Dout, kNPad);
     h->ct = (cfg->weight_dtype == MOE_F32) ? CT_F32 : CT_BF16;
     h->wt = (cfg->weight_dtype == MOE_F32) ? WT_F32 : (cfg->weight_dtype == MOE_BF16 ? WT_BF16 : WT_FP8);
@@ -513,7 +535,10 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->T_max = cfg->max_tokens;
     h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
     h->rows_max = h->T_max * h->kt;
-    h->max_tiles = h->rows_max / kGemmBM + h->E + 1;
+    h->bf16_gemm = h->ct == CT_BF16 && h->wt == WT_BF16;
+    // 256-row tiles when experts average at least 384 rows at max_tokens, else 128
+    h->bm = (h->bf16_gemm && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
+    h->max_tiles = h->rows_max / h->bm + h->E + 1;
     const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
     A((void **)&h->probs, sizeof(float) * T * E);
@@ -528,6 +553,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->cap, sizeof(int));
     A((void **)&h->tiles, sizeof(int2) * (size_t)h->max_tiles);
     A((void **)&h->num_tiles, sizeof(int));
+    A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
     A((void **)&h->perm, sizeof(int) * T * kt);
     A((void **)&h->pos_of, sizeof(int) * T * kt);
@@ -736,9 +762,11 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     std::vector<int> cnt(h->E, 0), off(h->E + 1, 0);
     cnt[expert] = n;
     for (int e = 0; e < h->E; ++e) off[e + 1] = off[e] + cnt[e];
-    const int nt = (n + kGemmBM - 1) / kGemmBM;
+    const int nt = (n + h->bm - 1) / h->bm;
     std::vector<int2> tl(nt);
-    for (int i = 0; i < nt; ++i) tl[i] = make_int2(expert, i * kGemmBM);
+    for (int i = 0; i < nt; ++i) tl[i] = make_int2(expert, i * h->bm);
+    std::vector<int> ts(h->E + 1, 0);
+    for (int e = 0; e <= h->E; ++e) ts[e] = e > expert ? nt : 0;
     void *xs = nullptr;
     HIP_TRY(h, hipMalloc(&xs, sizeof(float) * (size_t)n * h->D));
     hipError_t e = hipMemcpyAsync(xs, x, sizeof(float) * (size_t)n * h->D, hipMemcpyHostToDevice, s);
@@ -746,14 +774,15 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     if (e == hipSuccess) e = hipMemcpyAsync(h->offsets, off.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(h->tiles, tl.data(), sizeof(int2) * nt, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(h->num_tiles, &nt, sizeof(int), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(h->tile_start, ts.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(convert_rows_kernel, dim3(1024), dim3(256), 0, s, (const void *)xs, 0, n, h->D, h->ct,
                            h->xp, h->D_pad);
         e = hipGetLastError();
     }
-    if (e == hipSuccess) e = launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt,
-                                                 h->ct == CT_BF16 ? 1 : 0, up_args(h, nt), s);
-    if (e == hipSuccess) e = launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, nt), s);
+    if (e == hipSuccess) e = launch_up(h, nt, s);
+    if (e == hipSuccess) e = launch_down(h, nt, s);
     if (e == hipSuccess) e = hipMemcpyAsync(y, h->y, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s);
     hipError_t e2 = hipStreamSynchronize(s);
     if (e == hipSuccess) e = e2;
@@ -802,8 +831,7 @@ int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream) {
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    HIP_TRY(h, launch_grouped_gemm(h->gated ? MODE_GATED_UP : MODE_STD_UP, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0,
-                                   up_args(h, m_tiles_for(h, T)), s));
+    HIP_TRY(h, launch_up(h, m_tiles_for(h, T), s));
     return MOE_OK;
 }
 
@@ -813,7 +841,7 @@ int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream) {
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    HIP_TRY(h, launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, m_tiles_for(h, T)), s));
+    HIP_TRY(h, launch_down(h, m_tiles_for(h, T), s));
     return MOE_OK;
 }
 

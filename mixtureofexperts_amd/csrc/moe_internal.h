@@ -9,10 +9,11 @@
 namespace moe {
 
 constexpr int kRouteBlock = 256;   // tokens per routing block (one per thread)
-constexpr int kGemmBM = 128;       // grouped-GEMM tile rows (token rows)
-constexpr int kGemmBN = 128;       // grouped-GEMM tile columns
-constexpr int kKPad = 64;          // K (and H) padding of packed weights
-constexpr int kNPad = 128;         // N padding of packed weights
+constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
+constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
+constexpr int kKPad = 64;          // K padding of packed weights and activation rows
+constexpr int kNPadGated = 128;    // N padding of W1/W3 (bf16 gated up tile: 128 h columns)
+constexpr int kNPad = 256;         // N padding of every other packed weight (bf16 tile: 256 rows)
 
 enum ComputeType { CT_F32 = 0, CT_BF16 = 1 };
 enum WeightType { WT_F32 = 0, WT_BF16 = 1, WT_FP8 = 2 };
@@ -79,6 +80,7 @@ struct ScanArgs {
     int training, drop, z_enabled;
     float capacity_factor, alpha, beta;
     int bm;                // GEMM tile rows
+    int *tile_start;       // [E+1] first M tile of each expert (sum of ceil(count / bm))
     int *counts;           // [E]   (after capacity)
     int *offsets;          // [E+1]
     int *rank_base;        // [nblk][E] rank of the block's first entry per expert
@@ -125,6 +127,8 @@ struct GemmArgs {
     int K;                               // padded K (multiple of the tile K)
     void *C; long long ldc;              // output [rows][ldc]
     const int2 *tiles; const int *num_tiles; const int *counts; const int *offsets;
+    const int *tile_start;               // [E+1] (bf16 kernel work list)
+    int E;
     int m_tiles_grid; int n_tiles;
     int act;
 };
@@ -141,5 +145,7 @@ hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, 
 hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *out, hipStream_t s);
 hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const GemmArgs &g,
                                hipStream_t s);
+// bf16 activations x bf16 weights; bm = 128 or 256 rows per tile (the scan's bm)
+hipError_t launch_grouped_gemm_bf16(int mode, int bm, const GemmArgs &g, hipStream_t s);
 
 }  // namespace moe

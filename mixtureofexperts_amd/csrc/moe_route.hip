@@ -396,7 +396,10 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
         if (a.loss_out) a.loss_out[0] = loss;
     }
     __syncthreads();
-    for (int e = tid; e <= a.E; e += blockDim.x) a.offsets[e] = off[e];
+    for (int e = tid; e <= a.E; e += blockDim.x) {
+        a.offsets[e] = off[e];
+        a.tile_start[e] = tstart[e];
+    }
     for (int e = tid; e < a.E; e += blockDim.x) {
         a.counts[e] = cnt[e];
         const int nt = tstart[e + 1] - tstart[e];
