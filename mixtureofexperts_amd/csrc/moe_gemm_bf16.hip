@@ -37,20 +37,32 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 #define MOE_LDS_AS __attribute__((address_space(3)))
 
-__device__ inline float act_apply_bf(int act, float x) {
-    switch (act) {
-    case MOE_ACT_SILU:  // x * sigmoid(x)
-        return x / (1.0f + expf(-x));
-    case MOE_ACT_GELU: {  // NNlib gelu, tanh form
-        const float c = 0.7978845608028654f;  // sqrt(2/pi)
-        const float u = c * (x + 0.044715f * x * x * x);
-        return 0.5f * x * (1.0f + tanhf(u));
-    }
-    case MOE_ACT_RELU:
+// Activation in the epilogue of the bf16 path (outputs are rounded to bf16 or
+// checked at bf16 tolerance): silu(x) = x * sigmoid(x) and NNlib's tanh-form
+// gelu(x) = 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3),
+// both as x * rcp(1 + exp(-z)) with the hardware exp and reciprocal.
+template <int ACT>
+__device__ __forceinline__ float act_fast(float x) {
+    if constexpr (ACT == MOE_ACT_SILU) {
+        return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    } else if constexpr (ACT == MOE_ACT_GELU) {
+        const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+        return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
+    } else if constexpr (ACT == MOE_ACT_RELU) {
         return x > 0.0f ? x : 0.0f;
-    default:
+    } else {
         return x;
     }
+}
+
+// Four fp32 -> four bf16 (round to nearest even, v_cvt_pk_bf16_f32), packed.
+__device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t lo = {(__bf16)a, (__bf16)b}, hi = {(__bf16)c, (__bf16)d};
+    uint2 r;
+    __builtin_memcpy(&r.x, &lo, 4);
+    __builtin_memcpy(&r.y, &hi, 4);
+    return r;
 }
 
 // Wait until at most N vector-memory operations of this wave are outstanding.
@@ -86,7 +98,7 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
     return (uint32_t)(uintptr_t)(const MOE_LDS_AS uint8_t *)p;
 }
 
-template <int MODE, int BM>
+template <int MODE, int BM, int ACT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
@@ -97,8 +109,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int IM = WM / 32;          // 32-row blocks per wave
     constexpr int LA = BM / 32;          // A loads per wave per stage
     constexpr int NL = LA + 8;           // loads per wave per stage
-    __shared__ __attribute__((aligned(1024))) uint8_t buf0[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t buf1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];  // two stages
 
     // ---- work item -> (expert, n-tile, m-tile) --------------------------------
     const int NT = g.n_tiles;
@@ -128,14 +139,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     // ---- per-lane global offsets of this wave's load instructions -----------
+    // Load i of a wave fills LDS rows 8i .. 8i+7 of its row range (range bases
+    // are multiples of 16): lane l writes row 8i + (l >> 3), physical chunk
+    // l & 7, i.e. logical chunk (l & 7) ^ swz(row) with swz(row) = (row >> 1) & 7.
     const long long lda_b = g.lda * 2, ldb_b = g.ldb * 2;
     const int lr = lane >> 3;
-    const int lch = (lane & 7) ^ lr;  // logical chunk fetched by this lane (row & 7 == lr)
     const uint8_t *Abase = (const uint8_t *)g.A + arow0 * lda_b;
     uint32_t aoff[LA];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int r = w * (BM / 4) + 8 * i + lr;
+        const int lch = (lane & 7) ^ ((4 * i + (lr >> 1)) & 7);
         aoff[i] = (uint32_t)((long long)min(r, rows - 1) * lda_b) + lch * 16;
     }
     const uint8_t *Bsrc = (NB == 2 && w >= 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
@@ -145,12 +159,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int i = 0; i < 8; ++i) {
         // gated: waves 0,1 fetch W1 rows [0,128) of the tile, waves 2,3 the same W3 rows
         const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 8 * i + lr;
+        const int lch = (lane & 7) ^ ((4 * i + (lr >> 1)) & 7);
         boff[i] = (uint32_t)((long long)r * ldb_b) + lch * 16;
     }
     const uint32_t a_lds = w * (BM / 4) * ROWB;       // this wave's A rows in a stage
     const uint32_t b_lds = A_BYTES + w * 64 * ROWB;   // this wave's B rows in a stage
-    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(buf0));
-    const uint32_t lds1 = __builtin_amdgcn_readfirstlane(lds_addr(buf1));
+    const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     const uint8_t *Au = uniform_ptr(Abase), *Bu = uniform_ptr(Bbase);
 
     auto issue = [&](int kt, uint32_t lbuf) {
@@ -161,7 +175,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int i = 0; i < 8; ++i) lds_dma16(Bu + ko, boff[i], lbuf + b_lds + i * 1024);
     };
 
-    // ---- fragment addressing --------------------------------------------------
+    // ---- fragment addressing (every fragment row base is a multiple of 32, so
+    // swz(row) = (r32 >> 1) & 7) --------------------------------------------------
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const int wm = w & 1, wn = w >> 1;
@@ -174,7 +189,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     int choff[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) choff[ks] = ((ks * 2 + half) ^ (r32 & 7)) << 4;
+    for (int ks = 0; ks < 4; ++ks) choff[ks] = ((ks * 2 + half) ^ ((r32 >> 1) & 7)) << 4;
 
     f32x16_t acc[IM][4];
 #pragma unroll
@@ -184,111 +199,150 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    // Four k16 sub-steps per stage; the fragments of sub-step ks+1 are read
-    // from LDS before the MFMAs of sub-step ks are issued.
-    auto compute = [&](const uint8_t *buf) {
-        bf16x8_t af[2][IM], bfr[2][4];
+    bf16x8_t fa[2][IM], fb[2][4];
+    auto read_frags = [&](int sb, int ks, bf16x8_t *af, bf16x8_t *bfr) {
 #pragma unroll
-        for (int i = 0; i < IM; ++i) af[0][i] = *(const bf16x8_t *)(buf + a_frag + i * 32 * ROWB + choff[0]);
+        for (int i = 0; i < IM; ++i) af[i] = *(const bf16x8_t *)(lds + sb + a_frag + i * 32 * ROWB + choff[ks]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bfr[0][j] = *(const bf16x8_t *)(buf + b_frag[j] + choff[0]);
+        for (int j = 0; j < 4; ++j) bfr[j] = *(const bf16x8_t *)(lds + sb + b_frag[j] + choff[ks]);
+    };
+    auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int c = ks & 1;
-            if (ks < 3) {
+        for (int i = 0; i < IM; ++i)
 #pragma unroll
-                for (int i = 0; i < IM; ++i)
-                    af[c ^ 1][i] = *(const bf16x8_t *)(buf + a_frag + i * 32 * ROWB + choff[ks + 1]);
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    };
+    // Ask the scheduler to spread one sub-step's IM + 4 fragment reads over the
+    // IM * 4 MFMAs of the previous sub-step.
+    auto interleave = [&]() {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bfr[c ^ 1][j] = *(const bf16x8_t *)(buf + b_frag[j] + choff[ks + 1]);
-            }
-#pragma unroll
-            for (int i = 0; i < IM; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bfr[c][j], acc[i][j], 0, 0, 0);
+        for (int t = 0; t < IM + 4; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, (IM * 4) / (IM + 4), 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                    // DS read
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, (IM * 4) % (IM + 4), 0);
     };
 
-    // ---- main loop: stage kt lives in buf[kt & 1] --------------------------------
+    // ---- main loop --------------------------------------------------------------
+    // Stage kt lives at lds + (kt & 1) * STAGE.  Per stage: sub-steps 0..2 run
+    // their MFMAs while the next sub-step's fragments are read; then one barrier
+    // (every wave is done reading this stage's buffer, and stage kt+1 has
+    // landed), the loads of stage kt+2 into this buffer, and sub-step 3 runs
+    // while the first fragments of stage kt+1 are read.
     const int KT = g.K / 64;
-    issue(0, lds0);
-    int kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-        issue(kt + 1, lds1);
-        wait_vmcnt<NL>();
-        barrier_lds();
-        compute(buf0);
-        barrier_lds();
-        if (kt + 2 < KT) {
-            issue(kt + 2, lds0);
-            wait_vmcnt<NL>();
-        } else {
-            wait_vmcnt<0>();
+    issue(0, lbase);
+    wait_vmcnt<0>();
+    barrier_lds();
+    if (KT > 1) issue(1, lbase + STAGE);
+    read_frags(0, 0, fa[0], fb[0]);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int sb = (kt & 1) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks) {
+            read_frags(sb, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+            mfmas(fa[ks & 1], fb[ks & 1]);
+            interleave();
         }
-        barrier_lds();
-        compute(buf1);
-        barrier_lds();
-    }
-    if (kt < KT) {  // odd K-step count: the last stage is in buf0
         wait_vmcnt<0>();
         barrier_lds();
-        compute(buf0);
+        if (kt + 2 < KT) issue(kt + 2, lbase + sb);
+        // the last stage reads stale (in-bounds) fragments of the other buffer; they are never used
+        read_frags(sb ^ STAGE, 0, fa[0], fb[0]);
+        mfmas(fa[1], fb[1]);
+        interleave();
     }
 
-    // ---- epilogue: lane holds column r32 of each 32x32 block, rows
-    // 8*(q/4) + 4*half + q%4 ---------------------------------------------------
+    // ---- epilogue.  The MFMA computes the transposed block (weights are its A
+    // operand): lane l holds token row r32 of the 32-row block and output
+    // columns 8*(q/4) + 4*half + q%4, i.e. four consecutive columns per q/4,
+    // written as one 8-byte (bf16) or 16-byte (fp32) store. ----------------------
     const long long sofs = (long long)e * g.s_stride;
     if constexpr (MODE == MODE_GATED_UP) {
+        // h pad columns [N, Npad) come out as act(0) * 0 = 0 from the zero weight
+        // pad rows, so the whole tile is stored (ldc = Npad).
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const int n = n0 + wn * 64 + m * 32 + r32;
-            if (n >= g.N) continue;
+        for (int i = 0; i < IM; ++i) {
+            const int ml = wm * WM + i * 32 + r32;
+            if (ml >= rows) continue;
+            uint16_t *crow = (uint16_t *)g.C + (arow0 + ml) * g.ldc;
 #pragma unroll
-            for (int i = 0; i < IM; ++i)
+            for (int m = 0; m < 2; ++m)
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int ml = wm * WM + i * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
-                    if (ml >= rows) continue;
-                    const float v = act_apply_bf(g.act, acc[i][2 * m][q]) * acc[i][2 * m + 1][q];
-                    ((uint16_t *)g.C)[(arow0 + ml) * g.ldc + n] = f32_to_bf16(v);
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int n = n0 + wn * 64 + m * 32 + 8 * g4 + 4 * half;
+                    float v[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        v[c] = act_fast<ACT>(acc[i][2 * m][4 * g4 + c]) * acc[i][2 * m + 1][4 * g4 + c];
+                    *(uint2 *)(crow + n) = pack_bf16x4(v[0], v[1], v[2], v[3]);
                 }
         }
     } else {
+        // MODE_STD_UP stores bf16 h (pads are act(b1 pad = 0) of zero rows: 0 for
+        // silu, gelu, relu, identity); MODE_DOWN stores fp32 y with ldc = N.
+        const bool vec4 = (MODE == MODE_STD_UP) || ((g.ldc & 3) == 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + wn * 128 + j * 32 + r32;
-            if (n >= g.N) continue;
-            const float bias = g.bias ? g.bias[sofs + n] : 0.0f;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < IM; ++i)
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int n = n0 + wn * 128 + j * 32 + 8 * g4 + 4 * half;
+                float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (g.bias) {
+                    const float4 bv = *(const float4 *)(g.bias + sofs + n);
+                    b4[0] = bv.x; b4[1] = bv.y; b4[2] = bv.z; b4[3] = bv.w;
+                }
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int ml = wm * WM + i * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
+                for (int i = 0; i < IM; ++i) {
+                    const int ml = wm * WM + i * 32 + r32;
                     if (ml >= rows) continue;
                     if constexpr (MODE == MODE_STD_UP) {
-                        const float v = act_apply_bf(g.act, acc[i][j][q] + bias);
-                        ((uint16_t *)g.C)[(arow0 + ml) * g.ldc + n] = f32_to_bf16(v);
+                        uint16_t *crow = (uint16_t *)g.C + (arow0 + ml) * g.ldc;
+                        *(uint2 *)(crow + n) = pack_bf16x4(
+                            act_fast<ACT>(acc[i][j][4 * g4 + 0] + b4[0]), act_fast<ACT>(acc[i][j][4 * g4 + 1] + b4[1]),
+                            act_fast<ACT>(acc[i][j][4 * g4 + 2] + b4[2]), act_fast<ACT>(acc[i][j][4 * g4 + 3] + b4[3]));
                     } else {
-                        ((float *)g.C)[(arow0 + ml) * g.ldc + n] = acc[i][j][q] + bias;
+                        float *crow = (float *)g.C + (arow0 + ml) * g.ldc;
+                        if (vec4 && n + 3 < g.N) {
+                            *(float4 *)(crow + n) = make_float4(acc[i][j][4 * g4 + 0] + b4[0], acc[i][j][4 * g4 + 1] + b4[1],
+                                                                acc[i][j][4 * g4 + 2] + b4[2], acc[i][j][4 * g4 + 3] + b4[3]);
+                        } else {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c)
+                                if (n + c < g.N) crow[n + c] = acc[i][j][4 * g4 + c] + b4[c];
+                        }
                     }
                 }
-        }
+            }
     }
 }
 
-template <int MODE, int BM>
+template <int MODE, int BM, int ACT>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
     long long total = (long long)g.m_tiles_grid * g.n_tiles;
     total = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM>), dim3((unsigned)total), dim3(256), 0, s, g);
+    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
+}
+
+template <int MODE, int BM>
+static hipError_t launch_bf16_act(const GemmArgs &g, hipStream_t s) {
+    if constexpr (MODE == MODE_DOWN) {
+        return launch_bf16<MODE, BM, MOE_ACT_IDENTITY>(g, s);
+    } else {
+        switch (g.act) {
+        case MOE_ACT_SILU: return launch_bf16<MODE, BM, MOE_ACT_SILU>(g, s);
+        case MOE_ACT_GELU: return launch_bf16<MODE, BM, MOE_ACT_GELU>(g, s);
+        case MOE_ACT_RELU: return launch_bf16<MODE, BM, MOE_ACT_RELU>(g, s);
+        default: return launch_bf16<MODE, BM, MOE_ACT_IDENTITY>(g, s);
+        }
+    }
 }
 
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, const GemmArgs &g, hipStream_t s) {
     if (g.m_tiles_grid <= 0 || g.n_tiles <= 0) return hipSuccess;
 #define MOE_BF16_CASE(M, B) \
-    if (mode == M && bm == B) return launch_bf16<M, B>(g, s);
+    if (mode == M && bm == B) return launch_bf16_act<M, B>(g, s);
     MOE_BF16_CASE(MODE_GATED_UP, 256)
     MOE_BF16_CASE(MODE_STD_UP, 256)
     MOE_BF16_CASE(MODE_DOWN, 256)
