@@ -29,6 +29,8 @@
 // global_load_lds_dwordx4 writes 1 KB = 8 rows of LDS linearly (lane l ->
 // offset 16 l), so the swizzle is applied on the global side: lane l fetches
 // logical chunk (l & 7) ^ (l >> 3) of its row.
+#include <type_traits>
+
 #include "moe_internal.h"
 
 namespace moe {
@@ -102,14 +104,15 @@ template <int MODE, int BM, int ACT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
-    constexpr int ROWB = 128;            // bytes per LDS row = 64 bf16 of K
+    constexpr int NS = 3;                // LDS ring slots
+    constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
     constexpr int A_BYTES = BM * ROWB;
     constexpr int STAGE = A_BYTES + 256 * ROWB;
     constexpr int WM = BM / 2;           // wave tile rows
     constexpr int IM = WM / 32;          // 32-row blocks per wave
-    constexpr int LA = BM / 32;          // A loads per wave per stage
-    constexpr int NL = LA + 8;           // loads per wave per stage
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];  // two stages
+    constexpr int LA = BM / 64;          // A row groups (16 rows) per wave per stage
+    constexpr int NL = LA + 4;           // 16-byte loads per lane per stage
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
 
     // ---- work item -> (expert, n-tile, m-tile) --------------------------------
     const int NT = g.n_tiles;
@@ -138,45 +141,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-    // ---- per-lane global offsets of this wave's load instructions -----------
-    // Load i of a wave fills LDS rows 8i .. 8i+7 of its row range (range bases
-    // are multiples of 16): lane l writes row 8i + (l >> 3), physical chunk
-    // l & 7, i.e. logical chunk (l & 7) ^ swz(row) with swz(row) = (row >> 1) & 7.
+    // ---- global -> register -> LDS copy of one stage ----------------------------
+    // A stage row is 64 B = four 16-byte chunks; chunk c of row r is stored at
+    // c ^ swz(r), swz(r) = (r >> 2) & 3, so that 16 consecutive rows read at
+    // one logical chunk hit 16 distinct (bank group, chunk) slots.  Copy i of a
+    // wave moves 16 rows (range bases are multiples of 16): lane l takes row
+    // 16i + (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ ((l >> 4) & 3).
     const long long lda_b = g.lda * 2, ldb_b = g.ldb * 2;
-    const int lr = lane >> 3;
-    const uint8_t *Abase = (const uint8_t *)g.A + arow0 * lda_b;
-    uint32_t aoff[LA];
+    const int lr = lane >> 2;
+    const int lch = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint8_t *Ab = (const uint8_t *)g.A + arow0 * lda_b;
+    const uint8_t *gsrc[NL];
+    uint32_t ldst[NL];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int r = w * (BM / 4) + 8 * i + lr;
-        const int lch = (lane & 7) ^ ((4 * i + (lr >> 1)) & 7);
-        aoff[i] = (uint32_t)((long long)min(r, rows - 1) * lda_b) + lch * 16;
+        const int r = w * (BM / 4) + 16 * i + lr;
+        gsrc[i] = Ab + (long long)min(r, rows - 1) * lda_b + lch * 16;
+        ldst[i] = r * ROWB + (lane & 3) * 16;
     }
     const uint8_t *Bsrc = (NB == 2 && w >= 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
-    const uint8_t *Bbase = Bsrc + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * 2;  // row n0 of expert e
-    uint32_t boff[8];
+    const uint8_t *Bb = Bsrc + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * 2;  // row n0 of expert e
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
         // gated: waves 0,1 fetch W1 rows [0,128) of the tile, waves 2,3 the same W3 rows
-        const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 8 * i + lr;
-        const int lch = (lane & 7) ^ ((4 * i + (lr >> 1)) & 7);
-        boff[i] = (uint32_t)((long long)r * ldb_b) + lch * 16;
+        const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 16 * i + lr;
+        gsrc[LA + i] = Bb + (long long)r * ldb_b + lch * 16;
+        ldst[LA + i] = A_BYTES + (w * 64 + 16 * i + lr) * ROWB + (lane & 3) * 16;
     }
-    const uint32_t a_lds = w * (BM / 4) * ROWB;       // this wave's A rows in a stage
-    const uint32_t b_lds = A_BYTES + w * 64 * ROWB;   // this wave's B rows in a stage
-    const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-    const uint8_t *Au = uniform_ptr(Abase), *Bu = uniform_ptr(Bbase);
-
-    auto issue = [&](int kt, uint32_t lbuf) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    u32x4_t stg[3][NL];  // three stages in flight between global memory and LDS
+    // copies i in [i0, i1) of a stage: global -> registers, registers -> LDS
+    auto gload = [&](int kt, u32x4_t *rg, int i0, int i1) {
         const long long ko = (long long)kt * ROWB;
 #pragma unroll
-        for (int i = 0; i < LA; ++i) lds_dma16(Au + ko, aoff[i], lbuf + a_lds + i * 1024);
+        for (int i = 0; i < NL; ++i)
+            if (i >= i0 && i < i1) rg[i] = *(const u32x4_t *)(gsrc[i] + ko);
+    };
+    auto swrite = [&](int slot_, const u32x4_t *rg, int i0, int i1) {
+        uint8_t *sb = lds + slot_ * STAGE;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lds_dma16(Bu + ko, boff[i], lbuf + b_lds + i * 1024);
+        for (int i = 0; i < NL; ++i)
+            if (i >= i0 && i < i1) *(u32x4_t *)(sb + ldst[i]) = rg[i];
     };
 
-    // ---- fragment addressing (every fragment row base is a multiple of 32, so
-    // swz(row) = (r32 >> 1) & 7) --------------------------------------------------
+    // ---- fragment addressing (fragment row bases are multiples of 32, so
+    // swz(row) = (r32 >> 2) & 3) ------------------------------------------------
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const int wm = w & 1, wn = w >> 1;
@@ -187,9 +196,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int row = (NB == 2) ? ((j & 1) * 128 + wn * 64 + (j >> 1) * 32) : (wn * 128 + j * 32);
         b_frag[j] = A_BYTES + (row + r32) * ROWB;
     }
-    int choff[4];
+    int choff[2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) choff[ks] = ((ks * 2 + half) ^ ((r32 >> 1) & 7)) << 4;
+    for (int ks = 0; ks < 2; ++ks) choff[ks] = ((ks * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
 
     f32x16_t acc[IM][4];
 #pragma unroll
@@ -200,11 +209,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
     bf16x8_t fa[2][IM], fb[2][4];
-    auto read_frags = [&](int sb, int ks, bf16x8_t *af, bf16x8_t *bfr) {
+    auto read_frag = [&](int slot_, int ks, int r, bf16x8_t *af, bf16x8_t *bfr) {
+        const uint8_t *sb = lds + slot_ * STAGE;
+        if (r < IM) af[r] = *(const bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[ks]);
+        else bfr[r - IM] = *(const bf16x8_t *)(sb + b_frag[r - IM] + choff[ks]);
+    };
+    auto read_frags = [&](int slot_, int ks, bf16x8_t *af, bf16x8_t *bfr) {
 #pragma unroll
-        for (int i = 0; i < IM; ++i) af[i] = *(const bf16x8_t *)(lds + sb + a_frag + i * 32 * ROWB + choff[ks]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bfr[j] = *(const bf16x8_t *)(lds + sb + b_frag[j] + choff[ks]);
+        for (int r = 0; r < IM + 4; ++r) read_frag(slot_, ks, r, af, bfr);
     };
     auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
 #pragma unroll
@@ -213,45 +225,76 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int j = 0; j < 4; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     };
-    // Ask the scheduler to spread one sub-step's IM + 4 fragment reads over the
-    // IM * 4 MFMAs of the previous sub-step.
+    // The memory work of one sub-step, issued in this order: fragment read,
+    // copy, fragment read, copy, ...  The copies are half of the stage's global
+    // loads (copies [c0, c0 + NL/2)) followed by half of its LDS writes.  The
+    // compiler keeps LDS reads and writes in program order (it cannot prove the
+    // ring slots distinct), so this order is also the issue order.
+    constexpr int NRD = IM + 4, NCP = NL;
+    auto sub_mem = [&](int rslot, int ks, bf16x8_t *af, bf16x8_t *bfr, int gkt, u32x4_t *ld, int wslot,
+                       const u32x4_t *wr, int c0) {
+#pragma unroll
+        for (int t = 0; t < (NRD > NCP ? NRD : NCP); ++t) {
+            if (t < NRD) read_frag(rslot, ks, t, af, bfr);
+            if (t < NL / 2) gload(gkt, ld, c0 + t, c0 + t + 1);
+            else if (t < NL) swrite(wslot, wr, c0 + t - NL / 2, c0 + t - NL / 2 + 1);
+        }
+    };
+    // One MFMA, then the next memory instruction(s) in order, across the sub-step.
+    constexpr int NMF = IM * 4, NMEM = NRD + NCP;
     auto interleave = [&]() {
 #pragma unroll
-        for (int t = 0; t < IM + 4; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x008, (IM * 4) / (IM + 4), 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                    // DS read
+        for (int t = 0; t < NMF; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            const int k = ((t + 1) * NMEM) / NMF - (t * NMEM) / NMF;
+            if (k == 1) __builtin_amdgcn_sched_group_barrier(0x100 | 0x020 | 0x200, 1, 0);
+            else if (k == 2) __builtin_amdgcn_sched_group_barrier(0x100 | 0x020 | 0x200, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, (IM * 4) % (IM + 4), 0);
     };
 
     // ---- main loop --------------------------------------------------------------
-    // Stage kt lives at lds + (kt & 1) * STAGE.  Per stage: sub-steps 0..2 run
-    // their MFMAs while the next sub-step's fragments are read; then one barrier
-    // (every wave is done reading this stage's buffer, and stage kt+1 has
-    // landed), the loads of stage kt+2 into this buffer, and sub-step 3 runs
-    // while the first fragments of stage kt+1 are read.
-    const int KT = g.K / 64;
-    issue(0, lbase);
-    wait_vmcnt<0>();
+    // Stage s (32 K columns, two k16 sub-steps) lives in LDS slot s % 3 and,
+    // on its way there, in register set s % 3.  Per stage:
+    //   sub-step 0: MFMAs of (s, 0) | LDS reads of (s, 1)   | half of: global loads of s+4, LDS writes of s+2
+    //   sub-step 1: MFMAs of (s, 1) | LDS reads of (s+1, 0) | the other half
+    //   one barrier: stage s+2 is visible, slot s % 3 is free.
+    // (Slot (s+2) % 3 held stage s-1, whose reads ended before the previous
+    // barrier.)  A global load has two stages to land before its LDS write.
+    // Past the last stage the loads repeat stage KT-1 (in bounds) and the
+    // writes go to the slot of a finished stage; neither is read.
+    const int KT = g.K / 32;
+    gload(0, stg[0], 0, NL);
+    gload(min(1, KT - 1), stg[1], 0, NL);
+    swrite(0, stg[0], 0, NL);
+    swrite(1, stg[1], 0, NL);
+    gload(min(2, KT - 1), stg[2], 0, NL);
+    gload(min(3, KT - 1), stg[0], 0, NL);
     barrier_lds();
-    if (KT > 1) issue(1, lbase + STAGE);
     read_frags(0, 0, fa[0], fb[0]);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int sb = (kt & 1) * STAGE;
-#pragma unroll
-        for (int ks = 0; ks < 3; ++ks) {
-            read_frags(sb, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
-            mfmas(fa[ks & 1], fb[ks & 1]);
-            interleave();
-        }
-        wait_vmcnt<0>();
-        barrier_lds();
-        if (kt + 2 < KT) issue(kt + 2, lbase + sb);
-        // the last stage reads stale (in-bounds) fragments of the other buffer; they are never used
-        read_frags(sb ^ STAGE, 0, fa[0], fb[0]);
+    int sl = 0;  // slot of stage s
+    auto stage_body = [&](int st, u32x4_t *ld_set, const u32x4_t *wr_set) {
+        const int sl1 = (sl == NS - 1) ? 0 : sl + 1;
+        const int sl2 = (sl1 == NS - 1) ? 0 : sl1 + 1;
+        const int kl = min(st + 4, KT - 1);
+        sub_mem(sl, 1, fa[1], fb[1], kl, ld_set, sl2, wr_set, 0);
+        mfmas(fa[0], fb[0]);
+        interleave();
+        sub_mem(sl1, 0, fa[0], fb[0], kl, ld_set, sl2, wr_set, NL / 2);
         mfmas(fa[1], fb[1]);
         interleave();
+        barrier_lds();
+        sl = sl1;
+    };
+    // register set of stage t is t % 3: stage s loads s+4 into set (s+1) % 3
+    // and writes s+2 from set (s+2) % 3
+    int st = 0;
+    for (; st + 3 <= KT; st += 3) {
+        stage_body(st, stg[1], stg[2]);
+        stage_body(st + 1, stg[2], stg[0]);
+        stage_body(st + 2, stg[0], stg[1]);
     }
+    if (st < KT) stage_body(st, stg[1], stg[2]);
+    if (st + 1 < KT) stage_body(st + 1, stg[2], stg[0]);
 
     // ---- epilogue.  The MFMA computes the transposed block (weights are its A
     // operand): lane l holds token row r32 of the 32-row block and output
