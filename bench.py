@@ -144,14 +144,40 @@ def cpu_baseline(cfg, wl, sample_tokens):
                       f"median of 3 runs, {t:.2f} s each"}
 
 
+def up_kernel_name(cfg):
+    """Name of the dominant kernel (the expert up GEMM) of a workload."""
+    if cfg["w"] == "bf16":
+        return "grouped_gemm_bf16_kernel (expert up GEMM: {})".format(
+            "W1|W3 with silu*mul epilogue" if cfg["etype"] == "gated" else "W1 + b1 with activation epilogue")
+    return "grouped_gemm_kernel (expert up GEMM, {} weights)".format(cfg["w"])
+
+
+def measured_traffic(cfg):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (profiles/hbm_traffic.json),
+    or None when that workload has not been profiled."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data[cfg["workload"]]["expert_up"]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="mixtral", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample", type=int, default=512)
+    ap.add_argument("--cpu-sample", type=int, default=4096,
+                    help="tokens of the workload the CPU baseline runs (default: all of the mixtral batch)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the timed region, run one plain device copy of MIB MiB (fp32 multiply by 1, "
+                         "read MIB and write MIB): the reference kernel that scales rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -212,6 +238,15 @@ def main():
     stage_ms = {n: float(np.mean([ev[j].elapsed_time(ev[j + 1]) for ev in events])) for j, n in enumerate(stage_names)}
     assert bool(torch.isfinite(wl["out"]).all()), "non-finite output"
 
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
     ms_step = elapsed * 1000.0 / args.steps
     tokens_s = T * args.steps / elapsed
     kt = wl["kt"]
@@ -223,10 +258,13 @@ def main():
     up_tflops = up_flops / (stage_ms["expert_up"] * 1e-3) / 1e12
     down_tflops = down_flops / (stage_ms["expert_down"] * 1e-3) / 1e12
     xs = 2 if cfg["w"] != "f32" else 4
-    # algorithmic HBM bytes of the memory-bound stages (per launch)
-    router_bytes = T * D * xs + E * D * 4 + T * E * 4 * 2 + T * kt * (4 + 4 + 4)
-    permute_bytes = T * D * xs + rows * D * xs + rows * 16
-    combine_bytes = rows * D * 4 + T * D * 4 + T * kt * 12
+    # algorithmic HBM bytes of the memory-bound stages (per launch): read x,
+    # the router weight; write indices + gates, per-token logsumexp and probs;
+    # permute reads x and writes the k expert-ordered copies; combine reads the
+    # k fp32 expert outputs with their (position, gate) and writes fp32 out
+    router_bytes = T * D * xs + E * D * 4 + T * kt * (4 + 4) + T * 4 + E * T * 4
+    permute_bytes = T * D * xs + rows * D * xs
+    combine_bytes = rows * D * 4 + rows * 8 + T * D * 4
     gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -245,9 +283,9 @@ def main():
                    "top_k": k, "shared_experts": cfg["ns"], "expert_type": cfg["etype"], "activation": cfg["act"],
                    "weights": cfg["w"], "output": "f32"},
         "tflops": round((up_flops + down_flops) / (ms_step * 1e-3) / 1e12, 2),
-        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_kernel (expert up: gate+up GEMM, silu*mul epilogue)",
+        "roofline": {"bound": "mfma", "kernel": up_kernel_name(cfg),
                      "achieved": round(up_tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(up_tflops / peak, 4), "traffic": None},
+                     "frac": round(up_tflops / peak, 4), "traffic": measured_traffic(cfg)},
         "stages": {
             "router": {"ms": round(stage_ms["router"], 4), "GB/s": round(gbs(router_bytes, stage_ms["router"]), 1)},
             "permute": {"ms": round(stage_ms["permute"], 4), "GB/s": round(gbs(permute_bytes, stage_ms["permute"]), 1)},
