@@ -78,15 +78,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // not moved across it); the LDS reads of this wave are complete before it.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// global_load_lds_dwordx4: lane l copies 16 bytes from base + voff (its own
-// offset) to LDS address lds + 16 l.  Issued as inline assembly so that the
-// compiler's wait insertion does not treat every later LDS read as dependent
-// on it (it cannot tell the two stages apart and would wait for all loads);
-// the kernel waits for these loads explicitly with wait_vmcnt.  base and lds
-// are wave-uniform.
-__device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
+// global_load_lds_dwordx4: lane l copies 16 bytes from its own global address
+// to LDS byte lds + 16 l (lds is wave-uniform, passed in M0).  Issued as
+// inline assembly that the compiler does not see as a memory access: its wait
+// insertion would otherwise treat every later LDS read as possibly reading
+// these bytes and wait for all loads in flight.  Correct ordering is kept by
+// the kernel itself: each slot is refilled only after a barrier that follows
+// its last reads, and read only after a barrier that follows wait_vmcnt for
+// its loads (volatile asm statements keep their relative order).
+__device__ __forceinline__ void lds_dma16(const uint8_t *gaddr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds) : "m0");
 }
 
 __device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p) {
@@ -104,36 +105,55 @@ template <int MODE, int BM, int ACT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
-    constexpr int NS = 3;                // LDS ring slots
     constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
     constexpr int A_BYTES = BM * ROWB;
     constexpr int STAGE = A_BYTES + 256 * ROWB;
+    constexpr int NS = (BM == 256) ? 4 : 6;  // LDS ring slots: 128 KB / 144 KB
     constexpr int WM = BM / 2;           // wave tile rows
     constexpr int IM = WM / 32;          // 32-row blocks per wave
-    constexpr int LA = BM / 64;          // A row groups (16 rows) per wave per stage
+    constexpr int LA = BM / 64;          // A loads (16 rows each) per wave per stage
     constexpr int NL = LA + 4;           // 16-byte loads per lane per stage
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+    static_assert(NS * STAGE <= 160 * 1024, "LDS");
+    // One array per ring slot: the compiler tracks the direct-to-LDS loads per
+    // array, so a fragment read waits only for loads into its own slot.
+    __shared__ __attribute__((aligned(1024))) uint8_t slot0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot2[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot3[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot4[NS > 4 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot5[NS > 5 ? STAGE : 16];
+    auto slot = [&](auto J_) -> MOE_LDS_AS uint8_t * {
+        constexpr int J = decltype(J_)::value;
+        if constexpr (J == 0) return (MOE_LDS_AS uint8_t *)slot0;
+        else if constexpr (J == 1) return (MOE_LDS_AS uint8_t *)slot1;
+        else if constexpr (J == 2) return (MOE_LDS_AS uint8_t *)slot2;
+        else if constexpr (J == 3) return (MOE_LDS_AS uint8_t *)slot3;
+        else if constexpr (J == 4) return (MOE_LDS_AS uint8_t *)slot4;
+        else return (MOE_LDS_AS uint8_t *)slot5;
+    };
 
-    // ---- work item -> (expert, n-tile, m-tile) --------------------------------
+    // ---- work item -> (expert, n-tile, K range, m-tile) -------------------------
     const int NT = g.n_tiles;
-    const int W = g.tile_start[g.E] * NT;
+    const int KS = g.ksplit;                   // K ranges per output tile
+    const int W = g.tile_start[g.E] * NT * KS;
     const int L = blockIdx.x;
     const int perx = (W + 7) >> 3;
-    const int slot = L >> 3;
-    if (slot >= perx) return;
-    const int id = (L & 7) * perx + slot;
+    const int slot_id = L >> 3;
+    if (slot_id >= perx) return;
+    const int id = (L & 7) * perx + slot_id;
     if (id >= W) return;
-    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT <= id (a non-empty expert)
+    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT * KS <= id (a non-empty expert)
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (g.tile_start[mid] * NT <= id) lo = mid; else hi = mid - 1;
+        if (g.tile_start[mid] * NT * KS <= id) lo = mid; else hi = mid - 1;
     }
     const int e = lo;
     const int t0 = g.tile_start[e];
     const int nte = g.tile_start[e + 1] - t0;
-    const int local = id - t0 * NT;
-    const int nt = local / nte;
-    const int m0 = (local - nt * nte) * BM;
+    const int local = id - t0 * NT * KS;        // within the expert: (n-tile, K range) major, m-tile minor
+    const int ntks = local / nte;
+    const int nt = ntks / KS, ks = ntks - nt * KS;
+    const int m0 = (local - ntks * nte) * BM;
     const int rows = min(BM, g.counts[e] - m0);
     const long long arow0 = (long long)g.offsets[e] + m0;
     const int n0 = nt * (NB == 2 ? 128 : 256);  // first B row (h column for the gated mode)
@@ -141,47 +161,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-    // ---- global -> register -> LDS copy of one stage ----------------------------
+    // ---- direct global -> LDS copy of one stage ----------------------------------
     // A stage row is 64 B = four 16-byte chunks; chunk c of row r is stored at
     // c ^ swz(r), swz(r) = (r >> 2) & 3, so that 16 consecutive rows read at
-    // one logical chunk hit 16 distinct (bank group, chunk) slots.  Copy i of a
-    // wave moves 16 rows (range bases are multiples of 16): lane l takes row
-    // 16i + (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ ((l >> 4) & 3).
+    // one logical chunk hit 16 distinct (bank group, chunk) slots.  Load i of a
+    // wave writes 1 KB = 16 rows linearly (lane l -> byte 16 l: row 16i + (l >> 2),
+    // physical chunk l & 3), so lane l fetches logical chunk (l & 3) ^ ((l >> 4) & 3).
     const long long lda_b = g.lda * 2, ldb_b = g.ldb * 2;
+    const int KT = g.K / 32 / KS;               // stages of this item's K range
+    const long long k0b = (long long)ks * KT * ROWB;  // its first K byte in a row
     const int lr = lane >> 2;
     const int lch = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t *Ab = (const uint8_t *)g.A + arow0 * lda_b;
+    const uint8_t *Ab = (const uint8_t *)g.A + arow0 * lda_b + k0b;
     const uint8_t *gsrc[NL];
     uint32_t ldst[NL];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int r = w * (BM / 4) + 16 * i + lr;
-        gsrc[i] = Ab + (long long)min(r, rows - 1) * lda_b + lch * 16;
-        ldst[i] = r * ROWB + (lane & 3) * 16;
+        const int r = w * (BM / 4) + 16 * i;
+        gsrc[i] = Ab + (long long)min(r + lr, rows - 1) * lda_b + lch * 16;
+        ldst[i] = r * ROWB;
     }
     const uint8_t *Bsrc = (NB == 2 && w >= 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
     const uint8_t *Bb = Bsrc + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * 2;  // row n0 of expert e
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         // gated: waves 0,1 fetch W1 rows [0,128) of the tile, waves 2,3 the same W3 rows
-        const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 16 * i + lr;
-        gsrc[LA + i] = Bb + (long long)r * ldb_b + lch * 16;
-        ldst[LA + i] = A_BYTES + (w * 64 + 16 * i + lr) * ROWB + (lane & 3) * 16;
+        const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 16 * i;
+        gsrc[LA + i] = Bb + (long long)(r + lr) * ldb_b + k0b + lch * 16;
+        ldst[LA + i] = A_BYTES + (w * 64 + 16 * i) * ROWB;
     }
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-    u32x4_t stg[3][NL];  // three stages in flight between global memory and LDS
-    // copies i in [i0, i1) of a stage: global -> registers, registers -> LDS
-    auto gload = [&](int kt, u32x4_t *rg, int i0, int i1) {
-        const long long ko = (long long)kt * ROWB;
-#pragma unroll
-        for (int i = 0; i < NL; ++i)
-            if (i >= i0 && i < i1) rg[i] = *(const u32x4_t *)(gsrc[i] + ko);
-    };
-    auto swrite = [&](int slot_, const u32x4_t *rg, int i0, int i1) {
-        uint8_t *sb = lds + slot_ * STAGE;
-#pragma unroll
-        for (int i = 0; i < NL; ++i)
-            if (i >= i0 && i < i1) *(u32x4_t *)(sb + ldst[i]) = rg[i];
+    // load i of stage kt into ring slot J
+    auto dma = [&](auto J_, int kt, int i) {
+        const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
+        lds_dma16(gsrc[i] + (long long)kt * ROWB, __builtin_amdgcn_readfirstlane(l));
     };
 
     // ---- fragment addressing (fragment row bases are multiples of 32, so
@@ -198,7 +210,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     int choff[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) choff[ks] = ((ks * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
+    for (int kk = 0; kk < 2; ++kk) choff[kk] = ((kk * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
 
     f32x16_t acc[IM][4];
 #pragma unroll
@@ -209,14 +221,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
     bf16x8_t fa[2][IM], fb[2][4];
-    auto read_frag = [&](int slot_, int ks, int r, bf16x8_t *af, bf16x8_t *bfr) {
-        const uint8_t *sb = lds + slot_ * STAGE;
-        if (r < IM) af[r] = *(const bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[ks]);
-        else bfr[r - IM] = *(const bf16x8_t *)(sb + b_frag[r - IM] + choff[ks]);
-    };
-    auto read_frags = [&](int slot_, int ks, bf16x8_t *af, bf16x8_t *bfr) {
-#pragma unroll
-        for (int r = 0; r < IM + 4; ++r) read_frag(slot_, ks, r, af, bfr);
+    auto read_frag = [&](auto J_, int kk, int r, bf16x8_t *af, bf16x8_t *bfr) {
+        const MOE_LDS_AS uint8_t *sb = slot(J_);
+        if (r < IM) af[r] = *(const MOE_LDS_AS bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[kk]);
+        else bfr[r - IM] = *(const MOE_LDS_AS bf16x8_t *)(sb + b_frag[r - IM] + choff[kk]);
     };
     auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
 #pragma unroll
@@ -225,76 +233,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int j = 0; j < 4; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     };
-    // The memory work of one sub-step, issued in this order: fragment read,
-    // copy, fragment read, copy, ...  The copies are half of the stage's global
-    // loads (copies [c0, c0 + NL/2)) followed by half of its LDS writes.  The
-    // compiler keeps LDS reads and writes in program order (it cannot prove the
-    // ring slots distinct), so this order is also the issue order.
-    constexpr int NRD = IM + 4, NCP = NL;
-    auto sub_mem = [&](int rslot, int ks, bf16x8_t *af, bf16x8_t *bfr, int gkt, u32x4_t *ld, int wslot,
-                       const u32x4_t *wr, int c0) {
-#pragma unroll
-        for (int t = 0; t < (NRD > NCP ? NRD : NCP); ++t) {
-            if (t < NRD) read_frag(rslot, ks, t, af, bfr);
-            if (t < NL / 2) gload(gkt, ld, c0 + t, c0 + t + 1);
-            else if (t < NL) swrite(wslot, wr, c0 + t - NL / 2, c0 + t - NL / 2 + 1);
-        }
-    };
-    // One MFMA, then the next memory instruction(s) in order, across the sub-step.
-    constexpr int NMF = IM * 4, NMEM = NRD + NCP;
+    // One MFMA, then one of the IM + 4 fragment reads of the next sub-step,
+    // until the reads are placed; the remaining MFMAs follow.
+    constexpr int NMF = IM * 4, NRD = IM + 4;
+    static_assert(NRD <= NMF, "interleave pattern");
     auto interleave = [&]() {
 #pragma unroll
-        for (int t = 0; t < NMF; ++t) {
+        for (int t = 0; t < NRD; ++t) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            const int k = ((t + 1) * NMEM) / NMF - (t * NMEM) / NMF;
-            if (k == 1) __builtin_amdgcn_sched_group_barrier(0x100 | 0x020 | 0x200, 1, 0);
-            else if (k == 2) __builtin_amdgcn_sched_group_barrier(0x100 | 0x020 | 0x200, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
     };
 
     // ---- main loop --------------------------------------------------------------
-    // Stage s (32 K columns, two k16 sub-steps) lives in LDS slot s % 3 and,
-    // on its way there, in register set s % 3.  Per stage:
-    //   sub-step 0: MFMAs of (s, 0) | LDS reads of (s, 1)   | half of: global loads of s+4, LDS writes of s+2
-    //   sub-step 1: MFMAs of (s, 1) | LDS reads of (s+1, 0) | the other half
-    //   one barrier: stage s+2 is visible, slot s % 3 is free.
-    // (Slot (s+2) % 3 held stage s-1, whose reads ended before the previous
-    // barrier.)  A global load has two stages to land before its LDS write.
-    // Past the last stage the loads repeat stage KT-1 (in bounds) and the
-    // writes go to the slot of a finished stage; neither is read.
-    const int KT = g.K / 32;
-    gload(0, stg[0], 0, NL);
-    gload(min(1, KT - 1), stg[1], 0, NL);
-    swrite(0, stg[0], 0, NL);
-    swrite(1, stg[1], 0, NL);
-    gload(min(2, KT - 1), stg[2], 0, NL);
-    gload(min(3, KT - 1), stg[0], 0, NL);
+    // Stage s (32 K columns, two k16 sub-steps) lives in ring slot s % NS and is
+    // loaded NS - 1 stages ahead.  Per stage:
+    //   sub-step 0: MFMAs of (s, 0) | LDS reads of (s, 1)   | loads of stage s+NS-1, first half
+    //   wait until this wave's loads of stage s+1 landed; barrier (every wave's have)
+    //   sub-step 1: MFMAs of (s, 1) | LDS reads of (s+1, 0) | loads of stage s+NS-1, second half
+    // Stage s+NS-1 goes to the slot of stage s-1, whose last reads (its sub-step
+    // 1 fragments) ended before the barrier of stage s-1.  Past the last stage
+    // the loads repeat stage KT-1 (in bounds, into a slot nothing reads again),
+    // which keeps the vmcnt arithmetic exact: when the barrier of stage s is
+    // reached, the loads issued after those of stage s+1 are NS-3 whole stages
+    // and half a stage.
+    constexpr int AFTER = (NS - 3) * NL + NL / 2;
+#pragma unroll
+    for (int s0 = 0; s0 < NS - 1; ++s0) {
+        const int kt = min(s0, KT - 1);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            switch (s0) {
+            case 0: dma(std::integral_constant<int, 0>{}, kt, i); break;
+            case 1: dma(std::integral_constant<int, 1>{}, kt, i); break;
+            case 2: dma(std::integral_constant<int, 2>{}, kt, i); break;
+            case 3: dma(std::integral_constant<int, 3>{}, kt, i); break;
+            default: dma(std::integral_constant<int, 4>{}, kt, i); break;
+            }
+        }
+    }
+    wait_vmcnt<(NS - 2) * NL>();  // stage 0 landed
     barrier_lds();
-    read_frags(0, 0, fa[0], fb[0]);
-    int sl = 0;  // slot of stage s
-    auto stage_body = [&](int st, u32x4_t *ld_set, const u32x4_t *wr_set) {
-        const int sl1 = (sl == NS - 1) ? 0 : sl + 1;
-        const int sl2 = (sl1 == NS - 1) ? 0 : sl1 + 1;
-        const int kl = min(st + 4, KT - 1);
-        sub_mem(sl, 1, fa[1], fb[1], kl, ld_set, sl2, wr_set, 0);
+#pragma unroll
+    for (int r = 0; r < IM + 4; ++r) read_frag(std::integral_constant<int, 0>{}, 0, r, fa[0], fb[0]);
+
+    auto stage = [&](auto J_, int st) {
+        constexpr int J = decltype(J_)::value;
+        using Jn = std::integral_constant<int, (J + 1) % NS>;       // slot of stage s+1
+        using Jl = std::integral_constant<int, (J + NS - 1) % NS>;  // slot of stage s-1 = s+NS-1
+        const int kl = min(st + NS - 1, KT - 1);
+#pragma unroll
+        for (int t = 0; t < IM + 4; ++t) read_frag(J_, 1, t, fa[1], fb[1]);
+#pragma unroll
+        for (int t = 0; t < NL / 2; ++t) dma(Jl{}, kl, t);
         mfmas(fa[0], fb[0]);
         interleave();
-        sub_mem(sl1, 0, fa[0], fb[0], kl, ld_set, sl2, wr_set, NL / 2);
+        wait_vmcnt<AFTER>();
+        barrier_lds();
+#pragma unroll
+        for (int t = 0; t < IM + 4; ++t) read_frag(Jn{}, 0, t, fa[0], fb[0]);
+#pragma unroll
+        for (int t = 0; t < NL / 2; ++t) dma(Jl{}, kl, NL / 2 + t);
         mfmas(fa[1], fb[1]);
         interleave();
-        barrier_lds();
-        sl = sl1;
     };
-    // register set of stage t is t % 3: stage s loads s+4 into set (s+1) % 3
-    // and writes s+2 from set (s+2) % 3
     int st = 0;
-    for (; st + 3 <= KT; st += 3) {
-        stage_body(st, stg[1], stg[2]);
-        stage_body(st + 1, stg[2], stg[0]);
-        stage_body(st + 2, stg[0], stg[1]);
+    for (; st + NS <= KT; st += NS) {
+        stage(std::integral_constant<int, 0>{}, st);
+        stage(std::integral_constant<int, 1>{}, st + 1);
+        stage(std::integral_constant<int, 2>{}, st + 2);
+        stage(std::integral_constant<int, 3>{}, st + 3);
+        if constexpr (NS > 4) stage(std::integral_constant<int, 4 % NS>{}, st + 4);
+        if constexpr (NS > 5) stage(std::integral_constant<int, 5 % NS>{}, st + 5);
     }
-    if (st < KT) stage_body(st, stg[1], stg[2]);
-    if (st + 1 < KT) stage_body(st + 1, stg[2], stg[0]);
+    if (st < KT) stage(std::integral_constant<int, 0>{}, st);
+    if (st + 1 < KT) stage(std::integral_constant<int, 1 % NS>{}, st + 1);
+    if (st + 2 < KT) stage(std::integral_constant<int, 2 % NS>{}, st + 2);
+    if constexpr (NS > 4) if (st + 3 < KT) stage(std::integral_constant<int, 3 % NS>{}, st + 3);
+    if constexpr (NS > 5) if (st + 4 < KT) stage(std::integral_constant<int, 4 % NS>{}, st + 4);
+    wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
     // ---- epilogue.  The MFMA computes the transposed block (weights are its A
     // operand): lane l holds token row r32 of the 32-row block and output
@@ -331,7 +349,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int g4 = 0; g4 < 4; ++g4) {
                 const int n = n0 + wn * 128 + j * 32 + 8 * g4 + 4 * half;
                 float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g.bias) {
+                if (g.bias && ks == 0) {  // split K: the bias belongs to one partial sum only
                     const float4 bv = *(const float4 *)(g.bias + sofs + n);
                     b4[0] = bv.x; b4[1] = bv.y; b4[2] = bv.z; b4[3] = bv.w;
                 }
@@ -345,7 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                             act_fast<ACT>(acc[i][j][4 * g4 + 0] + b4[0]), act_fast<ACT>(acc[i][j][4 * g4 + 1] + b4[1]),
                             act_fast<ACT>(acc[i][j][4 * g4 + 2] + b4[2]), act_fast<ACT>(acc[i][j][4 * g4 + 3] + b4[3]));
                     } else {
-                        float *crow = (float *)g.C + (arow0 + ml) * g.ldc;
+                        float *crow = (float *)g.C + ks * g.c_split_stride + (arow0 + ml) * g.ldc;
                         if (vec4 && n + 3 < g.N) {
                             *(float4 *)(crow + n) = make_float4(acc[i][j][4 * g4 + 0] + b4[0], acc[i][j][4 * g4 + 1] + b4[1],
                                                                 acc[i][j][4 * g4 + 2] + b4[2], acc[i][j][4 * g4 + 3] + b4[3]);
@@ -362,7 +380,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 template <int MODE, int BM, int ACT>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
-    long long total = (long long)g.m_tiles_grid * g.n_tiles;
+    long long total = (long long)g.m_tiles_grid * g.n_tiles * g.ksplit;
     total = (total + 7) / 8 * 8;
     hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
@@ -384,6 +402,8 @@ static hipError_t launch_bf16_act(const GemmArgs &g, hipStream_t s) {
 
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, const GemmArgs &g, hipStream_t s) {
     if (g.m_tiles_grid <= 0 || g.n_tiles <= 0) return hipSuccess;
+    // a split K range must be whole stages, and only the fp32 down GEMM writes partial sums
+    if (g.ksplit < 1 || (g.K / 32) % g.ksplit != 0 || (g.ksplit > 1 && mode != MODE_DOWN)) return hipErrorInvalidValue;
 #define MOE_BF16_CASE(M, B) \
     if (mode == M && bm == B) return launch_bf16_act<M, B>(g, s);
     MOE_BF16_CASE(MODE_GATED_UP, 256)

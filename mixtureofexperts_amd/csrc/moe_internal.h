@@ -110,6 +110,8 @@ struct PermuteArgs {
 
 struct CombineArgs {
     const float *y; int ld_y;    // [rows][ld_y]
+    int nsplit;                  // y holds nsplit partial sums (split-K down GEMM), summed in order
+    long long split_stride;      // elements between partial-sum buffers
     const int *idx; const int *pos_of; const float *gates;
     int T, D, kt;
     float *out;                  // [T][D]
@@ -130,6 +132,8 @@ struct GemmArgs {
     const int *tile_start;               // [E+1] (bf16 kernel work list)
     int E;
     int m_tiles_grid; int n_tiles;
+    int ksplit;                          // bf16 kernel: K ranges per tile (partial outputs at C + ks * c_split_stride)
+    long long c_split_stride;
     int act;
 };
 

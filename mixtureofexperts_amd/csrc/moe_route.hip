@@ -532,11 +532,17 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         ++n;
     }
     float *o = a.out + (long long)t * a.D;
+    // y row of an entry: the sum, in split order, of the down GEMM's K-range partials
     if ((a.D & 3) == 0 && (a.ld_y & 3) == 0) {
         for (int d = lane * 4; d < a.D; d += 256) {
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             for (int i = 0; i < n; ++i) {
-                const float4 v = *(const float4 *)(a.y + (long long)pp[i] * a.ld_y + d);
+                const float *yr = a.y + (long long)pp[i] * a.ld_y + d;
+                float4 v = *(const float4 *)yr;
+                for (int sp = 1; sp < a.nsplit; ++sp) {
+                    const float4 u = *(const float4 *)(yr + sp * a.split_stride);
+                    v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
+                }
                 const float g = gg[i];
                 acc.x = acc.x + g * v.x;
                 acc.y = acc.y + g * v.y;
@@ -548,7 +554,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     } else {
         for (int d = lane; d < a.D; d += 64) {
             float acc = 0.0f;
-            for (int i = 0; i < n; ++i) acc = acc + gg[i] * a.y[(long long)pp[i] * a.ld_y + d];
+            for (int i = 0; i < n; ++i) {
+                const float *yr = a.y + (long long)pp[i] * a.ld_y + d;
+                float v = yr[0];
+                for (int sp = 1; sp < a.nsplit; ++sp) v = v + yr[sp * a.split_stride];
+                acc = acc + gg[i] * v;
+            }
             o[d] = acc;
         }
     }
