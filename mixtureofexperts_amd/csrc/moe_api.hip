@@ -32,6 +32,8 @@ struct moe_handle {
 
     // weights
     float *wr = nullptr, *br = nullptr;
+    uint16_t *wsplit = nullptr;  // router weight as three bf16 parts [3][Ep16][Dp32]
+    int Ep16 = 0, Dp32 = 0;
     bool router_set = false, has_bias = false;
     std::vector<char> expert_set;
     void *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
@@ -44,6 +46,7 @@ struct moe_handle {
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
+    float *logits_part = nullptr;  // [kRouterMaxSlices][T][Er] router GEMM partial sums
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
     double *blk_stats = nullptr;
     int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
@@ -349,11 +352,20 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
 // logits -> gating -> scan -> permute (mode PERMUTE_*)
 static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
                        int permute_mode, float *loss_dev, hipStream_t s) {
-    if (compute_logits)
-        HIP_TRY(h, launch_router_logits(x_dev, x_bf16, T, h->D, h->Er, h->Er_pad, h->wr,
-                                        h->has_bias ? h->br : nullptr, h->logits, s));
     RouteArgs ra{};
-    ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->E; ra.gate_kind = h->cfg.gate_kind;
+    if (compute_logits) {
+        RouterArgs rg{};
+        rg.x = x_dev; rg.x_bf16 = x_bf16; rg.T = T; rg.D = h->D; rg.Er = h->Er; rg.Ep = h->Ep16; rg.Dp = h->Dp32;
+        rg.ws = h->wsplit; rg.part = h->logits_part;
+        router_plan(rg);
+        HIP_TRY(h, launch_router_mfma(rg, x_bf16, s));
+        ra.nks = rg.nks;
+        ra.bias = h->has_bias ? h->br : nullptr;
+    } else {
+        ra.nks = 1;  // the caller's logits are in partial slot 0
+        ra.bias = nullptr;
+    }
+    ra.part = h->logits_part; ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->E; ra.gate_kind = h->cfg.gate_kind;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kt; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
     HIP_TRY(h, launch_route(ra, s));
@@ -532,6 +544,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     const size_t wr_bytes = sizeof(float) * (size_t)h->D * h->Er_pad;
     A((void **)&h->wr, wr_bytes);
     A((void **)&h->br, sizeof(float) * (size_t)h->Er_pad);
+    h->Ep16 = (int)round_up(h->Er, 16);
+    h->Dp32 = (int)round_up(h->D, 32);
+    A((void **)&h->wsplit, sizeof(uint16_t) * 3 * (size_t)h->Ep16 * h->Dp32);
     A(&h->w1, wsz * (size_t)h->E * h->w1_stride);
     if (h->gated) A(&h->w3, wsz * (size_t)h->E * h->w1_stride);
     A(&h->w2, wsz * (size_t)h->E * h->w2_stride);
@@ -553,6 +568,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->max_tiles = h->rows_max / h->bm + h->E + 1;
     const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
+    A((void **)&h->logits_part, sizeof(float) * kRouterMaxSlices * T * h->Er);
     A((void **)&h->probs, sizeof(float) * T * E);
     A((void **)&h->idx, sizeof(int) * T * kt);
     A((void **)&h->gates, sizeof(float) * T * kt);
@@ -629,6 +645,7 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     if (bias)
         HIP_TRY(h, hipMemcpyAsync(h->br, bias, sizeof(float) * h->Er, dev_b ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                   h->stream));
+    HIP_TRY(h, launch_router_split(h->wr, h->D, h->Er, h->Er_pad, h->Ep16, h->Dp32, h->wsplit, h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     h->has_bias = bias != nullptr;
     h->router_set = true;
@@ -699,7 +716,7 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     }
     hipStream_t s = h->stream;
     h->last_T = -1;  // routing state no longer matches a forward call
-    HIP_TRY(h, hipMemcpyAsync(h->logits, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->logits_part, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
     int r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
     if (r != MOE_OK) return r;
     const size_t nk = (size_t)T * h->kt;

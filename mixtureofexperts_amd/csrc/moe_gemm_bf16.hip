@@ -101,18 +101,24 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
     return (uint32_t)(uintptr_t)(const MOE_LDS_AS uint8_t *)p;
 }
 
-template <int MODE, int BM, int ACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
-    GemmArgs g) {
+template <int MODE, int BM, int ACT, int NWAVE>
+__global__ __launch_bounds__(NWAVE * 64) __attribute__((amdgpu_waves_per_eu(NWAVE / 4, NWAVE / 4))) void
+grouped_gemm_bf16_kernel(GemmArgs g) {
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
     constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
     constexpr int A_BYTES = BM * ROWB;
     constexpr int STAGE = A_BYTES + 256 * ROWB;
     constexpr int NS = (BM == 256) ? 4 : 6;  // LDS ring slots: 128 KB / 144 KB
-    constexpr int WM = BM / 2;           // wave tile rows
+    constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
+    constexpr int NWN = NWAVE / 2;       // waves along N
+    constexpr int WN = 256 / NWN;        // wave tile columns (B rows): 128 or 64
     constexpr int IM = WM / 32;          // 32-row blocks per wave
-    constexpr int LA = BM / 64;          // A loads (16 rows each) per wave per stage
-    constexpr int NL = LA + 4;           // 16-byte loads per lane per stage
+    constexpr int JN = WN / 32;          // 32-column blocks per wave
+    constexpr int LA = BM / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
+    constexpr int LB = 256 / (16 * NWAVE);  // B loads per wave per stage
+    constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
+    constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
+    static_assert(LA >= 1 && LB >= 1, "wave count");
     static_assert(NS * STAGE <= 160 * 1024, "LDS");
     // One array per ring slot: the compiler tracks the direct-to-LDS loads per
     // array, so a fragment read waits only for loads into its own slot.
@@ -160,6 +166,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w & 1, wn = w >> 1;
 
     // ---- direct global -> LDS copy of one stage ----------------------------------
     // A stage row is 64 B = four 16-byte chunks; chunk c of row r is stored at
@@ -177,18 +184,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     uint32_t ldst[NL];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int r = w * (BM / 4) + 16 * i;
+        const int r = w * (BM / NWAVE) + 16 * i;
         gsrc[i] = Ab + (long long)min(r + lr, rows - 1) * lda_b + lch * 16;
         ldst[i] = r * ROWB;
     }
-    const uint8_t *Bsrc = (NB == 2 && w >= 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
+    // B tile row r (of 256) is written by wave r / (256 / NWAVE).  Gated: tile rows
+    // [0, 128) are W1 rows n0.., rows [128, 256) the same W3 rows (the upper half of
+    // the waves fetch W3).
+    const uint8_t *Bsrc = (NB == 2 && w >= NWAVE / 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
     const uint8_t *Bb = Bsrc + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * 2;  // row n0 of expert e
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // gated: waves 0,1 fetch W1 rows [0,128) of the tile, waves 2,3 the same W3 rows
-        const int r = ((NB == 2) ? (w & 1) * 64 : w * 64) + 16 * i;
+    for (int i = 0; i < LB; ++i) {
+        const int t = w * (256 / NWAVE) + 16 * i;          // tile row
+        const int r = (NB == 2) ? (t & 127) : t;           // row within the weight matrix, from n0
         gsrc[LA + i] = Bb + (long long)(r + lr) * ldb_b + k0b + lch * 16;
-        ldst[LA + i] = A_BYTES + (w * 64 + 16 * i) * ROWB;
+        ldst[LA + i] = A_BYTES + t * ROWB;
     }
     // load i of stage kt into ring slot J
     auto dma = [&](auto J_, int kt, int i) {
@@ -198,29 +208,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // ---- fragment addressing (fragment row bases are multiples of 32, so
     // swz(row) = (r32 >> 2) & 3) ------------------------------------------------
+    // Gated: a wave's JN column blocks are (gate, up) pairs, block 2m from the W1
+    // half of the tile and block 2m + 1 the same rows of the W3 half, covering h
+    // columns wn * WN / 2 + 32 m.
     const int half = lane >> 5;
     const int r32 = lane & 31;
-    const int wm = w & 1, wn = w >> 1;
     const int a_frag = (wm * WM + r32) * ROWB;
-    int b_frag[4];
+    int b_frag[JN];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = (NB == 2) ? ((j & 1) * 128 + wn * 64 + (j >> 1) * 32) : (wn * 128 + j * 32);
+    for (int j = 0; j < JN; ++j) {
+        const int row = (NB == 2) ? ((j & 1) * 128 + wn * (WN / 2) + (j >> 1) * 32) : (wn * WN + j * 32);
         b_frag[j] = A_BYTES + (row + r32) * ROWB;
     }
     int choff[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) choff[kk] = ((kk * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
 
-    f32x16_t acc[IM][4];
+    f32x16_t acc[IM][JN];
 #pragma unroll
     for (int i = 0; i < IM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < JN; ++j)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    bf16x8_t fa[2][IM], fb[2][4];
+    bf16x8_t fa[2][IM], fb[2][JN];
     auto read_frag = [&](auto J_, int kk, int r, bf16x8_t *af, bf16x8_t *bfr) {
         const MOE_LDS_AS uint8_t *sb = slot(J_);
         if (r < IM) af[r] = *(const MOE_LDS_AS bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[kk]);
@@ -230,12 +242,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int i = 0; i < IM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < JN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     };
-    // One MFMA, then one of the IM + 4 fragment reads of the next sub-step,
+    // One MFMA, then one of the IM + JN fragment reads of the next sub-step,
     // until the reads are placed; the remaining MFMAs follow.
-    constexpr int NMF = IM * 4, NRD = IM + 4;
+    constexpr int NMF = IM * JN, NRD = IM + JN;
     static_assert(NRD <= NMF, "interleave pattern");
     auto interleave = [&]() {
 #pragma unroll
@@ -257,8 +269,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // the loads repeat stage KT-1 (in bounds, into a slot nothing reads again),
     // which keeps the vmcnt arithmetic exact: when the barrier of stage s is
     // reached, the loads issued after those of stage s+1 are NS-3 whole stages
-    // and half a stage.
-    constexpr int AFTER = (NS - 3) * NL + NL / 2;
+    // and the first NL0 loads of stage s+NS-1.
+    constexpr int AFTER = (NS - 3) * NL + NL0;
 #pragma unroll
     for (int s0 = 0; s0 < NS - 1; ++s0) {
         const int kt = min(s0, KT - 1);
@@ -276,7 +288,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     wait_vmcnt<(NS - 2) * NL>();  // stage 0 landed
     barrier_lds();
 #pragma unroll
-    for (int r = 0; r < IM + 4; ++r) read_frag(std::integral_constant<int, 0>{}, 0, r, fa[0], fb[0]);
+    for (int r = 0; r < IM + JN; ++r) read_frag(std::integral_constant<int, 0>{}, 0, r, fa[0], fb[0]);
 
     auto stage = [&](auto J_, int st) {
         constexpr int J = decltype(J_)::value;
@@ -284,17 +296,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         using Jl = std::integral_constant<int, (J + NS - 1) % NS>;  // slot of stage s-1 = s+NS-1
         const int kl = min(st + NS - 1, KT - 1);
 #pragma unroll
-        for (int t = 0; t < IM + 4; ++t) read_frag(J_, 1, t, fa[1], fb[1]);
+        for (int t = 0; t < IM + JN; ++t) read_frag(J_, 1, t, fa[1], fb[1]);
 #pragma unroll
-        for (int t = 0; t < NL / 2; ++t) dma(Jl{}, kl, t);
+        for (int t = 0; t < NL0; ++t) dma(Jl{}, kl, t);
         mfmas(fa[0], fb[0]);
         interleave();
         wait_vmcnt<AFTER>();
         barrier_lds();
 #pragma unroll
-        for (int t = 0; t < IM + 4; ++t) read_frag(Jn{}, 0, t, fa[0], fb[0]);
+        for (int t = 0; t < IM + JN; ++t) read_frag(Jn{}, 0, t, fa[0], fb[0]);
 #pragma unroll
-        for (int t = 0; t < NL / 2; ++t) dma(Jl{}, kl, NL / 2 + t);
+        for (int t = NL0; t < NL; ++t) dma(Jl{}, kl, t);
         mfmas(fa[1], fb[1]);
         interleave();
     };
@@ -328,10 +340,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             if (ml >= rows) continue;
             uint16_t *crow = (uint16_t *)g.C + (arow0 + ml) * g.ldc;
 #pragma unroll
-            for (int m = 0; m < 2; ++m)
+            for (int m = 0; m < JN / 2; ++m)
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    const int n = n0 + wn * 64 + m * 32 + 8 * g4 + 4 * half;
+                    const int n = n0 + wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
@@ -344,10 +356,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // silu, gelu, relu, identity); MODE_DOWN stores fp32 y with ldc = N.
         const bool vec4 = (MODE == MODE_STD_UP) || ((g.ldc & 3) == 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < JN; ++j)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-                const int n = n0 + wn * 128 + j * 32 + 8 * g4 + 4 * half;
+                const int n = n0 + wn * WN + j * 32 + 8 * g4 + 4 * half;
                 float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (g.bias && ks == 0) {  // split K: the bias belongs to one partial sum only
                     const float4 bv = *(const float4 *)(g.bias + sofs + n);
@@ -378,11 +390,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+#ifndef MOE_BF16_WAVES
+#define MOE_BF16_WAVES 4
+#endif
+
 template <int MODE, int BM, int ACT>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
+    constexpr int NWAVE = MOE_BF16_WAVES;
     long long total = (long long)g.m_tiles_grid * g.n_tiles * g.ksplit;
     total = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT>), dim3((unsigned)total), dim3(256), 0, s, g);
+    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, NWAVE>), dim3((unsigned)total), dim3(NWAVE * 64), 0, s,
+                       g);
     return hipGetLastError();
 }
 

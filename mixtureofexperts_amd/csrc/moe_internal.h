@@ -8,7 +8,9 @@
 
 namespace moe {
 
-constexpr int kRouteBlock = 256;   // tokens per routing block (one per thread)
+constexpr int kRouteBlock = 32;    // tokens per routing block
+constexpr int kRouteThreads = 256; // threads per routing block (the first kRouteBlock own one token each)
+constexpr int kRouterMaxSlices = 8;  // K slices of the router logits GEMM (partial sums)
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
 constexpr int kKPad = 64;          // K padding of packed weights and activation rows
@@ -62,8 +64,21 @@ __host__ __device__ inline uint32_t isless_key(float f) {
 
 // ---- kernel argument blocks --------------------------------------------------
 
+// Router logits GEMM: x [T][D] (bf16 or fp32) times the router weight split
+// into three bf16 parts ws [3][Ep][Dp] (Ep = Er rounded up to 16, Dp = D
+// rounded up to 32); partial sums over K slices of ks_len columns go to
+// part [nks][T][Er] (fp32).
+struct RouterArgs {
+    const void *x; int x_bf16; int T, D, Er, Ep, Dp;
+    const uint16_t *ws;
+    float *part; int nks, ks_len, kc;
+};
+
 struct RouteArgs {
-    const float *logits;   // [T][Er]
+    const float *part;     // [nks][T][Er] partial router logits (summed in slice order)
+    int nks;
+    const float *bias;     // [Er] or null
+    float *logits;         // [T][Er] out: sum of the partials + bias
     int T, Er, E, gate_kind, k, ns, kt;
     float *probs;          // [T][E]
     int *idx;              // [T][kt]
@@ -138,8 +153,11 @@ struct GemmArgs {
 };
 
 // ---- launchers ----------------------------------------------------------------
-hipError_t launch_router_logits(const void *x, int x_bf16, int T, int D, int Er, int Er_pad,
-                                const float *wr, const float *bias, float *logits, hipStream_t s);
+hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep, int Dp, uint16_t *ws,
+                               hipStream_t s);
+hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s);
+// K slicing of the router GEMM for a batch of T tokens (fills nks, ks_len, kc)
+void router_plan(RouterArgs &r);
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);

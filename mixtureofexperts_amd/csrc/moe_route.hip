@@ -11,6 +11,7 @@
 //   capacity constraint   src/core/moe_layer.jl:221-248
 //   Switch loss / z-loss  src/balancing/losses.jl:15-36, 103-114
 //   routing entropy       src/core/moe_layer.jl:250-264
+#include <algorithm>
 #include <climits>
 
 #include "moe_internal.h"
@@ -18,136 +19,219 @@
 namespace moe {
 
 // ============================================================================
-// Router logits: logits[t][e] = sum_d x[t][d] * W[d][e] (+ bias[e]), fp32.
-// W is the Flux weight memory [D][Er_pad] (experts contiguous per feature).
-// A block of 4 waves handles 16 tokens (4 per wave); each lane walks the
-// feature axis 4 at a time, experts in chunks of 8.
+// Router logits on MFMA at fp32 accuracy.
+//
+// The fp32 router weight is split once, at upload, into three bf16 parts,
+// W = W0 + W1 + W2 exactly (W0 = bf16(W), W1 = bf16(W - W0), W2 = bf16(W - W0
+// - W1); each difference is exact in fp32 and the three 8-bit significands
+// cover fp32's 24).  bf16 activations are exact in bf16, so x.W = x.W0 + x.W1
+// + x.W2 is three bf16 MFMAs per tile whose products are exact and whose sums
+// are fp32: the same accuracy as an fp32 dot product, in another summation
+// order.  fp32 activations are split the same way and the six cross terms of
+// order <= 2^-16 are kept (the three dropped ones are below 2^-24 relative).
 // ============================================================================
-template <int XBF16>
-__global__ __launch_bounds__(256) void router_logits_kernel(const void *__restrict__ xv, int T,
-                                                            int D, int Er, int Er_pad,
-                                                            const float *__restrict__ w,
-                                                            const float *__restrict__ bias,
-                                                            float *__restrict__ logits) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * 16 + wave * 4;
-    if (t0 >= T) return;
-    for (int e0 = 0; e0 < Er; e0 += 8) {
-        float acc[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) acc[j][c] = 0.0f;
-        for (int d0 = lane * 4; d0 < D; d0 += 256) {
-            float xv4[4][4];
-            const int nd = min(4, D - d0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = min(t0 + j, T - 1);
-                if (XBF16) {
-                    const uint16_t *xr = (const uint16_t *)xv + (long long)t * D + d0;
-                    if (nd == 4 && (D & 3) == 0) {
-                        uint2 p = *(const uint2 *)xr;
-                        xv4[j][0] = bf16_to_f32((uint16_t)(p.x & 0xffff));
-                        xv4[j][1] = bf16_to_f32((uint16_t)(p.x >> 16));
-                        xv4[j][2] = bf16_to_f32((uint16_t)(p.y & 0xffff));
-                        xv4[j][3] = bf16_to_f32((uint16_t)(p.y >> 16));
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) xv4[j][i] = (i < nd) ? bf16_to_f32(xr[i]) : 0.0f;
-                    }
-                } else {
-                    const float *xr = (const float *)xv + (long long)t * D + d0;
-                    if (nd == 4 && (D & 3) == 0) {
-                        float4 p = *(const float4 *)xr;
-                        xv4[j][0] = p.x; xv4[j][1] = p.y; xv4[j][2] = p.z; xv4[j][3] = p.w;
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) xv4[j][i] = (i < nd) ? xr[i] : 0.0f;
-                    }
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (i < nd) {
-                    const float4 *wr = (const float4 *)(w + (long long)(d0 + i) * Er_pad + e0);
-                    float4 wa = wr[0], wb = wr[1];
-                    float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int c = 0; c < 8; ++c) acc[j][c] = __builtin_fmaf(xv4[j][i], wv[c], acc[j][c]);
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                float v = acc[j][c];
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-                acc[j][c] = v;
-            }
-        if (lane == 0) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = t0 + j;
-                if (t < T) {
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        const int e = e0 + c;
-                        if (e < Er) logits[(long long)t * Er + e] = acc[j][c] + (bias ? bias[e] : 0.0f);
-                    }
-                }
-            }
-        }
+typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float rf32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kRouterLdsPieces = 4096;  // 16-byte weight pieces per chunk (64 KB)
+
+__global__ void router_split_kernel(const float *__restrict__ w, int D, int Er, int Er_pad, int Ep, int Dp,
+                                    uint16_t *__restrict__ ws) {
+#pragma clang fp contract(off)
+    const long long n = (long long)Ep * Dp;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        const int e = (int)(i / Dp), d = (int)(i - (long long)e * Dp);
+        const float v = (e < Er && d < D) ? w[(long long)d * Er_pad + e] : 0.0f;
+        const uint16_t b0 = f32_to_bf16(v);
+        const float r1 = v - bf16_to_f32(b0);
+        const uint16_t b1 = f32_to_bf16(r1);
+        const float r2 = r1 - bf16_to_f32(b1);
+        ws[i] = b0;
+        ws[n + i] = b1;
+        ws[2 * n + i] = f32_to_bf16(r2);
     }
 }
 
-hipError_t launch_router_logits(const void *x, int x_bf16, int T, int D, int Er, int Er_pad,
-                                const float *wr, const float *bias, float *logits, hipStream_t s) {
-    if (T <= 0) return hipSuccess;
-    dim3 grid((T + 15) / 16), block(256);
-    if (x_bf16)
-        hipLaunchKernelGGL(router_logits_kernel<1>, grid, block, 0, s, x, T, D, Er, Er_pad, wr, bias, logits);
-    else
-        hipLaunchKernelGGL(router_logits_kernel<0>, grid, block, 0, s, x, T, D, Er, Er_pad, wr, bias, logits);
+hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep, int Dp, uint16_t *ws,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(router_split_kernel, dim3(256), dim3(256), 0, s, w, D, Er, Er_pad, Ep, Dp, ws);
     return hipGetLastError();
+}
+
+// 8 consecutive x values of row t from column k (a multiple of 8) as bf16
+// parts (fp32 x: hi, mid, lo).  Otherwise columns >= D read as 0.  ALIGNED
+// (D a multiple of 32, so every 32-column block the MFMAs use lies below D):
+// one or two 16-byte loads from an address clamped into the row, no branch
+// and no select, so the loads of a chunk are all in flight together (a
+// select on the loaded value lets the compiler sink the load into a branch).
+template <int XBF16, int ALIGNED>
+__device__ inline void load_x8(const void *x, int D, int t, int k, rbf16x8_t *p) {
+    const bool in = k < D;
+    if (XBF16) {
+        const uint16_t *row = (const uint16_t *)x + (long long)t * D;
+        uint16_t v[8];
+        if (ALIGNED) {
+            const uint4 q = *(const uint4 *)(row + min(k, D - 8));
+            __builtin_memcpy(v, &q, 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (k + i < D) ? row[k + i] : (uint16_t)0;
+        }
+        __builtin_memcpy(&p[0], v, 16);
+    } else {
+#pragma clang fp contract(off)
+        const float *row = (const float *)x + (long long)t * D;
+        float v[8];
+        if (ALIGNED) {
+            const int kk = min(k, D - 8);
+            const float4 q0 = *(const float4 *)(row + kk), q1 = *(const float4 *)(row + kk + 4);
+            v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (k + i < D) ? row[k + i] : 0.0f;
+        }
+        uint16_t h0[8], h1[8], h2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            h0[i] = f32_to_bf16(v[i]);
+            const float r1 = v[i] - bf16_to_f32(h0[i]);
+            h1[i] = f32_to_bf16(r1);
+            h2[i] = f32_to_bf16(r1 - bf16_to_f32(h1[i]));
+        }
+        __builtin_memcpy(&p[0], h0, 16);
+        __builtin_memcpy(&p[1], h1, 16);
+        __builtin_memcpy(&p[2], h2, 16);
+    }
+}
+
+// Block: 4 waves x 32 tokens (two 16-token MFMA tiles per wave) over one K
+// slice; the slice's weight parts pass through LDS in chunks of KC columns
+// (rows padded by 16 bytes so the 16 rows one read touches fall in distinct
+// banks).  All global loads of a chunk are issued before any is used: the
+// wave's x fragments and the thread's share of the weight chunk (loads past
+// the slice use clamped in-bounds addresses and are not used).
+// v_mfma_f32_16x16x32_bf16: A = 16 tokens x 32 k (lane l: token l % 16,
+// k 8 (l / 16) .. +8), B = 32 k x 16 experts, D lane l: expert l % 16, tokens
+// 4 (l / 16) .. +4.
+template <int XBF16, int ALIGNED, int KC>
+__global__ __launch_bounds__(256) void router_mfma_kernel(RouterArgs r) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t rlds[];
+    constexpr int NP = XBF16 ? 1 : 3;       // activation parts
+    constexpr int RS = KC * 2 + 16;         // LDS row stride
+    constexpr int NWP = kRouterLdsPieces / 256;  // weight pieces per thread (upper bound)
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int tb = blockIdx.x * 128 + w * 32;
+    const int k_begin = blockIdx.y * r.ks_len, k_end = min(r.Dp, k_begin + r.ks_len);
+    const int ET = r.Ep / 16;
+    const int l16 = lane & 15, kq = (lane >> 4) * 8;
+    const long long np = (long long)r.Ep * r.Dp;
+    const int npieces = 3 * r.Ep * (KC / 8);  // 16-byte weight pieces per chunk (<= kRouterLdsPieces)
+    rf32x4_t acc[2][8];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int et = 0; et < 8; ++et) acc[ti][et] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kc0 = k_begin; kc0 < k_end; kc0 += KC) {
+        rbf16x8_t a[KC / 32][2][NP];
+#pragma unroll
+        for (int kq32 = 0; kq32 < KC / 32; ++kq32)
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti)
+                load_x8<XBF16, ALIGNED>(r.x, r.D, min(tb + ti * 16 + l16, r.T - 1), kc0 + kq32 * 32 + kq, a[kq32][ti]);
+        uint4 wv[NWP];
+#pragma unroll
+        for (int j = 0; j < NWP; ++j) {
+            const int i = min((int)threadIdx.x + j * 256, npieces - 1);
+            const int row = i / (KC / 8), c = i - row * (KC / 8);  // row = part * Ep + expert
+            const int part = row / r.Ep, e = row - part * r.Ep;
+            const int col = min(kc0 + c * 8, r.Dp - 8);              // the slice's last chunk may be short
+            wv[j] = *(const uint4 *)(r.ws + part * np + (long long)e * r.Dp + col);
+        }
+#pragma unroll
+        for (int j = 0; j < NWP; ++j) {  // clamped pieces rewrite the last piece with its own value
+            const int i = min((int)threadIdx.x + j * 256, npieces - 1);
+            const int row = i / (KC / 8), c = i - row * (KC / 8);
+            *(uint4 *)(rlds + row * RS + c * 16) = wv[j];
+        }
+        __syncthreads();
+        const int kn = min(KC, k_end - kc0);
+#pragma unroll
+        for (int kq32 = 0; kq32 < KC / 32; ++kq32) {
+            const int kk = kq32 * 32;
+#pragma unroll
+            for (int et = 0; et < 8; ++et) {
+                if (kk < kn && et < ET) {
+                    rbf16x8_t b[3];
+#pragma unroll
+                    for (int p = 0; p < 3; ++p)
+                        b[p] = *(const rbf16x8_t *)(rlds + (p * r.Ep + et * 16 + l16) * RS + (kk + kq) * 2);
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        // x parts i times weight parts j with i + j <= 2
+#pragma unroll
+                        for (int i = 0; i < NP; ++i)
+#pragma unroll
+                            for (int j = 0; j + i < 3; ++j)
+                                acc[ti][et] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kq32][ti][i], b[j], acc[ti][et], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float *out = r.part + (long long)blockIdx.y * r.T * r.Er;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int et = 0; et < 8; ++et) {
+            const int e = et * 16 + l16;
+            if (et < ET && e < r.Er)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int t = tb + ti * 16 + (lane >> 4) * 4 + rr;
+                    if (t < r.T) out[(long long)t * r.Er + e] = acc[ti][et][rr];
+                }
+        }
+}
+
+void router_plan(RouterArgs &r) {
+    // LDS chunk: three weight parts of Ep rows within 64 KB; 64, 128 or 256
+    // columns (64 for fp32 x, whose fragments take three times the registers)
+    const int fit = (65536 / (3 * r.Ep) - 16) / 2;
+    int kc = fit >= 256 ? 256 : (fit >= 128 ? 128 : 64);
+    if (!r.x_bf16) kc = 64;
+    // about 256 workgroups: K slices fill in for a small batch
+    const int blocks_t = (r.T + 127) / 128;
+    int nks = (256 + blocks_t - 1) / blocks_t;
+    nks = std::max(1, std::min(std::min(nks, kRouterMaxSlices), r.Dp / 32));
+    int ks_len = ((r.Dp + nks - 1) / nks + 31) / 32 * 32;
+    if (ks_len > kc) ks_len = (ks_len + kc - 1) / kc * kc;  // whole chunks
+    else kc = ks_len <= 64 ? 64 : (ks_len <= 128 ? 128 : 256);
+    nks = (r.Dp + ks_len - 1) / ks_len;
+    r.nks = nks;
+    r.ks_len = ks_len;
+    r.kc = kc;
+}
+
+hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s) {
+    if (r.T <= 0) return hipSuccess;
+    const size_t lds = (size_t)3 * r.Ep * (r.kc * 2 + 16);
+    dim3 grid((r.T + 127) / 128, r.nks), block(256);
+    const bool al = (r.D & 31) == 0;
+#define MOE_ROUTER_CASE(XB, AL, KC)                                                     \
+    if ((x_bf16 != 0) == (XB != 0) && al == (AL != 0) && r.kc == KC) {                  \
+        hipLaunchKernelGGL((router_mfma_kernel<XB, AL, KC>), grid, block, lds, s, r);   \
+        return hipGetLastError();                                                       \
+    }
+    MOE_ROUTER_CASE(1, 1, 256) MOE_ROUTER_CASE(1, 1, 128) MOE_ROUTER_CASE(1, 1, 64)
+    MOE_ROUTER_CASE(1, 0, 256) MOE_ROUTER_CASE(1, 0, 128) MOE_ROUTER_CASE(1, 0, 64)
+    MOE_ROUTER_CASE(0, 1, 64) MOE_ROUTER_CASE(0, 0, 64)
+#undef MOE_ROUTER_CASE
+    return hipErrorInvalidValue;
 }
 
 // ============================================================================
 // Gating.  One thread per token, 256 tokens per block.
 // ============================================================================
-
-// NNlib.softmax over l[0..n) into p (global), recipe:
-//   m = max (NaN ignored); e = (float)exp((double)(l - m)) (NNlib's branch for
-//   m == +Inf: e = l == +Inf); s = sequential fp32 sum; p = e / s.
-// Returns s and m so the caller can form logsumexp.
-__device__ inline void softmax_row(const float *__restrict__ l, int n, float *__restrict__ p,
-                                   float &m_out, float &s_out) {
-#pragma clang fp contract(off)
-    float m = -INFINITY;
-    for (int i = 0; i < n; ++i) {
-        const float v = l[i];
-        if (v > m) m = v;
-    }
-    float s = 0.0f;
-    for (int i = 0; i < n; ++i) {
-        const float v = l[i];
-        float e;
-        if (m == INFINITY)
-            e = (v == INFINITY) ? 1.0f : 0.0f;
-        else
-            e = (float)exp((double)(v - m));
-        p[i] = e;
-        s = s + e;
-    }
-    for (int i = 0; i < n; ++i) p[i] = p[i] / s;
-    m_out = m;
-    s_out = s;
-}
 
 // Top-k by the isless key, descending, lower index first on ties; then the
 // gates p_sel ./ sum(p_sel) with the sum in slot order.
@@ -171,39 +255,129 @@ __device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *
     for (int j = 0; j < k; ++j) g[j] = p[sel[j]] / s;
 }
 
-__global__ __launch_bounds__(kRouteBlock) void route_kernel(RouteArgs a) {
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma clang fp contract(off)
-    __shared__ int wcnt[kRouteBlock / 64][MOE_MAX_EXPERTS];
+    // Block: kRouteBlock tokens, kRouteThreads threads.  Work that the recipe
+    // makes sequential per token (max, the fp32 sum in expert order, top-k,
+    // the fp64 entropy sum) runs one thread per token (threads < kRouteBlock,
+    // all in wave 0); the per-element work (logits, fp64 exp and log terms) is
+    // spread over every thread.  Rows live in LDS (stride E + 1 words).
+    constexpr int NWV = 1;  // the token threads form one wave
+    constexpr int RW = MOE_MAX_EXPERTS + 1;
+    __shared__ int wcnt[NWV][MOE_MAX_EXPERTS];
     __shared__ double red[2][kRouteBlock];
+    __shared__ float lrow[kRouteBlock][RW];    // logits
+    __shared__ float prow[kRouteBlock][RW];    // exp terms, then probabilities (before the shared-gating scale)
+    __shared__ float srow[kRouteBlock][RW];    // output probabilities (after it)
+    __shared__ float zrow[kRouteBlock][RW];    // shared gating: exp terms of all rows for the z-loss
+    __shared__ double hrow[kRouteBlock][RW];   // entropy terms p log(p + 1e-8)
+    __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int t = blockIdx.x * kRouteBlock + tid;
-    const bool valid = t < a.T;
+    const int t0 = blockIdx.x * kRouteBlock;
+    const int t = t0 + tid;
+    const int ntok = min(kRouteBlock, a.T - t0);
+    const bool tok = tid < kRouteBlock;         // a token thread
+    const bool valid = tok && t < a.T;
+    const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
+    const int ns = shared_gate ? a.ns : 0;      // rows before the routed ones
+    const int Ero = a.E - ns;                   // routed rows (softmax width)
 
-    for (int i = tid; i < (kRouteBlock / 64) * MOE_MAX_EXPERTS; i += kRouteBlock) (&wcnt[0][0])[i] = 0;
+    for (int i = tid; i < NWV * MOE_MAX_EXPERTS; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
+
+    // (1) router logits: the K-slice partial sums in slice order, then the bias
+    for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
+        const int tt = q / a.Er, i = q - tt * a.Er;
+        const long long o = (long long)(t0 + tt) * a.Er + i;
+        float pv[kRouterMaxSlices];  // all slices loaded before the ordered sum
+#pragma unroll
+        for (int sl = 0; sl < kRouterMaxSlices; ++sl)
+            pv[sl] = (sl < a.nks) ? a.part[(long long)sl * a.T * a.Er + o] : 0.0f;
+        float v = pv[0];
+#pragma unroll
+        for (int sl = 1; sl < kRouterMaxSlices; ++sl)
+            if (sl < a.nks) v = v + pv[sl];
+        if (a.bias) v = v + a.bias[i];
+        a.logits[o] = v;
+        lrow[tt][i] = v;
+    }
+    __syncthreads();
+    // (2) per token: max of the routed logits (NaN ignored, first of equals
+    // kept) and, for shared gating, of all rows (z-loss)
+    if (valid) {
+        float m = -INFINITY;
+        for (int i = ns; i < a.E; ++i) {
+            const float v = lrow[tid][i];
+            if (v > m) m = v;
+        }
+        rmax[tid] = m;
+        if (shared_gate) {
+            float mz = -INFINITY;
+            for (int i = 0; i < a.Er; ++i) {
+                const float v = lrow[tid][i];
+                if (v > mz) mz = v;
+            }
+            zmax[tid] = mz;
+        }
+    }
+    __syncthreads();
+    // (3) exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m == +Inf)
+    for (int q = tid; q < ntok * Ero; q += kRouteThreads) {
+        const int tt = q / Ero, i = ns + (q - tt * Ero);
+        const float m = rmax[tt], v = lrow[tt][i];
+        prow[tt][i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
+    }
+    if (shared_gate)
+        for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
+            const int tt = q / a.Er, i = q - tt * a.Er;
+            zrow[tt][i] = (float)exp((double)(lrow[tt][i] - zmax[tt]));
+        }
+    __syncthreads();
+    // (4) per token: sum in expert order
+    if (valid) {
+        float s = 0.0f;
+        for (int i = ns; i < a.E; ++i) s = s + prow[tid][i];
+        rsum[tid] = s;
+    }
+    __syncthreads();
+    // (5) probabilities p = e / s; output rows (shared gating: shared rows 1/E,
+    // routed rows p scaled by 1 - ns/E in Float64) and their entropy terms
+    for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
+        const int tt = q / a.E, i = q - tt * a.E;
+        float pv;
+        if (i < ns) {
+            pv = 1.0f / (float)a.E;
+        } else {
+            const float pu = prow[tt][i] / rsum[tt];
+            prow[tt][i] = pu;
+            pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
+        }
+        srow[tt][i] = pv;
+        const double pd = (double)pv;
+        hrow[tt][i] = pd * log(pd + 1e-8);
+        a.probs[(long long)(t0 + tt) * a.E + i] = pv;
+    }
+    __syncthreads();
 
     int ex[MOE_MAX_TOPK];     // 1-based expert ids of this token's slots
     double zterm = 0.0, hterm = 0.0;
 #pragma unroll
     for (int j = 0; j < MOE_MAX_TOPK; ++j) ex[j] = 0;
 
+    // (6) per token: top-k and gates, logsumexp, entropy
     if (valid) {
-        const float *l = a.logits + (long long)t * a.Er;
-        float *p = a.probs + (long long)t * a.E;
+        const float *p = prow[tid];
         int sel[MOE_MAX_TOPK];
         float g[MOE_MAX_TOPK];
-        float m, s;
-        if (a.gate_kind == MOE_GATE_SHARED) {
-            const int ns = a.ns, Eall = a.E;
-            softmax_row(l + ns, Eall - ns, p + ns, m, s);
-            topk_row(p + ns, Eall - ns, a.k, sel, g);
+        if (shared_gate) {
+            // top-k and gates on the routed probabilities as the base gate
+            // returns them (before the 1 - ns/E scaling)
             const int tk = a.kt;
             const double gscale = 1.0 - (double)ns / (double)tk;
-            const double pscale = 1.0 - (double)ns / (double)Eall;
             const float gshared = 1.0f / (float)tk;
-            const float pshared = 1.0f / (float)Eall;
+            topk_row(p + ns, Ero, a.k, sel, g);
             for (int j = 0; j < ns; ++j) {
                 ex[j] = j + 1;
                 a.gates[(long long)t * tk + j] = gshared;
@@ -212,33 +386,24 @@ __global__ __launch_bounds__(kRouteBlock) void route_kernel(RouteArgs a) {
                 ex[ns + j] = sel[j] + ns + 1;
                 a.gates[(long long)t * tk + ns + j] = (float)((double)g[j] * gscale);
             }
-            for (int i = 0; i < ns; ++i) p[i] = pshared;
-            for (int i = ns; i < Eall; ++i) p[i] = (float)((double)p[i] * pscale);
-            // z-loss runs over every router row (src/core/moe_layer.jl:117-121)
-            float mz = -INFINITY;
-            for (int i = 0; i < a.Er; ++i) if (l[i] > mz) mz = l[i];
             float sz = 0.0f;
-            for (int i = 0; i < a.Er; ++i) sz = sz + (float)exp((double)(l[i] - mz));
-            m = mz;
-            s = sz;
+            for (int i = 0; i < a.Er; ++i) sz = sz + zrow[tid][i];
+            const float lse = zmax[tid] + (float)log((double)sz);
+            zterm = (double)(lse * lse);
         } else {
-            softmax_row(l, a.E, p, m, s);
             topk_row(p, a.E, a.k, sel, g);
             for (int j = 0; j < a.k; ++j) {
                 ex[j] = sel[j] + 1;
                 a.gates[(long long)t * a.kt + j] = g[j];
             }
+            // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe
+            const float lse = rmax[tid] + (float)log((double)rsum[tid]);
+            zterm = (double)(lse * lse);
         }
         for (int j = 0; j < a.kt; ++j) a.idx[(long long)t * a.kt + j] = ex[j];
-        // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe
-        const float lse = m + (float)log((double)s);
-        zterm = (double)(lse * lse);
-        // entropy of update_stats! in Float64
+        // entropy of update_stats! in Float64, expert order
         double hs = 0.0;
-        for (int i = 0; i < a.E; ++i) {
-            const double pv = (double)p[i];
-            hs = hs + pv * log(pv + 1e-8);
-        }
+        for (int i = 0; i < a.E; ++i) hs = hs + hrow[tid][i];
         hterm = -hs;
     }
     __syncthreads();
@@ -290,18 +455,19 @@ __global__ __launch_bounds__(kRouteBlock) void route_kernel(RouteArgs a) {
         }
     }
     const int nb = blockIdx.x;
-    for (int e = tid; e < a.E; e += kRouteBlock) {
+    for (int e = tid; e < a.E; e += kRouteThreads) {
         int c = 0;
-        for (int w = 0; w < kRouteBlock / 64; ++w) c += wcnt[w][e];
+        for (int w = 0; w < NWV; ++w) c += wcnt[w][e];
         a.blk_counts[(long long)nb * a.E + e] = c;
         // per-expert probability sums (Switch loss P_e) in fp64, token order
         double ps = 0.0;
-        const int tend = min(kRouteBlock, a.T - nb * kRouteBlock);
-        for (int i = 0; i < tend; ++i) ps += (double)a.probs[(long long)(nb * kRouteBlock + i) * a.E + e];
+        for (int i = 0; i < ntok; ++i) ps += (double)srow[i][e];
         a.blk_stats[(long long)nb * (a.E + 2) + e] = ps;
     }
-    red[0][tid] = zterm;
-    red[1][tid] = hterm;
+    if (tok) {
+        red[0][tid] = zterm;
+        red[1][tid] = hterm;
+    }
     __syncthreads();
     for (int st = kRouteBlock / 2; st > 0; st >>= 1) {
         if (tid < st) {
@@ -319,7 +485,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_kernel(RouteArgs a) {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
-    hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteBlock), 0, s, a);
+    hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), 0, s, a);
     return hipGetLastError();
 }
 
@@ -327,14 +493,23 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 // Scan: one block.  Per-expert totals, capacity clamp, offsets, per-block rank
 // bases, the (expert, m0) GEMM tile list and the loss scalars.
 // ============================================================================
-__global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
+// Wave-level fixed-order (butterfly) sum of a double: the same tree every call.
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
     __shared__ int cnt[MOE_MAX_EXPERTS];
     __shared__ int off[MOE_MAX_EXPERTS + 1];
     __shared__ int tstart[MOE_MAX_EXPERTS + 1];
     __shared__ double psum[MOE_MAX_EXPERTS];
+    __shared__ double zh[2];
     __shared__ int cap_s;
     const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, nwave = blockDim.x >> 6;
     if (tid == 0) {
         int cap = INT_MAX;
         if (a.training && a.drop) {
@@ -346,16 +521,42 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
         a.cap_out[0] = cap;
     }
     __syncthreads();
-    for (int e = tid; e < a.E; e += blockDim.x) {
-        int run = 0;
-        double ps = 0.0;
-        for (int b = 0; b < a.nblk; ++b) {
-            a.rank_base[(long long)b * a.E + e] = run;
-            run += a.blk_counts[(long long)b * a.E + e];
-            ps += a.blk_stats[(long long)b * (a.E + 2) + e];
+    // One wave per expert (and one more pair for the z / entropy sums): the
+    // exclusive prefix of the per-block counts over blocks (64 blocks per step,
+    // carried across steps), and the fp64 sums of the block statistics.
+    for (int e = wave; e < a.E + 1; e += nwave) {
+        if (e < a.E) {
+            int carry = 0;
+            double ps = 0.0;
+            for (int b0 = 0; b0 < a.nblk; b0 += 64) {
+                const int b = b0 + lane;
+                const int c = (b < a.nblk) ? a.blk_counts[(long long)b * a.E + e] : 0;
+                int incl = c;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int v = __shfl_up(incl, d);
+                    if (lane >= d) incl += v;
+                }
+                if (b < a.nblk) a.rank_base[(long long)b * a.E + e] = carry + incl - c;
+                carry += __shfl(incl, 63);
+                ps += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + e] : 0.0);
+            }
+            if (lane == 0) {
+                cnt[e] = min(carry, cap_s);
+                psum[e] = ps;
+            }
+        } else {
+            double zs = 0.0, hs = 0.0;
+            for (int b0 = 0; b0 < a.nblk; b0 += 64) {
+                const int b = b0 + lane;
+                zs += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + a.E] : 0.0);
+                hs += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + a.E + 1] : 0.0);
+            }
+            if (lane == 0) {
+                zh[0] = zs;
+                zh[1] = hs;
+            }
         }
-        cnt[e] = min(run, cap_s);
-        psum[e] = ps;
     }
     __syncthreads();
     if (tid == 0) {
@@ -371,11 +572,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
         a.num_tiles[0] = ts;
 
         // losses (src/balancing/losses.jl:15-36, 103-114)
-        double zs = 0.0, hs = 0.0;
-        for (int b = 0; b < a.nblk; ++b) {
-            zs += a.blk_stats[(long long)b * (a.E + 2) + a.E];
-            hs += a.blk_stats[(long long)b * (a.E + 2) + a.E + 1];
-        }
+        const double zs = zh[0], hs = zh[1];
         const float total = (float)((long long)a.T * a.kt);
         float s = 0.0f;
         for (int e = 0; e < a.E; ++e) {
@@ -408,7 +605,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
 }
 
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
