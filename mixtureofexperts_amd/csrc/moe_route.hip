@@ -18,6 +18,8 @@
 
 namespace moe {
 
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
 // ============================================================================
 // Router logits on MFMA at fp32 accuracy.
 //
@@ -609,6 +611,27 @@ hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Store U chunks of 8 bf16 per lane into the row of every position the token
+// holds (pos of lane j: position of entry j, < 0 if dropped).  Chunk u of a
+// lane is column min(d0 + 512 u + 8 lane, D - 8), the column its value was
+// loaded from: a lane past the row's end rewrites the last chunk with that
+// chunk's own value, so no store is conditional.
+template <int U>
+__device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int pos, int d0, int lane, const u32x4_t (&v)[U]) {
+    int cols[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) cols[u] = min(d0 + u * 512 + lane * 8, a.D - 8);
+#pragma nounroll
+    for (int j = 0; j < a.kt; ++j) {
+        const int p = __shfl(pos, j);
+        if (p >= 0) {
+            uint16_t *__restrict__ dst = (uint16_t *)a.xp + (long long)p * a.ld_xp;
+#pragma unroll
+            for (int u = 0; u < U; ++u) *(u32x4_t *)(dst + cols[u]) = v[u];
+        }
+    }
+}
+
 // ============================================================================
 // Permute: one wave per token.  Lanes < kt finalise the token's entries
 // (capacity drop + renormalisation, position), then the wave copies the
@@ -656,6 +679,38 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
         }
     }
     if (!a.copy_rows) return;
+    if (a.ct == CT_BF16 && a.x_bf16 && (a.D & 7) == 0) {
+        // 8 bf16 per lane per chunk; the loads of 8 chunks (8 KB per wave) are
+        // issued together from clamped in-row addresses, then stored to every
+        // position the token holds.
+        const uint16_t *__restrict__ src = (const uint16_t *)a.x + (long long)t * a.D;
+        constexpr int U = 8;
+        for (int d0 = 0; d0 < a.D; d0 += 512 * U) {
+            u32x4_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = *(const u32x4_t *)(src + min(d0 + u * 512 + lane * 8, a.D - 8));
+            store_row_chunk<U>(a, pos, d0, lane, v);
+        }
+        return;
+    }
+    if (a.ct == CT_BF16 && !a.x_bf16 && (a.D & 7) == 0) {
+        const float *__restrict__ src = (const float *)a.x + (long long)t * a.D;
+        constexpr int U = 4;
+        for (int d0 = 0; d0 < a.D; d0 += 512 * U) {
+            u32x4_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int d = min(d0 + u * 512 + lane * 8, a.D - 8);
+                const float4 f0 = *(const float4 *)(src + d), f1 = *(const float4 *)(src + d + 4);
+                v[u] = u32x4_t{f32_to_bf16(f0.x) | ((uint32_t)f32_to_bf16(f0.y) << 16),
+                                  f32_to_bf16(f0.z) | ((uint32_t)f32_to_bf16(f0.w) << 16),
+                                  f32_to_bf16(f1.x) | ((uint32_t)f32_to_bf16(f1.y) << 16),
+                                  f32_to_bf16(f1.z) | ((uint32_t)f32_to_bf16(f1.w) << 16)};
+            }
+            store_row_chunk<U>(a, pos, d0, lane, v);
+        }
+        return;
+    }
     for (int j = 0; j < a.kt; ++j) {
         const int p = __shfl(pos, j);
         if (p < 0) continue;
@@ -663,12 +718,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
             uint16_t *dst = (uint16_t *)a.xp + (long long)p * a.ld_xp;
             if (a.x_bf16) {
                 const uint16_t *src = (const uint16_t *)a.x + (long long)t * a.D;
-                if ((a.D & 7) == 0) {
-                    for (int d = lane * 8; d < a.D; d += 512)
-                        *(uint4 *)(dst + d) = *(const uint4 *)(src + d);
-                } else {
-                    for (int d = lane; d < a.D; d += 64) dst[d] = src[d];
-                }
+                for (int d = lane; d < a.D; d += 64) dst[d] = src[d];
             } else {
                 const float *src = (const float *)a.x + (long long)t * a.D;
                 for (int d = lane; d < a.D; d += 64) dst[d] = f32_to_bf16(src[d]);
@@ -701,12 +751,94 @@ hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
 // Combine: one wave per token.  out[t] = sum over the token's entries in
 // ascending expert order of gate * y, as separate fp32 multiply and add on a
 // zero start (src/core/moe_layer.jl:132, 205-217).  No atomics.
+//
+// Fast path (every one of the token's KT entries kept, y rows 16-byte
+// aligned): the entries are sorted by expert in registers, and all loads of
+// a chunk of U float4 per lane (KT entries x NS partial sums each) are issued
+// before any is summed.  Otherwise the generic path below.
 // ============================================================================
+template <int KT, int NS>
+__device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
+#pragma clang fp contract(off)
+    constexpr int U = (KT * NS >= 8) ? 2 : (KT * NS >= 4 ? 4 : 8);
+    int ee[KT], pp[KT];
+    float gg[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+        const long long ent = (long long)t * KT + j;
+        ee[j] = a.idx[ent];
+        pp[j] = a.pos_of[ent];
+        gg[j] = a.gates[ent];
+    }
+    // stable sort by expert id (distinct ids; a fixed compare-exchange network)
+#pragma unroll
+    for (int i = 0; i < KT; ++i)
+#pragma unroll
+        for (int j = 0; j + 1 < KT - i; ++j) {
+            const bool sw = ee[j] > ee[j + 1];
+            const int e0 = ee[j], p0 = pp[j];
+            const float g0 = gg[j];
+            ee[j] = sw ? ee[j + 1] : e0; ee[j + 1] = sw ? e0 : ee[j + 1];
+            pp[j] = sw ? pp[j + 1] : p0; pp[j + 1] = sw ? p0 : pp[j + 1];
+            gg[j] = sw ? gg[j + 1] : g0; gg[j + 1] = sw ? g0 : gg[j + 1];
+        }
+    float *__restrict__ o = a.out + (long long)t * a.D;
+    for (int d0 = 0; d0 < a.D; d0 += 256 * U) {
+        float4 v[KT][NS][U];
+#pragma unroll
+        for (int i = 0; i < KT; ++i)
+#pragma unroll
+            for (int sp = 0; sp < NS; ++sp)
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int d = min(d0 + u * 256 + lane * 4, a.D - 4);
+                    v[i][sp][u] = *(const float4 *)(a.y + (long long)pp[i] * a.ld_y + sp * a.split_stride + d);
+                }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int i = 0; i < KT; ++i) {
+                float4 y = v[i][0][u];
+#pragma unroll
+                for (int sp = 1; sp < NS; ++sp) {
+                    y.x = y.x + v[i][sp][u].x; y.y = y.y + v[i][sp][u].y;
+                    y.z = y.z + v[i][sp][u].z; y.w = y.w + v[i][sp][u].w;
+                }
+                const float g = gg[i];
+                acc.x = acc.x + g * y.x;
+                acc.y = acc.y + g * y.y;
+                acc.z = acc.z + g * y.z;
+                acc.w = acc.w + g * y.w;
+            }
+            const int d = d0 + u * 256 + lane * 4;
+            if (d < a.D) *(float4 *)(o + d) = acc;
+        }
+    }
+}
+
+template <int KT, int NS>
+__device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, int t, int lane) {
+    if (a.kt != KT || a.nsplit != NS) return false;
+    combine_fast<KT, NS>(a, t, lane);
+    return true;
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
+    bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0 && (a.split_stride & 3) == 0;
+    for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
+    if (all_kept) {
+        if (try_combine_fast<2, 1>(a, t, lane) || try_combine_fast<2, 2>(a, t, lane) ||
+            try_combine_fast<1, 1>(a, t, lane) || try_combine_fast<1, 2>(a, t, lane) ||
+            try_combine_fast<8, 1>(a, t, lane) || try_combine_fast<8, 2>(a, t, lane) ||
+            try_combine_fast<4, 1>(a, t, lane) || try_combine_fast<4, 2>(a, t, lane) ||
+            try_combine_fast<6, 1>(a, t, lane) || try_combine_fast<6, 2>(a, t, lane))
+            return;
+    }
     int ee[MOE_MAX_TOPK], pp[MOE_MAX_TOPK];
     float gg[MOE_MAX_TOPK];
     int n = 0;
