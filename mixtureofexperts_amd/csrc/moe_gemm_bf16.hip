@@ -1,7 +1,7 @@
 // moe_gemm_bf16.hip -- the bf16 grouped expert GEMM (the layer's MFMA-bound
-// hot spot) for CDNA4: direct global->LDS loads, two LDS stages, 256x256 block
-// tiles on v_mfma_f32_32x32x16_bf16 with the expert FFN's elementwise work in
-// the epilogue.
+// hot spot) for CDNA4: direct global->LDS loads into a ring of LDS stages,
+// 256-column block tiles on v_mfma_f32_32x32x16_bf16, with the expert FFN's
+// elementwise work in the epilogue.
 //
 //   MODE_GATED_UP : h = act(A W1^T) .* (A W3^T)       GatedExpert (src/experts/gated.jl:29-34)
 //   MODE_STD_UP   : h = act(A W1^T + b1)              StandardExpert (src/experts/standard.jl:38-47)
@@ -11,24 +11,28 @@
 // weights are packed [E][Npad][Kpad] bf16, K contiguous.
 //
 // Work list.  The device-side scan writes tile_start[e] = sum over e' < e of
-// ceil(count_e' / BM).  Work item id = (tile_start[e] + m) * ... is ordered
-// expert-major, then n-tile, then m-tile, so consecutive items share one
-// weight tile.  Workgroups are dealt round-robin to the 8 XCDs, so item ids
-// are assigned in contiguous per-XCD ranges: the blocks that share a weight
-// tile and walk K in step run behind the same L2.
+// ceil(count_e' / BM).  Work item id is ordered expert-major, then n-tile (and
+// K range), then m-tile, so consecutive items share one weight tile.
+// Workgroups are dealt round-robin to the 8 XCDs, so item ids are assigned in
+// contiguous per-XCD ranges: the blocks that share a weight tile and walk K in
+// step run behind the same L2.
 //
-// Block: 256 threads = 4 waves as 2 (M) x 2 (N); each wave owns a
-// (BM/2) x 128 sub-tile = (BM/64) x 4 blocks of 32x32 accumulators.  For
-// MODE_GATED_UP the 256 B-tile rows are 128 rows of W1 followed by the same
-// 128 rows of W3, and each wave's four 32-column blocks are (gate, up) pairs
-// for 64 h columns, so the silu-mul pairs sit in the same lane's registers.
+// Block: 4 waves, one per SIMD, as 2 (M) x 2 (N); each wave owns a (BM/2) x 128
+// sub-tile and interleaves its MFMAs with the fragment reads of the next
+// sub-step and the loads NS-1 stages ahead.  A wave runs MFMAs only on its
+// 32-row blocks that hold rows of the tile: the last tile of an expert skips
+// the padding past the expert's last row.
 //
-// LDS: per stage an A tile (BM rows) and a B tile (256 rows) of 64 bf16 =
-// 128 B per row; the 16-byte chunks of row r are stored at chunk ^ (r & 7) so
-// the fragment reads (32 rows, one chunk) are spread over all banks.  Each
-// global_load_lds_dwordx4 writes 1 KB = 8 rows of LDS linearly (lane l ->
-// offset 16 l), so the swizzle is applied on the global side: lane l fetches
-// logical chunk (l & 7) ^ (l >> 3) of its row.
+// For MODE_GATED_UP the 256 B-tile rows are 128 rows of W1 followed by the
+// same 128 rows of W3, and each wave's four 32-column blocks are (gate, up)
+// pairs for 64 h columns, so the silu-mul pairs sit in the same lane's
+// registers.
+//
+// LDS: per stage an A tile (BM rows) and a B tile (256 rows) of 32 bf16 =
+// 64 B per row; the 16-byte chunks of row r are stored at chunk ^ ((r >> 2) & 3)
+// so the fragment reads (32 rows, one chunk) spread over all 64 banks.  Each
+// global_load_lds_dwordx4 writes 1 KB = 16 rows linearly (lane l -> offset
+// 16 l), so the swizzle is applied on the global side.
 #include <type_traits>
 
 #include "moe_internal.h"
@@ -83,71 +87,34 @@ __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(
 // inline assembly that the compiler does not see as a memory access: its wait
 // insertion would otherwise treat every later LDS read as possibly reading
 // these bytes and wait for all loads in flight.  Correct ordering is kept by
-// the kernel itself: each slot is refilled only after a barrier that follows
-// its last reads, and read only after a barrier that follows wait_vmcnt for
-// its loads (volatile asm statements keep their relative order).
+// the kernels themselves: each slot is refilled only after a barrier that
+// follows its last reads, and read only after a barrier that follows
+// wait_vmcnt for its loads (volatile asm statements keep their relative order).
 __device__ __forceinline__ void lds_dma16(const uint8_t *gaddr, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds) : "m0");
 }
 
-__device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p) {
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (const uint8_t *)(((uint64_t)hi << 32) | lo);
-}
+// ---- work item -> tile --------------------------------------------------------
+struct TileJob {
+    int e;             // expert
+    int ks;            // K range (split-K index)
+    int KT;            // 32-wide K stages in the range
+    int rows;          // valid rows of the tile (<= BM)
+    int n0;            // first B row of the tile (first h column in the gated mode)
+    long long arow0;   // first A row
+};
 
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
-    return (uint32_t)(uintptr_t)(const MOE_LDS_AS uint8_t *)p;
-}
-
-template <int MODE, int BM, int ACT, int NWAVE>
-__global__ __launch_bounds__(NWAVE * 64) __attribute__((amdgpu_waves_per_eu(NWAVE / 4, NWAVE / 4))) void
-grouped_gemm_bf16_kernel(GemmArgs g) {
-    constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
-    constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
-    constexpr int A_BYTES = BM * ROWB;
-    constexpr int STAGE = A_BYTES + 256 * ROWB;
-    constexpr int NS = (BM == 256) ? 4 : 6;  // LDS ring slots: 128 KB / 144 KB
-    constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
-    constexpr int NWN = NWAVE / 2;       // waves along N
-    constexpr int WN = 256 / NWN;        // wave tile columns (B rows): 128 or 64
-    constexpr int IM = WM / 32;          // 32-row blocks per wave
-    constexpr int JN = WN / 32;          // 32-column blocks per wave
-    constexpr int LA = BM / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
-    constexpr int LB = 256 / (16 * NWAVE);  // B loads per wave per stage
-    constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
-    constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
-    static_assert(LA >= 1 && LB >= 1, "wave count");
-    static_assert(NS * STAGE <= 160 * 1024, "LDS");
-    // One array per ring slot: the compiler tracks the direct-to-LDS loads per
-    // array, so a fragment read waits only for loads into its own slot.
-    __shared__ __attribute__((aligned(1024))) uint8_t slot0[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot1[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot2[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot3[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot4[NS > 4 ? STAGE : 16];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot5[NS > 5 ? STAGE : 16];
-    auto slot = [&](auto J_) -> MOE_LDS_AS uint8_t * {
-        constexpr int J = decltype(J_)::value;
-        if constexpr (J == 0) return (MOE_LDS_AS uint8_t *)slot0;
-        else if constexpr (J == 1) return (MOE_LDS_AS uint8_t *)slot1;
-        else if constexpr (J == 2) return (MOE_LDS_AS uint8_t *)slot2;
-        else if constexpr (J == 3) return (MOE_LDS_AS uint8_t *)slot3;
-        else if constexpr (J == 4) return (MOE_LDS_AS uint8_t *)slot4;
-        else return (MOE_LDS_AS uint8_t *)slot5;
-    };
-
-    // ---- work item -> (expert, n-tile, K range, m-tile) -------------------------
+template <int BM, int NB>
+__device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
     const int NT = g.n_tiles;
-    const int KS = g.ksplit;                   // K ranges per output tile
+    const int KS = g.ksplit;
     const int W = g.tile_start[g.E] * NT * KS;
     const int L = blockIdx.x;
     const int perx = (W + 7) >> 3;
     const int slot_id = L >> 3;
-    if (slot_id >= perx) return;
+    if (slot_id >= perx) return false;
     const int id = (L & 7) * perx + slot_id;
-    if (id >= W) return;
+    if (id >= W) return false;
     int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT * KS <= id (a non-empty expert)
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -156,194 +123,85 @@ grouped_gemm_bf16_kernel(GemmArgs g) {
     const int e = lo;
     const int t0 = g.tile_start[e];
     const int nte = g.tile_start[e + 1] - t0;
-    const int local = id - t0 * NT * KS;        // within the expert: (n-tile, K range) major, m-tile minor
+    const int local = id - t0 * NT * KS;  // within the expert: (n-tile, K range) major, m-tile minor
     const int ntks = local / nte;
-    const int nt = ntks / KS, ks = ntks - nt * KS;
+    const int nt = ntks / KS;
     const int m0 = (local - ntks * nte) * BM;
-    const int rows = min(BM, g.counts[e] - m0);
-    const long long arow0 = (long long)g.offsets[e] + m0;
-    const int n0 = nt * (NB == 2 ? 128 : 256);  // first B row (h column for the gated mode)
+    jb.e = e;
+    jb.ks = ntks - nt * KS;
+    jb.KT = g.K / 32 / KS;
+    jb.rows = min(BM, g.counts[e] - m0);
+    jb.arow0 = (long long)g.offsets[e] + m0;
+    jb.n0 = nt * (NB == 2 ? 128 : 256);
+    return true;
+}
 
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w & 1, wn = w >> 1;
-
-    // ---- direct global -> LDS copy of one stage ----------------------------------
-    // A stage row is 64 B = four 16-byte chunks; chunk c of row r is stored at
-    // c ^ swz(r), swz(r) = (r >> 2) & 3, so that 16 consecutive rows read at
-    // one logical chunk hit 16 distinct (bank group, chunk) slots.  Load i of a
-    // wave writes 1 KB = 16 rows linearly (lane l -> byte 16 l: row 16i + (l >> 2),
-    // physical chunk l & 3), so lane l fetches logical chunk (l & 3) ^ ((l >> 4) & 3).
+// ---- global -> LDS load addressing -------------------------------------------
+// Load i of wave w fetches 16 rows of one stage (64 B each): lane l covers row
+// 16 i + (l >> 2) of its group and logical chunk (l & 3) ^ ((l >> 4) & 3), so
+// that the linear 1 KB LDS write lands each chunk at its swizzled place.  The
+// wave's LA loads cover A rows w * BM / NWAVE ..; its LB loads cover B-tile rows
+// w * 256 / NWAVE .. (gated: tile rows [0, 128) are W1 rows n0.., [128, 256) the
+// same W3 rows).  A rows past the tile's valid rows repeat its last row.
+template <int BM, int NB, int NWAVE, int LA, int LB>
+__device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, int w, int lane,
+                                          const uint8_t *(&gsrc)[LA + LB], uint32_t (&ldst)[LA + LB]) {
+    constexpr int ROWB = 64;
+    constexpr int A_BYTES = BM * ROWB;
     const long long lda_b = g.lda * 2, ldb_b = g.ldb * 2;
-    const int KT = g.K / 32 / KS;               // stages of this item's K range
-    const long long k0b = (long long)ks * KT * ROWB;  // its first K byte in a row
+    const long long k0b = (long long)jb.ks * jb.KT * ROWB;  // first K byte of the range in a row
     const int lr = lane >> 2;
     const int lch = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t *Ab = (const uint8_t *)g.A + arow0 * lda_b + k0b;
-    const uint8_t *gsrc[NL];
-    uint32_t ldst[NL];
+    const uint8_t *Ab = (const uint8_t *)g.A + jb.arow0 * lda_b + k0b;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int r = w * (BM / NWAVE) + 16 * i;
-        gsrc[i] = Ab + (long long)min(r + lr, rows - 1) * lda_b + lch * 16;
+        gsrc[i] = Ab + (long long)min(r + lr, jb.rows - 1) * lda_b + lch * 16;
         ldst[i] = r * ROWB;
     }
-    // B tile row r (of 256) is written by wave r / (256 / NWAVE).  Gated: tile rows
-    // [0, 128) are W1 rows n0.., rows [128, 256) the same W3 rows (the upper half of
-    // the waves fetch W3).
     const uint8_t *Bsrc = (NB == 2 && w >= NWAVE / 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
-    const uint8_t *Bb = Bsrc + ((long long)e * g.b_stride + (long long)n0 * g.ldb) * 2;  // row n0 of expert e
+    const uint8_t *Bb = Bsrc + ((long long)jb.e * g.b_stride + (long long)jb.n0 * g.ldb) * 2;  // row n0 of expert e
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
-        const int t = w * (256 / NWAVE) + 16 * i;          // tile row
-        const int r = (NB == 2) ? (t & 127) : t;           // row within the weight matrix, from n0
+        const int t = w * (256 / NWAVE) + 16 * i;  // tile row
+        const int r = (NB == 2) ? (t & 127) : t;   // row within the weight matrix, from n0
         gsrc[LA + i] = Bb + (long long)(r + lr) * ldb_b + k0b + lch * 16;
         ldst[LA + i] = A_BYTES + t * ROWB;
     }
-    // load i of stage kt into ring slot J
-    auto dma = [&](auto J_, int kt, int i) {
-        const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
-        lds_dma16(gsrc[i] + (long long)kt * ROWB, __builtin_amdgcn_readfirstlane(l));
-    };
+}
 
-    // ---- fragment addressing (fragment row bases are multiples of 32, so
-    // swz(row) = (r32 >> 2) & 3) ------------------------------------------------
-    // Gated: a wave's JN column blocks are (gate, up) pairs, block 2m from the W1
-    // half of the tile and block 2m + 1 the same rows of the W3 half, covering h
-    // columns wn * WN / 2 + 32 m.
+// B-tile row of fragment block j of a wave whose column group is wn (WN
+// B-tile rows per group).  Gated: blocks 2m and 2m + 1 are the W1 and W3 rows
+// of h columns wn * WN / 2 + 32 m.
+template <int NB, int WN>
+__device__ __forceinline__ int b_frag_row(int j, int wn) {
+    return (NB == 2) ? ((j & 1) * 128 + wn * (WN / 2) + (j >> 1) * 32) : (wn * WN + j * 32);
+}
+
+// ---- epilogue ---------------------------------------------------------------------
+// The MFMA computes the transposed block (weights are its A operand): lane l
+// holds token row l % 32 of the 32-row block and output columns 8 (q / 4) +
+// 4 (l / 32) + q % 4, i.e. four consecutive columns per q / 4, written as one
+// 8-byte (bf16) or 16-byte (fp32) store.  row0: the wave's first tile row.
+template <int MODE, int ACT, int IM, int JN, int WN>
+__device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
+                                           int row0, int wn, int lane) {
     const int half = lane >> 5;
     const int r32 = lane & 31;
-    const int a_frag = (wm * WM + r32) * ROWB;
-    int b_frag[JN];
-#pragma unroll
-    for (int j = 0; j < JN; ++j) {
-        const int row = (NB == 2) ? ((j & 1) * 128 + wn * (WN / 2) + (j >> 1) * 32) : (wn * WN + j * 32);
-        b_frag[j] = A_BYTES + (row + r32) * ROWB;
-    }
-    int choff[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) choff[kk] = ((kk * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
-
-    f32x16_t acc[IM][JN];
-#pragma unroll
-    for (int i = 0; i < IM; ++i)
-#pragma unroll
-        for (int j = 0; j < JN; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
-
-    bf16x8_t fa[2][IM], fb[2][JN];
-    auto read_frag = [&](auto J_, int kk, int r, bf16x8_t *af, bf16x8_t *bfr) {
-        const MOE_LDS_AS uint8_t *sb = slot(J_);
-        if (r < IM) af[r] = *(const MOE_LDS_AS bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[kk]);
-        else bfr[r - IM] = *(const MOE_LDS_AS bf16x8_t *)(sb + b_frag[r - IM] + choff[kk]);
-    };
-    auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
-#pragma unroll
-        for (int i = 0; i < IM; ++i)
-#pragma unroll
-            for (int j = 0; j < JN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-    };
-    // One MFMA, then one of the IM + JN fragment reads of the next sub-step,
-    // until the reads are placed; the remaining MFMAs follow.
-    constexpr int NMF = IM * JN, NRD = IM + JN;
-    static_assert(NRD <= NMF, "interleave pattern");
-    auto interleave = [&]() {
-#pragma unroll
-        for (int t = 0; t < NRD; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
-    };
-
-    // ---- main loop --------------------------------------------------------------
-    // Stage s (32 K columns, two k16 sub-steps) lives in ring slot s % NS and is
-    // loaded NS - 1 stages ahead.  Per stage:
-    //   sub-step 0: MFMAs of (s, 0) | LDS reads of (s, 1)   | loads of stage s+NS-1, first half
-    //   wait until this wave's loads of stage s+1 landed; barrier (every wave's have)
-    //   sub-step 1: MFMAs of (s, 1) | LDS reads of (s+1, 0) | loads of stage s+NS-1, second half
-    // Stage s+NS-1 goes to the slot of stage s-1, whose last reads (its sub-step
-    // 1 fragments) ended before the barrier of stage s-1.  Past the last stage
-    // the loads repeat stage KT-1 (in bounds, into a slot nothing reads again),
-    // which keeps the vmcnt arithmetic exact: when the barrier of stage s is
-    // reached, the loads issued after those of stage s+1 are NS-3 whole stages
-    // and the first NL0 loads of stage s+NS-1.
-    constexpr int AFTER = (NS - 3) * NL + NL0;
-#pragma unroll
-    for (int s0 = 0; s0 < NS - 1; ++s0) {
-        const int kt = min(s0, KT - 1);
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            switch (s0) {
-            case 0: dma(std::integral_constant<int, 0>{}, kt, i); break;
-            case 1: dma(std::integral_constant<int, 1>{}, kt, i); break;
-            case 2: dma(std::integral_constant<int, 2>{}, kt, i); break;
-            case 3: dma(std::integral_constant<int, 3>{}, kt, i); break;
-            default: dma(std::integral_constant<int, 4>{}, kt, i); break;
-            }
-        }
-    }
-    wait_vmcnt<(NS - 2) * NL>();  // stage 0 landed
-    barrier_lds();
-#pragma unroll
-    for (int r = 0; r < IM + JN; ++r) read_frag(std::integral_constant<int, 0>{}, 0, r, fa[0], fb[0]);
-
-    auto stage = [&](auto J_, int st) {
-        constexpr int J = decltype(J_)::value;
-        using Jn = std::integral_constant<int, (J + 1) % NS>;       // slot of stage s+1
-        using Jl = std::integral_constant<int, (J + NS - 1) % NS>;  // slot of stage s-1 = s+NS-1
-        const int kl = min(st + NS - 1, KT - 1);
-#pragma unroll
-        for (int t = 0; t < IM + JN; ++t) read_frag(J_, 1, t, fa[1], fb[1]);
-#pragma unroll
-        for (int t = 0; t < NL0; ++t) dma(Jl{}, kl, t);
-        mfmas(fa[0], fb[0]);
-        interleave();
-        wait_vmcnt<AFTER>();
-        barrier_lds();
-#pragma unroll
-        for (int t = 0; t < IM + JN; ++t) read_frag(Jn{}, 0, t, fa[0], fb[0]);
-#pragma unroll
-        for (int t = NL0; t < NL; ++t) dma(Jl{}, kl, t);
-        mfmas(fa[1], fb[1]);
-        interleave();
-    };
-    int st = 0;
-    for (; st + NS <= KT; st += NS) {
-        stage(std::integral_constant<int, 0>{}, st);
-        stage(std::integral_constant<int, 1>{}, st + 1);
-        stage(std::integral_constant<int, 2>{}, st + 2);
-        stage(std::integral_constant<int, 3>{}, st + 3);
-        if constexpr (NS > 4) stage(std::integral_constant<int, 4 % NS>{}, st + 4);
-        if constexpr (NS > 5) stage(std::integral_constant<int, 5 % NS>{}, st + 5);
-    }
-    if (st < KT) stage(std::integral_constant<int, 0>{}, st);
-    if (st + 1 < KT) stage(std::integral_constant<int, 1 % NS>{}, st + 1);
-    if (st + 2 < KT) stage(std::integral_constant<int, 2 % NS>{}, st + 2);
-    if constexpr (NS > 4) if (st + 3 < KT) stage(std::integral_constant<int, 3 % NS>{}, st + 3);
-    if constexpr (NS > 5) if (st + 4 < KT) stage(std::integral_constant<int, 4 % NS>{}, st + 4);
-    wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
-
-    // ---- epilogue.  The MFMA computes the transposed block (weights are its A
-    // operand): lane l holds token row r32 of the 32-row block and output
-    // columns 8*(q/4) + 4*half + q%4, i.e. four consecutive columns per q/4,
-    // written as one 8-byte (bf16) or 16-byte (fp32) store. ----------------------
-    const long long sofs = (long long)e * g.s_stride;
+    const long long sofs = (long long)jb.e * g.s_stride;
     if constexpr (MODE == MODE_GATED_UP) {
         // h pad columns [N, Npad) come out as act(0) * 0 = 0 from the zero weight
         // pad rows, so the whole tile is stored (ldc = Npad).
 #pragma unroll
         for (int i = 0; i < IM; ++i) {
-            const int ml = wm * WM + i * 32 + r32;
-            if (ml >= rows) continue;
-            uint16_t *crow = (uint16_t *)g.C + (arow0 + ml) * g.ldc;
+            const int ml = row0 + i * 32 + r32;
+            if (ml >= jb.rows) continue;
+            uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
 #pragma unroll
             for (int m = 0; m < JN / 2; ++m)
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    const int n = n0 + wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
+                    const int n = jb.n0 + wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
@@ -359,23 +217,23 @@ grouped_gemm_bf16_kernel(GemmArgs g) {
         for (int j = 0; j < JN; ++j)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-                const int n = n0 + wn * WN + j * 32 + 8 * g4 + 4 * half;
+                const int n = jb.n0 + wn * WN + j * 32 + 8 * g4 + 4 * half;
                 float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g.bias && ks == 0) {  // split K: the bias belongs to one partial sum only
+                if (g.bias && jb.ks == 0) {  // split K: the bias belongs to one partial sum only
                     const float4 bv = *(const float4 *)(g.bias + sofs + n);
                     b4[0] = bv.x; b4[1] = bv.y; b4[2] = bv.z; b4[3] = bv.w;
                 }
 #pragma unroll
                 for (int i = 0; i < IM; ++i) {
-                    const int ml = wm * WM + i * 32 + r32;
-                    if (ml >= rows) continue;
+                    const int ml = row0 + i * 32 + r32;
+                    if (ml >= jb.rows) continue;
                     if constexpr (MODE == MODE_STD_UP) {
-                        uint16_t *crow = (uint16_t *)g.C + (arow0 + ml) * g.ldc;
+                        uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
                         *(uint2 *)(crow + n) = pack_bf16x4(
                             act_fast<ACT>(acc[i][j][4 * g4 + 0] + b4[0]), act_fast<ACT>(acc[i][j][4 * g4 + 1] + b4[1]),
                             act_fast<ACT>(acc[i][j][4 * g4 + 2] + b4[2]), act_fast<ACT>(acc[i][j][4 * g4 + 3] + b4[3]));
                     } else {
-                        float *crow = (float *)g.C + ks * g.c_split_stride + (arow0 + ml) * g.ldc;
+                        float *crow = (float *)g.C + jb.ks * g.c_split_stride + (jb.arow0 + ml) * g.ldc;
                         if (vec4 && n + 3 < g.N) {
                             *(float4 *)(crow + n) = make_float4(acc[i][j][4 * g4 + 0] + b4[0], acc[i][j][4 * g4 + 1] + b4[1],
                                                                 acc[i][j][4 * g4 + 2] + b4[2], acc[i][j][4 * g4 + 3] + b4[3]);
@@ -390,17 +248,218 @@ grouped_gemm_bf16_kernel(GemmArgs g) {
     }
 }
 
-#ifndef MOE_BF16_WAVES
-#define MOE_BF16_WAVES 4
-#endif
+// LDS ring: one array per slot (slot index known at compile time everywhere).
+#define MOE_LDS_RING(STAGE, NS)                                                            \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot0[STAGE];                        \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot1[STAGE];                        \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot2[NS > 2 ? STAGE : 16];          \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot3[NS > 3 ? STAGE : 16];          \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot4[NS > 4 ? STAGE : 16];          \
+    __shared__ __attribute__((aligned(1024))) uint8_t slot5[NS > 5 ? STAGE : 16];          \
+    auto slot = [&](auto J_) -> MOE_LDS_AS uint8_t * {                                     \
+        constexpr int J = decltype(J_)::value;                                             \
+        if constexpr (J == 0) return (MOE_LDS_AS uint8_t *)slot0;                          \
+        else if constexpr (J == 1) return (MOE_LDS_AS uint8_t *)slot1;                     \
+        else if constexpr (J == 2) return (MOE_LDS_AS uint8_t *)slot2;                     \
+        else if constexpr (J == 3) return (MOE_LDS_AS uint8_t *)slot3;                     \
+        else if constexpr (J == 4) return (MOE_LDS_AS uint8_t *)slot4;                     \
+        else return (MOE_LDS_AS uint8_t *)slot5;                                           \
+    }
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+// Prologue: this wave's NL loads of stages 0 .. NS-2 (clamped to the last
+// stage), stage s into slot s.
+#define MOE_PROLOGUE_LOADS(NS, NL, KT)                                       \
+    _Pragma("unroll") for (int s0 = 0; s0 < NS - 1; ++s0) {                  \
+        const int kt = min(s0, KT - 1);                                      \
+        _Pragma("unroll") for (int i = 0; i < NL; ++i) {                     \
+            switch (s0) {                                                    \
+            case 0: dma(ic<0>{}, kt, i); break;                              \
+            case 1: dma(ic<1>{}, kt, i); break;                              \
+            case 2: dma(ic<2>{}, kt, i); break;                              \
+            case 3: dma(ic<3>{}, kt, i); break;                              \
+            default: dma(ic<4>{}, kt, i); break;                             \
+            }                                                                \
+        }                                                                    \
+    }
+
+// Runs stage(ic<slot>, s) for s = 0 .. KT-1 with slot = s % NS known at
+// compile time (the body is unrolled NS times).
+#define MOE_STAGE_LOOP(NS, KT)                                                    \
+    {                                                                             \
+        int st = 0;                                                               \
+        for (; st + NS <= KT; st += NS) {                                         \
+            stage(ic<0>{}, st);                                                   \
+            stage(ic<1>{}, st + 1);                                               \
+            stage(ic<2 % NS>{}, st + 2);                                          \
+            if constexpr (NS > 3) stage(ic<3 % NS>{}, st + 3);                    \
+            if constexpr (NS > 4) stage(ic<4 % NS>{}, st + 4);                    \
+            if constexpr (NS > 5) stage(ic<5 % NS>{}, st + 5);                    \
+        }                                                                         \
+        if (st < KT) stage(ic<0>{}, st);                                          \
+        if (st + 1 < KT) stage(ic<1 % NS>{}, st + 1);                             \
+        if constexpr (NS > 3) if (st + 2 < KT) stage(ic<2 % NS>{}, st + 2);       \
+        if constexpr (NS > 4) if (st + 3 < KT) stage(ic<3 % NS>{}, st + 3);       \
+        if constexpr (NS > 5) if (st + 4 < KT) stage(ic<4 % NS>{}, st + 4);       \
+    }
+
+// ============================================================================
+// 4-wave interleaved kernel, BM = 128 or 256.
+// ============================================================================
+template <int MODE, int BM, int ACT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
+    GemmArgs g) {
+    constexpr int NWAVE = 4;
+    constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
+    constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
+    constexpr int A_BYTES = BM * ROWB;
+    constexpr int STAGE = A_BYTES + 256 * ROWB;
+    constexpr int NS = (BM == 256) ? 4 : 6;  // LDS ring slots: 128 KB / 144 KB
+    constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
+    constexpr int WN = 128;              // wave tile columns (2 waves along N)
+    constexpr int IM = WM / 32;          // 32-row blocks per wave
+    constexpr int JN = WN / 32;          // 32-column blocks per wave
+    constexpr int LA = BM / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
+    constexpr int LB = 256 / (16 * NWAVE);  // B loads per wave per stage
+    constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
+    constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
+    static_assert(NS * STAGE <= 160 * 1024, "LDS");
+    MOE_LDS_RING(STAGE, NS);
+
+    TileJob jb;
+    if (!decode_job<BM, NB>(g, jb)) return;
+    const int KT = jb.KT;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w & 1, wn = w >> 1;
+
+    const uint8_t *gsrc[NL];
+    uint32_t ldst[NL];
+    load_plan<BM, NB, NWAVE, LA, LB>(g, jb, w, lane, gsrc, ldst);
+    // load i of stage kt into ring slot J
+    auto dma = [&](auto J_, int kt, int i) {
+        const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
+        lds_dma16(gsrc[i] + (long long)kt * ROWB, __builtin_amdgcn_readfirstlane(l));
+    };
+
+    // ---- fragment addressing (fragment row bases are multiples of 32, so
+    // swz(row) = (r32 >> 2) & 3) ------------------------------------------------
+    const int half = lane >> 5;
+    const int r32 = lane & 31;
+    const int a_frag = (wm * WM + r32) * ROWB;
+    int b_frag[JN];
+#pragma unroll
+    for (int j = 0; j < JN; ++j) b_frag[j] = A_BYTES + (b_frag_row<NB, WN>(j, wn) + r32) * ROWB;
+    int choff[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) choff[kk] = ((kk * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
+
+    f32x16_t acc[IM][JN];
+#pragma unroll
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int j = 0; j < JN; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+    bf16x8_t fa[2][IM], fb[2][JN];
+
+    // ---- main loop --------------------------------------------------------------
+    // Stage s (32 K columns, two k16 sub-steps) lives in ring slot s % NS and is
+    // loaded NS - 1 stages ahead.  Per stage:
+    //   sub-step 0: MFMAs of (s, 0) | LDS reads of (s, 1)   | loads of stage s+NS-1, first half
+    //   wait until this wave's loads of stage s+1 landed; barrier (every wave's have)
+    //   sub-step 1: MFMAs of (s, 1) | LDS reads of (s+1, 0) | loads of stage s+NS-1, second half
+    // Stage s+NS-1 goes to the slot of stage s-1, whose last reads (its sub-step
+    // 1 fragments) ended before the barrier of stage s-1.  Past the last stage
+    // the loads repeat stage KT-1 (in bounds, into a slot nothing reads again),
+    // which keeps the vmcnt arithmetic exact: when the barrier of stage s is
+    // reached, the loads issued after those of stage s+1 are NS-3 whole stages
+    // and the first NL0 loads of stage s+NS-1.
+    constexpr int AFTER = (NS - 3) * NL + NL0;
+    MOE_PROLOGUE_LOADS(NS, NL, KT)
+    wait_vmcnt<(NS - 2) * NL>();  // stage 0 landed
+    barrier_lds();
+
+    // The loop of a wave whose first NV 32-row blocks hold rows of the tile:
+    // MFMAs and A-fragment reads only for those (NV = 0: the wave only loads
+    // and takes part in the barriers).  Accumulators of the other blocks stay
+    // 0 and their rows are not stored.
+    auto run = [&](auto NV_) {
+        constexpr int NV = decltype(NV_)::value;
+        constexpr int NMF = NV * JN, NRD = NV > 0 ? NV + JN : 0;
+        constexpr int NPAIR = NMF < NRD ? NMF : NRD;
+        auto read_frags = [&](auto J_, int kk, bf16x8_t *af, bf16x8_t *bfr) {
+            if constexpr (NV > 0) {
+                const MOE_LDS_AS uint8_t *sb = slot(J_);
+#pragma unroll
+                for (int r = 0; r < NV; ++r)
+                    af[r] = *(const MOE_LDS_AS bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[kk]);
+#pragma unroll
+                for (int j = 0; j < JN; ++j) bfr[j] = *(const MOE_LDS_AS bf16x8_t *)(sb + b_frag[j] + choff[kk]);
+            }
+        };
+        auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+#pragma unroll
+                for (int j = 0; j < JN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+        };
+        // One MFMA, then one fragment read of the next sub-step, while both
+        // last; then the remaining MFMAs (or reads).
+        auto interleave = [&]() {
+            if constexpr (NMF > 0) {
+#pragma unroll
+                for (int t = 0; t < NPAIR; ++t) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+                }
+                if constexpr (NMF > NPAIR) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NPAIR, 0);
+                if constexpr (NRD > NPAIR) __builtin_amdgcn_sched_group_barrier(0x100, NRD - NPAIR, 0);
+            }
+        };
+        read_frags(ic<0>{}, 0, fa[0], fb[0]);
+        auto stage = [&](auto J_, int st) {
+            constexpr int J = decltype(J_)::value;
+            using Jn = ic<(J + 1) % NS>;       // slot of stage s+1
+            using Jl = ic<(J + NS - 1) % NS>;  // slot of stage s-1 = s+NS-1
+            const int kl = min(st + NS - 1, KT - 1);
+            read_frags(J_, 1, fa[1], fb[1]);
+#pragma unroll
+            for (int t = 0; t < NL0; ++t) dma(Jl{}, kl, t);
+            mfmas(fa[0], fb[0]);
+            interleave();
+            wait_vmcnt<AFTER>();
+            barrier_lds();
+            read_frags(Jn{}, 0, fa[0], fb[0]);
+#pragma unroll
+            for (int t = NL0; t < NL; ++t) dma(Jl{}, kl, t);
+            mfmas(fa[1], fb[1]);
+            interleave();
+        };
+        MOE_STAGE_LOOP(NS, KT)
+    };
+    const int nv = min(IM, (max(0, jb.rows - wm * WM) + 31) >> 5);  // wave-uniform
+    if (nv == IM) run(ic<IM>{});
+    else if (nv == 0) run(ic<0>{});
+    else if (nv == 1) run(ic<1>{});
+    else if constexpr (IM > 2) {
+        if (nv == 2) run(ic<2>{});
+        else run(ic<3>{});
+    }
+    wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
+
+    store_tile<MODE, ACT, IM, JN, WN>(g, jb, acc, wm * WM, wn, lane);
+}
 
 template <int MODE, int BM, int ACT>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
-    constexpr int NWAVE = MOE_BF16_WAVES;
     long long total = (long long)g.m_tiles_grid * g.n_tiles * g.ksplit;
     total = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, NWAVE>), dim3((unsigned)total), dim3(NWAVE * 64), 0, s,
-                       g);
+    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
