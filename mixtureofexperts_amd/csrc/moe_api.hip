@@ -427,12 +427,12 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit) {
 // register-staged kernel for fp32 and fp8 weights.
 static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
     const int mode = h->gated ? MODE_GATED_UP : MODE_STD_UP;
-    if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, up_args(h, mt_grid), s);
+    if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, h->wt == WT_FP8, up_args(h, mt_grid), s);
     return launch_grouped_gemm(mode, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0, up_args(h, mt_grid), s);
 }
 
 static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksplit) {
-    if (h->bf16_gemm) return launch_grouped_gemm_bf16(MODE_DOWN, h->bm, down_args(h, mt_grid, ksplit), s);
+    if (h->bf16_gemm) return launch_grouped_gemm_bf16(MODE_DOWN, h->bm, h->wt == WT_FP8, down_args(h, mt_grid, ksplit), s);
     return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid, 1), s);
 }
 
@@ -562,7 +562,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->T_max = cfg->max_tokens;
     h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
     h->rows_max = h->T_max * h->kt;
-    h->bf16_gemm = h->ct == CT_BF16 && h->wt == WT_BF16;
+    h->bf16_gemm = h->ct == CT_BF16 && (h->wt == WT_BF16 || h->wt == WT_FP8);
     // 256-row tiles when experts average at least 384 rows at max_tokens, else 128
     h->bm = (h->bf16_gemm && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
     h->max_tiles = h->rows_max / h->bm + h->E + 1;

@@ -8,7 +8,11 @@
 //   MODE_DOWN     : y = h W2^T (+ b2)                 both
 //
 // A is one expert's contiguous segment of rows (the permuted tokens, or h);
-// weights are packed [E][Npad][Kpad] bf16, K contiguous.
+// weights are packed [E][Npad][Kpad], K contiguous, bf16 or fp8 e4m3 (WF8).
+// fp8 weights stay fp8 in HBM and LDS (half the load bytes); each lane widens
+// its fragments to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact for e4m3, scale
+// 1) and the per-output-channel scale s multiplies the fp32 accumulator in
+// the epilogue: s[n] * sum_k a[k] q[n][k] = sum_k a[k] (s[n] q[n][k]).
 //
 // Work list.  The device-side scan writes tile_start[e] = sum over e' < e of
 // ceil(count_e' / BM).  Work item id is ordered expert-major, then n-tile (and
@@ -69,6 +73,17 @@ __device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d)
     __builtin_memcpy(&r.x, &lo, 4);
     __builtin_memcpy(&r.y, &hi, 4);
     return r;
+}
+
+// Eight fp8 e4m3 bytes (lo: bytes 0-3, hi: bytes 4-7) -> eight bf16 (exact).
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 // Wait until at most N vector-memory operations of this wave are outstanding.
@@ -143,13 +158,18 @@ __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
 // wave's LA loads cover A rows w * BM / NWAVE ..; its LB loads cover B-tile rows
 // w * 256 / NWAVE .. (gated: tile rows [0, 128) are W1 rows n0.., [128, 256) the
 // same W3 rows).  A rows past the tile's valid rows repeat its last row.
-template <int BM, int NB, int NWAVE, int LA, int LB>
+//
+// fp8 weights (WF8): a B-tile row is 32 B (two chunks) per stage and a load
+// covers 32 rows: lane l writes physical chunk l & 1 of row l >> 1, chunk c of
+// row r being stored at c ^ ((r >> 3) & 1).
+template <int BM, int NB, int NWAVE, int LA, int LB, int WF8>
 __device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, int w, int lane,
                                           const uint8_t *(&gsrc)[LA + LB], uint32_t (&ldst)[LA + LB]) {
     constexpr int ROWB = 64;
+    constexpr int BROWB = WF8 ? 32 : 64;  // B bytes per row per stage
     constexpr int A_BYTES = BM * ROWB;
-    const long long lda_b = g.lda * 2, ldb_b = g.ldb * 2;
-    const long long k0b = (long long)jb.ks * jb.KT * ROWB;  // first K byte of the range in a row
+    const long long lda_b = g.lda * 2, ldb_b = g.ldb * (WF8 ? 1 : 2);
+    const long long k0b = (long long)jb.ks * jb.KT * ROWB;  // first K byte of the range in an A row
     const int lr = lane >> 2;
     const int lch = (lane & 3) ^ ((lane >> 4) & 3);
     const uint8_t *Ab = (const uint8_t *)g.A + jb.arow0 * lda_b + k0b;
@@ -160,13 +180,17 @@ __device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, 
         ldst[i] = r * ROWB;
     }
     const uint8_t *Bsrc = (NB == 2 && w >= NWAVE / 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
-    const uint8_t *Bb = Bsrc + ((long long)jb.e * g.b_stride + (long long)jb.n0 * g.ldb) * 2;  // row n0 of expert e
+    const uint8_t *Bb = Bsrc + ((long long)jb.e * g.b_stride + (long long)jb.n0 * g.ldb) * (WF8 ? 1 : 2);
+    const long long k0bb = (long long)jb.ks * jb.KT * BROWB;  // first K byte of the range in a B row
+    constexpr int BR = WF8 ? 32 : 16;                         // B-tile rows per load
+    const int blr = WF8 ? (lane >> 1) : lr;
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
-        const int t = w * (256 / NWAVE) + 16 * i;  // tile row
+        const int t = w * (256 / NWAVE) + BR * i;  // first tile row of the load
         const int r = (NB == 2) ? (t & 127) : t;   // row within the weight matrix, from n0
-        gsrc[LA + i] = Bb + (long long)(r + lr) * ldb_b + k0b + lch * 16;
-        ldst[LA + i] = A_BYTES + t * ROWB;
+        const int bch = WF8 ? ((lane & 1) ^ (((t + blr) >> 3) & 1)) : lch;
+        gsrc[LA + i] = Bb + (long long)(r + blr) * ldb_b + k0bb + bch * 16;
+        ldst[LA + i] = A_BYTES + t * BROWB;
     }
 }
 
@@ -183,12 +207,22 @@ __device__ __forceinline__ int b_frag_row(int j, int wn) {
 // holds token row l % 32 of the 32-row block and output columns 8 (q / 4) +
 // 4 (l / 32) + q % 4, i.e. four consecutive columns per q / 4, written as one
 // 8-byte (bf16) or 16-byte (fp32) store.  row0: the wave's first tile row.
-template <int MODE, int ACT, int IM, int JN, int WN>
+// WF8: the accumulators are scaled by the weight rows' scales (s0: W1 or W2,
+// s1: W3) before bias and activation.
+template <int MODE, int ACT, int IM, int JN, int WN, int WF8>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
                                            int row0, int wn, int lane) {
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const long long sofs = (long long)jb.e * g.s_stride;
+    auto scale4 = [&](const float *sp, int n, float *sc) {
+        if constexpr (WF8) {
+            const float4 v = *(const float4 *)(sp + sofs + n);
+            sc[0] = v.x; sc[1] = v.y; sc[2] = v.z; sc[3] = v.w;
+        } else {
+            sc[0] = sc[1] = sc[2] = sc[3] = 1.0f;
+        }
+    };
     if constexpr (MODE == MODE_GATED_UP) {
         // h pad columns [N, Npad) come out as act(0) * 0 = 0 from the zero weight
         // pad rows, so the whole tile is stored (ldc = Npad).
@@ -202,10 +236,15 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
                     const int n = jb.n0 + wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
-                    float v[4];
+                    float v[4], sg[4], su[4];
+                    scale4(g.s0, n, sg);
+                    scale4(g.s1, n, su);
 #pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        v[c] = act_fast<ACT>(acc[i][2 * m][4 * g4 + c]) * acc[i][2 * m + 1][4 * g4 + c];
+                    for (int c = 0; c < 4; ++c) {
+                        const float gt = WF8 ? acc[i][2 * m][4 * g4 + c] * sg[c] : acc[i][2 * m][4 * g4 + c];
+                        const float up = WF8 ? acc[i][2 * m + 1][4 * g4 + c] * su[c] : acc[i][2 * m + 1][4 * g4 + c];
+                        v[c] = act_fast<ACT>(gt) * up;
+                    }
                     *(uint2 *)(crow + n) = pack_bf16x4(v[0], v[1], v[2], v[3]);
                 }
         }
@@ -223,24 +262,31 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
                     const float4 bv = *(const float4 *)(g.bias + sofs + n);
                     b4[0] = bv.x; b4[1] = bv.y; b4[2] = bv.z; b4[3] = bv.w;
                 }
+                float sc[4];
+                scale4(g.s0, n, sc);
 #pragma unroll
                 for (int i = 0; i < IM; ++i) {
                     const int ml = row0 + i * 32 + r32;
                     if (ml >= jb.rows) continue;
+                    f32x16_t a = acc[i][j];
+                    if constexpr (WF8) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) a[4 * g4 + c] = a[4 * g4 + c] * sc[c];
+                    }
                     if constexpr (MODE == MODE_STD_UP) {
                         uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
                         *(uint2 *)(crow + n) = pack_bf16x4(
-                            act_fast<ACT>(acc[i][j][4 * g4 + 0] + b4[0]), act_fast<ACT>(acc[i][j][4 * g4 + 1] + b4[1]),
-                            act_fast<ACT>(acc[i][j][4 * g4 + 2] + b4[2]), act_fast<ACT>(acc[i][j][4 * g4 + 3] + b4[3]));
+                            act_fast<ACT>(a[4 * g4 + 0] + b4[0]), act_fast<ACT>(a[4 * g4 + 1] + b4[1]),
+                            act_fast<ACT>(a[4 * g4 + 2] + b4[2]), act_fast<ACT>(a[4 * g4 + 3] + b4[3]));
                     } else {
                         float *crow = (float *)g.C + jb.ks * g.c_split_stride + (jb.arow0 + ml) * g.ldc;
                         if (vec4 && n + 3 < g.N) {
-                            *(float4 *)(crow + n) = make_float4(acc[i][j][4 * g4 + 0] + b4[0], acc[i][j][4 * g4 + 1] + b4[1],
-                                                                acc[i][j][4 * g4 + 2] + b4[2], acc[i][j][4 * g4 + 3] + b4[3]);
+                            *(float4 *)(crow + n) = make_float4(a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1],
+                                                                a[4 * g4 + 2] + b4[2], a[4 * g4 + 3] + b4[3]);
                         } else {
 #pragma unroll
                             for (int c = 0; c < 4; ++c)
-                                if (n + c < g.N) crow[n + c] = acc[i][j][4 * g4 + c] + b4[c];
+                                if (n + c < g.N) crow[n + c] = a[4 * g4 + c] + b4[c];
                         }
                     }
                 }
@@ -308,21 +354,22 @@ using ic = std::integral_constant<int, N>;
 // ============================================================================
 // 4-wave interleaved kernel, BM = 128 or 256.
 // ============================================================================
-template <int MODE, int BM, int ACT>
+template <int MODE, int BM, int ACT, int WF8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
     constexpr int NWAVE = 4;
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
-    constexpr int ROWB = 64;             // bytes per LDS row = 32 bf16 of K (one stage)
+    constexpr int ROWB = 64;             // bytes per LDS A row = 32 bf16 of K (one stage)
+    constexpr int BROWB = WF8 ? 32 : 64; // bytes per LDS B row
     constexpr int A_BYTES = BM * ROWB;
-    constexpr int STAGE = A_BYTES + 256 * ROWB;
-    constexpr int NS = (BM == 256) ? 4 : 6;  // LDS ring slots: 128 KB / 144 KB
+    constexpr int STAGE = A_BYTES + 256 * BROWB;
+    constexpr int NS = (BM == 256 && !WF8) ? 4 : 6;  // LDS ring slots (<= 144 KB)
     constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
     constexpr int WN = 128;              // wave tile columns (2 waves along N)
     constexpr int IM = WM / 32;          // 32-row blocks per wave
     constexpr int JN = WN / 32;          // 32-column blocks per wave
     constexpr int LA = BM / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
-    constexpr int LB = 256 / (16 * NWAVE);  // B loads per wave per stage
+    constexpr int LB = 256 / ((WF8 ? 32 : 16) * NWAVE);  // B loads per wave per stage
     constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
     constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
     static_assert(NS * STAGE <= 160 * 1024, "LDS");
@@ -337,24 +384,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const uint8_t *gsrc[NL];
     uint32_t ldst[NL];
-    load_plan<BM, NB, NWAVE, LA, LB>(g, jb, w, lane, gsrc, ldst);
+    load_plan<BM, NB, NWAVE, LA, LB, WF8>(g, jb, w, lane, gsrc, ldst);
     // load i of stage kt into ring slot J
     auto dma = [&](auto J_, int kt, int i) {
         const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
-        lds_dma16(gsrc[i] + (long long)kt * ROWB, __builtin_amdgcn_readfirstlane(l));
+        lds_dma16(gsrc[i] + (long long)kt * (i < LA ? ROWB : BROWB), __builtin_amdgcn_readfirstlane(l));
     };
 
     // ---- fragment addressing (fragment row bases are multiples of 32, so
     // swz(row) = (r32 >> 2) & 3) ------------------------------------------------
+    // Lane (r32, half) supplies 8 K values per k16 sub-step kk: K 16 kk + 8 half
+    // (bf16 weights, A chunk 2 kk + half) or K 16 half + 8 kk (fp8 weights: A
+    // chunk 2 half + kk, and the lane's 16 weight bytes of the stage, K 16 half
+    // .. +16, are one B chunk read once per stage).  The MFMA sums over K, so any
+    // assignment of K values to (sub-step, lane half) shared by A and B works.
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const int a_frag = (wm * WM + r32) * ROWB;
     int b_frag[JN];
 #pragma unroll
-    for (int j = 0; j < JN; ++j) b_frag[j] = A_BYTES + (b_frag_row<NB, WN>(j, wn) + r32) * ROWB;
+    for (int j = 0; j < JN; ++j)
+        b_frag[j] = A_BYTES + (b_frag_row<NB, WN>(j, wn) + r32) * BROWB + (WF8 ? ((half ^ ((r32 >> 3) & 1)) << 4) : 0);
     int choff[2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) choff[kk] = ((kk * 2 + half) ^ ((r32 >> 2) & 3)) << 4;
+    for (int kk = 0; kk < 2; ++kk)
+        choff[kk] = ((WF8 ? (half * 2 + kk) : (kk * 2 + half)) ^ ((r32 >> 2) & 3)) << 4;
 
     f32x16_t acc[IM][JN];
 #pragma unroll
@@ -365,6 +419,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
     bf16x8_t fa[2][IM], fb[2][JN];
+    u32x4_t braw[JN];  // WF8: this stage's weight bytes (K 16 half .. +16) per column block
 
     // ---- main loop --------------------------------------------------------------
     // Stage s (32 K columns, two k16 sub-steps) lives in ring slot s % NS and is
@@ -389,8 +444,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // 0 and their rows are not stored.
     auto run = [&](auto NV_) {
         constexpr int NV = decltype(NV_)::value;
-        constexpr int NMF = NV * JN, NRD = NV > 0 ? NV + JN : 0;
-        constexpr int NPAIR = NMF < NRD ? NMF : NRD;
+        constexpr int NMF = NV * JN;
+        // WF8: sub-step 0 reads the stage's weight bytes; each sub-step widens
+        // its 8 bytes (words 2 kk, 2 kk + 1 of braw) to bf16.
         auto read_frags = [&](auto J_, int kk, bf16x8_t *af, bf16x8_t *bfr) {
             if constexpr (NV > 0) {
                 const MOE_LDS_AS uint8_t *sb = slot(J_);
@@ -398,7 +454,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 for (int r = 0; r < NV; ++r)
                     af[r] = *(const MOE_LDS_AS bf16x8_t *)(sb + a_frag + r * 32 * ROWB + choff[kk]);
 #pragma unroll
-                for (int j = 0; j < JN; ++j) bfr[j] = *(const MOE_LDS_AS bf16x8_t *)(sb + b_frag[j] + choff[kk]);
+                for (int j = 0; j < JN; ++j) {
+                    if constexpr (WF8) {
+                        if (kk == 0) braw[j] = *(const MOE_LDS_AS u32x4_t *)(sb + b_frag[j]);
+                        bfr[j] = widen_fp8x8(braw[j][2 * kk], braw[j][2 * kk + 1]);
+                    } else {
+                        bfr[j] = *(const MOE_LDS_AS bf16x8_t *)(sb + b_frag[j] + choff[kk]);
+                    }
+                }
             }
         };
         auto mfmas = [&](const bf16x8_t *af, const bf16x8_t *bfr) {
@@ -408,9 +471,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 for (int j = 0; j < JN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
         };
-        // One MFMA, then one fragment read of the next sub-step, while both
-        // last; then the remaining MFMAs (or reads).
-        auto interleave = [&]() {
+        // One MFMA, then one fragment read of the next sub-step (NRD of them),
+        // while both last; then the remaining MFMAs (or reads).
+        auto interleave = [&](auto NRD_) {
+            constexpr int NRD = decltype(NRD_)::value;
+            constexpr int NPAIR = NMF < NRD ? NMF : NRD;
             if constexpr (NMF > 0) {
 #pragma unroll
                 for (int t = 0; t < NPAIR; ++t) {
@@ -431,14 +496,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int t = 0; t < NL0; ++t) dma(Jl{}, kl, t);
             mfmas(fa[0], fb[0]);
-            interleave();
+            interleave(ic<(NV > 0) ? (WF8 ? NV : NV + JN) : 0>{});
             wait_vmcnt<AFTER>();
             barrier_lds();
             read_frags(Jn{}, 0, fa[0], fb[0]);
 #pragma unroll
             for (int t = NL0; t < NL; ++t) dma(Jl{}, kl, t);
             mfmas(fa[1], fb[1]);
-            interleave();
+            interleave(ic<(NV > 0) ? NV + JN : 0>{});
         };
         MOE_STAGE_LOOP(NS, KT)
     };
@@ -452,43 +517,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
-    store_tile<MODE, ACT, IM, JN, WN>(g, jb, acc, wm * WM, wn, lane);
+    store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane);
 }
 
-template <int MODE, int BM, int ACT>
+template <int MODE, int BM, int ACT, int WF8>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
     long long total = (long long)g.m_tiles_grid * g.n_tiles * g.ksplit;
     total = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT>), dim3((unsigned)total), dim3(256), 0, s, g);
+    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
-template <int MODE, int BM>
+template <int MODE, int BM, int WF8>
 static hipError_t launch_bf16_act(const GemmArgs &g, hipStream_t s) {
     if constexpr (MODE == MODE_DOWN) {
-        return launch_bf16<MODE, BM, MOE_ACT_IDENTITY>(g, s);
+        return launch_bf16<MODE, BM, MOE_ACT_IDENTITY, WF8>(g, s);
     } else {
         switch (g.act) {
-        case MOE_ACT_SILU: return launch_bf16<MODE, BM, MOE_ACT_SILU>(g, s);
-        case MOE_ACT_GELU: return launch_bf16<MODE, BM, MOE_ACT_GELU>(g, s);
-        case MOE_ACT_RELU: return launch_bf16<MODE, BM, MOE_ACT_RELU>(g, s);
-        default: return launch_bf16<MODE, BM, MOE_ACT_IDENTITY>(g, s);
+        case MOE_ACT_SILU: return launch_bf16<MODE, BM, MOE_ACT_SILU, WF8>(g, s);
+        case MOE_ACT_GELU: return launch_bf16<MODE, BM, MOE_ACT_GELU, WF8>(g, s);
+        case MOE_ACT_RELU: return launch_bf16<MODE, BM, MOE_ACT_RELU, WF8>(g, s);
+        default: return launch_bf16<MODE, BM, MOE_ACT_IDENTITY, WF8>(g, s);
         }
     }
 }
 
-hipError_t launch_grouped_gemm_bf16(int mode, int bm, const GemmArgs &g, hipStream_t s) {
+hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s) {
     if (g.m_tiles_grid <= 0 || g.n_tiles <= 0) return hipSuccess;
     // a split K range must be whole stages, and only the fp32 down GEMM writes partial sums
     if (g.ksplit < 1 || (g.K / 32) % g.ksplit != 0 || (g.ksplit > 1 && mode != MODE_DOWN)) return hipErrorInvalidValue;
-#define MOE_BF16_CASE(M, B) \
-    if (mode == M && bm == B) return launch_bf16_act<M, B>(g, s);
-    MOE_BF16_CASE(MODE_GATED_UP, 256)
-    MOE_BF16_CASE(MODE_STD_UP, 256)
-    MOE_BF16_CASE(MODE_DOWN, 256)
-    MOE_BF16_CASE(MODE_GATED_UP, 128)
-    MOE_BF16_CASE(MODE_STD_UP, 128)
-    MOE_BF16_CASE(MODE_DOWN, 128)
+    if (wfp8 && (!g.s0 || (mode == MODE_GATED_UP && !g.s1))) return hipErrorInvalidValue;
+#define MOE_BF16_CASE(M, B, F) \
+    if (mode == M && bm == B && (wfp8 != 0) == (F != 0)) return launch_bf16_act<M, B, F>(g, s);
+    MOE_BF16_CASE(MODE_GATED_UP, 256, 0)
+    MOE_BF16_CASE(MODE_STD_UP, 256, 0)
+    MOE_BF16_CASE(MODE_DOWN, 256, 0)
+    MOE_BF16_CASE(MODE_GATED_UP, 128, 0)
+    MOE_BF16_CASE(MODE_STD_UP, 128, 0)
+    MOE_BF16_CASE(MODE_DOWN, 128, 0)
+    MOE_BF16_CASE(MODE_GATED_UP, 256, 1)
+    MOE_BF16_CASE(MODE_STD_UP, 256, 1)
+    MOE_BF16_CASE(MODE_DOWN, 256, 1)
+    MOE_BF16_CASE(MODE_GATED_UP, 128, 1)
+    MOE_BF16_CASE(MODE_STD_UP, 128, 1)
+    MOE_BF16_CASE(MODE_DOWN, 128, 1)
 #undef MOE_BF16_CASE
     return hipErrorInvalidValue;
 }

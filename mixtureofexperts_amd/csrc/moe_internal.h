@@ -168,6 +168,6 @@ hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *o
 hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const GemmArgs &g,
                                hipStream_t s);
 // bf16 activations x bf16 weights; bm = 128 or 256 rows per tile (the scan's bm)
-hipError_t launch_grouped_gemm_bf16(int mode, int bm, const GemmArgs &g, hipStream_t s);
+hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
 
 }  // namespace moe
