@@ -237,43 +237,94 @@ hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s) {
 
 // Top-k by the isless key, descending, lower index first on ties; then the
 // gates p_sel ./ sum(p_sel) with the sum in slot order.
-__device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *sel, float *g) {
+// Top-k of a row p[0..n) by the isless key, descending, lower index first
+// among equal keys (partialsortperm(p, 1:k, rev=true)), in one pass: the k
+// best so far sit in slots 0..k-1 in order; an entry enters only with a key
+// strictly above the k-th, is inserted after the equal keys already there,
+// and the slots after it move down by one.  Gates: p of the slots over their
+// sum in slot order.  p is an LDS row, 16-byte aligned, readable up to n
+// rounded up to 4.
+template <int K>
+__device__ inline void topk_row_k(const float *__restrict__ p, int n, int *sel, float *g) {
 #pragma clang fp contract(off)
-    uint64_t taken0 = 0, taken1 = 0;
-    for (int j = 0; j < k; ++j) {
-        int best = -1;
-        uint32_t bk = 0;
-        for (int i = 0; i < n; ++i) {
-            const bool taken = (i < 64) ? ((taken0 >> i) & 1ull) : ((taken1 >> (i - 64)) & 1ull);
-            if (taken) continue;
-            const uint32_t key = isless_key(p[i]);
-            if (best < 0 || key > bk) { best = i; bk = key; }
+    uint32_t kb[K];
+    int ib[K];
+    float vb[K];
+#pragma unroll
+    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0; vb[q] = 0.0f; }  // key 0: empty (below every float)
+    for (int i0 = 0; i0 < n; i0 += 4) {
+        const float4 v4 = *(const float4 *)(p + i0);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t ck = isless_key(vv[c]);
+            if (i0 + c < n && ck > kb[K - 1]) {
+                int ci = i0 + c;
+                float cv = vv[c];
+                bool shift = false;  // once inserted, every later slot moves down by one
+#pragma unroll
+                for (int q = 0; q < K; ++q) {
+                    const bool ins = shift || ck > kb[q];
+                    const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
+                    kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
+                    ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
+                    shift = ins;
+                }
+            }
         }
-        if (best < 64) taken0 |= 1ull << best; else taken1 |= 1ull << (best - 64);
-        sel[j] = best;
     }
-    float s = p[sel[0]];
-    for (int j = 1; j < k; ++j) s = s + p[sel[j]];
-    for (int j = 0; j < k; ++j) g[j] = p[sel[j]] / s;
+    float s = vb[0];
+#pragma unroll
+    for (int q = 1; q < K; ++q) s = s + vb[q];
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+        sel[q] = ib[q];
+        g[q] = vb[q] / s;
+    }
 }
+
+__device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *sel, float *g) {
+    switch (k) {
+    case 1: topk_row_k<1>(p, n, sel, g); break;
+    case 2: topk_row_k<2>(p, n, sel, g); break;
+    case 3: topk_row_k<3>(p, n, sel, g); break;
+    case 4: topk_row_k<4>(p, n, sel, g); break;
+    case 5: topk_row_k<5>(p, n, sel, g); break;
+    case 6: topk_row_k<6>(p, n, sel, g); break;
+    case 7: topk_row_k<7>(p, n, sel, g); break;
+    default: topk_row_k<8>(p, n, sel, g); break;
+    }
+}
+
+// LDS row strides of the routing kernel for E rows: floats (lrow, prow, zrow)
+// and doubles (hrow).  A multiple of 4 floats (16 B) whose count of 16-byte
+// units is odd, so that 16 token threads reading 16 B at one column hit 16
+// distinct bank quads.
+__host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) | 1)); }
+__host__ __device__ inline int route_rwd(int E) { return 2 * ((((E + 1) / 2 + 1) | 1)); }
 
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma clang fp contract(off)
     // Block: kRouteBlock tokens, kRouteThreads threads.  Work that the recipe
     // makes sequential per token (max, the fp32 sum in expert order, top-k,
     // the fp64 entropy sum) runs one thread per token (threads < kRouteBlock,
-    // all in wave 0); the per-element work (logits, fp64 exp and log terms) is
-    // spread over every thread.  Rows live in LDS (stride E + 1 words).
+    // all in wave 0), reading its LDS row 16 B at a time; the per-element work
+    // (logits, fp64 exp and log terms) is spread over every thread.  Rows are
+    // sized for this layer's E (dynamic LDS): lrow holds the logits and, once
+    // the exp terms are formed, the output probabilities.
     constexpr int NWV = 1;  // the token threads form one wave
-    constexpr int RW = MOE_MAX_EXPERTS + 1;
+    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
     __shared__ int wcnt[NWV][MOE_MAX_EXPERTS];
     __shared__ double red[2][kRouteBlock];
-    __shared__ float lrow[kRouteBlock][RW];    // logits
-    __shared__ float prow[kRouteBlock][RW];    // exp terms, then probabilities (before the shared-gating scale)
-    __shared__ float srow[kRouteBlock][RW];    // output probabilities (after it)
-    __shared__ float zrow[kRouteBlock][RW];    // shared gating: exp terms of all rows for the z-loss
-    __shared__ double hrow[kRouteBlock][RW];   // entropy terms p log(p + 1e-8)
     __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock];
+    const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
+    const int EM = max(a.Er, a.E);
+    const int RW = route_rw(EM), RWD = route_rwd(a.E);
+    float *lrow = (float *)rdyn;                         // [kRouteBlock][RW] logits, then output probabilities
+    float *prow = lrow + kRouteBlock * RW;               // exp terms, then probabilities (before the shared-gating scale)
+    double *hrow = (double *)(prow + kRouteBlock * RW);  // [kRouteBlock][RWD] entropy terms p log(p + 1e-8)
+    float *zrow = (float *)(hrow + kRouteBlock * RWD);   // shared gating: exp terms of all rows for the z-loss
+    float *srow = lrow;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -283,64 +334,87 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     const int ntok = min(kRouteBlock, a.T - t0);
     const bool tok = tid < kRouteBlock;         // a token thread
     const bool valid = tok && t < a.T;
-    const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
     const int ns = shared_gate ? a.ns : 0;      // rows before the routed ones
     const int Ero = a.E - ns;                   // routed rows (softmax width)
 
     for (int i = tid; i < NWV * MOE_MAX_EXPERTS; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
 
-    // (1) router logits: the K-slice partial sums in slice order, then the bias
-    for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
-        const int tt = q / a.Er, i = q - tt * a.Er;
-        const long long o = (long long)(t0 + tt) * a.Er + i;
-        float pv[kRouterMaxSlices];  // all slices loaded before the ordered sum
+    // (1) router logits: the K-slice partial sums in slice order, then the
+    // bias.  Elements q = tid + 256 u; the slices of 4 elements are loaded
+    // (from clamped addresses) before any is summed.
+    const int nq = ntok * a.Er;
+    const long long sstride = (long long)a.T * a.Er;
+    for (int q0 = 0; q0 < nq; q0 += 4 * kRouteThreads) {
+        float pv[4][kRouterMaxSlices];
 #pragma unroll
-        for (int sl = 0; sl < kRouterMaxSlices; ++sl)
-            pv[sl] = (sl < a.nks) ? a.part[(long long)sl * a.T * a.Er + o] : 0.0f;
-        float v = pv[0];
+        for (int u = 0; u < 4; ++u) {
+            const int q = min(q0 + u * kRouteThreads + tid, nq - 1);
+            const int tt = q / a.Er, i = q - tt * a.Er;
+            const long long o = (long long)(t0 + tt) * a.Er + i;
 #pragma unroll
-        for (int sl = 1; sl < kRouterMaxSlices; ++sl)
-            if (sl < a.nks) v = v + pv[sl];
-        if (a.bias) v = v + a.bias[i];
-        a.logits[o] = v;
-        lrow[tt][i] = v;
+            for (int sl = 0; sl < kRouterMaxSlices; ++sl)
+                pv[u][sl] = a.part[min(sl, a.nks - 1) * sstride + o];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * kRouteThreads + tid;
+            if (q < nq) {
+                const int tt = q / a.Er, i = q - tt * a.Er;
+                float v = pv[u][0];
+#pragma unroll
+                for (int sl = 1; sl < kRouterMaxSlices; ++sl)
+                    if (sl < a.nks) v = v + pv[u][sl];
+                if (a.bias) v = v + a.bias[i];
+                a.logits[(long long)(t0 + tt) * a.Er + i] = v;
+                lrow[tt * RW + i] = v;
+            }
+        }
     }
     __syncthreads();
     // (2) per token: max of the routed logits (NaN ignored, first of equals
     // kept) and, for shared gating, of all rows (z-loss)
     if (valid) {
-        float m = -INFINITY;
-        for (int i = ns; i < a.E; ++i) {
-            const float v = lrow[tid][i];
-            if (v > m) m = v;
+        const float *row = lrow + tid * RW;
+        float m = -INFINITY, mz = -INFINITY;
+        for (int i0 = 0; i0 < EM; i0 += 4) {
+            const float4 v4 = *(const float4 *)(row + i0);
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int i = i0 + c;
+                if (i >= ns && i < a.E && vv[c] > m) m = vv[c];
+                if (i < a.Er && vv[c] > mz) mz = vv[c];
+            }
         }
         rmax[tid] = m;
-        if (shared_gate) {
-            float mz = -INFINITY;
-            for (int i = 0; i < a.Er; ++i) {
-                const float v = lrow[tid][i];
-                if (v > mz) mz = v;
-            }
-            zmax[tid] = mz;
-        }
+        zmax[tid] = mz;
     }
     __syncthreads();
     // (3) exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m == +Inf)
     for (int q = tid; q < ntok * Ero; q += kRouteThreads) {
         const int tt = q / Ero, i = ns + (q - tt * Ero);
-        const float m = rmax[tt], v = lrow[tt][i];
-        prow[tt][i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
+        const float m = rmax[tt], v = lrow[tt * RW + i];
+        prow[tt * RW + i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
     }
     if (shared_gate)
         for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
             const int tt = q / a.Er, i = q - tt * a.Er;
-            zrow[tt][i] = (float)exp((double)(lrow[tt][i] - zmax[tt]));
+            zrow[tt * RW + i] = (float)exp((double)(lrow[tt * RW + i] - zmax[tt]));
         }
     __syncthreads();
     // (4) per token: sum in expert order
     if (valid) {
+        const float *row = prow + tid * RW;
         float s = 0.0f;
-        for (int i = ns; i < a.E; ++i) s = s + prow[tid][i];
+        for (int i0 = ns & ~3; i0 < a.E; i0 += 4) {
+            const float4 v4 = *(const float4 *)(row + i0);
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int i = i0 + c;
+                if (i >= ns && i < a.E) s = s + vv[c];
+            }
+        }
         rsum[tid] = s;
     }
     __syncthreads();
@@ -352,13 +426,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         if (i < ns) {
             pv = 1.0f / (float)a.E;
         } else {
-            const float pu = prow[tt][i] / rsum[tt];
-            prow[tt][i] = pu;
+            const float pu = prow[tt * RW + i] / rsum[tt];
+            prow[tt * RW + i] = pu;
             pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
         }
-        srow[tt][i] = pv;
+        srow[tt * RW + i] = pv;
         const double pd = (double)pv;
-        hrow[tt][i] = pd * log(pd + 1e-8);
+        hrow[tt * RWD + i] = pd * log(pd + 1e-8);
         a.probs[(long long)(t0 + tt) * a.E + i] = pv;
     }
     __syncthreads();
@@ -370,26 +444,36 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 
     // (6) per token: top-k and gates, logsumexp, entropy
     if (valid) {
-        const float *p = prow[tid];
+        const float *p = prow + tid * RW;
         int sel[MOE_MAX_TOPK];
         float g[MOE_MAX_TOPK];
         if (shared_gate) {
             // top-k and gates on the routed probabilities as the base gate
-            // returns them (before the 1 - ns/E scaling)
+            // returns them (before the 1 - ns/E scaling); the routed rows are
+            // read from the 16-byte-aligned row start, with the first ns masked
             const int tk = a.kt;
             const double gscale = 1.0 - (double)ns / (double)tk;
             const float gshared = 1.0f / (float)tk;
-            topk_row(p + ns, Ero, a.k, sel, g);
+            float *pm = prow + tid * RW;
+            for (int i = 0; i < ns; ++i) pm[i] = -INFINITY;  // below every probability
+            topk_row(p, a.E, a.k, sel, g);
             for (int j = 0; j < ns; ++j) {
                 ex[j] = j + 1;
                 a.gates[(long long)t * tk + j] = gshared;
             }
             for (int j = 0; j < a.k; ++j) {
-                ex[ns + j] = sel[j] + ns + 1;
+                ex[ns + j] = sel[j] + 1;
                 a.gates[(long long)t * tk + ns + j] = (float)((double)g[j] * gscale);
             }
+            const float *zr = zrow + tid * RW;
             float sz = 0.0f;
-            for (int i = 0; i < a.Er; ++i) sz = sz + zrow[tid][i];
+            for (int i0 = 0; i0 < a.Er; i0 += 4) {
+                const float4 v4 = *(const float4 *)(zr + i0);
+                const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (i0 + c < a.Er) sz = sz + vv[c];
+            }
             const float lse = zmax[tid] + (float)log((double)sz);
             zterm = (double)(lse * lse);
         } else {
@@ -404,8 +488,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         }
         for (int j = 0; j < a.kt; ++j) a.idx[(long long)t * a.kt + j] = ex[j];
         // entropy of update_stats! in Float64, expert order
+        const double *hr = hrow + tid * RWD;
         double hs = 0.0;
-        for (int i = 0; i < a.E; ++i) hs = hs + hrow[tid][i];
+        for (int i0 = 0; i0 < a.E; i0 += 2) {
+            const double2 h2 = *(const double2 *)(hr + i0);
+            hs = hs + h2.x;
+            if (i0 + 1 < a.E) hs = hs + h2.y;
+        }
         hterm = -hs;
     }
     __syncthreads();
@@ -463,7 +552,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         a.blk_counts[(long long)nb * a.E + e] = c;
         // per-expert probability sums (Switch loss P_e) in fp64, token order
         double ps = 0.0;
-        for (int i = 0; i < ntok; ++i) ps += (double)srow[i][e];
+#pragma unroll 8
+        for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
         a.blk_stats[(long long)nb * (a.E + 2) + e] = ps;
     }
     if (tok) {
@@ -487,7 +577,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
-    hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), 0, s, a);
+    const size_t lds = (size_t)kRouteBlock * (sizeof(float) * route_rw(std::max(a.Er, a.E)) *
+                                                  (a.gate_kind == MOE_GATE_SHARED ? 3 : 2) +
+                                              sizeof(double) * route_rwd(a.E));
+    static bool big_lds = false;  // dynamic LDS above 64 KB must be allowed explicitly (once per process)
+    if (lds > 65536 && !big_lds) {
+        const hipError_t e = hipFuncSetAttribute((const void *)route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 96 * 1024);
+        if (e != hipSuccess) return e;
+        big_lds = true;
+    }
+    hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -495,23 +595,18 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 // Scan: one block.  Per-expert totals, capacity clamp, offsets, per-block rank
 // bases, the (expert, m0) GEMM tile list and the loss scalars.
 // ============================================================================
-// Wave-level fixed-order (butterfly) sum of a double: the same tree every call.
-__device__ inline double wave_sum_f64(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
 __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
+    constexpr int MAXC = 1024;  // chunk partials (one per thread)
     __shared__ int cnt[MOE_MAX_EXPERTS];
     __shared__ int off[MOE_MAX_EXPERTS + 1];
     __shared__ int tstart[MOE_MAX_EXPERTS + 1];
     __shared__ double psum[MOE_MAX_EXPERTS];
     __shared__ double zh[2];
     __shared__ int cap_s;
+    __shared__ int csum[MAXC];
+    __shared__ double ssum[MAXC];
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, nwave = blockDim.x >> 6;
     if (tid == 0) {
         int cap = INT_MAX;
         if (a.training && a.drop) {
@@ -522,42 +617,69 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
         cap_s = cap;
         a.cap_out[0] = cap;
     }
-    __syncthreads();
-    // One wave per expert (and one more pair for the z / entropy sums): the
-    // exclusive prefix of the per-block counts over blocks (64 blocks per step,
-    // carried across steps), and the fp64 sums of the block statistics.
-    for (int e = wave; e < a.E + 1; e += nwave) {
-        if (e < a.E) {
-            int carry = 0;
-            double ps = 0.0;
-            for (int b0 = 0; b0 < a.nblk; b0 += 64) {
-                const int b = b0 + lane;
-                const int c = (b < a.nblk) ? a.blk_counts[(long long)b * a.E + e] : 0;
-                int incl = c;
+    // Thread (g, c), tid = g * NC + c, owns column c (an expert's counts and
+    // probability sums; columns E and E + 1: the z and entropy sums) over the
+    // g-th chunk of CH blocks.  Consecutive threads read consecutive columns of
+    // one block row, so the loads are coalesced; 8 rows are loaded at a time.
+    const int NC = a.E + 2;
+    const int G = max(1, min(MAXC / NC, (a.nblk + 7) / 8));  // chunks of >= 8 blocks
+    const int CH = (a.nblk + G - 1) / G;
+    const int g = tid / NC, c = tid - g * NC;
+    const bool act = g < G;
+    const int b0 = g * CH, b1 = min(a.nblk, b0 + CH);
+    int cs = 0;
+    double ss = 0.0;
+    if (act) {
+        for (int b = b0; b < b1; b += 8) {
+            int cv[8];
+            double sv[8];
 #pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const int v = __shfl_up(incl, d);
-                    if (lane >= d) incl += v;
+            for (int u = 0; u < 8; ++u) {
+                const int bb = min(b + u, b1 - 1);
+                cv[u] = (c < a.E) ? a.blk_counts[(long long)bb * a.E + c] : 0;
+                sv[u] = a.blk_stats[(long long)bb * NC + c];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (b + u < b1) {
+                    cs += cv[u];
+                    ss += sv[u];
                 }
-                if (b < a.nblk) a.rank_base[(long long)b * a.E + e] = carry + incl - c;
-                carry += __shfl(incl, 63);
-                ps += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + e] : 0.0);
-            }
-            if (lane == 0) {
-                cnt[e] = min(carry, cap_s);
-                psum[e] = ps;
-            }
+        }
+        csum[tid] = cs;
+        ssum[tid] = ss;
+    }
+    __syncthreads();
+    if (act && c < a.E) {
+        // rank base of each block of the chunk: the counts of the chunks
+        // before it, then of the chunk's earlier blocks
+        int base = 0;
+        for (int q = 0; q < g; ++q) base += csum[q * NC + c];
+        for (int b = b0; b < b1; b += 8) {
+            int cv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cv[u] = a.blk_counts[(long long)min(b + u, b1 - 1) * a.E + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (b + u < b1) {
+                    a.rank_base[(long long)(b + u) * a.E + c] = base;
+                    base += cv[u];
+                }
+        }
+    }
+    if (act && g == 0) {
+        // column totals, chunk sums in chunk order (fp64, a fixed order)
+        int tc = 0;
+        double ts = 0.0;
+        for (int q = 0; q < G; ++q) {
+            tc += csum[q * NC + c];
+            ts += ssum[q * NC + c];
+        }
+        if (c < a.E) {
+            cnt[c] = min(tc, cap_s);
+            psum[c] = ts;
         } else {
-            double zs = 0.0, hs = 0.0;
-            for (int b0 = 0; b0 < a.nblk; b0 += 64) {
-                const int b = b0 + lane;
-                zs += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + a.E] : 0.0);
-                hs += wave_sum_f64((b < a.nblk) ? a.blk_stats[(long long)b * (a.E + 2) + a.E + 1] : 0.0);
-            }
-            if (lane == 0) {
-                zh[0] = zs;
-                zh[1] = hs;
-            }
+            zh[c - a.E] = ts;
         }
     }
     __syncthreads();
