@@ -57,6 +57,8 @@ struct moe_handle {
     int *perm = nullptr, *pos_of = nullptr;
     void *xp = nullptr, *hbuf = nullptr;
     float *y = nullptr;
+    float *split_ws = nullptr;  // down-GEMM tail split: partials of the split tiles
+    int ncu = 256;              // compute units: workgroup slots of one GEMM round
     void *x_dev = nullptr;
     float *out_dev = nullptr;
 
@@ -390,22 +392,17 @@ static GemmArgs up_args(moe_handle *h, int mt_grid) {
     g.s0 = h->s1; g.s1 = h->s3; g.bias = h->gated ? nullptr : h->b1; g.s_stride = h->H_pad;
     g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
-    g.tile_start = h->tile_start; g.E = h->E; g.ksplit = 1;
+    g.tile_start = h->tile_start; g.E = h->E; g.ksplit = 1; g.ncu = h->ncu;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
     // bf16 kernel: 128 h columns (gated, W1 and W3 rows) or 256 rows per tile
     g.n_tiles = h->bf16_gemm ? h->H_pad / (h->gated ? 128 : 256) : h->H_pad / kGemmBN;
     return g;
 }
 
-// K ranges of the bf16 down GEMM: 2 when the launch would fill fewer than four
-// waves of 256 workgroups (one per CU), so that the last wave is not mostly
-// idle; the combine kernel then sums the two fp32 partials in order.
-static int down_ksplit(const moe_handle *h, int mt_grid) {
-    if (!h->bf16_gemm) return 1;
-    const long long items = (long long)mt_grid * (h->Dout_npad / 256);
-    const int stages = h->H_pad / 32;
-    return (items < 4LL * 256 && stages % 2 == 0 && stages >= 64) ? 2 : 1;
-}
+// The most K ranges a tile of the bf16 down GEMM may be split into: the
+// tiles of the last, partial round of ncu workgroups are split (tail_split),
+// and fold_split_kernel adds their partials to y in range order.
+static int down_ksplit(const moe_handle *h) { return h->bf16_gemm ? kDownSplitMax : 1; }
 
 static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit) {
     GemmArgs g{};
@@ -414,7 +411,7 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit) {
     g.b_stride = h->w2_stride; g.ldb = h->H_pad;
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
-    g.ksplit = ksplit; g.c_split_stride = (long long)h->rows_max * h->Dout;
+    g.ksplit = ksplit; g.ncu = h->ncu; g.split_ws = h->split_ws;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
@@ -432,21 +429,25 @@ static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
 }
 
 static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksplit) {
-    if (h->bf16_gemm) return launch_grouped_gemm_bf16(MODE_DOWN, h->bm, h->wt == WT_FP8, down_args(h, mt_grid, ksplit), s);
+    if (h->bf16_gemm) {
+        const GemmArgs g = down_args(h, mt_grid, ksplit);
+        hipError_t e = launch_grouped_gemm_bf16(MODE_DOWN, h->bm, h->wt == WT_FP8, g, s);
+        if (e == hipSuccess && ksplit > 1) e = launch_fold_split(h->bm, g, s);
+        return e;
+    }
     return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid, 1), s);
 }
 
 static int run_experts(moe_handle *h, int T, hipStream_t s) {
     const int mt = m_tiles_for(h, T);
     HIP_TRY(h, launch_up(h, mt, s));
-    HIP_TRY(h, launch_down(h, mt, s, down_ksplit(h, mt)));
+    HIP_TRY(h, launch_down(h, mt, s, down_ksplit(h)));
     return MOE_OK;
 }
 
 static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
     CombineArgs c{};
     c.y = h->y; c.ld_y = h->Dout; c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
-    c.nsplit = down_ksplit(h, m_tiles_for(h, T)); c.split_stride = (long long)h->rows_max * h->Dout;
     c.T = T; c.D = h->Dout; c.kt = h->kt; c.out = out_dev;
     HIP_TRY(h, launch_combine(c, s));
     return MOE_OK;
@@ -521,6 +522,11 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->gated = cfg->expert_type == MOE_EXPERT_GATED;
     h->expert_set.assign(h->E, 0);
     (void)hipGetDevice(&h->device);
+    {
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, h->device) == hipSuccess && cu > 0)
+            h->ncu = cu;
+    }
 
     auto cleanup = [&](int code) {
         g_create_error = h->err;
@@ -588,7 +594,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->gate_sorted, sizeof(float) * T * kt);
     A(&h->xp, asz * (size_t)h->rows_max * h->D_pad);
     A(&h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
-    A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout * (h->bf16_gemm ? 2 : 1));  // split-K partials
+    A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout);
+    // tail split: fewer than ncu split tiles, each with at most kDownSplitMax - 1 partial blocks of BM x 256
+    if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * (kDownSplitMax - 1));
     if (r != MOE_OK) return cleanup(r);
     // Pads of the packed weights and of the activation rows must read as 0.
     hipError_t ze = hipSuccess;
@@ -870,7 +878,7 @@ int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream) {
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    HIP_TRY(h, launch_down(h, m_tiles_for(h, T), s, down_ksplit(h, m_tiles_for(h, T))));
+    HIP_TRY(h, launch_down(h, m_tiles_for(h, T), s, down_ksplit(h)));
     return MOE_OK;
 }
 

@@ -113,41 +113,57 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *gaddr, uint32_t lds) {
 struct TileJob {
     int e;             // expert
     int ks;            // K range (split-K index)
+    int nks;           // K ranges of the tile (1: not split)
     int KT;            // 32-wide K stages in the range
     int rows;          // valid rows of the tile (<= BM)
     int n0;            // first B row of the tile (first h column in the gated mode)
+    int split_j;       // split tiles: index among them (partials in split_ws)
     long long arow0;   // first A row
 };
 
+// Work items: the tiles that are not split, then the K ranges of the split
+// ones (tail_split).  Each class is dealt to the 8 XCDs in contiguous ranges
+// (block L runs on XCD L mod 8): slots 0 .. pf-1 of an XCD take its whole
+// tiles, the next ps slots its split items, which are dispatched last.
 template <int BM, int NB>
 __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
     const int NT = g.n_tiles;
-    const int KS = g.ksplit;
-    const int W = g.tile_start[g.E] * NT * KS;
-    const int L = blockIdx.x;
-    const int perx = (W + 7) >> 3;
-    const int slot_id = L >> 3;
-    if (slot_id >= perx) return false;
-    const int id = (L & 7) * perx + slot_id;
-    if (id >= W) return false;
-    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT * KS <= id (a non-empty expert)
+    const int W = g.tile_start[g.E] * NT;
+    const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
+    const int nsi = (W - ts.nfull) * ts.S;  // split items
+    const int pf = (ts.nfull + 7) >> 3, ps = (nsi + 7) >> 3;
+    const int L = blockIdx.x, x = L & 7, slot = L >> 3;
+    int tile, ks = 0, nks = 1;
+    if (slot < pf) {
+        tile = x * pf + slot;
+        if (tile >= ts.nfull) return false;
+    } else {
+        if (slot - pf >= ps) return false;
+        const int q = x * ps + (slot - pf);
+        if (q >= nsi) return false;
+        tile = ts.nfull + q / ts.S;
+        ks = q - (q / ts.S) * ts.S;
+        nks = ts.S;
+    }
+    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT <= tile (a non-empty expert)
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (g.tile_start[mid] * NT * KS <= id) lo = mid; else hi = mid - 1;
+        if (g.tile_start[mid] * NT <= tile) lo = mid; else hi = mid - 1;
     }
     const int e = lo;
     const int t0 = g.tile_start[e];
     const int nte = g.tile_start[e + 1] - t0;
-    const int local = id - t0 * NT * KS;  // within the expert: (n-tile, K range) major, m-tile minor
-    const int ntks = local / nte;
-    const int nt = ntks / KS;
-    const int m0 = (local - ntks * nte) * BM;
+    const int local = tile - t0 * NT;  // within the expert: n-tile major, m-tile minor
+    const int nt = local / nte;
+    const int m0 = (local - nt * nte) * BM;
     jb.e = e;
-    jb.ks = ntks - nt * KS;
-    jb.KT = g.K / 32 / KS;
+    jb.ks = ks;
+    jb.nks = nks;
+    jb.KT = g.K / 32 / nks;
     jb.rows = min(BM, g.counts[e] - m0);
     jb.arow0 = (long long)g.offsets[e] + m0;
     jb.n0 = nt * (NB == 2 ? 128 : 256);
+    jb.split_j = tile - ts.nfull;
     return true;
 }
 
@@ -279,7 +295,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
                             act_fast<ACT>(a[4 * g4 + 0] + b4[0]), act_fast<ACT>(a[4 * g4 + 1] + b4[1]),
                             act_fast<ACT>(a[4 * g4 + 2] + b4[2]), act_fast<ACT>(a[4 * g4 + 3] + b4[3]));
                     } else {
-                        float *crow = (float *)g.C + jb.ks * g.c_split_stride + (jb.arow0 + ml) * g.ldc;
+                        // K range 0 (or an unsplit tile) writes y; range r >= 1 its
+                        // partial block in split_ws (BM x 256, row stride 256)
+                        float *crow = (jb.ks == 0)
+                                          ? (float *)g.C + (jb.arow0 + ml) * g.ldc
+                                          : g.split_ws +
+                                                ((long long)jb.split_j * (jb.nks - 1) + jb.ks - 1) * (IM * 64) * 256 +
+                                                (long long)ml * 256 - jb.n0;
                         if (vec4 && n + 3 < g.N) {
                             *(float4 *)(crow + n) = make_float4(a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1],
                                                                 a[4 * g4 + 2] + b4[2], a[4 * g4 + 3] + b4[3]);
@@ -520,10 +542,87 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane);
 }
 
+// ============================================================================
+// Fold of the down GEMM's split tiles (tail_split): y += partial 1, then
+// partial 2, ... (a fixed order, so results are deterministic).  Block
+// (j, q): split tile j, rows q, q + 4, ... of it; a thread covers 4 columns,
+// 4 rows at a time with all their loads in flight.
+// ============================================================================
+__global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
+#pragma clang fp contract(off)
+    const int NT = g.n_tiles;
+    const int W = g.tile_start[g.E] * NT;
+    const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
+    const int j = blockIdx.x;
+    if (ts.S < 2 || j >= W - ts.nfull) return;
+    const int tile = ts.nfull + j;
+    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT <= tile (a non-empty expert)
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (g.tile_start[mid] * NT <= tile) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int t0 = g.tile_start[e];
+    const int nte = g.tile_start[e + 1] - t0;
+    const int local = tile - t0 * NT;
+    const int nt = local / nte;
+    const int m0 = (local - nt * nte) * bm;
+    const int rows = min(bm, g.counts[e] - m0);
+    const long long arow0 = (long long)g.offsets[e] + m0;
+    const int n0 = nt * 256;
+    const int c4 = (threadIdx.x & 63) * 4;
+    const int n = n0 + c4;
+    const bool vec4 = (g.ldc & 3) == 0 && n + 3 < g.N;
+    const float *__restrict__ ws = g.split_ws + (long long)j * (ts.S - 1) * bm * 256 + c4;
+    const long long pstride = (long long)bm * 256;
+    for (int r0 = blockIdx.y * 4 + (threadIdx.x >> 6); r0 < rows; r0 += 64) {
+        float4 v[4], p[4][kDownSplitMax - 1];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = min(r0 + 16 * u, rows - 1);
+            float *__restrict__ yp = (float *)g.C + (arow0 + r) * g.ldc + n;
+            if (vec4) v[u] = *(const float4 *)yp;
+#pragma unroll
+            for (int k = 0; k < kDownSplitMax - 1; ++k)
+                if (k + 1 < ts.S) p[u][k] = *(const float4 *)(ws + k * pstride + (long long)r * 256);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = r0 + 16 * u;
+            if (r >= rows) continue;
+            float *__restrict__ yp = (float *)g.C + (arow0 + r) * g.ldc + n;
+            if (vec4) {
+                float4 a = v[u];
+#pragma unroll
+                for (int k = 0; k < kDownSplitMax - 1; ++k)
+                    if (k + 1 < ts.S) {
+                        a.x = a.x + p[u][k].x; a.y = a.y + p[u][k].y;
+                        a.z = a.z + p[u][k].z; a.w = a.w + p[u][k].w;
+                    }
+                *(float4 *)yp = a;
+            } else {
+                for (int c = 0; c < 4; ++c)
+                    if (n + c < g.N) {
+                        float a = yp[c];
+                        for (int k = 1; k < ts.S; ++k) a = a + ws[(k - 1) * pstride + (long long)r * 256 + c];
+                        yp[c] = a;
+                    }
+            }
+        }
+    }
+}
+
+hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s) {
+    if (g.ksplit < 2 || g.ncu < 1 || g.m_tiles_grid <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fold_split_kernel, dim3(g.ncu, 4), dim3(256), 0, s, g, bm);
+    return hipGetLastError();
+}
+
 template <int MODE, int BM, int ACT, int WF8>
 static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
-    long long total = (long long)g.m_tiles_grid * g.n_tiles * g.ksplit;
-    total = (total + 7) / 8 * 8;
+    // 8 XCDs x (slots for the whole tiles + slots for the split items)
+    const long long tiles = (long long)g.m_tiles_grid * g.n_tiles;
+    const long long total = 8 * ((tiles + 7) / 8 + (g.ksplit > 1 ? (g.ncu + 7) / 8 : 0));
     hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
 }
@@ -544,8 +643,8 @@ static hipError_t launch_bf16_act(const GemmArgs &g, hipStream_t s) {
 
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s) {
     if (g.m_tiles_grid <= 0 || g.n_tiles <= 0) return hipSuccess;
-    // a split K range must be whole stages, and only the fp32 down GEMM writes partial sums
-    if (g.ksplit < 1 || (g.K / 32) % g.ksplit != 0 || (g.ksplit > 1 && mode != MODE_DOWN)) return hipErrorInvalidValue;
+    // only the fp32 down GEMM writes partial sums
+    if (g.ksplit < 1 || (g.ksplit > 1 && (mode != MODE_DOWN || !g.split_ws || g.ncu < 1))) return hipErrorInvalidValue;
     if (wfp8 && (!g.s0 || (mode == MODE_GATED_UP && !g.s1))) return hipErrorInvalidValue;
 #define MOE_BF16_CASE(M, B, F) \
     if (mode == M && bm == B && (wfp8 != 0) == (F != 0)) return launch_bf16_act<M, B, F>(g, s);

@@ -123,10 +123,34 @@ struct PermuteArgs {
     int copy_rows;               // 0: only the index arrays
 };
 
+// Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots; the
+// rem = W mod ncu tiles of the last, partial round are each split into S K
+// ranges (the largest S <= smax with S dividing the K stages and rem * S <=
+// ncu), so that round is as long as 1/S of a tile.  Tiles are numbered
+// expert-major, then n-tile, then m-tile; tiles >= nfull are split.  K range
+// 0 of a split tile writes y, range r >= 1 writes its partial to split_ws
+// block j (S - 1) + r - 1 (j = tile - nfull; a block is BM x 256 fp32, row
+// stride 256); fold_split_kernel then adds them to y in range order.
+struct TailSplit {
+    int nfull;   // tiles not split
+    int S;       // K ranges of each split tile (1: none)
+};
+__host__ __device__ inline TailSplit tail_split(int W, int ncu, int smax, int stages) {
+    TailSplit t{W, 1};
+    const int rem = (ncu > 0) ? W % ncu : 0;
+    if (rem == 0 || smax < 2) return t;
+    for (int s = smax; s > 1; --s)
+        if (rem * s <= ncu && stages % s == 0) {
+            t.nfull = W - rem;
+            t.S = s;
+            return t;
+        }
+    return t;
+}
+constexpr int kDownSplitMax = 4;
+
 struct CombineArgs {
     const float *y; int ld_y;    // [rows][ld_y]
-    int nsplit;                  // y holds nsplit partial sums (split-K down GEMM), summed in order
-    long long split_stride;      // elements between partial-sum buffers
     const int *idx; const int *pos_of; const float *gates;
     int T, D, kt;
     float *out;                  // [T][D]
@@ -147,8 +171,9 @@ struct GemmArgs {
     const int *tile_start;               // [E+1] (bf16 kernel work list)
     int E;
     int m_tiles_grid; int n_tiles;
-    int ksplit;                          // bf16 kernel: K ranges per tile (partial outputs at C + ks * c_split_stride)
-    long long c_split_stride;
+    int ksplit;                          // bf16 kernel: the most K ranges a tail tile may be split into (tail_split)
+    int ncu;                             // workgroup slots of one round (compute units)
+    float *split_ws;                     // partials of split tiles (MODE_DOWN, ksplit > 1)
     int act;
 };
 
@@ -169,5 +194,7 @@ hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const Gem
                                hipStream_t s);
 // bf16 activations x bf16 weights; bm = 128 or 256 rows per tile (the scan's bm)
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
+// after a MODE_DOWN launch with ksplit > 1: y of each split tile += its partials, in range order
+hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s);
 
 }  // namespace moe

@@ -874,15 +874,14 @@ hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
 // ascending expert order of gate * y, as separate fp32 multiply and add on a
 // zero start (src/core/moe_layer.jl:132, 205-217).  No atomics.
 //
-// Fast path (every one of the token's KT entries kept, y rows 16-byte
-// aligned): the entries are sorted by expert in registers, and all loads of
-// a chunk of U float4 per lane (KT entries x NS partial sums each) are issued
-// before any is summed.  Otherwise the generic path below.
+// Fast path (every one of the token's KT entries kept, rows 16-byte
+// aligned): the entries are sorted by expert in registers, and all y loads of
+// a chunk of U float4 per lane are issued before any is summed.
 // ============================================================================
-template <int KT, int NS>
+template <int KT>
 __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
 #pragma clang fp contract(off)
-    constexpr int U = (KT * NS >= 8) ? 2 : (KT * NS >= 4 ? 4 : 8);
+    constexpr int U = (KT >= 8) ? 2 : (KT >= 4 ? 4 : 8);
     int ee[KT], pp[KT];
     float gg[KT];
 #pragma unroll
@@ -906,32 +905,24 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
         }
     float *__restrict__ o = a.out + (long long)t * a.D;
     for (int d0 = 0; d0 < a.D; d0 += 256 * U) {
-        float4 v[KT][NS][U];
+        float4 v[KT][U];
 #pragma unroll
         for (int i = 0; i < KT; ++i)
 #pragma unroll
-            for (int sp = 0; sp < NS; ++sp)
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int d = min(d0 + u * 256 + lane * 4, a.D - 4);
-                    v[i][sp][u] = *(const float4 *)(a.y + (long long)pp[i] * a.ld_y + sp * a.split_stride + d);
-                }
+            for (int u = 0; u < U; ++u) {
+                const int d = min(d0 + u * 256 + lane * 4, a.D - 4);
+                v[i][u] = *(const float4 *)(a.y + (long long)pp[i] * a.ld_y + d);
+            }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int i = 0; i < KT; ++i) {
-                float4 y = v[i][0][u];
-#pragma unroll
-                for (int sp = 1; sp < NS; ++sp) {
-                    y.x = y.x + v[i][sp][u].x; y.y = y.y + v[i][sp][u].y;
-                    y.z = y.z + v[i][sp][u].z; y.w = y.w + v[i][sp][u].w;
-                }
                 const float g = gg[i];
-                acc.x = acc.x + g * y.x;
-                acc.y = acc.y + g * y.y;
-                acc.z = acc.z + g * y.z;
-                acc.w = acc.w + g * y.w;
+                acc.x = acc.x + g * v[i][u].x;
+                acc.y = acc.y + g * v[i][u].y;
+                acc.z = acc.z + g * v[i][u].z;
+                acc.w = acc.w + g * v[i][u].w;
             }
             const int d = d0 + u * 256 + lane * 4;
             if (d < a.D) *(float4 *)(o + d) = acc;
@@ -939,10 +930,10 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
     }
 }
 
-template <int KT, int NS>
+template <int KT>
 __device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, int t, int lane) {
-    if (a.kt != KT || a.nsplit != NS) return false;
-    combine_fast<KT, NS>(a, t, lane);
+    if (a.kt != KT) return false;
+    combine_fast<KT>(a, t, lane);
     return true;
 }
 
@@ -951,14 +942,11 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
-    bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0 && (a.split_stride & 3) == 0;
+    bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0;
     for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
     if (all_kept) {
-        if (try_combine_fast<2, 1>(a, t, lane) || try_combine_fast<2, 2>(a, t, lane) ||
-            try_combine_fast<1, 1>(a, t, lane) || try_combine_fast<1, 2>(a, t, lane) ||
-            try_combine_fast<8, 1>(a, t, lane) || try_combine_fast<8, 2>(a, t, lane) ||
-            try_combine_fast<4, 1>(a, t, lane) || try_combine_fast<4, 2>(a, t, lane) ||
-            try_combine_fast<6, 1>(a, t, lane) || try_combine_fast<6, 2>(a, t, lane))
+        if (try_combine_fast<2>(a, t, lane) || try_combine_fast<1>(a, t, lane) || try_combine_fast<8>(a, t, lane) ||
+            try_combine_fast<4>(a, t, lane) || try_combine_fast<6>(a, t, lane))
             return;
     }
     int ee[MOE_MAX_TOPK], pp[MOE_MAX_TOPK];
@@ -983,36 +971,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         ++n;
     }
     float *o = a.out + (long long)t * a.D;
-    // y row of an entry: the sum, in split order, of the down GEMM's K-range partials
-    if ((a.D & 3) == 0 && (a.ld_y & 3) == 0) {
-        for (int d = lane * 4; d < a.D; d += 256) {
-            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int i = 0; i < n; ++i) {
-                const float *yr = a.y + (long long)pp[i] * a.ld_y + d;
-                float4 v = *(const float4 *)yr;
-                for (int sp = 1; sp < a.nsplit; ++sp) {
-                    const float4 u = *(const float4 *)(yr + sp * a.split_stride);
-                    v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
-                }
-                const float g = gg[i];
-                acc.x = acc.x + g * v.x;
-                acc.y = acc.y + g * v.y;
-                acc.z = acc.z + g * v.z;
-                acc.w = acc.w + g * v.w;
-            }
-            *(float4 *)(o + d) = acc;
-        }
-    } else {
-        for (int d = lane; d < a.D; d += 64) {
-            float acc = 0.0f;
-            for (int i = 0; i < n; ++i) {
-                const float *yr = a.y + (long long)pp[i] * a.ld_y + d;
-                float v = yr[0];
-                for (int sp = 1; sp < a.nsplit; ++sp) v = v + yr[sp * a.split_stride];
-                acc = acc + gg[i] * v;
-            }
-            o[d] = acc;
-        }
+    for (int d = lane; d < a.D; d += 64) {
+        float acc = 0.0f;
+        for (int i = 0; i < n; ++i) acc = acc + gg[i] * a.y[(long long)pp[i] * a.ld_y + d];
+        o[d] = acc;
     }
 }
 
