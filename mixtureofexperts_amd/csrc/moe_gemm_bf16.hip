@@ -545,8 +545,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // ============================================================================
 // Fold of the down GEMM's split tiles (tail_split): y += partial 1, then
 // partial 2, ... (a fixed order, so results are deterministic).  Block
-// (j, q): split tile j, rows q, q + 4, ... of it; a thread covers 4 columns,
-// 4 rows at a time with all their loads in flight.
+// (j, q): split tile j, its 16 rows from 16 q; a thread covers 4 columns of
+// 4 rows, with all their loads in flight (one batch: no store is followed by
+// a load in the same thread).
 // ============================================================================
 __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
 #pragma clang fp contract(off)
@@ -575,11 +576,12 @@ __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
     const bool vec4 = (g.ldc & 3) == 0 && n + 3 < g.N;
     const float *__restrict__ ws = g.split_ws + (long long)j * (ts.S - 1) * bm * 256 + c4;
     const long long pstride = (long long)bm * 256;
-    for (int r0 = blockIdx.y * 4 + (threadIdx.x >> 6); r0 < rows; r0 += 64) {
+    const int r0 = blockIdx.y * 16 + (threadIdx.x >> 6);
+    if (r0 < rows) {
         float4 v[4], p[4][kDownSplitMax - 1];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int r = min(r0 + 16 * u, rows - 1);
+            const int r = min(r0 + 4 * u, rows - 1);
             float *__restrict__ yp = (float *)g.C + (arow0 + r) * g.ldc + n;
             if (vec4) v[u] = *(const float4 *)yp;
 #pragma unroll
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int r = r0 + 16 * u;
+            const int r = r0 + 4 * u;
             if (r >= rows) continue;
             float *__restrict__ yp = (float *)g.C + (arow0 + r) * g.ldc + n;
             if (vec4) {
@@ -614,7 +616,7 @@ __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
 
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s) {
     if (g.ksplit < 2 || g.ncu < 1 || g.m_tiles_grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fold_split_kernel, dim3(g.ncu, 4), dim3(256), 0, s, g, bm);
+    hipLaunchKernelGGL(fold_split_kernel, dim3(g.ncu, (bm + 15) / 16), dim3(256), 0, s, g, bm);
     return hipGetLastError();
 }
 

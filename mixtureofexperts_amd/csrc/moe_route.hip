@@ -296,35 +296,54 @@ __device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *
     }
 }
 
-// LDS row strides of the routing kernel for E rows: floats (lrow, prow, zrow)
-// and doubles (hrow).  A multiple of 4 floats (16 B) whose count of 16-byte
-// units is odd, so that 16 token threads reading 16 B at one column hit 16
-// distinct bank quads.
+// LDS row stride of the routing kernel for E rows: a multiple of 4 floats
+// (16 B) whose count of 16-byte units is odd, so that 16 token threads
+// reading 16 B at one column hit 16 distinct bank quads.
 __host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) | 1)); }
-__host__ __device__ inline int route_rwd(int E) { return 2 * ((((E + 1) / 2 + 1) | 1)); }
+
+// Fixed-order sum over the TPT consecutive lanes of a token (a butterfly: the
+// same tree on every call).
+template <int TPT, typename F>
+__device__ __forceinline__ F token_sum(F v) {
+#pragma unroll
+    for (int o = 1; o < TPT; o <<= 1) v = v + __shfl_xor(v, o);
+    return v;
+}
+template <int TPT>
+__device__ __forceinline__ float token_max(float v) {  // NaN ignored (v > m is false for NaN)
+#pragma unroll
+    for (int o = 1; o < TPT; o <<= 1) {
+        const float w = __shfl_xor(v, o);
+        if (w > v) v = w;
+    }
+    return v;
+}
 
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma clang fp contract(off)
-    // Block: kRouteBlock tokens, kRouteThreads threads.  Work that the recipe
-    // makes sequential per token (max, the fp32 sum in expert order, top-k,
-    // the fp64 entropy sum) runs one thread per token (threads < kRouteBlock,
-    // all in wave 0), reading its LDS row 16 B at a time; the per-element work
-    // (logits, fp64 exp and log terms) is spread over every thread.  Rows are
-    // sized for this layer's E (dynamic LDS): lrow holds the logits and, once
-    // the exp terms are formed, the output probabilities.
+    // Block: kRouteBlock tokens, kRouteThreads threads.  The recipe's
+    // order-sensitive steps -- the fp32 softmax sum in expert order and the
+    // top-k -- run one thread per token (threads < kRouteBlock, all in wave 0),
+    // reading the token's LDS row 16 B at a time; the rest runs TPT threads
+    // per token (max, exp and probability terms; the fp64 entropy sum and the
+    // z-loss exponent sum as fixed-order per-token reductions).  Rows are sized
+    // for this layer's E (dynamic LDS).  Every global output is written in the
+    // last phase: a store's data register may not be reused before the store
+    // has completed, so stores in between would stall the phases that follow.
     constexpr int NWV = 1;  // the token threads form one wave
+    constexpr int TPT = kRouteThreads / kRouteBlock;
+    static_assert(TPT == 8 && kRouteBlock * TPT == kRouteThreads, "threads per token");
     extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
     __shared__ int wcnt[NWV][MOE_MAX_EXPERTS];
     __shared__ double red[2][kRouteBlock];
-    __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock];
+    __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock], zsum[kRouteBlock];
+    __shared__ double hsum[kRouteBlock];
     const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
     const int EM = max(a.Er, a.E);
-    const int RW = route_rw(EM), RWD = route_rwd(a.E);
-    float *lrow = (float *)rdyn;                         // [kRouteBlock][RW] logits, then output probabilities
-    float *prow = lrow + kRouteBlock * RW;               // exp terms, then probabilities (before the shared-gating scale)
-    double *hrow = (double *)(prow + kRouteBlock * RW);  // [kRouteBlock][RWD] entropy terms p log(p + 1e-8)
-    float *zrow = (float *)(hrow + kRouteBlock * RWD);   // shared gating: exp terms of all rows for the z-loss
-    float *srow = lrow;
+    const int RW = route_rw(EM);
+    float *lrow = (float *)rdyn;            // [kRouteBlock][RW] logits
+    float *prow = lrow + kRouteBlock * RW;  // exp terms, then probabilities (before the shared-gating scale)
+    float *srow = prow + kRouteBlock * RW;  // output probabilities (after it)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -336,16 +355,18 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     const bool valid = tok && t < a.T;
     const int ns = shared_gate ? a.ns : 0;      // rows before the routed ones
     const int Ero = a.E - ns;                   // routed rows (softmax width)
+    const int rt = tid / TPT, rs = tid - rt * TPT;  // row-parallel phases: token rt, lane rs of it
+    const bool rvalid = rt < ntok;
 
     for (int i = tid; i < NWV * MOE_MAX_EXPERTS; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
 
     // (1) router logits: the K-slice partial sums in slice order, then the
-    // bias.  Elements q = tid + 256 u; the slices of 4 elements are loaded
-    // (from clamped addresses) before any is summed.
+    // bias.  Elements q = tid + 256 u; the slices (and biases) of 4 elements
+    // are loaded, from clamped addresses, before any is summed.
     const int nq = ntok * a.Er;
     const long long sstride = (long long)a.T * a.Er;
     for (int q0 = 0; q0 < nq; q0 += 4 * kRouteThreads) {
-        float pv[4][kRouterMaxSlices];
+        float pv[4][kRouterMaxSlices], bv[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = min(q0 + u * kRouteThreads + tid, nq - 1);
@@ -354,6 +375,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma unroll
             for (int sl = 0; sl < kRouterMaxSlices; ++sl)
                 pv[u][sl] = a.part[min(sl, a.nks - 1) * sstride + o];
+            bv[u] = a.bias ? a.bias[i] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -364,53 +386,59 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma unroll
                 for (int sl = 1; sl < kRouterMaxSlices; ++sl)
                     if (sl < a.nks) v = v + pv[u][sl];
-                if (a.bias) v = v + a.bias[i];
-                a.logits[(long long)(t0 + tt) * a.Er + i] = v;
+                if (a.bias) v = v + bv[u];
                 lrow[tt * RW + i] = v;
             }
         }
     }
     __syncthreads();
-    // (2) per token: max of the routed logits (NaN ignored, first of equals
-    // kept) and, for shared gating, of all rows (z-loss)
-    if (valid) {
-        const float *row = lrow + tid * RW;
+    // (2) per token: max of the routed logits and, for shared gating, of all
+    // rows (z-loss); NaN ignored.  The order does not matter: only the sign of
+    // a zero maximum could, and exp(l - m) is the same for m = +0 and -0.
+    {
         float m = -INFINITY, mz = -INFINITY;
-        for (int i0 = 0; i0 < EM; i0 += 4) {
-            const float4 v4 = *(const float4 *)(row + i0);
-            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int i = i0 + c;
-                if (i >= ns && i < a.E && vv[c] > m) m = vv[c];
-                if (i < a.Er && vv[c] > mz) mz = vv[c];
+        if (rvalid)
+            for (int i = rs; i < EM; i += TPT) {
+                const float v = lrow[rt * RW + i];
+                if (i >= ns && i < a.E && v > m) m = v;
+                if (i < a.Er && v > mz) mz = v;
             }
+        m = token_max<TPT>(m);
+        mz = token_max<TPT>(mz);
+        if (rvalid && rs == 0) {
+            rmax[rt] = m;
+            zmax[rt] = mz;
         }
-        rmax[tid] = m;
-        zmax[tid] = mz;
     }
     __syncthreads();
-    // (3) exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m == +Inf)
-    for (int q = tid; q < ntok * Ero; q += kRouteThreads) {
-        const int tt = q / Ero, i = ns + (q - tt * Ero);
-        const float m = rmax[tt], v = lrow[tt * RW + i];
-        prow[tt * RW + i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
-    }
-    if (shared_gate)
-        for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
-            const int tt = q / a.Er, i = q - tt * a.Er;
-            zrow[tt * RW + i] = (float)exp((double)(lrow[tt * RW + i] - zmax[tt]));
+    // (3) exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m ==
+    // +Inf); shared gating: the z-loss exponent sum over all rows
+    {
+        float zs = 0.0f;
+        if (rvalid) {
+            const float m = rmax[rt], mz = zmax[rt];
+            for (int i = rs; i < a.Er; i += TPT) {
+                const float v = lrow[rt * RW + i];
+                if (i >= ns && i < a.E)
+                    prow[rt * RW + i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
+                if (shared_gate) zs = zs + (float)exp((double)(v - mz));
+            }
         }
+        if (shared_gate) {
+            zs = token_sum<TPT>(zs);
+            if (rvalid && rs == 0) zsum[rt] = zs;
+        }
+    }
     __syncthreads();
     // (4) per token: sum in expert order
     if (valid) {
         const float *row = prow + tid * RW;
         float s = 0.0f;
-        for (int i0 = ns & ~3; i0 < a.E; i0 += 4) {
-            const float4 v4 = *(const float4 *)(row + i0);
-            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        for (int i0 = ns & ~3; i0 < a.E; i0 += 8) {
+            const float4 va = *(const float4 *)(row + i0), vb = *(const float4 *)(row + i0 + 4);
+            const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < 8; ++c) {
                 const int i = i0 + c;
                 if (i >= ns && i < a.E) s = s + vv[c];
             }
@@ -419,83 +447,84 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
     __syncthreads();
     // (5) probabilities p = e / s; output rows (shared gating: shared rows 1/E,
-    // routed rows p scaled by 1 - ns/E in Float64) and their entropy terms
-    for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
-        const int tt = q / a.E, i = q - tt * a.E;
-        float pv;
-        if (i < ns) {
-            pv = 1.0f / (float)a.E;
-        } else {
-            const float pu = prow[tt * RW + i] / rsum[tt];
-            prow[tt * RW + i] = pu;
-            pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
+    // routed rows p scaled by 1 - ns/E in Float64); the entropy terms
+    // p log(p + 1e-8) summed in fp64 per token (a fixed order)
+    {
+        double hs = 0.0;
+        if (rvalid) {
+            const float s = rsum[rt];
+            for (int i = rs; i < a.E; i += TPT) {
+                float pv;
+                if (i < ns) {
+                    pv = 1.0f / (float)a.E;
+                } else {
+                    const float pu = prow[rt * RW + i] / s;
+                    prow[rt * RW + i] = pu;
+                    pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
+                }
+                srow[rt * RW + i] = pv;
+                const double pd = (double)pv;
+                hs = hs + pd * log(pd + 1e-8);
+            }
         }
-        srow[tt * RW + i] = pv;
-        const double pd = (double)pv;
-        hrow[tt * RWD + i] = pd * log(pd + 1e-8);
-        a.probs[(long long)(t0 + tt) * a.E + i] = pv;
+        hs = token_sum<TPT>(hs);
+        if (rvalid && rs == 0) hsum[rt] = hs;
     }
     __syncthreads();
 
     int ex[MOE_MAX_TOPK];     // 1-based expert ids of this token's slots
+    float gx[MOE_MAX_TOPK];   // their gates
     double zterm = 0.0, hterm = 0.0;
 #pragma unroll
-    for (int j = 0; j < MOE_MAX_TOPK; ++j) ex[j] = 0;
+    for (int j = 0; j < MOE_MAX_TOPK; ++j) {
+        ex[j] = 0;
+        gx[j] = 0.0f;
+    }
 
     // (6) per token: top-k and gates, logsumexp, entropy
     if (valid) {
-        const float *p = prow + tid * RW;
+        float *p = prow + tid * RW;
         int sel[MOE_MAX_TOPK];
         float g[MOE_MAX_TOPK];
         if (shared_gate) {
             // top-k and gates on the routed probabilities as the base gate
-            // returns them (before the 1 - ns/E scaling); the routed rows are
-            // read from the 16-byte-aligned row start, with the first ns masked
-            const int tk = a.kt;
-            const double gscale = 1.0 - (double)ns / (double)tk;
-            const float gshared = 1.0f / (float)tk;
-            float *pm = prow + tid * RW;
-            for (int i = 0; i < ns; ++i) pm[i] = -INFINITY;  // below every probability
+            // returns them (before the 1 - ns/E scaling); the row is read from
+            // its 16-byte-aligned start with the first ns entries masked
+            const double gscale = 1.0 - (double)ns / (double)a.kt;
+            const float gshared = 1.0f / (float)a.kt;
+            for (int i = 0; i < ns; ++i) p[i] = -INFINITY;  // below every probability
             topk_row(p, a.E, a.k, sel, g);
-            for (int j = 0; j < ns; ++j) {
-                ex[j] = j + 1;
-                a.gates[(long long)t * tk + j] = gshared;
-            }
-            for (int j = 0; j < a.k; ++j) {
-                ex[ns + j] = sel[j] + 1;
-                a.gates[(long long)t * tk + ns + j] = (float)((double)g[j] * gscale);
-            }
-            const float *zr = zrow + tid * RW;
-            float sz = 0.0f;
-            for (int i0 = 0; i0 < a.Er; i0 += 4) {
-                const float4 v4 = *(const float4 *)(zr + i0);
-                const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (i0 + c < a.Er) sz = sz + vv[c];
+            for (int j = 0; j < MOE_MAX_TOPK; ++j) {
+                if (j < ns) {
+                    ex[j] = j + 1;
+                    gx[j] = gshared;
+                }
+                if (j < a.k) {
+                    // slot ns + j (ns + k <= MOE_MAX_TOPK)
+#pragma unroll
+                    for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                        if (q == ns + j) {
+                            ex[q] = sel[j] + 1;
+                            gx[q] = (float)((double)g[j] * gscale);
+                        }
+                }
             }
-            const float lse = zmax[tid] + (float)log((double)sz);
+            const float lse = zmax[tid] + (float)log((double)zsum[tid]);
             zterm = (double)(lse * lse);
         } else {
             topk_row(p, a.E, a.k, sel, g);
-            for (int j = 0; j < a.k; ++j) {
-                ex[j] = sel[j] + 1;
-                a.gates[(long long)t * a.kt + j] = g[j];
-            }
+#pragma unroll
+            for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                if (j < a.k) {
+                    ex[j] = sel[j] + 1;
+                    gx[j] = g[j];
+                }
             // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe
             const float lse = rmax[tid] + (float)log((double)rsum[tid]);
             zterm = (double)(lse * lse);
         }
-        for (int j = 0; j < a.kt; ++j) a.idx[(long long)t * a.kt + j] = ex[j];
-        // entropy of update_stats! in Float64, expert order
-        const double *hr = hrow + tid * RWD;
-        double hs = 0.0;
-        for (int i0 = 0; i0 < a.E; i0 += 2) {
-            const double2 h2 = *(const double2 *)(hr + i0);
-            hs = hs + h2.x;
-            if (i0 + 1 < a.E) hs = hs + h2.y;
-        }
-        hterm = -hs;
+        hterm = -hsum[tid];  // entropy of update_stats!, Float64
     }
     __syncthreads();
 
@@ -517,9 +546,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         int mine = 0;
         if (has) {
             const int j0 = __ffs(~done & all) - 1;
-            mine = ex[j0];
+#pragma unroll
+            for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                if (j == j0) mine = ex[j];
         }
-        const int estar = __shfl(mine, leader);
+        const int estar = __builtin_amdgcn_readlane(mine, leader);
         int js = -1;
 #pragma unroll
         for (int j = 0; j < MOE_MAX_TOPK; ++j)
@@ -533,15 +564,39 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         }
         if (lane == leader) wcnt[wave][estar - 1] = __popcll(mm);
     }
+    if (tok) {
+        red[0][tid] = zterm;
+        red[1][tid] = hterm;
+    }
     __syncthreads();
+    for (int st = kRouteBlock / 2; st > 0; st >>= 1) {
+        if (tid < st) {
+            red[0][tid] += red[0][tid + st];
+            red[1][tid] += red[1][tid + st];
+        }
+        __syncthreads();
+    }
+
+    // ---- outputs --------------------------------------------------------------
+    for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
+        const int tt = q / a.Er, i = q - tt * a.Er;
+        a.logits[(long long)(t0 + tt) * a.Er + i] = lrow[tt * RW + i];
+    }
+    for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
+        const int tt = q / a.E, i = q - tt * a.E;
+        a.probs[(long long)(t0 + tt) * a.E + i] = srow[tt * RW + i];
+    }
     if (valid) {
 #pragma unroll
         for (int j = 0; j < MOE_MAX_TOPK; ++j) {
             if (j < a.kt) {
+                const long long ent = (long long)t * a.kt + j;
+                a.idx[ent] = ex[j];
+                a.gates[ent] = gx[j];
                 int base = 0;
                 if (ex[j] > 0)
                     for (int w = 0; w < wave; ++w) base += wcnt[w][ex[j] - 1];
-                a.rank[(long long)t * a.kt + j] = base + r[j];
+                a.rank[ent] = base + r[j];
             }
         }
     }
@@ -556,18 +611,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
         a.blk_stats[(long long)nb * (a.E + 2) + e] = ps;
     }
-    if (tok) {
-        red[0][tid] = zterm;
-        red[1][tid] = hterm;
-    }
-    __syncthreads();
-    for (int st = kRouteBlock / 2; st > 0; st >>= 1) {
-        if (tid < st) {
-            red[0][tid] += red[0][tid + st];
-            red[1][tid] += red[1][tid + st];
-        }
-        __syncthreads();
-    }
     if (tid == 0) {
         a.blk_stats[(long long)nb * (a.E + 2) + a.E] = red[0][0];
         a.blk_stats[(long long)nb * (a.E + 2) + a.E + 1] = red[1][0];
@@ -577,9 +620,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
-    const size_t lds = (size_t)kRouteBlock * (sizeof(float) * route_rw(std::max(a.Er, a.E)) *
-                                                  (a.gate_kind == MOE_GATE_SHARED ? 3 : 2) +
-                                              sizeof(double) * route_rwd(a.E));
+    const size_t lds = (size_t)kRouteBlock * sizeof(float) * route_rw(std::max(a.Er, a.E)) * 3;
     static bool big_lds = false;  // dynamic LDS above 64 KB must be allowed explicitly (once per process)
     if (lds > 65536 && !big_lds) {
         const hipError_t e = hipFuncSetAttribute((const void *)route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
