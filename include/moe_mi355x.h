@@ -160,6 +160,20 @@ int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_
  * the device expert path of expert e (0-based). */
 int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n, float *y);
 
+/* The decode caller: moe_ffn_forward! (src/llama2/inference.jl:58-121)
+ * after its rmsnorm, without shared experts.  Each of the n tokens is routed
+ * on its own (logits = W_router' xb with the router set by moe_set_router,
+ * then compute_gates, src/gating/topk.jl:24-44) and the gated experts of its
+ * k slots are combined in slot order on a zero start (:83-104):
+ * out = ((0 + g_1 y_1) + g_2 y_2) + ..., y = W2 (silu(W1 xb) .* (W3 xb)),
+ * silu(g) = g * (1 / (1 + exp(-g))) (gated_expert_forward!, :154-167).
+ * xb [n][D] fp32, out [n][D_out] fp32 (host); logits [n][E], indices [n][k]
+ * (1-based), gates [n][k] may be NULL.  Gated experts with TopKGating or
+ * SwitchGating only (else MOE_EUNSUPPORTED); 1 <= n <= max_tokens (handles
+ * with bf16 or fp8 weights: max_tokens / 2). */
+int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *logits, int32_t *indices,
+               float *gates);
+
 /* compute_loss(::SwitchTransformerLoss, indices, probs) --
  * src/balancing/losses.jl:15-36.  indices [T][k] 1-based (entries outside
  * 1..E are not counted), probs [T][E]; no handle needed.  Host pointers. */
@@ -176,6 +190,10 @@ int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *los
  * loss_dev (1 float) may be NULL.  Runs on `stream` (hipStream_t). */
 int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T,
                       int32_t training, float *out_dev, float *loss_dev, void *stream);
+
+/* moe_decode on device buffers: xb_dev [n][D] fp32, out_dev [n][D_out] fp32.
+ * Runs on `stream` (hipStream_t). */
+int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_dev, void *stream);
 
 /* Stage-level entry points for profiling: together they issue exactly the
  * kernels of moe_forward_async, one stage per call, on device buffers owned

@@ -5,7 +5,8 @@ The API mirrors the reference's exports for this path
 (src/MixtureOfExperts.jl:14-40): MoEConfig, MoELayer, Router, TopKGating,
 SwitchGating, SharedExpertGating, GatedExpert, StandardExpert,
 SwitchTransformerLoss, ZLoss, NoBalancingLoss, compute_gates, compute_loss,
-create_moe_config, create_moe_layer, reset_stats (reset_stats!).  All compute
+create_moe_config, create_moe_layer, reset_stats (reset_stats!), and the
+decode caller moe_ffn_forward (moe_ffn_forward!, src/llama2/inference.jl:58).  All compute
 runs in libmoe_mi355x.so (hand-written HIP kernels); nothing here falls back
 to a CPU path.
 """
@@ -15,11 +16,11 @@ from .balancing import LoadBalancingLoss, NoBalancingLoss, SwitchTransformerLoss
 from .experts import Expert, GatedExpert, StandardExpert
 from .gating import (GatingMechanism, SharedExpertGating, SwitchGating, TopKGating, compute_gates,
                      route_from_logits)
-from .layer import MoEConfig, MoELayer, Router, create_moe_config, create_moe_layer, reset_stats
+from .layer import MoEConfig, MoELayer, Router, create_moe_config, create_moe_layer, moe_ffn_forward, reset_stats
 
 __all__ = [
     "MoeError", "lib", "gelu", "identity", "relu", "silu", "swish", "LoadBalancingLoss", "NoBalancingLoss",
     "SwitchTransformerLoss", "ZLoss", "compute_loss", "Expert", "GatedExpert", "StandardExpert",
     "GatingMechanism", "SharedExpertGating", "SwitchGating", "TopKGating", "compute_gates", "route_from_logits",
-    "MoEConfig", "MoELayer", "Router", "create_moe_config", "create_moe_layer", "reset_stats",
+    "MoEConfig", "MoELayer", "Router", "create_moe_config", "create_moe_layer", "moe_ffn_forward", "reset_stats",
 ]

@@ -122,3 +122,17 @@ class DeviceLayer:
         y = np.zeros((n, self.output_dim), dtype=np.float32)
         _lib.check(_lib.lib().moe_expert_forward(self.h, int(e), x.ctypes.data, n, y.ctypes.data), self.h)
         return y
+
+    def decode(self, xb_nD):
+        """moe_ffn_forward! on n tokens (moe_decode): returns (out [n][Dout],
+        logits [n][E], indices [n][k] 1-based, gates [n][k])."""
+        x = np.ascontiguousarray(xb_nD, dtype=np.float32)
+        n = x.shape[0]
+        k = _lib.lib().moe_slots_per_token(self.h)
+        out = np.zeros((n, self.output_dim), dtype=np.float32)
+        logits = np.zeros((n, self.num_experts), dtype=np.float32)
+        idx = np.zeros((n, k), dtype=np.int32)
+        gates = np.zeros((n, k), dtype=np.float32)
+        _lib.check(_lib.lib().moe_decode(self.h, x.ctypes.data, n, out.ctypes.data, logits.ctypes.data,
+                                         idx.ctypes.data, gates.ctypes.data), self.h)
+        return out, logits, idx, gates

@@ -38,7 +38,7 @@ EXPORTED_SYMBOLS = [
     "moe_compute_gates", "moe_route_from_logits", "moe_forward", "moe_expert_forward",
     "moe_forward_async", "moe_stage_router_async", "moe_stage_permute_async",
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
-    "moe_read_counts", "moe_switch_loss", "moe_z_loss",
+    "moe_read_counts", "moe_switch_loss", "moe_z_loss", "moe_decode", "moe_decode_async",
 ]
 
 
@@ -129,6 +129,8 @@ def lib():
     L.moe_stage_expert_down_async.argtypes = [vp, i32, vp]
     L.moe_stage_combine_async.argtypes = [vp, i32, vp, vp]
     L.moe_read_counts.argtypes = [vp, vp]
+    L.moe_decode.argtypes = [vp, vp, i32, vp, vp, vp, vp]
+    L.moe_decode_async.argtypes = [vp, vp, i32, vp, vp]
     L.moe_switch_loss.argtypes = [vp, i32, i32, vp, i32, ctypes.c_float, f32p]
     L.moe_z_loss.argtypes = [vp, i32, i32, ctypes.c_float, f32p]
     for name in EXPORTED_SYMBOLS:

@@ -12,7 +12,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libmoe_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["moe_api.hip", "moe_route.hip", "moe_gemm.hip", "moe_gemm_bf16.hip"]
+SOURCES = ["moe_api.hip", "moe_route.hip", "moe_gemm.hip", "moe_gemm_bf16.hip", "moe_decode.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

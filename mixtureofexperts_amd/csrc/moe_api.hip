@@ -829,6 +829,66 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     return MOE_OK;
 }
 
+// ---- decode (moe_ffn_forward!, src/llama2/inference.jl:58-121) -------------
+static int decode_check(moe_handle *h, int n) {
+    int r = check_ready(h);
+    if (r != MOE_OK) return r;
+    if (!h->gated) return fail(h, MOE_EUNSUPPORTED, "decode path: gated experts only (gated_expert_forward!)");
+    if (h->cfg.gate_kind != MOE_GATE_TOPK && h->cfg.gate_kind != MOE_GATE_SWITCH)
+        return fail(h, MOE_EUNSUPPORTED, "decode path: TopKGating or SwitchGating only");
+    if ((h->D & 3) != 0) return fail(h, MOE_EUNSUPPORTED, "decode path: input_dim must be a multiple of 4");
+    // h of the n * k slots is kept as fp32 rows in the expert workspace
+    const long long cap = (long long)h->rows_max * h->H_pad * (h->ct == CT_F32 ? 4 : 2) / (4LL * h->H_pad * h->kt);
+    if (n < 1 || n > h->T_max || n > cap)
+        return fail(h, MOE_EINVAL, "n must be in [1, max_tokens] (bf16 / fp8 handles: [1, max_tokens / 2])");
+    return MOE_OK;
+}
+
+static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_dev, hipStream_t s) {
+    DecodeArgs a{};
+    a.x = x_dev; a.D = h->D; a.n = n; a.kt = h->kt; a.k = h->k; a.E = h->E;
+    a.wr = h->wr; a.Er_pad = h->Er_pad; a.br = h->has_bias ? h->br : nullptr;
+    a.logits = h->logits; a.probs = h->probs; a.idx = h->idx; a.gates = h->gates;
+    a.wt = h->wt; a.w1 = h->w1; a.w3 = h->w3; a.w2 = h->w2;
+    a.w1_stride = h->w1_stride; a.w2_stride = h->w2_stride;
+    a.Dpad = h->D_pad; a.H = h->H; a.Hpad = h->H_pad; a.Dout = h->Dout;
+    a.s1 = h->s1; a.s3 = h->s3; a.s2 = h->s2; a.Dout_npad = h->Dout_npad;
+    a.h = (float *)h->hbuf; a.out = out_dev;
+    HIP_TRY(h, launch_decode_route(a, s));
+    HIP_TRY(h, launch_decode_ffn(a, s));
+    h->last_T = -1;  // the routing buffers no longer describe a layer forward
+    return MOE_OK;
+}
+
+int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *logits, int32_t *indices, float *gates) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = decode_check(h, n);
+    if (r != MOE_OK) return r;
+    if (!xb || !out) return fail(h, MOE_EINVAL, "null xb or out");
+    r = ensure_io_buffers(h);
+    if (r != MOE_OK) return r;
+    hipStream_t s = h->stream;
+    HIP_TRY(h, hipMemcpyAsync(h->x_dev, xb, sizeof(float) * (size_t)n * h->D, hipMemcpyHostToDevice, s));
+    r = decode_locked(h, (const float *)h->x_dev, n, h->out_dev, s);
+    if (r != MOE_OK) return r;
+    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s));
+    if (logits) HIP_TRY(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)n * h->E, hipMemcpyDeviceToHost, s));
+    if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
+    if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    return MOE_OK;
+}
+
+int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_dev, void *stream) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    int r = decode_check(h, n);
+    if (r != MOE_OK) return r;
+    if (!xb_dev || !out_dev) return fail(h, MOE_EINVAL, "null buffer");
+    return decode_locked(h, xb_dev, n, out_dev, stream ? (hipStream_t)stream : h->stream);
+}
+
 int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, int32_t training, float *out_dev,
                       float *loss_dev, void *stream) {
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");

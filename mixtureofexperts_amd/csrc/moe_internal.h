@@ -177,6 +177,25 @@ struct GemmArgs {
     int act;
 };
 
+// Decode (moe_ffn_forward!, src/llama2/inference.jl:58-121): n tokens, each
+// routed and combined on its own, slots in order.
+struct DecodeArgs {
+    const float *x; int D;               // [n][D] fp32 (the rmsnorm'd xb)
+    int n, kt, k, E;
+    const float *wr; int Er_pad;         // router weight [D][Er_pad] fp32
+    const float *br;                     // router bias [E] or null
+    float *logits, *probs;               // [n][E]
+    int *idx; float *gates;              // [n][kt] (1-based expert ids)
+    int wt;                              // weight type (WT_*)
+    const void *w1, *w3, *w2;            // packed [E][Npad][Kpad]
+    long long w1_stride, w2_stride;      // elements per expert
+    int Dpad, H, Hpad, Dout;
+    const float *s1, *s3, *s2;           // fp8 per-row scales [E][Hpad] / [E][Dout_npad] or null
+    int Dout_npad;
+    float *h;                            // [n * kt][Hpad] fp32
+    float *out;                          // [n][Dout] fp32
+};
+
 // ---- launchers ----------------------------------------------------------------
 hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep, int Dp, uint16_t *ws,
                                hipStream_t s);
@@ -196,5 +215,9 @@ hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const Gem
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
 // after a MODE_DOWN launch with ksplit > 1: y of each split tile += its partials, in range order
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s);
+// decode: logits, gating (one block per token), then the gated expert FFN of
+// each selected slot and the slot-order combine
+hipError_t launch_decode_route(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_decode_ffn(const DecodeArgs &a, hipStream_t s);
 
 }  // namespace moe

@@ -633,6 +633,75 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 }
 
 // ============================================================================
+// Decode routing (moe_ffn_forward!, src/llama2/inference.jl:62-66): one block
+// per token.  logits = W' xb (W [D][Er_pad] fp32: 256 / E threads per expert
+// sum chunks of D, the chunk sums added in chunk order), plus the bias; then
+// compute_gates with the recipe of route_kernel (TopKGating / SwitchGating).
+// ============================================================================
+__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float part[256];
+    __shared__ __attribute__((aligned(16))) float prow[MOE_MAX_EXPERTS + 8];
+    __shared__ float lrow[MOE_MAX_EXPERTS];
+    __shared__ float mx;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int E = a.E;
+    const float *x = a.x + (long long)t * a.D;
+    const int G = max(1, 256 / E);          // chunks of D per expert
+    const int CH = (a.D + G - 1) / G;
+    const int g = tid / E, e = tid - g * E;
+    if (g < G) {
+        float sacc = 0.0f;
+        const int d1 = min(a.D, (g + 1) * CH);
+        for (int d = g * CH; d < d1; ++d) sacc = sacc + x[d] * a.wr[(long long)d * a.Er_pad + e];
+        part[tid] = sacc;
+    }
+    __syncthreads();
+    if (tid < E) {
+        float v = part[tid];
+        for (int q = 1; q < G; ++q) v = v + part[q * E + tid];
+        if (a.br) v = v + a.br[tid];
+        lrow[tid] = v;
+        a.logits[(long long)t * E + tid] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {  // max, NaN ignored, first of equals kept
+        float m = -INFINITY;
+        for (int i = 0; i < E; ++i)
+            if (lrow[i] > m) m = lrow[i];
+        mx = m;
+    }
+    __syncthreads();
+    if (tid < E) {
+        const float m = mx, v = lrow[tid];
+        prow[tid] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < E; ++i) s = s + prow[i];  // expert order
+        for (int i = 0; i < E; ++i) {
+            prow[i] = prow[i] / s;
+            a.probs[(long long)t * E + i] = prow[i];
+        }
+        int sel[MOE_MAX_TOPK];
+        float gg[MOE_MAX_TOPK];
+        topk_row(prow, E, a.k, sel, gg);
+        for (int j = 0; j < a.k; ++j) {
+            a.idx[(long long)t * a.kt + j] = sel[j] + 1;
+            a.gates[(long long)t * a.kt + j] = gg[j];
+        }
+    }
+}
+
+hipError_t launch_decode_route(const DecodeArgs &a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    if (a.E < 1 || a.E > MOE_MAX_EXPERTS || a.k < 1 || a.k > MOE_MAX_TOPK || a.k > a.E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(decode_route_kernel, dim3(a.n), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ============================================================================
 // Scan: one block.  Per-expert totals, capacity clamp, offsets, per-block rank
 // bases, the (expert, m0) GEMM tile list and the loss scalars.
 // ============================================================================

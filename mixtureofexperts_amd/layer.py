@@ -182,6 +182,29 @@ class MoELayer:
         return output, loss
 
 
+def moe_ffn_forward(moe, xb):
+    """moe_ffn_forward! -- src/llama2/inference.jl:58-121, the decode caller,
+    on this layer's router and gated experts, after the caller's rmsnorm and
+    without shared experts.  Each token is routed on its own (logits =
+    W_router' xb, compute_gates) and its experts are combined in slot order:
+    xb2 = 0; xb2 += gate_s * gated_expert_forward!(xb) for s = 1..k, with
+    silu(g) = g * (1 / (1 + exp(-g))) (:154-167).
+
+    xb: (input_dim,) or (input_dim, n) float32.  Returns (xb2 of the same
+    shape, selected_experts (k[, n]) Int64 1-based, expert_gates (k[, n])
+    Float32)."""
+    xa = np.asarray(xb, dtype=np.float32)
+    vec = xa.ndim == 1
+    X = xa.reshape(-1, 1) if vec else xa
+    if X.ndim != 2 or X.shape[0] != moe.config.input_dim:
+        raise _lib.MoeError(_lib.MOE_EINVAL, f"xb must be ({moe.config.input_dim},) or ({moe.config.input_dim}, n)")
+    dev = moe._dev if moe._dev is not None else moe.sync_weights()
+    out, _, idx, gates = dev.decode(np.ascontiguousarray(X.T))
+    if vec:
+        return out[0], idx[0].astype(np.int64), gates[0]
+    return out.T, idx.T.astype(np.int64), gates.T
+
+
 def reset_stats(moe):
     """reset_stats!(moe) -- src/core/moe_layer.jl:271-276."""
     moe.training_stats["tokens_per_expert"][:] = 0

@@ -243,6 +243,44 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
     return out, loss, aux
 
 
+# ---- decode caller ------------------------------------------------------------
+
+def silu_inline(x):
+    """The decode path's inline silu, g * (1 / (1 + exp(-g))) in Float32
+    (src/llama2/inference.jl:160)."""
+    x = np.asarray(x, np.float32)
+    return (x * (np.float32(1) / (np.float32(1) + np.exp(-x)))).astype(np.float32)
+
+
+def decode_ffn(xb_nD, router_w_ED, experts, *, gate="topk", k=2, router_bias=None, logits=None):
+    """moe_ffn_forward! (src/llama2/inference.jl:58-121) after its rmsnorm and
+    without shared experts, for n tokens each routed on its own: logits =
+    W_router' xb (:63), compute_gates (:65-66), then xb2 = 0 and, slot by slot
+    in order, xb2 += gate * gated_expert_forward!(xb) (:83-104, :154-167).
+
+    xb_nD: [n][D] float32; router_w_ED: (E, D); experts: dicts of fp32 "w1",
+    "w3" (H, D) and "w2" (D, H) in (out, in) shape.  ``logits`` may be given
+    to route identical logits.  Returns (out [n][Dout], idx, gates, logits)."""
+    x = np.asarray(xb_nD, np.float32)
+    if logits is None:
+        logits = (x @ np.asarray(router_w_ED, np.float32).T).astype(np.float32)
+        if router_bias is not None:
+            logits = (logits + router_bias).astype(np.float32)
+    idx, gates, _ = compute_gates_topk(logits, 1 if gate == "switch" else k)
+    n, kt = idx.shape
+    Dout = experts[0]["w2"].shape[0]
+    out = np.zeros((n, Dout), np.float32)
+    for j in range(kt):  # slot order
+        for e in range(len(experts)):
+            toks = np.nonzero(idx[:, j] == e + 1)[0]
+            if toks.size == 0:
+                continue
+            ex = experts[e]
+            y = gated_expert(x[toks], ex["w1"], ex["w2"], ex["w3"], silu_inline)
+            out[toks] = (out[toks] + (gates[toks, j][:, None] * y).astype(np.float32)).astype(np.float32)
+    return out, idx, gates, logits
+
+
 # ---- dtype helpers used by tests and the bench ------------------------------
 
 def f32_to_bf16_bits(a):

@@ -1,0 +1,122 @@
+"""GPU parity of the decode caller (moe_ffn_forward!, src/llama2/inference.jl:58-121)
+through the C ABI (moe_decode) against the oracle's restatement
+(oracle.decode_ffn) on identical seeded inputs.
+
+C2 shapes (stories42M MoE layer: D=512, H=1376, E=8, k=2, fp32).  Routing is
+compared bit-exactly on the GPU's own logits (the logits themselves against
+fp32 x W'); the output (slot-order combine) within 1e-4 relative at fp32
+weights, 2e-2 at bf16, 5e-2 at fp8; two runs are bitwise identical."""
+import numpy as np
+import pytest
+
+from test_gpu_layer import Case, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "bf16": 2e-2, "fp8": 5e-2}
+
+
+def check_decode(case, oracle, n, tol):
+    x = np.ascontiguousarray(case.x[:n])
+    print(f"decode n={n} E={case.E} k={case.k} gate={case.gate}", flush=True)
+    out, logits, idx, gates = case.dev.decode(x)
+    out2, _, _, _ = case.dev.decode(x)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32)), "not deterministic"
+    assert np.all(np.isfinite(out))
+    ref_logits = (x.astype(np.float64) @ case.wr.T.astype(np.float64))
+    assert np.max(np.abs(logits - ref_logits)) <= 1e-5 * max(1.0, float(np.max(np.abs(ref_logits))))
+    ref, ridx, rgates, _ = oracle.decode_ffn(x, case.wr, case.ex, gate=case.gate, k=case.k, logits=logits)
+    assert np.array_equal(idx, ridx)
+    assert np.array_equal(gates.view(np.uint32), rgates.view(np.uint32))
+    err = rel_err(out, ref)
+    assert err <= tol, f"relative error {err:.3e} > {tol}"
+    return out, idx, gates
+
+
+@pytest.mark.parametrize("n", [1, 8])
+def test_decode_c2_fp32(moe, oracle, n):
+    c = Case(moe, oracle, T=8, D=512, H=1376, E=8, k=2, wdtype="f32", seed=21)
+    try:
+        check_decode(c, oracle, n, TOL["f32"])
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "fp8"])
+def test_decode_low_precision_weights(moe, oracle, wdtype):
+    c = Case(moe, oracle, T=8, D=512, H=1376, E=8, k=2, wdtype=wdtype, seed=22)
+    try:
+        check_decode(c, oracle, 3, TOL[wdtype])
+    finally:
+        c.dev.close()
+
+
+def test_decode_switch_and_wide(moe, oracle):
+    # SwitchGating (gate exactly 1.0f0) over 64 experts, D not a multiple of 64
+    c = Case(moe, oracle, T=6, D=200, H=300, E=64, k=1, gate="switch", wdtype="f32", seed=23)
+    try:
+        _, _, gates = check_decode(c, oracle, 6, TOL["f32"])
+        assert np.all(gates == np.float32(1.0))
+    finally:
+        c.dev.close()
+
+
+def test_decode_slot_order_differs_from_layer_only_by_rounding(moe, oracle):
+    # the layer forward combines in expert order with the NNlib silu, the decode
+    # caller in slot order with the inline silu: equal up to fp32 rounding
+    c = Case(moe, oracle, T=4, D=512, H=1376, E=8, k=2, wdtype="f32", seed=24)
+    try:
+        out_dec, _, _, _ = c.dev.decode(np.ascontiguousarray(c.x[:4]))
+        out_fwd, _, _ = c.run(training=False, T=4)
+        assert rel_err(out_dec, out_fwd) <= 1e-5
+    finally:
+        c.dev.close()
+
+
+def test_decode_unsupported_and_bad_args(moe, oracle):
+    from mixtureofexperts_amd import _lib
+
+    c = Case(moe, oracle, T=4, D=64, H=128, E=8, k=2, expert_type="standard", act="gelu", wdtype="f32", seed=25)
+    try:
+        x = np.ascontiguousarray(c.x[:2])
+        with pytest.raises(_lib.MoeError) as ei:
+            c.dev.decode(x)
+        assert ei.value.status == _lib.MOE_EUNSUPPORTED
+    finally:
+        c.dev.close()
+    c = Case(moe, oracle, T=4, D=64, H=128, E=10, k=2, gate="shared", ns=2, wdtype="f32", seed=26)
+    try:
+        with pytest.raises(_lib.MoeError) as ei:
+            c.dev.decode(np.ascontiguousarray(c.x[:2]))
+        assert ei.value.status == _lib.MOE_EUNSUPPORTED
+    finally:
+        c.dev.close()
+    c = Case(moe, oracle, T=4, D=64, H=128, E=8, k=2, wdtype="f32", seed=27)
+    try:
+        with pytest.raises(_lib.MoeError) as ei:
+            c.dev.decode(np.zeros((5, 64), np.float32))  # n > max_tokens
+        assert ei.value.status == _lib.MOE_EINVAL
+    finally:
+        c.dev.close()
+
+
+def test_decode_python_api(moe, oracle):
+    # moe_ffn_forward(layer, xb) on a vector and on a (D, n) matrix
+    rng = np.random.default_rng(28)
+    cfg = moe.MoEConfig(num_experts=8, expert_type="gated", input_dim=512, hidden_dim=1376, output_dim=512,
+                        activation=moe.silu, gate_type=moe.TopKGating(2), max_tokens=16)
+    layer = moe.MoELayer(cfg, rng=rng)
+    try:
+        xb = rng.standard_normal(512).astype(np.float32)
+        y, sel, g = moe.moe_ffn_forward(layer, xb)
+        assert y.shape == (512,) and sel.shape == (2,) and sel.dtype == np.int64 and g.shape == (2,)
+        ex = [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]
+        ref, ridx, rg, _ = oracle.decode_ffn(xb[None, :], layer.router.weight, ex, k=2)
+        assert np.array_equal(sel, ridx[0].astype(np.int64))
+        assert rel_err(y, ref[0]) <= 1e-4
+        X = rng.standard_normal((512, 5)).astype(np.float32)
+        Y, S, G = moe.moe_ffn_forward(layer, X)
+        assert Y.shape == (512, 5) and S.shape == (2, 5) and G.shape == (2, 5)
+        assert np.allclose(Y[:, 0], moe.moe_ffn_forward(layer, X[:, 0])[0], rtol=0, atol=0)
+    finally:
+        layer.close()

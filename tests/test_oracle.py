@@ -321,3 +321,64 @@ def test_fp8_table_and_quantiser(oracle):
     # each row's max maps to code 448 (up to the rounding of the fp32 scale)
     assert np.all(np.abs(q & 0x7F).max(axis=1) == 0x7E)
     assert np.allclose(np.abs(deq).max(axis=1), np.abs(w).max(axis=1), rtol=1e-6, atol=0)
+
+
+def _decode_case(seed, n=6, D=48, H=80, E=8):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, D)).astype(np.float32)
+    wr = (rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)
+    ex = [dict(w1=(rng.standard_normal((H, D)) * 0.2).astype(np.float32),
+               w2=(rng.standard_normal((D, H)) * 0.2).astype(np.float32),
+               w3=(rng.standard_normal((H, D)) * 0.2).astype(np.float32)) for _ in range(E)]
+    return x, wr, ex
+
+
+def test_decode_ffn_matches_float64_loop(oracle):
+    # moe_ffn_forward! restated as plain fp64 loops: per token, per slot in order,
+    # xb2 += gate * w2 (silu(w1 xb) .* (w3 xb))
+    x, wr, ex = _decode_case(40)
+    out, idx, gates, logits = oracle.decode_ffn(x, wr, ex, k=2)
+    for t in range(x.shape[0]):
+        acc = np.zeros(x.shape[1])
+        for j in range(idx.shape[1]):
+            e = ex[idx[t, j] - 1]
+            g = e["w1"].astype(np.float64) @ x[t]
+            u = e["w3"].astype(np.float64) @ x[t]
+            h = g / (1.0 + np.exp(-g)) * u
+            acc += float(gates[t, j]) * (e["w2"].astype(np.float64) @ h)
+        assert np.max(np.abs(out[t] - acc)) <= 1e-5 * max(1.0, np.max(np.abs(acc)))
+    ref_idx, ref_g, _ = oracle.compute_gates_topk((x @ wr.T).astype(np.float32), 2)
+    assert np.array_equal(idx, ref_idx) and np.array_equal(gates, ref_g)
+
+
+def test_decode_ffn_k1_is_the_expert(oracle):
+    # SwitchGating: gate 1.0f0, so xb2 = 0 + 1 * y is the selected expert's output exactly
+    x, wr, ex = _decode_case(41)
+    out, idx, gates, _ = oracle.decode_ffn(x, wr, ex, gate="switch")
+    assert np.all(gates == np.float32(1.0))
+    for e in range(len(ex)):
+        toks = np.nonzero(idx[:, 0] == e + 1)[0]
+        if toks.size:  # the same token batch, so the same sgemm blocking
+            y = oracle.gated_expert(x[toks], ex[e]["w1"], ex[e]["w2"], ex[e]["w3"], oracle.silu_inline)
+            assert np.array_equal(out[toks], y)
+
+
+def test_decode_ffn_combines_in_slot_order(oracle):
+    # k = 3 with logits that put the experts in slots (6, 2, 4): the fp32 sum
+    # ((0 + g1 y6) + g2 y2) + g3 y4 is the result, which expert order would not give
+    x, wr, ex = _decode_case(42, n=1)
+    logits = np.full((1, 8), -5.0, np.float32)
+    logits[0, 5], logits[0, 1], logits[0, 3] = 3.0, 2.9, 2.8
+    out, idx, gates, _ = oracle.decode_ffn(x, wr, ex, k=3, logits=logits)
+    assert list(idx[0]) == [6, 2, 4]
+    ys = [oracle.gated_expert(x, ex[e - 1]["w1"], ex[e - 1]["w2"], ex[e - 1]["w3"], oracle.silu_inline)[0]
+          for e in idx[0]]
+    slot = np.zeros_like(ys[0])
+    for j in range(3):
+        slot = (slot + gates[0, j] * ys[j]).astype(np.float32)
+    assert np.array_equal(out[0], slot)
+    order = np.argsort(idx[0])
+    expert = np.zeros_like(ys[0])
+    for j in order:
+        expert = (expert + gates[0, j] * ys[j]).astype(np.float32)
+    assert not np.array_equal(slot, expert)  # the case distinguishes the two orders
