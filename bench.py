@@ -36,6 +36,12 @@ CONFIGS = {
                    workload="switch-k1-moe-layer"),
     "readme": dict(T=32, D=512, H=2048, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="f32",
                    workload="readme-moe-layer"),
+    # the decode caller (moe_ffn_forward!) of a stories42M-shaped
+    # Llama2 with layers 2, 4, 6 converted to 8 gated experts, top-2, fp32; a step
+    # is one token through the three MoE FFNs (the caller's attention and norms
+    # are not part of this path)
+    "stories42m-decode": dict(T=1, D=512, H=1376, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="f32",
+                              layers=3, workload="stories42m-moe-decode"),
 }
 
 
@@ -165,6 +171,98 @@ def measured_traffic(cfg):
         return None
 
 
+def bench_decode(args, cfg):
+    """The decode caller: one token at a time through cfg["layers"] MoE FFNs
+    (moe_decode_async, n = 1), each layer's output the next one's input.
+    Weight-bandwidth bound: per call the k selected experts' three fp32
+    matrices and the router weight are read."""
+    import numpy as np
+    import torch
+
+    from mixtureofexperts_amd import _lib
+    from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+    D, H, E, k, NL = cfg["D"], cfg["H"], cfg["E"], cfg["k"], cfg["layers"]
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4321)
+    layers, host = [], []
+    for _ in range(NL):
+        dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED, input_dim=D, hidden_dim=H, output_dim=D,
+                          activation=_lib.MOE_ACT_SILU, gate=GateSpec(_lib.MOE_GATE_TOPK, k, 0),
+                          weight_dtype=_lib.MOE_F32, balance_alpha=0.01, z_loss_weight=0.001, capacity_factor=1.25,
+                          drop_tokens=False, max_tokens=1)
+        wr = torch.randn(E, D, generator=gen, device="cuda") * (1.0 / D ** 0.5)
+        wr_mem = wr.t().contiguous()
+        _lib.check(_lib.lib().moe_set_router(dev.h, wr_mem.data_ptr(), None), dev.h)
+        ex = []
+        for e in range(E):
+            w1, w2, w3 = [(torch.randn(*shp, generator=gen, device="cuda") * (2.0 / shp[1]) ** 0.5).contiguous()
+                          for shp in [(H, D), (D, H), (H, D)]]
+            _lib.check(_lib.lib().moe_set_expert(dev.h, e, _lib.MOE_LAYOUT_FLUX_OUT_IN, _lib.MOE_F32, w1.data_ptr(),
+                                                 w2.data_ptr(), w3.data_ptr(), None, None, None, None, None), dev.h)
+            ex.append(dict(w1=w1, w2=w2, w3=w3))
+        torch.cuda.synchronize()
+        layers.append(dev)
+        host.append((wr, ex))
+    L = _lib.lib()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    bufs = [torch.randn(D, generator=gen, device="cuda") for _ in range(NL + 1)]
+
+    def step():
+        for i, dev in enumerate(layers):
+            _lib.check(L.moe_decode_async(dev.h, bufs[i].data_ptr(), 1, bufs[i + 1].data_ptr(), sp), dev.h)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    call_ms = e0.elapsed_time(e1) / (args.steps * NL)
+    assert bool(torch.isfinite(bufs[-1]).all()), "non-finite output"
+    call_bytes = k * 3 * D * H * 4 + D * E * 4
+    achieved = call_bytes / (call_ms * 1e-3) / 1e9
+    line = {
+        "metric": "decode tokens/s at 1 GPU, stories42M MoE (3 MoE FFNs, top-2 of 8 gated experts); "
+                  "% of HBM roofline",
+        "value": round(args.steps / elapsed, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg["workload"], "tokens_per_step": 1, "moe_layers": NL, "d_model": D,
+                   "d_expert_hidden": H, "experts": E, "top_k": k, "weights": "f32"},
+        "roofline": {"bound": "hbm", "kernel": "moe_decode (routing + gated-expert matrix-vector products)",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+        "ms_per_moe_call": round(call_ms, 5),
+    }
+    if not args.no_cpu_baseline:
+        from oracle import moe_oracle as oracle
+
+        hl = [(wr.cpu().numpy(), [{n: v.cpu().numpy() for n, v in e.items()} for e in ex]) for wr, ex in host]
+        x = bufs[0].cpu().numpy()[None, :]
+        n_tok = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 5.0:  # bounded sample: about 5 s of CPU work
+            y = x
+            for wr, ex in hl:
+                y = oracle.decode_ffn(y, wr, ex, k=k)[0]
+            n_tok += 1
+        t = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": n_tok / t, "unit": "tokens/s", "cores": 1, "kind": "port",
+                                "sample": f"{n_tok} tokens through the {NL} MoE FFNs (oracle decode_ffn: fp32 "
+                                          f"router, gating, numpy fp32 expert matrix-vector products), {t:.2f} s"}
+    print(json.dumps(line), flush=True)
+    for dev in layers:
+        dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,6 +281,8 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+    if "layers" in CONFIGS[args.config]:
+        return bench_decode(args, CONFIGS[args.config])
 
     import numpy as np
     import torch

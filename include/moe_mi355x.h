@@ -191,8 +191,8 @@ int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *los
 int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T,
                       int32_t training, float *out_dev, float *loss_dev, void *stream);
 
-/* moe_decode on device buffers: xb_dev [n][D] fp32, out_dev [n][D_out] fp32.
- * Runs on `stream` (hipStream_t). */
+/* moe_decode on device buffers: xb_dev [n][D] fp32 (16-byte aligned),
+ * out_dev [n][D_out] fp32.  Runs on `stream` (hipStream_t). */
 int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_dev, void *stream);
 
 /* Stage-level entry points for profiling: together they issue exactly the

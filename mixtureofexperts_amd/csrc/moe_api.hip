@@ -854,8 +854,7 @@ static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_de
     a.Dpad = h->D_pad; a.H = h->H; a.Hpad = h->H_pad; a.Dout = h->Dout;
     a.s1 = h->s1; a.s3 = h->s3; a.s2 = h->s2; a.Dout_npad = h->Dout_npad;
     a.h = (float *)h->hbuf; a.out = out_dev;
-    HIP_TRY(h, launch_decode_route(a, s));
-    HIP_TRY(h, launch_decode_ffn(a, s));
+    HIP_TRY(h, launch_decode_ffn(a, h->ncu, s));
     h->last_T = -1;  // the routing buffers no longer describe a layer forward
     return MOE_OK;
 }
@@ -886,6 +885,7 @@ int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_d
     int r = decode_check(h, n);
     if (r != MOE_OK) return r;
     if (!xb_dev || !out_dev) return fail(h, MOE_EINVAL, "null buffer");
+    if ((uintptr_t)xb_dev & 15) return fail(h, MOE_EINVAL, "xb_dev must be 16-byte aligned");
     return decode_locked(h, xb_dev, n, out_dev, stream ? (hipStream_t)stream : h->stream);
 }
 

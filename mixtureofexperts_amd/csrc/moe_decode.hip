@@ -2,22 +2,28 @@
 // src/llama2/inference.jl:58-121): one token at a time (or n independent
 // tokens), its k selected gated experts as matrix-vector products, combined
 // in slot order.  Weight-bandwidth bound: every selected expert's three
-// matrices are read once per token.
+// matrices are read once per token; two kernels per call.
 //
-//   decode_up_kernel   : h_s = silu(W1_e xb) .* (W3_e xb) for slot s (expert e),
+//   decode_up_kernel   : the token's routing (logits = W' xb + b, softmax,
+//                        top-k, gates; inference.jl:62-66), recomputed by every
+//                        block from the L2-resident router, then for the
+//                        block's share of the (slot, row) units
+//                        h_s = silu(W1_e xb) .* (W3_e xb),
 //                        silu(g) = g * (1 / (1 + exp(-g)))   (inference.jl:154-167)
 //   decode_down_kernel : out = ((0 + g_1 y_1) + g_2 y_2) + ...,  y_s = W2_e h_s
 //                                                             (inference.jl:83-104)
 //
 // The weights are the handle's packed [E][Npad][Kpad] rows (K contiguous), fp32,
-// bf16 or fp8-e4m3 with per-row scales.  A wave computes one row's dot product:
-// lane l takes elements 4 l, 4 l + 256, ... and the 64 partial sums are added
-// by a fixed butterfly, so results are deterministic.
+// bf16 or fp8-e4m3 with per-row scales.  A wave computes whole dot products:
+// lane l takes the 4-element chunks l, l + 64, ... of the row, in that order,
+// and the 64 partial sums are added by a fixed butterfly, so every result is
+// deterministic.  All of a batch's loads are issued before its products
+// (clamped addresses, out-of-row chunks selected to zero).
 #include "moe_internal.h"
 
 namespace moe {
 
-// 4 consecutive weights of row `row` (element offset `o`, a multiple of 4) as fp32
+// 4 consecutive weights (element offset `o`, a multiple of 4) as fp32
 template <int WT>
 __device__ __forceinline__ float4 load_w4(const void *w, long long o) {
     if constexpr (WT == WT_F32) {
@@ -33,93 +39,388 @@ __device__ __forceinline__ float4 load_w4(const void *w, long long o) {
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+__device__ __forceinline__ float readlane_f(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane row in a fixed order, every lane of the row ending
+// with the same bits: pairs (quad_perm 1,0,3,2), quads (quad_perm 2,3,0,1),
+// 8-lane halves (row_half_mirror), rows (row_mirror); additions commute
+// exactly, so partner lanes hold identical values after every step.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = v + dpp_f<0xb1>(v);
+    v = v + dpp_f<0x4e>(v);
+    v = v + dpp_f<0x141>(v);
+    v = v + dpp_f<0x140>(v);
     return v;
 }
 
-// dot(W row starting at element `row0`, v[0..n)), n a multiple of 4; v fp32
-template <int WT>
-__device__ __forceinline__ float dot_row(const void *w, long long row0, const float *v, int n, int lane) {
-    float acc = 0.0f;
-    for (int i = lane * 4; i < n; i += 256) {
-        const float4 a = load_w4<WT>(w, row0 + i);
-        const float4 b = *(const float4 *)(v + i);
-        acc = acc + a.x * b.x;
-        acc = acc + a.y * b.y;
-        acc = acc + a.z * b.z;
-        acc = acc + a.w * b.w;
-    }
-    return wave_sum(acc);
+// Wave sum (all 64 lanes active), uniform result: row sums, then the four rows
+// in row order.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    return ((readlane_f(v, 0) + readlane_f(v, 16)) + readlane_f(v, 32)) + readlane_f(v, 48);
 }
 
-// Block (token * kt + slot, row group): 4 waves, one h row each, over all
-// Hpad rows (pad rows have zero weights, so their h is 0 and the down
-// products may run over Hpad).
+__device__ __forceinline__ float4 zero_unless(bool v, float4 a) {
+    return v ? a : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+__device__ __forceinline__ float dot4_acc(float acc, float4 a, float4 b) {
+#pragma clang fp contract(off)
+    acc = acc + a.x * b.x;
+    acc = acc + a.y * b.y;
+    acc = acc + a.z * b.z;
+    acc = acc + a.w * b.w;
+    return acc;
+}
+
+// ---- routing of one token by a 256-thread block --------------------------------
+struct DecodeRouteLds {
+    __attribute__((aligned(16))) float part[4][MOE_MAX_EXPERTS];  // per-wave logit partials
+};
+
+// compute_gates of token t from the wave partials in L (see decode_route_block);
+// HI: E > 64, lane l also holds expert l + 64.
+template <bool HI>
+__device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, int t, bool write,
+                                                           const DecodeRouteLds &L) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, E = a.E;
+    constexpr int NH = HI ? 2 : 1;
+    float lg[NH], ev[NH], pv[NH];
+    uint32_t key[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        const int e = lane + 64 * h;
+        const int ec = min(e, a.Er_pad - 1);
+        float v = ((L.part[0][ec] + L.part[1][ec]) + L.part[2][ec]) + L.part[3][ec];
+        if (a.br) v = v + a.br[min(e, E - 1)];
+        lg[h] = v;
+    }
+    // lane i & 63 of half i >> 6
+#define MOE_LANE_OF(arr, i) (NH == 1 ? (arr)[0] : ((i) < 64 ? (arr)[0] : (arr)[NH - 1]))
+    float m = -INFINITY;                                // max, NaN ignored
+    for (int i0 = 0; i0 < E; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, E - 1);
+            v[u] = readlane_f(MOE_LANE_OF(lg, i), i & 63);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) m = (i0 + u < E) ? fmaxf(m, v[u]) : m;
+    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+        ev[h] = (m == INFINITY) ? ((lg[h] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(lg[h] - m));
+    float s = 0.0f;                                     // expert order
+    for (int i0 = 0; i0 < E; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, E - 1);
+            v[u] = readlane_f(MOE_LANE_OF(ev, i), i & 63);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s = (i0 + u < E) ? s + v[u] : s;
+    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        pv[h] = ev[h] / s;
+        key[h] = (lane + 64 * h < E) ? isless_key(pv[h]) : 0u;
+    }
+    int rank[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) rank[h] = 0;
+    for (int i0 = 0; i0 < E; i0 += 8) {
+        uint32_t kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, E - 1);
+            kv[u] = (uint32_t)__builtin_amdgcn_readlane((int)MOE_LANE_OF(key, i), i & 63);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const int e = lane + 64 * h;
+                rank[h] += (i < E && (kv[u] > key[h] || (kv[u] == key[h] && i < e))) ? 1 : 0;
+            }
+        }
+    }
+#undef MOE_LANE_OF
+    float ssum = 0.0f, myp = 0.0f;
+    int mye = 0;
+    unsigned long long packed = 0ull;
+    for (int j = 0; j < a.k; ++j) {
+        const unsigned long long b0 = __ballot(lane < E && rank[0] == j);
+        const unsigned long long b1 = HI ? __ballot(lane + 64 < E && rank[NH - 1] == j) : 0ull;
+        const int e = b0 ? __builtin_ctzll(b0) : 64 + __builtin_ctzll(b1);
+        const float pj = readlane_f(HI && e >= 64 ? pv[NH - 1] : pv[0], e & 63);
+        ssum = (j == 0) ? pj : ssum + pj;  // slot order
+        packed |= (unsigned long long)e << (8 * j);
+        if (lane == j) {
+            myp = pj;
+            mye = e;
+        }
+    }
+    if (write) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const int e = lane + 64 * h;
+            if (e < E) {
+                a.logits[(long long)t * E + e] = lg[h];
+                a.probs[(long long)t * E + e] = pv[h];
+            }
+        }
+        if (lane < a.k) {
+            a.idx[(long long)t * a.kt + lane] = mye + 1;
+            a.gates[(long long)t * a.kt + lane] = myp / ssum;
+        }
+    }
+    return packed;
+}
+
+// Logits: lane (q, c) = q C + c of wave w sums x[d] W[d][4q..4q+3] over the
+// chunk g = w C + c of D in d order (one float4 per router row, 4 rows in
+// flight); the C chunks of a wave are added by a fixed tree (DPP steps within
+// 16-lane rows, then lane xor 16 and 32), the 4 wave sums in wave order, then
+// the bias.  Every wave then evaluates compute_gates on its own copy (identical
+// results, no second barrier) with the recipe of the layer's routing kernel:
+// m = max (NaN ignored), e_i = (float)exp((double)(l_i - m)) (a +Inf maximum
+// gives 1 at the +Inf logits, 0 elsewhere), the sum in expert order, p_i = e_i
+// / sum; top-k by the isless key descending, lower index first among equal
+// keys (partialsortperm(p, 1:k, rev=true)): the rank of expert i is the number
+// of experts before it in that order; the gates are p of the slots over their
+// sum in slot order.  Lane l holds experts l and, for E > 64, l + 64.
+// Returns the 0-based expert of slot j in bits [8 j, 8 j + 8) (uniform);
+// `write` (wave 0 of one block per token) stores logits, probs, indices, gates.
+__device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int E = a.E, Q = a.Er_pad >> 2;               // router row: Q float4 (Er_pad % 8 == 0)
+    int QP = 1;
+    while (QP < Q) QP <<= 1;                            // Q <= 32
+    const int C = 64 / QP;                              // chunks per wave
+    const int q = lane / C, c = lane - q * C;
+    const int CH = (a.D + 4 * C - 1) / (4 * C);
+    const float *x = a.x + (long long)t * a.D;
+    const float4 *wr4 = (const float4 *)a.wr;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    {
+        const int d0 = (w * C + c) * CH, d1 = min(a.D, d0 + CH);
+        const int qq = min(q, Q - 1);
+        for (int d = d0; d < d1; d += 4) {
+            float xv[4];
+            float4 wv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int dd = min(d + u, d1 - 1);
+                xv[u] = x[dd];
+                wv[u] = wr4[(long long)dd * Q + qq];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (d + u < d1) {
+                    acc.x = acc.x + xv[u] * wv[u].x;
+                    acc.y = acc.y + xv[u] * wv[u].y;
+                    acc.z = acc.z + xv[u] * wv[u].z;
+                    acc.w = acc.w + xv[u] * wv[u].w;
+                }
+        }
+    }
+    // groups of C contiguous lanes: every lane of a group ends with the same sum
+    if (C >= 2) {
+        acc.x = acc.x + dpp_f<0xb1>(acc.x); acc.y = acc.y + dpp_f<0xb1>(acc.y);
+        acc.z = acc.z + dpp_f<0xb1>(acc.z); acc.w = acc.w + dpp_f<0xb1>(acc.w);
+    }
+    if (C >= 4) {
+        acc.x = acc.x + dpp_f<0x4e>(acc.x); acc.y = acc.y + dpp_f<0x4e>(acc.y);
+        acc.z = acc.z + dpp_f<0x4e>(acc.z); acc.w = acc.w + dpp_f<0x4e>(acc.w);
+    }
+    if (C >= 8) {
+        acc.x = acc.x + dpp_f<0x141>(acc.x); acc.y = acc.y + dpp_f<0x141>(acc.y);
+        acc.z = acc.z + dpp_f<0x141>(acc.z); acc.w = acc.w + dpp_f<0x141>(acc.w);
+    }
+    if (C >= 16) {
+        acc.x = acc.x + dpp_f<0x140>(acc.x); acc.y = acc.y + dpp_f<0x140>(acc.y);
+        acc.z = acc.z + dpp_f<0x140>(acc.z); acc.w = acc.w + dpp_f<0x140>(acc.w);
+    }
+    for (int o = 16; o < C; o <<= 1) {
+        acc.x = acc.x + __shfl_xor(acc.x, o); acc.y = acc.y + __shfl_xor(acc.y, o);
+        acc.z = acc.z + __shfl_xor(acc.z, o); acc.w = acc.w + __shfl_xor(acc.w, o);
+    }
+    if (c == 0 && q < Q) *(float4 *)&L.part[w][4 * q] = acc;
+    __syncthreads();
+
+    return E > 64 ? decode_gates<true>(a, t, write, L) : decode_gates<false>(a, t, write, L);
+}
+
+// ---- up: block (token t, y) routes t, then its waves take units u = (slot,
+// row j) two at a time, u0 = 2 (y * 4 + wave), stepping 8 gridDim.y.  A unit
+// is the pair of dot products (W1_e row j) . x and (W3_e row j) . x over all
+// Hpad rows (pad rows have zero weights, so their h is 0 and the down products
+// may run over Hpad).
 template <int WT>
 __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
+    __shared__ DecodeRouteLds L;
+    const int t = blockIdx.x;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int ts = blockIdx.x;  // token * kt + slot
-    const int t = ts / a.kt;
-    const int j = blockIdx.y * 4 + w;
-    if (j >= a.Hpad) return;
-    const int e = a.idx[ts] - 1;
-    float hv = 0.0f;
-    if (e >= 0 && e < a.E) {
-        const float *x = a.x + (long long)t * a.D;
-        const long long r = (long long)e * a.w1_stride + (long long)j * a.Dpad;
-        float gt = dot_row<WT>(a.w1, r, x, a.D, lane);
-        float up = dot_row<WT>(a.w3, r, x, a.D, lane);
-        if (WT == WT_FP8) {
-            gt = gt * a.s1[(long long)e * a.Hpad + j];
-            up = up * a.s3[(long long)e * a.Hpad + j];
+    const unsigned long long sel = decode_route_block(a, t, blockIdx.y == 0 && w == 0, L);
+    const int units = a.kt * a.Hpad;
+    const int nch = a.D >> 2;  // 4-element chunks per row
+    const float4 *x4 = (const float4 *)(a.x + (long long)t * a.D);
+    for (int u0 = (blockIdx.y * 4 + w) * 2; u0 < units; u0 += gridDim.y * 8) {
+        const bool two = u0 + 1 < units;
+        const int u1 = two ? u0 + 1 : u0;
+        const int s0 = u0 / a.Hpad, j0 = u0 - s0 * a.Hpad;
+        const int s1 = u1 / a.Hpad, j1 = u1 - s1 * a.Hpad;
+        const int e0 = (int)((sel >> (8 * s0)) & 0xff), e1 = (int)((sel >> (8 * s1)) & 0xff);
+        const bool ok0 = e0 >= 0 && e0 < a.E, ok1 = e1 >= 0 && e1 < a.E;
+        const long long r0 = (long long)(ok0 ? e0 : 0) * a.w1_stride + (long long)j0 * a.Dpad;
+        const long long r1 = (long long)(ok1 ? e1 : 0) * a.w1_stride + (long long)j1 * a.Dpad;
+        float g0 = 0.0f, q0 = 0.0f, g1 = 0.0f, q1 = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += 128) {
+            const int c = c0 + lane;
+            const bool va = c < nch, vb = c + 64 < nch;
+            const int ca = min(c, nch - 1), cb = min(c + 64, nch - 1);
+            const float4 xa = x4[ca], xb = x4[cb];
+            const float4 ga0 = load_w4<WT>(a.w1, r0 + 4 * ca), gb0 = load_w4<WT>(a.w1, r0 + 4 * cb);
+            const float4 ua0 = load_w4<WT>(a.w3, r0 + 4 * ca), ub0 = load_w4<WT>(a.w3, r0 + 4 * cb);
+            const float4 ga1 = load_w4<WT>(a.w1, r1 + 4 * ca), gb1 = load_w4<WT>(a.w1, r1 + 4 * cb);
+            const float4 ua1 = load_w4<WT>(a.w3, r1 + 4 * ca), ub1 = load_w4<WT>(a.w3, r1 + 4 * cb);
+            const float4 xa_ = zero_unless(va, xa), xb_ = zero_unless(vb, xb);
+            g0 = dot4_acc(g0, zero_unless(va, ga0), xa_);
+            q0 = dot4_acc(q0, zero_unless(va, ua0), xa_);
+            g1 = dot4_acc(g1, zero_unless(va, ga1), xa_);
+            q1 = dot4_acc(q1, zero_unless(va, ua1), xa_);
+            g0 = dot4_acc(g0, zero_unless(vb, gb0), xb_);
+            q0 = dot4_acc(q0, zero_unless(vb, ub0), xb_);
+            g1 = dot4_acc(g1, zero_unless(vb, gb1), xb_);
+            q1 = dot4_acc(q1, zero_unless(vb, ub1), xb_);
         }
-        hv = (gt * (1.0f / (1.0f + expf(-gt)))) * up;
+        g0 = wave_sum(g0);
+        q0 = wave_sum(q0);
+        g1 = wave_sum(g1);
+        q1 = wave_sum(q1);
+        if (lane == 0) {
+            if (WT == WT_FP8) {
+                if (ok0) {
+                    g0 = g0 * a.s1[(long long)e0 * a.Hpad + j0];
+                    q0 = q0 * a.s3[(long long)e0 * a.Hpad + j0];
+                }
+                if (ok1) {
+                    g1 = g1 * a.s1[(long long)e1 * a.Hpad + j1];
+                    q1 = q1 * a.s3[(long long)e1 * a.Hpad + j1];
+                }
+            }
+            const long long hb = (long long)t * a.kt * a.Hpad;
+            a.h[hb + u0] = ok0 ? (g0 * (1.0f / (1.0f + expf(-g0)))) * q0 : 0.0f;
+            if (two) a.h[hb + u1] = ok1 ? (g1 * (1.0f / (1.0f + expf(-g1)))) * q1 : 0.0f;
+        }
     }
-    if (lane == 0) a.h[(long long)ts * a.Hpad + j] = hv;
 }
 
-// Block (token, row group): 4 waves, one output row each; the slots' products
-// are combined in slot order on a zero start.
-template <int WT>
-__global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
+// ---- down: one wave per output row i of token t; slots two at a time, U
+// chunks per lane and slot in flight (one batch covers rows of up to 256 U
+// elements); the first batch's h loads do not depend on the routing and are
+// issued before the slot's expert is read.  The slots' products are combined
+// in slot order on a zero start.
+template <int WT, int U>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_down_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int t = blockIdx.x;
-    const int i = blockIdx.y * 4 + w;
-    if (i >= a.Dout) return;
+    const int lane = threadIdx.x;
+    const int t = blockIdx.x, i = blockIdx.y;
+    const int nch = a.Hpad >> 2;
     float acc = 0.0f;
-    for (int s = 0; s < a.kt; ++s) {
-        const int ts = t * a.kt + s;
-        const int e = a.idx[ts] - 1;
-        if (e < 0 || e >= a.E) continue;
-        float y = dot_row<WT>(a.w2, (long long)e * a.w2_stride + (long long)i * a.Hpad, a.h + (long long)ts * a.Hpad,
-                              a.Hpad, lane);
-        if (WT == WT_FP8) y = y * a.s2[(long long)e * a.Dout_npad + i];
-        acc = acc + a.gates[ts] * y;
-    }
+    int s0 = 0;
+    do {  // kt >= 1
+        const bool two = s0 + 1 < a.kt;
+        const int ts0 = t * a.kt + s0, ts1 = two ? ts0 + 1 : ts0;
+        const float4 *h0 = (const float4 *)(a.h + (long long)ts0 * a.Hpad);
+        const float4 *h1 = (const float4 *)(a.h + (long long)ts1 * a.Hpad);
+        float4 ha[U], hb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = min(u * 64 + lane, nch - 1);
+            ha[u] = h0[c];
+            hb[u] = h1[c];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the wait for idx
+        const int e0 = a.idx[ts0] - 1, e1 = a.idx[ts1] - 1;
+        const bool ok0 = e0 >= 0 && e0 < a.E, ok1 = two && e1 >= 0 && e1 < a.E;
+        const long long r0 = (long long)(ok0 ? e0 : 0) * a.w2_stride + (long long)i * a.Hpad;
+        const long long r1 = (long long)(ok1 ? e1 : 0) * a.w2_stride + (long long)i * a.Hpad;
+        float y0 = 0.0f, y1 = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += 64 * U) {
+            float4 wa[U], wb[U];
+            if (c0 > 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = min(c0 + u * 64 + lane, nch - 1);
+                    ha[u] = h0[c];
+                    hb[u] = h1[c];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = min(c0 + u * 64 + lane, nch - 1);
+                wa[u] = load_w4<WT>(a.w2, r0 + 4 * c);
+                wb[u] = load_w4<WT>(a.w2, r1 + 4 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool v = c0 + u * 64 + lane < nch;
+                y0 = dot4_acc(y0, zero_unless(v, wa[u]), zero_unless(v, ha[u]));
+                y1 = dot4_acc(y1, zero_unless(v, wb[u]), zero_unless(v, hb[u]));
+            }
+        }
+        y0 = wave_sum(y0);
+        y1 = wave_sum(y1);
+        if (WT == WT_FP8) {
+            if (ok0) y0 = y0 * a.s2[(long long)e0 * a.Dout_npad + i];
+            if (ok1) y1 = y1 * a.s2[(long long)e1 * a.Dout_npad + i];
+        }
+        if (ok0) acc = acc + a.gates[ts0] * y0;
+        if (ok1) acc = acc + a.gates[ts1] * y1;
+        s0 += 2;
+    } while (s0 < a.kt);
     if (lane == 0) a.out[(long long)t * a.Dout + i] = acc;
 }
 
 template <int WT>
-static hipError_t launch_decode_wt(const DecodeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(decode_up_kernel<WT>, dim3(a.n * a.kt, (a.Hpad + 3) / 4), dim3(256), 0, s, a);
+static hipError_t launch_decode_wt(const DecodeArgs &a, int ncu, hipStream_t s) {
+    const int tasks = (a.kt * a.Hpad + 1) / 2;                  // unit pairs per token
+    const int gy = max(1, min((tasks + 3) / 4, max(1, 4 * ncu / a.n)));
+    hipLaunchKernelGGL(decode_up_kernel<WT>, dim3(a.n, gy), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_down_kernel<WT>, dim3(a.n, (a.Dout + 3) / 4), dim3(256), 0, s, a);
+    if (a.Hpad <= 1024)
+        hipLaunchKernelGGL((decode_down_kernel<WT, 4>), dim3(a.n, a.Dout), dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_down_kernel<WT, 8>), dim3(a.n, a.Dout), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_decode_ffn(const DecodeArgs &a, hipStream_t s) {
+hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
-    // rows are read 4 elements at a time: the padded strides are multiples of 64
-    if ((a.D & 3) || (a.Dpad & 3) || (a.Hpad & 3) || a.D > a.Dpad || a.H > a.Hpad) return hipErrorInvalidValue;
+    if (a.E < 1 || a.E > MOE_MAX_EXPERTS || a.k < 1 || a.k > MOE_MAX_TOPK || a.k > a.E || a.kt != a.k)
+        return hipErrorInvalidValue;
+    // rows are read 4 elements at a time
+    if (a.D < 4 || (a.D & 3) || (a.Dpad & 3) || (a.Hpad & 3) || a.D > a.Dpad || a.H > a.Hpad) return hipErrorInvalidValue;
+    if (((uintptr_t)a.x & 15) || ((uintptr_t)a.h & 15)) return hipErrorInvalidValue;
     switch (a.wt) {
-    case WT_F32: return launch_decode_wt<WT_F32>(a, s);
-    case WT_BF16: return launch_decode_wt<WT_BF16>(a, s);
-    default: return launch_decode_wt<WT_FP8>(a, s);
+    case WT_F32: return launch_decode_wt<WT_F32>(a, ncu, s);
+    case WT_BF16: return launch_decode_wt<WT_BF16>(a, ncu, s);
+    default: return launch_decode_wt<WT_FP8>(a, ncu, s);
     }
 }
 

@@ -62,6 +62,65 @@ __host__ __device__ inline uint32_t isless_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Top-k of a row p[0..n) by the isless key, descending, lower index first
+// among equal keys (partialsortperm(p, 1:k, rev=true)), in one pass: the k
+// best so far sit in slots 0..k-1 in order; an entry enters only with a key
+// strictly above the k-th, is inserted after the equal keys already there,
+// and the slots after it move down by one.  Gates: p of the slots over their
+// sum in slot order.  p is an LDS row, 16-byte aligned, readable up to n
+// rounded up to 4.
+template <int K>
+__device__ inline void topk_row_k(const float *__restrict__ p, int n, int *sel, float *g) {
+#pragma clang fp contract(off)
+    uint32_t kb[K];
+    int ib[K];
+    float vb[K];
+#pragma unroll
+    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0; vb[q] = 0.0f; }  // key 0: empty (below every float)
+    for (int i0 = 0; i0 < n; i0 += 4) {
+        const float4 v4 = *(const float4 *)(p + i0);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t ck = isless_key(vv[c]);
+            if (i0 + c < n && ck > kb[K - 1]) {
+                int ci = i0 + c;
+                float cv = vv[c];
+                bool shift = false;  // once inserted, every later slot moves down by one
+#pragma unroll
+                for (int q = 0; q < K; ++q) {
+                    const bool ins = shift || ck > kb[q];
+                    const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
+                    kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
+                    ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
+                    shift = ins;
+                }
+            }
+        }
+    }
+    float s = vb[0];
+#pragma unroll
+    for (int q = 1; q < K; ++q) s = s + vb[q];
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+        sel[q] = ib[q];
+        g[q] = vb[q] / s;
+    }
+}
+
+__device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *sel, float *g) {
+    switch (k) {
+    case 1: topk_row_k<1>(p, n, sel, g); break;
+    case 2: topk_row_k<2>(p, n, sel, g); break;
+    case 3: topk_row_k<3>(p, n, sel, g); break;
+    case 4: topk_row_k<4>(p, n, sel, g); break;
+    case 5: topk_row_k<5>(p, n, sel, g); break;
+    case 6: topk_row_k<6>(p, n, sel, g); break;
+    case 7: topk_row_k<7>(p, n, sel, g); break;
+    default: topk_row_k<8>(p, n, sel, g); break;
+    }
+}
+
 // ---- kernel argument blocks --------------------------------------------------
 
 // Router logits GEMM: x [T][D] (bf16 or fp32) times the router weight split
@@ -215,9 +274,8 @@ hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const Gem
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
 // after a MODE_DOWN launch with ksplit > 1: y of each split tile += its partials, in range order
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s);
-// decode: logits, gating (one block per token), then the gated expert FFN of
-// each selected slot and the slot-order combine
-hipError_t launch_decode_route(const DecodeArgs &a, hipStream_t s);
-hipError_t launch_decode_ffn(const DecodeArgs &a, hipStream_t s);
+// decode: routing fused into the gated up products of each selected slot, then
+// the down products and the slot-order combine (two kernels)
+hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s);
 
 }  // namespace moe

@@ -235,67 +235,6 @@ hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s) {
 // Gating.  One thread per token, 256 tokens per block.
 // ============================================================================
 
-// Top-k by the isless key, descending, lower index first on ties; then the
-// gates p_sel ./ sum(p_sel) with the sum in slot order.
-// Top-k of a row p[0..n) by the isless key, descending, lower index first
-// among equal keys (partialsortperm(p, 1:k, rev=true)), in one pass: the k
-// best so far sit in slots 0..k-1 in order; an entry enters only with a key
-// strictly above the k-th, is inserted after the equal keys already there,
-// and the slots after it move down by one.  Gates: p of the slots over their
-// sum in slot order.  p is an LDS row, 16-byte aligned, readable up to n
-// rounded up to 4.
-template <int K>
-__device__ inline void topk_row_k(const float *__restrict__ p, int n, int *sel, float *g) {
-#pragma clang fp contract(off)
-    uint32_t kb[K];
-    int ib[K];
-    float vb[K];
-#pragma unroll
-    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0; vb[q] = 0.0f; }  // key 0: empty (below every float)
-    for (int i0 = 0; i0 < n; i0 += 4) {
-        const float4 v4 = *(const float4 *)(p + i0);
-        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            uint32_t ck = isless_key(vv[c]);
-            if (i0 + c < n && ck > kb[K - 1]) {
-                int ci = i0 + c;
-                float cv = vv[c];
-                bool shift = false;  // once inserted, every later slot moves down by one
-#pragma unroll
-                for (int q = 0; q < K; ++q) {
-                    const bool ins = shift || ck > kb[q];
-                    const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
-                    kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
-                    ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
-                    shift = ins;
-                }
-            }
-        }
-    }
-    float s = vb[0];
-#pragma unroll
-    for (int q = 1; q < K; ++q) s = s + vb[q];
-#pragma unroll
-    for (int q = 0; q < K; ++q) {
-        sel[q] = ib[q];
-        g[q] = vb[q] / s;
-    }
-}
-
-__device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *sel, float *g) {
-    switch (k) {
-    case 1: topk_row_k<1>(p, n, sel, g); break;
-    case 2: topk_row_k<2>(p, n, sel, g); break;
-    case 3: topk_row_k<3>(p, n, sel, g); break;
-    case 4: topk_row_k<4>(p, n, sel, g); break;
-    case 5: topk_row_k<5>(p, n, sel, g); break;
-    case 6: topk_row_k<6>(p, n, sel, g); break;
-    case 7: topk_row_k<7>(p, n, sel, g); break;
-    default: topk_row_k<8>(p, n, sel, g); break;
-    }
-}
-
 // LDS row stride of the routing kernel for E rows: a multiple of 4 floats
 // (16 B) whose count of 16-byte units is odd, so that 16 token threads
 // reading 16 B at one column hit 16 distinct bank quads.
@@ -629,75 +568,6 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
         big_lds = true;
     }
     hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), lds, s, a);
-    return hipGetLastError();
-}
-
-// ============================================================================
-// Decode routing (moe_ffn_forward!, src/llama2/inference.jl:62-66): one block
-// per token.  logits = W' xb (W [D][Er_pad] fp32: 256 / E threads per expert
-// sum chunks of D, the chunk sums added in chunk order), plus the bias; then
-// compute_gates with the recipe of route_kernel (TopKGating / SwitchGating).
-// ============================================================================
-__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a) {
-#pragma clang fp contract(off)
-    __shared__ float part[256];
-    __shared__ __attribute__((aligned(16))) float prow[MOE_MAX_EXPERTS + 8];
-    __shared__ float lrow[MOE_MAX_EXPERTS];
-    __shared__ float mx;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const int E = a.E;
-    const float *x = a.x + (long long)t * a.D;
-    const int G = max(1, 256 / E);          // chunks of D per expert
-    const int CH = (a.D + G - 1) / G;
-    const int g = tid / E, e = tid - g * E;
-    if (g < G) {
-        float sacc = 0.0f;
-        const int d1 = min(a.D, (g + 1) * CH);
-        for (int d = g * CH; d < d1; ++d) sacc = sacc + x[d] * a.wr[(long long)d * a.Er_pad + e];
-        part[tid] = sacc;
-    }
-    __syncthreads();
-    if (tid < E) {
-        float v = part[tid];
-        for (int q = 1; q < G; ++q) v = v + part[q * E + tid];
-        if (a.br) v = v + a.br[tid];
-        lrow[tid] = v;
-        a.logits[(long long)t * E + tid] = v;
-    }
-    __syncthreads();
-    if (tid == 0) {  // max, NaN ignored, first of equals kept
-        float m = -INFINITY;
-        for (int i = 0; i < E; ++i)
-            if (lrow[i] > m) m = lrow[i];
-        mx = m;
-    }
-    __syncthreads();
-    if (tid < E) {
-        const float m = mx, v = lrow[tid];
-        prow[tid] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float s = 0.0f;
-        for (int i = 0; i < E; ++i) s = s + prow[i];  // expert order
-        for (int i = 0; i < E; ++i) {
-            prow[i] = prow[i] / s;
-            a.probs[(long long)t * E + i] = prow[i];
-        }
-        int sel[MOE_MAX_TOPK];
-        float gg[MOE_MAX_TOPK];
-        topk_row(prow, E, a.k, sel, gg);
-        for (int j = 0; j < a.k; ++j) {
-            a.idx[(long long)t * a.kt + j] = sel[j] + 1;
-            a.gates[(long long)t * a.kt + j] = gg[j];
-        }
-    }
-}
-
-hipError_t launch_decode_route(const DecodeArgs &a, hipStream_t s) {
-    if (a.n <= 0) return hipSuccess;
-    if (a.E < 1 || a.E > MOE_MAX_EXPERTS || a.k < 1 || a.k > MOE_MAX_TOPK || a.k > a.E) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(decode_route_kernel, dim3(a.n), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

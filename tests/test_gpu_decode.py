@@ -24,6 +24,8 @@ def check_decode(case, oracle, n, tol):
     assert np.array_equal(out.view(np.uint32), out2.view(np.uint32)), "not deterministic"
     assert np.all(np.isfinite(out))
     ref_logits = (x.astype(np.float64) @ case.wr.T.astype(np.float64))
+    if case.rb is not None:
+        ref_logits = ref_logits + np.asarray(case.rb, np.float64)
     assert np.max(np.abs(logits - ref_logits)) <= 1e-5 * max(1.0, float(np.max(np.abs(ref_logits))))
     ref, ridx, rgates, _ = oracle.decode_ffn(x, case.wr, case.ex, gate=case.gate, k=case.k, logits=logits)
     assert np.array_equal(idx, ridx)
@@ -57,6 +59,17 @@ def test_decode_switch_and_wide(moe, oracle):
     try:
         _, _, gates = check_decode(c, oracle, 6, TOL["f32"])
         assert np.all(gates == np.float32(1.0))
+    finally:
+        c.dev.close()
+
+
+def test_decode_many_experts(moe, oracle):
+    # E > 64: each lane of the routing wave holds two experts; k = 4 slots;
+    # with a router bias
+    rb = np.random.default_rng(30).standard_normal(96).astype(np.float32)
+    c = Case(moe, oracle, T=5, D=128, H=96, E=96, k=4, wdtype="f32", seed=29, router_bias=rb)
+    try:
+        check_decode(c, oracle, 5, TOL["f32"])
     finally:
         c.dev.close()
 
