@@ -79,7 +79,11 @@ typedef struct {
     float capacity_factor;      /* MoEConfig.capacity_factor */
     int32_t drop_tokens;        /* MoEConfig.drop_tokens */
     int32_t max_tokens;         /* largest T a call may pass (workspace size) */
-    int32_t reserved[7];        /* zero */
+    int32_t num_shared_experts; /* MoEConfig.num_shared_experts: experts 1..ns run on every
+                                   token (forward_with_shared_experts,
+                                   src/core/moe_layer.jl:158-185); the router then has
+                                   num_experts - ns outputs.  TopK / Switch gates only. */
+    int32_t reserved[6];        /* zero */
 } moe_config;
 
 typedef struct moe_handle moe_handle;
@@ -87,7 +91,7 @@ typedef struct moe_handle moe_handle;
 /* Optional per-call outputs of moe_forward (any pointer may be NULL). */
 typedef struct {
     float *logits;          /* [T][E_router] fp32 router logits */
-    float *probs;           /* [T][E] router probabilities */
+    float *probs;           /* [T][E_router] router probabilities */
     int32_t *indices;       /* [T][k_total] 1-based expert ids (0 = dropped) */
     float *gates;           /* [T][k_total] */
     int32_t *counts;        /* [E] entries per expert this call */
@@ -107,9 +111,12 @@ int moe_destroy(moe_handle *h);
 /* Last error message of h (or of the last failed moe_create when h is NULL). */
 const char *moe_last_error(const moe_handle *h);
 int moe_abi_version(void);
-/* Number of router outputs: E for TopK/Switch/Shared gating. */
+/* Number of router outputs: E for TopK/Switch/Shared gating, E - ns with
+ * num_shared_experts = ns > 0. */
 int moe_router_outputs(const moe_handle *h);
-/* Slots per token: k, 1 (Switch) or num_shared + k (Shared). */
+/* Slots per token: k, 1 (Switch) or num_shared + k (SharedExpertGating, or
+ * num_shared_experts > 0: the ns shared slots first, with ids 1..ns, then the
+ * routed slots with ids shifted by ns, as expert_indices .+= ns makes them). */
 int moe_slots_per_token(const moe_handle *h);
 
 /* ---- weights (uploaded once, prepacked, device resident) --------------- */
@@ -151,7 +158,12 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
 
 /* (moe::MoELayer)(x; training) -- src/core/moe_layer.jl:107-156.
  * x [T][D] in x_dtype (F32 or BF16); out [T][D_out] fp32; *loss = Switch
- * loss + z-loss when training, else 0. */
+ * loss + z-loss when training, else 0.  With num_shared_experts = ns > 0 this
+ * is forward_with_shared_experts (src/core/moe_layer.jl:158-185): out =
+ * 0.5 * sum_i(y_i / ns) + 0.5 * routed, the routed part combined as in
+ * forward_standard over experts ns+1..E, no capacity constraint, and the
+ * Switch loss over the E - ns router probabilities with the shifted routed
+ * ids (ids above E - ns are not counted, src/balancing/losses.jl:22-26). */
 int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
                 float *out, float *loss, moe_forward_aux *aux);
 

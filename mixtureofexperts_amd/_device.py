@@ -19,7 +19,8 @@ def _ptr(a):
 
 class DeviceLayer:
     def __init__(self, *, num_experts, expert_type, input_dim, hidden_dim, output_dim, activation, gate,
-                 weight_dtype, balance_alpha, z_loss_weight, capacity_factor, drop_tokens, max_tokens):
+                 weight_dtype, balance_alpha, z_loss_weight, capacity_factor, drop_tokens, max_tokens,
+                 num_shared_experts=0):
         c = _lib.MoeConfigC()
         c.num_experts = num_experts
         c.expert_type = expert_type
@@ -36,6 +37,7 @@ class DeviceLayer:
         c.capacity_factor = capacity_factor
         c.drop_tokens = int(bool(drop_tokens))
         c.max_tokens = max_tokens
+        c.num_shared_experts = int(num_shared_experts)
         self.cfg = c
         self.max_tokens = max_tokens
         self.num_experts = num_experts
@@ -101,7 +103,7 @@ class DeviceLayer:
         aux.z_loss = zl.ctypes.data
         if want_aux:
             res["logits"] = np.zeros((T, self.router_outputs), dtype=np.float32)
-            res["probs"] = np.zeros((T, self.num_experts), dtype=np.float32)
+            res["probs"] = np.zeros((T, self.router_outputs), dtype=np.float32)
             res["indices"] = np.zeros((T, self.slots), dtype=np.int32)
             res["gates"] = np.zeros((T, self.slots), dtype=np.float32)
             res["offsets"] = np.zeros(self.num_experts + 1, dtype=np.int32)
@@ -130,7 +132,7 @@ class DeviceLayer:
         n = x.shape[0]
         k = _lib.lib().moe_slots_per_token(self.h)
         out = np.zeros((n, self.output_dim), dtype=np.float32)
-        logits = np.zeros((n, self.num_experts), dtype=np.float32)
+        logits = np.zeros((n, self.router_outputs), dtype=np.float32)
         idx = np.zeros((n, k), dtype=np.int32)
         gates = np.zeros((n, k), dtype=np.float32)
         _lib.check(_lib.lib().moe_decode(self.h, x.ctypes.data, n, out.ctypes.data, logits.ctypes.data,

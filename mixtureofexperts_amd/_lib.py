@@ -59,7 +59,8 @@ class MoeConfigC(ctypes.Structure):
         ("capacity_factor", ctypes.c_float),
         ("drop_tokens", ctypes.c_int32),
         ("max_tokens", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 7),
+        ("num_shared_experts", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 6),
     ]
 
 

@@ -32,17 +32,31 @@ HIP_FLAGS = [
 ]
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile all HIP sources into mixtureofexperts_amd/libmoe_mi355x.so."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC, *srcs, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode})")
+        raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode}): {' '.join(cmd)}")
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile the HIP sources (one hipcc process each, in parallel) and link
+    them into mixtureofexperts_amd/libmoe_mi355x.so."""
+    import concurrent.futures
+    import tempfile
+
+    incs = ["-I", os.path.join(REPO_DIR, "include"), "-I", CSRC]
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="moe_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[HIPCC, *compile_flags, *incs, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = LIB_PATH + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -21,7 +21,10 @@ inline long long round_up(long long v, long long m) { return (v + m - 1) / m * m
 
 struct moe_handle {
     moe_config cfg{};
-    int E = 0, Er = 0, Er_pad = 0, D = 0, H = 0, Dout = 0, k = 0, ns = 0, kt = 0;
+    // E experts; Er router outputs; k routed slots; ns shared slots of
+    // SharedExpertGating; lsh shared experts of the layer (num_shared_experts);
+    // kt = lsh + ns + k slots per token
+    int E = 0, Er = 0, Er_pad = 0, D = 0, H = 0, Dout = 0, k = 0, ns = 0, lsh = 0, kt = 0;
     int D_pad = 0, H_pad = 0, Dout_npad = 0;
     int ct = CT_BF16, wt = WT_BF16;
     bool gated = true;
@@ -103,9 +106,15 @@ static int validate_config(const moe_config *c, std::string &why) {
     if (c->max_tokens < 1) { why = "max_tokens must be >= 1"; return 0; }
     if (c->drop_tokens && !(c->capacity_factor > 0.0f)) { why = "capacity_factor must be > 0"; return 0; }
     const int k = (c->gate_kind == MOE_GATE_SWITCH) ? 1 : c->top_k;
+    const int lsh = c->num_shared_experts;
+    if (lsh < 0 || lsh >= c->num_experts) { why = "num_shared_experts must be in [0, num_experts)"; return 0; }
+    if (lsh > 0 && c->gate_kind == MOE_GATE_SHARED) {
+        why = "num_shared_experts > 0 with SharedExpertGating has no device path";
+        return 0;
+    }
     if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH) {
-        if (k < 1 || k > c->num_experts) { why = "top_k must be in [1, num_experts]"; return 0; }
-        if (k > MOE_MAX_TOPK) { why = "top_k above MOE_MAX_TOPK (8)"; return 0; }
+        if (k < 1 || k > c->num_experts - lsh) { why = "top_k must be in [1, num_experts - num_shared_experts]"; return 0; }
+        if (lsh + k > MOE_MAX_TOPK) { why = "num_shared_experts + top_k above MOE_MAX_TOPK (8)"; return 0; }
     } else if (c->gate_kind == MOE_GATE_SHARED) {
         const int ns = c->gate_num_shared;
         if (ns < 0 || ns >= c->num_experts) { why = "gate_num_shared must be in [0, num_experts)"; return 0; }
@@ -115,7 +124,7 @@ static int validate_config(const moe_config *c, std::string &why) {
         why = "unknown gate_kind";
         return 0;
     }
-    const long long rows = (long long)c->max_tokens * (k + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0));
+    const long long rows = (long long)c->max_tokens * (k + lsh + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0));
     if (rows > INT_MAX / 2) { why = "max_tokens * slots too large"; return 0; }
     return 1;
 }
@@ -340,11 +349,15 @@ static int m_tiles_for(const moe_handle *h, int T) {
 
 enum { PERMUTE_NONE = 0, PERMUTE_INDEX = 1, PERMUTE_ROWS = 2 };
 
+// The capacity constraint runs in forward_standard only
+// (src/core/moe_layer.jl:142-147), not in forward_with_shared_experts.
+static bool drop_active(const moe_handle *h) { return h->cfg.drop_tokens && h->lsh == 0; }
+
 static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
     PermuteArgs pa{};
     pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kt; pa.E = h->E;
     pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base;
-    pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && h->cfg.drop_tokens) ? 1 : 0;
+    pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && drop_active(h)) ? 1 : 0;
     pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
     pa.copy_rows = mode == PERMUTE_ROWS ? 1 : 0;
     HIP_TRY(h, launch_permute(pa, s));
@@ -367,14 +380,16 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         ra.nks = 1;  // the caller's logits are in partial slot 0
         ra.bias = nullptr;
     }
-    ra.part = h->logits_part; ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->E; ra.gate_kind = h->cfg.gate_kind;
+    ra.part = h->logits_part; ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->Er; ra.Eh = h->E;
+    ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kt; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
     HIP_TRY(h, launch_route(ra, s));
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
     sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kt;
-    sa.training = training; sa.drop = h->cfg.drop_tokens; sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
+    sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
+    sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kt - h->lsh;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
     sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
@@ -448,7 +463,7 @@ static int run_experts(moe_handle *h, int T, hipStream_t s) {
 static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
     CombineArgs c{};
     c.y = h->y; c.ld_y = h->Dout; c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
-    c.T = T; c.D = h->Dout; c.kt = h->kt; c.out = out_dev;
+    c.T = T; c.D = h->Dout; c.kt = h->kt; c.lsh = h->lsh; c.out = out_dev;
     HIP_TRY(h, launch_combine(c, s));
     return MOE_OK;
 }
@@ -505,14 +520,15 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     moe_handle *h = new moe_handle();
     h->cfg = *cfg;
     h->E = cfg->num_experts;
-    h->Er = cfg->num_experts;
+    h->lsh = cfg->num_shared_experts;
+    h->Er = cfg->num_experts - h->lsh;
     h->Er_pad = (int)round_up(h->Er, 8);
     h->D = cfg->input_dim;
     h->H = cfg->hidden_dim;
     h->Dout = cfg->output_dim;
     h->k = (cfg->gate_kind == MOE_GATE_SWITCH) ? 1 : cfg->top_k;
     h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
-    h->kt = h->ns + h->k;
+    h->kt = h->lsh + h->ns + h->k;
     h->D_pad = (int)round_up(h->D, kKPad);
     // N of the up GEMM, K of the down GEMM: a whole number of up-GEMM tiles
     h->H_pad = (int)round_up(h->H, cfg->expert_type == MOE_EXPERT_GATED ? kNPadGated : kNPad);
@@ -575,7 +591,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
     A((void **)&h->logits_part, sizeof(float) * kRouterMaxSlices * T * h->Er);
-    A((void **)&h->probs, sizeof(float) * T * E);
+    A((void **)&h->probs, sizeof(float) * T * h->Er);
     A((void **)&h->idx, sizeof(int) * T * kt);
     A((void **)&h->gates, sizeof(float) * T * kt);
     A((void **)&h->rank, sizeof(int) * T * kt);
@@ -730,7 +746,7 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     const size_t nk = (size_t)T * h->kt;
     if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
     if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * nk, hipMemcpyDeviceToHost, s));
-    if (probs) HIP_TRY(h, hipMemcpyAsync(probs, h->probs, sizeof(float) * (size_t)T * h->E, hipMemcpyDeviceToHost, s));
+    if (probs) HIP_TRY(h, hipMemcpyAsync(probs, h->probs, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
     if (counts) HIP_TRY(h, hipMemcpyAsync(counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost, s));
     if (offsets) HIP_TRY(h, hipMemcpyAsync(offsets, h->offsets, sizeof(int) * (h->E + 1), hipMemcpyDeviceToHost, s));
     if (perm) HIP_TRY(h, hipMemcpyAsync(perm, h->perm, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
@@ -769,7 +785,7 @@ int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_
     const size_t nk = (size_t)T * h->kt;
     if (aux) {
         if (aux->logits) HIP_TRY(h, hipMemcpyAsync(aux->logits, h->logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
-        if (aux->probs) HIP_TRY(h, hipMemcpyAsync(aux->probs, h->probs, sizeof(float) * (size_t)T * h->E, hipMemcpyDeviceToHost, s));
+        if (aux->probs) HIP_TRY(h, hipMemcpyAsync(aux->probs, h->probs, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
         if (aux->indices) HIP_TRY(h, hipMemcpyAsync(aux->indices, h->idx, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
         if (aux->gates) HIP_TRY(h, hipMemcpyAsync(aux->gates, h->gates, sizeof(float) * nk, hipMemcpyDeviceToHost, s));
         if (aux->counts) HIP_TRY(h, hipMemcpyAsync(aux->counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost, s));
@@ -836,6 +852,7 @@ static int decode_check(moe_handle *h, int n) {
     if (!h->gated) return fail(h, MOE_EUNSUPPORTED, "decode path: gated experts only (gated_expert_forward!)");
     if (h->cfg.gate_kind != MOE_GATE_TOPK && h->cfg.gate_kind != MOE_GATE_SWITCH)
         return fail(h, MOE_EUNSUPPORTED, "decode path: TopKGating or SwitchGating only");
+    if (h->lsh > 0) return fail(h, MOE_EUNSUPPORTED, "decode path: no shared experts");
     if ((h->D & 3) != 0) return fail(h, MOE_EUNSUPPORTED, "decode path: input_dim must be a multiple of 4");
     // h of the n * k slots is kept as fp32 rows in the expert workspace
     const long long cap = (long long)h->rows_max * h->H_pad * (h->ct == CT_F32 ? 4 : 2) / (4LL * h->H_pad * h->kt);

@@ -138,19 +138,24 @@ struct RouteArgs {
     int nks;
     const float *bias;     // [Er] or null
     float *logits;         // [T][Er] out: sum of the partials + bias
-    int T, Er, E, gate_kind, k, ns, kt;
+    int T, Er;
+    int E;                 // probability rows (= Er)
+    int Eh;                // experts of the histogram: E + lsh
+    int gate_kind, k, ns, kt;
+    int lsh;               // shared experts of the layer (slots 0..lsh-1 of every token)
     float *probs;          // [T][E]
     int *idx;              // [T][kt]
     float *gates;          // [T][kt]
     int *rank;             // [T][kt] rank of the entry inside its block & expert
-    int *blk_counts;       // [nblk][E]
-    double *blk_stats;     // [nblk][E+2]: prob sums, sum lse^2, sum entropy
+    int *blk_counts;       // [nblk][Eh]
+    double *blk_stats;     // [nblk][Eh+2]: prob sums (0 past E), sum lse^2, sum entropy
 };
 
 struct ScanArgs {
     const int *blk_counts;
     const double *blk_stats;
-    int nblk, T, E, kt;
+    int nblk, T, E, kt;   // E: experts of the histogram
+    int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
     int training, drop, z_enabled;
     float capacity_factor, alpha, beta;
     int bm;                // GEMM tile rows
@@ -212,6 +217,7 @@ struct CombineArgs {
     const float *y; int ld_y;    // [rows][ld_y]
     const int *idx; const int *pos_of; const float *gates;
     int T, D, kt;
+    int lsh;                     // > 0: out = 0.5 * sum(y_shared / lsh) + 0.5 * routed
     float *out;                  // [T][D]
 };
 

@@ -67,7 +67,6 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep
 // select on the loaded value lets the compiler sink the load into a branch).
 template <int XBF16, int ALIGNED>
 __device__ inline void load_x8(const void *x, int D, int t, int k, rbf16x8_t *p) {
-    const bool in = k < D;
     if (XBF16) {
         const uint16_t *row = (const uint16_t *)x + (long long)t * D;
         uint16_t v[8];
@@ -293,7 +292,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     const bool tok = tid < kRouteBlock;         // a token thread
     const bool valid = tok && t < a.T;
     const int ns = shared_gate ? a.ns : 0;      // rows before the routed ones
-    const int Ero = a.E - ns;                   // routed rows (softmax width)
     const int rt = tid / TPT, rs = tid - rt * TPT;  // row-parallel phases: token rt, lane rs of it
     const bool rvalid = rt < ntok;
 
@@ -453,12 +451,35 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             zterm = (double)(lse * lse);
         } else {
             topk_row(p, a.E, a.k, sel, g);
+            if (a.lsh == 0) {
 #pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j < a.k) {
-                    ex[j] = sel[j] + 1;
-                    gx[j] = g[j];
+                for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                    if (j < a.k) {
+                        ex[j] = sel[j] + 1;
+                        gx[j] = g[j];
+                    }
+            } else {
+                // forward_with_shared_experts: shared experts 1..lsh in slots
+                // 0..lsh-1 (their outputs are averaged, the gate is only
+                // reported), then the routed ids shifted by lsh (expert_indices
+                // .+= num_shared_experts, src/core/moe_layer.jl:172)
+                const float gsh = 1.0f / (float)a.lsh;
+#pragma unroll
+                for (int j = 0; j < MOE_MAX_TOPK; ++j) {
+                    if (j < a.lsh) {
+                        ex[j] = j + 1;
+                        gx[j] = gsh;
+                    }
+                    if (j < a.k) {
+#pragma unroll
+                        for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                            if (q == a.lsh + j) {
+                                ex[q] = sel[j] + 1 + a.lsh;
+                                gx[q] = g[j];
+                            }
+                    }
                 }
+            }
             // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe
             const float lse = rmax[tid] + (float)log((double)rsum[tid]);
             zterm = (double)(lse * lse);
@@ -540,19 +561,21 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         }
     }
     const int nb = blockIdx.x;
-    for (int e = tid; e < a.E; e += kRouteThreads) {
+    for (int e = tid; e < a.Eh; e += kRouteThreads) {
         int c = 0;
         for (int w = 0; w < NWV; ++w) c += wcnt[w][e];
-        a.blk_counts[(long long)nb * a.E + e] = c;
-        // per-expert probability sums (Switch loss P_e) in fp64, token order
+        a.blk_counts[(long long)nb * a.Eh + e] = c;
+        // per-row probability sums (Switch loss P_e) in fp64, token order
         double ps = 0.0;
+        if (e < a.E) {
 #pragma unroll 8
-        for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
-        a.blk_stats[(long long)nb * (a.E + 2) + e] = ps;
+            for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
+        }
+        a.blk_stats[(long long)nb * (a.Eh + 2) + e] = ps;
     }
     if (tid == 0) {
-        a.blk_stats[(long long)nb * (a.E + 2) + a.E] = red[0][0];
-        a.blk_stats[(long long)nb * (a.E + 2) + a.E + 1] = red[1][0];
+        a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh] = red[0][0];
+        a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh + 1] = red[1][0];
     }
 }
 
@@ -675,18 +698,22 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
         tstart[a.E] = ts;
         a.num_tiles[0] = ts;
 
-        // losses (src/balancing/losses.jl:15-36, 103-114)
+        // losses (src/balancing/losses.jl:15-36, 103-114): N = a.Np probability
+        // rows, f over the router's kl * T index entries counted by id <= N.
+        // With shared experts of the layer the ids are the shifted routed ids
+        // (src/core/moe_layer.jl:172-182): expert e < lsh holds only shared
+        // entries, which the router's indices do not contain.
         const double zs = zh[0], hs = zh[1];
-        const float total = (float)((long long)a.T * a.kt);
+        const float total = (float)((long long)a.T * a.kl);
         float s = 0.0f;
-        for (int e = 0; e < a.E; ++e) {
-            float f = (float)cnt[e];
-            if (a.T * a.kt > 0) f = f / total;
+        for (int e = 0; e < a.Np; ++e) {
+            float f = (e < a.lsh) ? 0.0f : (float)cnt[e];
+            if (a.T * a.kl > 0) f = f / total;
             const float P = (float)psum[e] / (float)a.T;
             const float fp = f * P;
             s = (e == 0) ? fp : s + fp;
         }
-        const float sw = (a.alpha * (float)a.E) * s;
+        const float sw = (a.alpha * (float)a.Np) * s;
         const float z = a.beta * ((float)zs / (float)a.T);
         float loss = 0.0f;
         if (a.training) loss = a.z_enabled ? sw + z : sw;
@@ -854,11 +881,17 @@ hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
 // ascending expert order of gate * y, as separate fp32 multiply and add on a
 // zero start (src/core/moe_layer.jl:132, 205-217).  No atomics.
 //
+// With shared experts of the layer (lsh > 0, forward_with_shared_experts,
+// src/core/moe_layer.jl:158-185) the token's first lsh entries in expert
+// order are the shared experts: shared = sum of y / lsh (IEEE division,
+// `expert_out ./ num_shared_experts`, :164-166), routed = the sum above over
+// the rest, out = 0.5f * shared + 0.5f * routed (:179-180).
+//
 // Fast path (every one of the token's KT entries kept, rows 16-byte
 // aligned): the entries are sorted by expert in registers, and all y loads of
 // a chunk of U float4 per lane are issued before any is summed.
 // ============================================================================
-template <int KT>
+template <int KT, bool BLEND>
 __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
 #pragma clang fp contract(off)
     constexpr int U = (KT >= 8) ? 2 : (KT >= 4 ? 4 : 8);
@@ -896,13 +929,28 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float4 sh = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int i = 0; i < KT; ++i) {
-                const float g = gg[i];
-                acc.x = acc.x + g * v[i][u].x;
-                acc.y = acc.y + g * v[i][u].y;
-                acc.z = acc.z + g * v[i][u].z;
-                acc.w = acc.w + g * v[i][u].w;
+                if (BLEND && i < a.lsh) {
+                    const float n = (float)a.lsh;
+                    sh.x = sh.x + v[i][u].x / n;
+                    sh.y = sh.y + v[i][u].y / n;
+                    sh.z = sh.z + v[i][u].z / n;
+                    sh.w = sh.w + v[i][u].w / n;
+                } else {
+                    const float g = gg[i];
+                    acc.x = acc.x + g * v[i][u].x;
+                    acc.y = acc.y + g * v[i][u].y;
+                    acc.z = acc.z + g * v[i][u].z;
+                    acc.w = acc.w + g * v[i][u].w;
+                }
+            }
+            if (BLEND) {
+                acc.x = 0.5f * sh.x + 0.5f * acc.x;
+                acc.y = 0.5f * sh.y + 0.5f * acc.y;
+                acc.z = 0.5f * sh.z + 0.5f * acc.z;
+                acc.w = 0.5f * sh.w + 0.5f * acc.w;
             }
             const int d = d0 + u * 256 + lane * 4;
             if (d < a.D) *(float4 *)(o + d) = acc;
@@ -913,7 +961,7 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
 template <int KT>
 __device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, int t, int lane) {
     if (a.kt != KT) return false;
-    combine_fast<KT>(a, t, lane);
+    combine_fast<KT, false>(a, t, lane);
     return true;
 }
 
@@ -925,9 +973,18 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0;
     for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
     if (all_kept) {
-        if (try_combine_fast<2>(a, t, lane) || try_combine_fast<1>(a, t, lane) || try_combine_fast<8>(a, t, lane) ||
-            try_combine_fast<4>(a, t, lane) || try_combine_fast<6>(a, t, lane))
+        if (a.lsh > 0) {
+            switch (a.kt) {
+            case 2: combine_fast<2, true>(a, t, lane); return;
+            case 3: combine_fast<3, true>(a, t, lane); return;
+            case 4: combine_fast<4, true>(a, t, lane); return;
+            default: break;
+            }
+        } else if (try_combine_fast<2>(a, t, lane) || try_combine_fast<1>(a, t, lane) ||
+                   try_combine_fast<8>(a, t, lane) || try_combine_fast<4>(a, t, lane) ||
+                   try_combine_fast<6>(a, t, lane)) {
             return;
+        }
     }
     int ee[MOE_MAX_TOPK], pp[MOE_MAX_TOPK];
     float gg[MOE_MAX_TOPK];
@@ -952,8 +1009,13 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
     float *o = a.out + (long long)t * a.D;
     for (int d = lane; d < a.D; d += 64) {
-        float acc = 0.0f;
-        for (int i = 0; i < n; ++i) acc = acc + gg[i] * a.y[(long long)pp[i] * a.ld_y + d];
+        float acc = 0.0f, sh = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const float v = a.y[(long long)pp[i] * a.ld_y + d];
+            if (i < a.lsh) sh = sh + v / (float)a.lsh;
+            else acc = acc + gg[i] * v;
+        }
+        if (a.lsh > 0) acc = 0.5f * sh + 0.5f * acc;
         o[d] = acc;
     }
 }

@@ -116,10 +116,6 @@ class MoELayer:
     # ---- device state ----------------------------------------------------
     def _check_supported(self, training):
         c = self.config
-        if c.num_shared_experts > 0:
-            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED,
-                                "MoEConfig.num_shared_experts > 0 (forward_with_shared_experts) has no device path; "
-                                "use SharedExpertGating")
         if training and c.noise_scale > 0:
             raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "router noise in training has no device path")
         if training and c.expert_dropout > 0 and c.expert_type != "gated":
@@ -137,7 +133,8 @@ class MoELayer:
             input_dim=c.input_dim, hidden_dim=c.hidden_dim, output_dim=c.output_dim,
             activation=activation_code(c.activation), gate=spec, weight_dtype=_DTYPES[c.weight_dtype],
             balance_alpha=balance_alpha(self.balance_loss), z_loss_weight=c.z_loss_weight,
-            capacity_factor=c.capacity_factor, drop_tokens=c.drop_tokens, max_tokens=c.max_tokens)
+            capacity_factor=c.capacity_factor, drop_tokens=c.drop_tokens, max_tokens=c.max_tokens,
+            num_shared_experts=c.num_shared_experts)
         self._dev.set_router(np.ascontiguousarray(self.router.weight.T), self.router.bias)
         for e, ex in enumerate(self.experts):
             ex.upload(self._dev, e)
@@ -151,6 +148,11 @@ class MoELayer:
     # ---- forward -----------------------------------------------------------
     def __call__(self, x, training=False, return_stats=False, x_dtype="f32", _aux=None):
         """(moe::MoELayer)(x; training, return_stats) -- src/core/moe_layer.jl:107-156.
+
+        With ``num_shared_experts > 0`` this is forward_with_shared_experts
+        (src/core/moe_layer.jl:158-185): experts 1..ns run on every token and
+        are averaged, the router picks among the others, the output is the
+        0.5/0.5 blend, and, as there, the training statistics are not updated.
 
         x: (input_dim, T) float32, or uint16 bf16 bit patterns with
         ``x_dtype="bf16"``.  Returns (output (output_dim, T) float32,
@@ -172,9 +174,10 @@ class MoELayer:
         out, loss, res = dev.forward(xt, xcode, training, want_aux=_aux is not None)
         if _aux is not None:
             _aux.update(res)
-        # update_stats! -- src/core/moe_layer.jl:250-264
-        self.training_stats["tokens_per_expert"] += res["counts"].astype(np.int64)
-        self.training_stats["routing_entropy"].append(np.float32(res["mean_entropy"]))
+        if self.config.num_shared_experts == 0:
+            # update_stats! -- src/core/moe_layer.jl:153, 250-264 (forward_standard only)
+            self.training_stats["tokens_per_expert"] += res["counts"].astype(np.int64)
+            self.training_stats["routing_entropy"].append(np.float32(res["mean_entropy"]))
         output = out.T
         loss = np.float32(loss)
         if return_stats:

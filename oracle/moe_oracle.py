@@ -13,6 +13,7 @@ matrices.
 
 Reference lines followed (MixtureOfExperts.jl):
   forward_standard         src/core/moe_layer.jl:107-156
+  forward_with_shared_experts src/core/moe_layer.jl:158-185
   process_expert_forward!  src/core/moe_layer.jl:187-219
   Router                   src/core/router.jl:25-46
   GatedExpert              src/experts/gated.jl:29-35
@@ -240,6 +241,50 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
             loss = np.float32(loss + zl)
     aux = dict(logits=logits, idx=idx, gates=gates, probs=probs, counts=counts, offsets=offsets, perm=perm,
                switch_loss=sw, z_loss=zl, mean_entropy=mean_entropy(probs))
+    return out, loss, aux
+
+
+def moe_forward_shared_experts(x_TD, router_w_ED, experts, num_shared, *, gate="topk", k=2, expert_type="gated",
+                               act="silu", alpha=0.01, z_weight=0.001, training=False, router_bias=None, logits=None):
+    """forward_with_shared_experts + the z-loss of MoELayer's call
+    (src/core/moe_layer.jl:107-128, 158-185), num_shared_experts = ns > 0.
+
+    experts: all E experts, the first ns the shared ones; router_w_ED is the
+    (E - ns, D) router.  shared = sum_i (y_i ./ ns) from zeros (:161-166);
+    the router's indices are shifted by ns (:172) and the routed experts run
+    through process_expert_forward! with the unshifted ids (:174-177);
+    output = 0.5f0 .* shared .+ 0.5f0 .* routed (:179-180); the Switch loss
+    takes the shifted indices and the (E - ns) router probabilities (:182),
+    so ids above E - ns are not counted (src/balancing/losses.jl:22-26); no
+    capacity constraint and no update_stats!.  Returns (out, loss, aux)."""
+    x = np.asarray(x_TD, np.float32)
+    T = x.shape[0]
+    ns = int(num_shared)
+    fn = ACTS[act]
+    shared = np.zeros((T, experts[0]["w2"].shape[0]), np.float32)
+    for i in range(ns):
+        ex = experts[i]
+        if expert_type == "gated":
+            y = gated_expert(x, ex["w1"], ex["w2"], ex["w3"], fn)
+        else:
+            y = standard_expert(x, ex["w1"], ex["w2"], ex.get("b1"), ex.get("b2"), fn)
+        shared = (shared + (y / np.float32(ns)).astype(np.float32)).astype(np.float32)
+    routed, _, ra = moe_forward(x, router_w_ED, experts[ns:], gate=gate, k=k, expert_type=expert_type, act=act,
+                                alpha=alpha, z_weight=0.0, training=False, router_bias=router_bias, logits=logits)
+    half = np.float32(0.5)
+    out = ((half * shared).astype(np.float32) + (half * routed).astype(np.float32)).astype(np.float32)
+    shifted = (ra["idx"] + ns).astype(np.int32)
+    loss = np.float32(0.0)
+    sw = np.float32(0.0)
+    zl = np.float32(0.0)
+    if training:
+        sw = switch_loss(shifted, ra["probs"], alpha)
+        loss = sw
+        if z_weight > 0:
+            zl = z_loss(ra["logits"], z_weight)
+            loss = np.float32(loss + zl)
+    aux = dict(logits=ra["logits"], idx=shifted, gates=ra["gates"], probs=ra["probs"], routed_idx=ra["idx"],
+               routed_counts=ra["counts"], shared=shared, routed=routed, switch_loss=sw, z_loss=zl)
     return out, loss, aux
 
 

@@ -24,7 +24,7 @@ class Case:
 
     def __init__(self, moe, oracle, *, T, D, H, Dout=None, E, k, gate="topk", ns=0, expert_type="gated", act="silu",
                  wdtype="f32", xdtype="f32", seed=0, router_bias=None, alpha=0.01, z=0.001, drop=False, cf=1.25,
-                 max_tokens=None, wscale=None):
+                 max_tokens=None, wscale=None, lsh=0):
         from mixtureofexperts_amd import _lib
         from mixtureofexperts_amd._device import DeviceLayer, GateSpec
 
@@ -34,6 +34,7 @@ class Case:
         self.T, self.D, self.H, self.Dout, self.E, self.k = T, D, H, Dout, E, k
         self.gate, self.ns, self.expert_type, self.act = gate, ns, expert_type, act
         self.alpha, self.z, self.drop, self.cf = alpha, z, drop, cf
+        self.lsh = lsh  # MoEConfig.num_shared_experts: the router sees E - lsh experts
         x = rng.standard_normal((T, D)).astype(np.float32)
         if xdtype == "bf16":
             self.x_dev = oracle.f32_to_bf16_bits(x)
@@ -42,7 +43,7 @@ class Case:
         else:
             self.x_dev = self.x = x
             self.xcode = _lib.MOE_F32
-        self.wr = (rng.standard_normal((E, D)) * (1.0 / np.sqrt(D))).astype(np.float32)
+        self.wr = (rng.standard_normal((E - lsh, D)) * (1.0 / np.sqrt(D))).astype(np.float32)
         self.rb = router_bias
         s_in = np.sqrt(2.0 / D) if wscale is None else wscale
         s_h = np.sqrt(2.0 / H) if wscale is None else wscale
@@ -73,13 +74,13 @@ class Case:
         acts = {"silu": _lib.MOE_ACT_SILU, "gelu": _lib.MOE_ACT_GELU, "relu": _lib.MOE_ACT_RELU,
                 "identity": _lib.MOE_ACT_IDENTITY}
         wcode = {"f32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3}[wdtype]
-        print(f"layer case T={T} D={D} H={H} E={E} k={k} gate={gate} ns={ns} type={expert_type} w={wdtype} "
-              f"x={xdtype}", flush=True)
+        print(f"layer case T={T} D={D} H={H} E={E} k={k} gate={gate} ns={ns} lsh={lsh} type={expert_type} "
+              f"w={wdtype} x={xdtype}", flush=True)
         self.dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED if expert_type == "gated"
                                else _lib.MOE_EXPERT_STANDARD, input_dim=D, hidden_dim=H, output_dim=Dout,
                                activation=acts[act], gate=spec, weight_dtype=wcode, balance_alpha=alpha,
                                z_loss_weight=z, capacity_factor=cf, drop_tokens=drop,
-                               max_tokens=max_tokens or T)
+                               max_tokens=max_tokens or T, num_shared_experts=lsh)
         self.dev.set_router(np.ascontiguousarray(self.wr.T), router_bias)
         for e, d in enumerate(dev_ex):
             self.dev.set_expert(e, d["w"][0], d["w"][1], d["w"][2], d["b"][0], d["b"][1], src_dtype=d["src"],
@@ -123,6 +124,69 @@ def check_case(case, tol, training=True, T=None):
     if not training:
         assert loss == 0.0
     return out, err
+
+
+def check_shared_experts_case(case, tol, training=True):
+    """forward_with_shared_experts (num_shared_experts = lsh > 0) against the
+    oracle on the GPU's router logits."""
+    out, loss, res = case.run(training)
+    T, lsh, k, E = case.T, case.lsh, case.k, case.E
+    ref_logits = (case.x @ case.wr.T).astype(np.float32)
+    assert np.max(np.abs(res["logits"] - ref_logits)) <= 1e-5 * max(1.0, np.max(np.abs(ref_logits)))
+    ref_out, ref_loss, aux = case.oracle.moe_forward_shared_experts(
+        case.x, case.wr, case.ex, lsh, gate=case.gate, k=k, expert_type=case.expert_type, act=case.act,
+        alpha=case.alpha, z_weight=case.z, training=training, logits=res["logits"])
+    # slots: the shared experts 1..lsh, then the shifted routed ids, bit-exact
+    assert res["indices"].shape == (T, lsh + k)
+    assert np.array_equal(res["indices"][:, :lsh], np.tile(np.arange(1, lsh + 1, dtype=np.int32), (T, 1)))
+    assert np.array_equal(res["indices"][:, lsh:], aux["idx"])
+    assert np.array_equal(res["gates"][:, lsh:].view(np.uint32), aux["gates"].view(np.uint32))
+    assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32))
+    assert np.array_equal(res["counts"][:lsh], np.full(lsh, T, np.int32))
+    assert np.array_equal(res["counts"][lsh:], aux["routed_counts"])
+    err = rel_err(out, ref_out)
+    assert err <= tol, f"relative error {err:.3e} > {tol}"
+    assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (loss, ref_loss)
+    if training:
+        assert abs(res["switch_loss"] - aux["switch_loss"]) <= 1e-5 * max(1.0, abs(float(aux["switch_loss"])))
+    else:
+        assert loss == 0.0
+    return out, err
+
+
+@pytest.mark.parametrize("lsh,k,E,gate,etype,act,wdtype,xdtype", [
+    (1, 2, 6, "topk", "gated", "silu", "f32", "f32"),        # blend fast path, kt = 3
+    (2, 2, 10, "topk", "gated", "silu", "bf16", "bf16"),     # kt = 4, 1/ns exact
+    (3, 1, 9, "switch", "standard", "gelu", "bf16", "f32"),  # division by 3, Switch gate
+    (2, 3, 12, "topk", "gated", "silu", "fp8", "bf16"),      # kt = 5: the general combine path
+])
+def test_shared_experts_layer(moe, oracle, lsh, k, E, gate, etype, act, wdtype, xdtype):
+    c = Case(moe, oracle, T=500, D=128, H=192, E=E, k=k, gate=gate, expert_type=etype, act=act, wdtype=wdtype,
+             xdtype=xdtype, seed=30 + lsh, lsh=lsh)
+    check_shared_experts_case(c, TOL[wdtype], training=True)
+    check_shared_experts_case(c, TOL[wdtype], training=False)
+
+
+def test_shared_experts_python_api(moe, oracle):
+    # MoEConfig(num_shared_experts=2): the router has E - 2 outputs, the
+    # training statistics are not updated (forward_with_shared_experts has no
+    # update_stats!)
+    rng = np.random.default_rng(40)
+    cfg = moe.MoEConfig(num_experts=6, expert_type="gated", input_dim=64, hidden_dim=96, output_dim=64,
+                        activation=moe.silu, gate_type=moe.TopKGating(2), num_shared_experts=2, max_tokens=64)
+    layer = moe.MoELayer(cfg, rng=rng)
+    assert layer.router.weight.shape == (4, 64)
+    x = rng.standard_normal((64, 40)).astype(np.float32)
+    aux = {}
+    out, loss = layer(x, training=True, _aux=aux)
+    ex = [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]
+    ref, ref_loss, _ = oracle.moe_forward_shared_experts(x.T, layer.router.weight, ex, 2, k=2, training=True,
+                                                         logits=aux["logits"])
+    assert rel_err(out.T, ref) <= 1e-4
+    assert abs(loss - ref_loss) <= 1e-5
+    assert layer.training_stats["tokens_per_expert"].sum() == 0
+    assert layer.training_stats["routing_entropy"] == []
+    layer.close()
 
 
 def test_readme_config_fp32(moe, oracle):

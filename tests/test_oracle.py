@@ -294,6 +294,97 @@ def test_combine_order_is_ascending_expert(oracle):
     assert out[0, 0] == np.float32(np.float32(1e8 + -1e8) + 1.0)  # (e1 + e2) + e3 = 1
 
 
+# ---- forward_with_shared_experts (num_shared_experts > 0) ----------------------
+
+def _shared_case(rng, T, D, H, E, scale=0.2):
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ex = [dict(w1=(rng.standard_normal((H, D)) * scale).astype(np.float32),
+               w2=(rng.standard_normal((D, H)) * scale).astype(np.float32),
+               w3=(rng.standard_normal((H, D)) * scale).astype(np.float32)) for _ in range(E)]
+    return x, ex
+
+
+def test_shared_experts_identical_experts_give_the_expert(oracle):
+    # every expert the same FFN: shared = sum_i y/ns = y, routed = sum_j g_j y
+    # = y (gates sum to 1), so out = 0.5 y + 0.5 y = y; a wrong blend weight,
+    # a sum instead of the mean over the shared experts or ungated routed
+    # outputs all fail this
+    rng = np.random.default_rng(21)
+    T, D, H, E = 24, 16, 40, 6
+    x, ex = _shared_case(rng, T, D, H, 1)
+    ex = [ex[0]] * E
+    for ns, k in ((1, 2), (2, 2), (3, 1), (2, 4)):
+        wr = (rng.standard_normal((E - ns, D)) * 0.5).astype(np.float32)
+        out, _, aux = oracle.moe_forward_shared_experts(x, wr, ex, ns, k=k)
+        a = ex[0]["w1"].astype(np.float64) @ x.T.astype(np.float64)
+        h = a / (1 + np.exp(-a)) * (ex[0]["w3"].astype(np.float64) @ x.T.astype(np.float64))
+        y64 = (ex[0]["w2"].astype(np.float64) @ h).T
+        assert np.max(np.abs(out - y64)) / np.max(np.abs(y64)) < 1e-5, (ns, k)
+        assert aux["idx"].shape == (T, k) and aux["idx"].min() >= ns + 1 and aux["idx"].max() <= E
+
+
+def test_shared_experts_zero_shared_is_half_the_standard_forward(oracle):
+    # shared experts with w2 = 0 output zeros: out = 0.5f0 * forward_standard
+    # over the routed experts with the same router, bit for bit
+    rng = np.random.default_rng(22)
+    T, D, H, E, ns = 30, 16, 24, 7, 2
+    x, ex = _shared_case(rng, T, D, H, E)
+    for i in range(ns):
+        ex[i] = dict(ex[i], w2=np.zeros_like(ex[i]["w2"]))
+    wr = (rng.standard_normal((E - ns, D)) * 0.5).astype(np.float32)
+    out, _, _ = oracle.moe_forward_shared_experts(x, wr, ex, ns, k=2)
+    std, _, _ = oracle.moe_forward(x, wr, ex[ns:], k=2)
+    assert np.array_equal(out, (np.float32(0.5) * std).astype(np.float32))
+
+
+def test_shared_experts_zero_routed_is_half_the_shared_mean(oracle):
+    # routed experts with w2 = 0: out = 0.5 * mean of the ns shared outputs
+    # (against float64, ns = 3 so 1/ns is inexact)
+    rng = np.random.default_rng(23)
+    T, D, H, E, ns = 20, 16, 24, 6, 3
+    x, ex = _shared_case(rng, T, D, H, E)
+    for i in range(ns, E):
+        ex[i] = dict(ex[i], w2=np.zeros_like(ex[i]["w2"]))
+    wr = (rng.standard_normal((E - ns, D)) * 0.5).astype(np.float32)
+    out, _, _ = oracle.moe_forward_shared_experts(x, wr, ex, ns, k=2)
+    ref = np.zeros((T, D))
+    for i in range(ns):
+        a = ex[i]["w1"].astype(np.float64) @ x.T.astype(np.float64)
+        h = a / (1 + np.exp(-a)) * (ex[i]["w3"].astype(np.float64) @ x.T.astype(np.float64))
+        ref += (ex[i]["w2"].astype(np.float64) @ h).T / ns
+    ref *= 0.5
+    assert np.max(np.abs(out - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
+def test_shared_experts_switch_loss_counts_shifted_ids(oracle):
+    # the loss sees the router indices shifted by ns against the E - ns
+    # probability rows (src/core/moe_layer.jl:172, 182): ids above E - ns are
+    # not counted.  E = 4, ns = 2: every shifted id is 3 or 4 > N = 2, so the
+    # Switch loss is exactly 0.  E = 5, ns = 1, k = 2: brute-force count of
+    # shifted ids 2..4 against the probability means.
+    rng = np.random.default_rng(24)
+    x, ex = _shared_case(rng, 16, 8, 8, 4)
+    wr = rng.standard_normal((2, 8)).astype(np.float32)
+    _, loss, aux = oracle.moe_forward_shared_experts(x, wr, ex, 2, k=1, training=True, z_weight=0.0)
+    assert loss == 0.0 and aux["switch_loss"] == 0.0
+    x, ex = _shared_case(rng, 33, 8, 8, 5)
+    wr = rng.standard_normal((4, 8)).astype(np.float32)
+    alpha = 0.01
+    _, loss, aux = oracle.moe_forward_shared_experts(x, wr, ex, 1, k=2, training=True, alpha=alpha,
+                                                     z_weight=0.0)
+    N, T, k = 4, 33, 2
+    f = [sum(1 for t in range(T) for j in range(k) if aux["idx"][t, j] == e + 1) / (k * T) for e in range(N)]
+    P = [float(np.mean(aux["probs"][:, e].astype(np.float64))) for e in range(N)]
+    ref = alpha * N * sum(fe * pe for fe, pe in zip(f, P))
+    assert f[0] == 0.0 and sum(f) < 1.0  # shared id 1 never counted, id 5 dropped
+    assert abs(float(loss) - ref) < 1e-7
+    # and the z-loss is the standard one over the router logits
+    _, loss_z, aux_z = oracle.moe_forward_shared_experts(x, wr, ex, 1, k=2, training=True, alpha=alpha,
+                                                         z_weight=0.001)
+    assert aux_z["z_loss"] == oracle.z_loss(aux_z["logits"], 0.001)
+    assert loss_z == np.float32(aux_z["switch_loss"] + aux_z["z_loss"])
+
+
 # ---- dtype helpers -----------------------------------------------------------
 
 def test_bf16_rounding_matches_torch(oracle):
