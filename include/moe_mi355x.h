@@ -140,6 +140,24 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
                    const float *b1, const float *b2,
                    const float *s1, const float *s2, const float *s3);
 
+/* AuxiliaryFreeLoss(E; bias_init, learning_rate, momentum, update_freq,
+ * use_complementary_loss, complementary_weight) as the layer's balance loss
+ * (src/balancing/auxiliary_free.jl:11-34).  With enable != 0, moe_forward
+ * gates on logits + bias (get_biased_logits, forward_standard,
+ * src/core/moe_layer.jl:137-140; the probabilities, z-loss and statistics stay
+ * those of the plain logits), its balance loss is complementary_weight *
+ * Switch(1) or 0 (:78-87), and each training call counts one compute_loss:
+ * update_counter += 1 and, when it is a multiple of update_freq, the bias
+ * update of update_bias! (:36-69) runs on the device over the kept entries.
+ * bias / bias_momentum: E_router floats (host), NULL = zeros.  enable = 0
+ * restores the loss set at moe_create.  Not with num_shared_experts > 0. */
+int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const float *bias_momentum,
+                     float learning_rate, float momentum, int32_t update_freq, int64_t update_counter,
+                     int32_t use_complementary_loss, float complementary_weight);
+/* Read back the AuxiliaryFreeLoss state (E_router floats each; any pointer
+ * may be NULL).  Blocks until the handle's queued work has finished. */
+int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *update_counter);
+
 /* ---- host-buffer entry points (blocking) -------------------------------- */
 
 /* compute_gates(gate, logits) -- src/gating/topk.jl:24-44,
@@ -195,6 +213,14 @@ int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *p
 /* compute_loss(::ZLoss, logits) -- src/balancing/losses.jl:103-114.
  * logits [T][E]; *loss = beta * mean_t(logsumexp_t^2).  Host pointers. */
 int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *loss);
+
+/* The bias step of update_bias!(::AuxiliaryFreeLoss, indices)
+ * (src/balancing/auxiliary_free.jl:44-69), without its update_counter check
+ * (the caller keeps the counter): indices [n] 1-based (entries <= 0 are not
+ * counted, an id above E is MOE_EINVAL as Julia's BoundsError), bias and
+ * bias_momentum [E] updated in place.  Host pointers. */
+int moe_aux_free_update_bias(const int32_t *indices, int64_t n, int32_t E, float learning_rate, float momentum,
+                             float *bias, float *bias_momentum);
 
 /* ---- device-buffer entry points (enqueue only) -------------------------- */
 

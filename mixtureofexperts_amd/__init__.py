@@ -4,7 +4,8 @@ MI355X (gfx950).
 The API mirrors the reference's exports for this path
 (src/MixtureOfExperts.jl:14-40): MoEConfig, MoELayer, Router, TopKGating,
 SwitchGating, SharedExpertGating, GatedExpert, StandardExpert,
-SwitchTransformerLoss, ZLoss, NoBalancingLoss, compute_gates, compute_loss,
+SwitchTransformerLoss, ZLoss, NoBalancingLoss, AuxiliaryFreeLoss (update_bias!,
+get_biased_logits), DeepSeekLoss, compute_gates, compute_loss,
 create_moe_config, create_moe_layer, reset_stats (reset_stats!), and the
 decode caller moe_ffn_forward (moe_ffn_forward!, src/llama2/inference.jl:58).  All compute
 runs in libmoe_mi355x.so (hand-written HIP kernels); nothing here falls back
@@ -12,7 +13,8 @@ to a CPU path.
 """
 from ._lib import MoeError, lib
 from .activations import gelu, identity, relu, silu, swish
-from .balancing import LoadBalancingLoss, NoBalancingLoss, SwitchTransformerLoss, ZLoss, compute_loss
+from .balancing import (AuxiliaryFreeLoss, DeepSeekLoss, LoadBalancingLoss, NoBalancingLoss, SwitchTransformerLoss,
+                        ZLoss, compute_loss, get_biased_logits, update_bias)
 from .experts import Expert, GatedExpert, StandardExpert
 from .gating import (GatingMechanism, SharedExpertGating, SwitchGating, TopKGating, compute_gates,
                      route_from_logits)
@@ -20,7 +22,8 @@ from .layer import MoEConfig, MoELayer, Router, create_moe_config, create_moe_la
 
 __all__ = [
     "MoeError", "lib", "gelu", "identity", "relu", "silu", "swish", "LoadBalancingLoss", "NoBalancingLoss",
-    "SwitchTransformerLoss", "ZLoss", "compute_loss", "Expert", "GatedExpert", "StandardExpert",
+    "SwitchTransformerLoss", "ZLoss", "AuxiliaryFreeLoss", "DeepSeekLoss", "update_bias", "get_biased_logits",
+    "compute_loss", "Expert", "GatedExpert", "StandardExpert",
     "GatingMechanism", "SharedExpertGating", "SwitchGating", "TopKGating", "compute_gates", "route_from_logits",
     "MoEConfig", "MoELayer", "Router", "create_moe_config", "create_moe_layer", "moe_ffn_forward", "reset_stats",
 ]

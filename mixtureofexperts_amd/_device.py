@@ -86,6 +86,26 @@ class DeviceLayer:
             self.h,
         )
 
+    def set_aux_free(self, loss):
+        """Load an AuxiliaryFreeLoss's state and parameters into the handle."""
+        bias = np.ascontiguousarray(loss.bias, dtype=np.float32)
+        mom = np.ascontiguousarray(loss.bias_momentum, dtype=np.float32)
+        if bias.size != self.router_outputs or mom.size != self.router_outputs:
+            raise _lib.MoeError(_lib.MOE_EINVAL, "AuxiliaryFreeLoss.num_experts must equal the router outputs")
+        _lib.check(_lib.lib().moe_set_aux_free(self.h, 1, bias.ctypes.data, mom.ctypes.data, loss.learning_rate,
+                                               loss.momentum, loss.update_freq, loss.update_counter,
+                                               int(loss.use_complementary_loss), loss.complementary_weight),
+                   self.h)
+
+    def get_aux_free(self, loss):
+        """Copy the handle's AuxiliaryFreeLoss state back into ``loss``."""
+        bias = np.zeros(self.router_outputs, dtype=np.float32)
+        mom = np.zeros(self.router_outputs, dtype=np.float32)
+        cnt = ctypes.c_int64(0)
+        _lib.check(_lib.lib().moe_get_aux_free(self.h, bias.ctypes.data, mom.ctypes.data, ctypes.byref(cnt)),
+                   self.h)
+        loss.bias, loss.bias_momentum, loss.update_counter = bias, mom, int(cnt.value)
+
     # ---- calls ------------------------------------------------------------
     def forward(self, x_TD, x_dtype, training, want_aux=False):
         T = x_TD.shape[0]

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = [
     "moe_forward_async", "moe_stage_router_async", "moe_stage_permute_async",
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
     "moe_read_counts", "moe_switch_loss", "moe_z_loss", "moe_decode", "moe_decode_async",
+    "moe_set_aux_free", "moe_get_aux_free", "moe_aux_free_update_bias",
 ]
 
 
@@ -134,6 +135,10 @@ def lib():
     L.moe_decode_async.argtypes = [vp, vp, i32, vp, vp]
     L.moe_switch_loss.argtypes = [vp, i32, i32, vp, i32, ctypes.c_float, f32p]
     L.moe_z_loss.argtypes = [vp, i32, i32, ctypes.c_float, f32p]
+    i64, f32 = ctypes.c_int64, ctypes.c_float
+    L.moe_set_aux_free.argtypes = [vp, i32, vp, vp, f32, f32, i32, i64, i32, f32]
+    L.moe_get_aux_free.argtypes = [vp, vp, vp, ctypes.POINTER(i64)]
+    L.moe_aux_free_update_bias.argtypes = [vp, i64, i32, f32, f32, vp, vp]
     for name in EXPORTED_SYMBOLS:
         if name not in ("moe_last_error",):
             getattr(L, name).restype = ctypes.c_int

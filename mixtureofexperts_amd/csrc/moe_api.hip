@@ -65,6 +65,14 @@ struct moe_handle {
     void *x_dev = nullptr;
     float *out_dev = nullptr;
 
+    // AuxiliaryFreeLoss state (src/balancing/auxiliary_free.jl:11-20): bias and
+    // momentum on the device, the update counter on the host
+    bool aux_free = false, aux_use_comp = true;
+    float aux_lr = 0.01f, aux_momentum = 0.9f, aux_cw = 0.001f;
+    int aux_update_freq = 1;
+    long long aux_counter = 0;
+    float *aux_bias = nullptr, *aux_mom = nullptr;
+
     int last_T = -1, last_training = 0, last_x_bf16 = 0;
     std::vector<void *> allocs;
 };
@@ -364,9 +372,18 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     return MOE_OK;
 }
 
-// logits -> gating -> scan -> permute (mode PERMUTE_*)
+// logits -> gating -> scan -> permute (mode PERMUTE_*).  A forward
+// (compute_logits) with an AuxiliaryFreeLoss gates on logits + its bias
+// (src/core/moe_layer.jl:137-140) in a second route pass and, when training,
+// counts one compute_loss call for the bias update (auxiliary_free.jl:36-40).
 static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
                        int permute_mode, float *loss_dev, hipStream_t s) {
+    const bool aux = compute_logits && h->aux_free;
+    bool aux_update = false;
+    if (aux && training) {
+        ++h->aux_counter;
+        aux_update = h->aux_counter % h->aux_update_freq == 0;
+    }
     RouteArgs ra{};
     if (compute_logits) {
         RouterArgs rg{};
@@ -384,6 +401,16 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kt; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
+    if (aux) {
+        ra.out_mask = ROUTE_OUT_PROBS;
+        HIP_TRY(h, launch_route(ra, s));
+        ra.part = h->logits;  // the logits just written, plus the loss's bias
+        ra.nks = 1;
+        ra.bias = h->aux_bias;
+        ra.out_mask = ROUTE_OUT_GATING;
+    } else {
+        ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
+    }
     HIP_TRY(h, launch_route(ra, s));
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
@@ -394,6 +421,9 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
     sa.loss_out = loss_dev;
+    sa.aux_free = aux; sa.aux_use_comp = h->aux_use_comp; sa.aux_update = aux_update;
+    sa.aux_cw = h->aux_cw; sa.aux_lr = h->aux_lr; sa.aux_momentum = h->aux_momentum;
+    sa.aux_bias = h->aux_bias; sa.aux_mom = h->aux_mom;
     HIP_TRY(h, launch_scan(sa, s));
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
@@ -605,6 +635,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->num_tiles, sizeof(int));
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
+    A((void **)&h->aux_bias, sizeof(float) * h->Er);
+    A((void **)&h->aux_mom, sizeof(float) * h->Er);
     A((void **)&h->perm, sizeof(int) * T * kt);
     A((void **)&h->pos_of, sizeof(int) * T * kt);
     A((void **)&h->gate_sorted, sizeof(float) * T * kt);
@@ -629,6 +661,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    Z(h->aux_bias, sizeof(float) * h->Er);
+    Z(h->aux_mom, sizeof(float) * h->Er);
     Z(h->xp, asz * (size_t)h->rows_max * h->D_pad);
     Z(h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
     if (ze == hipSuccess) ze = hipStreamSynchronize(h->stream);
@@ -720,6 +754,48 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
                                  is_device_ptr(b2) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice));
     }
     h->expert_set[expert] = 1;
+    return MOE_OK;
+}
+
+int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const float *bias_momentum,
+                     float learning_rate, float momentum, int32_t update_freq, int64_t update_counter,
+                     int32_t use_complementary_loss, float complementary_weight) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (!enable) {
+        h->aux_free = false;
+        return MOE_OK;
+    }
+    if (h->lsh > 0)
+        return fail(h, MOE_EUNSUPPORTED, "AuxiliaryFreeLoss with num_shared_experts > 0 has no device path");
+    if (update_freq < 1) return fail(h, MOE_EINVAL, "update_freq must be >= 1");
+    if (update_counter < 0) return fail(h, MOE_EINVAL, "update_counter must be >= 0");
+    hipStream_t s = h->stream;
+    const size_t bytes = sizeof(float) * h->Er;
+    if (bias) HIP_TRY(h, hipMemcpyAsync(h->aux_bias, bias, bytes, hipMemcpyHostToDevice, s));
+    else HIP_TRY(h, hipMemsetAsync(h->aux_bias, 0, bytes, s));
+    if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(h->aux_mom, bias_momentum, bytes, hipMemcpyHostToDevice, s));
+    else HIP_TRY(h, hipMemsetAsync(h->aux_mom, 0, bytes, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    h->aux_free = true;
+    h->aux_lr = learning_rate;
+    h->aux_momentum = momentum;
+    h->aux_update_freq = update_freq;
+    h->aux_counter = update_counter;
+    h->aux_use_comp = use_complementary_loss != 0;
+    h->aux_cw = complementary_weight;
+    return MOE_OK;
+}
+
+int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *update_counter) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    hipStream_t s = h->stream;
+    const size_t bytes = sizeof(float) * h->Er;
+    if (bias) HIP_TRY(h, hipMemcpyAsync(bias, h->aux_bias, bytes, hipMemcpyDeviceToHost, s));
+    if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(bias_momentum, h->aux_mom, bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    if (update_counter) *update_counter = h->aux_counter;
     return MOE_OK;
 }
 
@@ -1005,6 +1081,28 @@ int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *los
     if (e == hipSuccess) e = hipMemcpy(loss, dout, sizeof(float), hipMemcpyDeviceToHost);
     (void)hipFree(buf);
     if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("z loss failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+int moe_aux_free_update_bias(const int32_t *indices, int64_t n, int32_t E, float learning_rate, float momentum,
+                             float *bias, float *bias_momentum) {
+    if (n < 0 || E < 1 || E > MOE_MAX_EXPERTS || !bias || !bias_momentum || (n > 0 && !indices))
+        return fail(nullptr, MOE_EINVAL, "bad update_bias! arguments");
+    for (int64_t i = 0; i < n; ++i)
+        if (indices[i] > E) return fail(nullptr, MOE_EINVAL, "expert id above num_experts (BoundsError in update_bias!)");
+    int *di = nullptr;
+    float *db = nullptr;
+    hipError_t e = hipMalloc(&di, sizeof(int) * (size_t)(n > 0 ? n : 1));
+    if (e == hipSuccess) e = hipMalloc(&db, sizeof(float) * 2 * (size_t)E);
+    if (e == hipSuccess && n > 0) e = hipMemcpy(di, indices, sizeof(int) * (size_t)n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, bias, sizeof(float) * E, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db + E, bias_momentum, sizeof(float) * E, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_aux_free_update(di, n, E, learning_rate, momentum, db, db + E, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(bias, db, sizeof(float) * E, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(bias_momentum, db + E, sizeof(float) * E, hipMemcpyDeviceToHost);
+    (void)hipFree(di);
+    (void)hipFree(db);
+    if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("update_bias! failed: ") + hipGetErrorString(e));
     return MOE_OK;
 }
 

@@ -133,6 +133,12 @@ struct RouterArgs {
     float *part; int nks, ks_len, kc;
 };
 
+// Outputs of one route_kernel pass.  A plain forward writes both; with an
+// AuxiliaryFreeLoss the probabilities pass runs on the router logits and the
+// gating pass on logits + the loss's bias (src/core/moe_layer.jl:137-140).
+enum { ROUTE_OUT_PROBS = 1,    // logits, probs, per-block probability / z / entropy sums
+       ROUTE_OUT_GATING = 2 }; // indices, gates, ranks, per-block expert counts
+
 struct RouteArgs {
     const float *part;     // [nks][T][Er] partial router logits (summed in slice order)
     int nks;
@@ -143,6 +149,7 @@ struct RouteArgs {
     int Eh;                // experts of the histogram: E + lsh
     int gate_kind, k, ns, kt;
     int lsh;               // shared experts of the layer (slots 0..lsh-1 of every token)
+    int out_mask;          // ROUTE_OUT_*: which outputs this pass writes
     float *probs;          // [T][E]
     int *idx;              // [T][kt]
     float *gates;          // [T][kt]
@@ -168,6 +175,12 @@ struct ScanArgs {
     int *num_tiles;        // [1]
     float *scalars;        // [4]: switch, z, loss, mean entropy
     float *loss_out;       // optional extra destination of the loss
+    // AuxiliaryFreeLoss (src/balancing/auxiliary_free.jl): balance loss =
+    // complementary_weight * Switch(1) when use_complementary, else 0; the
+    // update_bias! step of this call when aux_update (training only)
+    int aux_free, aux_use_comp, aux_update;
+    float aux_cw, aux_lr, aux_momentum;
+    float *aux_bias, *aux_mom;  // [E] device state
 };
 
 struct PermuteArgs {
@@ -274,6 +287,9 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,
                               float *out, hipStream_t s);
 hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *out, hipStream_t s);
+// update_bias!(AuxiliaryFreeLoss, indices) on given indices [n] (entries > 0 counted)
+hipError_t launch_aux_free_update(const int *idx, long long n, int E, float lr, float momentum, float *bias,
+                                  float *mom, hipStream_t s);
 hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const GemmArgs &g,
                                hipStream_t s);
 // bf16 activations x bf16 weights; bm = 128 or 256 rows per tile (the scan's bm)

@@ -538,15 +538,19 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
 
     // ---- outputs --------------------------------------------------------------
-    for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
-        const int tt = q / a.Er, i = q - tt * a.Er;
-        a.logits[(long long)(t0 + tt) * a.Er + i] = lrow[tt * RW + i];
+    const bool out_probs = (a.out_mask & ROUTE_OUT_PROBS) != 0;
+    const bool out_gating = (a.out_mask & ROUTE_OUT_GATING) != 0;
+    if (out_probs) {
+        for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
+            const int tt = q / a.Er, i = q - tt * a.Er;
+            a.logits[(long long)(t0 + tt) * a.Er + i] = lrow[tt * RW + i];
+        }
+        for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
+            const int tt = q / a.E, i = q - tt * a.E;
+            a.probs[(long long)(t0 + tt) * a.E + i] = srow[tt * RW + i];
+        }
     }
-    for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
-        const int tt = q / a.E, i = q - tt * a.E;
-        a.probs[(long long)(t0 + tt) * a.E + i] = srow[tt * RW + i];
-    }
-    if (valid) {
+    if (valid && out_gating) {
 #pragma unroll
         for (int j = 0; j < MOE_MAX_TOPK; ++j) {
             if (j < a.kt) {
@@ -562,18 +566,22 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
     const int nb = blockIdx.x;
     for (int e = tid; e < a.Eh; e += kRouteThreads) {
-        int c = 0;
-        for (int w = 0; w < NWV; ++w) c += wcnt[w][e];
-        a.blk_counts[(long long)nb * a.Eh + e] = c;
-        // per-row probability sums (Switch loss P_e) in fp64, token order
-        double ps = 0.0;
-        if (e < a.E) {
-#pragma unroll 8
-            for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
+        if (out_gating) {
+            int c = 0;
+            for (int w = 0; w < NWV; ++w) c += wcnt[w][e];
+            a.blk_counts[(long long)nb * a.Eh + e] = c;
         }
-        a.blk_stats[(long long)nb * (a.Eh + 2) + e] = ps;
+        if (out_probs) {
+            // per-row probability sums (Switch loss P_e) in fp64, token order
+            double ps = 0.0;
+            if (e < a.E) {
+#pragma unroll 8
+                for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
+            }
+            a.blk_stats[(long long)nb * (a.Eh + 2) + e] = ps;
+        }
     }
-    if (tid == 0) {
+    if (tid == 0 && out_probs) {
         a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh] = red[0][0];
         a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh + 1] = red[1][0];
     }
@@ -598,6 +606,28 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 // Scan: one block.  Per-expert totals, capacity clamp, offsets, per-block rank
 // bases, the (expert, m0) GEMM tile list and the loss scalars.
 // ============================================================================
+// update_bias!(::AuxiliaryFreeLoss, expert_indices) after its counter check
+// (src/balancing/auxiliary_free.jl:36-69), one thread, with Julia's types:
+// counts Float32, target = total / E and the gradient in Float64, the
+// momentum stored as Float32 of a Float64 sum, the bias step in Float32, then
+// bias .-= mean(bias) with the Float32 sum taken in index order.
+__device__ inline void aux_free_step(const int *cnt, long long total, int E, float lr, float momentum,
+                                     float *bias, float *mom) {
+#pragma clang fp contract(off)
+    if (total <= 0) return;
+    const double target = (double)total / (double)E;
+    for (int e = 0; e < E; ++e) {
+        const double grad = ((double)(float)cnt[e] - target) / (double)total;
+        const float m = (float)((double)(momentum * mom[e]) + (double)(1.0f - momentum) * grad);
+        mom[e] = m;
+        bias[e] = bias[e] - lr * m;
+    }
+    float s = bias[0];
+    for (int e = 1; e < E; ++e) s = s + bias[e];
+    const float mean = s / (float)E;
+    for (int e = 0; e < E; ++e) bias[e] = bias[e] - mean;
+}
+
 __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
     constexpr int MAXC = 1024;  // chunk partials (one per thread)
@@ -713,7 +743,11 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
             const float fp = f * P;
             s = (e == 0) ? fp : s + fp;
         }
-        const float sw = (a.alpha * (float)a.Np) * s;
+        // AuxiliaryFreeLoss: complementary_weight * Switch(1.0f0) or 0.0f0
+        // (src/balancing/auxiliary_free.jl:78-87)
+        float sw;
+        if (a.aux_free) sw = a.aux_use_comp ? a.aux_cw * ((1.0f * (float)a.Np) * s) : 0.0f;
+        else sw = (a.alpha * (float)a.Np) * s;
         const float z = a.beta * ((float)zs / (float)a.T);
         float loss = 0.0f;
         if (a.training) loss = a.z_enabled ? sw + z : sw;
@@ -722,6 +756,12 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
         a.scalars[2] = loss;
         a.scalars[3] = (float)(hs / (double)a.T);
         if (a.loss_out) a.loss_out[0] = loss;
+        if (a.aux_free && a.training && a.aux_update) {
+            // the kept entries of each expert are the counts after capacity
+            long long total = 0;
+            for (int e = 0; e < a.E; ++e) total += cnt[e];
+            aux_free_step(cnt, total, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
+        }
     }
     __syncthreads();
     for (int e = tid; e <= a.E; e += blockDim.x) {
@@ -1079,6 +1119,34 @@ __global__ __launch_bounds__(256) void z_loss_kernel(const float *logits, int T,
         __syncthreads();
     }
     if (tid == 0) out[0] = beta * ((float)red[0] / (float)T);
+}
+
+// update_bias! on given indices: one block counts entries 1..E, one thread steps.
+__global__ __launch_bounds__(256) void aux_free_update_kernel(const int *idx, long long n, int E, float lr,
+                                                              float momentum, float *bias, float *mom) {
+    __shared__ int cnt[MOE_MAX_EXPERTS];
+    __shared__ unsigned long long tot;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < MOE_MAX_EXPERTS; e += 256) cnt[e] = 0;
+    if (tid == 0) tot = 0;
+    __syncthreads();
+    unsigned long long mine = 0;
+    for (long long i = tid; i < n; i += 256) {
+        const int e = idx[i];
+        if (e > 0 && e <= E) {  // the host checked that no id exceeds E
+            atomicAdd(&cnt[e - 1], 1);
+            ++mine;
+        }
+    }
+    atomicAdd(&tot, mine);
+    __syncthreads();
+    if (tid == 0) aux_free_step(cnt, (long long)tot, E, lr, momentum, bias, mom);
+}
+
+hipError_t launch_aux_free_update(const int *idx, long long n, int E, float lr, float momentum, float *bias,
+                                  float *mom, hipStream_t s) {
+    hipLaunchKernelGGL(aux_free_update_kernel, dim3(1), dim3(256), 0, s, idx, n, E, lr, momentum, bias, mom);
+    return hipGetLastError();
 }
 
 hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,

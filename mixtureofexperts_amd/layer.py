@@ -14,7 +14,7 @@ import numpy as np
 from . import _lib
 from ._device import DeviceLayer
 from .activations import activation_code, gelu
-from .balancing import LoadBalancingLoss, SwitchTransformerLoss, balance_alpha
+from .balancing import AuxiliaryFreeLoss, LoadBalancingLoss, SwitchTransformerLoss, balance_alpha
 from .experts import GatedExpert, StandardExpert
 from .gating import GatingMechanism, TopKGating, gate_spec
 
@@ -171,7 +171,12 @@ class MoELayer:
             xt = np.ascontiguousarray(xa.T, dtype=np.float32)
             xcode = _lib.MOE_F32
         dev = self._dev if self._dev is not None else self.sync_weights()
+        aux_free = self.balance_loss if isinstance(self.balance_loss, AuxiliaryFreeLoss) else None
+        if aux_free is not None:
+            dev.set_aux_free(aux_free)
         out, loss, res = dev.forward(xt, xcode, training, want_aux=_aux is not None)
+        if aux_free is not None:
+            dev.get_aux_free(aux_free)
         if _aux is not None:
             _aux.update(res)
         if self.config.num_shared_experts == 0:

@@ -188,15 +188,51 @@ def standard_expert(xb, w1, w2, b1, b2, act):
     return y.astype(np.float32)
 
 
+def aux_free_update_bias(idx, bias, mom, lr, momentum):
+    """The bias step of update_bias!(::AuxiliaryFreeLoss, indices) after its
+    counter check (src/balancing/auxiliary_free.jl:44-69), in place, with
+    Julia's types: counts Float32; target_count = total / E and the gradient
+    Float64; momentum[i] = Float32(Float32(m * momentum[i]) + Float32(1 - m) *
+    gradient) (the sum in Float64); bias[i] -= lr * momentum[i] in Float32;
+    then bias .-= mean(bias), the Float32 sum in index order (Julia's order
+    for fewer than 16 experts)."""
+    f32 = np.float32
+    E = bias.size
+    counts = [f32(0)] * E
+    total = 0
+    for e in np.asarray(idx).reshape(-1):
+        if e > 0:
+            counts[int(e) - 1] = f32(counts[int(e) - 1] + f32(1))
+            total += 1
+    if total == 0:
+        return
+    target = total / E
+    m32, lr32 = f32(momentum), f32(lr)
+    for i in range(E):
+        grad = (float(counts[i]) - target) / total
+        mom[i] = f32(float(f32(m32 * mom[i])) + float(f32(f32(1) - m32)) * grad)
+        bias[i] = f32(bias[i] - f32(lr32 * mom[i]))
+    s = bias[0]
+    for i in range(1, E):
+        s = f32(s + bias[i])
+    mean = f32(s / f32(E))
+    for i in range(E):
+        bias[i] = f32(bias[i] - mean)
+
+
 def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, expert_type="gated", act="silu",
                 alpha=0.01, z_weight=0.001, training=False, drop_tokens=False, capacity_factor=1.25,
-                router_bias=None, logits=None):
+                router_bias=None, logits=None, aux_free=None):
     """forward_standard + the z-loss of MoELayer's call (moe_layer.jl:107-156).
 
     x_TD: [T][D] float32.  router_w_ED: (E, D) Flux weight.  experts: list of
     dicts with fp32 "w1","w2"(,"w3") in (out, in) shape (+ "b1","b2").
-    ``logits`` may be given to route identical logits.  Returns (out [T][Dout],
-    loss, aux dict)."""
+    ``logits`` may be given to route identical logits.  ``aux_free``: the
+    state of an AuxiliaryFreeLoss balance loss (dict bias, mom, lr, momentum,
+    update_freq, counter, use_comp, cw), updated in place: the gating runs on
+    logits .+ bias (:137-140) and the balance loss is its compute_loss
+    (src/balancing/auxiliary_free.jl:78-87).  Returns (out [T][Dout], loss,
+    aux dict)."""
     x = np.asarray(x_TD, np.float32)
     T = x.shape[0]
     if logits is None:
@@ -204,10 +240,15 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
         if router_bias is not None:
             logits = (logits + router_bias).astype(np.float32)
     E = len(experts)
-    if gate == "shared":
-        idx, gates, probs = compute_gates_shared(logits, num_shared, k)
-    else:
-        idx, gates, probs = compute_gates_topk(logits, 1 if gate == "switch" else k)
+
+    def gating(lg):
+        if gate == "shared":
+            return compute_gates_shared(lg, num_shared, k)
+        return compute_gates_topk(lg, 1 if gate == "switch" else k)
+
+    idx, gates, probs = gating(logits)
+    if aux_free is not None:
+        idx, gates, _ = gating((logits + aux_free["bias"].reshape(1, -1)).astype(np.float32))
     if drop_tokens and training:
         idx, gates, _ = capacity(idx, gates, E, capacity_factor)
     counts, offsets, perm = bucket(idx, E)
@@ -234,7 +275,14 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
     sw = np.float32(0.0)
     zl = np.float32(0.0)
     if training:
-        sw = switch_loss(idx, probs, alpha)
+        if aux_free is not None:
+            aux_free["counter"] += 1
+            if aux_free["counter"] % aux_free["update_freq"] == 0:
+                aux_free_update_bias(idx, aux_free["bias"], aux_free["mom"], aux_free["lr"], aux_free["momentum"])
+            sw = np.float32(np.float32(aux_free["cw"]) * switch_loss(idx, probs, 1.0)) if aux_free["use_comp"] \
+                else np.float32(0.0)
+        else:
+            sw = switch_loss(idx, probs, alpha)
         loss = sw
         if z_weight > 0:
             zl = z_loss(logits, z_weight)

@@ -189,6 +189,77 @@ def test_shared_experts_python_api(moe, oracle):
     layer.close()
 
 
+@pytest.mark.parametrize("freq,use_comp,drop,wdtype", [(1, True, False, "f32"), (2, False, True, "bf16")])
+def test_aux_free_loss_layer(moe, oracle, freq, use_comp, drop, wdtype):
+    # AuxiliaryFreeLoss as the balance loss: gating on logits + bias, the bias
+    # state after every call bit-exact against the oracle's update_bias!
+    # restatement, inference calls leave it alone
+    rng = np.random.default_rng(50 + freq)
+    E = 8
+    c = Case(moe, oracle, T=600, D=128, H=192, E=E, k=2, wdtype=wdtype, xdtype=wdtype, seed=50 + freq, drop=drop,
+             cf=1.0)
+    lossfn = moe.AuxiliaryFreeLoss(E, learning_rate=0.05, update_freq=freq, use_complementary_loss=use_comp)
+    lossfn.bias = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    st = dict(bias=lossfn.bias.copy(), mom=np.zeros(E, np.float32), lr=0.05, momentum=0.9, update_freq=freq,
+              counter=0, use_comp=use_comp, cw=0.001)
+    for step, training in enumerate((True, True, False, True, True)):
+        c.dev.set_aux_free(lossfn)
+        out, loss, res = c.run(training)
+        c.dev.get_aux_free(lossfn)
+        ref_out, ref_loss, aux = oracle.moe_forward(c.x, c.wr, c.ex, k=2, training=training, drop_tokens=drop,
+                                                    capacity_factor=1.0, z_weight=c.z, logits=res["logits"],
+                                                    aux_free=st)
+        assert np.array_equal(res["indices"], aux["idx"]), step
+        assert np.array_equal(res["gates"].view(np.uint32), aux["gates"].view(np.uint32)), step
+        assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32)), step
+        assert np.array_equal(res["counts"], aux["counts"]), step
+        assert lossfn.update_counter == st["counter"], step
+        assert np.array_equal(lossfn.bias.view(np.uint32), st["bias"].view(np.uint32)), (step, lossfn.bias, st["bias"])
+        assert np.array_equal(lossfn.bias_momentum.view(np.uint32), st["mom"].view(np.uint32)), step
+        err = rel_err(out, ref_out)
+        assert err <= TOL[wdtype], (step, err)
+        assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (step, loss, ref_loss)
+    assert st["counter"] == 4 and np.any(st["mom"] != 0)
+
+
+def test_aux_free_python_api(moe, oracle):
+    # the layer keeps the loss object's state in step with the device, and
+    # update_bias! / compute_loss on given indices match the oracle
+    rng = np.random.default_rng(52)
+    E = 6
+    lossfn = moe.AuxiliaryFreeLoss(E, learning_rate=0.02)
+    cfg = moe.MoEConfig(num_experts=E, expert_type="gated", input_dim=64, hidden_dim=96, output_dim=64,
+                        activation=moe.silu, gate_type=moe.TopKGating(2), balance_loss=lossfn, max_tokens=64)
+    layer = moe.MoELayer(cfg, rng=rng)
+    x = rng.standard_normal((64, 50)).astype(np.float32)
+    st = dict(bias=np.zeros(E, np.float32), mom=np.zeros(E, np.float32), lr=0.02, momentum=0.9, update_freq=1,
+              counter=0, use_comp=True, cw=0.001)
+    ex = [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]
+    for _ in range(3):
+        aux = {}
+        out, loss = layer(x, training=True, _aux=aux)
+        ref, ref_loss, _ = oracle.moe_forward(x.T, layer.router.weight, ex, k=2, training=True,
+                                              logits=aux["logits"], aux_free=st)
+        assert rel_err(out.T, ref) <= 1e-4
+        assert abs(loss - ref_loss) <= 1e-5
+    assert lossfn.update_counter == 3
+    assert np.array_equal(lossfn.bias.view(np.uint32), st["bias"].view(np.uint32))
+    layer.close()
+    # standalone update_bias! and compute_loss(AuxiliaryFreeLoss, ...)
+    idx = rng.integers(0, E + 1, size=(2, 300)).astype(np.int64)  # 0 entries are not counted
+    probs = rng.random((E, 300)).astype(np.float32)
+    l2 = moe.AuxiliaryFreeLoss(E, bias_init=0.25)
+    b, m = l2.bias.copy(), l2.bias_momentum.copy()
+    val = moe.compute_loss(l2, idx, probs)
+    oracle.aux_free_update_bias(idx.T, b, m, l2.learning_rate, l2.momentum)
+    assert np.array_equal(l2.bias.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(l2.bias_momentum.view(np.uint32), m.view(np.uint32))
+    # the loss: the balance-loss bar (1e-5); the mean over tokens is summed in another order
+    assert abs(val - np.float32(np.float32(0.001) * oracle.switch_loss(idx.T, probs.T, 1.0))) <= 1e-5 * abs(val)
+    with pytest.raises(moe.MoeError):
+        moe.update_bias(l2, np.array([[E + 1]]))
+
+
 def test_readme_config_fp32(moe, oracle):
     # README MoELayer, 8 gated silu experts, 512/2048/512,
     # TopKGating(2), SwitchTransformerLoss(0.01), x randn(512, 32), fp32

@@ -385,6 +385,60 @@ def test_shared_experts_switch_loss_counts_shifted_ids(oracle):
     assert loss_z == np.float32(aux_z["switch_loss"] + aux_z["z_loss"])
 
 
+# ---- AuxiliaryFreeLoss ---------------------------------------------------------
+
+def test_aux_free_update_closed_form(oracle):
+    # every entry on expert 1 of 4, from momentum 0 and bias 1: total = n,
+    # target = n/4, gradient = (0.75, -0.25, -0.25, -0.25); momentum =
+    # (1 - 0.9) * gradient; bias = 1 - 0.01 * momentum, then centred (mean 1
+    # removed).  A wrong sign, a missing (1 - momentum) factor or a missing
+    # centring step fails this.
+    idx = np.full((10, 2), 1, np.int32)
+    bias = np.ones(4, np.float32)
+    mom = np.zeros(4, np.float32)
+    oracle.aux_free_update_bias(idx, bias, mom, 0.01, 0.9)
+    grad = np.array([0.75, -0.25, -0.25, -0.25])
+    assert np.allclose(mom, 0.1 * grad, rtol=1e-6, atol=0)
+    assert np.allclose(bias, -0.001 * grad, rtol=1e-4, atol=1e-9)
+    assert abs(float(np.sum(bias.astype(np.float64)))) < 2.5e-7  # Float32 rounding of values near 1
+
+
+def test_aux_free_update_balanced_and_empty(oracle):
+    # balanced counts: gradient 0, the momentum decays by `momentum` exactly and
+    # the bias moves by -lr * momentum; no entries > 0: nothing changes
+    idx = np.array([[1, 2], [3, 4], [2, 1], [4, 3]], np.int32)
+    bias = np.zeros(4, np.float32)
+    mom = np.array([0.5, -0.5, 0.25, -0.25], np.float32)
+    oracle.aux_free_update_bias(idx, bias, mom, 0.01, 0.9)
+    assert np.array_equal(mom, (np.float32(0.9) * np.array([0.5, -0.5, 0.25, -0.25], np.float32)))
+    assert np.allclose(bias, -0.01 * mom.astype(np.float64), rtol=1e-6)
+    b0, m0 = bias.copy(), mom.copy()
+    oracle.aux_free_update_bias(np.zeros((3, 2), np.int32), bias, mom, 0.01, 0.9)
+    assert np.array_equal(bias, b0) and np.array_equal(mom, m0)
+
+
+def test_aux_free_forward_regates_on_biased_logits(oracle):
+    # a large bias on expert 2 puts it in slot 1 for every token while the
+    # probabilities stay those of the plain logits; the update runs every
+    # update_freq-th training call; the balance loss is cw * Switch(1)
+    rng = np.random.default_rng(25)
+    T, D, H, E = 40, 16, 24, 4
+    x, ex = _shared_case(rng, T, D, H, E)
+    wr = (rng.standard_normal((E, D)) * 0.5).astype(np.float32)
+    st = dict(bias=np.array([0, 100, 0, 0], np.float32), mom=np.zeros(E, np.float32), lr=0.01, momentum=0.9,
+              update_freq=2, counter=0, use_comp=True, cw=0.001)
+    out, loss, aux = oracle.moe_forward(x, wr, ex, k=2, training=True, z_weight=0.0, aux_free=st)
+    plain = oracle.moe_forward(x, wr, ex, k=2, training=True, z_weight=0.0)[2]
+    assert np.all(aux["idx"][:, 0] == 2)
+    assert np.array_equal(aux["probs"], plain["probs"])
+    assert st["counter"] == 1 and np.all(st["mom"] == 0)  # first call: no update (freq 2)
+    assert loss == np.float32(np.float32(0.001) * oracle.switch_loss(aux["idx"], aux["probs"], 1.0))
+    oracle.moe_forward(x, wr, ex, k=2, training=True, z_weight=0.0, aux_free=st)
+    assert st["counter"] == 2 and st["mom"][1] > 0 and st["bias"][1] < 100  # expert 2 overloaded: pushed down
+    oracle.moe_forward(x, wr, ex, k=2, training=False, aux_free=st)
+    assert st["counter"] == 2  # inference calls do not count
+
+
 # ---- dtype helpers -----------------------------------------------------------
 
 def test_bf16_rounding_matches_torch(oracle):
