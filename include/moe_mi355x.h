@@ -59,8 +59,23 @@ typedef enum { MOE_EXPERT_GATED = 0, MOE_EXPERT_STANDARD = 1 } moe_expert_type;
 typedef enum { MOE_ACT_GELU = 0, MOE_ACT_SILU = 1, MOE_ACT_RELU = 2, MOE_ACT_IDENTITY = 3 } moe_activation;
 
 /* Gating mechanism (src/gating/topk.jl:16-22, switch.jl:7-11,
- * advanced.jl:74-108). */
-typedef enum { MOE_GATE_TOPK = 0, MOE_GATE_SWITCH = 1, MOE_GATE_SHARED = 2 } moe_gate_kind;
+ * advanced.jl:7-108, expert_choice.jl:7-53).
+ * SOFT: SoftMoEGating(k, lambda): softmax of logits ./ lambda, top-k indices,
+ *   and, as the reference's dispatch reads gates[slot, t] of its (E, T) gate
+ *   matrix, slot j's gate is the probability of expert j (advanced.jl:17-33).
+ * EXPERT_CHOICE: ExpertChoiceGating(capacity_factor): each expert takes the
+ *   capacity = ceil(T * cf / E) tokens of largest logit (ties to the lower
+ *   token), gate = its softmax probability; a token's slots hold the experts
+ *   that took it in ascending id order, at most capacity of them
+ *   (expert_choice.jl:11-53).  Slots per token: min(E, 8); a call whose
+ *   min(capacity, E) exceeds 8 is MOE_EUNSUPPORTED. */
+typedef enum {
+    MOE_GATE_TOPK = 0,
+    MOE_GATE_SWITCH = 1,
+    MOE_GATE_SHARED = 2,
+    MOE_GATE_SOFT = 3,
+    MOE_GATE_EXPERT_CHOICE = 4
+} moe_gate_kind;
 
 /* Mirror of MoEConfig (src/core/moe_layer.jl:4-29) plus device sizing. */
 typedef struct {
@@ -83,7 +98,9 @@ typedef struct {
                                    token (forward_with_shared_experts,
                                    src/core/moe_layer.jl:158-185); the router then has
                                    num_experts - ns outputs.  TopK / Switch gates only. */
-    int32_t reserved[6];        /* zero */
+    float gate_param;           /* SoftMoEGating.lambda (SOFT), ExpertChoiceGating.capacity_factor
+                                   (EXPERT_CHOICE); unused otherwise */
+    int32_t reserved[5];        /* zero */
 } moe_config;
 
 typedef struct moe_handle moe_handle;
@@ -184,6 +201,19 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
  * ids (ids above E - ns are not counted, src/balancing/losses.jl:22-26). */
 int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
                 float *out, float *loss, moe_forward_aux *aux);
+
+/* forward_standard with the gate's compute_gates done by the caller
+ * (src/core/moe_layer.jl:130-156 with process_expert_forward!, :187-219): for
+ * gates whose indices come from host code -- HashGating's hash function,
+ * RandomGating's sampler (src/gating/advanced.jl:37-66, simple.jl:7-28).
+ * The router GEMM still runs (logits for aux and the z-loss); indices [T][kd]
+ * 1-based (ids outside 1..E are skipped, :198; an id repeated within a token
+ * is MOE_EUNSUPPORTED), gates [T][kd], probs [T][E] for the Switch loss and
+ * the statistics (NULL: ones ./ E).  The capacity constraint applies as in
+ * moe_forward.  kd <= MOE_MAX_TOPK and T * kd <= max_tokens * slots. */
+int moe_forward_routed(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
+                       const int32_t *indices, const float *gates, int32_t kd, const float *probs, float *out,
+                       float *loss, moe_forward_aux *aux);
 
 /* (e::Expert)(x) on a block of tokens -- src/experts/gated.jl:29-34,
  * src/experts/standard.jl:38-55.  x [n][D] fp32 -> y [n][D_out] fp32 through

@@ -10,7 +10,7 @@ import numpy as np
 
 from . import _lib
 
-GateSpec = namedtuple("GateSpec", "kind k num_shared")
+GateSpec = namedtuple("GateSpec", "kind k num_shared param", defaults=(0.0,))
 
 
 def _ptr(a):
@@ -38,6 +38,7 @@ class DeviceLayer:
         c.drop_tokens = int(bool(drop_tokens))
         c.max_tokens = max_tokens
         c.num_shared_experts = int(num_shared_experts)
+        c.gate_param = float(gate.param)
         self.cfg = c
         self.max_tokens = max_tokens
         self.num_experts = num_experts
@@ -111,32 +112,57 @@ class DeviceLayer:
         T = x_TD.shape[0]
         out = np.zeros((T, self.output_dim), dtype=np.float32)
         loss = ctypes.c_float(0.0)
-        aux = _lib.MoeForwardAux()
-        res = {}
-        counts = np.zeros(self.num_experts, dtype=np.int32)
-        ent = np.zeros(1, dtype=np.float32)
-        sw = np.zeros(1, dtype=np.float32)
-        zl = np.zeros(1, dtype=np.float32)
-        aux.counts = counts.ctypes.data
-        aux.mean_entropy = ent.ctypes.data
-        aux.switch_loss = sw.ctypes.data
-        aux.z_loss = zl.ctypes.data
-        if want_aux:
-            res["logits"] = np.zeros((T, self.router_outputs), dtype=np.float32)
-            res["probs"] = np.zeros((T, self.router_outputs), dtype=np.float32)
-            res["indices"] = np.zeros((T, self.slots), dtype=np.int32)
-            res["gates"] = np.zeros((T, self.slots), dtype=np.float32)
-            res["offsets"] = np.zeros(self.num_experts + 1, dtype=np.int32)
-            res["perm"] = np.zeros(T * self.slots, dtype=np.int32)
-            for k in ("logits", "probs", "indices", "gates", "offsets", "perm"):
-                setattr(aux, k, res[k].ctypes.data)
+        aux, res, keep = self._aux(T, self.slots, want_aux)
         _lib.check(
             _lib.lib().moe_forward(self.h, x_TD.ctypes.data, int(x_dtype), T, int(bool(training)), out.ctypes.data,
                                    ctypes.byref(loss), ctypes.byref(aux)),
             self.h,
         )
-        res.update(counts=counts, mean_entropy=float(ent[0]), switch_loss=float(sw[0]), z_loss=float(zl[0]))
-        return out, float(np.float32(loss.value)), res
+        return out, float(np.float32(loss.value)), self._aux_result(res, keep)
+
+    def forward_routed(self, x_TD, x_dtype, training, idx_Tk, gates_Tk, probs_TE=None, want_aux=False):
+        """moe_forward_routed: the layer forward on the caller's routing."""
+        T = x_TD.shape[0]
+        idx = np.ascontiguousarray(idx_Tk, dtype=np.int32)
+        gates = np.ascontiguousarray(gates_Tk, dtype=np.float32)
+        kd = idx.shape[1]
+        probs = None if probs_TE is None else np.ascontiguousarray(probs_TE, dtype=np.float32)
+        out = np.zeros((T, self.output_dim), dtype=np.float32)
+        loss = ctypes.c_float(0.0)
+        aux, res, keep = self._aux(T, kd, want_aux)
+        _lib.check(
+            _lib.lib().moe_forward_routed(self.h, x_TD.ctypes.data, int(x_dtype), T, int(bool(training)),
+                                          idx.ctypes.data, gates.ctypes.data, kd, _ptr(probs), out.ctypes.data,
+                                          ctypes.byref(loss), ctypes.byref(aux)),
+            self.h,
+        )
+        return out, float(np.float32(loss.value)), self._aux_result(res, keep)
+
+    def _aux(self, T, slots, want_aux):
+        aux = _lib.MoeForwardAux()
+        res = {}
+        keep = dict(counts=np.zeros(self.num_experts, dtype=np.int32), ent=np.zeros(1, dtype=np.float32),
+                    sw=np.zeros(1, dtype=np.float32), zl=np.zeros(1, dtype=np.float32))
+        aux.counts = keep["counts"].ctypes.data
+        aux.mean_entropy = keep["ent"].ctypes.data
+        aux.switch_loss = keep["sw"].ctypes.data
+        aux.z_loss = keep["zl"].ctypes.data
+        if want_aux:
+            res["logits"] = np.zeros((T, self.router_outputs), dtype=np.float32)
+            res["probs"] = np.zeros((T, self.router_outputs), dtype=np.float32)
+            res["indices"] = np.zeros((T, slots), dtype=np.int32)
+            res["gates"] = np.zeros((T, slots), dtype=np.float32)
+            res["offsets"] = np.zeros(self.num_experts + 1, dtype=np.int32)
+            res["perm"] = np.zeros(T * slots, dtype=np.int32)
+            for k in ("logits", "probs", "indices", "gates", "offsets", "perm"):
+                setattr(aux, k, res[k].ctypes.data)
+        return aux, res, keep
+
+    @staticmethod
+    def _aux_result(res, keep):
+        res.update(counts=keep["counts"], mean_entropy=float(keep["ent"][0]), switch_loss=float(keep["sw"][0]),
+                   z_loss=float(keep["zl"][0]))
+        return res
 
     def expert_forward(self, e, x_nD):
         x = np.ascontiguousarray(x_nD, dtype=np.float32)

@@ -27,7 +27,7 @@ MOE_F32, MOE_BF16, MOE_FP8_E4M3 = 0, 1, 2
 MOE_LAYOUT_FLUX_OUT_IN, MOE_LAYOUT_LLAMA_IN_OUT = 0, 1
 MOE_EXPERT_GATED, MOE_EXPERT_STANDARD = 0, 1
 MOE_ACT_GELU, MOE_ACT_SILU, MOE_ACT_RELU, MOE_ACT_IDENTITY = 0, 1, 2, 3
-MOE_GATE_TOPK, MOE_GATE_SWITCH, MOE_GATE_SHARED = 0, 1, 2
+MOE_GATE_TOPK, MOE_GATE_SWITCH, MOE_GATE_SHARED, MOE_GATE_SOFT, MOE_GATE_EXPERT_CHOICE = 0, 1, 2, 3, 4
 MOE_MAX_TOPK = 8
 MOE_MAX_EXPERTS = 128
 
@@ -39,7 +39,7 @@ EXPORTED_SYMBOLS = [
     "moe_forward_async", "moe_stage_router_async", "moe_stage_permute_async",
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
     "moe_read_counts", "moe_switch_loss", "moe_z_loss", "moe_decode", "moe_decode_async",
-    "moe_set_aux_free", "moe_get_aux_free", "moe_aux_free_update_bias",
+    "moe_set_aux_free", "moe_get_aux_free", "moe_aux_free_update_bias", "moe_forward_routed",
 ]
 
 
@@ -61,7 +61,8 @@ class MoeConfigC(ctypes.Structure):
         ("drop_tokens", ctypes.c_int32),
         ("max_tokens", ctypes.c_int32),
         ("num_shared_experts", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 6),
+        ("gate_param", ctypes.c_float),
+        ("reserved", ctypes.c_int32 * 5),
     ]
 
 
@@ -123,6 +124,7 @@ def lib():
     L.moe_compute_gates.argtypes = [vp, vp, i32, vp, vp, vp]
     L.moe_route_from_logits.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]
     L.moe_forward.argtypes = [vp, vp, i32, i32, i32, vp, f32p, ctypes.POINTER(MoeForwardAux)]
+    L.moe_forward_routed.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, vp, vp, f32p, ctypes.POINTER(MoeForwardAux)]
     L.moe_expert_forward.argtypes = [vp, i32, vp, i32, vp]
     L.moe_forward_async.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
     L.moe_stage_router_async.argtypes = [vp, vp, i32, i32, i32, vp]

@@ -1,6 +1,7 @@
 // moe_api.hip -- the C ABI of libmoe_mi355x.so (declared in moe_mi355x.h):
 // handle lifecycle, weight upload/prepack on the device, and the stage
 // orchestration of the MoE-layer forward pass on one HIP stream.
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdio>
@@ -25,6 +26,12 @@ struct moe_handle {
     // SharedExpertGating; lsh shared experts of the layer (num_shared_experts);
     // kt = lsh + ns + k slots per token
     int E = 0, Er = 0, Er_pad = 0, D = 0, H = 0, Dout = 0, k = 0, ns = 0, lsh = 0, kt = 0;
+    // slots per token of the current call (the stride of idx / gates / ranks):
+    // kt, or the caller's for moe_forward_routed; kl: slots the Switch loss
+    // divides by (the router's index rows: kt - lsh, ExpertChoice's capacity)
+    int kc = 0, kl = 0;
+    bool given = false, given_probs = false;  // the current call routes on the caller's indices
+    uint8_t *ec_sel = nullptr;                // ExpertChoiceGating selections [T][E]
     int D_pad = 0, H_pad = 0, Dout_npad = 0;
     int ct = CT_BF16, wt = WT_BF16;
     bool gated = true;
@@ -120,9 +127,15 @@ static int validate_config(const moe_config *c, std::string &why) {
         why = "num_shared_experts > 0 with SharedExpertGating has no device path";
         return 0;
     }
-    if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH) {
+    if ((c->gate_kind == MOE_GATE_SOFT || c->gate_kind == MOE_GATE_EXPERT_CHOICE) && lsh > 0) {
+        why = "num_shared_experts > 0 needs TopKGating or SwitchGating";
+        return 0;
+    }
+    if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH || c->gate_kind == MOE_GATE_SOFT) {
         if (k < 1 || k > c->num_experts - lsh) { why = "top_k must be in [1, num_experts - num_shared_experts]"; return 0; }
         if (lsh + k > MOE_MAX_TOPK) { why = "num_shared_experts + top_k above MOE_MAX_TOPK (8)"; return 0; }
+    } else if (c->gate_kind == MOE_GATE_EXPERT_CHOICE) {
+        if (!(c->gate_param > 0.0f)) { why = "ExpertChoiceGating capacity_factor (gate_param) must be > 0"; return 0; }
     } else if (c->gate_kind == MOE_GATE_SHARED) {
         const int ns = c->gate_num_shared;
         if (ns < 0 || ns >= c->num_experts) { why = "gate_num_shared must be in [0, num_experts)"; return 0; }
@@ -132,7 +145,10 @@ static int validate_config(const moe_config *c, std::string &why) {
         why = "unknown gate_kind";
         return 0;
     }
-    const long long rows = (long long)c->max_tokens * (k + lsh + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0));
+    const int slots = (c->gate_kind == MOE_GATE_EXPERT_CHOICE)
+                          ? std::min(c->num_experts, MOE_MAX_TOPK)
+                          : k + lsh + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0);
+    const long long rows = (long long)c->max_tokens * slots;
     if (rows > INT_MAX / 2) { why = "max_tokens * slots too large"; return 0; }
     return 1;
 }
@@ -350,7 +366,7 @@ static int check_ready(moe_handle *h) {
 }
 
 static int m_tiles_for(const moe_handle *h, int T) {
-    long long mt = (long long)T * h->kt / h->bm + h->E;
+    long long mt = (long long)T * h->kc / h->bm + h->E;
     if (mt > h->max_tiles) mt = h->max_tiles;
     return (int)mt;
 }
@@ -363,7 +379,7 @@ static bool drop_active(const moe_handle *h) { return h->cfg.drop_tokens && h->l
 
 static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
     PermuteArgs pa{};
-    pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kt; pa.E = h->E;
+    pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kc; pa.E = h->E;
     pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base;
     pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && drop_active(h)) ? 1 : 0;
     pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
@@ -378,7 +394,8 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
 // counts one compute_loss call for the bias update (auxiliary_free.jl:36-40).
 static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
                        int permute_mode, float *loss_dev, hipStream_t s) {
-    const bool aux = compute_logits && h->aux_free;
+    const bool aux = compute_logits && h->aux_free && !h->given;
+    const bool ec = h->cfg.gate_kind == MOE_GATE_EXPERT_CHOICE && !h->given;
     bool aux_update = false;
     if (aux && training) {
         ++h->aux_counter;
@@ -399,7 +416,8 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     }
     ra.part = h->logits_part; ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->Er; ra.Eh = h->E;
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
-    ra.k = h->k; ra.ns = h->ns; ra.kt = h->kt; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
+    ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
+    ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
     if (aux) {
         ra.out_mask = ROUTE_OUT_PROBS;
@@ -408,15 +426,22 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         ra.nks = 1;
         ra.bias = h->aux_bias;
         ra.out_mask = ROUTE_OUT_GATING;
+    } else if (ec) {
+        // softmax pass, the experts' choices, then a gating pass on them
+        ra.out_mask = ROUTE_OUT_PROBS;
+        HIP_TRY(h, launch_route(ra, s));
+        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates, s));
+        ra.given = 1;
+        ra.out_mask = ROUTE_OUT_GATING;
     } else {
         ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
     }
     HIP_TRY(h, launch_route(ra, s));
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
-    sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kt;
+    sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
-    sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kt - h->lsh;
+    sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
     sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
@@ -493,8 +518,26 @@ static int run_experts(moe_handle *h, int T, hipStream_t s) {
 static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
     CombineArgs c{};
     c.y = h->y; c.ld_y = h->Dout; c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
-    c.T = T; c.D = h->Dout; c.kt = h->kt; c.lsh = h->lsh; c.out = out_dev;
+    c.T = T; c.D = h->Dout; c.kt = h->kc; c.lsh = h->lsh; c.out = out_dev;
     HIP_TRY(h, launch_combine(c, s));
+    return MOE_OK;
+}
+
+// Slots of a call routed by the handle's own gate: kt per token, and the
+// Switch loss's index rows (ExpertChoiceGating: its capacity
+// ceil(Int, T * capacity_factor / E) in Float32, expert_choice.jl:13).
+static int begin_call(moe_handle *h, int T) {
+    h->given = false;
+    h->given_probs = false;
+    h->kc = h->kt;
+    h->kl = h->kt - h->lsh;
+    if (h->cfg.gate_kind == MOE_GATE_EXPERT_CHOICE) {
+        const float c = ceilf(((float)T * h->cfg.gate_param) / (float)h->E);
+        const long long C = (c >= 2147483647.0f) ? INT_MAX : (long long)c;
+        if (std::min<long long>(C, h->E) > MOE_MAX_TOPK)
+            return fail(h, MOE_EUNSUPPORTED, "ExpertChoiceGating: min(capacity, num_experts) above MOE_MAX_TOPK (8)");
+        h->kl = (int)C;
+    }
     return MOE_OK;
 }
 
@@ -505,6 +548,10 @@ static int forward_locked(moe_handle *h, const void *x_dev, int x_dtype, int T, 
     if (x_dtype != MOE_F32 && x_dtype != MOE_BF16) return fail(h, MOE_EINVAL, "x_dtype must be F32 or BF16");
     if (T < 1 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [1, max_tokens]");
     if (!x_dev || !out_dev) return fail(h, MOE_EINVAL, "null buffer");
+    if (!h->given) {
+        r = begin_call(h, T);
+        if (r != MOE_OK) return r;
+    }
     const int xb = x_dtype == MOE_BF16;
     r = run_routing(h, x_dev, xb, T, training, true, PERMUTE_ROWS, loss_dev, s);
     if (r != MOE_OK) return r;
@@ -556,9 +603,11 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->D = cfg->input_dim;
     h->H = cfg->hidden_dim;
     h->Dout = cfg->output_dim;
-    h->k = (cfg->gate_kind == MOE_GATE_SWITCH) ? 1 : cfg->top_k;
+    h->k = (cfg->gate_kind == MOE_GATE_SWITCH || cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) ? 1 : cfg->top_k;
     h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
-    h->kt = h->lsh + h->ns + h->k;
+    h->kt = (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) ? std::min(h->E, MOE_MAX_TOPK) : h->lsh + h->ns + h->k;
+    h->kc = h->kt;
+    h->kl = h->kt - h->lsh;
     h->D_pad = (int)round_up(h->D, kKPad);
     // N of the up GEMM, K of the down GEMM: a whole number of up-GEMM tiles
     h->H_pad = (int)round_up(h->H, cfg->expert_type == MOE_EXPERT_GATED ? kNPadGated : kNPad);
@@ -635,6 +684,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->num_tiles, sizeof(int));
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
+    if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
     A((void **)&h->aux_mom, sizeof(float) * h->Er);
     A((void **)&h->perm, sizeof(int) * T * kt);
@@ -816,10 +866,12 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     }
     hipStream_t s = h->stream;
     h->last_T = -1;  // routing state no longer matches a forward call
-    HIP_TRY(h, hipMemcpyAsync(h->logits_part, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
-    int r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
+    int r = begin_call(h, T);
     if (r != MOE_OK) return r;
-    const size_t nk = (size_t)T * h->kt;
+    HIP_TRY(h, hipMemcpyAsync(h->logits_part, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
+    r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
+    if (r != MOE_OK) return r;
+    const size_t nk = (size_t)T * h->kc;
     if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
     if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * nk, hipMemcpyDeviceToHost, s));
     if (probs) HIP_TRY(h, hipMemcpyAsync(probs, h->probs, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
@@ -830,10 +882,59 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     return MOE_OK;
 }
 
+static int forward_host_locked(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
+                               float *out, float *loss, moe_forward_aux *aux);
+
 int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training, float *out, float *loss,
                 moe_forward_aux *aux) {
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
     std::lock_guard<std::mutex> lk(h->mu);
+    h->given = false;
+    return forward_host_locked(h, x, x_dtype, T, training, out, loss, aux);
+}
+
+int moe_forward_routed(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
+                       const int32_t *indices, const float *gates, int32_t kd, const float *probs, float *out,
+                       float *loss, moe_forward_aux *aux) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (T < 0 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [0, max_tokens]");
+    if (kd < 1 || kd > MOE_MAX_TOPK) return fail(h, MOE_EINVAL, "slots per token must be in [1, MOE_MAX_TOPK]");
+    if ((long long)T * kd > h->rows_max) return fail(h, MOE_EINVAL, "T * slots exceeds the handle's max_tokens * slots");
+    if (h->lsh > 0) return fail(h, MOE_EUNSUPPORTED, "routed forward with num_shared_experts > 0");
+    if (h->aux_free) return fail(h, MOE_EUNSUPPORTED, "routed forward with an AuxiliaryFreeLoss");
+    if (T > 0 && (!indices || !gates)) return fail(h, MOE_EINVAL, "null indices or gates");
+    // an expert listed twice for one token would be computed twice in the
+    // reference; the bucketing here assumes distinct ids per token
+    for (int t = 0; t < T; ++t)
+        for (int i = 0; i < kd; ++i) {
+            const int e = indices[(size_t)t * kd + i];
+            if (e < 1 || e > h->E) continue;
+            for (int j = i + 1; j < kd; ++j)
+                if (indices[(size_t)t * kd + j] == e)
+                    return fail(h, MOE_EUNSUPPORTED, "an expert id repeated within one token's slots");
+        }
+    h->given = true;
+    h->given_probs = probs != nullptr;
+    h->kc = kd;
+    h->kl = kd;
+    hipStream_t s = h->stream;
+    if (T > 0) {
+        HIP_TRY(h, hipMemcpyAsync(h->idx, indices, sizeof(int) * (size_t)T * kd, hipMemcpyHostToDevice, s));
+        HIP_TRY(h, hipMemcpyAsync(h->gates, gates, sizeof(float) * (size_t)T * kd, hipMemcpyHostToDevice, s));
+        if (probs)
+            HIP_TRY(h, hipMemcpyAsync(h->probs, probs, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
+    }
+    const int r = forward_host_locked(h, x, x_dtype, T, training, out, loss, aux);
+    h->given = false;
+    h->kc = h->kt;
+    h->kl = h->kt - h->lsh;
+    h->last_T = -1;  // the stage entry points replay the handle's own gate only
+    return r;
+}
+
+static int forward_host_locked(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
+                               float *out, float *loss, moe_forward_aux *aux) {
     if (T < 0 || T > h->T_max) return fail(h, MOE_EINVAL, "T must be in [0, max_tokens]");
     if (T == 0) {
         // empty batch: zero-size output; loss 0 (inference) or NaN (means over no tokens)
@@ -858,7 +959,7 @@ int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_
     HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, sizeof(float) * (size_t)T * h->Dout, hipMemcpyDeviceToHost, s));
     float sc[4] = {0, 0, 0, 0};
     HIP_TRY(h, hipMemcpyAsync(sc, h->scalars, sizeof(float) * 4, hipMemcpyDeviceToHost, s));
-    const size_t nk = (size_t)T * h->kt;
+    const size_t nk = (size_t)T * h->kc;
     if (aux) {
         if (aux->logits) HIP_TRY(h, hipMemcpyAsync(aux->logits, h->logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));
         if (aux->probs) HIP_TRY(h, hipMemcpyAsync(aux->probs, h->probs, sizeof(float) * (size_t)T * h->Er, hipMemcpyDeviceToHost, s));

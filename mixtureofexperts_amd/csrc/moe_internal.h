@@ -150,6 +150,9 @@ struct RouteArgs {
     int gate_kind, k, ns, kt;
     int lsh;               // shared experts of the layer (slots 0..lsh-1 of every token)
     int out_mask;          // ROUTE_OUT_*: which outputs this pass writes
+    float soft_lambda;     // SoftMoEGating: the softmax runs on logits / lambda
+    int given;             // idx / gates hold the caller's routing (no top-k); probs from
+    int given_probs;       //   a.probs when given_probs, else 1/E
     float *probs;          // [T][E]
     int *idx;              // [T][kt]
     float *gates;          // [T][kt]
@@ -282,6 +285,10 @@ hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s);
 void router_plan(RouterArgs &r);
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
+// ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
+// gates [T][kt] (kt >= min(C, E))
+hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
+                                int *idx, float *gates, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,

@@ -277,6 +277,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock], zsum[kRouteBlock];
     __shared__ double hsum[kRouteBlock];
     const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
+    const bool soft = a.gate_kind == MOE_GATE_SOFT;
+    const bool zsep = shared_gate || soft;  // z-loss from a softmax of its own (all rows, unscaled)
+    const bool out_probs = (a.out_mask & ROUTE_OUT_PROBS) != 0;
+    const bool out_gating = (a.out_mask & ROUTE_OUT_GATING) != 0;
+    // a gating pass on the caller's routing needs none of the softmax phases
+    const bool softmax = out_probs || !a.given;
     const int EM = max(a.Er, a.E);
     const int RW = route_rw(EM);
     float *lrow = (float *)rdyn;            // [kRouteBlock][RW] logits
@@ -300,6 +306,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     // (1) router logits: the K-slice partial sums in slice order, then the
     // bias.  Elements q = tid + 256 u; the slices (and biases) of 4 elements
     // are loaded, from clamped addresses, before any is summed.
+    if (softmax) {
     const int nq = ntok * a.Er;
     const long long sstride = (long long)a.T * a.Er;
     for (int q0 = 0; q0 < nq; q0 += 4 * kRouteThreads) {
@@ -337,7 +344,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         if (rvalid)
             for (int i = rs; i < EM; i += TPT) {
                 const float v = lrow[rt * RW + i];
-                if (i >= ns && i < a.E && v > m) m = v;
+                const float sv = soft ? v / a.soft_lambda : v;  // logits ./ lambda (advanced.jl:18)
+                if (i >= ns && i < a.E && sv > m) m = sv;
                 if (i < a.Er && v > mz) mz = v;
             }
         m = token_max<TPT>(m);
@@ -356,12 +364,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             const float m = rmax[rt], mz = zmax[rt];
             for (int i = rs; i < a.Er; i += TPT) {
                 const float v = lrow[rt * RW + i];
+                const float sv = soft ? v / a.soft_lambda : v;
                 if (i >= ns && i < a.E)
-                    prow[rt * RW + i] = (m == INFINITY) ? ((v == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(v - m));
-                if (shared_gate) zs = zs + (float)exp((double)(v - mz));
+                    prow[rt * RW + i] = (m == INFINITY) ? ((sv == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv - m));
+                if (zsep) zs = zs + (float)exp((double)(v - mz));
             }
         }
-        if (shared_gate) {
+        if (zsep) {
             zs = token_sum<TPT>(zs);
             if (rvalid && rs == 0) zsum[rt] = zs;
         }
@@ -392,7 +401,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             const float s = rsum[rt];
             for (int i = rs; i < a.E; i += TPT) {
                 float pv;
-                if (i < ns) {
+                if (a.given) {
+                    // the caller's gate: its probabilities, or ones ./ E
+                    pv = a.given_probs ? a.probs[(long long)(t0 + rt) * a.E + i] : 1.0f / (float)a.E;
+                } else if (i < ns) {
                     pv = 1.0f / (float)a.E;
                 } else {
                     const float pu = prow[rt * RW + i] / s;
@@ -408,6 +420,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         if (rvalid && rs == 0) hsum[rt] = hs;
     }
     __syncthreads();
+    }  // softmax phases
 
     int ex[MOE_MAX_TOPK];     // 1-based expert ids of this token's slots
     float gx[MOE_MAX_TOPK];   // their gates
@@ -419,11 +432,42 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
 
     // (6) per token: top-k and gates, logsumexp, entropy
-    if (valid) {
+    if (valid && a.given) {
+        // the caller's routing: ids outside 1..E are skipped, as the
+        // dispatch's `expert_id > 0 && expert_id <= length(experts)` does
+        // (src/core/moe_layer.jl:198)
+#pragma unroll
+        for (int j = 0; j < MOE_MAX_TOPK; ++j)
+            if (j < a.kt) {
+                const long long ent = (long long)t * a.kt + j;
+                const int e = a.idx[ent];
+                ex[j] = (e >= 1 && e <= a.Eh) ? e : 0;
+                gx[j] = a.gates[ent];
+            }
+        if (softmax) {
+            const float lse = zsep ? zmax[tid] + (float)log((double)zsum[tid])
+                                   : rmax[tid] + (float)log((double)rsum[tid]);
+            zterm = (double)(lse * lse);
+            hterm = -hsum[tid];
+        }
+    } else if (valid) {
         float *p = prow + tid * RW;
         int sel[MOE_MAX_TOPK];
         float g[MOE_MAX_TOPK];
-        if (shared_gate) {
+        if (soft) {
+            // SoftMoEGating: top-k of the scaled-softmax probabilities; the
+            // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
+            // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
+            topk_row(p, a.E, a.k, sel, g);
+#pragma unroll
+            for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                if (j < a.k) {
+                    ex[j] = sel[j] + 1;
+                    gx[j] = p[j];
+                }
+            const float lse = zmax[tid] + (float)log((double)zsum[tid]);
+            zterm = (double)(lse * lse);
+        } else if (shared_gate) {
             // top-k and gates on the routed probabilities as the base gate
             // returns them (before the 1 - ns/E scaling); the row is read from
             // its 16-byte-aligned start with the first ns entries masked
@@ -538,8 +582,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
 
     // ---- outputs --------------------------------------------------------------
-    const bool out_probs = (a.out_mask & ROUTE_OUT_PROBS) != 0;
-    const bool out_gating = (a.out_mask & ROUTE_OUT_GATING) != 0;
     if (out_probs) {
         for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
             const int tt = q / a.Er, i = q - tt * a.Er;
@@ -599,6 +641,104 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
         big_lds = true;
     }
     hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+// ============================================================================
+// ExpertChoiceGating (src/gating/expert_choice.jl:11-53).
+// ============================================================================
+// Block e: expert e takes the min(C, T) tokens of largest logit,
+// partialsortperm(scores[:, e], 1:C, rev=true): Julia's isless order (NaN
+// largest), ties to the lower token.  A 4-pass 8-bit radix select finds the
+// C-th largest key K and how many tokens of key K to take; the tokens of key
+// > K and the first of key == K in token order are marked in sel[t][e].
+__global__ __launch_bounds__(256) void expert_choice_select_kernel(const float *__restrict__ logits, int T, int E,
+                                                                   int C, uint8_t *__restrict__ sel) {
+    __shared__ unsigned hist[256];
+    __shared__ unsigned s_prefix, s_rem;
+    __shared__ unsigned wties[4];
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t prefix = 0, mask = 0;
+    unsigned rem = (unsigned)min(C, T);
+    for (int pos = 24; pos >= 0; pos -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
+        for (int t = tid; t < T; t += 256) {
+            const uint32_t key = isless_key(logits[(long long)t * E + e]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> pos) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            unsigned cum = 0;
+            int d = 255;
+            for (; d > 0; --d) {
+                if (cum + hist[d] >= rem) break;
+                cum += hist[d];
+            }
+            s_prefix = prefix | ((uint32_t)d << pos);
+            s_rem = rem - cum;
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        rem = s_rem;
+        mask |= 255u << pos;
+    }
+    // take key > K, and the first `rem` tokens of key == K in token order
+    unsigned ties_before = 0;
+    for (int t0 = 0; t0 < T; t0 += 256) {
+        const int t = t0 + tid;
+        const uint32_t key = (t < T) ? isless_key(logits[(long long)t * E + e]) : 0u;
+        const bool eq = t < T && key == prefix;
+        const uint64_t b = __ballot(eq);
+        if (lane == 0) wties[wave] = __popcll(b);
+        __syncthreads();
+        unsigned r = ties_before + __popcll(b & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+        for (int w = 0; w < wave; ++w) r += wties[w];
+        if (t < T) sel[(long long)t * E + e] = (key > prefix || (eq && r < rem)) ? 1 : 0;
+        ties_before += wties[0] + wties[1] + wties[2] + wties[3];
+        __syncthreads();
+    }
+}
+
+// One thread per token: its slots hold the experts that took it in ascending
+// id order, at most kcap = min(C, E) of them (a later expert past the
+// capacity rows is left out, expert_choice.jl:40-50), gate = probability of
+// the expert for the token; the remaining slots of the kt are empty (id 0).
+__global__ __launch_bounds__(256) void expert_choice_assemble_kernel(const uint8_t *__restrict__ sel,
+                                                                     const float *__restrict__ probs, int T, int E,
+                                                                     int kt, int kcap, int *idx, float *gates) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    int ids[MOE_MAX_TOPK];
+    float gs[MOE_MAX_TOPK];
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_TOPK; ++j) { ids[j] = 0; gs[j] = 0.0f; }
+    int c = 0;
+    for (int e = 0; e < E; ++e) {
+        if (sel[(long long)t * E + e]) {
+#pragma unroll
+            for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                if (j == c && c < kcap) {
+                    ids[j] = e + 1;
+                    gs[j] = probs[(long long)t * E + e];
+                }
+            ++c;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_TOPK; ++j)
+        if (j < kt) {
+            idx[(long long)t * kt + j] = ids[j];
+            gates[(long long)t * kt + j] = gs[j];
+        }
+}
+
+hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
+                                int *idx, float *gates, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
+    hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
+                       min(C, E), idx, gates);
     return hipGetLastError();
 }
 

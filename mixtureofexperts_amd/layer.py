@@ -16,7 +16,7 @@ from ._device import DeviceLayer
 from .activations import activation_code, gelu
 from .balancing import AuxiliaryFreeLoss, LoadBalancingLoss, SwitchTransformerLoss, balance_alpha
 from .experts import GatedExpert, StandardExpert
-from .gating import GatingMechanism, TopKGating, gate_spec
+from .gating import HOST_ROUTED_GATES, GatingMechanism, TopKGating, gate_spec
 
 _DTYPES = {"f32": _lib.MOE_F32, "fp32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3,
            "fp8_e4m3": _lib.MOE_FP8_E4M3}
@@ -174,7 +174,14 @@ class MoELayer:
         aux_free = self.balance_loss if isinstance(self.balance_loss, AuxiliaryFreeLoss) else None
         if aux_free is not None:
             dev.set_aux_free(aux_free)
-        out, loss, res = dev.forward(xt, xcode, training, want_aux=_aux is not None)
+        gate = self.router.gate_type
+        if isinstance(gate, HOST_ROUTED_GATES):
+            # the gate's indices come from host code (a hash function, a
+            # sampler); the device runs the rest of forward_standard on them
+            idx, gates = gate.host_routing(T, self.router.weight.shape[0])
+            out, loss, res = dev.forward_routed(xt, xcode, training, idx, gates, None, want_aux=_aux is not None)
+        else:
+            out, loss, res = dev.forward(xt, xcode, training, want_aux=_aux is not None)
         if aux_free is not None:
             dev.get_aux_free(aux_free)
         if _aux is not None:

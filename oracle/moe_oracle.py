@@ -101,6 +101,48 @@ def compute_gates_shared(logits_TE, num_shared, k):
     return idx, g, p
 
 
+def compute_gates_soft(logits_TE, k, lam):
+    """SoftMoEGating(k, lambda) -- advanced.jl:17-33: probs = softmax(logits ./
+    lambda), indices = top-k of probs; the returned gate matrix is probs, so
+    the dispatch's gates[slot, t] is the probability of expert `slot`.
+    Returns (idx [T][k], slot gates [T][k], probs [T][E])."""
+    lg = _c(logits_TE, np.float32)
+    scaled = (lg / np.float32(lam)).astype(np.float32)
+    idx, _, probs = compute_gates_topk(scaled, k)
+    return idx, np.ascontiguousarray(probs[:, :k]), probs
+
+
+def expert_choice_capacity(T, E, capacity_factor):
+    """ceil(Int, batch_size * capacity_factor / num_experts) in Float32."""
+    return int(np.ceil(np.float32(np.float32(T) * np.float32(capacity_factor)) / np.float32(E)))
+
+
+def compute_gates_expert_choice(logits_TE, capacity_factor):
+    """ExpertChoiceGating -- expert_choice.jl:11-53, by full sorts: expert e
+    takes the first min(C, T) tokens of sortperm(scores[:, e], rev=true) with
+    Julia's isless order (NaN largest) and ties to the lower token; token t's
+    slots list the experts that took it in ascending id order, at most C.
+    Returns (idx [T][C], gates [T][C], probs [T][E])."""
+    lg = _c(logits_TE, np.float32)
+    T, E = lg.shape
+    C = expert_choice_capacity(T, E, capacity_factor)
+    probs = softmax(lg)
+    idx = np.zeros((T, C), np.int32)
+    g = np.zeros((T, C), np.float32)
+    cnt = np.zeros(T, np.int64)
+    for e in range(E):
+        col = lg[:, e]
+        nan = np.isnan(col)
+        # descending isless: NaN first, then by value descending, ties by token ascending
+        order = np.lexsort((np.arange(T), -np.where(nan, 0, col).astype(np.float64), ~nan))
+        for t in order[:min(C, T)]:
+            cnt[t] += 1
+            if cnt[t] <= C:
+                idx[t, cnt[t] - 1] = e + 1
+                g[t, cnt[t] - 1] = probs[t, e]
+    return idx, g, probs
+
+
 def capacity(idx, gates, num_experts, capacity_factor):
     """apply_capacity_constraint (in place on copies) -- moe_layer.jl:221-248."""
     idx = _c(idx, np.int32).copy()
@@ -222,12 +264,15 @@ def aux_free_update_bias(idx, bias, mom, lr, momentum):
 
 def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, expert_type="gated", act="silu",
                 alpha=0.01, z_weight=0.001, training=False, drop_tokens=False, capacity_factor=1.25,
-                router_bias=None, logits=None, aux_free=None):
+                router_bias=None, logits=None, aux_free=None, gate_param=None, given=None):
     """forward_standard + the z-loss of MoELayer's call (moe_layer.jl:107-156).
 
     x_TD: [T][D] float32.  router_w_ED: (E, D) Flux weight.  experts: list of
     dicts with fp32 "w1","w2"(,"w3") in (out, in) shape (+ "b1","b2").
-    ``logits`` may be given to route identical logits.  ``aux_free``: the
+    ``logits`` may be given to route identical logits.  ``gate``: "topk",
+    "switch", "shared", "soft" (gate_param = lambda) or "expert_choice"
+    (gate_param = capacity factor); ``given`` = (indices, gates, probs or
+    None) replaces compute_gates (a gate computed by host code).  ``aux_free``: the
     state of an AuxiliaryFreeLoss balance loss (dict bias, mom, lr, momentum,
     update_freq, counter, use_comp, cw), updated in place: the gating runs on
     logits .+ bias (:137-140) and the balance loss is its compute_loss
@@ -244,9 +289,18 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
     def gating(lg):
         if gate == "shared":
             return compute_gates_shared(lg, num_shared, k)
+        if gate == "soft":
+            return compute_gates_soft(lg, k, gate_param)
+        if gate == "expert_choice":
+            return compute_gates_expert_choice(lg, gate_param)
         return compute_gates_topk(lg, 1 if gate == "switch" else k)
 
-    idx, gates, probs = gating(logits)
+    if given is not None:
+        idx, gates = np.asarray(given[0], np.int32), np.asarray(given[1], np.float32)
+        probs = given[2] if given[2] is not None else np.full((T, len(experts)), np.float32(1) / np.float32(
+            len(experts)), np.float32)
+    else:
+        idx, gates, probs = gating(logits)
     if aux_free is not None:
         idx, gates, _ = gating((logits + aux_free["bias"].reshape(1, -1)).astype(np.float32))
     if drop_tokens and training:

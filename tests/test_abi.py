@@ -69,6 +69,9 @@ def _cfg(**kw):
     (dict(num_shared_experts=7), "top_k"),
     (dict(num_shared_experts=2, top_k=7, num_experts=16), "MOE_MAX_TOPK"),
     (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1), "SharedExpertGating"),
+    (dict(gate_kind=4, gate_param=0.0), "capacity_factor"),
+    (dict(gate_kind=3, top_k=9), "top_k"),
+    (dict(gate_kind=3, num_shared_experts=1), "TopKGating or SwitchGating"),
 ])
 def test_create_rejects_bad_config(moe, bad, msg):
     from mixtureofexperts_amd import _lib
@@ -127,7 +130,14 @@ def test_host_mirror_rejects_unsupported_before_device(moe):
 def test_gate_spec_mapping(moe):
     from mixtureofexperts_amd import _lib
 
-    assert tuple(moe.gating.gate_spec(moe.TopKGating(3), 8)) == (_lib.MOE_GATE_TOPK, 3, 0)
-    assert tuple(moe.gating.gate_spec(moe.SwitchGating(), 8)) == (_lib.MOE_GATE_SWITCH, 1, 0)
+    assert tuple(moe.gating.gate_spec(moe.TopKGating(3), 8)) == (_lib.MOE_GATE_TOPK, 3, 0, 0.0)
+    assert tuple(moe.gating.gate_spec(moe.SwitchGating(), 8)) == (_lib.MOE_GATE_SWITCH, 1, 0, 0.0)
     g = moe.SharedExpertGating(2, moe.TopKGating(6), 66)
-    assert tuple(moe.gating.gate_spec(g, 66)) == (_lib.MOE_GATE_SHARED, 6, 2)
+    assert tuple(moe.gating.gate_spec(g, 66)) == (_lib.MOE_GATE_SHARED, 6, 2, 0.0)
+    assert tuple(moe.gating.gate_spec(moe.SoftMoEGating(2, 0.5), 8)) == (_lib.MOE_GATE_SOFT, 2, 0, 0.5)
+    assert tuple(moe.gating.gate_spec(moe.ExpertChoiceGating(1.25), 8)) == (_lib.MOE_GATE_EXPERT_CHOICE, 1, 0, 1.25)
+    # in a layer the router passes no `training` / noise logits: base gate / TopKGating(k)
+    assert tuple(moe.gating.gate_spec(moe.JitterGating(moe.SwitchGating(), 0.1), 8))[:3] == (_lib.MOE_GATE_SWITCH, 1, 0)
+    assert tuple(moe.gating.gate_spec(moe.StochasticTopKGating(3), 8))[:3] == (_lib.MOE_GATE_TOPK, 3, 0)
+    # host-routed gates run on a top-k handle of their k
+    assert tuple(moe.gating.gate_spec(moe.HashGating(2, 8), 8))[:3] == (_lib.MOE_GATE_TOPK, 2, 0)

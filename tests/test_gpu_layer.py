@@ -260,6 +260,85 @@ def test_aux_free_python_api(moe, oracle):
         moe.update_bias(l2, np.array([[E + 1]]))
 
 
+@pytest.mark.parametrize("gate,param,E,k,wdtype", [("soft", 0.5, 8, 2, "bf16"), ("soft", 1.0, 6, 3, "f32"),
+                                                    ("expert_choice", 1.25, 8, 0, "bf16"),
+                                                    ("expert_choice", 0.125, 16, 0, "f32")])
+def test_soft_and_expert_choice_layer(moe, oracle, gate, param, E, k, wdtype):
+    # the layer forward with SoftMoEGating / ExpertChoiceGating against the
+    # oracle on the GPU's logits: routing bit-exact, output and loss in tolerance
+    from mixtureofexperts_amd import _lib
+    from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+    rng = np.random.default_rng(70 + E)
+    T, D, H = 512, 128, 192
+    print(f"layer gate={gate} param={param} E={E} k={k} w={wdtype}", flush=True)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    wr = (rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)
+    ex, dev_w = [], []
+    for _ in range(E):
+        mats = [(rng.standard_normal(sh) * np.sqrt(2.0 / D)).astype(np.float32) for sh in ((H, D), (D, H), (H, D))]
+        if wdtype == "bf16":
+            bits = [oracle.f32_to_bf16_bits(m) for m in mats]
+            mats = [oracle.bf16_bits_to_f32(b) for b in bits]
+            dev_w.append((bits, _lib.MOE_BF16))
+        else:
+            dev_w.append((mats, _lib.MOE_F32))
+        ex.append(dict(w1=mats[0], w2=mats[1], w3=mats[2]))
+    kind = _lib.MOE_GATE_SOFT if gate == "soft" else _lib.MOE_GATE_EXPERT_CHOICE
+    dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED, input_dim=D, hidden_dim=H, output_dim=D,
+                      activation=_lib.MOE_ACT_SILU, gate=GateSpec(kind, k if k else 1, 0, param),
+                      weight_dtype={"bf16": _lib.MOE_BF16, "f32": _lib.MOE_F32}[wdtype], balance_alpha=0.01,
+                      z_loss_weight=0.001, capacity_factor=1.25, drop_tokens=False, max_tokens=T)
+    dev.set_router(np.ascontiguousarray(wr.T))
+    for e, (w, src) in enumerate(dev_w):
+        dev.set_expert(e, w[0], w[1], w[2], src_dtype=src)
+    out, loss, res = dev.forward(x, _lib.MOE_F32, True, want_aux=True)
+    ref, ref_loss, aux = oracle.moe_forward(x, wr, ex, gate=gate, k=k, gate_param=param, training=True,
+                                            logits=res["logits"])
+    kt = res["indices"].shape[1]
+    n = min(kt, aux["idx"].shape[1])
+    assert np.array_equal(res["indices"][:, :n], aux["idx"][:, :n])
+    assert np.all(aux["idx"][:, n:] == 0) and np.all(res["indices"][:, n:] == 0)
+    assert np.array_equal(res["gates"][:, :n].view(np.uint32), aux["gates"][:, :n].view(np.uint32))
+    assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32))
+    assert np.array_equal(res["counts"], aux["counts"])
+    # permutation: (token, slot) of each position (entry ids are t * slots + slot)
+    m = int(aux["offsets"][-1])
+    ko = aux["idx"].shape[1]
+    assert np.array_equal(np.divmod(res["perm"][:m], kt), np.divmod(aux["perm"], ko))
+    assert rel_err(out, ref) <= TOL[wdtype]
+    assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (loss, ref_loss)
+    dev.close()
+
+
+def test_host_routed_gates_layer(moe, oracle):
+    # HashGating / RandomGating in a layer: indices from host code, the rest of
+    # forward_standard on the device (moe_forward_routed), capacity included
+    rng = np.random.default_rng(80)
+    for gate, drop in ((moe.HashGating(2, 8, hash_fn=lambda i: 3 * i + i // 7), False),
+                       (moe.RandomGating(3, rng=np.random.default_rng(2)), True)):
+        cfg = moe.MoEConfig(num_experts=8, expert_type="gated", input_dim=64, hidden_dim=96, output_dim=64,
+                            activation=moe.silu, gate_type=gate, max_tokens=128, drop_tokens=drop,
+                            capacity_factor=1.0)
+        layer = moe.MoELayer(cfg, rng=rng)
+        x = rng.standard_normal((64, 100)).astype(np.float32)
+        aux = {}
+        out, loss = layer(x, training=True, _aux=aux)
+        ex = [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]
+        kk = gate.k
+        given_idx = aux["indices"] if drop else gate.host_routing(100, 8)[0]
+        if not drop:
+            assert np.array_equal(aux["indices"], given_idx)
+        ref, ref_loss, oa = oracle.moe_forward(x.T, layer.router.weight, ex, k=kk, training=True, drop_tokens=False,
+                                               logits=aux["logits"],
+                                               given=(aux["indices"], aux["gates"], None))
+        assert np.array_equal(aux["counts"], oa["counts"])
+        assert rel_err(out.T, ref) <= 1e-4
+        if not drop:
+            assert abs(loss - ref_loss) <= 1e-5
+        layer.close()
+
+
 def test_readme_config_fp32(moe, oracle):
     # README MoELayer, 8 gated silu experts, 512/2048/512,
     # TopKGating(2), SwitchTransformerLoss(0.01), x randn(512, 32), fp32

@@ -159,3 +159,75 @@ def test_routing_is_deterministic(moe, oracle):
     b = gpu_route(moe, logits, "topk", 6, 0)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("T,E,k,lam", [(2048, 8, 2, 0.7), (1000, 64, 6, 2.0), (77, 5, 3, -1.5)])
+def test_soft_moe_gating(moe, oracle, T, E, k, lam):
+    # SoftMoEGating: top-k of softmax(logits ./ lambda), the gate matrix is the
+    # probabilities (the dispatch reads the probability of expert `slot`)
+    rng = np.random.default_rng(T + E)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[::7] = np.round(lg[::7])  # ties
+    print(f"soft gating T={T} E={E} k={k} lambda={lam}", flush=True)
+    idx, gates, probs = moe.compute_gates(moe.SoftMoEGating(k, lam), lg.T)
+    oi, og, op = oracle.compute_gates_soft(lg, k, lam)
+    assert same(idx.T.astype(np.int32), oi)
+    assert same(probs.T, op) and same(gates, probs)
+
+
+@pytest.mark.parametrize("T,E,cf,ties", [(4096, 8, 1.25, False), (64, 16, 1.0, True), (300, 8, 0.25, True),
+                                         (33, 6, 3.0, True)])
+def test_expert_choice_gating(moe, oracle, T, E, cf, ties):
+    # ExpertChoiceGating: the (capacity, T) indices / gates bit-exact
+    rng = np.random.default_rng(T * E)
+    lg = (rng.integers(-3, 4, size=(T, E)) if ties else rng.standard_normal((T, E))).astype(np.float32)
+    print(f"expert choice T={T} E={E} cf={cf}", flush=True)
+    idx, gates, probs = moe.compute_gates(moe.ExpertChoiceGating(cf), lg.T)
+    oi, og, op = oracle.compute_gates_expert_choice(lg, cf)
+    assert idx.shape == (oi.shape[1], T)
+    assert same(idx.T.astype(np.int32), oi)
+    assert same(gates.T, og) and same(probs.T, op)
+
+
+def test_expert_choice_too_many_slots_is_unsupported(moe):
+    # 16 experts and capacity 16: a token may be taken by more than 8 experts
+    lg = np.zeros((16, 64), np.float32)
+    with pytest.raises(moe.MoeError) as ei:
+        moe.compute_gates(moe.ExpertChoiceGating(4.0), lg)
+    assert "MOE_MAX_TOPK" in str(ei.value)
+
+
+def test_jitter_and_stochastic_gates(moe, oracle):
+    # without training / noise logits both are their base gate; with them the
+    # perturbed logits (numpy's stream, replayed here) go through the base gate
+    rng = np.random.default_rng(61)
+    lg = rng.standard_normal((8, 500)).astype(np.float32)
+    base = moe.compute_gates(moe.TopKGating(2), lg)
+    for g in (moe.JitterGating(moe.TopKGating(2), 0.1), moe.StochasticTopKGating(2)):
+        out = moe.compute_gates(g, lg)
+        assert all(same(a, b) for a, b in zip(out, base))
+    jit = moe.JitterGating(moe.TopKGating(2), 0.1, rng=np.random.default_rng(5))
+    out = moe.compute_gates(jit, lg, training=True)
+    u = np.random.default_rng(5).random(lg.shape, dtype=np.float32)
+    jl = (lg * (np.float32(1) + (np.float32(2) * u - np.float32(1)) * np.float32(0.1))).astype(np.float32)
+    oi, og, op = oracle.compute_gates_topk(jl.T, 2)
+    assert same(out[0].T.astype(np.int32), oi) and same(out[1].T, og) and same(out[2].T, op)
+    st = moe.StochasticTopKGating(2, train_only=False, rng=np.random.default_rng(6))
+    nl = rng.standard_normal(lg.shape).astype(np.float32)
+    out = moe.compute_gates(st, lg, noise_logits=nl)
+    noise = (np.random.default_rng(6).standard_normal(lg.shape, dtype=np.float32)
+             * np.logaddexp(np.float32(0), nl).astype(np.float32)).astype(np.float32)
+    oi, og, op = oracle.compute_gates_topk((lg + noise).astype(np.float32).T, 2)
+    assert same(out[0].T.astype(np.int32), oi) and same(out[2].T, op)
+
+
+def test_host_routed_gates(moe):
+    # HashGating: (hash(i) + j) % E + 1 with a user hash; RandomGating: k
+    # distinct experts per token; both with gates 1/k and probabilities 1/E
+    idx, gates, probs = moe.compute_gates(moe.HashGating(3, 8, hash_fn=lambda i: 5 * i), np.zeros((8, 10), np.float32))
+    t = np.arange(1, 11)
+    assert np.array_equal(idx, np.stack([(5 * t + j) % 8 + 1 for j in range(3)]))
+    assert np.all(gates == np.float32(1) / np.float32(3)) and np.all(probs == np.float32(0.125))
+    idx, gates, _ = moe.compute_gates(moe.RandomGating(4, rng=np.random.default_rng(1)), np.zeros((6, 200), np.float32))
+    assert idx.shape == (4, 200) and idx.min() >= 1 and idx.max() <= 6
+    assert all(len(set(idx[:, i])) == 4 for i in range(200))

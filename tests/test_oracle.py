@@ -385,6 +385,64 @@ def test_shared_experts_switch_loss_counts_shifted_ids(oracle):
     assert loss_z == np.float32(aux_z["switch_loss"] + aux_z["z_loss"])
 
 
+# ---- SoftMoEGating / ExpertChoiceGating ------------------------------------------
+
+def test_soft_gating_closed_forms(oracle):
+    # lambda = 1: the indices of TopKGating; the slot gates are the
+    # probabilities of experts 1..k (the reference reads gates[slot, t] of the
+    # (E, T) probability matrix), not of the selected experts; lambda = 2
+    # flattens the softmax: p = softmax(l / 2)
+    rng = np.random.default_rng(26)
+    lg = rng.standard_normal((50, 6)).astype(np.float32)
+    idx, g, p = oracle.compute_gates_soft(lg, 2, 1.0)
+    i2, _, p2 = oracle.compute_gates_topk(lg, 2)
+    assert np.array_equal(idx, i2) and np.array_equal(p, p2)
+    assert np.array_equal(g, p[:, :2])
+    idx, g, p = oracle.compute_gates_soft(lg, 3, 2.0)
+    ref = np.exp(lg.astype(np.float64) / 2)
+    ref /= ref.sum(axis=1, keepdims=True)
+    assert np.max(np.abs(p - ref)) < 1e-6
+    assert np.array_equal(g, p[:, :3])
+
+
+def test_expert_choice_closed_forms(oracle):
+    rng = np.random.default_rng(27)
+    T, E = 12, 4
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    # capacity factor E: capacity T, every expert takes every token, so each
+    # token's slots are 1..E and the gates its probabilities
+    idx, g, p = oracle.compute_gates_expert_choice(lg, float(E))
+    assert idx.shape == (T, T)
+    assert np.all(idx[:, :E] == np.arange(1, E + 1)) and np.all(idx[:, E:] == 0)
+    assert np.array_equal(g[:, :E], p)
+    # capacity 1 (cf = E / T): expert e takes its argmax token
+    idx, g, p = oracle.compute_gates_expert_choice(lg, E / T)
+    for e in range(E):
+        t = int(np.argmax(lg[:, e]))
+        assert (e + 1) in idx[t]
+    assert int((idx > 0).sum()) == E
+    # equal logits: every expert takes the first C tokens (ties to the lower token)
+    idx, _, _ = oracle.compute_gates_expert_choice(np.zeros((10, 3), np.float32), 0.9)  # C = ceil(3.0) = 3
+    assert np.all(idx[:3, :3] == np.array([1, 2, 3])) and np.all(idx[3:] == 0)
+    # brute force on small inputs with ties: the set of (expert, token) pairs
+    for trial in range(50):
+        T, E = int(rng.integers(1, 9)), int(rng.integers(1, 6))
+        cf = float(rng.choice([0.5, 1.0, 1.25, 2.0]))
+        lg = rng.integers(-2, 3, size=(T, E)).astype(np.float32)
+        idx, _, _ = oracle.compute_gates_expert_choice(lg, cf)
+        C = oracle.expert_choice_capacity(T, E, cf)
+        chosen = set()
+        for e in range(E):
+            ranked = sorted(range(T), key=lambda t: (-float(lg[t, e]), t))
+            chosen |= {(e + 1, t) for t in ranked[:min(C, T)]}
+        got = {(int(idx[t, j]), t) for t in range(T) for j in range(idx.shape[1]) if idx[t, j] > 0}
+        expect = set()
+        for t in range(T):
+            es = sorted(e for e, tt in chosen if tt == t)[:C]
+            expect |= {(e, t) for e in es}
+        assert got == expect
+
+
 # ---- AuxiliaryFreeLoss ---------------------------------------------------------
 
 def test_aux_free_update_closed_form(oracle):
