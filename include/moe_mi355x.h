@@ -175,6 +175,36 @@ int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const flo
  * may be NULL).  Blocks until the handle's queued work has finished. */
 int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *update_counter);
 
+/* Expert initialisation strategies of convert_to_moe / create_single_expert
+ * (src/llama2/conversion.jl:277-318). */
+typedef enum {
+    MOE_INIT_COPY = 0,     /* every expert a copy of the dense FFN */
+    MOE_INIT_PERTURB = 1,  /* dense .+ randn .* noise_scale */
+    MOE_INIT_SPLIT = 2,    /* expert e keeps hidden units [e H / E, min((e+1) H / E, H)), zeros elsewhere */
+    MOE_INIT_RANDOM = 3    /* randn .* sqrt(2f0 / dim) */
+} moe_init_strategy;
+
+/* convert_layer_to_moe's experts (create_experts_from_layer /
+ * create_single_expert, src/llama2/conversion.jl:262-331) made on the device
+ * from one dense gated FFN: the dense w1 (H,D), w2 (D_out,H), w3 (H,D) -- in
+ * `layout` and src_dtype as for moe_set_expert, host or device memory (NULL
+ * for MOE_INIT_RANDOM) -- are read once and every expert of the handle is
+ * derived from them and prepacked in cfg.weight_dtype (fp8: per-output-channel
+ * scales of the derived weights).  Normal draws come from a counter-based
+ * generator keyed by (seed, expert, matrix, element): reproducible for a seed,
+ * not Julia's randn stream.  Gated experts only. */
+int moe_init_experts_from_dense(moe_handle *h, int32_t layout, int32_t src_dtype, const void *w1, const void *w2,
+                                const void *w3, const float *s1, const float *s2, const float *s3, int32_t strategy,
+                                float noise_scale, uint64_t seed);
+
+/* Read expert e's prepacked weights back (the save side of save_moe_model,
+ * src/llama2/utils.jl:22-67): w1/w2/w3 as (out, in) matrices in `layout`, in
+ * the packed dtype (F32 float, BF16 uint16 bits, FP8_E4M3 bytes), s1/s2/s3 the
+ * fp8 per-output-channel scales (ignored otherwise).  Any pointer may be NULL.
+ * Host pointers; blocking. */
+int moe_get_expert(moe_handle *h, int32_t expert, int32_t layout, void *w1, void *w2, void *w3, float *s1, float *s2,
+                   float *s3);
+
 /* ---- host-buffer entry points (blocking) -------------------------------- */
 
 /* compute_gates(gate, logits) -- src/gating/topk.jl:24-44,

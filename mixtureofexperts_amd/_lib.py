@@ -28,6 +28,7 @@ MOE_LAYOUT_FLUX_OUT_IN, MOE_LAYOUT_LLAMA_IN_OUT = 0, 1
 MOE_EXPERT_GATED, MOE_EXPERT_STANDARD = 0, 1
 MOE_ACT_GELU, MOE_ACT_SILU, MOE_ACT_RELU, MOE_ACT_IDENTITY = 0, 1, 2, 3
 MOE_GATE_TOPK, MOE_GATE_SWITCH, MOE_GATE_SHARED, MOE_GATE_SOFT, MOE_GATE_EXPERT_CHOICE = 0, 1, 2, 3, 4
+MOE_INIT_COPY, MOE_INIT_PERTURB, MOE_INIT_SPLIT, MOE_INIT_RANDOM = 0, 1, 2, 3
 MOE_MAX_TOPK = 8
 MOE_MAX_EXPERTS = 128
 
@@ -40,6 +41,7 @@ EXPORTED_SYMBOLS = [
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
     "moe_read_counts", "moe_switch_loss", "moe_z_loss", "moe_decode", "moe_decode_async",
     "moe_set_aux_free", "moe_get_aux_free", "moe_aux_free_update_bias", "moe_forward_routed",
+    "moe_init_experts_from_dense", "moe_get_expert",
 ]
 
 
@@ -141,6 +143,8 @@ def lib():
     L.moe_set_aux_free.argtypes = [vp, i32, vp, vp, f32, f32, i32, i64, i32, f32]
     L.moe_get_aux_free.argtypes = [vp, vp, vp, ctypes.POINTER(i64)]
     L.moe_aux_free_update_bias.argtypes = [vp, i64, i32, f32, f32, vp, vp]
+    L.moe_init_experts_from_dense.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp, i32, f32, ctypes.c_uint64]
+    L.moe_get_expert.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp]
     for name in EXPORTED_SYMBOLS:
         if name not in ("moe_last_error",):
             getattr(L, name).restype = ctypes.c_int

@@ -264,6 +264,62 @@ __global__ void convert_rows_kernel(const void *src, int src_bf16, int n, int D,
     }
 }
 
+// ---- convert_to_moe expert initialisation (src/llama2/conversion.jl:277-331) ----
+
+// Counter-based standard normal for (seed, stream, index): a splitmix64 hash
+// of the three gives two 24-bit uniforms in (0, 1), Box-Muller gives N(0, 1).
+__device__ inline float init_normal(unsigned long long seed, unsigned long long stream, unsigned long long i) {
+    unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (stream + 1) + 0xD1B54A32D192ED03ull * i;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = ((float)(z & 0xFFFFFFull) + 0.5f) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+
+// Expert e's matrix m (0 = w1, 1 = w2, 2 = w3) from the dense one, rows
+// [N][K] fp32 (K = the matrix's input features), per create_single_expert:
+// COPY: the dense rows; PERTURB: w .+ randn .* noise_scale; SPLIT: only the
+// hidden units [lo, hi) of expert e, lo = e H / E, hi = min((e + 1) H / E,
+// H) (w1 / w3 rows, w2 columns), zero elsewhere; RANDOM: randn .* sigma.
+__global__ void init_expert_kernel(const float *__restrict__ src, int N, int K, int strategy, int m, int e, int E,
+                                   int H, float noise_scale, float sigma, unsigned long long seed,
+                                   float *__restrict__ dst) {
+#pragma clang fp contract(off)
+    const long long total = (long long)N * K;
+    const int lo = (int)(((long long)e * H) / E);
+    const int hi = min((int)(((long long)(e + 1) * H) / E), H);
+    const unsigned long long stream = (unsigned long long)e * 3 + m;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        float v = src ? src[i] : 0.0f;
+        if (strategy == MOE_INIT_PERTURB) {
+            v = v + init_normal(seed, stream, (unsigned long long)i) * noise_scale;
+        } else if (strategy == MOE_INIT_RANDOM) {
+            v = init_normal(seed, stream, (unsigned long long)i) * sigma;
+        } else if (strategy == MOE_INIT_SPLIT) {
+            const int hu = (m == 1) ? (int)(i % K) : (int)(i / K);  // the hidden unit of this element
+            if (hu < lo || hu >= hi) v = 0.0f;
+        }
+        dst[i] = v;
+    }
+}
+
+// Packed [Npad][Kpad] rows of expert weights back to an (N out, K in) matrix
+// in the caller's layout and the packed dtype (bytes per element esz).
+__global__ void unpack_rows_kernel(const uint8_t *__restrict__ src, int esz, int N, int K, int Kpad, int layout,
+                                   uint8_t *__restrict__ dst) {
+    const long long total = (long long)N * K;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int o = (int)(i / K), k = (int)(i % K);
+        const long long d = (layout == MOE_LAYOUT_FLUX_OUT_IN) ? (long long)k * N + o : i;
+        const long long sidx = (long long)o * Kpad + k;
+        for (int b = 0; b < esz; ++b) dst[d * esz + b] = src[sidx * esz + b];
+    }
+}
+
 }  // namespace
 
 static bool is_device_ptr(const void *p) {
@@ -292,6 +348,62 @@ static int stage_to_device(moe_handle *h, const void *p, size_t bytes, const voi
     }
     *dptr = d;
     *owned = d;
+    return MOE_OK;
+}
+
+// fp32 rows [N][K] (device) -> the packed dtype of the handle, [N][Kpad]
+// (fp8: per-row scales), on the handle's stream.
+static hipError_t pack_f32_rows(moe_handle *h, const float *tmp, int N, int K, int Kpad, void *dst, float *scales) {
+    if (h->wt == WT_F32)
+        hipLaunchKernelGGL(pack_rows_kernel<WT_F32>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad, dst, scales);
+    else if (h->wt == WT_BF16)
+        hipLaunchKernelGGL(pack_rows_kernel<WT_BF16>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad, dst, scales);
+    else
+        hipLaunchKernelGGL(pack_rows_kernel<WT_FP8>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad, dst, scales);
+    return hipGetLastError();
+}
+
+// Source matrix (any layout / dtype, host or device) -> fp32 rows [N][K] in
+// a new device buffer *out (the caller frees it).
+static int load_f32_rows(moe_handle *h, int layout, int src_dtype, const void *src, const float *src_scales, int N,
+                         int K, float **out) {
+    *out = nullptr;
+    const size_t esz = src_dtype == MOE_F32 ? 4 : (src_dtype == MOE_BF16 ? 2 : 1);
+    const void *dsrc = nullptr, *dsc = nullptr;
+    void *own_src = nullptr, *own_sc = nullptr;
+    int r = stage_to_device(h, src, esz * (size_t)N * K, &dsrc, &own_src);
+    if (r != MOE_OK) return r;
+    if (src_dtype == MOE_FP8_E4M3) {
+        r = stage_to_device(h, src_scales, sizeof(float) * (size_t)N, &dsc, &own_sc);
+        if (r != MOE_OK) {
+            if (own_src) (void)hipFree(own_src);
+            return r;
+        }
+    }
+    float *tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, sizeof(float) * (size_t)N * K);
+    if (e == hipSuccess) {
+        dim3 grid((N + 31) / 32, (K + 31) / 32), block(32, 8);
+        if (src_dtype == MOE_F32)
+            hipLaunchKernelGGL(to_f32_rows_kernel<MOE_F32>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                               (const float *)dsc, tmp);
+        else if (src_dtype == MOE_BF16)
+            hipLaunchKernelGGL(to_f32_rows_kernel<MOE_BF16>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                               (const float *)dsc, tmp);
+        else
+            hipLaunchKernelGGL(to_f32_rows_kernel<MOE_FP8_E4M3>, grid, block, 0, h->stream, dsrc, layout, N, K,
+                               (const float *)dsc, tmp);
+        e = hipGetLastError();
+        hipError_t e2 = hipStreamSynchronize(h->stream);
+        if (e == hipSuccess) e = e2;
+    }
+    if (own_src) (void)hipFree(own_src);
+    if (own_sc) (void)hipFree(own_sc);
+    if (e != hipSuccess) {
+        if (tmp) (void)hipFree(tmp);
+        return fail(h, MOE_EHIP, std::string("weight load failed: ") + hipGetErrorString(e));
+    }
+    *out = tmp;
     return MOE_OK;
 }
 
@@ -330,18 +442,7 @@ static int pack_matrix(moe_handle *h, int layout, int src_dtype, const void *src
                 hipLaunchKernelGGL(to_f32_rows_kernel<MOE_FP8_E4M3>, grid, block, 0, h->stream, dsrc, layout, N, K,
                                    (const float *)dsc, tmp);
             e = hipGetLastError();
-            if (e == hipSuccess) {
-                if (h->wt == WT_F32)
-                    hipLaunchKernelGGL(pack_rows_kernel<WT_F32>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
-                                       dst_expert, dst_scales);
-                else if (h->wt == WT_BF16)
-                    hipLaunchKernelGGL(pack_rows_kernel<WT_BF16>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
-                                       dst_expert, dst_scales);
-                else
-                    hipLaunchKernelGGL(pack_rows_kernel<WT_FP8>, dim3(N), dim3(256), 0, h->stream, tmp, K, Kpad,
-                                       dst_expert, dst_scales);
-                e = hipGetLastError();
-            }
+            if (e == hipSuccess) e = pack_f32_rows(h, tmp, N, K, Kpad, dst_expert, dst_scales);
             hipError_t e2 = hipStreamSynchronize(h->stream);
             if (e == hipSuccess) e = e2;
             (void)hipFree(tmp);
@@ -804,6 +905,114 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
                                  is_device_ptr(b2) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice));
     }
     h->expert_set[expert] = 1;
+    return MOE_OK;
+}
+
+int moe_init_experts_from_dense(moe_handle *h, int32_t layout, int32_t src_dtype, const void *w1, const void *w2,
+                                const void *w3, const float *s1, const float *s2, const float *s3, int32_t strategy,
+                                float noise_scale, uint64_t seed) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (!h->gated) return fail(h, MOE_EUNSUPPORTED, "expert initialisation from a dense FFN: gated experts only");
+    if (layout != MOE_LAYOUT_FLUX_OUT_IN && layout != MOE_LAYOUT_LLAMA_IN_OUT) return fail(h, MOE_EINVAL, "bad layout");
+    if (src_dtype < MOE_F32 || src_dtype > MOE_FP8_E4M3) return fail(h, MOE_EINVAL, "bad src_dtype");
+    if (strategy < MOE_INIT_COPY || strategy > MOE_INIT_RANDOM)
+        return fail(h, MOE_EINVAL, "unknown initialisation strategy (ArgumentError)");
+    const bool need_src = strategy != MOE_INIT_RANDOM;
+    if (need_src && (!w1 || !w2 || !w3)) return fail(h, MOE_EINVAL, "missing dense FFN matrix");
+    if (need_src && src_dtype == MOE_FP8_E4M3 && (!s1 || !s2 || !s3))
+        return fail(h, MOE_EINVAL, "fp8 weights need per-output-channel scales");
+    {
+        const void *srcs[6] = {w1, w2, w3, s1, s2, s3};
+        bool any_dev = false;
+        for (const void *p : srcs)
+            if (p && is_device_ptr(p)) any_dev = true;
+        if (any_dev) HIP_TRY(h, hipDeviceSynchronize());
+    }
+    // the three dense matrices as fp32 rows: w1 / w3 (H, D), w2 (Dout, H)
+    const int Ns[3] = {h->H, h->Dout, h->H}, Ks[3] = {h->D, h->H, h->D}, Kp[3] = {h->D_pad, h->H_pad, h->D_pad};
+    const void *ws[3] = {w1, w2, w3};
+    const float *ss[3] = {s1, s2, s3};
+    float *dense[3] = {nullptr, nullptr, nullptr};
+    float *tmp = nullptr;
+    int r = MOE_OK;
+    size_t most = 0;
+    for (int m = 0; m < 3; ++m) {
+        most = std::max(most, (size_t)Ns[m] * Ks[m]);
+        if (need_src && r == MOE_OK) r = load_f32_rows(h, layout, src_dtype, ws[m], ss[m], Ns[m], Ks[m], &dense[m]);
+    }
+    hipError_t e = hipSuccess;
+    if (r == MOE_OK) e = hipMalloc(&tmp, sizeof(float) * most);
+    const size_t wsz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
+    // Random init: sigma = sqrt(2f0 / dim) in Float32 (conversion.jl:306-310)
+    const float sigma = sqrtf(2.0f / (float)h->D);
+    for (int x = 0; x < h->E && r == MOE_OK && e == hipSuccess; ++x) {
+        for (int m = 0; m < 3 && e == hipSuccess; ++m) {
+            const long long total = (long long)Ns[m] * Ks[m];
+            const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
+            hipLaunchKernelGGL(init_expert_kernel, dim3(blocks), dim3(256), 0, h->stream, dense[m], Ns[m], Ks[m],
+                               strategy, m, x, h->E, h->H, noise_scale, sigma, (unsigned long long)seed, tmp);
+            e = hipGetLastError();
+            void *base = (m == 0) ? h->w1 : (m == 1 ? h->w2 : h->w3);
+            const long long stride = (m == 1) ? h->w2_stride : h->w1_stride;
+            float *sc = nullptr;
+            if (h->wt == WT_FP8) {
+                float *sb = (m == 0) ? h->s1 : (m == 1 ? h->s2 : h->s3);
+                sc = sb + (size_t)x * (m == 1 ? h->Dout_npad : h->H_pad);
+            }
+            if (e == hipSuccess)
+                e = pack_f32_rows(h, tmp, Ns[m], Ks[m], Kp[m], (uint8_t *)base + wsz * (size_t)x * stride, sc);
+            // tmp is reused by the next matrix: the stream orders the kernels
+        }
+        if (e == hipSuccess) h->expert_set[x] = 1;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+    for (float *d : dense)
+        if (d) (void)hipFree(d);
+    if (tmp) (void)hipFree(tmp);
+    if (r != MOE_OK) return r;
+    if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("expert initialisation failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+int moe_get_expert(moe_handle *h, int32_t expert, int32_t layout, void *w1, void *w2, void *w3, float *s1, float *s2,
+                   float *s3) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (expert < 0 || expert >= h->E) return fail(h, MOE_EINVAL, "expert index out of range");
+    if (!h->expert_set[expert]) return fail(h, MOE_ENOTREADY, "expert has no weights");
+    if (layout != MOE_LAYOUT_FLUX_OUT_IN && layout != MOE_LAYOUT_LLAMA_IN_OUT) return fail(h, MOE_EINVAL, "bad layout");
+    const int esz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
+    const int Ns[3] = {h->H, h->Dout, h->H}, Ks[3] = {h->D, h->H, h->D}, Kp[3] = {h->D_pad, h->H_pad, h->D_pad};
+    void *outs[3] = {w1, w2, h->gated ? w3 : nullptr};
+    float *souts[3] = {s1, s2, h->gated ? s3 : nullptr};
+    const size_t most = (size_t)std::max((size_t)h->H * h->D, (size_t)h->Dout * h->H) * esz;
+    uint8_t *tmp = nullptr;
+    HIP_TRY(h, hipMalloc(&tmp, most));
+    hipError_t e = hipSuccess;
+    for (int m = 0; m < 3 && e == hipSuccess; ++m) {
+        if (!outs[m] && !souts[m]) continue;
+        const void *base = (m == 0) ? h->w1 : (m == 1 ? h->w2 : h->w3);
+        const long long stride = (m == 1) ? h->w2_stride : h->w1_stride;
+        if (outs[m]) {
+            const long long total = (long long)Ns[m] * Ks[m];
+            const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
+            hipLaunchKernelGGL(unpack_rows_kernel, dim3(blocks), dim3(256), 0, h->stream,
+                               (const uint8_t *)base + (size_t)esz * expert * stride, esz, Ns[m], Ks[m], Kp[m], layout,
+                               tmp);
+            e = hipGetLastError();
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(outs[m], tmp, (size_t)esz * total, hipMemcpyDeviceToHost, h->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+        }
+        if (souts[m] && h->wt == WT_FP8 && e == hipSuccess) {
+            const float *sb = (m == 0) ? h->s1 : (m == 1 ? h->s2 : h->s3);
+            e = hipMemcpy(souts[m], sb + (size_t)expert * (m == 1 ? h->Dout_npad : h->H_pad), sizeof(float) * Ns[m],
+                          hipMemcpyDeviceToHost);
+        }
+    }
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("expert readback failed: ") + hipGetErrorString(e));
     return MOE_OK;
 }
 

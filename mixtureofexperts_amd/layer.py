@@ -121,13 +121,14 @@ class MoELayer:
         if training and c.expert_dropout > 0 and c.expert_type != "gated":
             raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "expert dropout in training has no device path")
 
-    def sync_weights(self):
-        """(Re)build the device handle and upload router and expert weights."""
+    def _new_device(self):
+        """A device handle for this layer's configuration (no weights yet)."""
         c = self.config
         if self._dev is not None:
             self._dev.close()
+            self._dev = None
         spec = gate_spec(self.router.gate_type, self.router.weight.shape[0])
-        self._dev = DeviceLayer(
+        return DeviceLayer(
             num_experts=c.num_experts, expert_type=(_lib.MOE_EXPERT_GATED if c.expert_type == "gated"
                                                     else _lib.MOE_EXPERT_STANDARD),
             input_dim=c.input_dim, hidden_dim=c.hidden_dim, output_dim=c.output_dim,
@@ -135,6 +136,10 @@ class MoELayer:
             balance_alpha=balance_alpha(self.balance_loss), z_loss_weight=c.z_loss_weight,
             capacity_factor=c.capacity_factor, drop_tokens=c.drop_tokens, max_tokens=c.max_tokens,
             num_shared_experts=c.num_shared_experts)
+
+    def sync_weights(self):
+        """(Re)build the device handle and upload router and expert weights."""
+        self._dev = self._new_device()
         self._dev.set_router(np.ascontiguousarray(self.router.weight.T), self.router.bias)
         for e, ex in enumerate(self.experts):
             ex.upload(self._dev, e)

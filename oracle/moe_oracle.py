@@ -428,6 +428,26 @@ def decode_ffn(xb_nD, router_w_ED, experts, *, gate="topk", k=2, router_bias=Non
     return out, idx, gates, logits
 
 
+# ---- convert_to_moe ---------------------------------------------------------------
+
+def split_expert(w1, w2, w3, e, E):
+    """create_single_expert(..., :split, expert_idx = e + 1) --
+    src/llama2/conversion.jl:296-304: Llama (in, out) matrices w1, w3 (dim,
+    hidden), w2 (hidden, dim); expert e keeps hidden units start:end with
+    start = (e * hidden) / E + 1 and end = min((e + 1) * hidden / E, hidden)
+    (integer division, 1-based), zeros elsewhere."""
+    hidden = w1.shape[1]
+    start = (e * hidden) // E + 1
+    end = min(((e + 1) * hidden) // E, hidden)
+    o1 = np.zeros_like(w1)
+    o2 = np.zeros_like(w2)
+    o3 = np.zeros_like(w3)
+    o1[:, start - 1:end] = w1[:, start - 1:end]
+    o2[start - 1:end, :] = w2[start - 1:end, :]
+    o3[:, start - 1:end] = w3[:, start - 1:end]
+    return o1, o2, o3
+
+
 # ---- dtype helpers used by tests and the bench ------------------------------
 
 def f32_to_bf16_bits(a):

@@ -443,6 +443,28 @@ def test_expert_choice_closed_forms(oracle):
         assert got == expect
 
 
+# ---- convert_to_moe :split ---------------------------------------------------------
+
+def test_split_experts_partition_the_dense_ffn(oracle):
+    # the :split experts' hidden units partition the dense FFN's, and silu(0)
+    # * 0 = 0, so the sum of the experts' outputs is the dense output
+    rng = np.random.default_rng(28)
+    dim, hid, E = 24, 50, 8
+    w1 = rng.standard_normal((dim, hid)).astype(np.float32)
+    w2 = rng.standard_normal((hid, dim)).astype(np.float32)
+    w3 = rng.standard_normal((dim, hid)).astype(np.float32)
+    x = rng.standard_normal((5, dim)).astype(np.float32)
+    dense = oracle.gated_expert(x, w1.T, w2.T, w3.T, oracle.act_silu).astype(np.float64)
+    total = np.zeros_like(dense)
+    kept = np.zeros(hid, int)
+    for e in range(E):
+        a, b, c = oracle.split_expert(w1, w2, w3, e, E)
+        kept += (np.abs(a).sum(axis=0) > 0).astype(int)
+        total += oracle.gated_expert(x, a.T, b.T, c.T, oracle.act_silu)
+    assert np.all(kept == 1)  # every hidden unit in exactly one expert
+    assert np.max(np.abs(total - dense)) / np.max(np.abs(dense)) < 1e-5
+
+
 # ---- AuxiliaryFreeLoss ---------------------------------------------------------
 
 def test_aux_free_update_closed_form(oracle):
