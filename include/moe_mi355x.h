@@ -251,14 +251,18 @@ int moe_forward_routed(moe_handle *h, const void *x, int32_t x_dtype, int32_t T,
 int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n, float *y);
 
 /* The decode caller: moe_ffn_forward! (src/llama2/inference.jl:58-121)
- * after its rmsnorm, without shared experts.  Each of the n tokens is routed
+ * after its rmsnorm.  Each of the n tokens is routed
  * on its own (logits = W_router' xb with the router set by moe_set_router,
  * then compute_gates, src/gating/topk.jl:24-44) and the gated experts of its
  * k slots are combined in slot order on a zero start (:83-104):
  * out = ((0 + g_1 y_1) + g_2 y_2) + ..., y = W2 (silu(W1 xb) .* (W3 xb)),
  * silu(g) = g * (1 / (1 + exp(-g))) (gated_expert_forward!, :154-167).
- * xb [n][D] fp32, out [n][D_out] fp32 (host); logits [n][E], indices [n][k]
- * (1-based), gates [n][k] may be NULL.  Gated experts with TopKGating or
+ * With num_shared_experts = ns > 0 the layer's shared experts are
+ * process_shared_experts! (:184-216): shared = sum_i (1f0/ns) * y_i, out =
+ * 0.5f0 * shared + 0.5f0 * out; the slots then hold the shared experts 1..ns
+ * first and the routed ones shifted by ns.
+ * xb [n][D] fp32, out [n][D_out] fp32 (host); logits [n][E_router], indices
+ * [n][slots] (1-based), gates [n][slots] may be NULL.  Gated experts with TopKGating or
  * SwitchGating only (else MOE_EUNSUPPORTED); 1 <= n <= max_tokens (handles
  * with bf16 or fp8 weights: max_tokens / 2). */
 int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *logits, int32_t *indices,

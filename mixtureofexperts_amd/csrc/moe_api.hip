@@ -1238,7 +1238,6 @@ static int decode_check(moe_handle *h, int n) {
     if (!h->gated) return fail(h, MOE_EUNSUPPORTED, "decode path: gated experts only (gated_expert_forward!)");
     if (h->cfg.gate_kind != MOE_GATE_TOPK && h->cfg.gate_kind != MOE_GATE_SWITCH)
         return fail(h, MOE_EUNSUPPORTED, "decode path: TopKGating or SwitchGating only");
-    if (h->lsh > 0) return fail(h, MOE_EUNSUPPORTED, "decode path: no shared experts");
     if ((h->D & 3) != 0) return fail(h, MOE_EUNSUPPORTED, "decode path: input_dim must be a multiple of 4");
     // h of the n * k slots is kept as fp32 rows in the expert workspace
     const long long cap = (long long)h->rows_max * h->H_pad * (h->ct == CT_F32 ? 4 : 2) / (4LL * h->H_pad * h->kt);
@@ -1249,7 +1248,7 @@ static int decode_check(moe_handle *h, int n) {
 
 static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_dev, hipStream_t s) {
     DecodeArgs a{};
-    a.x = x_dev; a.D = h->D; a.n = n; a.kt = h->kt; a.k = h->k; a.E = h->E;
+    a.x = x_dev; a.D = h->D; a.n = n; a.kt = h->kt; a.k = h->k; a.E = h->Er; a.lsh = h->lsh;
     a.wr = h->wr; a.Er_pad = h->Er_pad; a.br = h->has_bias ? h->br : nullptr;
     a.logits = h->logits; a.probs = h->probs; a.idx = h->idx; a.gates = h->gates;
     a.wt = h->wt; a.w1 = h->w1; a.w3 = h->w3; a.w2 = h->w2;
@@ -1275,7 +1274,7 @@ int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *log
     r = decode_locked(h, (const float *)h->x_dev, n, h->out_dev, s);
     if (r != MOE_OK) return r;
     HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s));
-    if (logits) HIP_TRY(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)n * h->E, hipMemcpyDeviceToHost, s));
+    if (logits) HIP_TRY(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)n * h->Er, hipMemcpyDeviceToHost, s));
     if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
     if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));

@@ -1,7 +1,8 @@
 // moe_decode.hip -- the decode caller of the MoE FFN (moe_ffn_forward!,
 // src/llama2/inference.jl:58-121): one token at a time (or n independent
 // tokens), its k selected gated experts as matrix-vector products, combined
-// in slot order.  Weight-bandwidth bound: every selected expert's three
+// in slot order, and the layer's shared experts (process_shared_experts!,
+// :184-216) averaged and blended 0.5 / 0.5 with them.  Weight-bandwidth bound: every selected expert's three
 // matrices are read once per token; two kernels per call.
 //
 //   decode_up_kernel   : the token's routing (logits = W' xb + b, softmax,
@@ -180,9 +181,14 @@ __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, 
                 a.probs[(long long)t * E + e] = pv[h];
             }
         }
+        // slots: the shared experts 1..lsh, then the routed ones shifted by lsh
+        if (lane < a.lsh) {
+            a.idx[(long long)t * a.kt + lane] = lane + 1;
+            a.gates[(long long)t * a.kt + lane] = 1.0f / (float)a.lsh;
+        }
         if (lane < a.k) {
-            a.idx[(long long)t * a.kt + lane] = mye + 1;
-            a.gates[(long long)t * a.kt + lane] = myp / ssum;
+            a.idx[(long long)t * a.kt + a.lsh + lane] = a.lsh + mye + 1;
+            a.gates[(long long)t * a.kt + a.lsh + lane] = myp / ssum;
         }
     }
     return packed;
@@ -283,8 +289,10 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
         const int u1 = two ? u0 + 1 : u0;
         const int s0 = u0 / a.Hpad, j0 = u0 - s0 * a.Hpad;
         const int s1 = u1 / a.Hpad, j1 = u1 - s1 * a.Hpad;
-        const int e0 = (int)((sel >> (8 * s0)) & 0xff), e1 = (int)((sel >> (8 * s1)) & 0xff);
-        const bool ok0 = e0 >= 0 && e0 < a.E, ok1 = e1 >= 0 && e1 < a.E;
+        // expert of a slot: shared s < lsh, else routed lsh + (slot s - lsh's pick)
+        const int e0 = s0 < a.lsh ? s0 : a.lsh + (int)((sel >> (8 * (s0 - a.lsh))) & 0xff);
+        const int e1 = s1 < a.lsh ? s1 : a.lsh + (int)((sel >> (8 * (s1 - a.lsh))) & 0xff);
+        const bool ok0 = e0 >= 0 && e0 < a.E + a.lsh, ok1 = e1 >= 0 && e1 < a.E + a.lsh;
         const long long r0 = (long long)(ok0 ? e0 : 0) * a.w1_stride + (long long)j0 * a.Dpad;
         const long long r1 = (long long)(ok1 ? e1 : 0) * a.w1_stride + (long long)j1 * a.Dpad;
         float g0 = 0.0f, q0 = 0.0f, g1 = 0.0f, q1 = 0.0f;
@@ -340,7 +348,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     const int lane = threadIdx.x;
     const int t = blockIdx.x, i = blockIdx.y;
     const int nch = a.Hpad >> 2;
-    float acc = 0.0f;
+    const float sw = a.lsh > 0 ? 1.0f / (float)a.lsh : 0.0f;  // shared_weight (inference.jl:201)
+    float acc = 0.0f, sh = 0.0f;
     int s0 = 0;
     do {  // kt >= 1
         const bool two = s0 + 1 < a.kt;
@@ -356,7 +365,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
         }
         __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the wait for idx
         const int e0 = a.idx[ts0] - 1, e1 = a.idx[ts1] - 1;
-        const bool ok0 = e0 >= 0 && e0 < a.E, ok1 = two && e1 >= 0 && e1 < a.E;
+        const bool ok0 = e0 >= 0 && e0 < a.E + a.lsh, ok1 = two && e1 >= 0 && e1 < a.E + a.lsh;
         const long long r0 = (long long)(ok0 ? e0 : 0) * a.w2_stride + (long long)i * a.Hpad;
         const long long r1 = (long long)(ok1 ? e1 : 0) * a.w2_stride + (long long)i * a.Hpad;
         float y0 = 0.0f, y1 = 0.0f;
@@ -389,10 +398,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
             if (ok0) y0 = y0 * a.s2[(long long)e0 * a.Dout_npad + i];
             if (ok1) y1 = y1 * a.s2[(long long)e1 * a.Dout_npad + i];
         }
-        if (ok0) acc = acc + a.gates[ts0] * y0;
-        if (ok1) acc = acc + a.gates[ts1] * y1;
+        // routed slots: xb2 += gate * y in slot order (inference.jl:94-104);
+        // shared slots: shared_output += shared_weight * y in order (:196-205)
+        if (ok0) {
+            if (s0 < a.lsh) sh = sh + sw * y0;
+            else acc = acc + a.gates[ts0] * y0;
+        }
+        if (ok1) {
+            if (s0 + 1 < a.lsh) sh = sh + sw * y1;
+            else acc = acc + a.gates[ts1] * y1;
+        }
         s0 += 2;
     } while (s0 < a.kt);
+    // xb2 = 0.5 * shared + 0.5 * xb2 (:208-215)
+    if (a.lsh > 0) acc = 0.5f * sh + 0.5f * acc;
     if (lane == 0) a.out[(long long)t * a.Dout + i] = acc;
 }
 
@@ -412,7 +431,8 @@ static hipError_t launch_decode_wt(const DecodeArgs &a, int ncu, hipStream_t s) 
 
 hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
-    if (a.E < 1 || a.E > MOE_MAX_EXPERTS || a.k < 1 || a.k > MOE_MAX_TOPK || a.k > a.E || a.kt != a.k)
+    if (a.E < 1 || a.E + a.lsh > MOE_MAX_EXPERTS || a.k < 1 || a.k > a.E || a.lsh < 0 || a.kt != a.k + a.lsh ||
+        a.kt > MOE_MAX_TOPK)
         return hipErrorInvalidValue;
     // rows are read 4 elements at a time
     if (a.D < 4 || (a.D & 3) || (a.Dpad & 3) || (a.Hpad & 3) || a.D > a.Dpad || a.H > a.Hpad) return hipErrorInvalidValue;

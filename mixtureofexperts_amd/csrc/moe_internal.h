@@ -262,7 +262,9 @@ struct GemmArgs {
 // routed and combined on its own, slots in order.
 struct DecodeArgs {
     const float *x; int D;               // [n][D] fp32 (the rmsnorm'd xb)
-    int n, kt, k, E;
+    int n, kt, k, E;                     // E: router outputs (routed experts)
+    int lsh;                             // shared experts (slots 0..lsh-1, experts 0..lsh-1); routed
+                                         // expert e is expert lsh + e of the weights
     const float *wr; int Er_pad;         // router weight [D][Er_pad] fp32
     const float *br;                     // router bias [E] or null
     float *logits, *probs;               // [n][E]

@@ -14,7 +14,7 @@ import numpy as np
 from . import _lib
 from ._device import DeviceLayer
 from .activations import activation_code, gelu
-from .balancing import AuxiliaryFreeLoss, LoadBalancingLoss, SwitchTransformerLoss, balance_alpha
+from .balancing import AuxiliaryFreeLoss, LoadBalancingLoss, SwitchTransformerLoss, balance_alpha, update_bias
 from .experts import GatedExpert, StandardExpert
 from .gating import HOST_ROUTED_GATES, GatingMechanism, TopKGating, gate_spec
 
@@ -204,8 +204,9 @@ class MoELayer:
 
 def moe_ffn_forward(moe, xb):
     """moe_ffn_forward! -- src/llama2/inference.jl:58-121, the decode caller,
-    on this layer's router and gated experts, after the caller's rmsnorm and
-    without shared experts.  Each token is routed on its own (logits =
+    on this layer's router and gated experts, after the caller's rmsnorm; the
+    layer's shared experts (num_shared_experts) are process_shared_experts!
+    (:184-216), and an AuxiliaryFreeLoss gets update_bias! per token.  Each token is routed on its own (logits =
     W_router' xb, compute_gates) and its experts are combined in slot order:
     xb2 = 0; xb2 += gate_s * gated_expert_forward!(xb) for s = 1..k, with
     silu(g) = g * (1 / (1 + exp(-g))) (:154-167).
@@ -220,6 +221,15 @@ def moe_ffn_forward(moe, xb):
         raise _lib.MoeError(_lib.MOE_EINVAL, f"xb must be ({moe.config.input_dim},) or ({moe.config.input_dim}, n)")
     dev = moe._dev if moe._dev is not None else moe.sync_weights()
     out, _, idx, gates = dev.decode(np.ascontiguousarray(X.T))
+    ns = moe.config.num_shared_experts
+    if ns > 0:
+        # selected_experts as the router numbers them (the shared experts are
+        # process_shared_experts!'s, not slots of the routing)
+        idx, gates = idx[:, ns:] - ns, gates[:, ns:]
+    if isinstance(moe.balance_loss, AuxiliaryFreeLoss):
+        # update_bias!(config.moe_balance_loss, selected_experts) per token (:109-111)
+        for t in range(idx.shape[0]):
+            update_bias(moe.balance_loss, idx[t])
     if vec:
         return out[0], idx[0].astype(np.int64), gates[0]
     return out.T, idx.T.astype(np.int64), gates.T

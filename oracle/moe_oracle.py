@@ -399,9 +399,9 @@ def silu_inline(x):
     return (x * (np.float32(1) / (np.float32(1) + np.exp(-x)))).astype(np.float32)
 
 
-def decode_ffn(xb_nD, router_w_ED, experts, *, gate="topk", k=2, router_bias=None, logits=None):
-    """moe_ffn_forward! (src/llama2/inference.jl:58-121) after its rmsnorm and
-    without shared experts, for n tokens each routed on its own: logits =
+def decode_ffn(xb_nD, router_w_ED, experts, *, gate="topk", k=2, router_bias=None, logits=None, num_shared=0):
+    """moe_ffn_forward! (src/llama2/inference.jl:58-121) after its rmsnorm,
+    for n tokens each routed on its own: logits =
     W_router' xb (:63), compute_gates (:65-66), then xb2 = 0 and, slot by slot
     in order, xb2 += gate * gated_expert_forward!(xb) (:83-104, :154-167).
 
@@ -415,16 +415,29 @@ def decode_ffn(xb_nD, router_w_ED, experts, *, gate="topk", k=2, router_bias=Non
             logits = (logits + router_bias).astype(np.float32)
     idx, gates, _ = compute_gates_topk(logits, 1 if gate == "switch" else k)
     n, kt = idx.shape
+    ns = int(num_shared)
+    routed = experts[ns:]
     Dout = experts[0]["w2"].shape[0]
     out = np.zeros((n, Dout), np.float32)
     for j in range(kt):  # slot order
-        for e in range(len(experts)):
+        for e in range(len(routed)):
             toks = np.nonzero(idx[:, j] == e + 1)[0]
             if toks.size == 0:
                 continue
-            ex = experts[e]
+            ex = routed[e]
             y = gated_expert(x[toks], ex["w1"], ex["w2"], ex["w3"], silu_inline)
             out[toks] = (out[toks] + (gates[toks, j][:, None] * y).astype(np.float32)).astype(np.float32)
+    if ns > 0:
+        # process_shared_experts! (src/llama2/inference.jl:184-216): shared =
+        # sum_i (1f0 / ns) * y_i from zeros, xb2 = 0.5f0 * shared + 0.5f0 * xb2
+        sw = np.float32(1) / np.float32(ns)
+        sh = np.zeros((n, Dout), np.float32)
+        for i in range(ns):
+            ex = experts[i]
+            y = gated_expert(x, ex["w1"], ex["w2"], ex["w3"], silu_inline)
+            sh = (sh + (sw * y).astype(np.float32)).astype(np.float32)
+        half = np.float32(0.5)
+        out = ((half * sh).astype(np.float32) + (half * out).astype(np.float32)).astype(np.float32)
     return out, idx, gates, logits
 
 

