@@ -10,7 +10,7 @@ namespace moe {
 
 constexpr int kRouteBlock = 32;    // tokens per routing block
 constexpr int kRouteThreads = 256; // threads per routing block (the first kRouteBlock own one token each)
-constexpr int kRouterMaxSlices = 8;  // K slices of the router logits GEMM (partial sums)
+constexpr int kRouterMaxSlices = 8;   // K slices of the router logits GEMM (partial sums)
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
 constexpr int kKPad = 64;          // K padding of packed weights and activation rows

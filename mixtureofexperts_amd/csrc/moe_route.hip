@@ -309,29 +309,43 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     if (softmax) {
     const int nq = ntok * a.Er;
     const long long sstride = (long long)a.T * a.Er;
+    // elements per thread per round (block-uniform): up to 4 rows of
+    // kRouterMaxSlices partials in flight, but never more than the block has
+    const int nu = min(4, (nq + kRouteThreads - 1) / kRouteThreads);
     for (int q0 = 0; q0 < nq; q0 += 4 * kRouteThreads) {
-        float pv[4][kRouterMaxSlices], bv[4];
+        long long o[4];
+        int qq[4];
+        float v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int q = min(q0 + u * kRouteThreads + tid, nq - 1);
-            const int tt = q / a.Er, i = q - tt * a.Er;
-            const long long o = (long long)(t0 + tt) * a.Er + i;
+            qq[u] = min(q0 + u * kRouteThreads + tid, nq - 1);
+            const int tt = qq[u] / a.Er;
+            o[u] = (long long)(t0 + tt) * a.Er + (qq[u] - tt * a.Er);
+            v[u] = 0.0f;
+        }
+        // slices in groups of 4 (clamped to the last slice): every load of a
+        // group is issued before the group's sums, which run in slice order
+        for (int sg = 0; sg < a.nks; sg += 4) {
+            float pv[4][4];
 #pragma unroll
-            for (int sl = 0; sl < kRouterMaxSlices; ++sl)
-                pv[u][sl] = a.part[min(sl, a.nks - 1) * sstride + o];
-            bv[u] = a.bias ? a.bias[i] : 0.0f;
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (u < nu) pv[u][c] = a.part[min(sg + c, a.nks - 1) * sstride + o[u]];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (u < nu && sg + c < a.nks) v[u] = (sg + c == 0) ? pv[u][c] : v[u] + pv[u][c];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int q = q0 + u * kRouteThreads + tid;
-            if (q < nq) {
+            if (u < nu && q < nq) {
                 const int tt = q / a.Er, i = q - tt * a.Er;
-                float v = pv[u][0];
-#pragma unroll
-                for (int sl = 1; sl < kRouterMaxSlices; ++sl)
-                    if (sl < a.nks) v = v + pv[u][sl];
-                if (a.bias) v = v + bv[u];
-                lrow[tt * RW + i] = v;
+                float w = v[u];
+                if (a.bias) w = w + a.bias[i];
+                lrow[tt * RW + i] = w;
             }
         }
     }
