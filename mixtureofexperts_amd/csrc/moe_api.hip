@@ -79,6 +79,8 @@ struct moe_handle {
     int aux_update_freq = 1;
     long long aux_counter = 0;
     float *aux_bias = nullptr, *aux_mom = nullptr;
+    int *tot_counts = nullptr;       // scan work: column totals
+    double *tot_stats = nullptr;
 
     int last_T = -1, last_training = 0, last_x_bf16 = 0;
     std::vector<void *> allocs;
@@ -550,6 +552,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.aux_free = aux; sa.aux_use_comp = h->aux_use_comp; sa.aux_update = aux_update;
     sa.aux_cw = h->aux_cw; sa.aux_lr = h->aux_lr; sa.aux_momentum = h->aux_momentum;
     sa.aux_bias = h->aux_bias; sa.aux_mom = h->aux_mom;
+    sa.tot_counts = h->tot_counts; sa.tot_stats = h->tot_stats;
     HIP_TRY(h, launch_scan(sa, s));
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
@@ -785,6 +788,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->num_tiles, sizeof(int));
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
+    A((void **)&h->tot_counts, sizeof(int) * E);
+    A((void **)&h->tot_stats, sizeof(double) * (E + 2));
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
     A((void **)&h->aux_mom, sizeof(float) * h->Er);

@@ -184,6 +184,8 @@ struct ScanArgs {
     int aux_free, aux_use_comp, aux_update;
     float aux_cw, aux_lr, aux_momentum;
     float *aux_bias, *aux_mom;  // [E] device state
+    int *tot_counts;            // [E]   work: column totals of blk_counts
+    double *tot_stats;          // [E+2] work: column totals of blk_stats
 };
 
 struct PermuteArgs {

@@ -257,6 +257,138 @@ __device__ __forceinline__ float token_max(float v) {  // NaN ignored (v > m is 
     return v;
 }
 
+// The value of the partner lane in butterfly step o (1, 2, 4) of an 8-lane
+// group, by DPP: lane ^ 1, lane ^ 2 (quad permutations), then the mirrored
+// lane of the other quad (7 - lane within the group; after two steps every
+// lane of a quad holds the same list, so any pairing of the two quads works).
+__device__ __forceinline__ int lane_swap8(int o, int v) {
+    if (o == 1) return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
+    if (o == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);              // row_half_mirror
+}
+
+// Entry (key a, index ia) before entry (b, ib) in the top-k order: larger
+// isless key, then the lower index (partialsortperm's Perm ordering).
+__device__ __forceinline__ bool topk_before(uint32_t a, int ia, uint32_t b, int ib) {
+    return a > b || (a == b && ia < ib);
+}
+
+// Top-K of row p[lo, n) by the order above, over the TPT consecutive lanes of
+// a token: lane rs keeps the best K of elements rs, rs + TPT, ... in K sorted
+// register slots, then log2(TPT) butterfly steps merge the lanes' lists (a
+// strict total order, so both partners end with the same list).  Every lane
+// of the wave must call it (rows of invalid tokens pass active = false).
+// Slots past the row's size stay empty (key 0, below every float's key).
+template <int K, int TPT>
+__device__ __forceinline__ void topk_lanes(const float *__restrict__ p, int lo, int n, int rs, bool active, int *sel,
+                                           float *val) {
+    uint32_t kb[K];
+    int ib[K];
+    float vb[K];
+#pragma unroll
+    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0x7fffffff; vb[q] = 0.0f; }
+    auto insert = [&](uint32_t ck, int ci, float cv) {
+        if (!topk_before(ck, ci, kb[K - 1], ib[K - 1])) return;
+        bool shift = false;  // once inserted, every later slot moves down by one
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            const bool ins = shift || topk_before(ck, ci, kb[q], ib[q]);
+            const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
+            kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
+            ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
+            shift = ins;
+        }
+    };
+    if (active) {
+        for (int i0 = rs; i0 < n; i0 += 4 * TPT) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = p[min(i0 + u * TPT, n - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * TPT;
+                if (i < n && i >= lo) insert(isless_key(v[u]), i, v[u]);
+            }
+        }
+    }
+    // a rolled loop: its body is fetched once (the kernel's once-per-block
+    // phases are bound by instruction fetch, not by their arithmetic)
+#pragma unroll 1
+    for (int o = 1; o < TPT; o <<= 1) {
+        uint32_t pk[K];
+        int pi[K];
+        float pv[K];
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            pk[q] = (uint32_t)lane_swap8(o, (int)kb[q]);
+            pi[q] = lane_swap8(o, ib[q]);
+            pv[q] = __int_as_float(lane_swap8(o, __float_as_int(vb[q])));
+        }
+#pragma unroll
+        for (int q = 0; q < K; ++q) insert(pk[q], pi[q], pv[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+        sel[q] = ib[q];
+        val[q] = vb[q];
+    }
+}
+
+// Top-k of row p[lo, n) for n - lo <= 8 TPT by ranks: lane rs owns elements
+// lo + rs + TPT u and counts, over the row, the elements before each of them
+// in the top-k order; an element of rank r < k is slot r.  No lane exchanges
+// anything: the owner writes its winners to ksel / kval directly.
+template <int TPT>
+__device__ __forceinline__ void topk_ranks(const float *__restrict__ p, int lo, int n, int k, int rs, bool active,
+                                           int *ksel, float *kval) {
+    constexpr int U = 8;
+    if (!active) return;
+    uint64_t mine[U];  // (key, inverted index): larger is earlier in the order
+    int rank[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = lo + rs + TPT * u;
+        const float v = p[min(i, n - 1)];
+        mine[u] = ((uint64_t)isless_key(v) << 32) | (uint32_t)(0x7fffffff - i);
+        rank[u] = 0;
+    }
+    for (int j0 = lo; j0 < n; j0 += 4) {
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = p[min(j0 + c, n - 1)];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int j = j0 + c;
+            const uint64_t kj = ((uint64_t)isless_key(v[c]) << 32) | (uint32_t)(0x7fffffff - j);
+#pragma unroll
+            for (int u = 0; u < U; ++u) rank[u] += (j < n && kj > mine[u]) ? 1 : 0;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = lo + rs + TPT * u;
+        if (i < n && rank[u] < k) {
+            ksel[rank[u]] = i;
+            kval[rank[u]] = p[i];
+        }
+    }
+}
+
+template <int TPT>
+__device__ __forceinline__ void topk_lanes_k(const float *__restrict__ p, int lo, int n, int k, int rs, bool active,
+                                             int *sel, float *val) {
+    switch (k) {
+    case 1: topk_lanes<1, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 2: topk_lanes<2, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 3: topk_lanes<3, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 4: topk_lanes<4, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 5: topk_lanes<5, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 6: topk_lanes<6, TPT>(p, lo, n, rs, active, sel, val); break;
+    case 7: topk_lanes<7, TPT>(p, lo, n, rs, active, sel, val); break;
+    default: topk_lanes<8, TPT>(p, lo, n, rs, active, sel, val); break;
+    }
+}
+
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma clang fp contract(off)
     // Block: kRouteBlock tokens, kRouteThreads threads.  The recipe's
@@ -268,11 +400,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     // for this layer's E (dynamic LDS).  Every global output is written in the
     // last phase: a store's data register may not be reused before the store
     // has completed, so stores in between would stall the phases that follow.
-    constexpr int NWV = 1;  // the token threads form one wave
     constexpr int TPT = kRouteThreads / kRouteBlock;
     static_assert(TPT == 8 && kRouteBlock * TPT == kRouteThreads, "threads per token");
     extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
-    __shared__ int wcnt[NWV][MOE_MAX_EXPERTS];
+    // stable ranks: bit i of emask[e][i / 32] marks entry i (token * kt + slot)
+    // of expert e + 1 in this block; ent_e holds each entry's expert
+    __shared__ unsigned emask[MOE_MAX_EXPERTS * MOE_MAX_TOPK];
+    __shared__ int ent_e[kRouteBlock * MOE_MAX_TOPK];
+    __shared__ int ksel[kRouteBlock][MOE_MAX_TOPK];    // top-k of each token: experts (0-based)
+    __shared__ float kval[kRouteBlock][MOE_MAX_TOPK];  // and their probabilities
     __shared__ double red[2][kRouteBlock];
     __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock], zsum[kRouteBlock];
     __shared__ double hsum[kRouteBlock];
@@ -290,8 +426,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     float *srow = prow + kRouteBlock * RW;  // output probabilities (after it)
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
     const int t0 = blockIdx.x * kRouteBlock;
     const int t = t0 + tid;
     const int ntok = min(kRouteBlock, a.T - t0);
@@ -301,7 +435,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     const int rt = tid / TPT, rs = tid - rt * TPT;  // row-parallel phases: token rt, lane rs of it
     const bool rvalid = rt < ntok;
 
-    for (int i = tid; i < NWV * MOE_MAX_EXPERTS; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
+    for (int i = tid; i < MOE_MAX_EXPERTS * MOE_MAX_TOPK; i += kRouteThreads) emask[i] = 0u;
 
     // (1) router logits: the K-slice partial sums in slice order, then the
     // bias.  Elements q = tid + 256 u; the slices (and biases) of 4 elements
@@ -309,15 +443,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     if (softmax) {
     const int nq = ntok * a.Er;
     const long long sstride = (long long)a.T * a.Er;
-    // elements per thread per round (block-uniform): up to 4 rows of
-    // kRouterMaxSlices partials in flight, but never more than the block has
-    const int nu = min(4, (nq + kRouteThreads - 1) / kRouteThreads);
-    for (int q0 = 0; q0 < nq; q0 += 4 * kRouteThreads) {
-        long long o[4];
-        int qq[4];
-        float v[4];
+    // elements per thread per round (block-uniform): up to 8, with the
+    // partials of 4 slices each in flight, but never more than the block has
+    constexpr int RU = 8;
+    const int nu = min(RU, (nq + kRouteThreads - 1) / kRouteThreads);
+    for (int q0 = 0; q0 < nq; q0 += RU * kRouteThreads) {
+        long long o[RU];
+        int qq[RU];
+        float v[RU];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < RU; ++u) {
             qq[u] = min(q0 + u * kRouteThreads + tid, nq - 1);
             const int tt = qq[u] / a.Er;
             o[u] = (long long)(t0 + tt) * a.Er + (qq[u] - tt * a.Er);
@@ -326,20 +461,20 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         // slices in groups of 4 (clamped to the last slice): every load of a
         // group is issued before the group's sums, which run in slice order
         for (int sg = 0; sg < a.nks; sg += 4) {
-            float pv[4][4];
+            float pv[RU][4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < RU; ++u)
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
                     if (u < nu) pv[u][c] = a.part[min(sg + c, a.nks - 1) * sstride + o[u]];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < RU; ++u)
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
                     if (u < nu && sg + c < a.nks) v[u] = (sg + c == 0) ? pv[u][c] : v[u] + pv[u][c];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < RU; ++u) {
             const int q = q0 + u * kRouteThreads + tid;
             if (u < nu && q < nq) {
                 const int tt = q / a.Er, i = q - tt * a.Er;
@@ -426,8 +561,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
                     pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
                 }
                 srow[rt * RW + i] = pv;
+                // p * log(p + 1e-8) with p + 1e-8 in Float64 as Julia
+                // promotes it; the log in fp32 (a statistic: the mean entropy
+                // is checked to 1e-5)
                 const double pd = (double)pv;
-                hs = hs + pd * log(pd + 1e-8);
+                hs = hs + pd * (double)logf((float)(pd + 1e-8));
             }
         }
         hs = token_sum<TPT>(hs);
@@ -435,6 +573,29 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     }
     __syncthreads();
     }  // softmax phases
+
+    // (6a) top-k of each token's probabilities over its TPT lanes; the shared
+    // rows of SharedExpertGating are left out (the base gate sees the routed
+    // rows only)
+    if (!a.given) {
+        if (a.E - ns <= 8 * TPT) {
+            // up to 64 routed experts: ranks (no cross-lane dependence chain)
+            topk_ranks<TPT>(prow + rt * RW, ns, a.E, a.k, rs, rvalid, ksel[rt], kval[rt]);
+        } else {
+            int sl[MOE_MAX_TOPK];
+            float vl[MOE_MAX_TOPK];
+            topk_lanes_k<TPT>(prow + rt * RW, ns, a.E, a.k, rs, rvalid, sl, vl);
+            if (rvalid && rs == 0) {
+#pragma unroll
+                for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                    if (q < a.k) {
+                        ksel[rt][q] = sl[q];
+                        kval[rt][q] = vl[q];
+                    }
+            }
+        }
+    }
+    __syncthreads();
 
     int ex[MOE_MAX_TOPK];     // 1-based expert ids of this token's slots
     float gx[MOE_MAX_TOPK];   // their gates
@@ -459,8 +620,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
                 gx[j] = a.gates[ent];
             }
         if (softmax) {
-            const float lse = zsep ? zmax[tid] + (float)log((double)zsum[tid])
-                                   : rmax[tid] + (float)log((double)rsum[tid]);
+            const float lse = zsep ? zmax[tid] + logf(zsum[tid])
+                                   : rmax[tid] + logf(rsum[tid]);
             zterm = (double)(lse * lse);
             hterm = -hsum[tid];
         }
@@ -468,27 +629,39 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         float *p = prow + tid * RW;
         int sel[MOE_MAX_TOPK];
         float g[MOE_MAX_TOPK];
+        {
+            // the winners in slot order; gates: p of the slots over their sum
+            // in slot order
+            float v[MOE_MAX_TOPK];
+#pragma unroll
+            for (int q = 0; q < MOE_MAX_TOPK; ++q) {
+                sel[q] = (q < a.k) ? ksel[tid][q] : 0;
+                v[q] = (q < a.k) ? kval[tid][q] : 0.0f;
+            }
+            float sg = v[0];
+#pragma unroll
+            for (int q = 1; q < MOE_MAX_TOPK; ++q)
+                if (q < a.k) sg = sg + v[q];
+#pragma unroll
+            for (int q = 0; q < MOE_MAX_TOPK; ++q) g[q] = v[q] / sg;
+        }
         if (soft) {
             // SoftMoEGating: top-k of the scaled-softmax probabilities; the
             // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
             // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
-            topk_row(p, a.E, a.k, sel, g);
 #pragma unroll
             for (int j = 0; j < MOE_MAX_TOPK; ++j)
                 if (j < a.k) {
                     ex[j] = sel[j] + 1;
                     gx[j] = p[j];
                 }
-            const float lse = zmax[tid] + (float)log((double)zsum[tid]);
+            const float lse = zmax[tid] + logf(zsum[tid]);
             zterm = (double)(lse * lse);
         } else if (shared_gate) {
             // top-k and gates on the routed probabilities as the base gate
-            // returns them (before the 1 - ns/E scaling); the row is read from
-            // its 16-byte-aligned start with the first ns entries masked
+            // returns them (before the 1 - ns/E scaling)
             const double gscale = 1.0 - (double)ns / (double)a.kt;
             const float gshared = 1.0f / (float)a.kt;
-            for (int i = 0; i < ns; ++i) p[i] = -INFINITY;  // below every probability
-            topk_row(p, a.E, a.k, sel, g);
 #pragma unroll
             for (int j = 0; j < MOE_MAX_TOPK; ++j) {
                 if (j < ns) {
@@ -505,10 +678,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
                         }
                 }
             }
-            const float lse = zmax[tid] + (float)log((double)zsum[tid]);
+            const float lse = zmax[tid] + logf(zsum[tid]);
             zterm = (double)(lse * lse);
         } else {
-            topk_row(p, a.E, a.k, sel, g);
             if (a.lsh == 0) {
 #pragma unroll
                 for (int j = 0; j < MOE_MAX_TOPK; ++j)
@@ -538,8 +710,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
                     }
                 }
             }
-            // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe
-            const float lse = rmax[tid] + (float)log((double)rsum[tid]);
+            // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
+            // the log in Float32 as Julia takes it of the Float32 sum
+            const float lse = rmax[tid] + logf(rsum[tid]);
             zterm = (double)(lse * lse);
         }
         hterm = -hsum[tid];  // entropy of update_stats!, Float64
@@ -547,40 +720,25 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     __syncthreads();
 
     // ---- stable rank of each entry among the block's entries of its expert ----
-    int r[MOE_MAX_TOPK];
-    unsigned done = 0;
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_TOPK; ++j) {
-        r[j] = 0;
-        if (j >= a.kt || ex[j] <= 0) done |= 1u << j;
-    }
-    const unsigned all = (1u << MOE_MAX_TOPK) - 1u;
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    while (true) {
-        const bool has = done != all;
-        const uint64_t act = __ballot(has);
-        if (act == 0) break;
-        const int leader = __ffsll((unsigned long long)act) - 1;
-        int mine = 0;
-        if (has) {
-            const int j0 = __ffs(~done & all) - 1;
-#pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j == j0) mine = ex[j];
-        }
-        const int estar = __builtin_amdgcn_readlane(mine, leader);
-        int js = -1;
+    // (entries in token-then-slot order, as the bucket loop visits them)
+    const int nent = kRouteBlock * a.kt;
+    if (tok) {
 #pragma unroll
         for (int j = 0; j < MOE_MAX_TOPK; ++j)
-            if (!((done >> j) & 1u) && ex[j] == estar) js = j;
-        const uint64_t mm = __ballot(js >= 0);
-        if (js >= 0) {
-#pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j == js) r[j] = __popcll(mm & lt_mask);
-            done |= 1u << js;
-        }
-        if (lane == leader) wcnt[wave][estar - 1] = __popcll(mm);
+            if (j < a.kt) ent_e[tid * a.kt + j] = ex[j];
+    }
+    __syncthreads();
+    int my_e = 0, my_r = 0;
+    if (tid < nent) {
+        my_e = ent_e[tid];
+        if (my_e > 0) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (tid >> 5)], 1u << (tid & 31));
+    }
+    __syncthreads();
+    if (tid < nent && my_e > 0) {
+        const unsigned *m = &emask[(my_e - 1) * MOE_MAX_TOPK];
+        int rr = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
+        for (int w = 0; w < (tid >> 5); ++w) rr += __popc(m[w]);
+        my_r = rr;
     }
     if (tok) {
         red[0][tid] = zterm;
@@ -613,18 +771,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
                 const long long ent = (long long)t * a.kt + j;
                 a.idx[ent] = ex[j];
                 a.gates[ent] = gx[j];
-                int base = 0;
-                if (ex[j] > 0)
-                    for (int w = 0; w < wave; ++w) base += wcnt[w][ex[j] - 1];
-                a.rank[ent] = base + r[j];
             }
         }
     }
+    if (out_gating && tid < ntok * a.kt) a.rank[(long long)t0 * a.kt + tid] = my_r;
     const int nb = blockIdx.x;
     for (int e = tid; e < a.Eh; e += kRouteThreads) {
         if (out_gating) {
             int c = 0;
-            for (int w = 0; w < NWV; ++w) c += wcnt[w][e];
+#pragma unroll
+            for (int w = 0; w < MOE_MAX_TOPK; ++w) c += __popc(emask[e * MOE_MAX_TOPK + w]);
             a.blk_counts[(long long)nb * a.Eh + e] = c;
         }
         if (out_probs) {
@@ -757,8 +913,9 @@ hipError_t launch_expert_choice(const float *logits, const float *probs, int T, 
 }
 
 // ============================================================================
-// Scan: one block.  Per-expert totals, capacity clamp, offsets, per-block rank
-// bases, the (expert, m0) GEMM tile list and the loss scalars.
+// Scan: per-expert totals, per-block rank bases (many blocks), then the
+// capacity clamp, offsets, the (expert, m0) GEMM tile list and the loss
+// scalars (one block).
 // ============================================================================
 // update_bias!(::AuxiliaryFreeLoss, expert_indices) after its counter check
 // (src/balancing/auxiliary_free.jl:36-69), one thread, with Julia's types:
@@ -782,48 +939,36 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
     for (int e = 0; e < E; ++e) bias[e] = bias[e] - mean;
 }
 
-__global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
+// Scan, part 1: many blocks.  Block b takes kScanCols columns (expert
+// counts and fp64 statistics of column c; columns E, E + 1: the z and
+// entropy sums) and splits the nblk route-block rows into kScanChunks
+// contiguous chunks, one thread per (chunk, column): the chunk sums go to
+// LDS, every thread then writes the rank bases of its chunk's rows (the
+// counts of the earlier chunks, then of the chunk's earlier rows), and the
+// first chunk's threads the column totals, chunk sums added in chunk order.
+constexpr int kScanCols = 8;
+constexpr int kScanChunks = 32;
+
+__global__ __launch_bounds__(kScanCols * kScanChunks) void scan_columns_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
-    constexpr int MAXC = 1024;  // chunk partials (one per thread)
-    __shared__ int cnt[MOE_MAX_EXPERTS];
-    __shared__ int off[MOE_MAX_EXPERTS + 1];
-    __shared__ int tstart[MOE_MAX_EXPERTS + 1];
-    __shared__ double psum[MOE_MAX_EXPERTS];
-    __shared__ double zh[2];
-    __shared__ int cap_s;
-    __shared__ int csum[MAXC];
-    __shared__ double ssum[MAXC];
-    const int tid = threadIdx.x;
-    if (tid == 0) {
-        int cap = INT_MAX;
-        if (a.training && a.drop) {
-            // capacity = ceil(Int, capacity_factor * batch_size / num_experts), Float32
-            const float c = ceilf((a.capacity_factor * (float)a.T) / (float)a.E);
-            cap = (c >= 2147483647.0f) ? INT_MAX : (int)c;
-        }
-        cap_s = cap;
-        a.cap_out[0] = cap;
-    }
-    // Thread (g, c), tid = g * NC + c, owns column c (an expert's counts and
-    // probability sums; columns E and E + 1: the z and entropy sums) over the
-    // g-th chunk of CH blocks.  Consecutive threads read consecutive columns of
-    // one block row, so the loads are coalesced; 8 rows are loaded at a time.
+    __shared__ int csum[kScanChunks][kScanCols];
+    __shared__ double ssum[kScanChunks][kScanCols];
     const int NC = a.E + 2;
-    const int G = max(1, min(MAXC / NC, (a.nblk + 7) / 8));  // chunks of >= 8 blocks
-    const int CH = (a.nblk + G - 1) / G;
-    const int g = tid / NC, c = tid - g * NC;
-    const bool act = g < G;
-    const int b0 = g * CH, b1 = min(a.nblk, b0 + CH);
+    const int c = blockIdx.x * kScanCols + (threadIdx.x % kScanCols);
+    const int g = threadIdx.x / kScanCols;
+    const int R = (a.nblk + kScanChunks - 1) / kScanChunks;
+    const int b0 = min(a.nblk, g * R), b1 = min(a.nblk, b0 + R);
+    const bool col = c < NC, cnt_col = c < a.E;
     int cs = 0;
     double ss = 0.0;
-    if (act) {
+    if (col) {
         for (int b = b0; b < b1; b += 8) {
             int cv[8];
             double sv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int bb = min(b + u, b1 - 1);
-                cv[u] = (c < a.E) ? a.blk_counts[(long long)bb * a.E + c] : 0;
+                cv[u] = cnt_col ? a.blk_counts[(long long)bb * a.E + c] : 0;
                 sv[u] = a.blk_stats[(long long)bb * NC + c];
             }
 #pragma unroll
@@ -833,15 +978,13 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
                     ss += sv[u];
                 }
         }
-        csum[tid] = cs;
-        ssum[tid] = ss;
     }
+    csum[g][threadIdx.x % kScanCols] = cs;
+    ssum[g][threadIdx.x % kScanCols] = ss;
     __syncthreads();
-    if (act && c < a.E) {
-        // rank base of each block of the chunk: the counts of the chunks
-        // before it, then of the chunk's earlier blocks
+    if (cnt_col) {
         int base = 0;
-        for (int q = 0; q < g; ++q) base += csum[q * NC + c];
+        for (int q = 0; q < g; ++q) base += csum[q][threadIdx.x % kScanCols];
         for (int b = b0; b < b1; b += 8) {
             int cv[8];
 #pragma unroll
@@ -854,48 +997,84 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
                 }
         }
     }
-    if (act && g == 0) {
-        // column totals, chunk sums in chunk order (fp64, a fixed order)
+    if (col && g == 0) {
         int tc = 0;
         double ts = 0.0;
-        for (int q = 0; q < G; ++q) {
-            tc += csum[q * NC + c];
-            ts += ssum[q * NC + c];
+        for (int q = 0; q < kScanChunks; ++q) {
+            tc += csum[q][threadIdx.x % kScanCols];
+            ts += ssum[q][threadIdx.x % kScanCols];
         }
-        if (c < a.E) {
-            cnt[c] = min(tc, cap_s);
-            psum[c] = ts;
-        } else {
-            zh[c - a.E] = ts;
+        if (cnt_col) a.tot_counts[c] = tc;
+        a.tot_stats[c] = ts;
+    }
+}
+
+// Scan, part 2: one block.  Capacity clamp, offsets, per-expert GEMM tile
+// starts and the (expert, m0) tile list, the Switch and z losses, the mean
+// entropy and the AuxiliaryFreeLoss step, from the column totals.
+__global__ __launch_bounds__(256) void scan_finish_kernel(ScanArgs a) {
+#pragma clang fp contract(off)
+    __shared__ int cnt[MOE_MAX_EXPERTS];
+    __shared__ int off[MOE_MAX_EXPERTS + 1];
+    __shared__ int tstart[MOE_MAX_EXPERTS + 1];
+    __shared__ float fp[MOE_MAX_EXPERTS];
+    __shared__ int cap_s;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int cap = INT_MAX;
+        if (a.training && a.drop) {
+            // capacity = ceil(Int, capacity_factor * batch_size / num_experts), Float32
+            const float cf = ceilf((a.capacity_factor * (float)a.T) / (float)a.E);
+            cap = (cf >= 2147483647.0f) ? INT_MAX : (int)cf;
+        }
+        cap_s = cap;
+        a.cap_out[0] = cap;
+    }
+    __syncthreads();
+    const float total = (float)((long long)a.T * a.kl);
+    for (int e = tid; e < a.E; e += 256) {
+        const int ce = min(a.tot_counts[e], cap_s);
+        cnt[e] = ce;
+        // the terms f_e * P_e of the Switch loss (src/balancing/losses.jl:15-36)
+        // over the a.Np probability rows; with shared experts of the layer the
+        // ids are the shifted routed ids and expert e < lsh holds none of them
+        if (e < a.Np) {
+            float f = (e < a.lsh) ? 0.0f : (float)ce;
+            if (a.T * a.kl > 0) f = f / total;
+            const float P = (float)a.tot_stats[e] / (float)a.T;
+            fp[e] = f * P;
         }
     }
     __syncthreads();
     if (tid == 0) {
+        // sequential prefixes and sums, the LDS values read 8 at a time
         int o = 0, ts = 0;
-        for (int e = 0; e < a.E; ++e) {
-            off[e] = o;
-            tstart[e] = ts;
-            o += cnt[e];
-            ts += (cnt[e] + a.bm - 1) / a.bm;
+        for (int e0 = 0; e0 < a.E; e0 += 8) {
+            int cv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cv[u] = cnt[min(e0 + u, a.E - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (e0 + u < a.E) {
+                    off[e0 + u] = o;
+                    tstart[e0 + u] = ts;
+                    o += cv[u];
+                    ts += (cv[u] + a.bm - 1) / a.bm;
+                }
         }
         off[a.E] = o;
         tstart[a.E] = ts;
         a.num_tiles[0] = ts;
 
-        // losses (src/balancing/losses.jl:15-36, 103-114): N = a.Np probability
-        // rows, f over the router's kl * T index entries counted by id <= N.
-        // With shared experts of the layer the ids are the shifted routed ids
-        // (src/core/moe_layer.jl:172-182): expert e < lsh holds only shared
-        // entries, which the router's indices do not contain.
-        const double zs = zh[0], hs = zh[1];
-        const float total = (float)((long long)a.T * a.kl);
+        const double zs = a.tot_stats[a.E], hs = a.tot_stats[a.E + 1];
         float s = 0.0f;
-        for (int e = 0; e < a.Np; ++e) {
-            float f = (e < a.lsh) ? 0.0f : (float)cnt[e];
-            if (a.T * a.kl > 0) f = f / total;
-            const float P = (float)psum[e] / (float)a.T;
-            const float fp = f * P;
-            s = (e == 0) ? fp : s + fp;
+        for (int e0 = 0; e0 < a.Np; e0 += 8) {
+            float fv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) fv[u] = fp[min(e0 + u, a.Np - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (e0 + u < a.Np) s = (e0 + u == 0) ? fv[u] : s + fv[u];
         }
         // AuxiliaryFreeLoss: complementary_weight * Switch(1.0f0) or 0.0f0
         // (src/balancing/auxiliary_free.jl:78-87)
@@ -912,17 +1091,17 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
         if (a.loss_out) a.loss_out[0] = loss;
         if (a.aux_free && a.training && a.aux_update) {
             // the kept entries of each expert are the counts after capacity
-            long long total = 0;
-            for (int e = 0; e < a.E; ++e) total += cnt[e];
-            aux_free_step(cnt, total, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
+            long long kept = 0;
+            for (int e = 0; e < a.E; ++e) kept += cnt[e];
+            aux_free_step(cnt, kept, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
         }
     }
     __syncthreads();
-    for (int e = tid; e <= a.E; e += blockDim.x) {
+    for (int e = tid; e <= a.E; e += 256) {
         a.offsets[e] = off[e];
         a.tile_start[e] = tstart[e];
     }
-    for (int e = tid; e < a.E; e += blockDim.x) {
+    for (int e = tid; e < a.E; e += 256) {
         a.counts[e] = cnt[e];
         const int nt = tstart[e + 1] - tstart[e];
         for (int i = 0; i < nt; ++i) a.tiles[tstart[e] + i] = make_int2(e, i * a.bm);
@@ -930,7 +1109,10 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
 }
 
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, a);
+    const int NC = a.E + 2;
+    hipLaunchKernelGGL(scan_columns_kernel, dim3((NC + kScanCols - 1) / kScanCols), dim3(kScanCols * kScanChunks), 0, s,
+                       a);
+    hipLaunchKernelGGL(scan_finish_kernel, dim3(1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1263,7 +1445,7 @@ __global__ __launch_bounds__(256) void z_loss_kernel(const float *logits, int T,
         for (int i = 0; i < E; ++i) if (l[i] > m) m = l[i];
         float s = 0.0f;
         for (int i = 0; i < E; ++i) s = s + (float)exp((double)(l[i] - m));
-        const float lse = m + (float)log((double)s);
+        const float lse = m + logf(s);
         acc += (double)(lse * lse);
     }
     red[tid] = acc;
