@@ -376,8 +376,11 @@ using ic = std::integral_constant<int, N>;
 // ============================================================================
 // 4-wave interleaved kernel, BM = 128 or 256.
 // ============================================================================
-template <int MODE, int BM, int ACT, int WF8>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_bf16_kernel(
+// OCC: workgroups per CU.  The up GEMM of 128-row tiles (small experts,
+// weight-bandwidth bound) runs two per CU on a shorter ring, so one
+// workgroup's prologue and epilogue overlap the other's main loop.
+template <int MODE, int BM, int ACT, int WF8, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
     constexpr int NWAVE = 4;
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
@@ -385,7 +388,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int BROWB = WF8 ? 32 : 64; // bytes per LDS B row
     constexpr int A_BYTES = BM * ROWB;
     constexpr int STAGE = A_BYTES + 256 * BROWB;
-    constexpr int NS = (BM == 256 && !WF8) ? 4 : 6;  // LDS ring slots (<= 144 KB)
+    // LDS ring slots (<= 144 KB per CU)
+    constexpr int NS = (OCC == 2) ? (WF8 ? 4 : 3) : ((BM == 256 && !WF8) ? 4 : 6);
     constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
     constexpr int WN = 128;              // wave tile columns (2 waves along N)
     constexpr int IM = WM / 32;          // 32-row blocks per wave
@@ -394,7 +398,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int LB = 256 / ((WF8 ? 32 : 16) * NWAVE);  // B loads per wave per stage
     constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
     constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
-    static_assert(NS * STAGE <= 160 * 1024, "LDS");
+    static_assert(NS * STAGE * OCC <= 160 * 1024, "LDS");
     MOE_LDS_RING(STAGE, NS);
 
     TileJob jb;
@@ -625,7 +629,10 @@ static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
     // 8 XCDs x (slots for the whole tiles + slots for the split items)
     const long long tiles = (long long)g.m_tiles_grid * g.n_tiles;
     const long long total = 8 * ((tiles + 7) / 8 + (g.ksplit > 1 ? (g.ncu + 7) / 8 : 0));
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8>), dim3((unsigned)total), dim3(256), 0, s, g);
+    // two per CU for the up GEMM of 128-row tiles; the down GEMM's tail split
+    // sizes its last round for one workgroup per CU
+    constexpr int OCC = (BM == 128 && MODE != MODE_DOWN) ? 2 : 1;
+    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8, OCC>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 

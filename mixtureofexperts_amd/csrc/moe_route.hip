@@ -1046,36 +1046,56 @@ __global__ __launch_bounds__(256) void scan_finish_kernel(ScanArgs a) {
         }
     }
     __syncthreads();
+    // offsets and GEMM tile starts: exclusive prefixes over the experts by
+    // wave 0 (lane l holds experts 2 l and 2 l + 1; E <= 128)
+    __shared__ float lsum_s;
+    if (tid < 64) {
+        const int e0 = 2 * tid, e1 = e0 + 1;
+        const int c0 = (e0 < a.E) ? cnt[e0] : 0, c1 = (e1 < a.E) ? cnt[e1] : 0;
+        const int n0 = (c0 + a.bm - 1) / a.bm, n1 = (c1 + a.bm - 1) / a.bm;
+        int cs = c0 + c1, ns = n0 + n1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int cu = __shfl_up(cs, o), nu = __shfl_up(ns, o);
+            if (tid >= o) {
+                cs += cu;
+                ns += nu;
+            }
+        }
+        const int ce = cs - (c0 + c1), ne = ns - (n0 + n1);  // exclusive
+        if (e0 <= a.E) {
+            off[e0] = ce;
+            tstart[e0] = ne;
+        }
+        if (e1 <= a.E) {
+            off[e1] = ce + c0;
+            tstart[e1] = ne + n0;
+        }
+        if (tid == 63) {  // the totals (also for E = 128, past the last pair)
+            off[a.E] = cs;
+            tstart[a.E] = ns;
+        }
+        // the Switch-loss sum over the a.Np terms: in expert order up to 16
+        // experts (Julia's sequential sum), else a fixed tree (Julia's order
+        // for longer arrays is its SIMD reduction, not reproduced)
+        float part = 0.0f;
+        if (a.Np > 16) {
+            part = (e0 < a.Np) ? fp[e0] : 0.0f;
+            if (e1 < a.Np) part = part + fp[e1];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) part = part + __shfl_xor(part, o);
+        } else if (tid == 0) {
+            part = fp[0];
+            for (int e = 1; e < a.Np; ++e) part = part + fp[e];
+        }
+        if (tid == 0) lsum_s = part;
+    }
+    __syncthreads();
     if (tid == 0) {
-        // sequential prefixes and sums, the LDS values read 8 at a time
-        int o = 0, ts = 0;
-        for (int e0 = 0; e0 < a.E; e0 += 8) {
-            int cv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) cv[u] = cnt[min(e0 + u, a.E - 1)];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (e0 + u < a.E) {
-                    off[e0 + u] = o;
-                    tstart[e0 + u] = ts;
-                    o += cv[u];
-                    ts += (cv[u] + a.bm - 1) / a.bm;
-                }
-        }
-        off[a.E] = o;
-        tstart[a.E] = ts;
+        const int ts = tstart[a.E];
         a.num_tiles[0] = ts;
-
         const double zs = a.tot_stats[a.E], hs = a.tot_stats[a.E + 1];
-        float s = 0.0f;
-        for (int e0 = 0; e0 < a.Np; e0 += 8) {
-            float fv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) fv[u] = fp[min(e0 + u, a.Np - 1)];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (e0 + u < a.Np) s = (e0 + u == 0) ? fv[u] : s + fv[u];
-        }
+        const float s = lsum_s;
         // AuxiliaryFreeLoss: complementary_weight * Switch(1.0f0) or 0.0f0
         // (src/balancing/auxiliary_free.jl:78-87)
         float sw;
