@@ -578,13 +578,14 @@ static GemmArgs up_args(moe_handle *h, int mt_grid) {
 // and fold_split_kernel adds their partials to y in range order.
 static int down_ksplit(const moe_handle *h) { return h->bf16_gemm ? kDownSplitMax : 1; }
 
-static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit) {
+static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     GemmArgs g{};
     g.A = h->hbuf; g.lda = h->H_pad;
     g.B0 = h->w2; g.B1 = nullptr;
     g.b_stride = h->w2_stride; g.ldb = h->H_pad;
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
+    g.c_bf16 = (h->bf16_gemm && !y_f32) ? 1 : 0;  // the bf16-kernel paths keep y in bf16
     g.ksplit = ksplit; g.ncu = h->ncu; g.split_ws = h->split_ws;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E;
@@ -602,14 +603,16 @@ static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
     return launch_grouped_gemm(mode, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0, up_args(h, mt_grid), s);
 }
 
-static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksplit) {
+// y_f32: write y in fp32 also on the bf16-kernel path (moe_expert_forward
+// hands y back as fp32); the layer paths keep it in bf16 there.
+static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksplit, bool y_f32 = false) {
     if (h->bf16_gemm) {
-        const GemmArgs g = down_args(h, mt_grid, ksplit);
+        const GemmArgs g = down_args(h, mt_grid, ksplit, y_f32);
         hipError_t e = launch_grouped_gemm_bf16(MODE_DOWN, h->bm, h->wt == WT_FP8, g, s);
         if (e == hipSuccess && ksplit > 1) e = launch_fold_split(h->bm, g, s);
         return e;
     }
-    return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid, 1), s);
+    return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid, 1, true), s);
 }
 
 static int run_experts(moe_handle *h, int T, hipStream_t s) {
@@ -621,7 +624,8 @@ static int run_experts(moe_handle *h, int T, hipStream_t s) {
 
 static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
     CombineArgs c{};
-    c.y = h->y; c.ld_y = h->Dout; c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
+    c.y = h->y; c.ld_y = h->Dout; c.y_bf16 = h->bf16_gemm ? 1 : 0;
+    c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
     c.T = T; c.D = h->Dout; c.kt = h->kc; c.lsh = h->lsh; c.out = out_dev;
     HIP_TRY(h, launch_combine(c, s));
     return MOE_OK;
@@ -800,7 +804,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A(&h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
     A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout);
     // tail split: fewer than ncu split tiles, each with at most kDownSplitMax - 1 partial blocks of BM x 256
-    if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * (kDownSplitMax - 1));
+    if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * kDownSplitMax);
     if (r != MOE_OK) return cleanup(r);
     // Pads of the packed weights and of the activation rows must read as 0.
     hipError_t ze = hipSuccess;
@@ -1226,7 +1230,7 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = launch_up(h, nt, s);
-    if (e == hipSuccess) e = launch_down(h, nt, s, 1);
+    if (e == hipSuccess) e = launch_down(h, nt, s, 1, true);
     if (e == hipSuccess) e = hipMemcpyAsync(y, h->y, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s);
     hipError_t e2 = hipStreamSynchronize(s);
     if (e == hipSuccess) e = e2;

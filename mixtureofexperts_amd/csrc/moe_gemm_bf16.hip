@@ -77,6 +77,7 @@ __device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d)
 
 // Eight fp8 e4m3 bytes (lo: bytes 0-3, hi: bytes 4-7) -> eight bf16 (exact).
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bf16x8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
@@ -221,13 +222,19 @@ __device__ __forceinline__ int b_frag_row(int j, int wn) {
 // ---- epilogue ---------------------------------------------------------------------
 // The MFMA computes the transposed block (weights are its A operand): lane l
 // holds token row l % 32 of the 32-row block and output columns 8 (q / 4) +
-// 4 (l / 32) + q % 4, i.e. four consecutive columns per q / 4, written as one
-// 8-byte (bf16) or 16-byte (fp32) store.  row0: the wave's first tile row.
-// WF8: the accumulators are scaled by the weight rows' scales (s0: W1 or W2,
-// s1: W3) before bias and activation.
-template <int MODE, int ACT, int IM, int JN, int WN, int WF8>
+// 4 (l / 32) + q % 4, i.e. four consecutive columns per q / 4.  row0: the
+// wave's first tile row.  WF8: the accumulators are scaled by the weight
+// rows' scales (s0: W1 or W2, s1: W3) before bias and activation.
+//
+// bf16 outputs (h of both up modes; y of the down GEMM when c_bf16) go to
+// put(ml, lc, v0, v1, v2, v3): tile row ml, tile column lc (a multiple of 4),
+// four values.  The sink either stores them directly (8 bytes per lane: 32
+// rows per store instruction) or stages the tile in LDS for row-contiguous
+// stores (stage_put / store_staged).  fp32 y and the partials of split tiles
+// are stored directly.
+template <int MODE, int ACT, int IM, int JN, int WN, int WF8, typename Put>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
-                                           int row0, int wn, int lane) {
+                                           int row0, int wn, int lane, Put &&put) {
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const long long sofs = (long long)jb.e * g.s_stride;
@@ -243,36 +250,38 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
         // h pad columns [N, Npad) come out as act(0) * 0 = 0 from the zero weight
         // pad rows, so the whole tile is stored (ldc = Npad).
 #pragma unroll
-        for (int i = 0; i < IM; ++i) {
-            const int ml = row0 + i * 32 + r32;
-            if (ml >= jb.rows) continue;
-            uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
+        for (int m = 0; m < JN / 2; ++m)
 #pragma unroll
-            for (int m = 0; m < JN / 2; ++m)
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int lc = wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
+                float sg[4], su[4];
+                scale4(g.s0, jb.n0 + lc, sg);
+                scale4(g.s1, jb.n0 + lc, su);
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int n = jb.n0 + wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
-                    float v[4], sg[4], su[4];
-                    scale4(g.s0, n, sg);
-                    scale4(g.s1, n, su);
+                for (int i = 0; i < IM; ++i) {
+                    const int ml = row0 + i * 32 + r32;
+                    float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         const float gt = WF8 ? acc[i][2 * m][4 * g4 + c] * sg[c] : acc[i][2 * m][4 * g4 + c];
                         const float up = WF8 ? acc[i][2 * m + 1][4 * g4 + c] * su[c] : acc[i][2 * m + 1][4 * g4 + c];
                         v[c] = act_fast<ACT>(gt) * up;
                     }
-                    *(uint2 *)(crow + n) = pack_bf16x4(v[0], v[1], v[2], v[3]);
+                    put(ml, lc, v[0], v[1], v[2], v[3]);
                 }
-        }
+            }
     } else {
         // MODE_STD_UP stores bf16 h (pads are act(b1 pad = 0) of zero rows: 0 for
-        // silu, gelu, relu, identity); MODE_DOWN stores fp32 y with ldc = N.
+        // silu, gelu, relu, identity); MODE_DOWN stores y with ldc = N, in bf16
+        // (c_bf16) or fp32.
         const bool vec4 = (MODE == MODE_STD_UP) || ((g.ldc & 3) == 0);
+        const bool yb = (MODE == MODE_STD_UP) || (g.c_bf16 && jb.nks == 1);
 #pragma unroll
         for (int j = 0; j < JN; ++j)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-                const int n = jb.n0 + wn * WN + j * 32 + 8 * g4 + 4 * half;
+                const int lc = wn * WN + j * 32 + 8 * g4 + 4 * half;
+                const int n = jb.n0 + lc;
                 float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (g.bias && jb.ks == 0) {  // split K: the bias belongs to one partial sum only
                     const float4 bv = *(const float4 *)(g.bias + sofs + n);
@@ -283,25 +292,27 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
 #pragma unroll
                 for (int i = 0; i < IM; ++i) {
                     const int ml = row0 + i * 32 + r32;
-                    if (ml >= jb.rows) continue;
                     f32x16_t a = acc[i][j];
                     if constexpr (WF8) {
 #pragma unroll
                         for (int c = 0; c < 4; ++c) a[4 * g4 + c] = a[4 * g4 + c] * sc[c];
                     }
                     if constexpr (MODE == MODE_STD_UP) {
-                        uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
-                        *(uint2 *)(crow + n) = pack_bf16x4(
-                            act_fast<ACT>(a[4 * g4 + 0] + b4[0]), act_fast<ACT>(a[4 * g4 + 1] + b4[1]),
+                        put(ml, lc, act_fast<ACT>(a[4 * g4 + 0] + b4[0]), act_fast<ACT>(a[4 * g4 + 1] + b4[1]),
                             act_fast<ACT>(a[4 * g4 + 2] + b4[2]), act_fast<ACT>(a[4 * g4 + 3] + b4[3]));
+                    } else if (yb) {
+                        put(ml, lc, a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1], a[4 * g4 + 2] + b4[2],
+                            a[4 * g4 + 3] + b4[3]);
                     } else {
-                        // K range 0 (or an unsplit tile) writes y; range r >= 1 its
-                        // partial block in split_ws (BM x 256, row stride 256)
-                        float *crow = (jb.ks == 0)
+                        if (ml >= jb.rows) continue;
+                        // fp32 y: K range 0 (or an unsplit tile) writes y; range
+                        // r >= 1 its partial block in split_ws (BM x 256, row
+                        // stride 256).  bf16 y: every range writes its block.
+                        const long long blk = g.c_bf16 ? (long long)jb.split_j * jb.nks + jb.ks
+                                                       : (long long)jb.split_j * (jb.nks - 1) + jb.ks - 1;
+                        float *crow = (jb.ks == 0 && !g.c_bf16)
                                           ? (float *)g.C + (jb.arow0 + ml) * g.ldc
-                                          : g.split_ws +
-                                                ((long long)jb.split_j * (jb.nks - 1) + jb.ks - 1) * (IM * 64) * 256 +
-                                                (long long)ml * 256 - jb.n0;
+                                          : g.split_ws + blk * (IM * 64) * 256 + (long long)ml * 256 - jb.n0;
                         if (vec4 && n + 3 < g.N) {
                             *(float4 *)(crow + n) = make_float4(a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1],
                                                                 a[4 * g4 + 2] + b4[2], a[4 * g4 + 3] + b4[3]);
@@ -313,6 +324,69 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
                     }
                 }
             }
+    }
+}
+
+// Direct bf16 sink: rows past the tile's valid rows are skipped; the down
+// GEMM's y columns past N are cut (ldc = N, possibly not a multiple of 4).
+template <int MODE>
+struct DirectPut {
+    const GemmArgs &g;
+    const TileJob &jb;
+    __device__ __forceinline__ void operator()(int ml, int lc, float v0, float v1, float v2, float v3) const {
+        if (ml >= jb.rows) return;
+        uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
+        const int n = jb.n0 + lc;
+        if (MODE != MODE_DOWN || (((g.ldc & 3) == 0) && n + 3 < g.N)) {
+            *(uint2 *)(crow + n) = pack_bf16x4(v0, v1, v2, v3);
+        } else {
+            const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (n + c < g.N) crow[n + c] = f32_to_bf16(v[c]);
+        }
+    }
+};
+
+// LDS staging of a bf16 output tile: row ml at row_addr(ml), CW bytes (CH
+// 16-byte chunks) per row, chunk c of row r kept at chunk c ^ (r mod CH), so
+// that both the column-block writes (32 rows, one chunk) and the row reads
+// (one row, all chunks) spread over all LDS banks.
+template <int CH, typename RowAddr>
+struct StagePut {
+    RowAddr row_addr;
+    __device__ __forceinline__ void operator()(int ml, int lc, float v0, float v1, float v2, float v3) const {
+        const int ch = lc >> 3;
+        MOE_LDS_AS uint8_t *p = row_addr(ml) + ((ch ^ (ml & (CH - 1))) << 4) + ((lc & 4) << 1);
+        const uint2 w = pack_bf16x4(v0, v1, v2, v3);
+        *(MOE_LDS_AS u32x2_t *)p = u32x2_t{w.x, w.y};
+    }
+};
+
+// Stores the staged tile: thread t copies chunk t mod CH of rows t / CH + k
+// (256 / CH), U rows' LDS reads in flight before their global stores; a wave
+// writes 1 KB of whole rows per store.  Only the valid rows, and for the
+// down GEMM the chunks below N (N a multiple of 8), are stored.
+template <int MODE, int BM, int CH, typename RowAddr>
+__device__ __forceinline__ void store_staged(const GemmArgs &g, const TileJob &jb, RowAddr row_addr) {
+    constexpr int RPP = 256 / CH;  // rows per pass of the workgroup
+    constexpr int U = 8;
+    const int ch = threadIdx.x % CH;
+    const int rr = threadIdx.x / CH;
+    const bool colok = (MODE != MODE_DOWN) || (jb.n0 + ch * 8 < g.N);
+    uint16_t *cbase = (uint16_t *)g.C + jb.arow0 * g.ldc + jb.n0 + ch * 8;
+    for (int p0 = 0; p0 < jb.rows; p0 += RPP * U) {
+        u32x4_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = min(p0 + u * RPP + rr, BM - 1);
+            v[u] = *(const MOE_LDS_AS u32x4_t *)(row_addr(r) + ((ch ^ (r & (CH - 1))) << 4));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = p0 + u * RPP + rr;
+            if (r < jb.rows && colok) *(u32x4_t *)(cbase + (long long)r * g.ldc) = v[u];
+        }
     }
 }
 
@@ -543,7 +617,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     }
     wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
-    store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane);
+    // bf16 outputs are staged in the (now idle) LDS ring, STAGE / CW rows per
+    // slot, and stored row-contiguously; the down GEMM stages when y is bf16,
+    // the tile not split and N, ldc multiples of 8 (whole 16-byte chunks).
+    constexpr int CW = (MODE == MODE_GATED_UP ? 128 : 256) * 2;  // output bytes per tile row
+    constexpr int CH = CW / 16;
+    constexpr int RPS = STAGE / CW;
+    static_assert(RPS * NS >= BM, "LDS staging of the output tile");
+    const bool staged = (MODE != MODE_DOWN) || (g.c_bf16 && jb.nks == 1 && ((g.N | g.ldc) & 7) == 0);
+    if (staged) {
+        auto row_addr = [&](int r) -> MOE_LDS_AS uint8_t * {
+            const int q = r / RPS;
+            MOE_LDS_AS uint8_t *p = slot(ic<0>{});
+            p = (q == 1) ? slot(ic<1>{}) : p;
+            if constexpr (NS > 2) p = (q == 2) ? slot(ic<2 % NS>{}) : p;
+            if constexpr (NS > 3) p = (q == 3) ? slot(ic<3 % NS>{}) : p;
+            if constexpr (NS > 4) p = (q == 4) ? slot(ic<4 % NS>{}) : p;
+            if constexpr (NS > 5) p = (q == 5) ? slot(ic<5 % NS>{}) : p;
+            return p + (r - q * RPS) * CW;
+        };
+        __syncthreads();  // every wave's ring reads and loads are done
+        store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane,
+                                               StagePut<CH, decltype(row_addr)>{row_addr});
+        __syncthreads();
+        store_staged<MODE, BM, CH>(g, jb, row_addr);
+    } else {
+        store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane, DirectPut<MODE>{g, jb});
+    }
 }
 
 // ============================================================================
@@ -578,9 +678,43 @@ __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
     const int c4 = (threadIdx.x & 63) * 4;
     const int n = n0 + c4;
     const bool vec4 = (g.ldc & 3) == 0 && n + 3 < g.N;
-    const float *__restrict__ ws = g.split_ws + (long long)j * (ts.S - 1) * bm * 256 + c4;
     const long long pstride = (long long)bm * 256;
     const int r0 = blockIdx.y * 16 + (threadIdx.x >> 6);
+    if (g.c_bf16) {
+        // y = bf16(((p0 + p1) + p2) + p3), the partials of all ranges
+        const float *__restrict__ ws = g.split_ws + (long long)j * ts.S * bm * 256 + c4;
+        if (r0 >= rows) return;
+        float4 p[4][kDownSplitMax];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = min(r0 + 4 * u, rows - 1);
+#pragma unroll
+            for (int k = 0; k < kDownSplitMax; ++k)
+                if (k < ts.S) p[u][k] = *(const float4 *)(ws + k * pstride + (long long)r * 256);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = r0 + 4 * u;
+            if (r >= rows) continue;
+            float4 a = p[u][0];
+#pragma unroll
+            for (int k = 1; k < kDownSplitMax; ++k)
+                if (k < ts.S) {
+                    a.x = a.x + p[u][k].x; a.y = a.y + p[u][k].y;
+                    a.z = a.z + p[u][k].z; a.w = a.w + p[u][k].w;
+                }
+            uint16_t *__restrict__ yp = (uint16_t *)g.C + (arow0 + r) * g.ldc + n;
+            if (vec4) {
+                *(uint2 *)yp = pack_bf16x4(a.x, a.y, a.z, a.w);
+            } else {
+                const float av[4] = {a.x, a.y, a.z, a.w};
+                for (int c = 0; c < 4; ++c)
+                    if (n + c < g.N) yp[c] = f32_to_bf16(av[c]);
+            }
+        }
+        return;
+    }
+    const float *__restrict__ ws = g.split_ws + (long long)j * (ts.S - 1) * bm * 256 + c4;
     if (r0 < rows) {
         float4 v[4], p[4][kDownSplitMax - 1];
 #pragma unroll

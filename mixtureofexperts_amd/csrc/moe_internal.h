@@ -212,7 +212,9 @@ struct PermuteArgs {
 // expert-major, then n-tile, then m-tile; tiles >= nfull are split.  K range
 // 0 of a split tile writes y, range r >= 1 writes its partial to split_ws
 // block j (S - 1) + r - 1 (j = tile - nfull; a block is BM x 256 fp32, row
-// stride 256); fold_split_kernel then adds them to y in range order.
+// stride 256); fold_split_kernel then adds them to y in range order.  With
+// a bf16 y every K range r of a split tile writes its partial to block
+// j S + r, and the fold rounds their sum once.
 struct TailSplit {
     int nfull;   // tiles not split
     int S;       // K ranges of each split tile (1: none)
@@ -232,7 +234,8 @@ __host__ __device__ inline TailSplit tail_split(int W, int ncu, int smax, int st
 constexpr int kDownSplitMax = 4;
 
 struct CombineArgs {
-    const float *y; int ld_y;    // [rows][ld_y]
+    const void *y; int ld_y;     // [rows][ld_y], fp32 or (y_bf16) bf16
+    int y_bf16;
     const int *idx; const int *pos_of; const float *gates;
     int T, D, kt;
     int lsh;                     // > 0: out = 0.5 * sum(y_shared / lsh) + 0.5 * routed
@@ -258,6 +261,7 @@ struct GemmArgs {
     int ncu;                             // workgroup slots of one round (compute units)
     float *split_ws;                     // partials of split tiles (MODE_DOWN, ksplit > 1)
     int act;
+    int c_bf16;                          // MODE_DOWN: y in bf16 (else fp32)
 };
 
 // Decode (moe_ffn_forward!, src/llama2/inference.jl:58-121): n tokens, each

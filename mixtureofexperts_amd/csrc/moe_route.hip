@@ -1283,11 +1283,24 @@ hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
 // `expert_out ./ num_shared_experts`, :164-166), routed = the sum above over
 // the rest, out = 0.5f * shared + 0.5f * routed (:179-180).
 //
+// y is fp32, or bf16 (a.y_bf16) where the down GEMM ran on the bf16 kernel;
+// each term is widened to fp32 before it is scaled and summed.
+//
 // Fast path (every one of the token's KT entries kept, rows 16-byte
 // aligned): the entries are sorted by expert in registers, and all y loads of
-// a chunk of U float4 per lane are issued before any is summed.
+// a chunk of U groups of 4 per lane are issued before any is summed.
 // ============================================================================
-template <int KT, bool BLEND>
+template <bool YB>
+__device__ __forceinline__ float4 load_y4(const void *y, long long off) {
+    if (YB) {
+        const uint2 r = *(const uint2 *)((const uint16_t *)y + off);
+        return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                           __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+    }
+    return *(const float4 *)((const float *)y + off);
+}
+
+template <int KT, bool BLEND, bool YB>
 __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
 #pragma clang fp contract(off)
     constexpr int U = (KT >= 8) ? 2 : (KT >= 4 ? 4 : 8);
@@ -1320,7 +1333,7 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int d = min(d0 + u * 256 + lane * 4, a.D - 4);
-                v[i][u] = *(const float4 *)(a.y + (long long)pp[i] * a.ld_y + d);
+                v[i][u] = load_y4<YB>(a.y, (long long)pp[i] * a.ld_y + d);
             }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -1357,7 +1370,16 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
 template <int KT>
 __device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, int t, int lane) {
     if (a.kt != KT) return false;
-    combine_fast<KT, false>(a, t, lane);
+    if (a.y_bf16) combine_fast<KT, false, true>(a, t, lane);
+    else combine_fast<KT, false, false>(a, t, lane);
+    return true;
+}
+
+template <int KT>
+__device__ __forceinline__ bool try_combine_blend(const CombineArgs &a, int t, int lane) {
+    if (a.kt != KT) return false;
+    if (a.y_bf16) combine_fast<KT, true, true>(a, t, lane);
+    else combine_fast<KT, true, false>(a, t, lane);
     return true;
 }
 
@@ -1370,12 +1392,9 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
     if (all_kept) {
         if (a.lsh > 0) {
-            switch (a.kt) {
-            case 2: combine_fast<2, true>(a, t, lane); return;
-            case 3: combine_fast<3, true>(a, t, lane); return;
-            case 4: combine_fast<4, true>(a, t, lane); return;
-            default: break;
-            }
+            if (try_combine_blend<2>(a, t, lane) || try_combine_blend<3>(a, t, lane) ||
+                try_combine_blend<4>(a, t, lane))
+                return;
         } else if (try_combine_fast<2>(a, t, lane) || try_combine_fast<1>(a, t, lane) ||
                    try_combine_fast<8>(a, t, lane) || try_combine_fast<4>(a, t, lane) ||
                    try_combine_fast<6>(a, t, lane)) {
@@ -1407,7 +1426,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     for (int d = lane; d < a.D; d += 64) {
         float acc = 0.0f, sh = 0.0f;
         for (int i = 0; i < n; ++i) {
-            const float v = a.y[(long long)pp[i] * a.ld_y + d];
+            const long long off = (long long)pp[i] * a.ld_y + d;
+            const float v = a.y_bf16 ? bf16_to_f32(((const uint16_t *)a.y)[off]) : ((const float *)a.y)[off];
             if (i < a.lsh) sh = sh + v / (float)a.lsh;
             else acc = acc + gg[i] * v;
         }
