@@ -152,9 +152,9 @@ def cpu_baseline(cfg, wl, sample_tokens):
 
 def up_kernel_name(cfg):
     """Name of the dominant kernel (the expert up GEMM) of a workload."""
-    if cfg["w"] == "bf16":
-        return "grouped_gemm_bf16_kernel (expert up GEMM: {})".format(
-            "W1|W3 with silu*mul epilogue" if cfg["etype"] == "gated" else "W1 + b1 with activation epilogue")
+    if cfg["w"] in ("bf16", "fp8"):
+        return "grouped_gemm_bf16_kernel (expert up GEMM, {} weights: {})".format(
+            cfg["w"], "W1|W3 with silu*mul epilogue" if cfg["etype"] == "gated" else "W1 + b1 with activation epilogue")
     return "grouped_gemm_kernel (expert up GEMM, {} weights)".format(cfg["w"])
 
 
@@ -361,10 +361,11 @@ def main():
     # algorithmic HBM bytes of the memory-bound stages (per launch): read x,
     # the router weight; write indices + gates, per-token logsumexp and probs;
     # permute reads x and writes the k expert-ordered copies; combine reads the
-    # k fp32 expert outputs with their (position, gate) and writes fp32 out
+    # k expert outputs (bf16 on the bf16/fp8-weight paths, else fp32) with
+    # their (position, gate) and writes fp32 out
     router_bytes = T * D * xs + E * D * 4 + T * kt * (4 + 4) + T * 4 + E * T * 4
     permute_bytes = T * D * xs + rows * D * xs
-    combine_bytes = rows * D * 4 + rows * 8 + T * D * 4
+    combine_bytes = rows * D * xs + rows * 8 + T * D * 4
     gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,

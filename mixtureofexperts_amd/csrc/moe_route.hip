@@ -231,7 +231,9 @@ hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s) {
 }
 
 // ============================================================================
-// Gating.  One thread per token, 256 tokens per block.
+// Gating.  kRouteBlock tokens per block of kRouteThreads threads: TPT lanes
+// per token for the per-element work and the top-k, one thread per token for
+// the fp32 sum in expert order and the per-token outputs.
 // ============================================================================
 
 // LDS row stride of the routing kernel for E rows: a multiple of 4 floats
@@ -392,11 +394,12 @@ __device__ __forceinline__ void topk_lanes_k(const float *__restrict__ p, int lo
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 #pragma clang fp contract(off)
     // Block: kRouteBlock tokens, kRouteThreads threads.  The recipe's
-    // order-sensitive steps -- the fp32 softmax sum in expert order and the
-    // top-k -- run one thread per token (threads < kRouteBlock, all in wave 0),
-    // reading the token's LDS row 16 B at a time; the rest runs TPT threads
-    // per token (max, exp and probability terms; the fp64 entropy sum and the
-    // z-loss exponent sum as fixed-order per-token reductions).  Rows are sized
+    // order-sensitive fp32 softmax sum in expert order and the per-token
+    // gates, logsumexp and entropy run one thread per token (threads <
+    // kRouteBlock, all in wave 0), reading the token's LDS row 16 B at a
+    // time; the rest runs TPT threads per token (max, exp and probability
+    // terms, the top-k by ranks or by a lane merge, the fp64 entropy sum and
+    // the z-loss exponent sum as fixed-order per-token reductions).  Rows are sized
     // for this layer's E (dynamic LDS).  Every global output is written in the
     // last phase: a store's data register may not be reused before the store
     // has completed, so stores in between would stall the phases that follow.
