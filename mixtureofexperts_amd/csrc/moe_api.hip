@@ -47,12 +47,16 @@ struct moe_handle {
     bool router_set = false, has_bias = false;
     std::vector<char> expert_set;
     void *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
+    // bf16 kernel handles: the same matrices as B tile images (the packed rows
+    // above stay for the decode caller and the readback)
+    void *w1t = nullptr, *w3t = nullptr, *w2t = nullptr;
     float *s1 = nullptr, *s3 = nullptr, *s2 = nullptr;
     float *b1 = nullptr, *b2 = nullptr;
     long long w1_stride = 0, w2_stride = 0;  // elements per expert
 
     // workspace
     int T_max = 0, nblk_max = 0, rows_max = 0, max_tiles = 0;
+    long long act_rows = 0;     // rows of xp and h (bf16 kernel: max_tiles * bm, tile images)
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
@@ -254,15 +258,25 @@ __global__ void fp8_rows_kernel(const uint8_t *src, int layout, int N, int K, in
     }
 }
 
-// rows [n][D] of fp32/bf16 -> compute type with row stride ld (pads untouched)
-__global__ void convert_rows_kernel(const void *src, int src_bf16, int n, int D, int ct, void *dst, int ld) {
+// rows [n][D] of fp32/bf16 -> compute type with row stride ld (pads
+// untouched); bm > 0: bf16 rows of one expert starting at M tile 0 of the
+// bf16 kernel's A tile image (row r: row r mod bm of tile r / bm, ld / 32 K
+// stages of 64 B, chunk q of a stage at q ^ ((row >> 2) & 3))
+__global__ void convert_rows_kernel(const void *src, int src_bf16, int n, int D, int ct, void *dst, int ld, int bm) {
     const long long total = (long long)n * D;
     for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
          t += (long long)gridDim.x * blockDim.x) {
         const long long r = t / D, c = t % D;
         const float v = src_bf16 ? bf16_to_f32(((const uint16_t *)src)[t]) : ((const float *)src)[t];
-        if (ct == CT_F32) ((float *)dst)[r * ld + c] = v;
-        else ((uint16_t *)dst)[r * ld + c] = f32_to_bf16(v);
+        if (ct == CT_F32) {
+            ((float *)dst)[r * ld + c] = v;
+        } else if (bm > 0) {
+            const long long mt = r / bm, lr = r % bm, st = c / 32;
+            const long long q = ((c % 32) / 8) ^ ((lr >> 2) & 3);
+            ((uint16_t *)dst)[((mt * (ld / 32) + st) * bm + lr) * 32 + q * 8 + c % 8] = f32_to_bf16(v);
+        } else {
+            ((uint16_t *)dst)[r * ld + c] = f32_to_bf16(v);
+        }
     }
 }
 
@@ -486,6 +500,7 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base;
     pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && drop_active(h)) ? 1 : 0;
     pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
+    pa.tiled = h->bf16_gemm ? 1 : 0; pa.bm = h->bm; pa.ktt = h->D_pad / 32; pa.tile_start = h->tile_start;
     pa.copy_rows = mode == PERMUTE_ROWS ? 1 : 0;
     HIP_TRY(h, launch_permute(pa, s));
     return MOE_OK;
@@ -561,7 +576,8 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
 static GemmArgs up_args(moe_handle *h, int mt_grid) {
     GemmArgs g{};
     g.A = h->xp; g.lda = h->D_pad;
-    g.B0 = h->w1; g.B1 = h->gated ? h->w3 : nullptr;
+    g.B0 = h->bf16_gemm ? h->w1t : h->w1;
+    g.B1 = h->gated ? (h->bf16_gemm ? h->w3t : h->w3) : nullptr;
     g.b_stride = h->w1_stride; g.ldb = h->D_pad;
     g.s0 = h->s1; g.s1 = h->s3; g.bias = h->gated ? nullptr : h->b1; g.s_stride = h->H_pad;
     g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
@@ -581,7 +597,7 @@ static int down_ksplit(const moe_handle *h) { return h->bf16_gemm ? kDownSplitMa
 static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     GemmArgs g{};
     g.A = h->hbuf; g.lda = h->H_pad;
-    g.B0 = h->w2; g.B1 = nullptr;
+    g.B0 = h->bf16_gemm ? h->w2t : h->w2; g.B1 = nullptr;
     g.b_stride = h->w2_stride; g.ldb = h->H_pad;
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
@@ -775,6 +791,13 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     // 256-row tiles when experts average at least 384 rows at max_tokens, else 128
     h->bm = (h->bf16_gemm && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
     h->max_tiles = h->rows_max / h->bm + h->E + 1;
+    // bf16 kernel: xp and h are A tile images of up to max_tiles M tiles
+    h->act_rows = h->bf16_gemm ? (long long)h->max_tiles * h->bm : h->rows_max;
+    if (h->bf16_gemm) {
+        A(&h->w1t, wsz * (size_t)h->E * h->w1_stride);
+        if (h->gated) A(&h->w3t, wsz * (size_t)h->E * h->w1_stride);
+        A(&h->w2t, wsz * (size_t)h->E * h->w2_stride);
+    }
     const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
     A((void **)&h->logits_part, sizeof(float) * kRouterMaxSlices * T * h->Er);
@@ -800,8 +823,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->perm, sizeof(int) * T * kt);
     A((void **)&h->pos_of, sizeof(int) * T * kt);
     A((void **)&h->gate_sorted, sizeof(float) * T * kt);
-    A(&h->xp, asz * (size_t)h->rows_max * h->D_pad);
-    A(&h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
+    A(&h->xp, asz * (size_t)h->act_rows * h->D_pad);
+    A(&h->hbuf, asz * (size_t)h->act_rows * h->H_pad);
     A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout);
     // tail split: fewer than ncu split tiles, each with at most kDownSplitMax - 1 partial blocks of BM x 256
     if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * kDownSplitMax);
@@ -816,6 +839,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->w1, wsz * (size_t)h->E * h->w1_stride);
     Z(h->w3, wsz * (size_t)h->E * h->w1_stride);
     Z(h->w2, wsz * (size_t)h->E * h->w2_stride);
+    Z(h->w1t, wsz * (size_t)h->E * h->w1_stride);
+    Z(h->w3t, wsz * (size_t)h->E * h->w1_stride);
+    Z(h->w2t, wsz * (size_t)h->E * h->w2_stride);
     Z(h->s1, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->s3, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
@@ -823,8 +849,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->aux_bias, sizeof(float) * h->Er);
     Z(h->aux_mom, sizeof(float) * h->Er);
-    Z(h->xp, asz * (size_t)h->rows_max * h->D_pad);
-    Z(h->hbuf, asz * (size_t)h->rows_max * h->H_pad);
+    Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);
+    Z(h->hbuf, asz * (size_t)h->act_rows * h->H_pad);
     if (ze == hipSuccess) ze = hipStreamSynchronize(h->stream);
     if (ze != hipSuccess) {
         h->err = std::string("initialising device memory failed: ") + hipGetErrorString(ze);
@@ -870,6 +896,25 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     return MOE_OK;
 }
 
+// The bf16 kernel's B tile images of expert x's packed matrices (W1 / W3 in
+// 128-row blocks when gated, else 256; W2 in 256-row blocks), on the handle's
+// stream after the packing.
+static hipError_t retile_expert(moe_handle *h, int x) {
+    if (!h->bf16_gemm) return hipSuccess;
+    const size_t esz = (h->wt == WT_FP8) ? 1 : 2;
+    const size_t o1 = esz * (size_t)x * h->w1_stride, o2 = esz * (size_t)x * h->w2_stride;
+    const int rb1 = h->gated ? kNPadGated : kNPad;
+    hipError_t e = launch_retile_weights((uint8_t *)h->w1 + o1, (uint8_t *)h->w1t + o1, h->H_pad, h->D_pad, (int)esz,
+                                         rb1, h->stream);
+    if (e == hipSuccess && h->gated)
+        e = launch_retile_weights((uint8_t *)h->w3 + o1, (uint8_t *)h->w3t + o1, h->H_pad, h->D_pad, (int)esz, rb1,
+                                  h->stream);
+    if (e == hipSuccess)
+        e = launch_retile_weights((uint8_t *)h->w2 + o2, (uint8_t *)h->w2t + o2, h->Dout_npad, h->H_pad, (int)esz,
+                                  kNPad, h->stream);
+    return e;
+}
+
 int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dtype, const void *w1, const void *w2,
                    const void *w3, const float *b1, const float *b2, const float *s1, const float *s2,
                    const float *s3) {
@@ -905,6 +950,8 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
     }
     r = pack_matrix(h, layout, src_dtype, w2, s2, h->Dout, h->H, h->H_pad, w2d, s2d);
     if (r != MOE_OK) return r;
+    HIP_TRY(h, retile_expert(h, expert));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
     if (!h->gated) {
         if (b1)
             HIP_TRY(h, hipMemcpy(h->b1 + (size_t)expert * h->H_pad, b1, sizeof(float) * h->H,
@@ -973,6 +1020,7 @@ int moe_init_experts_from_dense(moe_handle *h, int32_t layout, int32_t src_dtype
                 e = pack_f32_rows(h, tmp, Ns[m], Ks[m], Kp[m], (uint8_t *)base + wsz * (size_t)x * stride, sc);
             // tmp is reused by the next matrix: the stream orders the kernels
         }
+        if (e == hipSuccess) e = retile_expert(h, x);
         if (e == hipSuccess) h->expert_set[x] = 1;
     }
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
@@ -1226,7 +1274,7 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
         e = hipMemcpyAsync(h->tile_start, ts.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(convert_rows_kernel, dim3(1024), dim3(256), 0, s, (const void *)xs, 0, n, h->D, h->ct,
-                           h->xp, h->D_pad);
+                           h->xp, h->D_pad, h->bf16_gemm ? h->bm : 0);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = launch_up(h, nt, s);

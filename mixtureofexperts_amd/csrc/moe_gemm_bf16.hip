@@ -7,8 +7,11 @@
 //   MODE_STD_UP   : h = act(A W1^T + b1)              StandardExpert (src/experts/standard.jl:38-47)
 //   MODE_DOWN     : y = h W2^T (+ b2)                 both
 //
-// A is one expert's contiguous segment of rows (the permuted tokens, or h);
-// weights are packed [E][Npad][Kpad], K contiguous, bf16 or fp8 e4m3 (WF8).
+// A (the permuted tokens, or h) and the weights (bf16 or fp8 e4m3, WF8) are
+// read as tile images: each LDS stage's bytes stored contiguously in the
+// order the DMA writes them (load_plan), so every load is a whole-line 1 KB
+// read.  The permute writes xp and the up GEMM's epilogue writes h in that
+// form; the weights are retiled from their packed rows once per upload.
 // fp8 weights stay fp8 in HBM and LDS (half the load bytes); each lane widens
 // its fragments to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact for e4m3, scale
 // 1) and the per-output-channel scale s multiplies the fp32 accumulator in
@@ -36,7 +39,8 @@
 // 64 B per row; the 16-byte chunks of row r are stored at chunk ^ ((r >> 2) & 3)
 // so the fragment reads (32 rows, one chunk) spread over all 64 banks.  Each
 // global_load_lds_dwordx4 writes 1 KB = 16 rows linearly (lane l -> offset
-// 16 l), so the swizzle is applied on the global side.
+// 16 l), so the swizzle is part of the tile images.
+#include <algorithm>
 #include <type_traits>
 
 #include "moe_internal.h"
@@ -119,7 +123,8 @@ struct TileJob {
     int rows;          // valid rows of the tile (<= BM)
     int n0;            // first B row of the tile (first h column in the gated mode)
     int split_j;       // split tiles: index among them (partials in split_ws)
-    long long arow0;   // first A row
+    int mt;            // M tile (tile image block of the A operand and of h)
+    long long arow0;   // first A row (expert-ordered row of the tile's first row)
 };
 
 // Work items: the tiles that are not split, then the K ranges of the split
@@ -165,48 +170,53 @@ __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
     jb.arow0 = (long long)g.offsets[e] + m0;
     jb.n0 = nt * (NB == 2 ? 128 : 256);
     jb.split_j = tile - ts.nfull;
+    jb.mt = t0 + m0 / BM;
     return true;
 }
 
-// ---- global -> LDS load addressing -------------------------------------------
-// Load i of wave w fetches 16 rows of one stage (64 B each): lane l covers row
-// 16 i + (l >> 2) of its group and logical chunk (l & 3) ^ ((l >> 4) & 3), so
-// that the linear 1 KB LDS write lands each chunk at its swizzled place.  The
-// wave's LA loads cover A rows w * BM / NWAVE ..; its LB loads cover B-tile rows
-// w * 256 / NWAVE .. (gated: tile rows [0, 128) are W1 rows n0.., [128, 256) the
-// same W3 rows).  A rows past the tile's valid rows repeat its last row.
-//
-// fp8 weights (WF8): a B-tile row is 32 B (two chunks) per stage and a load
-// covers 32 rows: lane l writes physical chunk l & 1 of row l >> 1, chunk c of
-// row r being stored at c ^ ((r >> 3) & 1).
+// ---- tile images: global -> LDS load addressing ---------------------------------
+// The operands of this kernel are stored as tile images, the bytes of each
+// LDS ring stage in the order the DMA writes them, so that every load is one
+// contiguous, whole-line 1 KB read:
+//   A (xp, h): block (M tile mt, K stage s) at ((mt * KTT + s) * BM) * 64 B,
+//     BM rows of 64 B (32 bf16 of K);
+//   B (packed weights, per expert): block (n block nb of RB rows, stage s) at
+//     ((nb * KTT + s) * RB) * BROWB, RB rows of BROWB bytes; RB = 128 for the
+//     gated W1 and W3 (a tile takes the same 128 rows of each), else 256;
+//     BROWB = 64 (bf16) or 32 (fp8);
+// with KTT = K / 32.  Within a row, 16-byte chunk c of K sits at chunk
+// position c ^ ((r >> 2) & 3) for 64-B rows and c ^ ((r >> 3) & 1) for
+// 32-B rows (r: row in the block), the swizzle the fragment reads expect.
+// Load i of wave w covers A rows w * BM / NWAVE + 16 i .. +16 (lane l: 16 B
+// at l * 16) and B-tile rows w * 256 / NWAVE + BR i .. +BR, BR = 16 (bf16) or
+// 32 (fp8) (gated: tile rows [0, 128) are W1 rows n0.., [128, 256) the same
+// W3 rows).  An expert's last M tile also holds rows past its valid ones;
+// their products land in rows that are never stored.
 template <int BM, int NB, int NWAVE, int LA, int LB, int WF8>
 __device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, int w, int lane,
                                           const uint8_t *(&gsrc)[LA + LB], uint32_t (&ldst)[LA + LB]) {
     constexpr int ROWB = 64;
     constexpr int BROWB = WF8 ? 32 : 64;  // B bytes per row per stage
     constexpr int A_BYTES = BM * ROWB;
-    const long long lda_b = g.lda * 2, ldb_b = g.ldb * (WF8 ? 1 : 2);
-    const long long k0b = (long long)jb.ks * jb.KT * ROWB;  // first K byte of the range in an A row
-    const int lr = lane >> 2;
-    const int lch = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t *Ab = (const uint8_t *)g.A + jb.arow0 * lda_b + k0b;
+    constexpr int RB = (NB == 2) ? 128 : 256;
+    const long long KTT = g.K / 32;
+    const long long s0 = (long long)jb.ks * jb.KT;  // first stage of the K range
+    const uint8_t *Ab = (const uint8_t *)g.A + ((long long)jb.mt * KTT + s0) * A_BYTES + lane * 16;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int r = w * (BM / NWAVE) + 16 * i;
-        gsrc[i] = Ab + (long long)min(r + lr, jb.rows - 1) * lda_b + lch * 16;
+        gsrc[i] = Ab + (long long)r * ROWB;
         ldst[i] = r * ROWB;
     }
-    const uint8_t *Bsrc = (NB == 2 && w >= NWAVE / 2) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
-    const uint8_t *Bb = Bsrc + ((long long)jb.e * g.b_stride + (long long)jb.n0 * g.ldb) * (WF8 ? 1 : 2);
-    const long long k0bb = (long long)jb.ks * jb.KT * BROWB;  // first K byte of the range in a B row
-    constexpr int BR = WF8 ? 32 : 16;                         // B-tile rows per load
-    const int blr = WF8 ? (lane >> 1) : lr;
+    constexpr int BR = WF8 ? 32 : 16;  // B-tile rows per load
+    const long long esz = WF8 ? 1 : 2;
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
         const int t = w * (256 / NWAVE) + BR * i;  // first tile row of the load
-        const int r = (NB == 2) ? (t & 127) : t;   // row within the weight matrix, from n0
-        const int bch = WF8 ? ((lane & 1) ^ (((t + blr) >> 3) & 1)) : lch;
-        gsrc[LA + i] = Bb + (long long)(r + blr) * ldb_b + k0bb + bch * 16;
+        const int r = (NB == 2) ? (t & 127) : t;   // row within the n block
+        const uint8_t *Bsrc = (NB == 2 && t >= 128) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
+        gsrc[LA + i] = Bsrc + (long long)jb.e * g.b_stride * esz +
+                       ((long long)(jb.n0 / RB) * KTT + s0) * RB * BROWB + (long long)r * BROWB + lane * 16;
         ldst[LA + i] = A_BYTES + t * BROWB;
     }
 }
@@ -228,10 +238,11 @@ __device__ __forceinline__ int b_frag_row(int j, int wn) {
 //
 // bf16 outputs (h of both up modes; y of the down GEMM when c_bf16) go to
 // put(ml, lc, v0, v1, v2, v3): tile row ml, tile column lc (a multiple of 4),
-// four values.  The sink either stores them directly (8 bytes per lane: 32
-// rows per store instruction) or stages the tile in LDS for row-contiguous
-// stores (stage_put / store_staged).  fp32 y and the partials of split tiles
-// are stored directly.
+// four values.  The sink stages the tile in LDS (StagePut, then
+// store_staged: h as its tile image, y as whole rows) or, for y rows whose
+// N or ldc is not a multiple of 8, stores them directly (DirectPut: 8 bytes
+// per lane, 32 rows per store instruction).  fp32 y and the partials of
+// split tiles are stored directly.
 template <int MODE, int ACT, int IM, int JN, int WN, int WF8, typename Put>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
                                            int row0, int wn, int lane, Put &&put) {
@@ -327,9 +338,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
     }
 }
 
-// Direct bf16 sink: rows past the tile's valid rows are skipped; the down
-// GEMM's y columns past N are cut (ldc = N, possibly not a multiple of 4).
-template <int MODE>
+// Direct bf16 sink of the down GEMM's y rows (N or ldc not a multiple of 8):
+// rows past the tile's valid rows are skipped, columns past N cut.
 struct DirectPut {
     const GemmArgs &g;
     const TileJob &jb;
@@ -337,7 +347,7 @@ struct DirectPut {
         if (ml >= jb.rows) return;
         uint16_t *crow = (uint16_t *)g.C + (jb.arow0 + ml) * g.ldc;
         const int n = jb.n0 + lc;
-        if (MODE != MODE_DOWN || (((g.ldc & 3) == 0) && n + 3 < g.N)) {
+        if (((g.ldc & 3) == 0) && n + 3 < g.N) {
             *(uint2 *)(crow + n) = pack_bf16x4(v0, v1, v2, v3);
         } else {
             const float v[4] = {v0, v1, v2, v3};
@@ -363,29 +373,52 @@ struct StagePut {
     }
 };
 
-// Stores the staged tile: thread t copies chunk t mod CH of rows t / CH + k
-// (256 / CH), U rows' LDS reads in flight before their global stores; a wave
-// writes 1 KB of whole rows per store.  Only the valid rows, and for the
-// down GEMM the chunks below N (N a multiple of 8), are stored.
+// Stores the staged tile.  Up GEMMs: h goes out as the down GEMM's A tile
+// image, in which the tile's CW / 64 K stages of 64-B rows are one contiguous
+// region (all BM rows, including rows past the valid ones): thread t writes
+// 16-byte units t, t + 256, ..., unit u being chunk position u & 3 of row
+// (u >> 2) mod BM of stage block u / (4 BM).  Down GEMM: y rows; thread t
+// copies chunk t mod CH of rows t / CH + k (256 / CH), valid rows only and
+// the chunks below N (N a multiple of 8).  U LDS reads are in flight before
+// their global stores.
 template <int MODE, int BM, int CH, typename RowAddr>
 __device__ __forceinline__ void store_staged(const GemmArgs &g, const TileJob &jb, RowAddr row_addr) {
-    constexpr int RPP = 256 / CH;  // rows per pass of the workgroup
     constexpr int U = 8;
-    const int ch = threadIdx.x % CH;
-    const int rr = threadIdx.x / CH;
-    const bool colok = (MODE != MODE_DOWN) || (jb.n0 + ch * 8 < g.N);
-    uint16_t *cbase = (uint16_t *)g.C + jb.arow0 * g.ldc + jb.n0 + ch * 8;
-    for (int p0 = 0; p0 < jb.rows; p0 += RPP * U) {
-        u32x4_t v[U];
+    if constexpr (MODE != MODE_DOWN) {
+        constexpr int NU = BM * CH;  // 16-byte units of the tile
+        const long long KTT = g.ldc / 32;  // h: K of the down GEMM = ldc
+        uint8_t *base = (uint8_t *)g.C + ((long long)jb.mt * KTT + jb.n0 / 32) * BM * 64;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = min(p0 + u * RPP + rr, BM - 1);
-            v[u] = *(const MOE_LDS_AS u32x4_t *)(row_addr(r) + ((ch ^ (r & (CH - 1))) << 4));
+        for (int u0 = 0; u0 < NU; u0 += 256 * U) {
+            u32x4_t v[U];
+#pragma unroll
+            for (int q = 0; q < U; ++q) {
+                const int u = u0 + q * 256 + (int)threadIdx.x;
+                const int r = (u >> 2) % BM;
+                const int ch = (u / (4 * BM)) * 4 + ((u & 3) ^ ((r >> 2) & 3));  // column chunk in the tile
+                v[q] = *(const MOE_LDS_AS u32x4_t *)(row_addr(r) + ((ch ^ (r & (CH - 1))) << 4));
+            }
+#pragma unroll
+            for (int q = 0; q < U; ++q) *(u32x4_t *)(base + (long long)(u0 + q * 256 + threadIdx.x) * 16) = v[q];
         }
+    } else {
+        constexpr int RPP = 256 / CH;  // rows per pass of the workgroup
+        const int ch = threadIdx.x % CH;
+        const int rr = threadIdx.x / CH;
+        const bool colok = jb.n0 + ch * 8 < g.N;
+        uint16_t *cbase = (uint16_t *)g.C + jb.arow0 * g.ldc + jb.n0 + ch * 8;
+        for (int p0 = 0; p0 < jb.rows; p0 += RPP * U) {
+            u32x4_t v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = p0 + u * RPP + rr;
-            if (r < jb.rows && colok) *(u32x4_t *)(cbase + (long long)r * g.ldc) = v[u];
+            for (int u = 0; u < U; ++u) {
+                const int r = min(p0 + u * RPP + rr, BM - 1);
+                v[u] = *(const MOE_LDS_AS u32x4_t *)(row_addr(r) + ((ch ^ (r & (CH - 1))) << 4));
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int r = p0 + u * RPP + rr;
+                if (r < jb.rows && colok) *(u32x4_t *)(cbase + (long long)r * g.ldc) = v[u];
+            }
         }
     }
 }
@@ -488,7 +521,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     // load i of stage kt into ring slot J
     auto dma = [&](auto J_, int kt, int i) {
         const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
-        lds_dma16(gsrc[i] + (long long)kt * (i < LA ? ROWB : BROWB), __builtin_amdgcn_readfirstlane(l));
+        lds_dma16(gsrc[i] + (long long)kt * (i < LA ? A_BYTES : (NB == 2 ? 128 : 256) * BROWB),
+                  __builtin_amdgcn_readfirstlane(l));
     };
 
     // ---- fragment addressing (fragment row bases are multiples of 32, so
@@ -618,8 +652,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
     // bf16 outputs are staged in the (now idle) LDS ring, STAGE / CW rows per
-    // slot, and stored row-contiguously; the down GEMM stages when y is bf16,
-    // the tile not split and N, ldc multiples of 8 (whole 16-byte chunks).
+    // slot: h as its tile image; y rows when y is bf16, the tile not split and
+    // N, ldc multiples of 8 (whole 16-byte chunks).
     constexpr int CW = (MODE == MODE_GATED_UP ? 128 : 256) * 2;  // output bytes per tile row
     constexpr int CH = CW / 16;
     constexpr int RPS = STAGE / CW;
@@ -641,8 +675,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
                                                StagePut<CH, decltype(row_addr)>{row_addr});
         __syncthreads();
         store_staged<MODE, BM, CH>(g, jb, row_addr);
-    } else {
-        store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane, DirectPut<MODE>{g, jb});
+    } else if constexpr (MODE == MODE_DOWN) {
+        store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane, DirectPut{g, jb});
     }
 }
 
@@ -750,6 +784,38 @@ __global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
             }
         }
     }
+}
+
+// ============================================================================
+// Packed weights -> B tile image.  src: one expert's matrix, Npad rows of Kp
+// elements of esz bytes (row-major, as packed); dst: its tile image (RB-row
+// blocks, 32-wide K stages, chunk c of a row at c ^ swizzle(row)).  One
+// thread per 16-byte unit of the image, written in order.
+// ============================================================================
+__global__ __launch_bounds__(256) void retile_weights_kernel(const uint8_t *__restrict__ src,
+                                                             uint8_t *__restrict__ dst, int Npad, int Kp, int esz,
+                                                             int RB) {
+    const int upr = 2 * esz;  // 16-byte units per row per stage: 4 (bf16) or 2 (fp8)
+    const long long KTT = Kp / 32;
+    const long long total = (long long)Npad * Kp * esz / 16;
+    for (long long u = blockIdx.x * 256LL + threadIdx.x; u < total; u += (long long)gridDim.x * 256) {
+        const long long blk = u / ((long long)RB * upr);
+        const int within = (int)(u - blk * RB * upr);
+        const int r = within / upr, slot = within - (within / upr) * upr;
+        const long long nb = blk / KTT, st = blk - nb * KTT;
+        const int c = (upr == 4) ? (slot ^ ((r >> 2) & 3)) : (slot ^ ((r >> 3) & 1));
+        const uint8_t *sp = src + (nb * RB + r) * (long long)Kp * esz + st * 32 * esz + c * 16;
+        *(u32x4_t *)(dst + u * 16) = *(const u32x4_t *)sp;
+    }
+}
+
+hipError_t launch_retile_weights(const void *src, void *dst, int Npad, int Kp, int esz, int RB, hipStream_t s) {
+    if (Npad % RB != 0 || Kp % 32 != 0 || (esz != 1 && esz != 2)) return hipErrorInvalidValue;
+    const long long units = (long long)Npad * Kp * esz / 16;
+    const int blocks = (int)std::min<long long>((units + 255) / 256, 8192);
+    hipLaunchKernelGGL(retile_weights_kernel, dim3(blocks), dim3(256), 0, s, (const uint8_t *)src, (uint8_t *)dst,
+                       Npad, Kp, esz, RB);
+    return hipGetLastError();
 }
 
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s) {

@@ -203,6 +203,11 @@ struct PermuteArgs {
     float *gate_sorted;          // [T*kt]
     void *xp;                    // [rows][ld_xp]
     int copy_rows;               // 0: only the index arrays
+    // xp as the bf16 GEMM kernel's A tile image (tiled != 0): the row of
+    // expert e's rank rk is row (rk mod bm) of M tile tile_start[e] + rk / bm,
+    // ktt = 32-wide K stages per row
+    int tiled, bm, ktt;
+    const int *tile_start;       // [E+1]
 };
 
 // Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots; the
@@ -311,6 +316,9 @@ hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const Gem
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
 // after a MODE_DOWN launch with ksplit > 1: y of each split tile += its partials, in range order
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s);
+// one expert's packed weight matrix (Npad x Kp, esz-byte elements) -> the
+// bf16 kernel's B tile image (RB-row blocks: 128 for gated W1 / W3, else 256)
+hipError_t launch_retile_weights(const void *src, void *dst, int Npad, int Kp, int esz, int RB, hipStream_t s);
 // decode: routing fused into the gated up products of each selected slot, then
 // the down products and the slot-order combine (two kernels)
 hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s);

@@ -1139,23 +1139,35 @@ hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Store U chunks of 8 bf16 per lane into the row of every position the token
-// holds (pos of lane j: position of entry j, < 0 if dropped).  Chunk u of a
-// lane is column min(d0 + 512 u + 8 lane, D - 8), the column its value was
+// Element offset in xp of column col of row q: row-major (row stride ld_xp),
+// or, for the bf16 GEMM kernel (tiled), its place in the A tile image: row
+// q mod bm of M tile q / bm, K stage col / 32 of 64 B, 16-byte chunk
+// (col mod 32) / 8 at chunk position chunk ^ ((row >> 2) & 3).
+__device__ __forceinline__ long long xp_index(const PermuteArgs &a, long long q, int col) {
+    if (!a.tiled) return q * a.ld_xp + col;
+    const long long mt = q / a.bm;
+    const int lr = (int)(q - mt * a.bm);
+    const int chunk = ((col & 31) >> 3) ^ ((lr >> 2) & 3);
+    return ((mt * a.ktt + (col >> 5)) * a.bm + lr) * 32 + chunk * 8 + (col & 7);
+}
+
+// Store U chunks of 8 bf16 per lane into the xp row of every position the
+// token holds (row of lane j: xp row of entry j, < 0 if dropped).  Chunk u of
+// a lane is column min(d0 + 512 u + 8 lane, D - 8), the column its value was
 // loaded from: a lane past the row's end rewrites the last chunk with that
 // chunk's own value, so no store is conditional.
 template <int U>
-__device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int pos, int d0, int lane, const u32x4_t (&v)[U]) {
+__device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int row, int d0, int lane,
+                                                const u32x4_t (&v)[U]) {
     int cols[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) cols[u] = min(d0 + u * 512 + lane * 8, a.D - 8);
 #pragma nounroll
     for (int j = 0; j < a.kt; ++j) {
-        const int p = __shfl(pos, j);
-        if (p >= 0) {
-            uint16_t *__restrict__ dst = (uint16_t *)a.xp + (long long)p * a.ld_xp;
+        const int q = __shfl(row, j);
+        if (q >= 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) *(u32x4_t *)(dst + cols[u]) = v[u];
+            for (int u = 0; u < U; ++u) *(u32x4_t *)((uint16_t *)a.xp + xp_index(a, q, cols[u])) = v[u];
         }
     }
 }
@@ -1172,7 +1184,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
     if (t >= a.T) return;
     const int blk = t / kRouteBlock;
     const int cap = a.cap[0];
-    int e = 0, pos = -1;
+    int e = 0, pos = -1, row = -1;  // position in expert order; xp row (tile image row when tiled)
     float g = 0.0f;
     if (lane < a.kt) {
         const long long ent = (long long)t * a.kt + lane;
@@ -1182,6 +1194,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
             const int rk = a.rank_base[(long long)blk * a.E + (e - 1)] + a.rank[ent];
             if (rk < cap) {
                 pos = a.offsets[e - 1] + rk;
+                row = a.tiled ? a.tile_start[e - 1] * a.bm + rk : pos;
             } else {
                 e = 0;
                 g = 0.0f;
@@ -1217,7 +1230,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
             u32x4_t v[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) v[u] = *(const u32x4_t *)(src + min(d0 + u * 512 + lane * 8, a.D - 8));
-            store_row_chunk<U>(a, pos, d0, lane, v);
+            store_row_chunk<U>(a, row, d0, lane, v);
         }
         return;
     }
@@ -1235,21 +1248,21 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
                                   f32_to_bf16(f1.x) | ((uint32_t)f32_to_bf16(f1.y) << 16),
                                   f32_to_bf16(f1.z) | ((uint32_t)f32_to_bf16(f1.w) << 16)};
             }
-            store_row_chunk<U>(a, pos, d0, lane, v);
+            store_row_chunk<U>(a, row, d0, lane, v);
         }
         return;
     }
     for (int j = 0; j < a.kt; ++j) {
-        const int p = __shfl(pos, j);
+        const int p = __shfl(row, j);
         if (p < 0) continue;
         if (a.ct == CT_BF16) {
-            uint16_t *dst = (uint16_t *)a.xp + (long long)p * a.ld_xp;
+            uint16_t *dst = (uint16_t *)a.xp;
             if (a.x_bf16) {
                 const uint16_t *src = (const uint16_t *)a.x + (long long)t * a.D;
-                for (int d = lane; d < a.D; d += 64) dst[d] = src[d];
+                for (int d = lane; d < a.D; d += 64) dst[xp_index(a, p, d)] = src[d];
             } else {
                 const float *src = (const float *)a.x + (long long)t * a.D;
-                for (int d = lane; d < a.D; d += 64) dst[d] = f32_to_bf16(src[d]);
+                for (int d = lane; d < a.D; d += 64) dst[xp_index(a, p, d)] = f32_to_bf16(src[d]);
             }
         } else {
             float *dst = (float *)a.xp + (long long)p * a.ld_xp;
