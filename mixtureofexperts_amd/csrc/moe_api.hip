@@ -57,6 +57,7 @@ struct moe_handle {
     // workspace
     int T_max = 0, nblk_max = 0, rows_max = 0, max_tiles = 0;
     long long act_rows = 0;     // rows of xp and h (bf16 kernel: max_tiles * bm, tile images)
+    int ld_y = 0;               // row stride of y (elements)
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
@@ -600,7 +601,7 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     g.B0 = h->bf16_gemm ? h->w2t : h->w2; g.B1 = nullptr;
     g.b_stride = h->w2_stride; g.ldb = h->H_pad;
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
-    g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->Dout;
+    g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->ld_y;
     g.c_bf16 = (h->bf16_gemm && !y_f32) ? 1 : 0;  // the bf16-kernel paths keep y in bf16
     g.ksplit = ksplit; g.ncu = h->ncu; g.split_ws = h->split_ws;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
@@ -640,7 +641,7 @@ static int run_experts(moe_handle *h, int T, hipStream_t s) {
 
 static int run_combine(moe_handle *h, int T, float *out_dev, hipStream_t s) {
     CombineArgs c{};
-    c.y = h->y; c.ld_y = h->Dout; c.y_bf16 = h->bf16_gemm ? 1 : 0;
+    c.y = h->y; c.ld_y = h->ld_y; c.y_bf16 = h->bf16_gemm ? 1 : 0;
     c.idx = h->idx; c.pos_of = h->pos_of; c.gates = h->gates;
     c.T = T; c.D = h->Dout; c.kt = h->kc; c.lsh = h->lsh; c.out = out_dev;
     HIP_TRY(h, launch_combine(c, s));
@@ -825,7 +826,11 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->gate_sorted, sizeof(float) * T * kt);
     A(&h->xp, asz * (size_t)h->act_rows * h->D_pad);
     A(&h->hbuf, asz * (size_t)h->act_rows * h->H_pad);
-    A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->Dout);
+    // bf16 kernel: y rows padded by 128 B (bf16) past a multiple of 64
+    // elements, so that a tile's rows (a power-of-two stride apart otherwise)
+    // spread over the HBM channels
+    h->ld_y = h->bf16_gemm ? (int)round_up(h->Dout, 64) + 64 : h->Dout;
+    A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->ld_y);
     // tail split: fewer than ncu split tiles, each with at most kDownSplitMax - 1 partial blocks of BM x 256
     if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * kDownSplitMax);
     if (r != MOE_OK) return cleanup(r);
@@ -1279,7 +1284,9 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     }
     if (e == hipSuccess) e = launch_up(h, nt, s);
     if (e == hipSuccess) e = launch_down(h, nt, s, 1, true);
-    if (e == hipSuccess) e = hipMemcpyAsync(y, h->y, sizeof(float) * (size_t)n * h->Dout, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(y, sizeof(float) * h->Dout, h->y, sizeof(float) * (size_t)h->ld_y,
+                             sizeof(float) * h->Dout, n, hipMemcpyDeviceToHost, s);
     hipError_t e2 = hipStreamSynchronize(s);
     if (e == hipSuccess) e = e2;
     (void)hipFree(xs);
