@@ -595,6 +595,10 @@ static GemmArgs up_args(moe_handle *h, int mt_grid) {
 // and fold_split_kernel adds their partials to y in range order.
 static int down_ksplit(const moe_handle *h) { return h->bf16_gemm ? kDownSplitMax : 1; }
 
+// Workgroup slots of the bf16 down GEMM (the tail split plans its last
+// round over them): 128-row tiles run two workgroups per CU.
+static int down_slots(const moe_handle *h) { return h->bm == 128 ? 2 * h->ncu : h->ncu; }
+
 static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     GemmArgs g{};
     g.A = h->hbuf; g.lda = h->H_pad;
@@ -603,7 +607,7 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->ld_y;
     g.c_bf16 = (h->bf16_gemm && !y_f32) ? 1 : 0;  // the bf16-kernel paths keep y in bf16
-    g.ksplit = ksplit; g.ncu = h->ncu; g.split_ws = h->split_ws;
+    g.ksplit = ksplit; g.ncu = down_slots(h); g.split_ws = h->split_ws;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
@@ -789,8 +793,10 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
     h->rows_max = h->T_max * h->kt;
     h->bf16_gemm = h->ct == CT_BF16 && (h->wt == WT_BF16 || h->wt == WT_FP8);
-    // 256-row tiles when experts average at least 384 rows at max_tokens, else 128
-    h->bm = (h->bf16_gemm && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
+    // 256-row tiles for a few large experts (at most 16, averaging at least 384
+    // rows at max_tokens); 128-row tiles, two workgroups per CU, for many or
+    // small ones (fine-grained MoE layers: skewed counts, short K)
+    h->bm = (h->bf16_gemm && h->E <= 16 && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
     h->max_tiles = h->rows_max / h->bm + h->E + 1;
     // bf16 kernel: xp and h are A tile images of up to max_tiles M tiles
     h->act_rows = h->bf16_gemm ? (long long)h->max_tiles * h->bm : h->rows_max;
@@ -831,8 +837,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     // spread over the HBM channels
     h->ld_y = h->bf16_gemm ? (int)round_up(h->Dout, 64) + 64 : h->Dout;
     A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->ld_y);
-    // tail split: fewer than ncu split tiles, each with at most kDownSplitMax - 1 partial blocks of BM x 256
-    if (h->bf16_gemm) A((void **)&h->split_ws, sizeof(float) * (size_t)h->ncu * h->bm * 256 * kDownSplitMax);
+    // tail split: fewer split tiles than down-GEMM slots, each with up to kDownSplitMax partial blocks of BM x 256
+    if (h->bf16_gemm)
+        A((void **)&h->split_ws, sizeof(float) * (size_t)down_slots(h) * h->bm * 256 * kDownSplitMax);
     if (r != MOE_OK) return cleanup(r);
     // Pads of the packed weights and of the activation rows must read as 0.
     hipError_t ze = hipSuccess;

@@ -483,9 +483,9 @@ using ic = std::integral_constant<int, N>;
 // ============================================================================
 // 4-wave interleaved kernel, BM = 128 or 256.
 // ============================================================================
-// OCC: workgroups per CU.  The up GEMM of 128-row tiles (small experts,
-// weight-bandwidth bound) runs two per CU on a shorter ring, so one
-// workgroup's prologue and epilogue overlap the other's main loop.
+// OCC: workgroups per CU.  128-row tiles (small experts, weight-bandwidth
+// bound, or short K) run two per CU on a shorter ring, so one workgroup's
+// prologue and epilogue overlap the other's main loop.
 template <int MODE, int BM, int ACT, int WF8, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void grouped_gemm_bf16_kernel(
     GemmArgs g) {
@@ -829,9 +829,9 @@ static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
     // 8 XCDs x (slots for the whole tiles + slots for the split items)
     const long long tiles = (long long)g.m_tiles_grid * g.n_tiles;
     const long long total = 8 * ((tiles + 7) / 8 + (g.ksplit > 1 ? (g.ncu + 7) / 8 : 0));
-    // two per CU for the up GEMM of 128-row tiles; the down GEMM's tail split
-    // sizes its last round for one workgroup per CU
-    constexpr int OCC = (BM == 128 && MODE != MODE_DOWN) ? 2 : 1;
+    // 128-row tiles run two workgroups per CU (the down GEMM's tail split then
+    // plans its last round over g.ncu = 2 slots per CU)
+    constexpr int OCC = (BM == 128) ? 2 : 1;
     hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8, OCC>), dim3((unsigned)total), dim3(256), 0, s, g);
     return hipGetLastError();
 }
