@@ -210,7 +210,8 @@ struct PermuteArgs {
     const int *tile_start;       // [E+1]
 };
 
-// Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots; the
+// Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots (one
+// per CU for 256-row tiles, two for 128-row tiles); the
 // rem = W mod ncu tiles of the last, partial round are each split into S K
 // ranges (the largest S <= smax with S dividing the K stages and rem * S <=
 // ncu), so that round is as long as 1/S of a tile.  Tiles are numbered
@@ -248,8 +249,8 @@ struct CombineArgs {
 };
 
 struct GemmArgs {
-    const void *A; long long lda;        // activations [rows][lda] (elements)
-    const void *B0; const void *B1;      // packed weights [E][Npad][ldb]
+    const void *A; long long lda;        // activations [rows][lda] (elements); bf16 kernel: A tile image
+    const void *B0; const void *B1;      // packed weights [E][Npad][ldb]; bf16 kernel: B tile images
     long long b_stride;                  // elements per expert
     long long ldb;                       // = padded K
     const float *s0; const float *s1;    // per-output-channel scales [E][Npad] or null
@@ -257,13 +258,14 @@ struct GemmArgs {
     long long s_stride;                  // = Npad
     int N;                               // real N (store bound)
     int K;                               // padded K (multiple of the tile K)
-    void *C; long long ldc;              // output [rows][ldc]
+    void *C; long long ldc;              // output [rows][ldc]; bf16 up GEMMs: h as the down GEMM's A
+                                         // tile image (ldc = its K)
     const int2 *tiles; const int *num_tiles; const int *counts; const int *offsets;
     const int *tile_start;               // [E+1] (bf16 kernel work list)
     int E;
     int m_tiles_grid; int n_tiles;
     int ksplit;                          // bf16 kernel: the most K ranges a tail tile may be split into (tail_split)
-    int ncu;                             // workgroup slots of one round (compute units)
+    int ncu;                             // workgroup slots of one round (CUs x workgroups per CU)
     float *split_ws;                     // partials of split tiles (MODE_DOWN, ksplit > 1)
     int act;
     int c_bf16;                          // MODE_DOWN: y in bf16 (else fp32)
