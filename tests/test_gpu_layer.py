@@ -362,6 +362,24 @@ def test_mixtral_shape_scaled(moe, oracle):
     check_case(c, TOL["bf16"])
 
 
+@pytest.mark.parametrize("E,k,etype,act,wdtype", [
+    (4, 1, "gated", "silu", "bf16"),
+    (4, 1, "gated", "silu", "fp8"),
+    (4, 1, "standard", "gelu", "bf16"),
+    (4, 1, "standard", "gelu", "fp8"),
+    (8, 2, "gated", "silu", "bf16"),
+])
+def test_256_row_tiles(moe, oracle, E, k, etype, act, wdtype):
+    # at most 16 experts averaging >= 384 rows: the 256-row tile kernels (one
+    # workgroup per CU); a skewed router bias gives partial last tiles, and
+    # D = 320 leaves y rows past the last 256-column block (cut at N)
+    rng = np.random.default_rng(70 + E)
+    bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
+    c = Case(moe, oracle, T=1600, D=320, H=384, E=E, k=k, gate="switch" if k == 1 else "topk", expert_type=etype,
+             act=act, wdtype=wdtype, xdtype="bf16", seed=70 + E, router_bias=bias)
+    check_case(c, TOL[wdtype])
+
+
 def test_standard_experts_gelu(moe, oracle):
     # C5 structure at reduced size: StandardExpert + gelu + biases, SwitchGating
     for wd in ("f32", "bf16"):
