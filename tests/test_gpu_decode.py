@@ -157,3 +157,19 @@ def test_decode_shared_experts(moe, oracle, lsh, k, wdtype):
         from mixtureofexperts_amd.layer import moe_ffn_forward  # noqa: F401
     finally:
         c.dev.close()
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "fp8"])
+def test_decode_between_forwards_leaves_forward_unchanged(moe, oracle, wdtype):
+    # the decode caller uses the layer's h workspace as fp32 scratch; the
+    # forward call (h as the GEMM's tile image) must come out bit-identical
+    # before and after it, on a batch with several tiles per expert
+    c = Case(moe, oracle, T=600, D=256, H=688, E=8, k=2, wdtype=wdtype, xdtype="bf16", seed=44)
+    try:
+        print(f"forward / decode / forward w={wdtype}", flush=True)
+        out1, loss1, _ = c.run(training=True)
+        c.dev.decode(np.ascontiguousarray(c.x[:8]))
+        out2, loss2, _ = c.run(training=True)
+        assert np.array_equal(out1.view(np.uint32), out2.view(np.uint32)) and loss1 == loss2
+    finally:
+        c.dev.close()
