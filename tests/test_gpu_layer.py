@@ -500,3 +500,28 @@ def test_async_device_path_matches_host(moe, oracle):
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     assert float(loss.item()) == ref_loss
+
+
+def test_random_layer_shapes(moe, oracle):
+    # seeded shapes across the paths the bf16 kernel takes: D / Dout not
+    # multiples of 8 (direct y stores) or of 256 (cut columns), 2..40
+    # experts, top-1..4, gated / standard, bf16 / fp8, batches that give
+    # 128- and 256-row tiles, partial tiles and tail-split down tiles
+    rng = np.random.default_rng(2026)
+    for case in range(10):
+        E = int(rng.integers(2, 41))
+        k = int(rng.integers(1, min(4, E) + 1))
+        D = int(rng.choice([64, 96, 200, 256, 320, 512]))
+        Dout = int(rng.choice([D, 72, 136, 264]))
+        H = int(rng.choice([96, 200, 384, 688]))
+        T = int(rng.integers(16, 700))
+        etype = "gated" if rng.random() < 0.7 else "standard"
+        act = "silu" if etype == "gated" else str(rng.choice(["gelu", "relu"]))
+        wdtype = str(rng.choice(["bf16", "fp8"]))
+        bias = (rng.standard_normal(E) * float(rng.choice([0.0, 1.0]))).astype(np.float32)
+        c = Case(moe, oracle, T=T, D=D, H=H, Dout=Dout, E=E, k=k, gate="switch" if k == 1 else "topk",
+                 expert_type=etype, act=act, wdtype=wdtype, xdtype="bf16", seed=900 + case, router_bias=bias)
+        try:
+            check_case(c, TOL[wdtype])
+        finally:
+            c.dev.close()
