@@ -189,6 +189,41 @@ def test_capacity_matches_loop(oracle):
         assert dropped == nd
 
 
+def test_capacity_keeps_the_head_of_each_stable_segment(oracle):
+    # An independent characterisation of apply_capacity_constraint: bucket the
+    # uncapped routing (stable: tokens ascending inside each expert); the
+    # entries kept are exactly the first min(count_e, cap) of expert e's
+    # segment, every other entry becomes (0, 0), and each token's surviving
+    # gates are its original gates over their slot-order sum.
+    rng = np.random.default_rng(9)
+    for _ in range(40):
+        T, E = int(rng.integers(1, 120)), int(rng.integers(2, 12))
+        k = int(rng.integers(1, min(E, 4) + 1))
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        lg[:, int(rng.integers(0, E))] += 1.5
+        idx, g, _ = oracle.compute_gates_topk(lg, k)
+        cf = float(rng.choice([0.25, 0.5, 1.0, 1.25, 2.0]))
+        i2, g2, dropped = oracle.capacity(idx, g, E, cf)
+        cap = math.ceil(np.float32(np.float32(cf) * np.float32(T)) / np.float32(E))
+        counts, offsets, perm = oracle.bucket(idx, E)
+        keep = np.zeros(T * k, bool)
+        for e in range(E):
+            seg = perm[offsets[e]:offsets[e + 1]]
+            keep[seg[:cap]] = True
+        kept = keep.reshape(T, k)
+        assert np.array_equal(i2 != 0, kept)
+        assert np.array_equal(i2[kept], idx[kept])
+        assert np.all(g2[~kept] == 0)
+        assert dropped == int((~kept).sum())
+        for t in range(T):
+            s = np.float32(0)
+            for j in range(k):
+                if kept[t, j]:
+                    s = np.float32(s + g[t, j])
+            if s > 0:
+                assert np.array_equal(g2[t, kept[t]], (g[t, kept[t]] / s).astype(np.float32))
+
+
 # ---- losses / stats ---------------------------------------------------------
 
 def test_switch_loss_closed_forms(oracle):
@@ -292,6 +327,101 @@ def test_combine_order_is_ascending_expert(oracle):
     oracle._lib().oracle_combine(yp.ctypes.data, perm.ctypes.data, 3, gates.ctypes.data, 3, 1, 1,
                                  out.ctypes.data)
     assert out[0, 0] == np.float32(np.float32(1e8 + -1e8) + 1.0)  # (e1 + e2) + e3 = 1
+
+
+# ---- activations and StandardExpert -------------------------------------------
+
+def test_gelu_is_the_tanh_form_of_the_erf_gelu(oracle):
+    # Mathematics of GELU, independent of the oracle's formula:
+    #  * odd part: gelu(x) - gelu(-x) = x for both the erf GELU and its tanh
+    #    approximation (x Phi(x) + x Phi(-x) = x), so a wrong 0.5 or a wrong
+    #    sign of the odd argument fails;
+    #  * gelu(0) = 0 and gelu'(0) = 1/2;
+    #  * closeness to the exact 0.5 x (1 + erf(x / sqrt 2)) (stdlib math.erf):
+    #    the tanh form with sqrt(2/pi) and 0.044715 deviates from it by at most
+    #    4.73e-4, reached near |x| = 2.70; the erf form itself (deviation 0)
+    #    and a wrong constant (the deviation moves) both fail the window.
+    x = np.linspace(-8, 8, 160001).astype(np.float32)
+    g = oracle.act_gelu(x)
+    assert g.dtype == np.float32
+    odd = g.astype(np.float64) - oracle.act_gelu(-x).astype(np.float64) - x.astype(np.float64)
+    assert np.max(np.abs(odd) / np.maximum(np.abs(x), 1.0)) < 4e-7
+    assert oracle.act_gelu(np.float32(0.0)) == 0.0
+    h = np.float32(1e-3)
+    assert abs((float(oracle.act_gelu(h)) - float(oracle.act_gelu(-h))) / (2 * float(h)) - 0.5) < 1e-3
+    exact = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in x.astype(np.float64)])
+    dev = np.abs(g.astype(np.float64) - exact)
+    assert 4.6e-4 < dev.max() < 4.9e-4
+    assert 2.6 < abs(float(x[dev.argmax()])) < 2.8
+    # far tails: x for large positive x, 0 for large negative x
+    assert oracle.act_gelu(np.float32(8.0)) == np.float32(8.0)
+    assert abs(float(oracle.act_gelu(np.float32(-8.0)))) < 1e-10
+
+
+def test_relu_and_identity_closed_forms(oracle):
+    x = np.array([-np.inf, -3.5, -1e-30, -0.0, 0.0, 1e-30, 2.25, np.inf], np.float32)
+    r = oracle.act_relu(x)
+    assert r.tolist() == [0.0, 0.0, 0.0, 0.0, 0.0, np.float32(1e-30), 2.25, np.inf]
+    assert np.array_equal(oracle.act_identity(x), x)
+    # silu(x) = x sigmoid(x): silu(0) = 0, silu(x) - silu(-x) = x, silu(x) -> x
+    s = oracle.act_silu(np.linspace(-30, 30, 601).astype(np.float32)).astype(np.float64)
+    xs = np.linspace(-30, 30, 601)
+    assert s[300] == 0.0
+    assert np.max(np.abs(s - s[::-1] - xs) / np.maximum(np.abs(xs), 1.0)) < 4e-7
+    assert abs(s[-1] - 30.0) < 1e-10
+
+
+def test_standard_expert_with_permutation_weights(oracle):
+    # W1 and W2 as scaled permutation matrices (not symmetric, so a transposed
+    # weight fails): the expert is an index gather, computed here with no
+    # matrix product: y[o] = s2 act(s1 x[p1[p2[o]]] + b1[p2[o]]) + b2[o].
+    # relu with biases that flip signs catches b1 applied after the
+    # activation; s2 != 1 catches b2 added before W2.
+    rng = np.random.default_rng(31)
+    n = 12
+    p1, p2 = rng.permutation(n), rng.permutation(n)
+    s1, s2 = np.float32(0.5), np.float32(-2.0)
+    w1 = np.zeros((n, n), np.float32)
+    w1[np.arange(n), p1] = s1      # (W1 x)[i] = s1 x[p1[i]]
+    w2 = np.zeros((n, n), np.float32)
+    w2[np.arange(n), p2] = s2      # (W2 h)[o] = s2 h[p2[o]]
+    b1 = rng.standard_normal(n).astype(np.float32)
+    b2 = rng.standard_normal(n).astype(np.float32)
+    x = rng.standard_normal((5, n)).astype(np.float32)
+    for name in ("relu", "gelu", "silu", "identity"):
+        act = oracle.ACTS[name]
+        y = oracle.standard_expert(x, w1, w2, b1, b2, act)
+        hid = act((s1 * x[:, p1] + b1).astype(np.float32))
+        expect = (s2 * hid[:, p2] + b2).astype(np.float32)
+        assert np.array_equal(y, expect), name
+    # zero biases (the reference's init, standard.jl:30-31) and missing biases agree
+    y0 = oracle.standard_expert(x, w1, w2, np.zeros(n, np.float32), np.zeros(n, np.float32), oracle.act_relu)
+    assert np.array_equal(y0, oracle.standard_expert(x, w1, w2, None, None, oracle.act_relu))
+
+
+def test_standard_moe_forward_matches_float64_loops(oracle):
+    # forward_standard with StandardExperts (GELU) against a float64 per-token
+    # restatement of the slot loop: W2 act(W1 x + b1) + b2 with the erf-free
+    # tanh GELU written from its definition 0.5 v (1 + tanh(sqrt(2/pi)(v +
+    # 0.044715 v^3))) in float64
+    rng = np.random.default_rng(32)
+    T, D, H, Dout, E = 30, 24, 40, 20, 5
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    wr = (rng.standard_normal((E, D)) * 0.3).astype(np.float32)
+    ex = [dict(w1=(rng.standard_normal((H, D)) * 0.2).astype(np.float32),
+               w2=(rng.standard_normal((Dout, H)) * 0.2).astype(np.float32),
+               b1=(rng.standard_normal(H) * 0.5).astype(np.float32),
+               b2=(rng.standard_normal(Dout) * 0.5).astype(np.float32)) for _ in range(E)]
+    for gate, k in (("switch", 1), ("topk", 2)):
+        out, _, aux = oracle.moe_forward(x, wr, ex, gate=gate, k=k, expert_type="standard", act="gelu")
+        ref = np.zeros((T, Dout))
+        for t in range(T):
+            for j in range(aux["idx"].shape[1]):
+                w = ex[aux["idx"][t, j] - 1]
+                v = w["w1"].astype(np.float64) @ x[t].astype(np.float64) + w["b1"]
+                hid = 0.5 * v * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (v + 0.044715 * v ** 3)))
+                ref[t] += float(aux["gates"][t, j]) * (w["w2"].astype(np.float64) @ hid + w["b2"])
+        assert np.max(np.abs(out - ref)) / np.max(np.abs(ref)) < 1e-5, gate
 
 
 # ---- forward_with_shared_experts (num_shared_experts > 0) ----------------------
