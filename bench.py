@@ -37,9 +37,9 @@ CONFIGS = {
     "readme": dict(T=32, D=512, H=2048, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="f32",
                    workload="readme-moe-layer"),
     # the decode caller (moe_ffn_forward!) of a stories42M-shaped
-    # Llama2 with layers 2, 4, 6 converted to 8 gated experts, top-2, fp32; a step
-    # is one token through the three MoE FFNs (the caller's attention and norms
-    # are not part of this path)
+    # Llama2 with layers 2, 4, 6 converted (convert_to_moe, :perturb, noise
+    # 0.01) to 8 gated experts, top-2, fp32; a step is one token through the
+    # three MoE FFNs (the caller's attention and norms are not part of this path)
     "stories42m-decode": dict(T=1, D=512, H=1376, E=8, k=2, gate="topk", ns=0, etype="gated", act="silu", w="f32",
                               layers=3, workload="stories42m-moe-decode"),
 }
@@ -144,10 +144,26 @@ def cpu_baseline(cfg, wl, sample_tokens):
         oracle.moe_forward(x, wr, ex, router_bias=rb, **kwargs)
         times.append(time.perf_counter() - t0)
     t = sorted(times)[1]
-    return {"value": S / t, "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": f"first {S} of {cfg['T']} tokens of the same workload, full layer forward (router GEMM, "
-                      f"gating, per-expert OpenBLAS sgemm FFN on fp32-dequantised weights, combine, losses); "
-                      f"median of 3 runs, {t:.2f} s each"}
+    res = {"value": S / t, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+           "sample": f"first {S} of {cfg['T']} tokens of the same workload, full layer forward (router GEMM, "
+                     f"gating, per-expert OpenBLAS sgemm FFN on fp32-dequantised weights, combine, losses); "
+                     f"median of 3 runs, {t:.2f} s each",
+           "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    # the same restatement on one host thread, over a smaller bounded sample
+    # (about 1/8 of the all-thread sample's tokens), one run
+    try:
+        from threadpoolctl import threadpool_limits
+
+        S1 = max(1, S // 8)
+        with threadpool_limits(limits=1):
+            t0 = time.perf_counter()
+            oracle.moe_forward(x[:S1], wr, ex, router_bias=rb, **kwargs)
+            t1 = time.perf_counter() - t0
+        res["single_thread"] = {"value": S1 / t1, "unit": "tokens/s", "cores": 1,
+                                "sample": f"first {S1} tokens, one run of {t1:.2f} s"}
+    except ImportError:
+        pass
+    return res
 
 
 def up_kernel_name(cfg):
@@ -188,21 +204,27 @@ def bench_decode(args, cfg):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4321)
     layers, host = [], []
-    for _ in range(NL):
+    for li in range(NL):
         dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_GATED, input_dim=D, hidden_dim=H, output_dim=D,
                           activation=_lib.MOE_ACT_SILU, gate=GateSpec(_lib.MOE_GATE_TOPK, k, 0),
                           weight_dtype=_lib.MOE_F32, balance_alpha=0.01, z_loss_weight=0.001, capacity_factor=1.25,
                           drop_tokens=False, max_tokens=1)
-        wr = torch.randn(E, D, generator=gen, device="cuda") * (1.0 / D ** 0.5)
+        # create_router_weights: randn(dim, E) .* sqrt(2f0 / dim)
+        wr = torch.randn(E, D, generator=gen, device="cuda") * (2.0 / D) ** 0.5
         wr_mem = wr.t().contiguous()
         _lib.check(_lib.lib().moe_set_router(dev.h, wr_mem.data_ptr(), None), dev.h)
+        # the layer's dense Llama FFN (Llama (in, out) layout = memory [out][in])
+        dense = [(torch.randn(*shp, generator=gen, device="cuda") * 0.02).contiguous()
+                 for shp in [(H, D), (D, H), (H, D)]]
+        _lib.check(_lib.lib().moe_init_experts_from_dense(
+            dev.h, _lib.MOE_LAYOUT_LLAMA_IN_OUT, _lib.MOE_F32, dense[0].data_ptr(), dense[1].data_ptr(),
+            dense[2].data_ptr(), None, None, None, _lib.MOE_INIT_PERTURB, 0.01, 1000 + li), dev.h)
         ex = []
         for e in range(E):
-            w1, w2, w3 = [(torch.randn(*shp, generator=gen, device="cuda") * (2.0 / shp[1]) ** 0.5).contiguous()
-                          for shp in [(H, D), (D, H), (H, D)]]
-            _lib.check(_lib.lib().moe_set_expert(dev.h, e, _lib.MOE_LAYOUT_FLUX_OUT_IN, _lib.MOE_F32, w1.data_ptr(),
-                                                 w2.data_ptr(), w3.data_ptr(), None, None, None, None, None), dev.h)
-            ex.append(dict(w1=w1, w2=w2, w3=w3))
+            w = [np.zeros(shp, np.float32) for shp in [(H, D), (D, H), (H, D)]]
+            _lib.check(_lib.lib().moe_get_expert(dev.h, e, _lib.MOE_LAYOUT_LLAMA_IN_OUT, w[0].ctypes.data,
+                                                 w[1].ctypes.data, w[2].ctypes.data, None, None, None), dev.h)
+            ex.append(dict(w1=w[0], w2=w[1], w3=w[2]))
         torch.cuda.synchronize()
         layers.append(dev)
         host.append((wr, ex))
@@ -236,7 +258,8 @@ def bench_decode(args, cfg):
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": cfg["workload"], "tokens_per_step": 1, "moe_layers": NL, "d_model": D,
-                   "d_expert_hidden": H, "experts": E, "top_k": k, "weights": "f32"},
+                   "d_expert_hidden": H, "experts": E, "top_k": k, "weights": "f32",
+                   "expert_init": "convert_to_moe :perturb 0.01"},
         "roofline": {"bound": "hbm", "kernel": "moe_decode (routing + gated-expert matrix-vector products)",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
@@ -245,7 +268,7 @@ def bench_decode(args, cfg):
     if not args.no_cpu_baseline:
         from oracle import moe_oracle as oracle
 
-        hl = [(wr.cpu().numpy(), [{n: v.cpu().numpy() for n, v in e.items()} for e in ex]) for wr, ex in host]
+        hl = [(wr.cpu().numpy(), ex) for wr, ex in host]
         x = bufs[0].cpu().numpy()[None, :]
         n_tok = 0
         t0 = time.perf_counter()

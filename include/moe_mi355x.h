@@ -31,7 +31,7 @@ extern "C" {
 #endif
 
 #define MOE_ABI_VERSION 1
-#define MOE_MAX_TOPK 8        /* maximum slots per token (shared + routed) */
+#define MOE_MAX_TOPK 8        /* maximum slots per token of the top-k gates (shared + routed) */
 #define MOE_MAX_EXPERTS 128   /* maximum experts seen by one router */
 
 typedef enum {
@@ -67,8 +67,9 @@ typedef enum { MOE_ACT_GELU = 0, MOE_ACT_SILU = 1, MOE_ACT_RELU = 2, MOE_ACT_IDE
  *   capacity = ceil(T * cf / E) tokens of largest logit (ties to the lower
  *   token), gate = its softmax probability; a token's slots hold the experts
  *   that took it in ascending id order, at most capacity of them
- *   (expert_choice.jl:11-53).  Slots per token: min(E, 8); a call whose
- *   min(capacity, E) exceeds 8 is MOE_EUNSUPPORTED. */
+ *   (expert_choice.jl:11-53).  Slots per token (moe_slots_per_token):
+ *   min(E, capacity at max_tokens); a call fills the first min(capacity, E)
+ *   of them (the rest, like the reference's rows past them, are empty). */
 typedef enum {
     MOE_GATE_TOPK = 0,
     MOE_GATE_SWITCH = 1,

@@ -21,14 +21,20 @@ HIP_FLAGS = [
     "-std=c++17",
     f"--offload-arch={ARCH}",
     "-fPIC",
-    "-shared",
-    # packed fp32 VALU ops stay off (compiler-generated v_pk_*_f32 are avoided)
-    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # IEEE fp32 division / sqrt in device code (routing must be bit-exact)
-    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-fast-math",
     "-Wall",
     "-Wno-unused-function",
+]
+# Device pass only: packed fp32 VALU ops stay off (no compiler-generated
+# v_pk_*_f32).  clang cannot forward -Xclang through -Xarch_device, so each
+# source is compiled in two steps: the device code alone (with this feature)
+# into an offload bundle, then the host code, which embeds that bundle.  A
+# fixed -cuid per source keeps the two steps' compilation-unit ids equal,
+# which makes the result byte-identical to a one-step hipcc compile.
+DEVICE_ONLY_FLAGS = [
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # IEEE fp32 division / sqrt in device code (routing must be bit-exact)
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
 ]
 
 
@@ -48,13 +54,22 @@ def build_library(verbose: bool = False) -> str:
     import tempfile
 
     incs = ["-I", os.path.join(REPO_DIR, "include"), "-I", CSRC]
-    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+
+    def compile_one(src, tmpdir):
+        stem = os.path.splitext(src)[0]
+        path = os.path.join(CSRC, src)
+        bundle = os.path.join(tmpdir, stem + ".hipfb")
+        obj = os.path.join(tmpdir, stem + ".o")
+        cuid = f"-cuid=moe_{stem}"
+        _run([HIPCC, *HIP_FLAGS, *DEVICE_ONLY_FLAGS, *incs, cuid, "--cuda-device-only", "-c", path, "-o", bundle],
+             verbose)
+        _run([HIPCC, *HIP_FLAGS, *incs, cuid, "--cuda-host-only", "-Xclang", "-fcuda-include-gpubinary", "-Xclang",
+              bundle, "-c", path, "-o", obj], verbose)
+        return obj
+
     with tempfile.TemporaryDirectory(prefix="moe_build_") as tmpdir:
-        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-        cmds = [[HIPCC, *compile_flags, *incs, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
-        with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
-            for f in [pool.submit(_run, c, verbose) for c in cmds]:
-                f.result()
+        with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+            objs = [f.result() for f in [pool.submit(compile_one, s, tmpdir) for s in SOURCES]]
         tmp = LIB_PATH + ".tmp"
         _run([HIPCC, f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)

@@ -37,6 +37,12 @@ struct moe_handle {
     bool gated = true;
     int device = 0;
     hipStream_t stream = nullptr;
+    // Calls on one handle share its workspace and weights.  `done` is
+    // recorded after the work of every call that enqueues; a call on a stream
+    // other than the last one's first makes its stream wait for it.
+    hipEvent_t done = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool pending = false;
     std::mutex mu;
     std::string err;
 
@@ -55,7 +61,11 @@ struct moe_handle {
     long long w1_stride = 0, w2_stride = 0;  // elements per expert
 
     // workspace
+    // rows_max: expert-ordered positions (rows of xp, h, y); ent_max: entries
+    // (t * kt + slot) of the per-slot arrays.  Equal except for
+    // ExpertChoiceGating, whose positions are at most E * min(capacity, T).
     int T_max = 0, nblk_max = 0, rows_max = 0, max_tiles = 0;
+    long long ent_max = 0;
     long long act_rows = 0;     // rows of xp and h (bf16 kernel: max_tiles * bm, tile images)
     int ld_y = 0;               // row stride of y (elements)
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
@@ -119,6 +129,35 @@ static void free_all(moe_handle *h) {
     h->allocs.clear();
 }
 
+// Stream order between calls on one handle (see moe_handle::done): before a
+// call enqueues on s, s waits for the previous call's work when that went to
+// another stream.
+static int join_stream(moe_handle *h, hipStream_t s) {
+    if (h->pending && h->last_stream != s) {
+        const hipError_t e = hipStreamWaitEvent(s, h->done, 0);
+        if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipStreamWaitEvent: ") + hipGetErrorString(e));
+    }
+    return MOE_OK;
+}
+// After a call has enqueued its work on s (and not waited for it).
+static int mark_stream(moe_handle *h, hipStream_t s) {
+    const hipError_t e = hipEventRecord(h->done, s);
+    if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
+    h->last_stream = s;
+    h->pending = true;
+    return MOE_OK;
+}
+// After a call that joined and then synchronised its stream: nothing of the
+// handle is in flight.
+static void settle(moe_handle *h) { h->pending = false; }
+
+// ExpertChoiceGating capacity ceil(Int, T * capacity_factor / E) in Float32
+// (src/gating/expert_choice.jl:13), saturated at INT_MAX.
+static long long expert_choice_capacity(int T, float cf, int E) {
+    const float c = ceilf(((float)T * cf) / (float)E);
+    return (c >= 2147483647.0f) ? INT_MAX : (long long)c;
+}
+
 static int validate_config(const moe_config *c, std::string &why) {
     if (c->num_experts < 1 || c->num_experts > MOE_MAX_EXPERTS) { why = "num_experts out of range [1,128]"; return 0; }
     if (c->input_dim < 1 || c->hidden_dim < 1 || c->output_dim < 1) { why = "dimensions must be positive"; return 0; }
@@ -153,7 +192,8 @@ static int validate_config(const moe_config *c, std::string &why) {
         return 0;
     }
     const int slots = (c->gate_kind == MOE_GATE_EXPERT_CHOICE)
-                          ? std::min(c->num_experts, MOE_MAX_TOPK)
+                          ? (int)std::min<long long>(
+                                c->num_experts, expert_choice_capacity(c->max_tokens, c->gate_param, c->num_experts))
                           : k + lsh + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0);
     const long long rows = (long long)c->max_tokens * slots;
     if (rows > INT_MAX / 2) { why = "max_tokens * slots too large"; return 0; }
@@ -546,16 +586,16 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         ra.bias = h->aux_bias;
         ra.out_mask = ROUTE_OUT_GATING;
     } else if (ec) {
-        // softmax pass, the experts' choices, then a gating pass on them
+        // softmax pass; the experts' choices give the slots, the stable ranks
+        // and the per-block histogram
         ra.out_mask = ROUTE_OUT_PROBS;
         HIP_TRY(h, launch_route(ra, s));
-        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates, s));
-        ra.given = 1;
-        ra.out_mask = ROUTE_OUT_GATING;
+        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
+                                        h->rank, h->blk_counts, s));
     } else {
         ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
     }
-    HIP_TRY(h, launch_route(ra, s));
+    if (!ec) HIP_TRY(h, launch_route(ra, s));
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
     sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kc;
@@ -616,12 +656,12 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
 }
 
 // The expert up GEMM (W1/W3 or W1 + activation) and the down GEMM (W2) over
-// mt_grid M tiles: the LDS-DMA bf16 kernel for bf16 weights, the
-// register-staged kernel for fp32 and fp8 weights.
+// mt_grid M tiles: the LDS-DMA kernel for bf16 and fp8 weights (bf16
+// activations), the register-staged fp32 kernel for fp32 weights.
 static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
     const int mode = h->gated ? MODE_GATED_UP : MODE_STD_UP;
     if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, h->wt == WT_FP8, up_args(h, mt_grid), s);
-    return launch_grouped_gemm(mode, h->ct, h->wt, h->ct == CT_BF16 ? 1 : 0, up_args(h, mt_grid), s);
+    return launch_grouped_gemm_f32(mode, up_args(h, mt_grid), s);
 }
 
 // y_f32: write y in fp32 also on the bf16-kernel path (moe_expert_forward
@@ -633,7 +673,7 @@ static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksp
         if (e == hipSuccess && ksplit > 1) e = launch_fold_split(h->bm, g, s);
         return e;
     }
-    return launch_grouped_gemm(MODE_DOWN, h->ct, h->wt, 0, down_args(h, mt_grid, 1, true), s);
+    return launch_grouped_gemm_f32(MODE_DOWN, down_args(h, mt_grid, 1, true), s);
 }
 
 static int run_experts(moe_handle *h, int T, hipStream_t s) {
@@ -661,11 +701,10 @@ static int begin_call(moe_handle *h, int T) {
     h->kc = h->kt;
     h->kl = h->kt - h->lsh;
     if (h->cfg.gate_kind == MOE_GATE_EXPERT_CHOICE) {
-        const float c = ceilf(((float)T * h->cfg.gate_param) / (float)h->E);
-        const long long C = (c >= 2147483647.0f) ? INT_MAX : (long long)c;
-        if (std::min<long long>(C, h->E) > MOE_MAX_TOPK)
-            return fail(h, MOE_EUNSUPPORTED, "ExpertChoiceGating: min(capacity, num_experts) above MOE_MAX_TOPK (8)");
-        h->kl = (int)C;
+        // the call's min(capacity, E) <= kt = min(capacity at max_tokens, E)
+        // slots are filled, the rest stay empty; the Switch loss counts all
+        // capacity rows of the reference's (capacity, T) index matrix
+        h->kl = (int)expert_choice_capacity(T, h->cfg.gate_param, h->E);
     }
     return MOE_OK;
 }
@@ -734,7 +773,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->Dout = cfg->output_dim;
     h->k = (cfg->gate_kind == MOE_GATE_SWITCH || cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) ? 1 : cfg->top_k;
     h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
-    h->kt = (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) ? std::min(h->E, MOE_MAX_TOPK) : h->lsh + h->ns + h->k;
+    h->kt = (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE)
+                ? (int)std::min<long long>(h->E, expert_choice_capacity(cfg->max_tokens, cfg->gate_param, h->E))
+                : h->lsh + h->ns + h->k;
     h->kc = h->kt;
     h->kl = h->kt - h->lsh;
     h->D_pad = (int)round_up(h->D, kKPad);
@@ -755,12 +796,19 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     auto cleanup = [&](int code) {
         g_create_error = h->err;
         free_all(h);
+        if (h->done) (void)hipEventDestroy(h->done);
         if (h->stream) (void)hipStreamDestroy(h->stream);
         delete h;
         return code;
     };
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         h->err = "hipStreamCreate failed";
+        return cleanup(MOE_EHIP);
+    }
+    // ordering between streams of this device only: no system-scope fence
+    // (a cache write-back each time it is recorded)
+    if (hipEventCreateWithFlags(&h->done, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess) {
+        h->err = "hipEventCreate failed";
         return cleanup(MOE_EHIP);
     }
     int r = MOE_OK;
@@ -791,7 +839,14 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     }
     h->T_max = cfg->max_tokens;
     h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
+    h->ent_max = (long long)h->T_max * h->kt;
     h->rows_max = h->T_max * h->kt;
+    if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) {
+        // each expert takes at most min(capacity, T) tokens
+        const long long cmax = std::min<long long>(
+            expert_choice_capacity(h->T_max, cfg->gate_param, h->E), h->T_max);
+        h->rows_max = (int)std::min<long long>(h->rows_max, (long long)h->E * cmax);
+    }
     h->bf16_gemm = h->ct == CT_BF16 && (h->wt == WT_BF16 || h->wt == WT_FP8);
     // 256-row tiles for a few large experts (at most 16, averaging at least 384
     // rows at max_tokens); 128-row tiles, two workgroups per CU, for many or
@@ -805,13 +860,13 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
         if (h->gated) A(&h->w3t, wsz * (size_t)h->E * h->w1_stride);
         A(&h->w2t, wsz * (size_t)h->E * h->w2_stride);
     }
-    const size_t T = (size_t)h->T_max, kt = (size_t)h->kt, E = (size_t)h->E;
+    const size_t T = (size_t)h->T_max, E = (size_t)h->E, nent = (size_t)h->ent_max;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
     A((void **)&h->logits_part, sizeof(float) * kRouterMaxSlices * T * h->Er);
     A((void **)&h->probs, sizeof(float) * T * h->Er);
-    A((void **)&h->idx, sizeof(int) * T * kt);
-    A((void **)&h->gates, sizeof(float) * T * kt);
-    A((void **)&h->rank, sizeof(int) * T * kt);
+    A((void **)&h->idx, sizeof(int) * nent);
+    A((void **)&h->gates, sizeof(float) * nent);
+    A((void **)&h->rank, sizeof(int) * nent);
     A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * E);
     A((void **)&h->blk_stats, sizeof(double) * (size_t)h->nblk_max * (E + 2));
     A((void **)&h->counts, sizeof(int) * E);
@@ -827,9 +882,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
     A((void **)&h->aux_mom, sizeof(float) * h->Er);
-    A((void **)&h->perm, sizeof(int) * T * kt);
-    A((void **)&h->pos_of, sizeof(int) * T * kt);
-    A((void **)&h->gate_sorted, sizeof(float) * T * kt);
+    A((void **)&h->perm, sizeof(int) * nent);
+    A((void **)&h->pos_of, sizeof(int) * nent);
+    A((void **)&h->gate_sorted, sizeof(float) * (size_t)h->rows_max);
     A(&h->xp, asz * (size_t)h->act_rows * h->D_pad);
     A(&h->hbuf, asz * (size_t)h->act_rows * h->H_pad);
     // bf16 kernel: y rows padded by 128 B (bf16) past a multiple of 64
@@ -876,8 +931,10 @@ int moe_destroy(moe_handle *h) {
     if (!h) return MOE_OK;
     {
         std::lock_guard<std::mutex> lk(h->mu);
+        if (h->pending) (void)hipEventSynchronize(h->done);
         if (h->stream) (void)hipStreamSynchronize(h->stream);
         free_all(h);
+        if (h->done) (void)hipEventDestroy(h->done);
         if (h->stream) (void)hipStreamDestroy(h->stream);
         h->stream = nullptr;
     }
@@ -894,6 +951,8 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     // device sources may still be in flight on another stream (this handle's
     // stream does not order with the caller's): wait for the whole device
     if (dev_w || dev_b) HIP_TRY(h, hipDeviceSynchronize());
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
     // memory [D][Er] -> [D][Er_pad]
     HIP_TRY(h, hipMemcpy2DAsync(h->wr, sizeof(float) * h->Er_pad, weight, sizeof(float) * h->Er,
                                 sizeof(float) * h->Er, h->D, dev_w ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
@@ -903,6 +962,7 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
                                   h->stream));
     HIP_TRY(h, launch_router_split(h->wr, h->D, h->Er, h->Er_pad, h->Ep16, h->Dp32, h->wsplit, h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
+    settle(h);
     h->has_bias = bias != nullptr;
     h->router_set = true;
     return MOE_OK;
@@ -947,12 +1007,14 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
             if (p && is_device_ptr(p)) any_dev = true;
         if (any_dev) HIP_TRY(h, hipDeviceSynchronize());
     }
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
     const size_t wsz = (h->wt == WT_F32) ? 4 : (h->wt == WT_BF16 ? 2 : 1);
     uint8_t *w1d = (uint8_t *)h->w1 + wsz * (size_t)expert * h->w1_stride;
     uint8_t *w2d = (uint8_t *)h->w2 + wsz * (size_t)expert * h->w2_stride;
     float *s1d = h->s1 ? h->s1 + (size_t)expert * h->H_pad : nullptr;
     float *s2d = h->s2 ? h->s2 + (size_t)expert * h->Dout_npad : nullptr;
-    int r = pack_matrix(h, layout, src_dtype, w1, s1, h->H, h->D, h->D_pad, w1d, s1d);
+    r = pack_matrix(h, layout, src_dtype, w1, s1, h->H, h->D, h->D_pad, w1d, s1d);
     if (r != MOE_OK) return r;
     if (h->gated) {
         uint8_t *w3d = (uint8_t *)h->w3 + wsz * (size_t)expert * h->w1_stride;
@@ -964,6 +1026,7 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
     if (r != MOE_OK) return r;
     HIP_TRY(h, retile_expert(h, expert));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
+    settle(h);
     if (!h->gated) {
         if (b1)
             HIP_TRY(h, hipMemcpy(h->b1 + (size_t)expert * h->H_pad, b1, sizeof(float) * h->H,
@@ -997,13 +1060,14 @@ int moe_init_experts_from_dense(moe_handle *h, int32_t layout, int32_t src_dtype
             if (p && is_device_ptr(p)) any_dev = true;
         if (any_dev) HIP_TRY(h, hipDeviceSynchronize());
     }
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
     // the three dense matrices as fp32 rows: w1 / w3 (H, D), w2 (Dout, H)
     const int Ns[3] = {h->H, h->Dout, h->H}, Ks[3] = {h->D, h->H, h->D}, Kp[3] = {h->D_pad, h->H_pad, h->D_pad};
     const void *ws[3] = {w1, w2, w3};
     const float *ss[3] = {s1, s2, s3};
     float *dense[3] = {nullptr, nullptr, nullptr};
     float *tmp = nullptr;
-    int r = MOE_OK;
     size_t most = 0;
     for (int m = 0; m < 3; ++m) {
         most = std::max(most, (size_t)Ns[m] * Ks[m]);
@@ -1036,6 +1100,7 @@ int moe_init_experts_from_dense(moe_handle *h, int32_t layout, int32_t src_dtype
         if (e == hipSuccess) h->expert_set[x] = 1;
     }
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+    if (e == hipSuccess) settle(h);
     for (float *d : dense)
         if (d) (void)hipFree(d);
     if (tmp) (void)hipFree(tmp);
@@ -1056,6 +1121,8 @@ int moe_get_expert(moe_handle *h, int32_t expert, int32_t layout, void *w1, void
     void *outs[3] = {w1, w2, h->gated ? w3 : nullptr};
     float *souts[3] = {s1, s2, h->gated ? s3 : nullptr};
     const size_t most = (size_t)std::max((size_t)h->H * h->D, (size_t)h->Dout * h->H) * esz;
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
     uint8_t *tmp = nullptr;
     HIP_TRY(h, hipMalloc(&tmp, most));
     hipError_t e = hipSuccess;
@@ -1082,6 +1149,8 @@ int moe_get_expert(moe_handle *h, int32_t expert, int32_t layout, void *w1, void
     }
     (void)hipFree(tmp);
     if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("expert readback failed: ") + hipGetErrorString(e));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    settle(h);
     return MOE_OK;
 }
 
@@ -1099,12 +1168,15 @@ int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const flo
     if (update_freq < 1) return fail(h, MOE_EINVAL, "update_freq must be >= 1");
     if (update_counter < 0) return fail(h, MOE_EINVAL, "update_counter must be >= 0");
     hipStream_t s = h->stream;
+    int r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     const size_t bytes = sizeof(float) * h->Er;
     if (bias) HIP_TRY(h, hipMemcpyAsync(h->aux_bias, bias, bytes, hipMemcpyHostToDevice, s));
     else HIP_TRY(h, hipMemsetAsync(h->aux_bias, 0, bytes, s));
     if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(h->aux_mom, bias_momentum, bytes, hipMemcpyHostToDevice, s));
     else HIP_TRY(h, hipMemsetAsync(h->aux_mom, 0, bytes, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
     h->aux_free = true;
     h->aux_lr = learning_rate;
     h->aux_momentum = momentum;
@@ -1119,10 +1191,13 @@ int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
     std::lock_guard<std::mutex> lk(h->mu);
     hipStream_t s = h->stream;
+    int r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     const size_t bytes = sizeof(float) * h->Er;
     if (bias) HIP_TRY(h, hipMemcpyAsync(bias, h->aux_bias, bytes, hipMemcpyDeviceToHost, s));
     if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(bias_momentum, h->aux_mom, bytes, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
     if (update_counter) *update_counter = h->aux_counter;
     return MOE_OK;
 }
@@ -1146,6 +1221,8 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     h->last_T = -1;  // routing state no longer matches a forward call
     int r = begin_call(h, T);
     if (r != MOE_OK) return r;
+    r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     HIP_TRY(h, hipMemcpyAsync(h->logits_part, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
     r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
     if (r != MOE_OK) return r;
@@ -1157,6 +1234,7 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     if (offsets) HIP_TRY(h, hipMemcpyAsync(offsets, h->offsets, sizeof(int) * (h->E + 1), hipMemcpyDeviceToHost, s));
     if (perm) HIP_TRY(h, hipMemcpyAsync(perm, h->perm, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
     return MOE_OK;
 }
 
@@ -1197,6 +1275,8 @@ int moe_forward_routed(moe_handle *h, const void *x, int32_t x_dtype, int32_t T,
     h->kc = kd;
     h->kl = kd;
     hipStream_t s = h->stream;
+    int jr = join_stream(h, s);
+    if (jr != MOE_OK) return jr;
     if (T > 0) {
         HIP_TRY(h, hipMemcpyAsync(h->idx, indices, sizeof(int) * (size_t)T * kd, hipMemcpyHostToDevice, s));
         HIP_TRY(h, hipMemcpyAsync(h->gates, gates, sizeof(float) * (size_t)T * kd, hipMemcpyHostToDevice, s));
@@ -1230,6 +1310,8 @@ static int forward_host_locked(moe_handle *h, const void *x, int32_t x_dtype, in
     int r = ensure_io_buffers(h);
     if (r != MOE_OK) return r;
     hipStream_t s = h->stream;
+    r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     const size_t xbytes = (x_dtype == MOE_BF16 ? 2 : 4) * (size_t)T * h->D;
     HIP_TRY(h, hipMemcpyAsync(h->x_dev, x, xbytes, hipMemcpyHostToDevice, s));
     r = forward_locked(h, h->x_dev, x_dtype, T, training, h->out_dev, nullptr, s);
@@ -1248,6 +1330,7 @@ static int forward_host_locked(moe_handle *h, const void *x, int32_t x_dtype, in
         if (aux->perm) HIP_TRY(h, hipMemcpyAsync(aux->perm, h->perm, sizeof(int) * nk, hipMemcpyDeviceToHost, s));
     }
     HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
     if (loss) *loss = sc[2];
     if (aux) {
         if (aux->switch_loss) *aux->switch_loss = sc[0];
@@ -1266,6 +1349,8 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     if (n == 0) return MOE_OK;
     if (!x || !y) return fail(h, MOE_EINVAL, "null buffer");
     hipStream_t s = h->stream;
+    int r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     // single segment: counts[expert] = n, all others 0
     std::vector<int> cnt(h->E, 0), off(h->E + 1, 0);
     cnt[expert] = n;
@@ -1296,6 +1381,7 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
                              sizeof(float) * h->Dout, n, hipMemcpyDeviceToHost, s);
     hipError_t e2 = hipStreamSynchronize(s);
     if (e == hipSuccess) e = e2;
+    if (e == hipSuccess) settle(h);
     (void)hipFree(xs);
     h->last_T = -1;  // routing state no longer matches a forward call
     if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("expert forward failed: ") + hipGetErrorString(e));
@@ -1307,6 +1393,11 @@ static int decode_check(moe_handle *h, int n) {
     int r = check_ready(h);
     if (r != MOE_OK) return r;
     if (!h->gated) return fail(h, MOE_EUNSUPPORTED, "decode path: gated experts only (gated_expert_forward!)");
+    // gated_expert_forward! applies silu inline whatever the layer's config says
+    // (src/llama2/inference.jl:160); a layer configured with another activation
+    // would compute something else through layer(x) than through this path
+    if (h->cfg.activation != MOE_ACT_SILU)
+        return fail(h, MOE_EUNSUPPORTED, "decode path: silu experts only (gated_expert_forward! applies silu)");
     if (h->cfg.gate_kind != MOE_GATE_TOPK && h->cfg.gate_kind != MOE_GATE_SWITCH)
         return fail(h, MOE_EUNSUPPORTED, "decode path: TopKGating or SwitchGating only");
     if ((h->D & 3) != 0) return fail(h, MOE_EUNSUPPORTED, "decode path: input_dim must be a multiple of 4");
@@ -1341,6 +1432,8 @@ int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *log
     r = ensure_io_buffers(h);
     if (r != MOE_OK) return r;
     hipStream_t s = h->stream;
+    r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     HIP_TRY(h, hipMemcpyAsync(h->x_dev, xb, sizeof(float) * (size_t)n * h->D, hipMemcpyHostToDevice, s));
     r = decode_locked(h, (const float *)h->x_dev, n, h->out_dev, s);
     if (r != MOE_OK) return r;
@@ -1349,6 +1442,7 @@ int moe_decode(moe_handle *h, const float *xb, int32_t n, float *out, float *log
     if (indices) HIP_TRY(h, hipMemcpyAsync(indices, h->idx, sizeof(int) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
     if (gates) HIP_TRY(h, hipMemcpyAsync(gates, h->gates, sizeof(float) * (size_t)n * h->kt, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
     return MOE_OK;
 }
 
@@ -1359,7 +1453,11 @@ int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_d
     if (r != MOE_OK) return r;
     if (!xb_dev || !out_dev) return fail(h, MOE_EINVAL, "null buffer");
     if ((uintptr_t)xb_dev & 15) return fail(h, MOE_EINVAL, "xb_dev must be 16-byte aligned");
-    return decode_locked(h, xb_dev, n, out_dev, stream ? (hipStream_t)stream : h->stream);
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    r = join_stream(h, s);
+    if (r == MOE_OK) r = decode_locked(h, xb_dev, n, out_dev, s);
+    if (r == MOE_OK) r = mark_stream(h, s);
+    return r;
 }
 
 int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, int32_t training, float *out_dev,
@@ -1367,7 +1465,10 @@ int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
     std::lock_guard<std::mutex> lk(h->mu);
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    return forward_locked(h, x_dev, x_dtype, T, training, out_dev, loss_dev, s);
+    int r = join_stream(h, s);
+    if (r == MOE_OK) r = forward_locked(h, x_dev, x_dtype, T, training, out_dev, loss_dev, s);
+    if (r == MOE_OK) r = mark_stream(h, s);
+    return r;
 }
 
 static int stage_check(moe_handle *h, int T) {
@@ -1383,7 +1484,10 @@ int moe_stage_router_async(moe_handle *h, const void *x_dev, int32_t x_dtype, in
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     h->last_training = training;
-    return run_routing(h, x_dev, x_dtype == MOE_BF16, T, training, true, PERMUTE_NONE, nullptr, s);
+    r = join_stream(h, s);
+    if (r == MOE_OK) r = run_routing(h, x_dev, x_dtype == MOE_BF16, T, training, true, PERMUTE_NONE, nullptr, s);
+    if (r == MOE_OK) r = mark_stream(h, s);
+    return r;
 }
 
 int moe_stage_permute_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t T, void *stream) {
@@ -1392,7 +1496,10 @@ int moe_stage_permute_async(moe_handle *h, const void *x_dev, int32_t x_dtype, i
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    return run_permute(h, x_dev, x_dtype == MOE_BF16, T, h->last_training, PERMUTE_ROWS, s);
+    r = join_stream(h, s);
+    if (r == MOE_OK) r = run_permute(h, x_dev, x_dtype == MOE_BF16, T, h->last_training, PERMUTE_ROWS, s);
+    if (r == MOE_OK) r = mark_stream(h, s);
+    return r;
 }
 
 int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream) {
@@ -1401,8 +1508,10 @@ int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream) {
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     HIP_TRY(h, launch_up(h, m_tiles_for(h, T), s));
-    return MOE_OK;
+    return mark_stream(h, s);
 }
 
 int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream) {
@@ -1411,8 +1520,10 @@ int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream) {
     int r = stage_check(h, T);
     if (r != MOE_OK) return r;
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    r = join_stream(h, s);
+    if (r != MOE_OK) return r;
     HIP_TRY(h, launch_down(h, m_tiles_for(h, T), s, down_ksplit(h)));
-    return MOE_OK;
+    return mark_stream(h, s);
 }
 
 int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stream) {
@@ -1422,7 +1533,10 @@ int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stre
     if (r != MOE_OK) return r;
     if (!out_dev) return fail(h, MOE_EINVAL, "null out");
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
-    return run_combine(h, T, out_dev, s);
+    r = join_stream(h, s);
+    if (r == MOE_OK) r = run_combine(h, T, out_dev, s);
+    if (r == MOE_OK) r = mark_stream(h, s);
+    return r;
 }
 
 int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *probs, int32_t E, float alpha,
@@ -1489,8 +1603,11 @@ int moe_aux_free_update_bias(const int32_t *indices, int64_t n, int32_t E, float
 int moe_read_counts(moe_handle *h, int32_t *counts) {
     if (!h || !counts) return fail(h, MOE_EINVAL, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
+    HIP_TRY(h, hipMemcpyAsync(counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
-    HIP_TRY(h, hipMemcpy(counts, h->counts, sizeof(int) * h->E, hipMemcpyDeviceToHost));
+    settle(h);
     return MOE_OK;
 }
 

@@ -103,15 +103,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // global_load_lds_dwordx4: lane l copies 16 bytes from its own global address
-// to LDS byte lds + 16 l (lds is wave-uniform, passed in M0).  Issued as
-// inline assembly that the compiler does not see as a memory access: its wait
-// insertion would otherwise treat every later LDS read as possibly reading
-// these bytes and wait for all loads in flight.  Correct ordering is kept by
-// the kernels themselves: each slot is refilled only after a barrier that
-// follows its last reads, and read only after a barrier that follows
-// wait_vmcnt for its loads (volatile asm statements keep their relative order).
+// to LDS byte lds + 16 l (lds is wave-uniform, passed in M0: an input operand
+// bound to M0, so the compiler itself writes M0 before the load and knows it
+// is used).  Issued as inline assembly that the compiler does not see as a
+// memory access: its wait insertion would otherwise treat every later LDS
+// read as possibly reading these bytes and wait for all loads in flight.
+// Correct ordering is kept by the kernels themselves: each slot is refilled
+// only after a barrier that follows its last reads, and read only after a
+// barrier that follows wait_vmcnt for its loads (volatile asm statements keep
+// their relative order).
 __device__ __forceinline__ void lds_dma16(const uint8_t *gaddr, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds) : "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds));
 }
 
 // ---- work item -> tile --------------------------------------------------------

@@ -301,9 +301,11 @@ void router_plan(RouterArgs &r);
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
 // ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
-// gates [T][kt] (kt >= min(C, E))
+// gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
+// bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
+// expert's entries in its route block) and blk_counts [nblk][E]
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, hipStream_t s);
+                                int *idx, float *gates, int *rank, int *blk_counts, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,
@@ -312,8 +314,8 @@ hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *o
 // update_bias!(AuxiliaryFreeLoss, indices) on given indices [n] (entries > 0 counted)
 hipError_t launch_aux_free_update(const int *idx, long long n, int E, float lr, float momentum, float *bias,
                                   float *mom, hipStream_t s);
-hipError_t launch_grouped_gemm(int mode, int ct, int wt, int out_bf16, const GemmArgs &g,
-                               hipStream_t s);
+// fp32 activations x fp32 weights (the reference-precision path)
+hipError_t launch_grouped_gemm_f32(int mode, const GemmArgs &g, hipStream_t s);
 // bf16 activations x bf16 weights; bm = 128 or 256 rows per tile (the scan's bm)
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s);
 // after a MODE_DOWN launch with ksplit > 1: y of each split tile += its partials, in range order

@@ -723,25 +723,28 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     __syncthreads();
 
     // ---- stable rank of each entry among the block's entries of its expert ----
-    // (entries in token-then-slot order, as the bucket loop visits them)
-    const int nent = kRouteBlock * a.kt;
-    if (tok) {
-#pragma unroll
-        for (int j = 0; j < MOE_MAX_TOPK; ++j)
-            if (j < a.kt) ent_e[tid * a.kt + j] = ex[j];
-    }
-    __syncthreads();
+    // (entries in token-then-slot order, as the bucket loop visits them; a
+    // gating pass only: kt <= MOE_MAX_TOPK there)
     int my_e = 0, my_r = 0;
-    if (tid < nent) {
-        my_e = ent_e[tid];
-        if (my_e > 0) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (tid >> 5)], 1u << (tid & 31));
-    }
-    __syncthreads();
-    if (tid < nent && my_e > 0) {
-        const unsigned *m = &emask[(my_e - 1) * MOE_MAX_TOPK];
-        int rr = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
-        for (int w = 0; w < (tid >> 5); ++w) rr += __popc(m[w]);
-        my_r = rr;
+    if (out_gating) {
+        const int nent = kRouteBlock * a.kt;
+        if (tok) {
+#pragma unroll
+            for (int j = 0; j < MOE_MAX_TOPK; ++j)
+                if (j < a.kt) ent_e[tid * a.kt + j] = ex[j];
+        }
+        __syncthreads();
+        if (tid < nent) {
+            my_e = ent_e[tid];
+            if (my_e > 0) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (tid >> 5)], 1u << (tid & 31));
+        }
+        __syncthreads();
+        if (tid < nent && my_e > 0) {
+            const unsigned *m = &emask[(my_e - 1) * MOE_MAX_TOPK];
+            int rr = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
+            for (int w = 0; w < (tid >> 5); ++w) rr += __popc(m[w]);
+            my_r = rr;
+        }
     }
     if (tok) {
         red[0][tid] = zterm;
@@ -805,14 +808,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
+    // three rows of route_rw(E) floats per token: 50.7 KB at E = MOE_MAX_EXPERTS,
+    // within the 64 KB of dynamic LDS a launch gets without an attribute
     const size_t lds = (size_t)kRouteBlock * sizeof(float) * route_rw(std::max(a.Er, a.E)) * 3;
-    static bool big_lds = false;  // dynamic LDS above 64 KB must be allowed explicitly (once per process)
-    if (lds > 65536 && !big_lds) {
-        const hipError_t e = hipFuncSetAttribute((const void *)route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 96 * 1024);
-        if (e != hipSuccess) return e;
-        big_lds = true;
-    }
+    if (lds > 65536) return hipErrorInvalidValue;
     hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), lds, s, a);
     return hipGetLastError();
 }
@@ -877,41 +876,65 @@ __global__ __launch_bounds__(256) void expert_choice_select_kernel(const float *
 // id order, at most kcap = min(C, E) of them (a later expert past the
 // capacity rows is left out, expert_choice.jl:40-50), gate = probability of
 // the expert for the token; the remaining slots of the kt are empty (id 0).
-__global__ __launch_bounds__(256) void expert_choice_assemble_kernel(const uint8_t *__restrict__ sel,
+// sel[t][e] becomes the slot + 1 of entry (t, e) (<= kcap <= 128), or 0 when
+// expert e did not take token t or the entry was left out.
+__global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__restrict__ sel,
                                                                      const float *__restrict__ probs, int T, int E,
                                                                      int kt, int kcap, int *idx, float *gates) {
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (t >= T) return;
-    int ids[MOE_MAX_TOPK];
-    float gs[MOE_MAX_TOPK];
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_TOPK; ++j) { ids[j] = 0; gs[j] = 0.0f; }
     int c = 0;
     for (int e = 0; e < E; ++e) {
-        if (sel[(long long)t * E + e]) {
-#pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j == c && c < kcap) {
-                    ids[j] = e + 1;
-                    gs[j] = probs[(long long)t * E + e];
-                }
+        const long long o = (long long)t * E + e;
+        if (sel[o]) {
+            if (c < kcap) {
+                idx[(long long)t * kt + c] = e + 1;
+                gates[(long long)t * kt + c] = probs[o];
+                sel[o] = (uint8_t)(c + 1);
+            } else {
+                sel[o] = 0;
+            }
             ++c;
         }
     }
-#pragma unroll
-    for (int j = 0; j < MOE_MAX_TOPK; ++j)
-        if (j < kt) {
-            idx[(long long)t * kt + j] = ids[j];
-            gates[(long long)t * kt + j] = gs[j];
+    for (int j = min(c, kcap); j < kt; ++j) {
+        idx[(long long)t * kt + j] = 0;
+        gates[(long long)t * kt + j] = 0.0f;
+    }
+}
+
+// The bucketing inputs of the kept entries, per route block of kRouteBlock
+// tokens: thread e walks the block's tokens in order; a token holds expert e
+// in at most one slot, so the entry's rank among expert e's entries of the
+// block (token-then-slot order, the bucket loop's) is the count of earlier
+// tokens that hold e.
+__global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
+                                                                            int E, int kt, int *rank,
+                                                                            int *blk_counts) {
+    const int e = threadIdx.x;
+    if (e >= E) return;
+    const int t0 = blockIdx.x * kRouteBlock;
+    const int ntok = min(kRouteBlock, T - t0);
+    int c = 0;
+    for (int i = 0; i < ntok; ++i) {
+        const int sl = sel[(long long)(t0 + i) * E + e];
+        if (sl) {
+            rank[(long long)(t0 + i) * kt + sl - 1] = c;
+            ++c;
         }
+    }
+    blk_counts[(long long)blockIdx.x * E + e] = c;
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, hipStream_t s) {
+                                int *idx, float *gates, int *rank, int *blk_counts, hipStream_t s) {
     if (T <= 0) return hipSuccess;
+    if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
                        min(C, E), idx, gates);
+    hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + kRouteBlock - 1) / kRouteBlock), dim3(MOE_MAX_EXPERTS),
+                       0, s, sel, T, E, kt, rank, blk_counts);
     return hipGetLastError();
 }
 
@@ -1282,9 +1305,82 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
     }
 }
 
+// Permute for more slots per token than a wave has lanes (ExpertChoiceGating
+// with min(capacity, E) > 64; kt <= MOE_MAX_EXPERTS): lane l owns entries l
+// and l + 64; same finalisation as permute_kernel, then one row copy per kept
+// entry, element by element (most of these slots are empty).
+__global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int blk = t / kRouteBlock;
+    const int cap = a.cap[0];
+    int ee[2], pos[2], row[2];
+    float g[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int j = lane + 64 * c;
+        ee[c] = 0; pos[c] = -1; row[c] = -1; g[c] = 0.0f;
+        if (j < a.kt) {
+            const long long ent = (long long)t * a.kt + j;
+            ee[c] = a.idx[ent];
+            g[c] = a.gates[ent];
+            if (ee[c] > 0 && ee[c] <= a.E) {
+                const int rk = a.rank_base[(long long)blk * a.E + (ee[c] - 1)] + a.rank[ent];
+                if (rk < cap) {
+                    pos[c] = a.offsets[ee[c] - 1] + rk;
+                    row[c] = a.tiled ? a.tile_start[ee[c] - 1] * a.bm + rk : pos[c];
+                } else {
+                    ee[c] = 0;
+                    g[c] = 0.0f;
+                }
+            }
+        }
+    }
+    if (a.renorm) {
+        // gate_sum over the slots in slot order; divide when > 0
+        float sum = __shfl(g[0], 0);
+        for (int j = 1; j < a.kt; ++j) sum = sum + __shfl(g[j >> 6], j & 63);
+        if (sum > 0.0f) {
+            g[0] = g[0] / sum;
+            g[1] = g[1] / sum;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int j = lane + 64 * c;
+        if (j < a.kt) {
+            const long long ent = (long long)t * a.kt + j;
+            if (a.renorm) {
+                a.idx[ent] = ee[c];
+                a.gates[ent] = g[c];
+            }
+            a.pos_of[ent] = pos[c];
+            if (pos[c] >= 0) {
+                a.perm[pos[c]] = (int)ent;
+                a.gate_sorted[pos[c]] = g[c];
+            }
+        }
+    }
+    if (!a.copy_rows) return;
+    for (int j = 0; j < a.kt; ++j) {
+        const int p = __shfl(row[j >> 6], j & 63);
+        if (p < 0) continue;
+        for (int d = lane; d < a.D; d += 64) {
+            const float v = a.x_bf16 ? bf16_to_f32(((const uint16_t *)a.x)[(long long)t * a.D + d])
+                                     : ((const float *)a.x)[(long long)t * a.D + d];
+            if (a.ct == CT_BF16) ((uint16_t *)a.xp)[xp_index(a, p, d)] = f32_to_bf16(v);
+            else ((float *)a.xp)[(long long)p * a.ld_xp + d] = v;
+        }
+    }
+}
+
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(permute_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
+    if (a.kt > 2 * 64) return hipErrorInvalidValue;
+    if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(permute_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1404,6 +1500,25 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
+    if (a.kt > MOE_MAX_TOPK) {
+        // more slots than a token's sort network holds: ExpertChoiceGating,
+        // whose slots list the token's experts in ascending id order (empty
+        // and dropped slots have no position), so slot order is expert order
+        float *o = a.out + (long long)t * a.D;
+        for (int d = lane; d < a.D; d += 64) {
+            float acc = 0.0f;
+            for (int j = 0; j < a.kt; ++j) {
+                const long long ent = (long long)t * a.kt + j;
+                const int p = a.pos_of[ent];
+                if (p < 0) continue;
+                const long long off = (long long)p * a.ld_y + d;
+                const float v = a.y_bf16 ? bf16_to_f32(((const uint16_t *)a.y)[off]) : ((const float *)a.y)[off];
+                acc = acc + a.gates[ent] * v;
+            }
+            o[d] = acc;
+        }
+        return;
+    }
     bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0;
     for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
     if (all_kept) {

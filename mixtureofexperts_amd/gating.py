@@ -237,13 +237,15 @@ def compute_gates(gate, router_logits, noise_logits=None, training=False):
         return idx.T.astype(np.int64), gates.T, probs
     spec = gate_spec(gate, E)
     kt = spec.num_shared + spec.k
+    dev = _gating_handle(spec, E, T) if T > 0 else None
     if isinstance(gate, ExpertChoiceGating):
-        kt = min(E, _lib.MOE_MAX_TOPK)
+        # the handle's slots: min(capacity at its max_tokens, E), of which a
+        # call fills min(capacity, E)
+        kt = dev.slots if dev is not None else 0
     idx = np.zeros((T, kt), dtype=np.int32)
     gates = np.zeros((T, kt), dtype=np.float32)
     probs = np.zeros((T, E), dtype=np.float32)
     if T > 0:
-        dev = _gating_handle(spec, E, T)
         lt = np.ascontiguousarray(logits.T)
         _lib.check(
             _lib.lib().moe_compute_gates(dev.h, lt.ctypes.data, T, idx.ctypes.data, gates.ctypes.data,

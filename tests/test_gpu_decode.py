@@ -111,6 +111,15 @@ def test_decode_unsupported_and_bad_args(moe, oracle):
         assert ei.value.status == _lib.MOE_EINVAL
     finally:
         c.dev.close()
+    # gated_expert_forward! applies silu: a gated layer configured with gelu
+    # (MoEConfig's default) is refused instead of silently computing silu
+    c = Case(moe, oracle, T=4, D=64, H=128, E=8, k=2, act="gelu", wdtype="f32", seed=29)
+    try:
+        with pytest.raises(_lib.MoeError) as ei:
+            c.dev.decode(np.ascontiguousarray(c.x[:2]))
+        assert ei.value.status == _lib.MOE_EUNSUPPORTED and "silu" in str(ei.value)
+    finally:
+        c.dev.close()
 
 
 def test_decode_python_api(moe, oracle):
@@ -173,3 +182,55 @@ def test_decode_between_forwards_leaves_forward_unchanged(moe, oracle, wdtype):
         assert np.array_equal(out1.view(np.uint32), out2.view(np.uint32)) and loss1 == loss2
     finally:
         c.dev.close()
+
+
+def test_stories42m_moe_decode_chain(moe, oracle):
+    # BASELINE config 2's MoE part: three stories42M-shaped FFNs (dim 512,
+    # hidden 1376) converted with convert_to_moe's :perturb (noise 0.01) into 8
+    # gated silu experts, top-2, fp32, then tokens decoded one at a time
+    # through the three layers in order (moe_ffn_forward! per layer,
+    # src/llama2/inference.jl:58-121; sample_moe's per-token loop,
+    # src/llama2/generation.jl:38-128).  Every layer of every token is checked
+    # against oracle.decode_ffn on the GPU's logits with the experts read back
+    # from the device: routing and gates bit-exact, output within 1e-4; the
+    # chain's final output also against the oracle run end to end on its own.
+    rng = np.random.default_rng(42)
+    dim, hid, E, n_tok = 512, 1376, 8, 48
+    layers, host = [], []
+    try:
+        for li in range(3):
+            w1, w3 = [(rng.standard_normal((dim, hid)) * 0.02).astype(np.float32) for _ in range(2)]
+            w2 = (rng.standard_normal((hid, dim)) * 0.02).astype(np.float32)
+            layer = moe.convert_layer_to_moe(w1, w2, w3, num_experts=E, top_k=2, expert_init_strategy="perturb",
+                                             expert_init_noise=0.01, max_tokens=4, seed=100 + li,
+                                             rng=np.random.default_rng(li))
+            layers.append(layer)
+            host.append((layer.router.weight, [dict(w1=e.w1, w2=e.w2, w3=e.w3) for e in layer.experts]))
+            # :perturb: each expert is the dense FFN plus N(0, 0.01^2) noise
+            d = layers[-1].experts[3].w1 - w1.T
+            assert abs(float(d.std()) - 0.01) < 5e-4 and abs(float(d.mean())) < 5e-4
+        x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+        final = np.zeros((n_tok, dim), np.float32)
+        usage = np.zeros((3, E), np.int64)
+        for t in range(n_tok):
+            print(f"decode chain token {t}", flush=True) if t % 16 == 0 else None
+            v = x[t:t + 1]
+            for li, layer in enumerate(layers):
+                out, logits, idx, gates = layer._dev.decode(np.ascontiguousarray(v))
+                wr, ex = host[li]
+                ref, ridx, rgates, _ = oracle.decode_ffn(v, wr, ex, k=2, logits=logits)
+                assert np.array_equal(idx, ridx), (t, li)
+                assert np.array_equal(gates.view(np.uint32), rgates.view(np.uint32)), (t, li)
+                assert rel_err(out, ref) <= 1e-4, (t, li)
+                usage[li, idx[0] - 1] += 1
+                v = out
+            final[t] = v[0]
+        # end to end on the oracle alone (its own fp32 logits)
+        ref = x
+        for wr, ex in host:
+            ref = oracle.decode_ffn(ref, wr, ex, k=2)[0]
+        assert rel_err(final, ref) <= 1e-4
+        assert usage.sum() == 3 * n_tok * 2
+    finally:
+        for layer in layers:
+            layer.close()

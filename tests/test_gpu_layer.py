@@ -260,18 +260,23 @@ def test_aux_free_python_api(moe, oracle):
         moe.update_bias(l2, np.array([[E + 1]]))
 
 
-@pytest.mark.parametrize("gate,param,E,k,wdtype", [("soft", 0.5, 8, 2, "bf16"), ("soft", 1.0, 6, 3, "f32"),
-                                                    ("expert_choice", 1.25, 8, 0, "bf16"),
-                                                    ("expert_choice", 0.125, 16, 0, "f32")])
-def test_soft_and_expert_choice_layer(moe, oracle, gate, param, E, k, wdtype):
+@pytest.mark.parametrize("gate,param,E,k,wdtype,T", [("soft", 0.5, 8, 2, "bf16", 512), ("soft", 1.0, 6, 3, "f32", 512),
+                                                      ("soft", 0.8, 128, 4, "bf16", 1024),
+                                                      ("expert_choice", 1.25, 8, 0, "bf16", 512),
+                                                      ("expert_choice", 0.125, 16, 0, "f32", 512),
+                                                      # more than 8 slots per token: min(capacity, E) = 16, 64, 86
+                                                      ("expert_choice", 1.25, 16, 0, "bf16", 4096),
+                                                      ("expert_choice", 1.25, 64, 0, "bf16", 4096),
+                                                      ("expert_choice", 4.0, 96, 0, "f32", 2048)])
+def test_soft_and_expert_choice_layer(moe, oracle, gate, param, E, k, wdtype, T):
     # the layer forward with SoftMoEGating / ExpertChoiceGating against the
     # oracle on the GPU's logits: routing bit-exact, output and loss in tolerance
     from mixtureofexperts_amd import _lib
     from mixtureofexperts_amd._device import DeviceLayer, GateSpec
 
     rng = np.random.default_rng(70 + E)
-    T, D, H = 512, 128, 192
-    print(f"layer gate={gate} param={param} E={E} k={k} w={wdtype}", flush=True)
+    D, H = 128, 192
+    print(f"layer gate={gate} param={param} E={E} k={k} w={wdtype} T={T}", flush=True)
     x = rng.standard_normal((T, D)).astype(np.float32)
     wr = (rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)
     ex, dev_w = [], []
@@ -411,6 +416,22 @@ def test_other_activations_and_odd_sizes(moe, oracle):
     check_case(c, TOL["bf16"])
 
 
+@pytest.mark.parametrize("E,k,gate,ns", [(96, 3, "topk", 0), (128, 2, "topk", 0), (70, 8, "topk", 0),
+                                        (100, 6, "shared", 2)])
+def test_over_64_routed_experts(moe, oracle, E, k, gate, ns):
+    # more than 64 routed experts with k >= 2: the top-k by per-lane sorted
+    # lists and the butterfly merge of the routing kernel, in a full layer
+    rng = np.random.default_rng(E + k)
+    bias = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    c = Case(moe, oracle, T=900, D=128, H=160, E=E, k=k, gate=gate, ns=ns, wdtype="bf16", xdtype="bf16",
+             seed=E * 10 + k, router_bias=bias)
+    try:
+        check_case(c, TOL["bf16"])
+        check_case(c, TOL["bf16"], training=False)
+    finally:
+        c.dev.close()
+
+
 def test_varying_batch_on_one_handle(moe, oracle):
     c = Case(moe, oracle, T=300, D=128, H=256, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=9)
     for T in (300, 1, 7, 129, 300):
@@ -502,19 +523,63 @@ def test_async_device_path_matches_host(moe, oracle):
     assert float(loss.item()) == ref_loss
 
 
+def test_calls_on_other_streams_are_ordered(moe, oracle):
+    # moe_forward_async enqueued on a non-blocking torch stream, then, with no
+    # synchronisation in between, a blocking moe_decode and moe_forward (both
+    # on the handle's own stream, sharing its workspace): the library orders
+    # them after the async work, so every result is bit-identical to the same
+    # call made alone
+    torch = pytest.importorskip("torch")
+    import ctypes
+
+    from mixtureofexperts_amd import _lib
+
+    c = Case(moe, oracle, T=2048, D=512, H=1024, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=15)
+    try:
+        ref, ref_loss, _ = c.run(training=True)
+        xd = np.ascontiguousarray(c.x[:8])
+        ref_dec = c.dev.decode(xd)[0]
+        x = torch.from_numpy(c.x_dev.view(np.int16)).cuda().view(torch.bfloat16)
+        outs = [torch.empty((c.T, c.Dout), dtype=torch.float32, device="cuda") for _ in range(3)]
+        stream = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        L = _lib.lib()
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        for o in outs:
+            _lib.check(L.moe_forward_async(c.dev.h, x.data_ptr(), _lib.MOE_BF16, c.T, 1, o.data_ptr(), None, sp),
+                       c.dev.h)
+        dec = c.dev.decode(xd)[0]
+        fwd, fwd_loss, _ = c.run(training=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(dec.view(np.uint32), ref_dec.view(np.uint32))
+        assert np.array_equal(fwd.view(np.uint32), ref.view(np.uint32)) and fwd_loss == ref_loss
+        for o in outs:
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+        # and the other way round: a blocking call, then async work on the torch stream
+        _lib.check(L.moe_forward_async(c.dev.h, x.data_ptr(), _lib.MOE_BF16, c.T, 1, outs[0].data_ptr(), None, sp),
+                   c.dev.h)
+        stream.synchronize()
+        assert np.array_equal(outs[0].cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    finally:
+        c.dev.close()
+
+
 def test_random_layer_shapes(moe, oracle):
     # seeded shapes across the paths the bf16 kernel takes: D / Dout not
-    # multiples of 8 (direct y stores) or of 256 (cut columns), 2..40
-    # experts, top-1..4, gated / standard, bf16 / fp8, batches that give
-    # 128- and 256-row tiles, partial tiles and tail-split down tiles
+    # multiples of 8 (element-wise permute, direct y stores) or of 256 (cut
+    # columns), 2..40 experts, top-1..4, gated / standard, bf16 / fp8, batches
+    # that give 128- and 256-row tiles, partial tiles and tail-split down tiles
     rng = np.random.default_rng(2026)
-    for case in range(10):
+    for case in range(14):
         E = int(rng.integers(2, 41))
         k = int(rng.integers(1, min(4, E) + 1))
-        D = int(rng.choice([64, 96, 200, 256, 320, 512]))
-        Dout = int(rng.choice([D, 72, 136, 264]))
+        D = int(rng.choice([64, 90, 100, 130, 200, 262, 320, 512]))
+        Dout = int(rng.choice([D, 72, 90, 130, 136, 262]))
         H = int(rng.choice([96, 200, 384, 688]))
-        T = int(rng.integers(16, 700))
+        T = int(rng.integers(16, 700)) if case % 2 == 0 else int(rng.integers(1200, 2400))
+        if case % 4 == 1:
+            E = int(rng.integers(2, 9))  # few large experts: 256-row tiles
+            k = int(rng.integers(1, min(2, E) + 1))
         etype = "gated" if rng.random() < 0.7 else "standard"
         act = "silu" if etype == "gated" else str(rng.choice(["gelu", "relu"]))
         wdtype = str(rng.choice(["bf16", "fp8"]))

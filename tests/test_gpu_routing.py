@@ -63,6 +63,38 @@ def test_topk_random_logits(moe, oracle, T, E, k):
     check_route(moe, oracle, logits, "topk", k)
 
 
+@pytest.mark.parametrize("E", [65, 96, 128])
+@pytest.mark.parametrize("k", [2, 3, 6, 8])
+def test_topk_over_64_experts(moe, oracle, E, k):
+    # more than 64 routed experts with k >= 2: each of a token's 8 lanes keeps
+    # the best k of its share in sorted registers, three butterfly steps merge
+    # the lists; random, tie-heavy integer and non-finite logits
+    rng = np.random.default_rng(E * 100 + k)
+    lg = rng.standard_normal((3000, E)).astype(np.float32)
+    check_route(moe, oracle, lg, "topk", k)
+    lg = rng.integers(-2, 3, size=(2000, E)).astype(np.float32)
+    check_route(moe, oracle, lg, "topk", k)
+    lg = rng.standard_normal((300, E)).astype(np.float32)
+    lg[3, 7] = np.inf
+    lg[4, :] = -np.inf
+    lg[5, E - 1] = np.nan
+    lg[6, [1, E - 2]] = np.inf
+    lg[7, ::3] = np.nan
+    lg[8, :] = 0.0
+    lg[9, :] = np.float32(-0.0)
+    check_route(moe, oracle, lg, "topk", k)
+
+
+@pytest.mark.parametrize("E,ns,k", [(100, 2, 6), (128, 1, 7), (67, 2, 2)])
+def test_shared_gating_over_64_routed(moe, oracle, E, ns, k):
+    rng = np.random.default_rng(E + ns + k)
+    lg = rng.standard_normal((2500, E)).astype(np.float32)
+    lg[:, ns:] += np.log(1.0 / np.arange(1, E - ns + 1) ** 1.1).astype(np.float32)
+    lg[::5] = np.round(lg[::5])
+    d = check_route(moe, oracle, lg, "shared", k, ns)
+    assert np.all(d[3][:ns] == 2500)
+
+
 def test_topk_skewed_and_ties(moe, oracle):
     rng = np.random.default_rng(11)
     # small integer logits: exact ties everywhere
@@ -161,7 +193,8 @@ def test_routing_is_deterministic(moe, oracle):
         assert np.array_equal(x, y)
 
 
-@pytest.mark.parametrize("T,E,k,lam", [(2048, 8, 2, 0.7), (1000, 64, 6, 2.0), (77, 5, 3, -1.5)])
+@pytest.mark.parametrize("T,E,k,lam", [(2048, 8, 2, 0.7), (1000, 64, 6, 2.0), (77, 5, 3, -1.5), (1500, 128, 4, 0.9),
+                                       (600, 96, 8, 1.0)])
 def test_soft_moe_gating(moe, oracle, T, E, k, lam):
     # SoftMoEGating: top-k of softmax(logits ./ lambda), the gate matrix is the
     # probabilities (the dispatch reads the probability of expert `slot`)
@@ -176,7 +209,8 @@ def test_soft_moe_gating(moe, oracle, T, E, k, lam):
 
 
 @pytest.mark.parametrize("T,E,cf,ties", [(4096, 8, 1.25, False), (64, 16, 1.0, True), (300, 8, 0.25, True),
-                                         (33, 6, 3.0, True)])
+                                         (33, 6, 3.0, True), (4096, 16, 1.25, False), (4096, 64, 1.25, False),
+                                         (1000, 64, 2.0, True), (2048, 128, 6.0, False)])
 def test_expert_choice_gating(moe, oracle, T, E, cf, ties):
     # ExpertChoiceGating: the (capacity, T) indices / gates bit-exact
     rng = np.random.default_rng(T * E)
@@ -189,12 +223,30 @@ def test_expert_choice_gating(moe, oracle, T, E, cf, ties):
     assert same(gates.T, og) and same(probs.T, op)
 
 
-def test_expert_choice_too_many_slots_is_unsupported(moe):
-    # 16 experts and capacity 16: a token may be taken by more than 8 experts
-    lg = np.zeros((16, 64), np.float32)
-    with pytest.raises(moe.MoeError) as ei:
-        moe.compute_gates(moe.ExpertChoiceGating(4.0), lg)
-    assert "MOE_MAX_TOPK" in str(ei.value)
+def test_expert_choice_many_slots_bucketing(moe, oracle):
+    # 16 experts, capacity 16 (equal logits: every expert takes tokens 1..16,
+    # so each of them holds all 16 experts); and 64 experts at T = 4096:
+    # indices, counts, offsets and the permutation bit-exact
+    lg = np.zeros((64, 16), np.float32)
+    idx, gates, probs = moe.compute_gates(moe.ExpertChoiceGating(4.0), lg.T)
+    assert idx.shape == (16, 64)
+    assert np.array_equal(idx[:, :16], np.tile(np.arange(1, 17)[:, None], (1, 16)))
+    assert np.all(idx[:, 16:] == 0)
+    rng = np.random.default_rng(77)
+    for T, E, cf in ((64, 16, 4.0), (4096, 64, 1.25), (500, 128, 40.0)):
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        g = moe.ExpertChoiceGating(cf)
+        print(f"expert choice bucketing T={T} E={E} cf={cf}", flush=True)
+        di, dg, dp, counts, offsets, perm = moe.route_from_logits(g, lg.T)
+        oi, og, op = oracle.compute_gates_expert_choice(lg, cf)
+        kt = di.shape[0]
+        n = min(kt, oi.shape[1])
+        assert np.array_equal(di.T[:, :n].astype(np.int32), oi[:, :n]) and np.all(oi[:, n:] == 0)
+        assert same(dg.T[:, :n], og[:, :n]) and same(dp.T, op)
+        oc, oo, opm = oracle.bucket(oi, E)
+        assert np.array_equal(counts, oc) and np.array_equal(offsets, oo)
+        m = int(oo[-1])
+        assert np.array_equal(np.divmod(perm[:m], kt), np.divmod(opm, oi.shape[1]))
 
 
 def test_jitter_and_stochastic_gates(moe, oracle):
