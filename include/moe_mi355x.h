@@ -287,6 +287,24 @@ int moe_z_loss(const float *logits, int32_t T, int32_t E, float beta, float *los
 int moe_aux_free_update_bias(const int32_t *indices, int64_t n, int32_t E, float learning_rate, float momentum,
                              float *bias, float *bias_momentum);
 
+/* ---- allocation-free entry point ----------------------------------------- */
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): compute_loss(::SwitchTransformerLoss, indices, probs) as
+ * moe_switch_loss computes it (the same kernels, bit for bit), on device
+ * buffers indices_dev [T][k], probs_dev [T][E] and loss_dev (1 float),
+ * enqueued on `stream` (hipStream_t; NULL = the null stream).  Its partial
+ * sums live in a fixed device array of the library,
+ * MOE_SWITCH_LOSS_SCRATCH_BYTES per GPU, held until the process ends, instead
+ * of a per-call allocation.  E <= MOE_MAX_EXPERTS (else MOE_EINVAL).  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other threads) race.  The first call on a device looks the array
+ * up (hipGetSymbolAddress): make it outside stream capture. */
+#define MOE_SWITCH_LOSS_SCRATCH_BYTES (64 * MOE_MAX_EXPERTS * 12)
+int moe_switch_loss_noalloc(const int32_t *indices_dev, int32_t T, int32_t k, const float *probs_dev, int32_t E,
+                            float alpha, float *loss_dev, void *stream);
+
 /* ---- device-buffer entry points (enqueue only) -------------------------- */
 
 /* moe_forward on device buffers: x_dev [T][D], out_dev [T][D_out] fp32,

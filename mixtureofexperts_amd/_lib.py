@@ -41,7 +41,7 @@ EXPORTED_SYMBOLS = [
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
     "moe_read_counts", "moe_switch_loss", "moe_z_loss", "moe_decode", "moe_decode_async",
     "moe_set_aux_free", "moe_get_aux_free", "moe_aux_free_update_bias", "moe_forward_routed",
-    "moe_init_experts_from_dense", "moe_get_expert",
+    "moe_init_experts_from_dense", "moe_get_expert", "moe_switch_loss_noalloc",
 ]
 
 
@@ -139,6 +139,7 @@ def lib():
     L.moe_decode_async.argtypes = [vp, vp, i32, vp, vp]
     L.moe_switch_loss.argtypes = [vp, i32, i32, vp, i32, ctypes.c_float, f32p]
     L.moe_z_loss.argtypes = [vp, i32, i32, ctypes.c_float, f32p]
+    L.moe_switch_loss_noalloc.argtypes = [vp, i32, i32, vp, i32, ctypes.c_float, vp, vp]
     i64, f32 = ctypes.c_int64, ctypes.c_float
     L.moe_set_aux_free.argtypes = [vp, i32, vp, vp, f32, f32, i32, i64, i32, f32]
     L.moe_get_aux_free.argtypes = [vp, vp, vp, ctypes.POINTER(i64)]

@@ -1542,21 +1542,80 @@ int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stre
 int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *probs, int32_t E, float alpha,
                     float *loss) {
     if (!loss || T < 0 || k < 1 || E < 1) return fail(nullptr, MOE_EINVAL, "bad switch-loss arguments");
+    if (E > MOE_MAX_EXPERTS) return fail(nullptr, MOE_EINVAL, "switch loss: E above MOE_MAX_EXPERTS (128)");
+    if ((long long)T * k > INT_MAX) return fail(nullptr, MOE_EINVAL, "switch loss: T * k too large");
     if (T > 0 && (!indices || !probs)) return fail(nullptr, MOE_EINVAL, "null indices or probs");
     if (T == 0) { *loss = NAN; return MOE_OK; }
     const size_t ni = (size_t)T * k, np_ = (size_t)T * E;
+    // one allocation: the partials (8-byte aligned first), indices, probs, the loss
+    const size_t pb = switch_loss_scratch_bytes(T, E);
     void *buf = nullptr;
-    const size_t bytes = sizeof(int) * ni + sizeof(float) * np_ + sizeof(int) * E + 16;
+    const size_t bytes = pb + sizeof(int) * ni + sizeof(float) * np_ + 16;
     if (hipMalloc(&buf, bytes) != hipSuccess) return fail(nullptr, MOE_EOOM, "hipMalloc failed");
-    int *di = (int *)buf;
+    int *di = (int *)((uint8_t *)buf + pb);
     float *dp = (float *)(di + ni);
-    int *dc = (int *)(dp + np_);
-    float *dout = (float *)(dc + E);
+    float *dout = dp + np_;
     hipError_t e = hipMemcpy(di, indices, sizeof(int) * ni, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(dp, probs, sizeof(float) * np_, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = launch_switch_loss(di, T, k, dp, E, alpha, dc, dout, nullptr);
+    if (e == hipSuccess) e = launch_switch_loss(di, T, k, dp, E, alpha, buf, dout, nullptr);
     if (e == hipSuccess) e = hipMemcpy(loss, dout, sizeof(float), hipMemcpyDeviceToHost);
     (void)hipFree(buf);
+    if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("switch loss failed: ") + hipGetErrorString(e));
+    return MOE_OK;
+}
+
+// ---- the allocation-free Switch loss -------------------------------------------
+// The largest partials launch_switch_loss writes: kSwitchLossMaxBlocks rows of
+// MOE_MAX_EXPERTS doubles and ints (96 KiB).
+constexpr size_t kSwitchLossScratchBytes =
+    (size_t)kSwitchLossMaxBlocks * MOE_MAX_EXPERTS * (sizeof(double) + sizeof(int));
+static_assert(kSwitchLossScratchBytes == MOE_SWITCH_LOSS_SCRATCH_BYTES, "header and library agree");
+
+// File-scope device array of those partials.  Each GPU the library runs on
+// holds its own copy until the process ends.  In host code its name is a
+// host-side stand-in, never an address: the device address of a GPU's copy
+// comes from hipGetSymbolAddress, looked up once per device (the first call
+// on it) and kept in scratch_dev.
+static __device__ __align__(256) uint8_t scratch[kSwitchLossScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *scratch_dev[kMaxDevices] = {};
+
+// The device address of the current device's scratch array.
+static int current_scratch(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(nullptr, MOE_EINVAL, "device ordinal above 63");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!scratch_dev[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(nullptr, MOE_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        scratch_dev[dev] = p;
+    }
+    *out = scratch_dev[dev];
+    return MOE_OK;
+}
+
+int moe_switch_loss_noalloc(const int32_t *indices_dev, int32_t T, int32_t k, const float *probs_dev, int32_t E,
+                            float alpha, float *loss_dev, void *stream) {
+    if (!loss_dev || T < 0 || k < 1 || E < 1) return fail(nullptr, MOE_EINVAL, "bad switch-loss arguments");
+    if (E > MOE_MAX_EXPERTS)
+        return fail(nullptr, MOE_EINVAL,
+                    "moe_switch_loss_noalloc: E above MOE_MAX_EXPERTS (128), the limit of its scratch array");
+    if ((long long)T * k > INT_MAX) return fail(nullptr, MOE_EINVAL, "switch loss: T * k too large");
+    if (T > 0 && (!indices_dev || !probs_dev)) return fail(nullptr, MOE_EINVAL, "null indices or probs");
+    if (switch_loss_scratch_bytes(T, E) > kSwitchLossScratchBytes)
+        return fail(nullptr, MOE_EINVAL, "moe_switch_loss_noalloc: partials exceed the scratch array");
+    void *ws = nullptr;
+    const int r = current_scratch(&ws);
+    if (r != MOE_OK) return r;
+    // T = 0 runs too: the partials are zeros and the loss the NaN of a mean
+    // over no tokens, as moe_switch_loss returns
+    const hipError_t e = launch_switch_loss(indices_dev, T, k, probs_dev, E, alpha, ws, loss_dev, (hipStream_t)stream);
     if (e != hipSuccess) return fail(nullptr, MOE_EHIP, std::string("switch loss failed: ") + hipGetErrorString(e));
     return MOE_OK;
 }

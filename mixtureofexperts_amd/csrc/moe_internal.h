@@ -308,7 +308,18 @@ hipError_t launch_expert_choice(const float *logits, const float *probs, int T, 
                                 int *idx, float *gates, int *rank, int *blk_counts, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
-hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,
+// compute_loss(::SwitchTransformerLoss) on device buffers in two launches
+// (per-block partial counts and probability sums, then their fold in block
+// order); `partials` holds switch_loss_scratch_bytes(T, E) bytes, written
+// before they are read (no clearing needed).  E <= MOE_MAX_EXPERTS.
+constexpr int kSwitchLossMaxBlocks = 64;
+int switch_loss_blocks(long long T);
+inline size_t switch_loss_sum_bytes(int nb, int E) { return sizeof(double) * (size_t)nb * E; }
+inline size_t switch_loss_scratch_bytes(long long T, int E) {
+    const int nb = switch_loss_blocks(T);
+    return switch_loss_sum_bytes(nb, E) + sizeof(int) * (size_t)nb * E;
+}
+hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, void *partials,
                               float *out, hipStream_t s);
 hipError_t launch_z_loss(const float *logits, int T, int E, float beta, float *out, hipStream_t s);
 // update_bias!(AuxiliaryFreeLoss, indices) on given indices [n] (entries > 0 counted)

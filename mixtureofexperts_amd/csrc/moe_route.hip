@@ -1576,32 +1576,82 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
 // ============================================================================
 // Standalone losses on given routing (compute_loss seams).
 // ============================================================================
-// compute_loss(::SwitchTransformerLoss, indices, probs): one block.
-__global__ __launch_bounds__(256) void switch_loss_kernel(const int *idx, int T, int k, const float *probs, int E,
-                                                          float alpha, int *cnt_ws, float *out) {
-#pragma clang fp contract(off)
+// compute_loss(::SwitchTransformerLoss, indices, probs) in two launches.
+// Part 1: block b of nb takes the contiguous token range [b R, (b + 1) R),
+// R = ceil(T / nb): its entries' expert counts (LDS histogram) and, per
+// expert e (thread e), the fp64 sum of probs[t][e] over the range in token
+// order; both go to the block's row of the partials (cnt [nb][E], sum
+// [nb][E]).  Every row is written (zeros for an empty range), so the
+// partials need no clearing.
+__global__ __launch_bounds__(256) void switch_loss_partial_kernel(const int *__restrict__ idx, int T, int k,
+                                                                  const float *__restrict__ probs, int E,
+                                                                  int *__restrict__ cnt_part,
+                                                                  double *__restrict__ sum_part) {
+    __shared__ int cnt[MOE_MAX_EXPERTS];
     const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += 256) cnt_ws[e] = 0;
+    const int R = (T + gridDim.x - 1) / gridDim.x;
+    const int t0 = min(T, (int)blockIdx.x * R), t1 = min(T, t0 + R);
+    for (int e = tid; e < E; e += 256) cnt[e] = 0;
     __syncthreads();
-    for (long long i = tid; i < (long long)T * k; i += 256) {
+    for (long long i = (long long)t0 * k + tid; i < (long long)t1 * k; i += 256) {
         const int e = idx[i];
-        if (e > 0 && e <= E) atomicAdd(&cnt_ws[e - 1], 1);
+        if (e > 0 && e <= E) atomicAdd(&cnt[e - 1], 1);
+    }
+    for (int e = tid; e < E; e += 256) {
+        double ps = 0.0;
+        for (int t = t0; t < t1; ++t) ps += (double)probs[(long long)t * E + e];
+        sum_part[(long long)blockIdx.x * E + e] = ps;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) cnt_part[(long long)blockIdx.x * E + e] = cnt[e];
+}
+
+// Part 2, one block: thread e adds its expert's partials in block order;
+// f_e = count / (T k) (the length of indices counts every entry,
+// src/balancing/losses.jl:17,30), P_e = mean_t probs[t][e] (:33), and the
+// f_e P_e terms are summed in expert order (:35).  T = 0 gives NaN, the mean
+// over no tokens.
+__global__ __launch_bounds__(256) void switch_loss_finish_kernel(const int *__restrict__ cnt_part,
+                                                                 const double *__restrict__ sum_part, int nb, int T,
+                                                                 int k, int E, float alpha, float *out) {
+#pragma clang fp contract(off)
+    __shared__ float fp[MOE_MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 256) {
+        long long c = 0;
+        double ps = 0.0;
+        for (int b = 0; b < nb; ++b) {
+            c += cnt_part[(long long)b * E + e];
+            ps += sum_part[(long long)b * E + e];
+        }
+        float f = (float)c;
+        if ((long long)T * k > 0) f = f / (float)((long long)T * k);
+        const float P = (float)ps / (float)T;
+        fp[e] = f * P;
     }
     __syncthreads();
     if (tid == 0) {
-        const float total = (float)((long long)T * k);
-        float s = 0.0f;
-        for (int e = 0; e < E; ++e) {
-            double ps = 0.0;
-            for (int t = 0; t < T; ++t) ps += (double)probs[(long long)t * E + e];
-            float f = (float)cnt_ws[e];
-            if ((long long)T * k > 0) f = f / total;
-            const float P = (float)ps / (float)T;
-            const float fp = f * P;
-            s = (e == 0) ? fp : s + fp;
-        }
+        float s = fp[0];
+        for (int e = 1; e < E; ++e) s = s + fp[e];
         out[0] = (alpha * (float)E) * s;
     }
+}
+
+int switch_loss_blocks(long long T) {
+    // about 512 tokens per block, at most kSwitchLossMaxBlocks blocks
+    return (int)std::max<long long>(1, std::min<long long>(kSwitchLossMaxBlocks, (T + 511) / 512));
+}
+
+hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, void *partials,
+                              float *out, hipStream_t s) {
+    if (E < 1 || E > MOE_MAX_EXPERTS || T < 0 || k < 1) return hipErrorInvalidValue;
+    const int nb = switch_loss_blocks(T);
+    int *cnt_part = (int *)((uint8_t *)partials + switch_loss_sum_bytes(nb, E));
+    double *sum_part = (double *)partials;
+    hipLaunchKernelGGL(switch_loss_partial_kernel, dim3(nb), dim3(256), 0, s, idx, T, k, probs, E, cnt_part, sum_part);
+    hipLaunchKernelGGL(switch_loss_finish_kernel, dim3(1), dim3(256), 0, s, cnt_part, sum_part, nb, T, k, E, alpha,
+                       out);
+    return hipGetLastError();
 }
 
 // compute_loss(::ZLoss, logits): beta * mean_t(logsumexp_t^2), one block.
@@ -1653,12 +1703,6 @@ __global__ __launch_bounds__(256) void aux_free_update_kernel(const int *idx, lo
 hipError_t launch_aux_free_update(const int *idx, long long n, int E, float lr, float momentum, float *bias,
                                   float *mom, hipStream_t s) {
     hipLaunchKernelGGL(aux_free_update_kernel, dim3(1), dim3(256), 0, s, idx, n, E, lr, momentum, bias, mom);
-    return hipGetLastError();
-}
-
-hipError_t launch_switch_loss(const int *idx, int T, int k, const float *probs, int E, float alpha, int *cnt_ws,
-                              float *out, hipStream_t s) {
-    hipLaunchKernelGGL(switch_loss_kernel, dim3(1), dim3(256), 0, s, idx, T, k, probs, E, alpha, cnt_ws, out);
     return hipGetLastError();
 }
 
