@@ -48,7 +48,7 @@ struct moe_handle {
 
     // weights
     float *wr = nullptr, *br = nullptr;
-    uint16_t *wsplit = nullptr;  // router weight as three bf16 parts [3][Ep16][Dp32]
+    uint16_t *wsplit = nullptr;  // router weight's three bf16 parts as the fused router's fragment image
     int Ep16 = 0, Dp32 = 0;
     bool router_set = false, has_bias = false;
     std::vector<char> expert_set;
@@ -71,7 +71,7 @@ struct moe_handle {
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
-    float *logits_part = nullptr;  // [kRouterMaxSlices][T][Er] router GEMM partial sums
+    float *logits_part = nullptr;  // [kRouterMaxSlices][T][Er] K-slice partial logits (slot 0: the caller's logits)
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
     double *blk_stats = nullptr;
     int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
@@ -96,6 +96,7 @@ struct moe_handle {
     float *aux_bias = nullptr, *aux_mom = nullptr;
     int *tot_counts = nullptr;       // scan work: column totals
     double *tot_stats = nullptr;
+    unsigned *scan_ticket = nullptr; // scan work: finished column blocks
 
     int last_T = -1, last_training = 0, last_x_bf16 = 0;
     std::vector<void *> allocs;
@@ -561,41 +562,42 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         aux_update = h->aux_counter % h->aux_update_freq == 0;
     }
     RouteArgs ra{};
+    RouterArgs rg{};
     if (compute_logits) {
-        RouterArgs rg{};
+        // the first route pass computes the logits (router_fused_kernel)
         rg.x = x_dev; rg.x_bf16 = x_bf16; rg.T = T; rg.D = h->D; rg.Er = h->Er; rg.Ep = h->Ep16; rg.Dp = h->Dp32;
-        rg.ws = h->wsplit; rg.part = h->logits_part;
-        router_plan(rg);
-        HIP_TRY(h, launch_router_mfma(rg, x_bf16, s));
-        ra.nks = rg.nks;
+        rg.ws = h->wsplit;
         ra.bias = h->has_bias ? h->br : nullptr;
     } else {
-        ra.nks = 1;  // the caller's logits are in partial slot 0
         ra.bias = nullptr;
     }
-    ra.part = h->logits_part; ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->Er; ra.Eh = h->E;
+    ra.part = h->logits_part;  // K-slice partial logits, or the caller's logits (slot 0)
+    ra.nks = 1;
+    if (compute_logits) HIP_TRY(h, launch_router_logits(rg, h->logits_part, kRouterMaxSlices, &ra.nks, s));
+    ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->Er; ra.Eh = h->E;
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
+    auto first_pass = [&](const RouteArgs &a) { return launch_route(a, s); };
     if (aux) {
         ra.out_mask = ROUTE_OUT_PROBS;
-        HIP_TRY(h, launch_route(ra, s));
+        HIP_TRY(h, first_pass(ra));
         ra.part = h->logits;  // the logits just written, plus the loss's bias
-        ra.nks = 1;
         ra.bias = h->aux_bias;
         ra.out_mask = ROUTE_OUT_GATING;
+        HIP_TRY(h, launch_route(ra, s));
     } else if (ec) {
         // softmax pass; the experts' choices give the slots, the stable ranks
         // and the per-block histogram
         ra.out_mask = ROUTE_OUT_PROBS;
-        HIP_TRY(h, launch_route(ra, s));
+        HIP_TRY(h, first_pass(ra));
         HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
                                         h->rank, h->blk_counts, s));
     } else {
         ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
+        HIP_TRY(h, first_pass(ra));
     }
-    if (!ec) HIP_TRY(h, launch_route(ra, s));
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
     sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kc;
@@ -608,7 +610,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.aux_free = aux; sa.aux_use_comp = h->aux_use_comp; sa.aux_update = aux_update;
     sa.aux_cw = h->aux_cw; sa.aux_lr = h->aux_lr; sa.aux_momentum = h->aux_momentum;
     sa.aux_bias = h->aux_bias; sa.aux_mom = h->aux_mom;
-    sa.tot_counts = h->tot_counts; sa.tot_stats = h->tot_stats;
+    sa.tot_counts = h->tot_counts; sa.tot_stats = h->tot_stats; sa.ticket = h->scan_ticket;
     HIP_TRY(h, launch_scan(sa, s));
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
@@ -879,6 +881,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->scalars, sizeof(float) * 8);
     A((void **)&h->tot_counts, sizeof(int) * E);
     A((void **)&h->tot_stats, sizeof(double) * (E + 2));
+    A((void **)&h->scan_ticket, 256);
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
     A((void **)&h->aux_mom, sizeof(float) * h->Er);
@@ -914,6 +917,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
+    Z(h->scan_ticket, 256);
     Z(h->aux_bias, sizeof(float) * h->Er);
     Z(h->aux_mom, sizeof(float) * h->Er);
     Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);
@@ -960,7 +964,7 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     if (bias)
         HIP_TRY(h, hipMemcpyAsync(h->br, bias, sizeof(float) * h->Er, dev_b ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                   h->stream));
-    HIP_TRY(h, launch_router_split(h->wr, h->D, h->Er, h->Er_pad, h->Ep16, h->Dp32, h->wsplit, h->stream));
+    HIP_TRY(h, launch_router_split(h->wr, h->D, h->Er, h->Er_pad, h->Dp32, h->wsplit, h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     settle(h);
     h->has_bias = bias != nullptr;

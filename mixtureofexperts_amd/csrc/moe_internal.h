@@ -9,7 +9,7 @@
 namespace moe {
 
 constexpr int kRouteBlock = 32;    // tokens per routing block
-constexpr int kRouteThreads = 256; // threads per routing block (the first kRouteBlock own one token each)
+constexpr int kRouteThreads = 256; // threads per routing block (8 per token)
 constexpr int kRouterMaxSlices = 8;   // K slices of the router logits GEMM (partial sums)
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
@@ -124,13 +124,13 @@ __device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *
 // ---- kernel argument blocks --------------------------------------------------
 
 // Router logits GEMM: x [T][D] (bf16 or fp32) times the router weight split
-// into three bf16 parts ws [3][Ep][Dp] (Ep = Er rounded up to 16, Dp = D
-// rounded up to 32); partial sums over K slices of ks_len columns go to
-// part [nks][T][Er] (fp32).
+// into three bf16 parts, held as the fragment image of router_split_kernel
+// (Dp = D rounded up to 32), computed by the routing workgroups themselves
+// (router_fused_kernel).
 struct RouterArgs {
     const void *x; int x_bf16; int T, D, Er, Ep, Dp;
     const uint16_t *ws;
-    float *part; int nks, ks_len, kc;
+    int kslice;   // router_logits_kernel: K steps (of 32) per slice, a multiple of 8
 };
 
 // Outputs of one route_kernel pass.  A plain forward writes both; with an
@@ -186,6 +186,7 @@ struct ScanArgs {
     float *aux_bias, *aux_mom;  // [E] device state
     int *tot_counts;            // [E]   work: column totals of blk_counts
     double *tot_stats;          // [E+2] work: column totals of blk_stats
+    unsigned *ticket;           // [1]   work: finished column blocks (0 between launches)
 };
 
 struct PermuteArgs {
@@ -293,12 +294,17 @@ struct DecodeArgs {
 };
 
 // ---- launchers ----------------------------------------------------------------
-hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep, int Dp, uint16_t *ws,
-                               hipStream_t s);
-hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s);
-// K slicing of the router GEMM for a batch of T tokens (fills nks, ks_len, kc)
-void router_plan(RouterArgs &r);
+// the router weight [D][Er_pad] fp32 -> the fused router's fragment image of
+// its three bf16 parts ((Dp / 32) * tiles per step KB, at most 3 * Ep * Dp * 2 B)
+hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp, uint16_t *img, hipStream_t s);
+// routing blocks that compute their logits (x . W) themselves: the route
+// pass of `a` (a.part / a.nks unused) on the logits of r, one launch
+hipError_t launch_router_fused(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
+// a route pass on logits summed from a.part's a.nks slices
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+// the logits GEMM alone: K slices of r.kslice steps into part [nks][T][Er]
+// (the slicing is chosen here; *nks receives the slice count)
+hipError_t launch_router_logits(RouterArgs r, float *part, int max_slices, int *nks, hipStream_t s);
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
 // ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
 // gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the

@@ -34,28 +34,47 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 // ============================================================================
 typedef __bf16 rbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float rf32x4_t __attribute__((ext_vector_type(4)));
-constexpr int kRouterLdsPieces = 4096;  // 16-byte weight pieces per chunk (64 KB)
 
-__global__ void router_split_kernel(const float *__restrict__ w, int D, int Er, int Er_pad, int Ep, int Dp,
-                                    uint16_t *__restrict__ ws) {
+// The router weight's three parts as the fused router's B-fragment image:
+// for each 32-wide K step s and each of its NTS 16-column tiles q, the 64
+// lanes' 16-byte fragments in lane order (1 KB), so that every fragment load
+// is one contiguous read.  Lane l of tile q holds column c = l % 16 at K
+// s * 32 + 8 (l / 16) .. +8.  Paired (Er <= 8): tile 0 holds part 0 of the
+// experts in columns 0..7 and part 1 in columns 8..15, tile 1 part 2 in
+// columns 0..7 (8..15 zero); otherwise tile q = 3 et + p holds part p of
+// experts 16 et .. 16 et + 15.  Past Er or D: zero.
+__global__ void router_split_kernel(const float *__restrict__ w, int D, int Er, int Er_pad, int S, int NTS,
+                                    int paired, uint16_t *__restrict__ img) {
 #pragma clang fp contract(off)
-    const long long n = (long long)Ep * Dp;
+    const long long n = (long long)S * NTS * 64 * 8;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
-        const int e = (int)(i / Dp), d = (int)(i - (long long)e * Dp);
-        const float v = (e < Er && d < D) ? w[(long long)d * Er_pad + e] : 0.0f;
+        const int m = (int)(i & 7), l = (int)((i >> 3) & 63);
+        const long long qs = i >> 9;
+        const int q = (int)(qs % NTS), st = (int)(qs / NTS);
+        const int k = st * 32 + 8 * (l >> 4) + m, c = l & 15;
+        int part, e;
+        if (paired) {
+            e = c & 7;
+            part = (q == 0) ? (c >> 3) : ((c < 8) ? 2 : -1);
+        } else {
+            part = q % 3;
+            e = (q / 3) * 16 + c;
+        }
+        const float v = (part >= 0 && e < Er && k < D) ? w[(long long)k * Er_pad + e] : 0.0f;
         const uint16_t b0 = f32_to_bf16(v);
         const float r1 = v - bf16_to_f32(b0);
         const uint16_t b1 = f32_to_bf16(r1);
         const float r2 = r1 - bf16_to_f32(b1);
-        ws[i] = b0;
-        ws[n + i] = b1;
-        ws[2 * n + i] = f32_to_bf16(r2);
+        img[i] = (part <= 0) ? b0 : (part == 1 ? b1 : f32_to_bf16(r2));
     }
 }
 
-hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Ep, int Dp, uint16_t *ws,
-                               hipStream_t s) {
-    hipLaunchKernelGGL(router_split_kernel, dim3(256), dim3(256), 0, s, w, D, Er, Er_pad, Ep, Dp, ws);
+static int router_tiles_per_step(int Er) { return Er <= 8 ? 2 : 3 * ((Er + 15) / 16); }
+
+hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp, uint16_t *img, hipStream_t s) {
+    if (Dp % 32 != 0 || Er < 1 || Er > MOE_MAX_EXPERTS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(router_split_kernel, dim3(512), dim3(256), 0, s, w, D, Er, Er_pad, Dp / 32,
+                       router_tiles_per_step(Er), Er <= 8 ? 1 : 0, img);
     return hipGetLastError();
 }
 
@@ -104,160 +123,233 @@ __device__ inline void load_x8(const void *x, int D, int t, int k, rbf16x8_t *p)
     }
 }
 
-// Block: 4 waves x 32 tokens (two 16-token MFMA tiles per wave) over one K
-// slice; the slice's weight parts pass through LDS in chunks of KC columns
-// (rows padded by 16 bytes so the 16 rows one read touches fall in distinct
-// banks).  All global loads of a chunk are issued before any is used: the
-// wave's x fragments and the thread's share of the weight chunk (loads past
-// the slice use clamped in-bounds addresses and are not used).
-// v_mfma_f32_16x16x32_bf16: A = 16 tokens x 32 k (lane l: token l % 16,
-// k 8 (l / 16) .. +8), B = 32 k x 16 experts, D lane l: expert l % 16, tokens
-// 4 (l / 16) .. +4.
-template <int XBF16, int ALIGNED, int KC>
-__global__ __launch_bounds__(256) void router_mfma_kernel(RouterArgs r) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t rlds[];
-    constexpr int NP = XBF16 ? 1 : 3;       // activation parts
-    constexpr int RS = KC * 2 + 16;         // LDS row stride
-    constexpr int NWP = kRouterLdsPieces / 256;  // weight pieces per thread (upper bound)
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int tb = blockIdx.x * 128 + w * 32;
-    const int k_begin = blockIdx.y * r.ks_len, k_end = min(r.Dp, k_begin + r.ks_len);
-    const int ET = r.Ep / 16;
-    const int l16 = lane & 15, kq = (lane >> 4) * 8;
-    const long long np = (long long)r.Ep * r.Dp;
-    const int npieces = 3 * r.Ep * (KC / 8);  // 16-byte weight pieces per chunk (<= kRouterLdsPieces)
-    rf32x4_t acc[2][8];
+// The router logits of TM tokens (32 or 64) over all of K, into LDS rows
+// lrow[t][RW].  K runs in chunks of 256 (8 MFMA steps of 32): the block
+// stages each chunk of x in LDS with coalesced loads (each 16-lane pass
+// reads 256 contiguous bytes; rows padded by 16 B so the fragment reads hit
+// distinct banks), double-buffered so the next chunk's loads are in flight
+// during this chunk's MFMAs.  The split router weight is read from its
+// fragment image (router_split_kernel): one contiguous 1 KB per fragment.
+// Waves split the expert tiles NG ways and the K steps of each chunk
+// 4 / NG ways; per step, row tile and expert tile: acc += x . W0 + x . W1 +
+// x . W2 as v_mfma_f32_16x16x32_bf16 (fp32 x: each of its three parts times
+// the weight parts).  The waves' accumulators then go to an LDS buffer and
+// each logit is their sum in K-group order (paired tiles: the three parts'
+// columns added in part order), plus the router bias.
+// A: 16 tokens x 32 k (lane l: token l % 16, k 8 (l / 16) .. +8); B: the
+// image tile; D lane l: column l % 16, tokens 4 (l / 16) .. +4.
+constexpr int kRouterKC = 256;  // K per staged chunk
+
+template <int XBF16, int TM>
+__host__ __device__ constexpr int router_stage_row_bytes() { return kRouterKC * (XBF16 ? 2 : 4) + 16; }
+
+template <int XBF16, int TM, int PAIRED, int NG, int TPW, typename Out>
+__device__ __forceinline__ void fused_logits(const RouterArgs &r, int t0, int ntok, int s_begin, int s_end,
+                                             uint8_t *stage, Out &&out) {
+#pragma clang fp contract(off)
+    constexpr int RT = TM / 16;                 // 16-token row tiles
+    constexpr int ESZ = XBF16 ? 2 : 4;
+    constexpr int ROWB = router_stage_row_bytes<XBF16, TM>();
+    constexpr int UPR = kRouterKC * ESZ / 16;   // 16-byte units per staged row
+    constexpr int NU = TM * UPR / kRouteThreads;  // units per thread per chunk
+    constexpr int KG = 4 / NG;                  // K groups
+    constexpr int SPW = 8 / KG;                 // steps per wave per chunk
+    constexpr int NPT = PAIRED ? 2 : 3;         // image tiles per expert tile
+    constexpr int NP = XBF16 ? 1 : 3;           // activation parts
+    constexpr int NACC = PAIRED ? 2 : TPW;      // accumulator tiles per row tile
+    static_assert(NU * kRouteThreads == TM * UPR, "staging units");
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15;
+    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
+    const int NTS = PAIRED ? 2 : 3 * ET;
+    const int gn = w % NG, gk = w / NG;         // this wave's expert-tile group and K group
+    // K steps [s_begin, s_end) (a multiple of 8 apart unless s_end = Dp / 32)
+    const int S = s_end;
+    const int NCH = (s_end - s_begin + 7) / 8;
+    uint8_t *buf[2] = {stage, stage + TM * ROWB};
+
+    // staging: unit u = tid + 256 j is row u / UPR, 16 bytes at column unit u % UPR
+    auto load_chunk = [&](int ch, u32x4_t (&v)[NU]) {
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+        for (int j = 0; j < NU; ++j) {
+            const int u = tid + j * kRouteThreads;
+            const int row = u / UPR, cu = u - row * UPR;
+            const int k0 = s_begin * 32 + ch * kRouterKC + cu * (16 / ESZ);
+            const long long t = min(t0 + row, r.T - 1);
+            if (k0 + 16 / ESZ <= r.D && (r.D % (16 / ESZ)) == 0) {
+                v[j] = *(const u32x4_t *)((const uint8_t *)r.x + (t * r.D + k0) * ESZ);
+            } else {
+                uint32_t q[4] = {0u, 0u, 0u, 0u};
+                if (XBF16) {
+                    uint16_t h[8];
 #pragma unroll
-        for (int et = 0; et < 8; ++et) acc[ti][et] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kc0 = k_begin; kc0 < k_end; kc0 += KC) {
-        rbf16x8_t a[KC / 32][2][NP];
+                    for (int i = 0; i < 8; ++i) h[i] = (k0 + i < r.D) ? ((const uint16_t *)r.x)[t * r.D + k0 + i] : 0;
+                    __builtin_memcpy(q, h, 16);
+                } else {
+                    float f[4];
 #pragma unroll
-        for (int kq32 = 0; kq32 < KC / 32; ++kq32)
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
-                load_x8<XBF16, ALIGNED>(r.x, r.D, min(tb + ti * 16 + l16, r.T - 1), kc0 + kq32 * 32 + kq, a[kq32][ti]);
-        uint4 wv[NWP];
-#pragma unroll
-        for (int j = 0; j < NWP; ++j) {
-            const int i = min((int)threadIdx.x + j * 256, npieces - 1);
-            const int row = i / (KC / 8), c = i - row * (KC / 8);  // row = part * Ep + expert
-            const int part = row / r.Ep, e = row - part * r.Ep;
-            const int col = min(kc0 + c * 8, r.Dp - 8);              // the slice's last chunk may be short
-            wv[j] = *(const uint4 *)(r.ws + part * np + (long long)e * r.Dp + col);
+                    for (int i = 0; i < 4; ++i) f[i] = (k0 + i < r.D) ? ((const float *)r.x)[t * r.D + k0 + i] : 0.0f;
+                    __builtin_memcpy(q, f, 16);
+                }
+                v[j] = u32x4_t{q[0], q[1], q[2], q[3]};
+            }
         }
+    };
+    auto store_chunk = [&](uint8_t *b, const u32x4_t (&v)[NU]) {
 #pragma unroll
-        for (int j = 0; j < NWP; ++j) {  // clamped pieces rewrite the last piece with its own value
-            const int i = min((int)threadIdx.x + j * 256, npieces - 1);
-            const int row = i / (KC / 8), c = i - row * (KC / 8);
-            *(uint4 *)(rlds + row * RS + c * 16) = wv[j];
+        for (int j = 0; j < NU; ++j) {
+            const int u = tid + j * kRouteThreads;
+            const int row = u / UPR, cu = u - row * UPR;
+            *(u32x4_t *)(b + row * ROWB + cu * 16) = v[j];
         }
-        __syncthreads();
-        const int kn = min(KC, k_end - kc0);
+    };
+    // the x fragment (parts) of step u of a staged chunk, row tile ti
+    auto x_frag = [&](const uint8_t *b, int u, int ti, rbf16x8_t *xa) {
+        const uint8_t *row = b + (ti * 16 + l16) * ROWB;
+        if (XBF16) {
+            xa[0] = *(const rbf16x8_t *)(row + u * 64 + (lane >> 4) * 16);
+        } else {
+            const float4 f0 = *(const float4 *)(row + (u * 32 + (lane >> 4) * 8) * 4);
+            const float4 f1 = *(const float4 *)(row + (u * 32 + (lane >> 4) * 8 + 4) * 4);
+            const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+            uint16_t h0[8], h1[8], h2[8];
 #pragma unroll
-        for (int kq32 = 0; kq32 < KC / 32; ++kq32) {
-            const int kk = kq32 * 32;
+            for (int i = 0; i < 8; ++i) {
+                h0[i] = f32_to_bf16(v[i]);
+                const float r1 = v[i] - bf16_to_f32(h0[i]);
+                h1[i] = f32_to_bf16(r1);
+                h2[i] = f32_to_bf16(r1 - bf16_to_f32(h1[i]));
+            }
+            __builtin_memcpy(&xa[0], h0, 16);
+            __builtin_memcpy(&xa[1], h1, 16);
+            __builtin_memcpy(&xa[2], h2, 16);
+        }
+    };
+
+    rf32x4_t acc[RT][NACC];
 #pragma unroll
-            for (int et = 0; et < 8; ++et) {
-                if (kk < kn && et < ET) {
-                    rbf16x8_t b[3];
+    for (int ti = 0; ti < RT; ++ti)
 #pragma unroll
-                    for (int p = 0; p < 3; ++p)
-                        b[p] = *(const rbf16x8_t *)(rlds + (p * r.Ep + et * 16 + l16) * RS + (kk + kq) * 2);
+        for (int j = 0; j < NACC; ++j) acc[ti][j] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // weight fragments of a chunk for this wave (independent of LDS); with
+    // few of them (small E) the next chunk's are loaded a chunk ahead
+    constexpr bool WPF = SPW * TPW * NPT <= 16;
+    using WFrag = rbf16x8_t[SPW][TPW][NPT];
+    auto load_w = [&](int ch, WFrag &wb) {
 #pragma unroll
-                    for (int ti = 0; ti < 2; ++ti) {
-                        // x parts i times weight parts j with i + j <= 2
+        for (int i = 0; i < SPW; ++i) {
+            const int st = min(s_begin + ch * 8 + gk * SPW + i, S - 1);
 #pragma unroll
-                        for (int i = 0; i < NP; ++i)
+            for (int j = 0; j < TPW; ++j) {
+                const int et = min(gn + j * NG, ET - 1);
 #pragma unroll
-                            for (int j = 0; j + i < 3; ++j)
-                                acc[ti][et] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kq32][ti][i], b[j], acc[ti][et], 0, 0, 0);
+                for (int p = 0; p < NPT; ++p) {
+                    const int q = PAIRED ? p : et * 3 + p;
+                    wb[i][j][p] = *(const rbf16x8_t *)(r.ws + (((long long)st * NTS + q) * 64 + lane) * 8);
+                }
+            }
+        }
+    };
+    // x of chunk 0 staged; chunks 1 and 2 in flight in registers (each chunk
+    // is stored one iteration after its loads were issued)
+    u32x4_t va[NU], vb[NU];
+    load_chunk(0, va);
+    store_chunk(buf[0], va);
+    if (NCH > 1) load_chunk(1, va);
+    WFrag wn;
+    if constexpr (WPF) load_w(0, wn);
+    __syncthreads();
+    for (int ch = 0; ch < NCH; ++ch) {
+        WFrag wb;
+        if constexpr (WPF) {
+#pragma unroll
+            for (int i = 0; i < SPW; ++i)
+#pragma unroll
+                for (int j = 0; j < TPW; ++j)
+#pragma unroll
+                    for (int p = 0; p < NPT; ++p) wb[i][j][p] = wn[i][j][p];
+            if (ch + 1 < NCH) load_w(ch + 1, wn);
+        } else {
+            load_w(ch, wb);
+        }
+        if (ch + 2 < NCH) load_chunk(ch + 2, vb);
+        const uint8_t *b = buf[ch & 1];
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+            const int u = gk * SPW + i;
+            if (s_begin + ch * 8 + u >= S) break;
+#pragma unroll
+            for (int ti = 0; ti < RT; ++ti) {
+                rbf16x8_t xa[NP];
+                x_frag(b, u, ti, xa);
+                if constexpr (PAIRED) {
+                    // tile 0 (parts 0, 1): every x part; tile 1 (part 2): x part 0
+#pragma unroll
+                    for (int xi = 0; xi < NP; ++xi)
+                        acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wb[i][0][0], acc[ti][0], 0, 0, 0);
+                    acc[ti][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], wb[i][0][1], acc[ti][1], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < TPW; ++j) {
+                        if (gn + j * NG >= ET) break;
+#pragma unroll
+                        for (int p = 0; p < 3; ++p)
+#pragma unroll
+                            for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
+                                acc[ti][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wb[i][j][p], acc[ti][j],
+                                                                                     0, 0, 0);
                     }
                 }
             }
         }
+        if (ch + 1 < NCH) store_chunk(buf[(ch + 1) & 1], va);
+#pragma unroll
+        for (int j = 0; j < NU; ++j) va[j] = vb[j];
         __syncthreads();
     }
-    float *out = r.part + (long long)blockIdx.y * r.T * r.Er;
+
+    // accumulators -> LDS partials P[gk][t][col] (the staging buffers are
+    // free now), col = image column of the expert tile (paired: 16 q + c)
+    const int NCOL = PAIRED ? 32 : ET * 16;
+    float *P = (float *)stage;
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+    for (int ti = 0; ti < RT; ++ti)
 #pragma unroll
-        for (int et = 0; et < 8; ++et) {
-            const int e = et * 16 + l16;
-            if (et < ET && e < r.Er)
+        for (int j = 0; j < NACC; ++j) {
+            const int col = PAIRED ? j * 16 + l16 : (gn + j * NG) * 16 + l16;
+            if (PAIRED || gn + j * NG < ET)
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const int t = tb + ti * 16 + (lane >> 4) * 4 + rr;
-                    if (t < r.T) out[(long long)t * r.Er + e] = acc[ti][et][rr];
+                    const int t = ti * 16 + (lane >> 4) * 4 + rr;
+                    P[((long long)gk * TM + t) * NCOL + col] = acc[ti][j][rr];
                 }
         }
-}
-
-void router_plan(RouterArgs &r) {
-    // LDS chunk: three weight parts of Ep rows within 64 KB; 64, 128 or 256
-    // columns (64 for fp32 x, whose fragments take three times the registers)
-    const int fit = (65536 / (3 * r.Ep) - 16) / 2;
-    int kc = fit >= 256 ? 256 : (fit >= 128 ? 128 : 64);
-    if (!r.x_bf16) kc = 64;
-    // about 256 workgroups: K slices fill in for a small batch
-    const int blocks_t = (r.T + 127) / 128;
-    int nks = (256 + blocks_t - 1) / blocks_t;
-    nks = std::max(1, std::min(std::min(nks, kRouterMaxSlices), r.Dp / 32));
-    int ks_len = ((r.Dp + nks - 1) / nks + 31) / 32 * 32;
-    if (ks_len > kc) ks_len = (ks_len + kc - 1) / kc * kc;  // whole chunks
-    else kc = ks_len <= 64 ? 64 : (ks_len <= 128 ? 128 : 256);
-    nks = (r.Dp + ks_len - 1) / ks_len;
-    r.nks = nks;
-    r.ks_len = ks_len;
-    r.kc = kc;
-}
-
-hipError_t launch_router_mfma(const RouterArgs &r, int x_bf16, hipStream_t s) {
-    if (r.T <= 0) return hipSuccess;
-    const size_t lds = (size_t)3 * r.Ep * (r.kc * 2 + 16);
-    dim3 grid((r.T + 127) / 128, r.nks), block(256);
-    const bool al = (r.D & 31) == 0;
-#define MOE_ROUTER_CASE(XB, AL, KC)                                                     \
-    if ((x_bf16 != 0) == (XB != 0) && al == (AL != 0) && r.kc == KC) {                  \
-        hipLaunchKernelGGL((router_mfma_kernel<XB, AL, KC>), grid, block, lds, s, r);   \
-        return hipGetLastError();                                                       \
+    __syncthreads();
+    // logit (of this K range) = the K groups' partials in order (paired: per
+    // part column, the parts then added in part order), to out(t, e, value)
+    for (int q = tid; q < ntok * r.Er; q += kRouteThreads) {
+        const int t = q / r.Er, e = q - t * r.Er;
+        auto col_sum = [&](int col) {
+            float v = P[(long long)t * NCOL + col];
+#pragma unroll
+            for (int g = 1; g < KG; ++g) v = v + P[((long long)g * TM + t) * NCOL + col];
+            return v;
+        };
+        out(t, e, PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e));
     }
-    MOE_ROUTER_CASE(1, 1, 256) MOE_ROUTER_CASE(1, 1, 128) MOE_ROUTER_CASE(1, 1, 64)
-    MOE_ROUTER_CASE(1, 0, 256) MOE_ROUTER_CASE(1, 0, 128) MOE_ROUTER_CASE(1, 0, 64)
-    MOE_ROUTER_CASE(0, 1, 64) MOE_ROUTER_CASE(0, 0, 64)
-#undef MOE_ROUTER_CASE
-    return hipErrorInvalidValue;
 }
 
 // ============================================================================
-// Gating.  kRouteBlock tokens per block of kRouteThreads threads: TPT lanes
-// per token for the per-element work and the top-k, one thread per token for
-// the fp32 sum in expert order and the per-token outputs.
+// Gating.  kRouteBlock tokens per routing block of kRouteThreads threads, 8
+// lanes per token, each holding a contiguous block of the token's experts in
+// registers (gate_block).
 // ============================================================================
 
 // LDS row stride of the routing kernel for E rows: a multiple of 4 floats
 // (16 B) whose count of 16-byte units is odd, so that 16 token threads
 // reading 16 B at one column hit 16 distinct bank quads.
 __host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) | 1)); }
-
-// Fixed-order sum over the TPT consecutive lanes of a token (a butterfly: the
-// same tree on every call).
-template <int TPT, typename F>
-__device__ __forceinline__ F token_sum(F v) {
-#pragma unroll
-    for (int o = 1; o < TPT; o <<= 1) v = v + __shfl_xor(v, o);
-    return v;
-}
-template <int TPT>
-__device__ __forceinline__ float token_max(float v) {  // NaN ignored (v > m is false for NaN)
-#pragma unroll
-    for (int o = 1; o < TPT; o <<= 1) {
-        const float w = __shfl_xor(v, o);
-        if (w > v) v = w;
-    }
-    return v;
-}
 
 // The value of the partner lane in butterfly step o (1, 2, 4) of an 8-lane
 // group, by DPP: lane ^ 1, lane ^ 2 (quad permutations), then the mirrored
@@ -275,15 +367,16 @@ __device__ __forceinline__ bool topk_before(uint32_t a, int ia, uint32_t b, int 
     return a > b || (a == b && ia < ib);
 }
 
-// Top-K of row p[lo, n) by the order above, over the TPT consecutive lanes of
-// a token: lane rs keeps the best K of elements rs, rs + TPT, ... in K sorted
-// register slots, then log2(TPT) butterfly steps merge the lanes' lists (a
-// strict total order, so both partners end with the same list).  Every lane
-// of the wave must call it (rows of invalid tokens pass active = false).
-// Slots past the row's size stay empty (key 0, below every float's key).
-template <int K, int TPT>
-__device__ __forceinline__ void topk_lanes(const float *__restrict__ p, int lo, int n, int rs, bool active, int *sel,
-                                           float *val) {
+// Top-K of a token's routed probabilities held in registers: lane rs of the
+// token's 8 keeps elements base + j (j < EPL) of the row; each lane keeps the
+// best K of its elements in sorted register slots (larger isless key, then
+// the lower index), then three butterfly steps merge the lanes' lists (a
+// strict total order, so every lane ends with the same list).  Every lane of
+// the wave must call it (inactive rows pass active = false).  Slots past the
+// row's routed size stay empty (key 0, below every float's key).
+template <int K, int EPL>
+__device__ __forceinline__ void topk_reg(const float (&p)[EPL], int base, int lo, int n, bool active, int *sel,
+                                         float *val) {
     uint32_t kb[K];
     int ib[K];
     float vb[K];
@@ -302,21 +395,14 @@ __device__ __forceinline__ void topk_lanes(const float *__restrict__ p, int lo, 
         }
     };
     if (active) {
-        for (int i0 = rs; i0 < n; i0 += 4 * TPT) {
-            float v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = p[min(i0 + u * TPT, n - 1)];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + u * TPT;
-                if (i < n && i >= lo) insert(isless_key(v[u]), i, v[u]);
-            }
+        for (int j = 0; j < EPL; ++j) {
+            const int i = base + j;
+            if (i >= lo && i < n) insert(isless_key(p[j]), i, p[j]);
         }
     }
-    // a rolled loop: its body is fetched once (the kernel's once-per-block
-    // phases are bound by instruction fetch, not by their arithmetic)
 #pragma unroll 1
-    for (int o = 1; o < TPT; o <<= 1) {
+    for (int o = 1; o < 8; o <<= 1) {
         uint32_t pk[K];
         int pi[K];
         float pv[K];
@@ -336,85 +422,53 @@ __device__ __forceinline__ void topk_lanes(const float *__restrict__ p, int lo, 
     }
 }
 
-// Top-k of row p[lo, n) for n - lo <= 8 TPT by ranks: lane rs owns elements
-// lo + rs + TPT u and counts, over the row, the elements before each of them
-// in the top-k order; an element of rank r < k is slot r.  No lane exchanges
-// anything: the owner writes its winners to ksel / kval directly.
-template <int TPT>
-__device__ __forceinline__ void topk_ranks(const float *__restrict__ p, int lo, int n, int k, int rs, bool active,
-                                           int *ksel, float *kval) {
-    constexpr int U = 8;
-    if (!active) return;
-    uint64_t mine[U];  // (key, inverted index): larger is earlier in the order
-    int rank[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int i = lo + rs + TPT * u;
-        const float v = p[min(i, n - 1)];
-        mine[u] = ((uint64_t)isless_key(v) << 32) | (uint32_t)(0x7fffffff - i);
-        rank[u] = 0;
-    }
-    for (int j0 = lo; j0 < n; j0 += 4) {
-        float v[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = p[min(j0 + c, n - 1)];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int j = j0 + c;
-            const uint64_t kj = ((uint64_t)isless_key(v[c]) << 32) | (uint32_t)(0x7fffffff - j);
-#pragma unroll
-            for (int u = 0; u < U; ++u) rank[u] += (j < n && kj > mine[u]) ? 1 : 0;
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int i = lo + rs + TPT * u;
-        if (i < n && rank[u] < k) {
-            ksel[rank[u]] = i;
-            kval[rank[u]] = p[i];
-        }
-    }
+template <int EPL>
+__device__ __forceinline__ void topk_reg_k(const float (&p)[EPL], int base, int lo, int n, int k, bool active,
+                                           int *sel, float *val) {
+    // K >= k slots: the first k of the best K are the top-k
+    if (k == 1) topk_reg<1, EPL>(p, base, lo, n, active, sel, val);
+    else if (k == 2) topk_reg<2, EPL>(p, base, lo, n, active, sel, val);
+    else if (k <= 4) topk_reg<4, EPL>(p, base, lo, n, active, sel, val);
+    else topk_reg<8, EPL>(p, base, lo, n, active, sel, val);
 }
 
-template <int TPT>
-__device__ __forceinline__ void topk_lanes_k(const float *__restrict__ p, int lo, int n, int k, int rs, bool active,
-                                             int *sel, float *val) {
-    switch (k) {
-    case 1: topk_lanes<1, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 2: topk_lanes<2, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 3: topk_lanes<3, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 4: topk_lanes<4, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 5: topk_lanes<5, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 6: topk_lanes<6, TPT>(p, lo, n, rs, active, sel, val); break;
-    case 7: topk_lanes<7, TPT>(p, lo, n, rs, active, sel, val); break;
-    default: topk_lanes<8, TPT>(p, lo, n, rs, active, sel, val); break;
+// Butterfly sum / max over the 8 lanes of a token (the same tree every call).
+template <typename F>
+__device__ __forceinline__ F lanes8_sum(F v) {
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) v = v + __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float lanes8_max(float v) {  // NaN ignored (v > m is false for NaN)
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        const float w = __shfl_xor(v, o);
+        if (w > v) v = w;
     }
+    return v;
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
+// One routing block, number blk: kRouteBlock tokens, 8 lanes per token (lane
+// rs of token rt = tid / 8 holds the contiguous experts rs EPL .. +EPL of the
+// row in registers).  Logits: the token's row of lin (LDS rows, stride RW)
+// when FROM_LDS, else the sum of a.part's nks K slices in slice order plus
+// the bias, read straight from global memory (each token's 8 lanes read its
+// row contiguously).  Per token, in registers: max; exp terms e =
+// (float)exp((double)(l - m)) (NNlib's branch for m == +Inf); their fp32 sum
+// in expert order (the recipe's order: lane r adds its experts after lane
+// r - 1's running sum); probabilities e / s; the fp64 entropy terms and the
+// logsumexp; the top-k by per-lane sorted lists and a butterfly merge; the
+// gates.  Then per entry (lane rs = slot rs): its stable rank among the
+// block's entries of its expert (LDS bitmask per expert, bit = entry), and
+// the block's histogram, probability sums and loss terms.  sl: LDS rows
+// [kRouteBlock][RW] for the output probabilities (the block sums).
+template <int EPL, bool FROM_LDS>
+__device__ __forceinline__ void gate_block(const RouteArgs &a, int blk, const float *lin, int RW, float *sl) {
 #pragma clang fp contract(off)
-    // Block: kRouteBlock tokens, kRouteThreads threads.  The recipe's
-    // order-sensitive fp32 softmax sum in expert order and the per-token
-    // gates, logsumexp and entropy run one thread per token (threads <
-    // kRouteBlock, all in wave 0), reading the token's LDS row 16 B at a
-    // time; the rest runs TPT threads per token (max, exp and probability
-    // terms, the top-k by ranks or by a lane merge, the fp64 entropy sum and
-    // the z-loss exponent sum as fixed-order per-token reductions).  Rows are sized
-    // for this layer's E (dynamic LDS).  Every global output is written in the
-    // last phase: a store's data register may not be reused before the store
-    // has completed, so stores in between would stall the phases that follow.
-    constexpr int TPT = kRouteThreads / kRouteBlock;
-    static_assert(TPT == 8 && kRouteBlock * TPT == kRouteThreads, "threads per token");
-    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
     // stable ranks: bit i of emask[e][i / 32] marks entry i (token * kt + slot)
-    // of expert e + 1 in this block; ent_e holds each entry's expert
+    // of expert e + 1 in this block
     __shared__ unsigned emask[MOE_MAX_EXPERTS * MOE_MAX_TOPK];
-    __shared__ int ent_e[kRouteBlock * MOE_MAX_TOPK];
-    __shared__ int ksel[kRouteBlock][MOE_MAX_TOPK];    // top-k of each token: experts (0-based)
-    __shared__ float kval[kRouteBlock][MOE_MAX_TOPK];  // and their probabilities
-    __shared__ double red[2][kRouteBlock];
-    __shared__ float rmax[kRouteBlock], zmax[kRouteBlock], rsum[kRouteBlock], zsum[kRouteBlock];
-    __shared__ double hsum[kRouteBlock];
+    __shared__ double wred[2][kRouteThreads / 64];
     const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
     const bool soft = a.gate_kind == MOE_GATE_SOFT;
     const bool zsep = shared_gate || soft;  // z-loss from a softmax of its own (all rows, unscaled)
@@ -422,397 +476,440 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     const bool out_gating = (a.out_mask & ROUTE_OUT_GATING) != 0;
     // a gating pass on the caller's routing needs none of the softmax phases
     const bool softmax = out_probs || !a.given;
-    const int EM = max(a.Er, a.E);
-    const int RW = route_rw(EM);
-    float *lrow = (float *)rdyn;            // [kRouteBlock][RW] logits
-    float *prow = lrow + kRouteBlock * RW;  // exp terms, then probabilities (before the shared-gating scale)
-    float *srow = prow + kRouteBlock * RW;  // output probabilities (after it)
-
-    const int tid = threadIdx.x;
-    const int t0 = blockIdx.x * kRouteBlock;
-    const int t = t0 + tid;
+    const int E = a.E;                       // router rows (= a.Er)
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int rt = tid >> 3, rs = tid & 7;   // token rt of the block, lane rs of it
+    const int t0 = blk * kRouteBlock;
     const int ntok = min(kRouteBlock, a.T - t0);
-    const bool tok = tid < kRouteBlock;         // a token thread
-    const bool valid = tok && t < a.T;
-    const int ns = shared_gate ? a.ns : 0;      // rows before the routed ones
-    const int rt = tid / TPT, rs = tid - rt * TPT;  // row-parallel phases: token rt, lane rs of it
     const bool rvalid = rt < ntok;
+    const long long t = (long long)t0 + rt;
+    const int ns = shared_gate ? a.ns : 0;   // rows before the routed ones
+    const int base = rs * EPL;
 
+    __syncthreads();  // the previous routing block of this workgroup is done with the LDS
     for (int i = tid; i < MOE_MAX_EXPERTS * MOE_MAX_TOPK; i += kRouteThreads) emask[i] = 0u;
 
-    // (1) router logits: the K-slice partial sums in slice order, then the
-    // bias.  Elements q = tid + 256 u; the slices (and biases) of 4 elements
-    // are loaded, from clamped addresses, before any is summed.
+    float v[EPL], pr[EPL];  // logits; exp terms, then probabilities (before the shared-gating scale)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) { v[j] = 0.0f; pr[j] = 0.0f; }
+    float m = -INFINITY, s = 0.0f, lse = 0.0f;
+    double hs = 0.0;
     if (softmax) {
-    const int nq = ntok * a.Er;
-    const long long sstride = (long long)a.T * a.Er;
-    // elements per thread per round (block-uniform): up to 8, with the
-    // partials of 4 slices each in flight, but never more than the block has
-    constexpr int RU = 8;
-    const int nu = min(RU, (nq + kRouteThreads - 1) / kRouteThreads);
-    for (int q0 = 0; q0 < nq; q0 += RU * kRouteThreads) {
-        long long o[RU];
-        int qq[RU];
-        float v[RU];
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-            qq[u] = min(q0 + u * kRouteThreads + tid, nq - 1);
-            const int tt = qq[u] / a.Er;
-            o[u] = (long long)(t0 + tt) * a.Er + (qq[u] - tt * a.Er);
-            v[u] = 0.0f;
-        }
-        // slices in groups of 4 (clamped to the last slice): every load of a
-        // group is issued before the group's sums, which run in slice order
-        for (int sg = 0; sg < a.nks; sg += 4) {
-            float pv[RU][4];
-#pragma unroll
-            for (int u = 0; u < RU; ++u)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (u < nu) pv[u][c] = a.part[min(sg + c, a.nks - 1) * sstride + o[u]];
-#pragma unroll
-            for (int u = 0; u < RU; ++u)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (u < nu && sg + c < a.nks) v[u] = (sg + c == 0) ? pv[u][c] : v[u] + pv[u][c];
-        }
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-            const int q = q0 + u * kRouteThreads + tid;
-            if (u < nu && q < nq) {
-                const int tt = q / a.Er, i = q - tt * a.Er;
-                float w = v[u];
-                if (a.bias) w = w + a.bias[i];
-                lrow[tt * RW + i] = w;
-            }
-        }
-    }
-    __syncthreads();
-    // (2) per token: max of the routed logits and, for shared gating, of all
-    // rows (z-loss); NaN ignored.  The order does not matter: only the sign of
-    // a zero maximum could, and exp(l - m) is the same for m = +0 and -0.
-    {
-        float m = -INFINITY, mz = -INFINITY;
-        if (rvalid)
-            for (int i = rs; i < EM; i += TPT) {
-                const float v = lrow[rt * RW + i];
-                const float sv = soft ? v / a.soft_lambda : v;  // logits ./ lambda (advanced.jl:18)
-                if (i >= ns && i < a.E && sv > m) m = sv;
-                if (i < a.Er && v > mz) mz = v;
-            }
-        m = token_max<TPT>(m);
-        mz = token_max<TPT>(mz);
-        if (rvalid && rs == 0) {
-            rmax[rt] = m;
-            zmax[rt] = mz;
-        }
-    }
-    __syncthreads();
-    // (3) exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m ==
-    // +Inf); shared gating: the z-loss exponent sum over all rows
-    {
-        float zs = 0.0f;
+        // ---- logits ----
         if (rvalid) {
-            const float m = rmax[rt], mz = zmax[rt];
-            for (int i = rs; i < a.Er; i += TPT) {
-                const float v = lrow[rt * RW + i];
-                const float sv = soft ? v / a.soft_lambda : v;
-                if (i >= ns && i < a.E)
-                    prow[rt * RW + i] = (m == INFINITY) ? ((sv == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv - m));
-                if (zsep) zs = zs + (float)exp((double)(v - mz));
-            }
-        }
-        if (zsep) {
-            zs = token_sum<TPT>(zs);
-            if (rvalid && rs == 0) zsum[rt] = zs;
-        }
-    }
-    __syncthreads();
-    // (4) per token: sum in expert order
-    if (valid) {
-        const float *row = prow + tid * RW;
-        float s = 0.0f;
-        for (int i0 = ns & ~3; i0 < a.E; i0 += 8) {
-            const float4 va = *(const float4 *)(row + i0), vb = *(const float4 *)(row + i0 + 4);
-            const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+            if constexpr (FROM_LDS) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const int i = i0 + c;
-                if (i >= ns && i < a.E) s = s + vv[c];
-            }
-        }
-        rsum[tid] = s;
-    }
-    __syncthreads();
-    // (5) probabilities p = e / s; output rows (shared gating: shared rows 1/E,
-    // routed rows p scaled by 1 - ns/E in Float64); the entropy terms
-    // p log(p + 1e-8) summed in fp64 per token (a fixed order)
-    {
-        double hs = 0.0;
-        if (rvalid) {
-            const float s = rsum[rt];
-            for (int i = rs; i < a.E; i += TPT) {
-                float pv;
-                if (a.given) {
-                    // the caller's gate: its probabilities, or ones ./ E
-                    pv = a.given_probs ? a.probs[(long long)(t0 + rt) * a.E + i] : 1.0f / (float)a.E;
-                } else if (i < ns) {
-                    pv = 1.0f / (float)a.E;
-                } else {
-                    const float pu = prow[rt * RW + i] / s;
-                    prow[rt * RW + i] = pu;
-                    pv = shared_gate ? (float)((double)pu * (1.0 - (double)ns / (double)a.E)) : pu;
+                for (int j = 0; j < EPL; ++j)
+                    if (base + j < E) v[j] = lin[rt * RW + base + j];
+            } else {
+                const long long sstride = (long long)a.T * a.Er;
+                const float *row = a.part + t * a.Er + base;
+                float pv[EPL];
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) pv[j] = (base + j < E) ? row[j] : 0.0f;
+                for (int sl_ = 1; sl_ < a.nks; ++sl_) {
+                    float q[EPL];
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) q[j] = (base + j < E) ? row[sl_ * sstride + j] : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) pv[j] = pv[j] + q[j];
                 }
-                srow[rt * RW + i] = pv;
-                // p * log(p + 1e-8) with p + 1e-8 in Float64 as Julia
-                // promotes it; the log in fp32 (a statistic: the mean entropy
-                // is checked to 1e-5)
-                const double pd = (double)pv;
-                hs = hs + pd * (double)logf((float)(pd + 1e-8));
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    float w = pv[j];
+                    if (a.bias && base + j < E) w = w + a.bias[base + j];
+                    v[j] = w;
+                }
             }
         }
-        hs = token_sum<TPT>(hs);
-        if (rvalid && rs == 0) hsum[rt] = hs;
-    }
-    __syncthreads();
-    }  // softmax phases
-
-    // (6a) top-k of each token's probabilities over its TPT lanes; the shared
-    // rows of SharedExpertGating are left out (the base gate sees the routed
-    // rows only)
-    if (!a.given) {
-        if (a.E - ns <= 8 * TPT) {
-            // up to 64 routed experts: ranks (no cross-lane dependence chain)
-            topk_ranks<TPT>(prow + rt * RW, ns, a.E, a.k, rs, rvalid, ksel[rt], kval[rt]);
+        // ---- max (of the routed rows; zsep: also of all rows) ----
+        float mz = -INFINITY;
+        float sv[EPL];  // logits ./ lambda for SoftMoEGating (advanced.jl:18)
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int i = base + j;
+            sv[j] = soft ? v[j] / a.soft_lambda : v[j];
+            if (rvalid && i >= ns && i < E && sv[j] > m) m = sv[j];
+            if (rvalid && i < E && v[j] > mz) mz = v[j];
+        }
+        m = lanes8_max(m);
+        mz = lanes8_max(mz);
+        // ---- exp terms; zsep: the z-loss exponent sum over all rows ----
+        float zs = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int i = base + j;
+            if (rvalid && i >= ns && i < E)
+                pr[j] = (m == INFINITY) ? ((sv[j] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv[j] - m));
+            if (zsep && rvalid && i < E) zs = zs + (float)exp((double)(v[j] - mz));
+        }
+        if (zsep) zs = lanes8_sum(zs);
+        // ---- sum in expert order ----
+        if constexpr (EPL == 1) {
+            float ev[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) ev[r] = __shfl(pr[0], (lane & ~7) | r);
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r >= ns && r < E) s = s + ev[r];
         } else {
-            int sl[MOE_MAX_TOPK];
-            float vl[MOE_MAX_TOPK];
-            topk_lanes_k<TPT>(prow + rt * RW, ns, a.E, a.k, rs, rvalid, sl, vl);
-            if (rvalid && rs == 0) {
 #pragma unroll
-                for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                    if (q < a.k) {
-                        ksel[rt][q] = sl[q];
-                        kval[rt][q] = vl[q];
+            for (int r = 0; r < 8; ++r) {
+                float c = s;
+                if (rs == r) {
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) {
+                        const int i = r * EPL + j;
+                        if (i >= ns && i < E) c = c + pr[j];
                     }
+                }
+                s = __shfl(c, (lane & ~7) | r);
             }
         }
-    }
-    __syncthreads();
-
-    int ex[MOE_MAX_TOPK];     // 1-based expert ids of this token's slots
-    float gx[MOE_MAX_TOPK];   // their gates
-    double zterm = 0.0, hterm = 0.0;
+        // ---- probabilities (outputs: shared gating's shared rows 1/E, routed
+        // rows p scaled by 1 - ns/E in Float64; the caller's gate: its
+        // probabilities or ones ./ E); entropy terms p log(p + 1e-8) with
+        // p + 1e-8 in Float64 as Julia promotes it, the log in fp32 (a
+        // statistic: the mean entropy is checked to 1e-5) ----
 #pragma unroll
-    for (int j = 0; j < MOE_MAX_TOPK; ++j) {
-        ex[j] = 0;
-        gx[j] = 0.0f;
-    }
-
-    // (6) per token: top-k and gates, logsumexp, entropy
-    if (valid && a.given) {
-        // the caller's routing: ids outside 1..E are skipped, as the
-        // dispatch's `expert_id > 0 && expert_id <= length(experts)` does
-        // (src/core/moe_layer.jl:198)
-#pragma unroll
-        for (int j = 0; j < MOE_MAX_TOPK; ++j)
-            if (j < a.kt) {
-                const long long ent = (long long)t * a.kt + j;
-                const int e = a.idx[ent];
-                ex[j] = (e >= 1 && e <= a.Eh) ? e : 0;
-                gx[j] = a.gates[ent];
+        for (int j = 0; j < EPL; ++j) {
+            const int i = base + j;
+            if (!rvalid || i >= E) continue;
+            float pv;
+            if (a.given) {
+                pv = a.given_probs ? a.probs[t * E + i] : 1.0f / (float)E;
+            } else if (i < ns) {
+                pv = 1.0f / (float)E;
+            } else {
+                pr[j] = pr[j] / s;
+                pv = shared_gate ? (float)((double)pr[j] * (1.0 - (double)ns / (double)E)) : pr[j];
             }
-        if (softmax) {
-            const float lse = zsep ? zmax[tid] + logf(zsum[tid])
-                                   : rmax[tid] + logf(rsum[tid]);
-            zterm = (double)(lse * lse);
-            hterm = -hsum[tid];
+            sl[rt * RW + i] = pv;
+            const double pd = (double)pv;
+            hs = hs + pd * (double)logf((float)(pd + 1e-8));
         }
-    } else if (valid) {
-        float *p = prow + tid * RW;
+        hs = lanes8_sum(hs);
+        // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
+        // the log in Float32 as Julia takes it of the Float32 sum
+        lse = zsep ? mz + logf(zs) : m + logf(s);
+        if (out_probs && rvalid) {
+#pragma unroll
+            for (int j = 0; j < EPL; ++j)
+                if (base + j < E) {
+                    a.logits[t * E + base + j] = v[j];
+                    a.probs[t * E + base + j] = sl[rt * RW + base + j];
+                }
+        }
+    }
+
+    // ---- top-k and gates; the entries' experts (slot rs of the token) ----
+    int my_e = 0;     // 1-based expert of entry (rt, rs), 0: none
+    float my_g = 0.0f;
+    if (!a.given) {
         int sel[MOE_MAX_TOPK];
-        float g[MOE_MAX_TOPK];
-        {
-            // the winners in slot order; gates: p of the slots over their sum
-            // in slot order
-            float v[MOE_MAX_TOPK];
+        float val[MOE_MAX_TOPK];
 #pragma unroll
-            for (int q = 0; q < MOE_MAX_TOPK; ++q) {
-                sel[q] = (q < a.k) ? ksel[tid][q] : 0;
-                v[q] = (q < a.k) ? kval[tid][q] : 0.0f;
-            }
-            float sg = v[0];
+        for (int q = 0; q < MOE_MAX_TOPK; ++q) { sel[q] = 0; val[q] = 0.0f; }
+        topk_reg_k<EPL>(pr, base, ns, E, a.k, rvalid, sel, val);
+        // gates: p of the slots over their sum in slot order
+        float sg = val[0];
 #pragma unroll
-            for (int q = 1; q < MOE_MAX_TOPK; ++q)
-                if (q < a.k) sg = sg + v[q];
-#pragma unroll
-            for (int q = 0; q < MOE_MAX_TOPK; ++q) g[q] = v[q] / sg;
-        }
+        for (int q = 1; q < MOE_MAX_TOPK; ++q)
+            if (q < a.k) sg = sg + val[q];
+        // the slot this lane reports: rs (slots 0 .. kt-1)
+        const int j = rs;
         if (soft) {
             // SoftMoEGating: top-k of the scaled-softmax probabilities; the
             // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
             // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
+            float pj = 0.0f;
+            const int src = (lane & ~7) | (j / EPL);  // the lane holding expert j (j < 8)
 #pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j < a.k) {
-                    ex[j] = sel[j] + 1;
-                    gx[j] = p[j];
-                }
-            const float lse = zmax[tid] + logf(zsum[tid]);
-            zterm = (double)(lse * lse);
+            for (int u = 0; u < EPL; ++u) {
+                const float w = __shfl(pr[u], src);
+                if (u == j % EPL) pj = w;
+            }
+            if (j < a.k) {
+#pragma unroll
+                for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                    if (q == j) my_e = sel[q] + 1;
+                my_g = pj;
+            }
         } else if (shared_gate) {
-            // top-k and gates on the routed probabilities as the base gate
-            // returns them (before the 1 - ns/E scaling)
-            const double gscale = 1.0 - (double)ns / (double)a.kt;
-            const float gshared = 1.0f / (float)a.kt;
+            // shared slots 0 .. ns-1 (gate 1/kt), then the routed top-k with
+            // gates scaled by 1 - ns/kt in Float64 (advanced.jl:80-108)
+            if (j < ns) {
+                my_e = j + 1;
+                my_g = 1.0f / (float)a.kt;
+            } else if (j < ns + a.k) {
+                const double gscale = 1.0 - (double)ns / (double)a.kt;
 #pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j) {
-                if (j < ns) {
-                    ex[j] = j + 1;
-                    gx[j] = gshared;
-                }
-                if (j < a.k) {
-                    // slot ns + j (ns + k <= MOE_MAX_TOPK)
-#pragma unroll
-                    for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                        if (q == ns + j) {
-                            ex[q] = sel[j] + 1;
-                            gx[q] = (float)((double)g[j] * gscale);
-                        }
-                }
+                for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                    if (q == j - ns) {
+                        my_e = sel[q] + 1;
+                        my_g = (float)((double)(val[q] / sg) * gscale);
+                    }
             }
-            const float lse = zmax[tid] + logf(zsum[tid]);
-            zterm = (double)(lse * lse);
-        } else {
-            if (a.lsh == 0) {
+        } else if (a.lsh > 0) {
+            // forward_with_shared_experts: shared experts 1..lsh in slots
+            // 0..lsh-1 (their outputs are averaged, the gate is only
+            // reported), then the routed ids shifted by lsh (expert_indices
+            // .+= num_shared_experts, src/core/moe_layer.jl:172)
+            if (j < a.lsh) {
+                my_e = j + 1;
+                my_g = 1.0f / (float)a.lsh;
+            } else if (j < a.lsh + a.k) {
 #pragma unroll
-                for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                    if (j < a.k) {
-                        ex[j] = sel[j] + 1;
-                        gx[j] = g[j];
+                for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                    if (q == j - a.lsh) {
+                        my_e = sel[q] + 1 + a.lsh;
+                        my_g = val[q] / sg;
                     }
-            } else {
-                // forward_with_shared_experts: shared experts 1..lsh in slots
-                // 0..lsh-1 (their outputs are averaged, the gate is only
-                // reported), then the routed ids shifted by lsh (expert_indices
-                // .+= num_shared_experts, src/core/moe_layer.jl:172)
-                const float gsh = 1.0f / (float)a.lsh;
-#pragma unroll
-                for (int j = 0; j < MOE_MAX_TOPK; ++j) {
-                    if (j < a.lsh) {
-                        ex[j] = j + 1;
-                        gx[j] = gsh;
-                    }
-                    if (j < a.k) {
-#pragma unroll
-                        for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                            if (q == a.lsh + j) {
-                                ex[q] = sel[j] + 1 + a.lsh;
-                                gx[q] = g[j];
-                            }
-                    }
-                }
             }
-            // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
-            // the log in Float32 as Julia takes it of the Float32 sum
-            const float lse = rmax[tid] + logf(rsum[tid]);
-            zterm = (double)(lse * lse);
+        } else if (j < a.k) {
+#pragma unroll
+            for (int q = 0; q < MOE_MAX_TOPK; ++q)
+                if (q == j) {
+                    my_e = sel[q] + 1;
+                    my_g = val[q] / sg;
+                }
         }
-        hterm = -hsum[tid];  // entropy of update_stats!, Float64
+        if (!rvalid) my_e = 0;
+    } else if (rvalid && rs < a.kt) {
+        // the caller's routing: ids outside 1..E are skipped, as the
+        // dispatch's `expert_id > 0 && expert_id <= length(experts)` does
+        // (src/core/moe_layer.jl:198)
+        const long long ent = t * a.kt + rs;
+        const int e = a.idx[ent];
+        my_e = (e >= 1 && e <= a.Eh) ? e : 0;
+        my_g = a.gates[ent];
     }
-    __syncthreads();
 
     // ---- stable rank of each entry among the block's entries of its expert ----
-    // (entries in token-then-slot order, as the bucket loop visits them; a
-    // gating pass only: kt <= MOE_MAX_TOPK there)
-    int my_e = 0, my_r = 0;
-    if (out_gating) {
-        const int nent = kRouteBlock * a.kt;
-        if (tok) {
+    // (entries in token-then-slot order, as the bucket loop visits them)
+    const int ent = rt * a.kt + rs;  // entry of this lane (rs < kt)
+    const bool has_ent = out_gating && rs < a.kt && my_e > 0;
+    __syncthreads();  // emask cleared
+    if (has_ent) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (ent >> 5)], 1u << (ent & 31));
+    // block sums of the per-token loss terms (tokens rt: lane rs == 0), in a
+    // fixed order: within a wave by a butterfly over its 8 tokens, then the
+    // waves in order
+    double zterm = 0.0, hterm = 0.0;
+    if (softmax && rvalid && rs == 0) {
+        zterm = (double)(lse * lse);
+        hterm = -hs;
+    }
 #pragma unroll
-            for (int j = 0; j < MOE_MAX_TOPK; ++j)
-                if (j < a.kt) ent_e[tid * a.kt + j] = ex[j];
-        }
-        __syncthreads();
-        if (tid < nent) {
-            my_e = ent_e[tid];
-            if (my_e > 0) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (tid >> 5)], 1u << (tid & 31));
-        }
-        __syncthreads();
-        if (tid < nent && my_e > 0) {
-            const unsigned *m = &emask[(my_e - 1) * MOE_MAX_TOPK];
-            int rr = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
-            for (int w = 0; w < (tid >> 5); ++w) rr += __popc(m[w]);
-            my_r = rr;
-        }
+    for (int o = 8; o < 64; o <<= 1) {
+        zterm = zterm + __shfl_xor(zterm, o);
+        hterm = hterm + __shfl_xor(hterm, o);
     }
-    if (tok) {
-        red[0][tid] = zterm;
-        red[1][tid] = hterm;
+    if (lane == 0) {
+        wred[0][wv] = zterm;
+        wred[1][wv] = hterm;
     }
-    __syncthreads();
-    for (int st = kRouteBlock / 2; st > 0; st >>= 1) {
-        if (tid < st) {
-            red[0][tid] += red[0][tid + st];
-            red[1][tid] += red[1][tid + st];
-        }
-        __syncthreads();
+    __syncthreads();  // emask complete, wred and the probability rows written
+    if (has_ent && rvalid) {
+        const unsigned *mk = &emask[(my_e - 1) * MOE_MAX_TOPK];
+        int rr = __popc(mk[ent >> 5] & ((1u << (ent & 31)) - 1u));
+        for (int w = 0; w < (ent >> 5); ++w) rr += __popc(mk[w]);
+        a.rank[t * a.kt + rs] = rr;
     }
-
-    // ---- outputs --------------------------------------------------------------
-    if (out_probs) {
-        for (int q = tid; q < ntok * a.Er; q += kRouteThreads) {
-            const int tt = q / a.Er, i = q - tt * a.Er;
-            a.logits[(long long)(t0 + tt) * a.Er + i] = lrow[tt * RW + i];
-        }
-        for (int q = tid; q < ntok * a.E; q += kRouteThreads) {
-            const int tt = q / a.E, i = q - tt * a.E;
-            a.probs[(long long)(t0 + tt) * a.E + i] = srow[tt * RW + i];
-        }
+    if (out_gating && rvalid && rs < a.kt) {
+        a.idx[t * a.kt + rs] = my_e;
+        a.gates[t * a.kt + rs] = my_g;
     }
-    if (valid && out_gating) {
-#pragma unroll
-        for (int j = 0; j < MOE_MAX_TOPK; ++j) {
-            if (j < a.kt) {
-                const long long ent = (long long)t * a.kt + j;
-                a.idx[ent] = ex[j];
-                a.gates[ent] = gx[j];
-            }
-        }
-    }
-    if (out_gating && tid < ntok * a.kt) a.rank[(long long)t0 * a.kt + tid] = my_r;
-    const int nb = blockIdx.x;
     for (int e = tid; e < a.Eh; e += kRouteThreads) {
         if (out_gating) {
             int c = 0;
 #pragma unroll
             for (int w = 0; w < MOE_MAX_TOPK; ++w) c += __popc(emask[e * MOE_MAX_TOPK + w]);
-            a.blk_counts[(long long)nb * a.Eh + e] = c;
+            a.blk_counts[(long long)blk * a.Eh + e] = c;
         }
         if (out_probs) {
             // per-row probability sums (Switch loss P_e) in fp64, token order
             double ps = 0.0;
-            if (e < a.E) {
+            if (e < E) {
 #pragma unroll 8
-                for (int i = 0; i < ntok; ++i) ps += (double)srow[i * RW + e];
+                for (int i = 0; i < ntok; ++i) ps += (double)sl[i * RW + e];
             }
-            a.blk_stats[(long long)nb * (a.Eh + 2) + e] = ps;
+            a.blk_stats[(long long)blk * (a.Eh + 2) + e] = ps;
         }
     }
     if (tid == 0 && out_probs) {
-        a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh] = red[0][0];
-        a.blk_stats[(long long)nb * (a.Eh + 2) + a.Eh + 1] = red[1][0];
+        double zb = 0.0, hb = 0.0;
+#pragma unroll
+        for (int w = 0; w < kRouteThreads / 64; ++w) {
+            zb += wred[0][w];
+            hb += wred[1][w];
+        }
+        a.blk_stats[(long long)blk * (a.Eh + 2) + a.Eh] = zb;
+        a.blk_stats[(long long)blk * (a.Eh + 2) + a.Eh + 1] = hb;
     }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
+    const int RW = route_rw(a.E);
+    gate_block<EPL, false>(a, blockIdx.x, nullptr, RW, (float *)rdyn);
+}
+
+// The router's MFMA logits GEMM and the gating of route_kernel in one
+// launch: a workgroup computes the logits of TM = 32 or 64 tokens over all of
+// K into LDS, then gates them as TM / 32 routing blocks (no partial sums
+// through HBM).  Dynamic LDS: the logit rows of the TM tokens, then one
+// routing block's probability rows, which the x staging of the logits phase
+// shares.
+template <int XBF16, int TM, int PAIRED, int NG, int TPW, int EPL>
+__global__ __launch_bounds__(kRouteThreads) void router_fused_kernel(RouteArgs a, RouterArgs r) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
+    const int RW = route_rw(a.E);
+    float *lrows = (float *)rdyn;
+    float *srow = lrows + TM * RW;
+    const int t0 = blockIdx.x * TM;
+    const float *bias = a.bias;
+    fused_logits<XBF16, TM, PAIRED, NG, TPW>(r, t0, min(TM, a.T - t0), 0, r.Dp / 32, (uint8_t *)srow,
+                                            [&](int t, int e, float v) {
+                                                if (bias) v = v + bias[e];
+                                                lrows[t * RW + e] = v;
+                                            });
+    constexpr int NSUB = TM / kRouteBlock;
+#pragma unroll 1
+    for (int sb = 0; sb < NSUB; ++sb) {
+        const int blk = blockIdx.x * NSUB + sb;
+        if (blk * kRouteBlock >= a.T) break;  // uniform over the workgroup
+        gate_block<EPL, true>(a, blk, lrows + sb * kRouteBlock * RW, RW, srow);
+    }
+}
+
+// The router's logits GEMM on its own: workgroup (token tile, K slice)
+// computes the partial logits of TM tokens over K steps [z S8, (z + 1) S8)
+// (S8 = r.kslice steps) into part[z][T][Er]; the routing kernel adds the
+// slices in slice order and the bias.  K slices spread a small batch over
+// every CU, and keep the x tile each workgroup streams small.
+template <int XBF16, int TM, int PAIRED, int NG, int TPW>
+__global__ __launch_bounds__(kRouteThreads) void router_logits_kernel(RouterArgs r, float *part) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
+    const int t0 = blockIdx.x * TM;
+    const int z = blockIdx.y;
+    const int S = r.Dp / 32;
+    const int sb = z * r.kslice, se = min(S, sb + r.kslice);
+    float *dst = part + (long long)z * r.T * r.Er + (long long)t0 * r.Er;
+    fused_logits<XBF16, TM, PAIRED, NG, TPW>(r, t0, min(TM, r.T - t0), sb, se, rdyn,
+                                            [&](int t, int e, float v) { dst[(long long)t * r.Er + e] = v; });
+}
+
+static size_t route_lds_bytes(const RouteArgs &a) {
+    // the probability rows of one routing block
+    return (size_t)kRouteBlock * sizeof(float) * route_rw(a.E);
+}
+
+// experts per lane of a token's 8 (the gating body's register blocks)
+static int route_epl(int E) { return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : 16))); }
+
+template <int XBF16, int TM, int PAIRED, int NG, int TPW, int EPL>
+static hipError_t launch_fused_case(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
+    const int RW = route_rw(a.E);
+    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
+    const size_t stage = std::max<size_t>((size_t)2 * TM * router_stage_row_bytes<XBF16, TM>(),
+                                          sizeof(float) * (size_t)(4 / NG) * TM * (PAIRED ? 32 : ET * 16));
+    const size_t lds = sizeof(float) * (size_t)TM * RW + std::max<size_t>(sizeof(float) * kRouteBlock * RW, stage);
+    if (lds > 150 * 1024) return hipErrorInvalidValue;
+    auto kern = router_fused_kernel<XBF16, TM, PAIRED, NG, TPW, EPL>;
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, dim3((a.T + TM - 1) / TM), dim3(kRouteThreads), lds, s, a, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_fused(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
+    if (a.T <= 0) return hipSuccess;
+    if (r.Er < 1 || r.Er > MOE_MAX_EXPERTS || r.Er != a.Er || a.E != a.Er || r.Dp % 32 != 0 || r.Dp < r.D ||
+        ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK))
+        return hipErrorInvalidValue;
+    const int ET = (r.Er + 15) / 16;
+    // 64-token workgroups for bf16 x when that still gives at least 256 of them
+    const bool tm64 = r.x_bf16 && a.T >= 64 * 256;
+    // expert tiles -> (paired, waves along N, tiles per wave) and the gating's
+    // experts per lane: E <= 8 | <= 16 | <= 32 (ET 2) | <= 48 / 64 (ET 3, 4) | more
+#define MOE_FUSED(XB, TM_, P, NG_, TPW_, EPL_) return launch_fused_case<XB, TM_, P, NG_, TPW_, EPL_>(a, r, s)
+#define MOE_FUSED_TILES(XB, TM_)                                  \
+    if (r.Er <= 8) MOE_FUSED(XB, TM_, 1, 1, 1, 1);                \
+    if (ET == 1) MOE_FUSED(XB, TM_, 0, 1, 1, 2);                  \
+    if (ET == 2) MOE_FUSED(XB, TM_, 0, 2, 1, 4);                  \
+    if (ET == 3) MOE_FUSED(XB, TM_, 0, 2, 2, 8);                  \
+    if (ET == 4) MOE_FUSED(XB, TM_, 0, 4, 1, 8);                  \
+    MOE_FUSED(XB, TM_, 0, 4, 2, 16);
+    if (!r.x_bf16) { MOE_FUSED_TILES(0, 32) }
+    if (tm64) { MOE_FUSED_TILES(1, 64) }
+    MOE_FUSED_TILES(1, 32)
+#undef MOE_FUSED_TILES
+#undef MOE_FUSED
+}
+
+template <int XBF16, int TM, int PAIRED, int NG, int TPW>
+static hipError_t launch_logits_case(const RouterArgs &r, float *part, int nks, hipStream_t s) {
+    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
+    const size_t lds = std::max<size_t>((size_t)2 * TM * router_stage_row_bytes<XBF16, TM>(),
+                                        sizeof(float) * (size_t)(4 / NG) * TM * (PAIRED ? 32 : ET * 16));
+    if (lds > 150 * 1024) return hipErrorInvalidValue;
+    auto kern = router_logits_kernel<XBF16, TM, PAIRED, NG, TPW>;
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, dim3((r.T + TM - 1) / TM, nks), dim3(kRouteThreads), lds, s, r, part);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_logits(RouterArgs r, float *part, int max_slices, int *nks, hipStream_t s) {
+    *nks = 1;
+    if (r.T <= 0) return hipSuccess;
+    if (r.Er < 1 || r.Er > MOE_MAX_EXPERTS || r.Dp % 32 != 0 || r.Dp < r.D || max_slices < 1)
+        return hipErrorInvalidValue;
+    const int ET = (r.Er + 15) / 16;
+    const bool tm64 = r.x_bf16 != 0;  // 64-token tiles for bf16 x (fp32 x: 32, its staging is twice as wide)
+    const int TM = tm64 ? 64 : 32;
+    const int tiles = (r.T + TM - 1) / TM;
+    // K slices of whole 8-step chunks so that tiles x slices reaches 256 workgroups
+    const int S = r.Dp / 32, chunks = (S + 7) / 8;
+    int want = std::max(1, std::min(std::min(max_slices, chunks), (256 + tiles - 1) / tiles));
+    const int per = (chunks + want - 1) / want;
+    r.kslice = per * 8;
+    const int n = (S + r.kslice - 1) / r.kslice;
+    *nks = n;
+#define MOE_LOGITS(XB, TM_, P, NG_, TPW_) return launch_logits_case<XB, TM_, P, NG_, TPW_>(r, part, n, s)
+#define MOE_LOGITS_TILES(XB, TM_)                                   \
+    if (r.Er <= 8) MOE_LOGITS(XB, TM_, 1, 1, 1);                    \
+    if (ET == 1) MOE_LOGITS(XB, TM_, 0, 1, 1);                      \
+    if (ET == 2) MOE_LOGITS(XB, TM_, 0, 2, 1);                      \
+    if (ET == 3) MOE_LOGITS(XB, TM_, 0, 2, 2);                      \
+    if (ET == 4) MOE_LOGITS(XB, TM_, 0, 4, 1);                      \
+    MOE_LOGITS(XB, TM_, 0, 4, 2);
+    if (tm64) { MOE_LOGITS_TILES(1, 64) }
+    MOE_LOGITS_TILES(0, 32)
+#undef MOE_LOGITS_TILES
+#undef MOE_LOGITS
 }
 
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
+    if (a.E != a.Er || a.E < 1 || a.E > MOE_MAX_EXPERTS || ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK))
+        return hipErrorInvalidValue;
     const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
-    // three rows of route_rw(E) floats per token: 50.7 KB at E = MOE_MAX_EXPERTS,
-    // within the 64 KB of dynamic LDS a launch gets without an attribute
-    const size_t lds = (size_t)kRouteBlock * sizeof(float) * route_rw(std::max(a.Er, a.E)) * 3;
-    if (lds > 65536) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(route_kernel, dim3(nblk), dim3(kRouteThreads), lds, s, a);
+    const size_t lds = route_lds_bytes(a);
+    switch (route_epl(a.E)) {
+    case 1: hipLaunchKernelGGL(route_kernel<1>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    case 2: hipLaunchKernelGGL(route_kernel<2>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    case 4: hipLaunchKernelGGL(route_kernel<4>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    case 8: hipLaunchKernelGGL(route_kernel<8>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    default: hipLaunchKernelGGL(route_kernel<16>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    }
     return hipGetLastError();
 }
 
@@ -975,8 +1072,11 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
 constexpr int kScanCols = 8;
 constexpr int kScanChunks = 32;
 
-__global__ __launch_bounds__(kScanCols * kScanChunks) void scan_columns_kernel(ScanArgs a) {
+__device__ __forceinline__ void scan_finish_block(const ScanArgs &a);
+
+__global__ __launch_bounds__(kScanCols * kScanChunks) void scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
+    static_assert(kScanCols * kScanChunks == 256, "the finish phase runs on 256 threads");
     __shared__ int csum[kScanChunks][kScanCols];
     __shared__ double ssum[kScanChunks][kScanCols];
     const int NC = a.E + 2;
@@ -1033,12 +1133,26 @@ __global__ __launch_bounds__(kScanCols * kScanChunks) void scan_columns_kernel(S
         if (cnt_col) a.tot_counts[c] = tc;
         a.tot_stats[c] = ts;
     }
+    // The block that finishes last runs the finish phase on all the column
+    // totals: every block publishes its totals (release fence), then takes a
+    // ticket; the last ticket's block acquires them and resets the ticket for
+    // the next launch (which stream order puts after this one).
+    __shared__ bool last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (threadIdx.x == 0) *a.ticket = 0u;
+    scan_finish_block(a);
 }
 
-// Scan, part 2: one block.  Capacity clamp, offsets, per-expert GEMM tile
-// starts and the (expert, m0) tile list, the Switch and z losses, the mean
-// entropy and the AuxiliaryFreeLoss step, from the column totals.
-__global__ __launch_bounds__(256) void scan_finish_kernel(ScanArgs a) {
+// Scan, part 2: one block (the last of part 1).  Capacity clamp, offsets,
+// per-expert GEMM tile starts and the (expert, m0) tile list, the Switch and
+// z losses, the mean entropy and the AuxiliaryFreeLoss step, from the column
+// totals.
+__device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
 #pragma clang fp contract(off)
     __shared__ int cnt[MOE_MAX_EXPERTS];
     __shared__ int off[MOE_MAX_EXPERTS + 1];
@@ -1155,10 +1269,9 @@ __global__ __launch_bounds__(256) void scan_finish_kernel(ScanArgs a) {
 }
 
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
+    if (!a.ticket || a.E > MOE_MAX_EXPERTS) return hipErrorInvalidValue;
     const int NC = a.E + 2;
-    hipLaunchKernelGGL(scan_columns_kernel, dim3((NC + kScanCols - 1) / kScanCols), dim3(kScanCols * kScanChunks), 0, s,
-                       a);
-    hipLaunchKernelGGL(scan_finish_kernel, dim3(1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(scan_kernel, dim3((NC + kScanCols - 1) / kScanCols), dim3(kScanCols * kScanChunks), 0, s, a);
     return hipGetLastError();
 }
 
