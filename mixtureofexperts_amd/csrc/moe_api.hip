@@ -71,7 +71,10 @@ struct moe_handle {
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
-    float *logits_part = nullptr;  // [kRouterMaxSlices][T][Er] K-slice partial logits (slot 0: the caller's logits)
+    float *logits_in = nullptr;    // [T][Er] the caller's logits (routing from logits)
+    int rb = kRtMinBlock;          // tokens per route block of the last routing call (rows of rank_base)
+    int ldc = 0, lds = 0;          // row strides of blk_counts / rank_base and blk_stats (E, E + 2 rounded up to 4)
+    bool keep_rows = false;        // the next routing call writes logits / probs to global memory
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
     double *blk_stats = nullptr;
     int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
@@ -539,7 +542,7 @@ static bool drop_active(const moe_handle *h) { return h->cfg.drop_tokens && h->l
 static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
     PermuteArgs pa{};
     pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kc; pa.E = h->E;
-    pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base;
+    pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base; pa.rb = h->rb; pa.ldc = h->ldc;
     pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && drop_active(h)) ? 1 : 0;
     pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
     pa.tiled = h->bf16_gemm ? 1 : 0; pa.bm = h->bm; pa.ktt = h->D_pad / 32; pa.tile_start = h->tile_start;
@@ -561,46 +564,26 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         ++h->aux_counter;
         aux_update = h->aux_counter % h->aux_update_freq == 0;
     }
-    RouteArgs ra{};
-    RouterArgs rg{};
+    RtArgs A{};
+    RouteArgs &ra = A.r;
     if (compute_logits) {
-        // the first route pass computes the logits (router_fused_kernel)
+        RouterArgs &rg = A.g;
         rg.x = x_dev; rg.x_bf16 = x_bf16; rg.T = T; rg.D = h->D; rg.Er = h->Er; rg.Ep = h->Ep16; rg.Dp = h->Dp32;
         rg.ws = h->wsplit;
         ra.bias = h->has_bias ? h->br : nullptr;
     } else {
+        ra.part = h->logits_in;  // the caller's logits
         ra.bias = nullptr;
     }
-    ra.part = h->logits_part;  // K-slice partial logits, or the caller's logits (slot 0)
-    ra.nks = 1;
-    if (compute_logits) HIP_TRY(h, launch_router_logits(rg, h->logits_part, kRouterMaxSlices, &ra.nks, s));
     ra.logits = h->logits; ra.T = T; ra.Er = h->Er; ra.E = h->Er; ra.Eh = h->E;
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
-    auto first_pass = [&](const RouteArgs &a) { return launch_route(a, s); };
-    if (aux) {
-        ra.out_mask = ROUTE_OUT_PROBS;
-        HIP_TRY(h, first_pass(ra));
-        ra.part = h->logits;  // the logits just written, plus the loss's bias
-        ra.bias = h->aux_bias;
-        ra.out_mask = ROUTE_OUT_GATING;
-        HIP_TRY(h, launch_route(ra, s));
-    } else if (ec) {
-        // softmax pass; the experts' choices give the slots, the stable ranks
-        // and the per-block histogram
-        ra.out_mask = ROUTE_OUT_PROBS;
-        HIP_TRY(h, first_pass(ra));
-        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
-                                        h->rank, h->blk_counts, s));
-    } else {
-        ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
-        HIP_TRY(h, first_pass(ra));
-    }
+    ra.ldc = h->ldc; ra.lds = h->lds;
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
-    sa.nblk = (T + kRouteBlock - 1) / kRouteBlock; sa.T = T; sa.E = h->E; sa.kt = h->kc;
+    sa.ldc = h->ldc; sa.lds = h->lds; sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
     sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
@@ -611,7 +594,33 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.aux_cw = h->aux_cw; sa.aux_lr = h->aux_lr; sa.aux_momentum = h->aux_momentum;
     sa.aux_bias = h->aux_bias; sa.aux_mom = h->aux_mom;
     sa.tot_counts = h->tot_counts; sa.tot_stats = h->tot_stats; sa.ticket = h->scan_ticket;
-    HIP_TRY(h, launch_scan(sa, s));
+    // logits / probs rows in global memory: for the caller, and for the
+    // ExpertChoiceGating kernels that read them
+    A.store_rows = (h->keep_rows || ec || !compute_logits) ? 1 : 0;
+    h->keep_rows = false;
+    if (aux) {
+        // probabilities pass on the logits, gating pass on logits + the loss's bias
+        A.npass = 2;
+        A.aux_bias = h->aux_bias;
+        ra.out_mask = ROUTE_OUT_PROBS | ROUTE_OUT_GATING;
+    } else {
+        A.npass = 1;
+        ra.out_mask = ec ? ROUTE_OUT_PROBS : (ROUTE_OUT_PROBS | ROUTE_OUT_GATING);
+    }
+    // the router kernel's last workgroup runs the scan, except for
+    // ExpertChoiceGating, whose slots come from its own kernels; their rank
+    // kernel works on route blocks of kRouteBlock tokens
+    A.tail = ec ? 0 : 1;
+    A.s = sa;
+    HIP_TRY(h, launch_router(A, ec ? kRouteBlock : 0, &h->rb, s));
+    if (ec) {
+        // the experts' choices give the slots, the stable ranks and the
+        // per-block histogram, then the scan
+        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
+                                        h->rank, h->blk_counts, h->ldc, s));
+        sa.nblk = (T + h->rb - 1) / h->rb;
+        HIP_TRY(h, launch_scan(sa, s));
+    }
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
 }
@@ -840,7 +849,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
         A((void **)&h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     }
     h->T_max = cfg->max_tokens;
-    h->nblk_max = (h->T_max + kRouteBlock - 1) / kRouteBlock;
+    h->nblk_max = (h->T_max + kRtMinBlock - 1) / kRtMinBlock;
     h->ent_max = (long long)h->T_max * h->kt;
     h->rows_max = h->T_max * h->kt;
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) {
@@ -864,16 +873,18 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     }
     const size_t T = (size_t)h->T_max, E = (size_t)h->E, nent = (size_t)h->ent_max;
     A((void **)&h->logits, sizeof(float) * T * h->Er);
-    A((void **)&h->logits_part, sizeof(float) * kRouterMaxSlices * T * h->Er);
+    A((void **)&h->logits_in, sizeof(float) * T * h->Er);
     A((void **)&h->probs, sizeof(float) * T * h->Er);
     A((void **)&h->idx, sizeof(int) * nent);
     A((void **)&h->gates, sizeof(float) * nent);
     A((void **)&h->rank, sizeof(int) * nent);
-    A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * E);
-    A((void **)&h->blk_stats, sizeof(double) * (size_t)h->nblk_max * (E + 2));
+    h->ldc = (int)((E + 3) / 4 * 4);
+    h->lds = (int)((E + 2 + 3) / 4 * 4);
+    A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * h->ldc);
+    A((void **)&h->blk_stats, sizeof(double) * (size_t)h->nblk_max * h->lds);
     A((void **)&h->counts, sizeof(int) * E);
     A((void **)&h->offsets, sizeof(int) * (E + 1));
-    A((void **)&h->rank_base, sizeof(int) * (size_t)h->nblk_max * E);
+    A((void **)&h->rank_base, sizeof(int) * (size_t)h->nblk_max * h->ldc);
     A((void **)&h->cap, sizeof(int));
     A((void **)&h->tiles, sizeof(int2) * (size_t)h->max_tiles);
     A((void **)&h->num_tiles, sizeof(int));
@@ -1227,7 +1238,7 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
     if (r != MOE_OK) return r;
     r = join_stream(h, s);
     if (r != MOE_OK) return r;
-    HIP_TRY(h, hipMemcpyAsync(h->logits_part, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->logits_in, logits, sizeof(float) * (size_t)T * h->Er, hipMemcpyHostToDevice, s));
     r = run_routing(h, nullptr, 0, T, training, false, PERMUTE_INDEX, nullptr, s);
     if (r != MOE_OK) return r;
     const size_t nk = (size_t)T * h->kc;
@@ -1318,6 +1329,7 @@ static int forward_host_locked(moe_handle *h, const void *x, int32_t x_dtype, in
     if (r != MOE_OK) return r;
     const size_t xbytes = (x_dtype == MOE_BF16 ? 2 : 4) * (size_t)T * h->D;
     HIP_TRY(h, hipMemcpyAsync(h->x_dev, x, xbytes, hipMemcpyHostToDevice, s));
+    h->keep_rows = aux && (aux->logits || aux->probs);
     r = forward_locked(h, h->x_dev, x_dtype, T, training, h->out_dev, nullptr, s);
     if (r != MOE_OK) return r;
     HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, sizeof(float) * (size_t)T * h->Dout, hipMemcpyDeviceToHost, s));

@@ -8,9 +8,9 @@
 
 namespace moe {
 
-constexpr int kRouteBlock = 32;    // tokens per routing block
-constexpr int kRouteThreads = 256; // threads per routing block (8 per token)
-constexpr int kRouterMaxSlices = 8;   // K slices of the router logits GEMM (partial sums)
+constexpr int kRouteBlock = 32;    // tokens per routing block of the ExpertChoiceGating kernels
+constexpr int kRtThreads = 512;    // threads per router_kernel workgroup (8 per token)
+constexpr int kRtMinBlock = 16;    // fewest tokens per router_kernel workgroup
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
 constexpr int kKPad = 64;          // K padding of packed weights and activation rows
@@ -62,88 +62,26 @@ __host__ __device__ inline uint32_t isless_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Top-k of a row p[0..n) by the isless key, descending, lower index first
-// among equal keys (partialsortperm(p, 1:k, rev=true)), in one pass: the k
-// best so far sit in slots 0..k-1 in order; an entry enters only with a key
-// strictly above the k-th, is inserted after the equal keys already there,
-// and the slots after it move down by one.  Gates: p of the slots over their
-// sum in slot order.  p is an LDS row, 16-byte aligned, readable up to n
-// rounded up to 4.
-template <int K>
-__device__ inline void topk_row_k(const float *__restrict__ p, int n, int *sel, float *g) {
-#pragma clang fp contract(off)
-    uint32_t kb[K];
-    int ib[K];
-    float vb[K];
-#pragma unroll
-    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0; vb[q] = 0.0f; }  // key 0: empty (below every float)
-    for (int i0 = 0; i0 < n; i0 += 4) {
-        const float4 v4 = *(const float4 *)(p + i0);
-        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            uint32_t ck = isless_key(vv[c]);
-            if (i0 + c < n && ck > kb[K - 1]) {
-                int ci = i0 + c;
-                float cv = vv[c];
-                bool shift = false;  // once inserted, every later slot moves down by one
-#pragma unroll
-                for (int q = 0; q < K; ++q) {
-                    const bool ins = shift || ck > kb[q];
-                    const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
-                    kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
-                    ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
-                    shift = ins;
-                }
-            }
-        }
-    }
-    float s = vb[0];
-#pragma unroll
-    for (int q = 1; q < K; ++q) s = s + vb[q];
-#pragma unroll
-    for (int q = 0; q < K; ++q) {
-        sel[q] = ib[q];
-        g[q] = vb[q] / s;
-    }
-}
-
-__device__ inline void topk_row(const float *__restrict__ p, int n, int k, int *sel, float *g) {
-    switch (k) {
-    case 1: topk_row_k<1>(p, n, sel, g); break;
-    case 2: topk_row_k<2>(p, n, sel, g); break;
-    case 3: topk_row_k<3>(p, n, sel, g); break;
-    case 4: topk_row_k<4>(p, n, sel, g); break;
-    case 5: topk_row_k<5>(p, n, sel, g); break;
-    case 6: topk_row_k<6>(p, n, sel, g); break;
-    case 7: topk_row_k<7>(p, n, sel, g); break;
-    default: topk_row_k<8>(p, n, sel, g); break;
-    }
-}
-
 // ---- kernel argument blocks --------------------------------------------------
 
 // Router logits GEMM: x [T][D] (bf16 or fp32) times the router weight split
 // into three bf16 parts, held as the fragment image of router_split_kernel
-// (Dp = D rounded up to 32), computed by the routing workgroups themselves
-// (router_fused_kernel).
+// (Dp = D rounded up to 32).
 struct RouterArgs {
     const void *x; int x_bf16; int T, D, Er, Ep, Dp;
     const uint16_t *ws;
-    int kslice;   // router_logits_kernel: K steps (of 32) per slice, a multiple of 8
 };
 
-// Outputs of one route_kernel pass.  A plain forward writes both; with an
-// AuxiliaryFreeLoss the probabilities pass runs on the router logits and the
-// gating pass on logits + the loss's bias (src/core/moe_layer.jl:137-140).
+// Outputs of one gating pass of router_kernel.  A plain forward writes both;
+// with an AuxiliaryFreeLoss the probabilities pass runs on the router logits
+// and the gating pass on logits + the loss's bias (src/core/moe_layer.jl:137-140).
 enum { ROUTE_OUT_PROBS = 1,    // logits, probs, per-block probability / z / entropy sums
        ROUTE_OUT_GATING = 2 }; // indices, gates, ranks, per-block expert counts
 
 struct RouteArgs {
-    const float *part;     // [nks][T][Er] partial router logits (summed in slice order)
-    int nks;
+    const float *part;     // [T][Er] the caller's router logits (when no logits GEMM runs)
     const float *bias;     // [Er] or null
-    float *logits;         // [T][Er] out: sum of the partials + bias
+    float *logits;         // [T][Er] out: logits + bias
     int T, Er;
     int E;                 // probability rows (= Er)
     int Eh;                // experts of the histogram: E + lsh
@@ -157,13 +95,15 @@ struct RouteArgs {
     int *idx;              // [T][kt]
     float *gates;          // [T][kt]
     int *rank;             // [T][kt] rank of the entry inside its block & expert
-    int *blk_counts;       // [nblk][Eh]
-    double *blk_stats;     // [nblk][Eh+2]: prob sums (0 past E), sum lse^2, sum entropy
+    int *blk_counts;       // [nblk][ldc]: entries per expert (columns < Eh)
+    double *blk_stats;     // [nblk][lds]: prob sums (0 past E), sum lse^2, sum entropy (columns < Eh + 2)
+    int ldc, lds;          // row strides: Eh and Eh + 2 rounded up to 4
 };
 
 struct ScanArgs {
-    const int *blk_counts;
-    const double *blk_stats;
+    const int *blk_counts;  // [nblk][ldc]
+    const double *blk_stats;  // [nblk][lds]
+    int ldc, lds;           // row strides (also of rank_base: ldc)
     int nblk, T, E, kt;   // E: experts of the histogram
     int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
     int training, drop, z_enabled;
@@ -172,7 +112,7 @@ struct ScanArgs {
     int *tile_start;       // [E+1] first M tile of each expert (sum of ceil(count / bm))
     int *counts;           // [E]   (after capacity)
     int *offsets;          // [E+1]
-    int *rank_base;        // [nblk][E] rank of the block's first entry per expert
+    int *rank_base;        // [nblk][ldc] rank of the block's first entry per expert
     int *cap_out;          // [1] capacity (INT_MAX when unused)
     int2 *tiles;           // [max_tiles] (expert, m0)
     int *num_tiles;        // [1]
@@ -189,13 +129,31 @@ struct ScanArgs {
     unsigned *ticket;           // [1]   work: finished column blocks (0 between launches)
 };
 
+// One router_kernel launch: logits (GEMM of g, or r.part), then one or two
+// gating passes over TB-token workgroups (route blocks).
+struct RtArgs {
+    RouteArgs r;           // gating (r.out_mask: outputs of the single pass)
+    RouterArgs g;          // logits GEMM (when the kernel computes the logits)
+    int TB;                // tokens per workgroup: 16, 32 or 64
+    int KP, RB, dma;       // x staging: K columns per pass, LDS bytes per row, by global_load_lds
+    int RW;                // LDS row stride of the logits / probability rows (floats)
+    int off_L;             // LDS byte offset of the logits rows
+    int npass;             // 2: AuxiliaryFreeLoss (probabilities pass, then gating on logits + aux_bias)
+    const float *aux_bias; // [Er]
+    int store_rows;        // write logits / probs [T][Er] to global memory
+    int tail;              // the last workgroup to finish runs the scan (s)
+    ScanArgs s;
+};
+
 struct PermuteArgs {
     const void *x; int x_bf16;   // [T][D]
     int T, D, ld_xp, kt, E;
     int ct;                      // compute type of xp
     int *idx; float *gates;      // [T][kt] (rewritten under capacity)
     const int *rank;             // [T][kt]
-    const int *rank_base;        // [nblk][E]
+    int rb;                      // tokens per route block (rows of rank_base)
+    int ldc;                     // row stride of rank_base
+    const int *rank_base;        // [nblk][ldc]
     const int *offsets;          // [E+1]
     const int *cap;              // [1]
     int renorm;                  // capacity active: renormalise gates
@@ -297,21 +255,16 @@ struct DecodeArgs {
 // the router weight [D][Er_pad] fp32 -> the fused router's fragment image of
 // its three bf16 parts ((Dp / 32) * tiles per step KB, at most 3 * Ep * Dp * 2 B)
 hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp, uint16_t *img, hipStream_t s);
-// routing blocks that compute their logits (x . W) themselves: the route
-// pass of `a` (a.part / a.nks unused) on the logits of r, one launch
-hipError_t launch_router_fused(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
-// a route pass on logits summed from a.part's a.nks slices
-hipError_t launch_route(const RouteArgs &a, hipStream_t s);
-// the logits GEMM alone: K slices of r.kslice steps into part [nks][T][Er]
-// (the slicing is chosen here; *nks receives the slice count)
-hipError_t launch_router_logits(RouterArgs r, float *part, int max_slices, int *nks, hipStream_t s);
+// the routing call's router_kernel launch; tb_force > 0 fixes the tokens per
+// workgroup (else chosen here); *tb receives them (rows of the scan)
+hipError_t launch_router(RtArgs a, int tb_force, int *tb, hipStream_t s);
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
 // ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
 // gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
 // bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
 // expert's entries in its route block) and blk_counts [nblk][E]
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, hipStream_t s);
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 // compute_loss(::SwitchTransformerLoss) on device buffers in two launches

@@ -13,6 +13,7 @@
 //   routing entropy       src/core/moe_layer.jl:250-264
 #include <algorithm>
 #include <climits>
+#include <mutex>
 
 #include "moe_internal.h"
 
@@ -78,604 +79,546 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp
     return hipGetLastError();
 }
 
-// 8 consecutive x values of row t from column k (a multiple of 8) as bf16
-// parts (fp32 x: hi, mid, lo).  Otherwise columns >= D read as 0.  ALIGNED
-// (D a multiple of 32, so every 32-column block the MFMAs use lies below D):
-// one or two 16-byte loads from an address clamped into the row, no branch
-// and no select, so the loads of a chunk are all in flight together (a
-// select on the loaded value lets the compiler sink the load into a branch).
-template <int XBF16, int ALIGNED>
-__device__ inline void load_x8(const void *x, int D, int t, int k, rbf16x8_t *p) {
-    if (XBF16) {
-        const uint16_t *row = (const uint16_t *)x + (long long)t * D;
-        uint16_t v[8];
-        if (ALIGNED) {
-            const uint4 q = *(const uint4 *)(row + min(k, D - 8));
-            __builtin_memcpy(v, &q, 16);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (k + i < D) ? row[k + i] : (uint16_t)0;
-        }
-        __builtin_memcpy(&p[0], v, 16);
-    } else {
-#pragma clang fp contract(off)
-        const float *row = (const float *)x + (long long)t * D;
-        float v[8];
-        if (ALIGNED) {
-            const int kk = min(k, D - 8);
-            const float4 q0 = *(const float4 *)(row + kk), q1 = *(const float4 *)(row + kk + 4);
-            v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (k + i < D) ? row[k + i] : 0.0f;
-        }
-        uint16_t h0[8], h1[8], h2[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            h0[i] = f32_to_bf16(v[i]);
-            const float r1 = v[i] - bf16_to_f32(h0[i]);
-            h1[i] = f32_to_bf16(r1);
-            h2[i] = f32_to_bf16(r1 - bf16_to_f32(h1[i]));
-        }
-        __builtin_memcpy(&p[0], h0, 16);
-        __builtin_memcpy(&p[1], h1, 16);
-        __builtin_memcpy(&p[2], h2, 16);
-    }
+// ============================================================================
+// The router kernel (router_kernel): one launch per routing call.  Workgroup
+// b of kRtThreads threads owns the TB = 16, 32 or 64 tokens [b TB, b TB + TB)
+// (its route block) and
+//   1. computes their router logits on MFMA into LDS rows (or reads the
+//      caller's logits), plus the router bias;
+//   2. gates them, 8 lanes per token (softmax, top-k, gates);
+//   3. writes the entries, the stable rank of each inside the route block
+//      and expert, the route block's expert histogram and its probability,
+//      z-loss and entropy sums (the scan turns them into offsets, tile lists
+//      and losses).
+// With an AuxiliaryFreeLoss the gating runs twice on the same LDS logits:
+// the probabilities pass on the logits, then the gating pass on logits + the
+// loss's bias.
+// ============================================================================
+#define RT_LDS __attribute__((address_space(3)))
+
+// LDS of the scan phases (scan_columns on nth threads, scan_finish_block, and
+// both as the router kernel's tail)
+__host__ __device__ constexpr int scan_ws_bytes(int nth) { return nth * 48; }
+constexpr int kScanFinishWs = 2560;
+constexpr int scan_tail_lds_bytes(int nth) { return scan_ws_bytes(nth) + 16 * (MOE_MAX_EXPERTS + 8) + kScanFinishWs; }
+__device__ __forceinline__ void scan_tail(const ScanArgs &a, uint8_t *lds);
+
+// LDS byte address of a pointer into the workgroup's LDS (the M0 operand of
+// global_load_lds).
+__device__ __forceinline__ uint32_t rt_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const RT_LDS uint8_t *)p;
 }
 
-// The router logits of TM tokens (32 or 64) over all of K, into LDS rows
-// lrow[t][RW].  K runs in chunks of 256 (8 MFMA steps of 32): the block
-// stages each chunk of x in LDS with coalesced loads (each 16-lane pass
-// reads 256 contiguous bytes; rows padded by 16 B so the fragment reads hit
-// distinct banks), double-buffered so the next chunk's loads are in flight
-// during this chunk's MFMAs.  The split router weight is read from its
-// fragment image (router_split_kernel): one contiguous 1 KB per fragment.
-// Waves split the expert tiles NG ways and the K steps of each chunk
-// 4 / NG ways; per step, row tile and expert tile: acc += x . W0 + x . W1 +
-// x . W2 as v_mfma_f32_16x16x32_bf16 (fp32 x: each of its three parts times
-// the weight parts).  The waves' accumulators then go to an LDS buffer and
-// each logit is their sum in K-group order (paired tiles: the three parts'
-// columns added in part order), plus the router bias.
-// A: 16 tokens x 32 k (lane l: token l % 16, k 8 (l / 16) .. +8); B: the
-// image tile; D lane l: column l % 16, tokens 4 (l / 16) .. +4.
-constexpr int kRouterKC = 256;  // K per staged chunk
+// global_load_lds_dwordx4: lane l copies 16 bytes from its own global address
+// to LDS byte lds + 16 l (lds wave-uniform, an input operand bound to M0).
+// The staging below waits for these with rt_wait_vm0 and a barrier before any
+// LDS read of the bytes.
+__device__ __forceinline__ void rt_dma16(const void *gaddr, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds));
+}
+__device__ __forceinline__ void rt_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int XBF16, int TM>
-__host__ __device__ constexpr int router_stage_row_bytes() { return kRouterKC * (XBF16 ? 2 : 4) + 16; }
+// Rows that the router kernel's last workgroup reads from the other
+// workgroups (the route-block histogram and statistics) are stored and loaded
+// as agent-scope relaxed atomics: sc1 accesses, coherent across the XCDs'
+// L2 caches without a full-L2 writeback / invalidate (a device-scope fence
+// in every workgroup would write back and invalidate each XCD's L2 while the
+// other workgroups still read the router weight from it).
+__device__ __forceinline__ void st_agent(int *p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(double *p, double v) {
+    __hip_atomic_store((unsigned long long *)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_agent(const int *p) {
+    return __hip_atomic_load((int *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_agent(const double *p) {
+    return __longlong_as_double(
+        (long long)__hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
 
-template <int XBF16, int TM, int PAIRED, int NG, int TPW, typename Out>
-__device__ __forceinline__ void fused_logits(const RouterArgs &r, int t0, int ntok, int s_begin, int s_end,
-                                             uint8_t *stage, Out &&out) {
+constexpr int kRtMaskWords = 16;  // rank bitmask words per expert: TB * kt <= 64 * 8 entries
+
+// The partner lane of butterfly step 1, 2, 3 inside an 8-lane group, by DPP:
+// lane ^ 1, lane ^ 2 (quad permutations), then the mirrored lane of the other
+// quad (7 - lane within the group).  After the first two steps every lane of
+// a quad holds the quad's value, so the third pairs the two quads.
+__device__ __forceinline__ int dpp_x1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false); }
+__device__ __forceinline__ int dpp_x2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false); }
+__device__ __forceinline__ int dpp_m8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); }
+template <int STEP>
+__device__ __forceinline__ int dpp_step(int v) {
+    if constexpr (STEP == 0) return dpp_x1(v);
+    else if constexpr (STEP == 1) return dpp_x2(v);
+    else return dpp_m8(v);
+}
+template <int STEP>
+__device__ __forceinline__ float dpp_stepf(float v) { return __int_as_float(dpp_step<STEP>(__float_as_int(v))); }
+template <int STEP>
+__device__ __forceinline__ double dpp_stepd(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)dpp_step<STEP>((int)(unsigned)u), hi = (unsigned)dpp_step<STEP>((int)(unsigned)(u >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+template <int STEP>
+__device__ __forceinline__ uint64_t dpp_stepu64(uint64_t v) {
+    const unsigned lo = (unsigned)dpp_step<STEP>((int)(unsigned)v), hi = (unsigned)dpp_step<STEP>((int)(unsigned)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Max over the 8 lanes of a token (NaN never enters: the callers' maxima
+// start at -Inf and take a value only when it compares greater).
+__device__ __forceinline__ float lanes8_max(float v) {
+    float w = dpp_stepf<0>(v); v = (w > v) ? w : v;
+    w = dpp_stepf<1>(v); v = (w > v) ? w : v;
+    w = dpp_stepf<2>(v); v = (w > v) ? w : v;
+    return v;
+}
+// Sum over the 8 lanes of a token as a fixed tree (lane pairs, then quads,
+// then the two quads); every lane ends with the same bits.
+__device__ __forceinline__ float lanes8_sum(float v) {
+    v = v + dpp_stepf<0>(v);
+    v = v + dpp_stepf<1>(v);
+    return v + dpp_stepf<2>(v);
+}
+__device__ __forceinline__ double lanes8_sum(double v) {
+    v = v + dpp_stepd<0>(v);
+    v = v + dpp_stepd<1>(v);
+    return v + dpp_stepd<2>(v);
+}
+
+// ---- router logits ----------------------------------------------------------
+// Logits of the workgroup's TB tokens into LDS rows L[t][RW] (plus the router
+// bias).  K runs in passes of KP columns.  A pass's x tile is staged in LDS
+// (row r at byte r RB; 16-byte unit u of the row at unit position u ^ (r & 15),
+// so the 16 rows of one fragment read hit 16 distinct bank groups): by
+// global_load_lds when x is 16-byte aligned and D is a multiple of 32, else
+// by register copies that write zeros past D.  Waves split the expert tiles
+// (ET groups; paired tiles: one) and the pass's K steps (KG = 8 / ET
+// groups).  A wave reads its weight fragments from the fragment image in
+// groups of kRtSG steps (4; fp32 x: 2) through a ring of three register
+// groups: the first two load with the x tile, then each group's loads are
+// issued two groups ahead of its MFMAs.  Per step and 16-token row
+// tile: acc += x . W0 + x . W1 + x . W2 (v_mfma_f32_16x16x32_bf16; fp32 x:
+// each part of x times the weight parts of combined order <= 2).  A: 16
+// tokens x 32 k (lane l: token l % 16, k 8 (l / 16) .. +8); B: the image
+// tile; D lane l: column l % 16, tokens 4 (l / 16) .. +4.  The accumulators
+// then go to LDS partials P[kg][t][col] and each logit is their sum in
+// K-group order (paired tiles: the three parts' columns added in part order).
+template <int XBF16, int PAIRED>
+__device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds, float *L) {
 #pragma clang fp contract(off)
-    constexpr int RT = TM / 16;                 // 16-token row tiles
     constexpr int ESZ = XBF16 ? 2 : 4;
-    constexpr int ROWB = router_stage_row_bytes<XBF16, TM>();
-    constexpr int UPR = kRouterKC * ESZ / 16;   // 16-byte units per staged row
-    constexpr int NU = TM * UPR / kRouteThreads;  // units per thread per chunk
-    constexpr int KG = 4 / NG;                  // K groups
-    constexpr int SPW = 8 / KG;                 // steps per wave per chunk
-    constexpr int NPT = PAIRED ? 2 : 3;         // image tiles per expert tile
-    constexpr int NP = XBF16 ? 1 : 3;           // activation parts
-    constexpr int NACC = PAIRED ? 2 : TPW;      // accumulator tiles per row tile
-    static_assert(NU * kRouteThreads == TM * UPR, "staging units");
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int l16 = lane & 15;
-    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
+    constexpr int NPT = PAIRED ? 2 : 3;   // image tiles per expert tile and step
+    constexpr int NP = XBF16 ? 1 : 3;     // activation parts
+    constexpr int NACC = PAIRED ? 2 : 1;  // accumulator tiles per row tile
+    constexpr int kRtSG = XBF16 ? 4 : 2;  // K steps per group of prefetched weight fragments
+    const RouterArgs &g = a.g;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int TB = a.TB, RT = TB >> 4, RB = a.RB, PPR = RB >> 4;
+    const int ET = PAIRED ? 1 : (g.Er + 15) >> 4;
     const int NTS = PAIRED ? 2 : 3 * ET;
-    const int gn = w % NG, gk = w / NG;         // this wave's expert-tile group and K group
-    // K steps [s_begin, s_end) (a multiple of 8 apart unless s_end = Dp / 32)
-    const int S = s_end;
-    const int NCH = (s_end - s_begin + 7) / 8;
-    uint8_t *buf[2] = {stage, stage + TM * ROWB};
+    const int KG = 8 / ET;
+    const int cg = w % ET, kg = w / ET;
+    const bool mw = kg < KG;  // this wave runs MFMAs
 
-    // staging: unit u = tid + 256 j is row u / UPR, 16 bytes at column unit u % UPR
-    auto load_chunk = [&](int ch, u32x4_t (&v)[NU]) {
+    rf32x4_t acc[4][NACC];
 #pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int u = tid + j * kRouteThreads;
-            const int row = u / UPR, cu = u - row * UPR;
-            const int k0 = s_begin * 32 + ch * kRouterKC + cu * (16 / ESZ);
-            const long long t = min(t0 + row, r.T - 1);
-            if (k0 + 16 / ESZ <= r.D && (r.D % (16 / ESZ)) == 0) {
-                v[j] = *(const u32x4_t *)((const uint8_t *)r.x + (t * r.D + k0) * ESZ);
-            } else {
-                uint32_t q[4] = {0u, 0u, 0u, 0u};
-                if (XBF16) {
-                    uint16_t h[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) h[i] = (k0 + i < r.D) ? ((const uint16_t *)r.x)[t * r.D + k0 + i] : 0;
-                    __builtin_memcpy(q, h, 16);
-                } else {
-                    float f[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) f[i] = (k0 + i < r.D) ? ((const float *)r.x)[t * r.D + k0 + i] : 0.0f;
-                    __builtin_memcpy(q, f, 16);
-                }
-                v[j] = u32x4_t{q[0], q[1], q[2], q[3]};
-            }
-        }
-    };
-    auto store_chunk = [&](uint8_t *b, const u32x4_t (&v)[NU]) {
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int u = tid + j * kRouteThreads;
-            const int row = u / UPR, cu = u - row * UPR;
-            *(u32x4_t *)(b + row * ROWB + cu * 16) = v[j];
-        }
-    };
-    // the x fragment (parts) of step u of a staged chunk, row tile ti
-    auto x_frag = [&](const uint8_t *b, int u, int ti, rbf16x8_t *xa) {
-        const uint8_t *row = b + (ti * 16 + l16) * ROWB;
-        if (XBF16) {
-            xa[0] = *(const rbf16x8_t *)(row + u * 64 + (lane >> 4) * 16);
-        } else {
-            const float4 f0 = *(const float4 *)(row + (u * 32 + (lane >> 4) * 8) * 4);
-            const float4 f1 = *(const float4 *)(row + (u * 32 + (lane >> 4) * 8 + 4) * 4);
-            const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-            uint16_t h0[8], h1[8], h2[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                h0[i] = f32_to_bf16(v[i]);
-                const float r1 = v[i] - bf16_to_f32(h0[i]);
-                h1[i] = f32_to_bf16(r1);
-                h2[i] = f32_to_bf16(r1 - bf16_to_f32(h1[i]));
-            }
-            __builtin_memcpy(&xa[0], h0, 16);
-            __builtin_memcpy(&xa[1], h1, 16);
-            __builtin_memcpy(&xa[2], h2, 16);
-        }
-    };
-
-    rf32x4_t acc[RT][NACC];
-#pragma unroll
-    for (int ti = 0; ti < RT; ++ti)
+    for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
         for (int j = 0; j < NACC; ++j) acc[ti][j] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // weight fragments of a chunk for this wave (independent of LDS); with
-    // few of them (small E) the next chunk's are loaded a chunk ahead
-    constexpr bool WPF = SPW * TPW * NPT <= 16;
-    using WFrag = rbf16x8_t[SPW][TPW][NPT];
-    auto load_w = [&](int ch, WFrag &wb) {
+    using WF = rbf16x8_t[kRtSG][NPT];
+    for (int k0 = 0; k0 < g.Dp; k0 += a.KP) {
+        const int kp = min(a.KP, g.Dp - k0);
+        const int UPR = kp * ESZ / 16;  // data units per staged row
+        // ---- stage x[t0 .. t0 + TB)[k0 .. k0 + kp) (rows past T: row T - 1) ----
+        if (a.dma) {
+            const int NCH = TB * PPR / 64;  // 1 KB pieces of LDS
+            for (int c = w; c < NCH; c += kRtThreads / 64) {
+                const int p = c * 64 + lane;
+                const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
+                const long long t = min(t0 + r, g.T - 1);
+                const uint8_t *src = (const uint8_t *)g.x + (t * g.D + k0) * ESZ + (u < UPR ? u : 0) * 16;
+                rt_dma16(src, __builtin_amdgcn_readfirstlane(rt_lds_addr(lds + c * 1024)));
+            }
+        } else {
+            for (int p = tid; p < TB * PPR; p += kRtThreads) {
+                const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
+                const long long t = min(t0 + r, g.T - 1);
+                uint32_t q[4] = {0u, 0u, 0u, 0u};
+                if (u < UPR) {
+                    const int kb = k0 + u * (16 / ESZ);
+                    if (XBF16) {
+                        const uint16_t *row = (const uint16_t *)g.x + t * g.D;
+                        uint16_t hv[8];
 #pragma unroll
-        for (int i = 0; i < SPW; ++i) {
-            const int st = min(s_begin + ch * 8 + gk * SPW + i, S - 1);
+                        for (int i = 0; i < 8; ++i) hv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : (uint16_t)0;
+                        __builtin_memcpy(q, hv, 16);
+                    } else {
+                        const float *row = (const float *)g.x + t * g.D;
+                        float fv[4];
 #pragma unroll
-            for (int j = 0; j < TPW; ++j) {
-                const int et = min(gn + j * NG, ET - 1);
-#pragma unroll
-                for (int p = 0; p < NPT; ++p) {
-                    const int q = PAIRED ? p : et * 3 + p;
-                    wb[i][j][p] = *(const rbf16x8_t *)(r.ws + (((long long)st * NTS + q) * 64 + lane) * 8);
+                        for (int i = 0; i < 4; ++i) fv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : 0.0f;
+                        __builtin_memcpy(q, fv, 16);
+                    }
                 }
+                *(u32x4_t *)(lds + p * 16) = u32x4_t{q[0], q[1], q[2], q[3]};
             }
         }
-    };
-    // x of chunk 0 staged; chunks 1 and 2 in flight in registers (each chunk
-    // is stored one iteration after its loads were issued)
-    u32x4_t va[NU], vb[NU];
-    load_chunk(0, va);
-    store_chunk(buf[0], va);
-    if (NCH > 1) load_chunk(1, va);
-    WFrag wn;
-    if constexpr (WPF) load_w(0, wn);
-    __syncthreads();
-    for (int ch = 0; ch < NCH; ++ch) {
-        WFrag wb;
-        if constexpr (WPF) {
+        // ---- this wave's K steps of the pass: [sb, se) ----
+        const int sp = kp >> 5, spw = (sp + KG - 1) / KG;
+        const int sb = (k0 >> 5) + kg * spw, se = min((k0 >> 5) + sp, sb + spw);
+        const bool act = mw && sb < se;
+        auto load_w = [&](int s0, WF &wf) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < SPW; ++i)
+            for (int i = 0; i < kRtSG; ++i) {
+                const int st = min(s0 + i, se - 1);
 #pragma unroll
-                for (int j = 0; j < TPW; ++j)
+                for (int p = 0; p < NPT; ++p) {
+                    const int q = PAIRED ? p : 3 * cg + p;
+                    const rbf16x8_t *src = (const rbf16x8_t *)(g.ws + (((long long)st * NTS + q) * 64 + lane) * 8);
+                    if (PAIRED && p == 1) {
+                        // paired tile 1: columns 8..15 are zero in the image; those lanes skip the load
+                        rbf16x8_t z = {};
+                        if ((lane & 8) == 0) z = *src;
+                        wf[i][p] = z;
+                    } else {
+                        wf[i][p] = *src;
+                    }
+                }
+            }
+        };
+        auto mma = [&](int s0, const WF &wf) __attribute__((always_inline)) {
 #pragma unroll
-                    for (int p = 0; p < NPT; ++p) wb[i][j][p] = wn[i][j][p];
-            if (ch + 1 < NCH) load_w(ch + 1, wn);
-        } else {
-            load_w(ch, wb);
-        }
-        if (ch + 2 < NCH) load_chunk(ch + 2, vb);
-        const uint8_t *b = buf[ch & 1];
+            for (int i = 0; i < kRtSG; ++i) {
+                const int st = s0 + i;
+                if (st >= se) break;
+                const int u = st - (k0 >> 5);  // step inside the pass
 #pragma unroll
-        for (int i = 0; i < SPW; ++i) {
-            const int u = gk * SPW + i;
-            if (s_begin + ch * 8 + u >= S) break;
+                for (int ti = 0; ti < 4; ++ti) {
+                    if (ti >= RT) break;
+                    const int r = ti * 16 + l16;
+                    const uint8_t *row = lds + r * RB;
+                    rbf16x8_t xa[NP];
+                    if (XBF16) {
+                        xa[0] = *(const rbf16x8_t *)(row + (((u * 4 + (lane >> 4)) ^ (r & 15)) << 4));
+                    } else {
+                        const int u0 = u * 8 + (lane >> 4) * 2;
+                        const float4 f0 = *(const float4 *)(row + ((u0 ^ (r & 15)) << 4));
+                        const float4 f1 = *(const float4 *)(row + (((u0 + 1) ^ (r & 15)) << 4));
+                        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+                        uint16_t h0[8], h1[8], h2[8];
 #pragma unroll
-            for (int ti = 0; ti < RT; ++ti) {
-                rbf16x8_t xa[NP];
-                x_frag(b, u, ti, xa);
-                if constexpr (PAIRED) {
-                    // tile 0 (parts 0, 1): every x part; tile 1 (part 2): x part 0
+                        for (int m = 0; m < 8; ++m) {
+                            h0[m] = f32_to_bf16(v[m]);
+                            const float r1 = v[m] - bf16_to_f32(h0[m]);
+                            h1[m] = f32_to_bf16(r1);
+                            h2[m] = f32_to_bf16(r1 - bf16_to_f32(h1[m]));
+                        }
+                        __builtin_memcpy(&xa[0], h0, 16);
+                        __builtin_memcpy(&xa[NP > 1 ? 1 : 0], h1, 16);
+                        __builtin_memcpy(&xa[NP > 2 ? 2 : 0], h2, 16);
+                    }
+                    if constexpr (PAIRED) {
+                        // tile 0 (parts 0 | 1): every x part; tile 1 (part 2): x part 0
 #pragma unroll
-                    for (int xi = 0; xi < NP; ++xi)
-                        acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wb[i][0][0], acc[ti][0], 0, 0, 0);
-                    acc[ti][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], wb[i][0][1], acc[ti][1], 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < TPW; ++j) {
-                        if (gn + j * NG >= ET) break;
+                        for (int xi = 0; xi < NP; ++xi)
+                            acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wf[i][0], acc[ti][0], 0, 0, 0);
+                        acc[ti][NACC - 1] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], wf[i][NPT - 1], acc[ti][NACC - 1], 0, 0, 0);
+                    } else {
 #pragma unroll
                         for (int p = 0; p < 3; ++p)
 #pragma unroll
                             for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
-                                acc[ti][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wb[i][j][p], acc[ti][j],
-                                                                                     0, 0, 0);
+                                acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wf[i][p < NPT ? p : 0],
+                                                                                     acc[ti][0], 0, 0, 0);
                     }
                 }
             }
+        };
+        // a ring of three weight groups: two in flight with the x tile, then
+        // each group's loads issued two groups ahead of its MFMAs
+        WF w0, w1, w2;
+        if (act) {
+            load_w(sb, w0);
+            if (sb + kRtSG < se) load_w(sb + kRtSG, w1);
         }
-        if (ch + 1 < NCH) store_chunk(buf[(ch + 1) & 1], va);
-#pragma unroll
-        for (int j = 0; j < NU; ++j) va[j] = vb[j];
+        rt_wait_vm0();  // this wave's x pieces (and its first weight groups) have landed
         __syncthreads();
+        if (act) {
+            for (int s0 = sb; s0 < se; s0 += 3 * kRtSG) {
+                if (s0 + 2 * kRtSG < se) load_w(s0 + 2 * kRtSG, w2);
+                mma(s0, w0);
+                if (s0 + kRtSG >= se) break;
+                if (s0 + 3 * kRtSG < se) load_w(s0 + 3 * kRtSG, w0);
+                mma(s0 + kRtSG, w1);
+                if (s0 + 2 * kRtSG >= se) break;
+                if (s0 + 4 * kRtSG < se) load_w(s0 + 4 * kRtSG, w1);
+                mma(s0 + 2 * kRtSG, w2);
+            }
+        }
+        __syncthreads();  // the pass's x tile is consumed
     }
 
-    // accumulators -> LDS partials P[gk][t][col] (the staging buffers are
-    // free now), col = image column of the expert tile (paired: 16 q + c)
+    // accumulators -> LDS partials P[kg][t][col] (over the staging region),
+    // col = image column of the expert tile (paired: 16 j + c)
     const int NCOL = PAIRED ? 32 : ET * 16;
-    float *P = (float *)stage;
+    float *P = (float *)lds;
+    if (mw) {
 #pragma unroll
-    for (int ti = 0; ti < RT; ++ti)
+        for (int ti = 0; ti < 4; ++ti) {
+            if (ti >= RT) break;
 #pragma unroll
-        for (int j = 0; j < NACC; ++j) {
-            const int col = PAIRED ? j * 16 + l16 : (gn + j * NG) * 16 + l16;
-            if (PAIRED || gn + j * NG < ET)
+            for (int j = 0; j < NACC; ++j) {
+                const int col = PAIRED ? j * 16 + l16 : cg * 16 + l16;
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int t = ti * 16 + (lane >> 4) * 4 + rr;
-                    P[((long long)gk * TM + t) * NCOL + col] = acc[ti][j][rr];
+                    P[(kg * TB + t) * NCOL + col] = acc[ti][j][rr];
                 }
+            }
         }
+    }
     __syncthreads();
-    // logit (of this K range) = the K groups' partials in order (paired: per
-    // part column, the parts then added in part order), to out(t, e, value)
-    for (int q = tid; q < ntok * r.Er; q += kRouteThreads) {
-        const int t = q / r.Er, e = q - t * r.Er;
-        auto col_sum = [&](int col) {
-            float v = P[(long long)t * NCOL + col];
-#pragma unroll
-            for (int g = 1; g < KG; ++g) v = v + P[((long long)g * TM + t) * NCOL + col];
+    const float *bias = a.r.bias;
+    for (int q = tid; q < TB * g.Er; q += kRtThreads) {
+        const int t = q / g.Er, e = q - t * g.Er;
+        auto col_sum = [&](int col) __attribute__((always_inline)) {
+            float v = P[t * NCOL + col];
+            for (int k = 1; k < KG; ++k) v = v + P[(k * TB + t) * NCOL + col];
             return v;
         };
-        out(t, e, PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e));
+        float v = PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e);
+        if (bias) v = v + bias[e];
+        L[t * a.RW + e] = v;
     }
 }
 
-// ============================================================================
-// Gating.  kRouteBlock tokens per routing block of kRouteThreads threads, 8
-// lanes per token, each holding a contiguous block of the token's experts in
-// registers (gate_block).
-// ============================================================================
-
-// LDS row stride of the routing kernel for E rows: a multiple of 4 floats
-// (16 B) whose count of 16-byte units is odd, so that 16 token threads
-// reading 16 B at one column hit 16 distinct bank quads.
-__host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) | 1)); }
-
-// The value of the partner lane in butterfly step o (1, 2, 4) of an 8-lane
-// group, by DPP: lane ^ 1, lane ^ 2 (quad permutations), then the mirrored
-// lane of the other quad (7 - lane within the group; after two steps every
-// lane of a quad holds the same list, so any pairing of the two quads works).
-__device__ __forceinline__ int lane_swap8(int o, int v) {
-    if (o == 1) return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
-    if (o == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
-    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);              // row_half_mirror
-}
-
-// Entry (key a, index ia) before entry (b, ib) in the top-k order: larger
-// isless key, then the lower index (partialsortperm's Perm ordering).
-__device__ __forceinline__ bool topk_before(uint32_t a, int ia, uint32_t b, int ib) {
-    return a > b || (a == b && ia < ib);
-}
-
-// Top-K of a token's routed probabilities held in registers: lane rs of the
-// token's 8 keeps elements base + j (j < EPL) of the row; each lane keeps the
-// best K of its elements in sorted register slots (larger isless key, then
-// the lower index), then three butterfly steps merge the lanes' lists (a
-// strict total order, so every lane ends with the same list).  Every lane of
-// the wave must call it (inactive rows pass active = false).  Slots past the
-// row's routed size stay empty (key 0, below every float's key).
-template <int K, int EPL>
-__device__ __forceinline__ void topk_reg(const float (&p)[EPL], int base, int lo, int n, bool active, int *sel,
-                                         float *val) {
-    uint32_t kb[K];
-    int ib[K];
-    float vb[K];
-#pragma unroll
-    for (int q = 0; q < K; ++q) { kb[q] = 0u; ib[q] = 0x7fffffff; vb[q] = 0.0f; }
-    auto insert = [&](uint32_t ck, int ci, float cv) {
-        if (!topk_before(ck, ci, kb[K - 1], ib[K - 1])) return;
-        bool shift = false;  // once inserted, every later slot moves down by one
-#pragma unroll
-        for (int q = 0; q < K; ++q) {
-            const bool ins = shift || topk_before(ck, ci, kb[q], ib[q]);
-            const uint32_t tk = kb[q]; const int ti = ib[q]; const float tv = vb[q];
-            kb[q] = ins ? ck : tk; ib[q] = ins ? ci : ti; vb[q] = ins ? cv : tv;
-            ck = ins ? tk : ck; ci = ins ? ti : ci; cv = ins ? tv : cv;
-            shift = ins;
-        }
-    };
-    if (active) {
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const int i = base + j;
-            if (i >= lo && i < n) insert(isless_key(p[j]), i, p[j]);
-        }
-    }
-#pragma unroll 1
-    for (int o = 1; o < 8; o <<= 1) {
-        uint32_t pk[K];
-        int pi[K];
-        float pv[K];
-#pragma unroll
-        for (int q = 0; q < K; ++q) {
-            pk[q] = (uint32_t)lane_swap8(o, (int)kb[q]);
-            pi[q] = lane_swap8(o, ib[q]);
-            pv[q] = __int_as_float(lane_swap8(o, __float_as_int(vb[q])));
-        }
-#pragma unroll
-        for (int q = 0; q < K; ++q) insert(pk[q], pi[q], pv[q]);
-    }
-#pragma unroll
-    for (int q = 0; q < K; ++q) {
-        sel[q] = ib[q];
-        val[q] = vb[q];
-    }
-}
-
+// ---- gating -------------------------------------------------------------------
+// One gating pass over the route block's tokens: lane rs of token rt = tid /
+// 8 holds the contiguous experts rs EPL .. +EPL of the token's row in
+// registers.  Logits: the LDS row L[rt] (plus xbias, the second pass's bias).
+// Per token: the max; exp terms e = (float)exp((double)(l - m)) (NNlib's
+// branch for m == +Inf); their fp32 sum in expert order (a chain through the
+// lanes: lane r adds its experts, in order, to lane r - 1's running sum,
+// passed on by DPP row_shr:1); probabilities e / s; the fp64 entropy terms
+// and the logsumexp.  Top-k: k rounds, each taking the largest (isless key,
+// then lower index) element below the previous round's, by a per-lane scan
+// and a 3-step DPP butterfly; the gates.  Then per entry (lane rs = slot
+// rs): its stable rank among the route block's entries of its expert (LDS
+// bitmask per expert, bit = entry), and the route block's histogram,
+// probability sums and loss terms.  Pr: LDS rows [TB][RW] for the output
+// probabilities.
 template <int EPL>
-__device__ __forceinline__ void topk_reg_k(const float (&p)[EPL], int base, int lo, int n, int k, bool active,
-                                           int *sel, float *val) {
-    // K >= k slots: the first k of the best K are the top-k
-    if (k == 1) topk_reg<1, EPL>(p, base, lo, n, active, sel, val);
-    else if (k == 2) topk_reg<2, EPL>(p, base, lo, n, active, sel, val);
-    else if (k <= 4) topk_reg<4, EPL>(p, base, lo, n, active, sel, val);
-    else topk_reg<8, EPL>(p, base, lo, n, active, sel, val);
-}
-
-// Butterfly sum / max over the 8 lanes of a token (the same tree every call).
-template <typename F>
-__device__ __forceinline__ F lanes8_sum(F v) {
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) v = v + __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ float lanes8_max(float v) {  // NaN ignored (v > m is false for NaN)
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-        const float w = __shfl_xor(v, o);
-        if (w > v) v = w;
-    }
-    return v;
-}
-
-// One routing block, number blk: kRouteBlock tokens, 8 lanes per token (lane
-// rs of token rt = tid / 8 holds the contiguous experts rs EPL .. +EPL of the
-// row in registers).  Logits: the token's row of lin (LDS rows, stride RW)
-// when FROM_LDS, else the sum of a.part's nks K slices in slice order plus
-// the bias, read straight from global memory (each token's 8 lanes read its
-// row contiguously).  Per token, in registers: max; exp terms e =
-// (float)exp((double)(l - m)) (NNlib's branch for m == +Inf); their fp32 sum
-// in expert order (the recipe's order: lane r adds its experts after lane
-// r - 1's running sum); probabilities e / s; the fp64 entropy terms and the
-// logsumexp; the top-k by per-lane sorted lists and a butterfly merge; the
-// gates.  Then per entry (lane rs = slot rs): its stable rank among the
-// block's entries of its expert (LDS bitmask per expert, bit = entry), and
-// the block's histogram, probability sums and loss terms.  sl: LDS rows
-// [kRouteBlock][RW] for the output probabilities (the block sums).
-template <int EPL, bool FROM_LDS>
-__device__ __forceinline__ void gate_block(const RouteArgs &a, int blk, const float *lin, int RW, float *sl) {
+__device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const float *xbias, int blk, int t0, int ntok,
+                                        const float *L, float *Pr, unsigned *emask, double (*wred)[kRtThreads / 64]) {
 #pragma clang fp contract(off)
-    // stable ranks: bit i of emask[e][i / 32] marks entry i (token * kt + slot)
-    // of expert e + 1 in this block
-    __shared__ unsigned emask[MOE_MAX_EXPERTS * MOE_MAX_TOPK];
-    __shared__ double wred[2][kRouteThreads / 64];
+    const RouteArgs &a = A.r;
+    const int RW = A.RW;
     const bool shared_gate = a.gate_kind == MOE_GATE_SHARED;
     const bool soft = a.gate_kind == MOE_GATE_SOFT;
     const bool zsep = shared_gate || soft;  // z-loss from a softmax of its own (all rows, unscaled)
-    const bool out_probs = (a.out_mask & ROUTE_OUT_PROBS) != 0;
-    const bool out_gating = (a.out_mask & ROUTE_OUT_GATING) != 0;
+    const bool out_probs = (out_mask & ROUTE_OUT_PROBS) != 0;
+    const bool out_gating = (out_mask & ROUTE_OUT_GATING) != 0;
     // a gating pass on the caller's routing needs none of the softmax phases
     const bool softmax = out_probs || !a.given;
-    const int E = a.E;                       // router rows (= a.Er)
+    const int E = a.E;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int rt = tid >> 3, rs = tid & 7;   // token rt of the block, lane rs of it
-    const int t0 = blk * kRouteBlock;
-    const int ntok = min(kRouteBlock, a.T - t0);
+    const int rt = tid >> 3, rs = tid & 7;
     const bool rvalid = rt < ntok;
     const long long t = (long long)t0 + rt;
-    const int ns = shared_gate ? a.ns : 0;   // rows before the routed ones
+    const int ns = shared_gate ? a.ns : 0;  // rows before the routed ones
     const int base = rs * EPL;
 
-    __syncthreads();  // the previous routing block of this workgroup is done with the LDS
-    for (int i = tid; i < MOE_MAX_EXPERTS * MOE_MAX_TOPK; i += kRouteThreads) emask[i] = 0u;
+    __syncthreads();  // a previous pass is done with emask and the rows
+    for (int i = tid; i < a.Eh * kRtMaskWords; i += kRtThreads) emask[i] = 0u;
 
     float v[EPL], pr[EPL];  // logits; exp terms, then probabilities (before the shared-gating scale)
 #pragma unroll
     for (int j = 0; j < EPL; ++j) { v[j] = 0.0f; pr[j] = 0.0f; }
-    float m = -INFINITY, s = 0.0f, lse = 0.0f;
+    float lse = 0.0f;
     double hs = 0.0;
     if (softmax) {
-        // ---- logits ----
-        if (rvalid) {
-            if constexpr (FROM_LDS) {
 #pragma unroll
-                for (int j = 0; j < EPL; ++j)
-                    if (base + j < E) v[j] = lin[rt * RW + base + j];
-            } else {
-                const long long sstride = (long long)a.T * a.Er;
-                const float *row = a.part + t * a.Er + base;
-                float pv[EPL];
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) pv[j] = (base + j < E) ? row[j] : 0.0f;
-                for (int sl_ = 1; sl_ < a.nks; ++sl_) {
-                    float q[EPL];
-#pragma unroll
-                    for (int j = 0; j < EPL; ++j) q[j] = (base + j < E) ? row[sl_ * sstride + j] : 0.0f;
-#pragma unroll
-                    for (int j = 0; j < EPL; ++j) pv[j] = pv[j] + q[j];
-                }
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) {
-                    float w = pv[j];
-                    if (a.bias && base + j < E) w = w + a.bias[base + j];
-                    v[j] = w;
-                }
-            }
+        for (int j = 0; j < EPL; ++j) {
+            const int i = base + j;
+            const bool ok = rvalid && i < E;
+            float x = ok ? L[ok ? rt * RW + i : 0] : 0.0f;
+            if (xbias) x = ok ? x + xbias[ok ? i : 0] : x;
+            v[j] = x;
         }
         // ---- max (of the routed rows; zsep: also of all rows) ----
-        float mz = -INFINITY;
+        float m = -INFINITY, mz = -INFINITY;
         float sv[EPL];  // logits ./ lambda for SoftMoEGating (advanced.jl:18)
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
+            const bool ok = rvalid && i < E;
             sv[j] = soft ? v[j] / a.soft_lambda : v[j];
-            if (rvalid && i >= ns && i < E && sv[j] > m) m = sv[j];
-            if (rvalid && i < E && v[j] > mz) mz = v[j];
+            m = (ok && i >= ns && sv[j] > m) ? sv[j] : m;
+            mz = (ok && v[j] > mz) ? v[j] : mz;
         }
         m = lanes8_max(m);
-        mz = lanes8_max(mz);
+        if (zsep) mz = lanes8_max(mz);
         // ---- exp terms; zsep: the z-loss exponent sum over all rows ----
         float zs = 0.0f;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
-            if (rvalid && i >= ns && i < E)
-                pr[j] = (m == INFINITY) ? ((sv[j] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv[j] - m));
-            if (zsep && rvalid && i < E) zs = zs + (float)exp((double)(v[j] - mz));
+            const bool okr = rvalid && i >= ns && i < E;
+            const float ex = (m == INFINITY) ? ((sv[j] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv[j] - m));
+            pr[j] = okr ? ex : 0.0f;
         }
-        if (zsep) zs = lanes8_sum(zs);
-        // ---- sum in expert order ----
-        if constexpr (EPL == 1) {
-            float ev[8];
+        if (zsep) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r) ev[r] = __shfl(pr[0], (lane & ~7) | r);
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (r >= ns && r < E) s = s + ev[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                float c = s;
-                if (rs == r) {
-#pragma unroll
-                    for (int j = 0; j < EPL; ++j) {
-                        const int i = r * EPL + j;
-                        if (i >= ns && i < E) c = c + pr[j];
-                    }
-                }
-                s = __shfl(c, (lane & ~7) | r);
+            for (int j = 0; j < EPL; ++j) {
+                const int i = base + j;
+                if (rvalid && i < E) zs = zs + (float)exp((double)(v[j] - mz));
             }
+            zs = lanes8_sum(zs);
+        }
+        // ---- sum in expert order: a chain through the token's lanes ----
+        float s;
+        {
+            float c = 0.0f;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) c = c + pr[j];
+            s = (rs == 0) ? c : 0.0f;
+#pragma unroll
+            for (int r = 1; r < 8; ++r) {
+                // lane i receives lane i - 1's running sum (row_shr:1 inside each 16-lane row)
+                float c2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x111, 0xf, 0xf, false));
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) c2 = c2 + pr[j];
+                s = (rs == r) ? c2 : s;
+            }
+            // every lane of the token takes lane 7's total (swizzle: lane (i & 0x18) | 7)
+            s = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0xF8));
         }
         // ---- probabilities (outputs: shared gating's shared rows 1/E, routed
         // rows p scaled by 1 - ns/E in Float64; the caller's gate: its
         // probabilities or ones ./ E); entropy terms p log(p + 1e-8) with
-        // p + 1e-8 in Float64 as Julia promotes it, the log in fp32 (a
-        // statistic: the mean entropy is checked to 1e-5) ----
+        // p + 1e-8 in Float64 as Julia promotes it, the log as the hardware
+        // log2 (v_log_f32, about 1 ulp) times ln 2 in fp32 (a statistic: the
+        // mean entropy is checked to 1e-5 relative) ----
+        const float invE = 1.0f / (float)E;
+        const double pscale = 1.0 - (double)ns / (double)E;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
-            if (!rvalid || i >= E) continue;
+            const bool ok = rvalid && i < E;
             float pv;
             if (a.given) {
-                pv = a.given_probs ? a.probs[t * E + i] : 1.0f / (float)E;
-            } else if (i < ns) {
-                pv = 1.0f / (float)E;
+                pv = a.given_probs ? (ok ? a.probs[ok ? t * E + i : 0] : 0.0f) : invE;
             } else {
                 pr[j] = pr[j] / s;
-                pv = shared_gate ? (float)((double)pr[j] * (1.0 - (double)ns / (double)E)) : pr[j];
+                pv = (i < ns) ? invE : (shared_gate ? (float)((double)pr[j] * pscale) : pr[j]);
             }
-            sl[rt * RW + i] = pv;
+            if (ok) Pr[rt * RW + i] = pv;
             const double pd = (double)pv;
-            hs = hs + pd * (double)logf((float)(pd + 1e-8));
+            const float lg = __builtin_amdgcn_logf((float)(pd + 1e-8)) * 0.693147180559945309f;
+            const double term = pd * (double)lg;
+            hs = ok ? hs + term : hs;
         }
         hs = lanes8_sum(hs);
         // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
         // the log in Float32 as Julia takes it of the Float32 sum
         lse = zsep ? mz + logf(zs) : m + logf(s);
-        if (out_probs && rvalid) {
+        if (A.store_rows && out_probs && rvalid) {
 #pragma unroll
             for (int j = 0; j < EPL; ++j)
                 if (base + j < E) {
                     a.logits[t * E + base + j] = v[j];
-                    a.probs[t * E + base + j] = sl[rt * RW + base + j];
+                    a.probs[t * E + base + j] = Pr[rt * RW + base + j];
                 }
         }
     }
 
-    // ---- top-k and gates; the entries' experts (slot rs of the token) ----
-    int my_e = 0;     // 1-based expert of entry (rt, rs), 0: none
+    // ---- top-k and gates; the entry of this lane (slot rs of the token) ----
+    int my_e = 0;  // 1-based expert of entry (rt, rs), 0: none
     float my_g = 0.0f;
-    if (!a.given) {
-        int sel[MOE_MAX_TOPK];
-        float val[MOE_MAX_TOPK];
+    if (out_gating && !a.given) {
+        // routed slot this lane reports: rs minus the shared slots before it
+        const int jr = rs - (shared_gate ? ns : (soft ? 0 : a.lsh));
+        uint64_t thr = ~0ull;
+        float sg = 0.0f, sel_v = 0.0f;
+        int sel_i = -1;
+#pragma unroll 1
+        for (int r = 0; r < a.k; ++r) {
+            uint64_t best = 0ull;
+            float bv = 0.0f;
 #pragma unroll
-        for (int q = 0; q < MOE_MAX_TOPK; ++q) { sel[q] = 0; val[q] = 0.0f; }
-        topk_reg_k<EPL>(pr, base, ns, E, a.k, rvalid, sel, val);
-        // gates: p of the slots over their sum in slot order
-        float sg = val[0];
-#pragma unroll
-        for (int q = 1; q < MOE_MAX_TOPK; ++q)
-            if (q < a.k) sg = sg + val[q];
-        // the slot this lane reports: rs (slots 0 .. kt-1)
-        const int j = rs;
+            for (int j = 0; j < EPL; ++j) {
+                const int i = base + j;
+                const bool okr = rvalid && i >= ns && i < E;
+                const uint64_t c = okr ? (((uint64_t)isless_key(pr[j]) << 32) | (uint32_t)~(uint32_t)i) : 0ull;
+                const bool take = (r == 0 || c < thr) && c > best;
+                best = take ? c : best;
+                bv = take ? pr[j] : bv;
+            }
+            {
+                uint64_t ob = dpp_stepu64<0>(best); float ov = dpp_stepf<0>(bv);
+                bool tk = ob > best; best = tk ? ob : best; bv = tk ? ov : bv;
+                ob = dpp_stepu64<1>(best); ov = dpp_stepf<1>(bv);
+                tk = ob > best; best = tk ? ob : best; bv = tk ? ov : bv;
+                ob = dpp_stepu64<2>(best); ov = dpp_stepf<2>(bv);
+                tk = ob > best; best = tk ? ob : best; bv = tk ? ov : bv;
+            }
+            thr = best;
+            sg = (r == 0) ? bv : sg + bv;  // gate sum in slot order
+            const bool mine = r == jr;
+            sel_i = mine ? (int)~(uint32_t)best : sel_i;
+            sel_v = mine ? bv : sel_v;
+        }
+        const bool routed = jr >= 0 && jr < a.k;
         if (soft) {
             // SoftMoEGating: top-k of the scaled-softmax probabilities; the
             // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
             // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
             float pj = 0.0f;
-            const int src = (lane & ~7) | (j / EPL);  // the lane holding expert j (j < 8)
+            const int src = (lane & ~7) | (rs / EPL);  // the lane holding expert rs (rs < 8)
 #pragma unroll
             for (int u = 0; u < EPL; ++u) {
-                const float w = __shfl(pr[u], src);
-                if (u == j % EPL) pj = w;
+                const float wv2 = __shfl(pr[u], src);
+                pj = (u == rs % EPL) ? wv2 : pj;
             }
-            if (j < a.k) {
-#pragma unroll
-                for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                    if (q == j) my_e = sel[q] + 1;
+            if (routed) {
+                my_e = sel_i + 1;
                 my_g = pj;
             }
         } else if (shared_gate) {
             // shared slots 0 .. ns-1 (gate 1/kt), then the routed top-k with
             // gates scaled by 1 - ns/kt in Float64 (advanced.jl:80-108)
-            if (j < ns) {
-                my_e = j + 1;
+            if (rs < ns) {
+                my_e = rs + 1;
                 my_g = 1.0f / (float)a.kt;
-            } else if (j < ns + a.k) {
-                const double gscale = 1.0 - (double)ns / (double)a.kt;
-#pragma unroll
-                for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                    if (q == j - ns) {
-                        my_e = sel[q] + 1;
-                        my_g = (float)((double)(val[q] / sg) * gscale);
-                    }
+            } else if (routed) {
+                my_e = sel_i + 1;
+                my_g = (float)((double)(sel_v / sg) * (1.0 - (double)ns / (double)a.kt));
             }
         } else if (a.lsh > 0) {
             // forward_with_shared_experts: shared experts 1..lsh in slots
             // 0..lsh-1 (their outputs are averaged, the gate is only
             // reported), then the routed ids shifted by lsh (expert_indices
             // .+= num_shared_experts, src/core/moe_layer.jl:172)
-            if (j < a.lsh) {
-                my_e = j + 1;
+            if (rs < a.lsh) {
+                my_e = rs + 1;
                 my_g = 1.0f / (float)a.lsh;
-            } else if (j < a.lsh + a.k) {
-#pragma unroll
-                for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                    if (q == j - a.lsh) {
-                        my_e = sel[q] + 1 + a.lsh;
-                        my_g = val[q] / sg;
-                    }
+            } else if (routed) {
+                my_e = sel_i + 1 + a.lsh;
+                my_g = sel_v / sg;
             }
-        } else if (j < a.k) {
-#pragma unroll
-            for (int q = 0; q < MOE_MAX_TOPK; ++q)
-                if (q == j) {
-                    my_e = sel[q] + 1;
-                    my_g = val[q] / sg;
-                }
+        } else if (routed) {
+            my_e = sel_i + 1;
+            my_g = sel_v / sg;
         }
-        if (!rvalid) my_e = 0;
-    } else if (rvalid && rs < a.kt) {
+        if (!rvalid || (routed && sel_i < 0)) my_e = 0;
+    } else if (out_gating && rvalid && rs < a.kt) {
         // the caller's routing: ids outside 1..E are skipped, as the
         // dispatch's `expert_id > 0 && expert_id <= length(experts)` does
         // (src/core/moe_layer.jl:198)
@@ -685,15 +628,15 @@ __device__ __forceinline__ void gate_block(const RouteArgs &a, int blk, const fl
         my_g = a.gates[ent];
     }
 
-    // ---- stable rank of each entry among the block's entries of its expert ----
-    // (entries in token-then-slot order, as the bucket loop visits them)
+    // ---- stable rank of each entry among the route block's entries of its
+    // expert (entries in token-then-slot order, as the bucket loop visits them)
     const int ent = rt * a.kt + rs;  // entry of this lane (rs < kt)
-    const bool has_ent = out_gating && rs < a.kt && my_e > 0;
+    const bool has_ent = out_gating && rvalid && rs < a.kt && my_e > 0;
     __syncthreads();  // emask cleared
-    if (has_ent) atomicOr(&emask[(my_e - 1) * MOE_MAX_TOPK + (ent >> 5)], 1u << (ent & 31));
-    // block sums of the per-token loss terms (tokens rt: lane rs == 0), in a
-    // fixed order: within a wave by a butterfly over its 8 tokens, then the
-    // waves in order
+    if (has_ent) atomicOr(&emask[(my_e - 1) * kRtMaskWords + (ent >> 5)], 1u << (ent & 31));
+    // route-block sums of the per-token loss terms (tokens rt: lane rs == 0),
+    // in a fixed order: within a wave by a butterfly over its 8 tokens, then
+    // the waves in order
     double zterm = 0.0, hterm = 0.0;
     if (softmax && rvalid && rs == 0) {
         zterm = (double)(lse * lse);
@@ -709,208 +652,188 @@ __device__ __forceinline__ void gate_block(const RouteArgs &a, int blk, const fl
         wred[1][wv] = hterm;
     }
     __syncthreads();  // emask complete, wred and the probability rows written
-    if (has_ent && rvalid) {
-        const unsigned *mk = &emask[(my_e - 1) * MOE_MAX_TOPK];
+    if (has_ent) {
+        const unsigned *mk = &emask[(my_e - 1) * kRtMaskWords];
         int rr = __popc(mk[ent >> 5] & ((1u << (ent & 31)) - 1u));
-        for (int w = 0; w < (ent >> 5); ++w) rr += __popc(mk[w]);
+        for (int wd = 0; wd < (ent >> 5); ++wd) rr += __popc(mk[wd]);
         a.rank[t * a.kt + rs] = rr;
     }
     if (out_gating && rvalid && rs < a.kt) {
         a.idx[t * a.kt + rs] = my_e;
         a.gates[t * a.kt + rs] = my_g;
     }
-    for (int e = tid; e < a.Eh; e += kRouteThreads) {
+    const int TW = (ntok * a.kt + 31) >> 5;  // mask words in use
+    for (int e = tid; e < a.Eh; e += kRtThreads) {
         if (out_gating) {
             int c = 0;
-#pragma unroll
-            for (int w = 0; w < MOE_MAX_TOPK; ++w) c += __popc(emask[e * MOE_MAX_TOPK + w]);
-            a.blk_counts[(long long)blk * a.Eh + e] = c;
+            for (int wd = 0; wd < TW; ++wd) c += __popc(emask[e * kRtMaskWords + wd]);
+            st_agent(&a.blk_counts[(long long)blk * a.ldc + e], c);
         }
         if (out_probs) {
             // per-row probability sums (Switch loss P_e) in fp64, token order
             double ps = 0.0;
             if (e < E) {
 #pragma unroll 8
-                for (int i = 0; i < ntok; ++i) ps += (double)sl[i * RW + e];
+                for (int i = 0; i < ntok; ++i) ps += (double)Pr[i * RW + e];
             }
-            a.blk_stats[(long long)blk * (a.Eh + 2) + e] = ps;
+            st_agent(&a.blk_stats[(long long)blk * a.lds + e], ps);
         }
     }
     if (tid == 0 && out_probs) {
         double zb = 0.0, hb = 0.0;
 #pragma unroll
-        for (int w = 0; w < kRouteThreads / 64; ++w) {
-            zb += wred[0][w];
-            hb += wred[1][w];
+        for (int wd = 0; wd < kRtThreads / 64; ++wd) {
+            zb += wred[0][wd];
+            hb += wred[1][wd];
         }
-        a.blk_stats[(long long)blk * (a.Eh + 2) + a.Eh] = zb;
-        a.blk_stats[(long long)blk * (a.Eh + 2) + a.Eh + 1] = hb;
+        st_agent(&a.blk_stats[(long long)blk * a.lds + a.Eh], zb);
+        st_agent(&a.blk_stats[(long long)blk * a.lds + a.Eh + 1], hb);
     }
 }
 
-template <int EPL>
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
-    const int RW = route_rw(a.E);
-    gate_block<EPL, false>(a, blockIdx.x, nullptr, RW, (float *)rdyn);
-}
+// LDS row stride of the logits and probability rows for E experts: a multiple
+// of 4 floats (16 B) whose count of 16-byte units is odd, so that token
+// threads reading 16 B at one column hit distinct bank quads.
+__host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) | 1)); }
 
-// The router's MFMA logits GEMM and the gating of route_kernel in one
-// launch: a workgroup computes the logits of TM = 32 or 64 tokens over all of
-// K into LDS, then gates them as TM / 32 routing blocks (no partial sums
-// through HBM).  Dynamic LDS: the logit rows of the TM tokens, then one
-// routing block's probability rows, which the x staging of the logits phase
-// shares.
-template <int XBF16, int TM, int PAIRED, int NG, int TPW, int EPL>
-__global__ __launch_bounds__(kRouteThreads) void router_fused_kernel(RouteArgs a, RouterArgs r) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
-    const int RW = route_rw(a.E);
-    float *lrows = (float *)rdyn;
-    float *srow = lrows + TM * RW;
-    const int t0 = blockIdx.x * TM;
-    const float *bias = a.bias;
-    fused_logits<XBF16, TM, PAIRED, NG, TPW>(r, t0, min(TM, a.T - t0), 0, r.Dp / 32, (uint8_t *)srow,
-                                            [&](int t, int e, float v) {
-                                                if (bias) v = v + bias[e];
-                                                lrows[t * RW + e] = v;
-                                            });
-    constexpr int NSUB = TM / kRouteBlock;
-#pragma unroll 1
-    for (int sb = 0; sb < NSUB; ++sb) {
-        const int blk = blockIdx.x * NSUB + sb;
-        if (blk * kRouteBlock >= a.T) break;  // uniform over the workgroup
-        gate_block<EPL, true>(a, blk, lrows + sb * kRouteBlock * RW, RW, srow);
+// LG: 0 = the caller's logits (r.part), 1 = logits GEMM on bf16 x, 2 = on fp32
+// x.  PAIRED: Er <= 8 (the paired weight tiles).  EPL: experts per lane.
+template <int LG, int PAIRED, int EPL>
+__global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t rdyn[];
+    __shared__ unsigned emask[MOE_MAX_EXPERTS * kRtMaskWords];
+    __shared__ double wred[2][kRtThreads / 64];
+    const int blk = blockIdx.x;
+    const int t0 = blk * A.TB;
+    const int ntok = min(A.TB, A.r.T - t0);
+    float *L = (float *)(rdyn + A.off_L);
+    float *Pr = (float *)rdyn;  // over the staging region, free once the logits are in L
+    if constexpr (LG > 0) {
+        rt_logits<LG == 1, PAIRED>(A, t0, rdyn, L);
+    } else {
+        const int Er = A.r.Er;
+        for (int q = threadIdx.x; q < ntok * Er; q += kRtThreads) {
+            const int t = q / Er, e = q - t * Er;
+            float v = A.r.part[(long long)(t0 + t) * Er + e];
+            if (A.r.bias) v = v + A.r.bias[e];
+            L[t * A.RW + e] = v;
+        }
+    }
+    if (A.npass == 2) {
+        rt_gate<EPL>(A, ROUTE_OUT_PROBS, nullptr, blk, t0, ntok, L, Pr, emask, wred);
+        rt_gate<EPL>(A, ROUTE_OUT_GATING, A.aux_bias, blk, t0, ntok, L, Pr, emask, wred);
+    } else {
+        rt_gate<EPL>(A, A.r.out_mask, nullptr, blk, t0, ntok, L, Pr, emask, wred);
+    }
+    if (A.tail) {
+        // the workgroup that finishes last runs the scan: every workgroup
+        // waits until its agent-scope row stores are complete, then takes a
+        // ticket; the last ticket's workgroup reads the rows with agent-scope
+        // loads and resets the ticket for the next launch (which stream order
+        // puts after this one)
+        __shared__ bool last;
+        rt_wait_vm0();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(A.s.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        __syncthreads();
+        if (!last) return;
+        if (threadIdx.x == 0) __hip_atomic_store(A.s.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        scan_tail(A.s, rdyn);
     }
 }
 
-// The router's logits GEMM on its own: workgroup (token tile, K slice)
-// computes the partial logits of TM tokens over K steps [z S8, (z + 1) S8)
-// (S8 = r.kslice steps) into part[z][T][Er]; the routing kernel adds the
-// slices in slice order and the bias.  K slices spread a small batch over
-// every CU, and keep the x tile each workgroup streams small.
-template <int XBF16, int TM, int PAIRED, int NG, int TPW>
-__global__ __launch_bounds__(kRouteThreads) void router_logits_kernel(RouterArgs r, float *part) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t rdyn[];
-    const int t0 = blockIdx.x * TM;
-    const int z = blockIdx.y;
-    const int S = r.Dp / 32;
-    const int sb = z * r.kslice, se = min(S, sb + r.kslice);
-    float *dst = part + (long long)z * r.T * r.Er + (long long)t0 * r.Er;
-    fused_logits<XBF16, TM, PAIRED, NG, TPW>(r, t0, min(TM, r.T - t0), sb, se, rdyn,
-                                            [&](int t, int e, float v) { dst[(long long)t * r.Er + e] = v; });
-}
-
-static size_t route_lds_bytes(const RouteArgs &a) {
-    // the probability rows of one routing block
-    return (size_t)kRouteBlock * sizeof(float) * route_rw(a.E);
-}
-
-// experts per lane of a token's 8 (the gating body's register blocks)
+// experts per lane of a token's 8 (the gating's register blocks)
 static int route_epl(int E) { return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : 16))); }
 
-template <int XBF16, int TM, int PAIRED, int NG, int TPW, int EPL>
-static hipError_t launch_fused_case(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
-    const int RW = route_rw(a.E);
-    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
-    const size_t stage = std::max<size_t>((size_t)2 * TM * router_stage_row_bytes<XBF16, TM>(),
-                                          sizeof(float) * (size_t)(4 / NG) * TM * (PAIRED ? 32 : ET * 16));
-    const size_t lds = sizeof(float) * (size_t)TM * RW + std::max<size_t>(sizeof(float) * kRouteBlock * RW, stage);
-    if (lds > 150 * 1024) return hipErrorInvalidValue;
-    auto kern = router_fused_kernel<XBF16, TM, PAIRED, NG, TPW, EPL>;
-    if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(kern, dim3((a.T + TM - 1) / TM), dim3(kRouteThreads), lds, s, a, r);
+template <int LG, int PAIRED, int EPL>
+static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipStream_t s) {
+    auto kern = router_kernel<LG, PAIRED, EPL>;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [&] {
+        attr = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+    });
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(kern, dim3(nblk), dim3(kRtThreads), lds, s, A);
     return hipGetLastError();
 }
 
-hipError_t launch_router_fused(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
-    if (a.T <= 0) return hipSuccess;
-    if (r.Er < 1 || r.Er > MOE_MAX_EXPERTS || r.Er != a.Er || a.E != a.Er || r.Dp % 32 != 0 || r.Dp < r.D ||
-        ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK))
-        return hipErrorInvalidValue;
-    const int ET = (r.Er + 15) / 16;
-    // 64-token workgroups for bf16 x when that still gives at least 256 of them
-    const bool tm64 = r.x_bf16 && a.T >= 64 * 256;
-    // expert tiles -> (paired, waves along N, tiles per wave) and the gating's
-    // experts per lane: E <= 8 | <= 16 | <= 32 (ET 2) | <= 48 / 64 (ET 3, 4) | more
-#define MOE_FUSED(XB, TM_, P, NG_, TPW_, EPL_) return launch_fused_case<XB, TM_, P, NG_, TPW_, EPL_>(a, r, s)
-#define MOE_FUSED_TILES(XB, TM_)                                  \
-    if (r.Er <= 8) MOE_FUSED(XB, TM_, 1, 1, 1, 1);                \
-    if (ET == 1) MOE_FUSED(XB, TM_, 0, 1, 1, 2);                  \
-    if (ET == 2) MOE_FUSED(XB, TM_, 0, 2, 1, 4);                  \
-    if (ET == 3) MOE_FUSED(XB, TM_, 0, 2, 2, 8);                  \
-    if (ET == 4) MOE_FUSED(XB, TM_, 0, 4, 1, 8);                  \
-    MOE_FUSED(XB, TM_, 0, 4, 2, 16);
-    if (!r.x_bf16) { MOE_FUSED_TILES(0, 32) }
-    if (tm64) { MOE_FUSED_TILES(1, 64) }
-    MOE_FUSED_TILES(1, 32)
-#undef MOE_FUSED_TILES
-#undef MOE_FUSED
-}
-
-template <int XBF16, int TM, int PAIRED, int NG, int TPW>
-static hipError_t launch_logits_case(const RouterArgs &r, float *part, int nks, hipStream_t s) {
-    const int ET = PAIRED ? 1 : (r.Er + 15) / 16;
-    const size_t lds = std::max<size_t>((size_t)2 * TM * router_stage_row_bytes<XBF16, TM>(),
-                                        sizeof(float) * (size_t)(4 / NG) * TM * (PAIRED ? 32 : ET * 16));
-    if (lds > 150 * 1024) return hipErrorInvalidValue;
-    auto kern = router_logits_kernel<XBF16, TM, PAIRED, NG, TPW>;
-    if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
+hipError_t launch_router(RtArgs A, int tb_force, int *tb, hipStream_t s) {
+    const RouteArgs &a = A.r;
+    if (a.T <= 0) {
+        *tb = kRtMinBlock;
+        return hipSuccess;
     }
-    hipLaunchKernelGGL(kern, dim3((r.T + TM - 1) / TM, nks), dim3(kRouteThreads), lds, s, r, part);
-    return hipGetLastError();
-}
-
-hipError_t launch_router_logits(RouterArgs r, float *part, int max_slices, int *nks, hipStream_t s) {
-    *nks = 1;
-    if (r.T <= 0) return hipSuccess;
-    if (r.Er < 1 || r.Er > MOE_MAX_EXPERTS || r.Dp % 32 != 0 || r.Dp < r.D || max_slices < 1)
+    const bool gemm = A.g.x != nullptr;
+    if (a.E != a.Er || a.E < 1 || a.E > MOE_MAX_EXPERTS || a.Eh > MOE_MAX_EXPERTS || a.k > MOE_MAX_TOPK ||
+        ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK) || (!gemm && !a.part))
         return hipErrorInvalidValue;
-    const int ET = (r.Er + 15) / 16;
-    const bool tm64 = r.x_bf16 != 0;  // 64-token tiles for bf16 x (fp32 x: 32, its staging is twice as wide)
-    const int TM = tm64 ? 64 : 32;
-    const int tiles = (r.T + TM - 1) / TM;
-    // K slices of whole 8-step chunks so that tiles x slices reaches 256 workgroups
-    const int S = r.Dp / 32, chunks = (S + 7) / 8;
-    int want = std::max(1, std::min(std::min(max_slices, chunks), (256 + tiles - 1) / tiles));
-    const int per = (chunks + want - 1) / want;
-    r.kslice = per * 8;
-    const int n = (S + r.kslice - 1) / r.kslice;
-    *nks = n;
-#define MOE_LOGITS(XB, TM_, P, NG_, TPW_) return launch_logits_case<XB, TM_, P, NG_, TPW_>(r, part, n, s)
-#define MOE_LOGITS_TILES(XB, TM_)                                   \
-    if (r.Er <= 8) MOE_LOGITS(XB, TM_, 1, 1, 1);                    \
-    if (ET == 1) MOE_LOGITS(XB, TM_, 0, 1, 1);                      \
-    if (ET == 2) MOE_LOGITS(XB, TM_, 0, 2, 1);                      \
-    if (ET == 3) MOE_LOGITS(XB, TM_, 0, 2, 2);                      \
-    if (ET == 4) MOE_LOGITS(XB, TM_, 0, 4, 1);                      \
-    MOE_LOGITS(XB, TM_, 0, 4, 2);
-    if (tm64) { MOE_LOGITS_TILES(1, 64) }
-    MOE_LOGITS_TILES(0, 32)
-#undef MOE_LOGITS_TILES
-#undef MOE_LOGITS
-}
-
-hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
-    if (a.T <= 0) return hipSuccess;
-    if (a.E != a.Er || a.E < 1 || a.E > MOE_MAX_EXPERTS || ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK))
-        return hipErrorInvalidValue;
-    const int nblk = (a.T + kRouteBlock - 1) / kRouteBlock;
-    const size_t lds = route_lds_bytes(a);
-    switch (route_epl(a.E)) {
-    case 1: hipLaunchKernelGGL(route_kernel<1>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
-    case 2: hipLaunchKernelGGL(route_kernel<2>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
-    case 4: hipLaunchKernelGGL(route_kernel<4>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
-    case 8: hipLaunchKernelGGL(route_kernel<8>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
-    default: hipLaunchKernelGGL(route_kernel<16>, dim3(nblk), dim3(kRouteThreads), lds, s, a); break;
+    const int Er = a.Er;
+    const bool paired = gemm && Er <= 8;
+    const int ET = paired ? 1 : (Er + 15) / 16;
+    // tokens per workgroup: 16 for the paired (few-expert) GEMM, whose x tile
+    // is widest; otherwise 64 / 32 / 16 while that leaves 256 workgroups;
+    // 64 without the GEMM
+    int TB;
+    if (tb_force > 0) TB = tb_force;
+    else if (!gemm) TB = 64;
+    else if (paired) TB = 16;
+    else TB = a.T >= 64 * 256 ? 64 : (a.T >= 32 * 256 ? 32 : 16);
+    if (TB != 16 && TB != 32 && TB != 64) return hipErrorInvalidValue;
+    *tb = TB;
+    A.TB = TB;
+    A.RW = route_rw(Er);
+    const size_t rows = sizeof(float) * (size_t)TB * A.RW;
+    const size_t lds_max = 150 * 1024;  // + the static emask / wred (9.2 KB) <= 160 KB
+    size_t region0 = rows;
+    if (gemm) {
+        const RouterArgs &g = A.g;
+        if (g.Dp % 32 != 0 || g.Dp < g.D || g.Er != Er) return hipErrorInvalidValue;
+        const int ESZ = g.x_bf16 ? 2 : 4;
+        // x tile bytes per row: what LDS holds beside the logits rows, in 256 B units
+        const size_t avail = lds_max - rows - 1024;
+        const int maxRB = (int)((avail / TB) & ~(size_t)255);
+        const int KPmax = maxRB / ESZ;
+        A.KP = std::min(g.Dp, KPmax);
+        A.RB = ((A.KP * ESZ + 255) / 256) * 256;
+        A.dma = (g.D % 32 == 0) && (((uintptr_t)g.x & 15) == 0);
+        const int KG = 8 / ET;
+        const size_t part = sizeof(float) * (size_t)KG * TB * (paired ? 32 : ET * 16);
+        region0 = std::max(region0, std::max((size_t)TB * A.RB, part));
     }
-    return hipGetLastError();
+    A.off_L = (int)((region0 + 1023) & ~(size_t)1023);
+    size_t lds = (size_t)A.off_L + rows;
+    const int nblk = (a.T + TB - 1) / TB;
+    if (A.tail) {
+        const ScanArgs &sc = A.s;
+        if (!sc.ticket || sc.E != a.Eh || sc.ldc % 4 || sc.lds % 4 || sc.ldc < sc.E || sc.lds < sc.E + 2)
+            return hipErrorInvalidValue;
+        A.s.nblk = nblk;
+        lds = std::max(lds, (size_t)scan_tail_lds_bytes(kRtThreads));
+    }
+    if (lds > lds_max) return hipErrorInvalidValue;
+    const int epl = route_epl(Er);
+#define MOE_RT(LG_, P_, EPL_) return launch_router_case<LG_, P_, EPL_>(A, nblk, lds, s)
+#define MOE_RT_EPL(LG_)                 \
+    switch (epl) {                      \
+    case 2: MOE_RT(LG_, 0, 2);          \
+    case 4: MOE_RT(LG_, 0, 4);          \
+    case 8: MOE_RT(LG_, 0, 8);          \
+    default: MOE_RT(LG_, 0, 16);        \
+    }
+    if (!gemm) {
+        if (epl == 1) MOE_RT(0, 0, 1);
+        MOE_RT_EPL(0)
+    }
+    if (A.g.x_bf16) {
+        if (paired) MOE_RT(1, 1, 1);
+        MOE_RT_EPL(1)
+    }
+    if (paired) MOE_RT(2, 1, 1);
+    MOE_RT_EPL(2)
+#undef MOE_RT_EPL
+#undef MOE_RT
 }
 
 // ============================================================================
@@ -1007,7 +930,7 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
 // tokens that hold e.
 __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
                                                                             int E, int kt, int *rank,
-                                                                            int *blk_counts) {
+                                                                            int *blk_counts, int ldc) {
     const int e = threadIdx.x;
     if (e >= E) return;
     const int t0 = blockIdx.x * kRouteBlock;
@@ -1020,18 +943,18 @@ __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(con
             ++c;
         }
     }
-    blk_counts[(long long)blockIdx.x * E + e] = c;
+    blk_counts[(long long)blockIdx.x * ldc + e] = c;
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, hipStream_t s) {
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255) return hipErrorInvalidValue;
+    if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255 || ldc < E) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
                        min(C, E), idx, gates);
     hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + kRouteBlock - 1) / kRouteBlock), dim3(MOE_MAX_EXPERTS),
-                       0, s, sel, T, E, kt, rank, blk_counts);
+                       0, s, sel, T, E, kt, rank, blk_counts, ldc);
     return hipGetLastError();
 }
 
@@ -1062,81 +985,99 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
     for (int e = 0; e < E; ++e) bias[e] = bias[e] - mean;
 }
 
-// Scan, part 1: many blocks.  Block b takes kScanCols columns (expert
-// counts and fp64 statistics of column c; columns E, E + 1: the z and
-// entropy sums) and splits the nblk route-block rows into kScanChunks
-// contiguous chunks, one thread per (chunk, column): the chunk sums go to
-// LDS, every thread then writes the rank bases of its chunk's rows (the
-// counts of the earlier chunks, then of the chunk's earlier rows), and the
-// first chunk's threads the column totals, chunk sums added in chunk order.
-constexpr int kScanCols = 8;
-constexpr int kScanChunks = 32;
+// Scan, column phase: for each column c of the route-block rows (counts
+// blk_counts[b][c], c < E; fp64 statistics blk_stats[b][c], c < E + 2: the
+// probability sums, then the z and entropy sums) the rank bases
+// rank_base[b][c] (the counts of the rows before b) and the column totals
+// (the chunks' sums added in chunk order; a chunk's rows in row order) into
+// tc / ts.  Thread (g, q) owns columns 4 (g0 + g) .. +3 (one 16-byte count
+// load and two 16-byte statistics loads per row) and row chunk q; the block
+// covers column groups g0 .. g0 + ng - 1.  ws: LDS, scan_ws_bytes(threads).
+constexpr int kScanGroups = 2;       // column groups per block of scan_kernel
 
-__device__ __forceinline__ void scan_finish_block(const ScanArgs &a);
-
-__global__ __launch_bounds__(kScanCols * kScanChunks) void scan_kernel(ScanArgs a) {
+__device__ __forceinline__ void scan_columns(const ScanArgs &a, int g0, int ng, uint8_t *ws, int *tc, double *ts) {
 #pragma clang fp contract(off)
-    static_assert(kScanCols * kScanChunks == 256, "the finish phase runs on 256 threads");
-    __shared__ int csum[kScanChunks][kScanCols];
-    __shared__ double ssum[kScanChunks][kScanCols];
+    const int tid = threadIdx.x, nth = blockDim.x;
     const int NC = a.E + 2;
-    const int c = blockIdx.x * kScanCols + (threadIdx.x % kScanCols);
-    const int g = threadIdx.x / kScanCols;
-    const int R = (a.nblk + kScanChunks - 1) / kScanChunks;
-    const int b0 = min(a.nblk, g * R), b1 = min(a.nblk, b0 + R);
-    const bool col = c < NC, cnt_col = c < a.E;
-    int cs = 0;
-    double ss = 0.0;
-    if (col) {
-        for (int b = b0; b < b1; b += 8) {
-            int cv[8];
-            double sv[8];
+    const int C = max(1, min(nth / ng, a.nblk / 4));  // row chunks (of at least 4 rows)
+    const int R = (a.nblk + C - 1) / C;
+    int *csum = (int *)ws;                     // [C][ng][4]
+    double *ssum = (double *)(ws + 16 * nth);  // [C][ng][4]
+    const int gl = tid % ng, q = tid / ng;
+    const int c0 = 4 * (g0 + gl);
+    const bool act = q < C && c0 < NC;
+    const bool cnt_grp = c0 < a.ldc;  // the group has count columns
+    const int b0 = min(a.nblk, q * R), b1 = min(a.nblk, b0 + R);
+    int cs[4] = {0, 0, 0, 0};
+    double ss[4] = {0.0, 0.0, 0.0, 0.0};
+    if (act) {
+#pragma unroll 4
+        for (int b = b0; b < b1; ++b) {
+            const int *cr = a.blk_counts + (long long)b * a.ldc + c0;
+            const double *sr = a.blk_stats + (long long)b * a.lds + c0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int bb = min(b + u, b1 - 1);
-                cv[u] = cnt_col ? a.blk_counts[(long long)bb * a.E + c] : 0;
-                sv[u] = a.blk_stats[(long long)bb * NC + c];
+            for (int i = 0; i < 4; ++i) {
+                if (cnt_grp) cs[i] += ld_agent(cr + i);
+                ss[i] += ld_agent(sr + i);
             }
+        }
+        const int o = (q * ng + gl) * 4;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (b + u < b1) {
-                    cs += cv[u];
-                    ss += sv[u];
-                }
+        for (int i = 0; i < 4; ++i) {
+            csum[o + i] = cs[i];
+            ssum[o + i] = ss[i];
         }
     }
-    csum[g][threadIdx.x % kScanCols] = cs;
-    ssum[g][threadIdx.x % kScanCols] = ss;
     __syncthreads();
-    if (cnt_col) {
-        int base = 0;
-        for (int q = 0; q < g; ++q) base += csum[q][threadIdx.x % kScanCols];
-        for (int b = b0; b < b1; b += 8) {
-            int cv[8];
+    if (act && cnt_grp) {
+        // the chunk's base, then its rows in order
+        int base[4] = {0, 0, 0, 0};
+        for (int qq = 0; qq < q; ++qq)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) cv[u] = a.blk_counts[(long long)min(b + u, b1 - 1) * a.E + c];
+            for (int i = 0; i < 4; ++i) base[i] += csum[(qq * ng + gl) * 4 + i];
+#pragma unroll 4
+        for (int b = b0; b < b1; ++b) {
+            const int *cr = a.blk_counts + (long long)b * a.ldc + c0;
+            int cv[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (b + u < b1) {
-                    a.rank_base[(long long)(b + u) * a.E + c] = base;
-                    base += cv[u];
-                }
+            for (int i = 0; i < 4; ++i) cv[i] = ld_agent(cr + i);
+            *(int4 *)(a.rank_base + (long long)b * a.ldc + c0) = make_int4(base[0], base[1], base[2], base[3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) base[i] += cv[i];
         }
     }
-    if (col && g == 0) {
-        int tc = 0;
-        double ts = 0.0;
-        for (int q = 0; q < kScanChunks; ++q) {
-            tc += csum[q][threadIdx.x % kScanCols];
-            ts += ssum[q][threadIdx.x % kScanCols];
+    if (act && q == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + i;
+            if (c >= NC) break;
+            int tcv = 0;
+            double tsv = 0.0;
+            for (int qq = 0; qq < C; ++qq) {
+                tcv += csum[(qq * ng + gl) * 4 + i];
+                tsv += ssum[(qq * ng + gl) * 4 + i];
+            }
+            if (c < a.E) tc[c] = tcv;
+            ts[c] = tsv;
         }
-        if (cnt_col) a.tot_counts[c] = tc;
-        a.tot_stats[c] = ts;
     }
-    // The block that finishes last runs the finish phase on all the column
-    // totals: every block publishes its totals (release fence), then takes a
-    // ticket; the last ticket's block acquires them and resets the ticket for
-    // the next launch (which stream order puts after this one).
+}
+
+__device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *tcnt, const double *tstat, uint8_t *ws);
+
+// Scan of a routing call whose route blocks were not scanned by the router
+// kernel (ExpertChoiceGating): blocks of kScanGroups column groups run the
+// column phase with the totals to global memory; the block that finishes
+// last runs the finish phase on them.  Every block publishes its totals
+// (release fence), then takes a ticket; the last ticket's block acquires
+// them and resets the ticket for the next launch (which stream order puts
+// after this one).
+__global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t ws[scan_ws_bytes(256)];
+    __shared__ __attribute__((aligned(16))) uint8_t fws[kScanFinishWs];
+    const int NG = (a.E + 2 + 3) / 4;
+    const int g0 = blockIdx.x * kScanGroups;
+    scan_columns(a, g0, min(kScanGroups, NG - g0), ws, a.tot_counts, a.tot_stats);
     __shared__ bool last;
     __threadfence();
     __syncthreads();
@@ -1145,21 +1086,35 @@ __global__ __launch_bounds__(kScanCols * kScanChunks) void scan_kernel(ScanArgs 
     if (!last) return;
     __threadfence();
     if (threadIdx.x == 0) *a.ticket = 0u;
-    scan_finish_block(a);
+    scan_finish_block(a, a.tot_counts, a.tot_stats, fws);
+}
+
+// The scan run by the router kernel's last workgroup: the column phase of
+// every column on this workgroup, totals in LDS, then the finish phase.
+__device__ __forceinline__ void scan_tail(const ScanArgs &a, uint8_t *lds) {
+    const int NG = (a.E + 2 + 3) / 4;
+    uint8_t *ws = lds;
+    int *tc = (int *)(lds + scan_ws_bytes(blockDim.x));
+    double *ts = (double *)(lds + scan_ws_bytes(blockDim.x) + 8 * (MOE_MAX_EXPERTS + 8));
+    uint8_t *fws = lds + scan_ws_bytes(blockDim.x) + 16 * (MOE_MAX_EXPERTS + 8);
+    scan_columns(a, 0, NG, ws, tc, ts);
+    __syncthreads();
+    scan_finish_block(a, tc, ts, fws);
 }
 
 // Scan, part 2: one block (the last of part 1).  Capacity clamp, offsets,
 // per-expert GEMM tile starts and the (expert, m0) tile list, the Switch and
 // z losses, the mean entropy and the AuxiliaryFreeLoss step, from the column
 // totals.
-__device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
+__device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *tcnt, const double *tstat, uint8_t *ws) {
 #pragma clang fp contract(off)
-    __shared__ int cnt[MOE_MAX_EXPERTS];
-    __shared__ int off[MOE_MAX_EXPERTS + 1];
-    __shared__ int tstart[MOE_MAX_EXPERTS + 1];
-    __shared__ float fp[MOE_MAX_EXPERTS];
-    __shared__ int cap_s;
-    const int tid = threadIdx.x;
+    int *cnt = (int *)ws;                       // [MOE_MAX_EXPERTS]
+    int *off = cnt + MOE_MAX_EXPERTS;           // [MOE_MAX_EXPERTS + 1]
+    int *tstart = off + MOE_MAX_EXPERTS + 1;    // [MOE_MAX_EXPERTS + 1]
+    float *fp = (float *)(tstart + MOE_MAX_EXPERTS + 1);  // [MOE_MAX_EXPERTS]
+    int &cap_s = *(int *)(fp + MOE_MAX_EXPERTS);
+    float &lsum_s = *(float *)(fp + MOE_MAX_EXPERTS + 1);
+    const int tid = threadIdx.x, nth = blockDim.x;
     if (tid == 0) {
         int cap = INT_MAX;
         if (a.training && a.drop) {
@@ -1172,8 +1127,8 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
     }
     __syncthreads();
     const float total = (float)((long long)a.T * a.kl);
-    for (int e = tid; e < a.E; e += 256) {
-        const int ce = min(a.tot_counts[e], cap_s);
+    for (int e = tid; e < a.E; e += nth) {
+        const int ce = min(tcnt[e], cap_s);
         cnt[e] = ce;
         // the terms f_e * P_e of the Switch loss (src/balancing/losses.jl:15-36)
         // over the a.Np probability rows; with shared experts of the layer the
@@ -1181,14 +1136,13 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
         if (e < a.Np) {
             float f = (e < a.lsh) ? 0.0f : (float)ce;
             if (a.T * a.kl > 0) f = f / total;
-            const float P = (float)a.tot_stats[e] / (float)a.T;
+            const float P = (float)tstat[e] / (float)a.T;
             fp[e] = f * P;
         }
     }
     __syncthreads();
     // offsets and GEMM tile starts: exclusive prefixes over the experts by
     // wave 0 (lane l holds experts 2 l and 2 l + 1; E <= 128)
-    __shared__ float lsum_s;
     if (tid < 64) {
         const int e0 = 2 * tid, e1 = e0 + 1;
         const int c0 = (e0 < a.E) ? cnt[e0] : 0, c1 = (e1 < a.E) ? cnt[e1] : 0;
@@ -1234,7 +1188,7 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
     if (tid == 0) {
         const int ts = tstart[a.E];
         a.num_tiles[0] = ts;
-        const double zs = a.tot_stats[a.E], hs = a.tot_stats[a.E + 1];
+        const double zs = tstat[a.E], hs = tstat[a.E + 1];
         const float s = lsum_s;
         // AuxiliaryFreeLoss: complementary_weight * Switch(1.0f0) or 0.0f0
         // (src/balancing/auxiliary_free.jl:78-87)
@@ -1257,11 +1211,11 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e <= a.E; e += 256) {
+    for (int e = tid; e <= a.E; e += nth) {
         a.offsets[e] = off[e];
         a.tile_start[e] = tstart[e];
     }
-    for (int e = tid; e < a.E; e += 256) {
+    for (int e = tid; e < a.E; e += nth) {
         a.counts[e] = cnt[e];
         const int nt = tstart[e + 1] - tstart[e];
         for (int i = 0; i < nt; ++i) a.tiles[tstart[e] + i] = make_int2(e, i * a.bm);
@@ -1269,9 +1223,10 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a) {
 }
 
 hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
-    if (!a.ticket || a.E > MOE_MAX_EXPERTS) return hipErrorInvalidValue;
-    const int NC = a.E + 2;
-    hipLaunchKernelGGL(scan_kernel, dim3((NC + kScanCols - 1) / kScanCols), dim3(kScanCols * kScanChunks), 0, s, a);
+    if (!a.ticket || a.E > MOE_MAX_EXPERTS || a.ldc % 4 || a.lds % 4 || a.ldc < a.E || a.lds < a.E + 2)
+        return hipErrorInvalidValue;
+    const int NG = (a.E + 2 + 3) / 4;
+    hipLaunchKernelGGL(scan_kernel, dim3((NG + kScanGroups - 1) / kScanGroups), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1318,7 +1273,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
-    const int blk = t / kRouteBlock;
+    const int blk = t / a.rb;
     const int cap = a.cap[0];
     int e = 0, pos = -1, row = -1;  // position in expert order; xp row (tile image row when tiled)
     float g = 0.0f;
@@ -1327,7 +1282,7 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
         e = a.idx[ent];
         g = a.gates[ent];
         if (e > 0 && e <= a.E) {
-            const int rk = a.rank_base[(long long)blk * a.E + (e - 1)] + a.rank[ent];
+            const int rk = a.rank_base[(long long)blk * a.ldc + (e - 1)] + a.rank[ent];
             if (rk < cap) {
                 pos = a.offsets[e - 1] + rk;
                 row = a.tiled ? a.tile_start[e - 1] * a.bm + rk : pos;
@@ -1427,7 +1382,7 @@ __global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
-    const int blk = t / kRouteBlock;
+    const int blk = t / a.rb;
     const int cap = a.cap[0];
     int ee[2], pos[2], row[2];
     float g[2];
@@ -1440,7 +1395,7 @@ __global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
             ee[c] = a.idx[ent];
             g[c] = a.gates[ent];
             if (ee[c] > 0 && ee[c] <= a.E) {
-                const int rk = a.rank_base[(long long)blk * a.E + (ee[c] - 1)] + a.rank[ent];
+                const int rk = a.rank_base[(long long)blk * a.ldc + (ee[c] - 1)] + a.rank[ent];
                 if (rk < cap) {
                     pos[c] = a.offsets[ee[c] - 1] + rk;
                     row[c] = a.tiled ? a.tile_start[ee[c] - 1] * a.bm + rk : pos[c];
@@ -1491,7 +1446,7 @@ __global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
 
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
-    if (a.kt > 2 * 64) return hipErrorInvalidValue;
+    if (a.kt > 2 * 64 || a.rb < 1) return hipErrorInvalidValue;
     if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
     else hipLaunchKernelGGL(permute_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
