@@ -72,12 +72,16 @@ struct moe_handle {
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
     float *logits_in = nullptr;    // [T][Er] the caller's logits (routing from logits)
-    int rb = kRtMinBlock;          // tokens per route block of the last routing call (rows of rank_base)
-    int ldc = 0, lds = 0;          // row strides of blk_counts / rank_base and blk_stats (E, E + 2 rounded up to 4)
+    int rb = kRtMinBlock;          // tokens per route block of the last routing call
+    int ldc = 0;                   // row stride of blk_counts (E rounded up to 4)
+    int rpar = 0;                  // parity of the next routing call's totals buffers
+    ScanArgs scan{};               // the last routing call's scan (run by its permute)
     bool keep_rows = false;        // the next routing call writes logits / probs to global memory
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
-    double *blk_stats = nullptr;
-    int *counts = nullptr, *offsets = nullptr, *rank_base = nullptr, *cap = nullptr;
+    double *blk_zh = nullptr;                 // [nblk][2] per route block z-loss / entropy sums
+    int *tot_cnt2 = nullptr;                  // [2][E] expert counts of a call (two parities)
+    unsigned long long *tot_p2 = nullptr;     // [2][E] probability sums of a call, fixed point
+    int *counts = nullptr, *offsets = nullptr, *cap = nullptr;
     int2 *tiles = nullptr;
     int *num_tiles = nullptr;
     int *tile_start = nullptr;
@@ -97,9 +101,6 @@ struct moe_handle {
     int aux_update_freq = 1;
     long long aux_counter = 0;
     float *aux_bias = nullptr, *aux_mom = nullptr;
-    int *tot_counts = nullptr;       // scan work: column totals
-    double *tot_stats = nullptr;
-    unsigned *scan_ticket = nullptr; // scan work: finished column blocks
 
     int last_T = -1, last_training = 0, last_x_bf16 = 0;
     std::vector<void *> allocs;
@@ -542,10 +543,10 @@ static bool drop_active(const moe_handle *h) { return h->cfg.drop_tokens && h->l
 static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
     PermuteArgs pa{};
     pa.x = x_dev; pa.x_bf16 = x_bf16; pa.T = T; pa.D = h->D; pa.ld_xp = h->D_pad; pa.kt = h->kc; pa.E = h->E;
-    pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rank_base = h->rank_base; pa.rb = h->rb; pa.ldc = h->ldc;
-    pa.offsets = h->offsets; pa.cap = h->cap; pa.renorm = (training && drop_active(h)) ? 1 : 0;
+    pa.ct = h->ct; pa.idx = h->idx; pa.gates = h->gates; pa.rank = h->rank; pa.rb = h->rb; pa.s = h->scan;
+    pa.renorm = (training && drop_active(h)) ? 1 : 0;
     pa.perm = h->perm; pa.pos_of = h->pos_of; pa.gate_sorted = h->gate_sorted; pa.xp = h->xp;
-    pa.tiled = h->bf16_gemm ? 1 : 0; pa.bm = h->bm; pa.ktt = h->D_pad / 32; pa.tile_start = h->tile_start;
+    pa.tiled = h->bf16_gemm ? 1 : 0; pa.bm = h->bm; pa.ktt = h->D_pad / 32;
     pa.copy_rows = mode == PERMUTE_ROWS ? 1 : 0;
     HIP_TRY(h, launch_permute(pa, s));
     return MOE_OK;
@@ -579,21 +580,26 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
-    ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.blk_stats = h->blk_stats;
-    ra.ldc = h->ldc; ra.lds = h->lds;
+    // the call's totals buffers (parity rpar); the router's workgroup 0
+    // zeroes the other parity's for the next call
+    const int par = h->rpar;
+    h->rpar ^= 1;
+    ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.ldc = h->ldc; ra.blk_zh = h->blk_zh;
+    ra.tot_cnt = h->tot_cnt2 + (size_t)par * h->E; ra.tot_p = h->tot_p2 + (size_t)par * h->E;
+    ra.clr_cnt = h->tot_cnt2 + (size_t)(par ^ 1) * h->E; ra.clr_p = h->tot_p2 + (size_t)(par ^ 1) * h->E;
     ScanArgs sa{};
-    sa.blk_counts = h->blk_counts; sa.blk_stats = h->blk_stats;
-    sa.ldc = h->ldc; sa.lds = h->lds; sa.T = T; sa.E = h->E; sa.kt = h->kc;
+    sa.blk_counts = h->blk_counts; sa.ldc = h->ldc; sa.blk_zh = h->blk_zh;
+    sa.tot_cnt = ra.tot_cnt; sa.tot_p = ra.tot_p;
+    sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
     sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
-    sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets; sa.rank_base = h->rank_base;
+    sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets;
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
     sa.loss_out = loss_dev;
     sa.aux_free = aux; sa.aux_use_comp = h->aux_use_comp; sa.aux_update = aux_update;
     sa.aux_cw = h->aux_cw; sa.aux_lr = h->aux_lr; sa.aux_momentum = h->aux_momentum;
     sa.aux_bias = h->aux_bias; sa.aux_mom = h->aux_mom;
-    sa.tot_counts = h->tot_counts; sa.tot_stats = h->tot_stats; sa.ticket = h->scan_ticket;
     // logits / probs rows in global memory: for the caller, and for the
     // ExpertChoiceGating kernels that read them
     A.store_rows = (h->keep_rows || ec || !compute_logits) ? 1 : 0;
@@ -607,20 +613,17 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         A.npass = 1;
         ra.out_mask = ec ? ROUTE_OUT_PROBS : (ROUTE_OUT_PROBS | ROUTE_OUT_GATING);
     }
-    // the router kernel's last workgroup runs the scan, except for
-    // ExpertChoiceGating, whose slots come from its own kernels; their rank
-    // kernel works on route blocks of kRouteBlock tokens
-    A.tail = ec ? 0 : 1;
-    A.s = sa;
+    // ExpertChoiceGating's rank kernel works on route blocks of kRouteBlock tokens
     HIP_TRY(h, launch_router(A, ec ? kRouteBlock : 0, &h->rb, s));
     if (ec) {
         // the experts' choices give the slots, the stable ranks and the
-        // per-block histogram, then the scan
+        // per-block histogram
         HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
-                                        h->rank, h->blk_counts, h->ldc, s));
-        sa.nblk = (T + h->rb - 1) / h->rb;
-        HIP_TRY(h, launch_scan(sa, s));
+                                        h->rank, h->blk_counts, h->ldc, ra.tot_cnt, s));
     }
+    // the scan runs in the permute kernel (its workgroups are the route blocks)
+    sa.nblk = (T + h->rb - 1) / h->rb;
+    h->scan = sa;
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
 }
@@ -879,20 +882,17 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->gates, sizeof(float) * nent);
     A((void **)&h->rank, sizeof(int) * nent);
     h->ldc = (int)((E + 3) / 4 * 4);
-    h->lds = (int)((E + 2 + 3) / 4 * 4);
     A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * h->ldc);
-    A((void **)&h->blk_stats, sizeof(double) * (size_t)h->nblk_max * h->lds);
+    A((void **)&h->blk_zh, sizeof(double) * (size_t)h->nblk_max * 2);
+    A((void **)&h->tot_cnt2, sizeof(int) * 2 * E);
+    A((void **)&h->tot_p2, sizeof(unsigned long long) * 2 * E);
     A((void **)&h->counts, sizeof(int) * E);
     A((void **)&h->offsets, sizeof(int) * (E + 1));
-    A((void **)&h->rank_base, sizeof(int) * (size_t)h->nblk_max * h->ldc);
     A((void **)&h->cap, sizeof(int));
     A((void **)&h->tiles, sizeof(int2) * (size_t)h->max_tiles);
     A((void **)&h->num_tiles, sizeof(int));
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
-    A((void **)&h->tot_counts, sizeof(int) * E);
-    A((void **)&h->tot_stats, sizeof(double) * (E + 2));
-    A((void **)&h->scan_ticket, 256);
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
     A((void **)&h->aux_mom, sizeof(float) * h->Er);
@@ -928,7 +928,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
-    Z(h->scan_ticket, 256);
+    Z(h->tot_cnt2, sizeof(int) * 2 * E);
+    Z(h->tot_p2, sizeof(unsigned long long) * 2 * E);
     Z(h->aux_bias, sizeof(float) * h->Er);
     Z(h->aux_mom, sizeof(float) * h->Er);
     Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);

@@ -11,6 +11,8 @@ namespace moe {
 constexpr int kRouteBlock = 32;    // tokens per routing block of the ExpertChoiceGating kernels
 constexpr int kRtThreads = 512;    // threads per router_kernel workgroup (8 per token)
 constexpr int kRtMinBlock = 16;    // fewest tokens per router_kernel workgroup
+constexpr int kPermThreads = 1024; // threads per permute workgroup (one route block)
+constexpr double kPsumScale = 281474976710656.0;  // 2^48: fixed-point scale of the probability sums
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
 constexpr int kKPad = 64;          // K padding of packed weights and activation rows
@@ -75,8 +77,8 @@ struct RouterArgs {
 // Outputs of one gating pass of router_kernel.  A plain forward writes both;
 // with an AuxiliaryFreeLoss the probabilities pass runs on the router logits
 // and the gating pass on logits + the loss's bias (src/core/moe_layer.jl:137-140).
-enum { ROUTE_OUT_PROBS = 1,    // logits, probs, per-block probability / z / entropy sums
-       ROUTE_OUT_GATING = 2 }; // indices, gates, ranks, per-block expert counts
+enum { ROUTE_OUT_PROBS = 1,    // logits, probs, probability sums, per-block z / entropy sums
+       ROUTE_OUT_GATING = 2 }; // indices, gates, ranks, per-block and total expert counts
 
 struct RouteArgs {
     const float *part;     // [T][Er] the caller's router logits (when no logits GEMM runs)
@@ -96,14 +98,27 @@ struct RouteArgs {
     float *gates;          // [T][kt]
     int *rank;             // [T][kt] rank of the entry inside its block & expert
     int *blk_counts;       // [nblk][ldc]: entries per expert (columns < Eh)
-    double *blk_stats;     // [nblk][lds]: prob sums (0 past E), sum lse^2, sum entropy (columns < Eh + 2)
-    int ldc, lds;          // row strides: Eh and Eh + 2 rounded up to 4
+    int ldc;               // row stride of blk_counts (Eh rounded up to 4)
+    double *blk_zh;        // [nblk][2]: the route block's sums of lse^2 and of the entropy
+    // totals over the call's route blocks, by integer atomics (order-free, so
+    // deterministic): entries per expert [Eh], probability sums per router
+    // row [E] in fixed point (kPsumScale); the call's parity of two buffers,
+    // block 0 zeroes the other parity's for the next call
+    int *tot_cnt;
+    unsigned long long *tot_p;
+    int *clr_cnt;
+    unsigned long long *clr_p;
 };
 
+// The scan of a routing call, run by every permute workgroup (its route
+// block's rank bases, the offsets and tile starts) and, for the outputs and
+// losses, by workgroup 0.
 struct ScanArgs {
     const int *blk_counts;  // [nblk][ldc]
-    const double *blk_stats;  // [nblk][lds]
-    int ldc, lds;           // row strides (also of rank_base: ldc)
+    int ldc;
+    const double *blk_zh;   // [nblk][2]
+    const int *tot_cnt;     // [E] entries per expert (before capacity)
+    const unsigned long long *tot_p;  // [Np] probability sums, fixed point
     int nblk, T, E, kt;   // E: experts of the histogram
     int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
     int training, drop, z_enabled;
@@ -112,7 +127,6 @@ struct ScanArgs {
     int *tile_start;       // [E+1] first M tile of each expert (sum of ceil(count / bm))
     int *counts;           // [E]   (after capacity)
     int *offsets;          // [E+1]
-    int *rank_base;        // [nblk][ldc] rank of the block's first entry per expert
     int *cap_out;          // [1] capacity (INT_MAX when unused)
     int2 *tiles;           // [max_tiles] (expert, m0)
     int *num_tiles;        // [1]
@@ -124,9 +138,6 @@ struct ScanArgs {
     int aux_free, aux_use_comp, aux_update;
     float aux_cw, aux_lr, aux_momentum;
     float *aux_bias, *aux_mom;  // [E] device state
-    int *tot_counts;            // [E]   work: column totals of blk_counts
-    double *tot_stats;          // [E+2] work: column totals of blk_stats
-    unsigned *ticket;           // [1]   work: finished column blocks (0 between launches)
 };
 
 // One router_kernel launch: logits (GEMM of g, or r.part), then one or two
@@ -141,8 +152,6 @@ struct RtArgs {
     int npass;             // 2: AuxiliaryFreeLoss (probabilities pass, then gating on logits + aux_bias)
     const float *aux_bias; // [Er]
     int store_rows;        // write logits / probs [T][Er] to global memory
-    int tail;              // the last workgroup to finish runs the scan (s)
-    ScanArgs s;
 };
 
 struct PermuteArgs {
@@ -150,12 +159,9 @@ struct PermuteArgs {
     int T, D, ld_xp, kt, E;
     int ct;                      // compute type of xp
     int *idx; float *gates;      // [T][kt] (rewritten under capacity)
-    const int *rank;             // [T][kt]
-    int rb;                      // tokens per route block (rows of rank_base)
-    int ldc;                     // row stride of rank_base
-    const int *rank_base;        // [nblk][ldc]
-    const int *offsets;          // [E+1]
-    const int *cap;              // [1]
+    const int *rank;             // [T][kt] rank inside the route block and expert
+    int rb;                      // tokens per route block (one workgroup each)
+    ScanArgs s;                  // the scan (route-block rows and totals)
     int renorm;                  // capacity active: renormalise gates
     int *perm;                   // [T*kt]
     int *pos_of;                 // [T*kt] (-1 = dropped)
@@ -166,7 +172,6 @@ struct PermuteArgs {
     // expert e's rank rk is row (rk mod bm) of M tile tile_start[e] + rk / bm,
     // ktt = 32-wide K stages per row
     int tiled, bm, ktt;
-    const int *tile_start;       // [E+1]
 };
 
 // Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots (one
@@ -258,13 +263,14 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp
 // the routing call's router_kernel launch; tb_force > 0 fixes the tokens per
 // workgroup (else chosen here); *tb receives them (rows of the scan)
 hipError_t launch_router(RtArgs a, int tb_force, int *tb, hipStream_t s);
-hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
 // ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
 // gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
 // bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
-// expert's entries in its route block) and blk_counts [nblk][E]
+// expert's entries in its route block), blk_counts [nblk][ldc] and the
+// totals tot_cnt [E] (atomic adds)
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, hipStream_t s);
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
+                                hipStream_t s);
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 // compute_loss(::SwitchTransformerLoss) on device buffers in two launches

@@ -87,21 +87,15 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp
 //      caller's logits), plus the router bias;
 //   2. gates them, 8 lanes per token (softmax, top-k, gates);
 //   3. writes the entries, the stable rank of each inside the route block
-//      and expert, the route block's expert histogram and its probability,
-//      z-loss and entropy sums (the scan turns them into offsets, tile lists
-//      and losses).
+//      and expert, the route block's expert histogram and z-loss / entropy
+//      sums, and adds its expert counts and probability sums (fixed point)
+//      to the call's totals with integer atomics (the permute kernel's scan
+//      turns them into rank bases, offsets, tile lists and losses).
 // With an AuxiliaryFreeLoss the gating runs twice on the same LDS logits:
 // the probabilities pass on the logits, then the gating pass on logits + the
 // loss's bias.
 // ============================================================================
 #define RT_LDS __attribute__((address_space(3)))
-
-// LDS of the scan phases (scan_columns on nth threads, scan_finish_block, and
-// both as the router kernel's tail)
-__host__ __device__ constexpr int scan_ws_bytes(int nth) { return nth * 48; }
-constexpr int kScanFinishWs = 2560;
-constexpr int scan_tail_lds_bytes(int nth) { return scan_ws_bytes(nth) + 16 * (MOE_MAX_EXPERTS + 8) + kScanFinishWs; }
-__device__ __forceinline__ void scan_tail(const ScanArgs &a, uint8_t *lds);
 
 // LDS byte address of a pointer into the workgroup's LDS (the M0 operand of
 // global_load_lds).
@@ -117,27 +111,6 @@ __device__ __forceinline__ void rt_dma16(const void *gaddr, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds));
 }
 __device__ __forceinline__ void rt_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Rows that the router kernel's last workgroup reads from the other
-// workgroups (the route-block histogram and statistics) are stored and loaded
-// as agent-scope relaxed atomics: sc1 accesses, coherent across the XCDs'
-// L2 caches without a full-L2 writeback / invalidate (a device-scope fence
-// in every workgroup would write back and invalidate each XCD's L2 while the
-// other workgroups still read the router weight from it).
-__device__ __forceinline__ void st_agent(int *p, int v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(double *p, double v) {
-    __hip_atomic_store((unsigned long long *)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_agent(const int *p) {
-    return __hip_atomic_load((int *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ double ld_agent(const double *p) {
-    return __longlong_as_double(
-        (long long)__hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
 
 constexpr int kRtMaskWords = 16;  // rank bitmask words per expert: TB * kt <= 64 * 8 entries
 
@@ -667,16 +640,18 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         if (out_gating) {
             int c = 0;
             for (int wd = 0; wd < TW; ++wd) c += __popc(emask[e * kRtMaskWords + wd]);
-            st_agent(&a.blk_counts[(long long)blk * a.ldc + e], c);
+            a.blk_counts[(long long)blk * a.ldc + e] = c;
+            if (c) atomicAdd(&a.tot_cnt[e], c);
         }
-        if (out_probs) {
-            // per-row probability sums (Switch loss P_e) in fp64, token order
+        if (out_probs && e < E) {
+            // per-row probability sums (Switch loss P_e): fp64 over the route
+            // block's tokens in token order, added to the call's total in
+            // fixed point (scale 2^48, at most 2^54 per route block)
             double ps = 0.0;
-            if (e < E) {
 #pragma unroll 8
-                for (int i = 0; i < ntok; ++i) ps += (double)Pr[i * RW + e];
-            }
-            st_agent(&a.blk_stats[(long long)blk * a.lds + e], ps);
+            for (int i = 0; i < ntok; ++i) ps += (double)Pr[i * RW + e];
+            const unsigned long long fx = __double2ull_rn(ps * kPsumScale);
+            if (fx) atomicAdd(&a.tot_p[e], fx);
         }
     }
     if (tid == 0 && out_probs) {
@@ -686,8 +661,8 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             zb += wred[0][wd];
             hb += wred[1][wd];
         }
-        st_agent(&a.blk_stats[(long long)blk * a.lds + a.Eh], zb);
-        st_agent(&a.blk_stats[(long long)blk * a.lds + a.Eh + 1], hb);
+        a.blk_zh[(long long)blk * 2] = zb;
+        a.blk_zh[(long long)blk * 2 + 1] = hb;
     }
 }
 
@@ -708,6 +683,13 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
     const int ntok = min(A.TB, A.r.T - t0);
     float *L = (float *)(rdyn + A.off_L);
     float *Pr = (float *)rdyn;  // over the staging region, free once the logits are in L
+    if (blk == 0) {
+        // the other parity's totals, last read by the previous call's permute
+        for (int e = threadIdx.x; e < A.r.Eh; e += kRtThreads) {
+            A.r.clr_cnt[e] = 0;
+            A.r.clr_p[e] = 0ull;
+        }
+    }
     if constexpr (LG > 0) {
         rt_logits<LG == 1, PAIRED>(A, t0, rdyn, L);
     } else {
@@ -724,22 +706,6 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
         rt_gate<EPL>(A, ROUTE_OUT_GATING, A.aux_bias, blk, t0, ntok, L, Pr, emask, wred);
     } else {
         rt_gate<EPL>(A, A.r.out_mask, nullptr, blk, t0, ntok, L, Pr, emask, wred);
-    }
-    if (A.tail) {
-        // the workgroup that finishes last runs the scan: every workgroup
-        // waits until its agent-scope row stores are complete, then takes a
-        // ticket; the last ticket's workgroup reads the rows with agent-scope
-        // loads and resets the ticket for the next launch (which stream order
-        // puts after this one)
-        __shared__ bool last;
-        rt_wait_vm0();
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(A.s.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-        __syncthreads();
-        if (!last) return;
-        if (threadIdx.x == 0) __hip_atomic_store(A.s.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        scan_tail(A.s, rdyn);
     }
 }
 
@@ -803,16 +769,10 @@ hipError_t launch_router(RtArgs A, int tb_force, int *tb, hipStream_t s) {
         region0 = std::max(region0, std::max((size_t)TB * A.RB, part));
     }
     A.off_L = (int)((region0 + 1023) & ~(size_t)1023);
-    size_t lds = (size_t)A.off_L + rows;
+    const size_t lds = (size_t)A.off_L + rows;
     const int nblk = (a.T + TB - 1) / TB;
-    if (A.tail) {
-        const ScanArgs &sc = A.s;
-        if (!sc.ticket || sc.E != a.Eh || sc.ldc % 4 || sc.lds % 4 || sc.ldc < sc.E || sc.lds < sc.E + 2)
-            return hipErrorInvalidValue;
-        A.s.nblk = nblk;
-        lds = std::max(lds, (size_t)scan_tail_lds_bytes(kRtThreads));
-    }
-    if (lds > lds_max) return hipErrorInvalidValue;
+    if (lds > lds_max || a.ldc < a.Eh || !a.tot_cnt || !a.tot_p || !a.clr_cnt || !a.clr_p || !a.blk_zh)
+        return hipErrorInvalidValue;
     const int epl = route_epl(Er);
 #define MOE_RT(LG_, P_, EPL_) return launch_router_case<LG_, P_, EPL_>(A, nblk, lds, s)
 #define MOE_RT_EPL(LG_)                 \
@@ -930,7 +890,8 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
 // tokens that hold e.
 __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
                                                                             int E, int kt, int *rank,
-                                                                            int *blk_counts, int ldc) {
+                                                                            int *blk_counts, int ldc,
+                                                                            int *tot_cnt) {
     const int e = threadIdx.x;
     if (e >= E) return;
     const int t0 = blockIdx.x * kRouteBlock;
@@ -944,24 +905,26 @@ __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(con
         }
     }
     blk_counts[(long long)blockIdx.x * ldc + e] = c;
+    if (c) atomicAdd(&tot_cnt[e], c);
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, hipStream_t s) {
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
+                                hipStream_t s) {
     if (T <= 0) return hipSuccess;
     if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255 || ldc < E) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
                        min(C, E), idx, gates);
     hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + kRouteBlock - 1) / kRouteBlock), dim3(MOE_MAX_EXPERTS),
-                       0, s, sel, T, E, kt, rank, blk_counts, ldc);
+                       0, s, sel, T, E, kt, rank, blk_counts, ldc, tot_cnt);
     return hipGetLastError();
 }
 
 // ============================================================================
-// Scan: per-expert totals, per-block rank bases (many blocks), then the
-// capacity clamp, offsets, the (expert, m0) GEMM tile list and the loss
-// scalars (one block).
+// Scan: the route blocks' rank bases, the capacity clamp, offsets, the
+// (expert, m0) GEMM tile list and the loss scalars, at the start of the
+// permute kernel.
 // ============================================================================
 // update_bias!(::AuxiliaryFreeLoss, expert_indices) after its counter check
 // (src/balancing/auxiliary_free.jl:36-69), one thread, with Julia's types:
@@ -985,136 +948,29 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
     for (int e = 0; e < E; ++e) bias[e] = bias[e] - mean;
 }
 
-// Scan, column phase: for each column c of the route-block rows (counts
-// blk_counts[b][c], c < E; fp64 statistics blk_stats[b][c], c < E + 2: the
-// probability sums, then the z and entropy sums) the rank bases
-// rank_base[b][c] (the counts of the rows before b) and the column totals
-// (the chunks' sums added in chunk order; a chunk's rows in row order) into
-// tc / ts.  Thread (g, q) owns columns 4 (g0 + g) .. +3 (one 16-byte count
-// load and two 16-byte statistics loads per row) and row chunk q; the block
-// covers column groups g0 .. g0 + ng - 1.  ws: LDS, scan_ws_bytes(threads).
-constexpr int kScanGroups = 2;       // column groups per block of scan_kernel
+// Scan, run by every permute workgroup for its route block blk: the
+// capacity, the expert counts after capacity (from the call's totals), their
+// offsets and GEMM tile starts (exclusive prefixes over the experts), and the
+// route block's rank bases (the counts of the route blocks before it, summed
+// with integer LDS atomics).  Workgroup 0 also writes the offsets, counts,
+// tile starts, the (expert, m0) GEMM tile list and the capacity, computes the
+// Switch and z losses and the mean entropy, and runs the AuxiliaryFreeLoss
+// step.  Ends with a barrier.
+struct ScanLds {
+    int cnt[MOE_MAX_EXPERTS];
+    int base[MOE_MAX_EXPERTS];
+    int off[MOE_MAX_EXPERTS + 1];
+    int tstart[MOE_MAX_EXPERTS + 1];
+    float fp[MOE_MAX_EXPERTS];
+    double zh[2];
+    int cap;
+    float lsum;
+};
 
-__device__ __forceinline__ void scan_columns(const ScanArgs &a, int g0, int ng, uint8_t *ws, int *tc, double *ts) {
+__device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &L) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x, nth = blockDim.x;
-    const int NC = a.E + 2;
-    const int C = max(1, min(nth / ng, a.nblk / 4));  // row chunks (of at least 4 rows)
-    const int R = (a.nblk + C - 1) / C;
-    int *csum = (int *)ws;                     // [C][ng][4]
-    double *ssum = (double *)(ws + 16 * nth);  // [C][ng][4]
-    const int gl = tid % ng, q = tid / ng;
-    const int c0 = 4 * (g0 + gl);
-    const bool act = q < C && c0 < NC;
-    const bool cnt_grp = c0 < a.ldc;  // the group has count columns
-    const int b0 = min(a.nblk, q * R), b1 = min(a.nblk, b0 + R);
-    int cs[4] = {0, 0, 0, 0};
-    double ss[4] = {0.0, 0.0, 0.0, 0.0};
-    if (act) {
-#pragma unroll 4
-        for (int b = b0; b < b1; ++b) {
-            const int *cr = a.blk_counts + (long long)b * a.ldc + c0;
-            const double *sr = a.blk_stats + (long long)b * a.lds + c0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (cnt_grp) cs[i] += ld_agent(cr + i);
-                ss[i] += ld_agent(sr + i);
-            }
-        }
-        const int o = (q * ng + gl) * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            csum[o + i] = cs[i];
-            ssum[o + i] = ss[i];
-        }
-    }
-    __syncthreads();
-    if (act && cnt_grp) {
-        // the chunk's base, then its rows in order
-        int base[4] = {0, 0, 0, 0};
-        for (int qq = 0; qq < q; ++qq)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) base[i] += csum[(qq * ng + gl) * 4 + i];
-#pragma unroll 4
-        for (int b = b0; b < b1; ++b) {
-            const int *cr = a.blk_counts + (long long)b * a.ldc + c0;
-            int cv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cv[i] = ld_agent(cr + i);
-            *(int4 *)(a.rank_base + (long long)b * a.ldc + c0) = make_int4(base[0], base[1], base[2], base[3]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) base[i] += cv[i];
-        }
-    }
-    if (act && q == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = c0 + i;
-            if (c >= NC) break;
-            int tcv = 0;
-            double tsv = 0.0;
-            for (int qq = 0; qq < C; ++qq) {
-                tcv += csum[(qq * ng + gl) * 4 + i];
-                tsv += ssum[(qq * ng + gl) * 4 + i];
-            }
-            if (c < a.E) tc[c] = tcv;
-            ts[c] = tsv;
-        }
-    }
-}
-
-__device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *tcnt, const double *tstat, uint8_t *ws);
-
-// Scan of a routing call whose route blocks were not scanned by the router
-// kernel (ExpertChoiceGating): blocks of kScanGroups column groups run the
-// column phase with the totals to global memory; the block that finishes
-// last runs the finish phase on them.  Every block publishes its totals
-// (release fence), then takes a ticket; the last ticket's block acquires
-// them and resets the ticket for the next launch (which stream order puts
-// after this one).
-__global__ __launch_bounds__(256) void scan_kernel(ScanArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t ws[scan_ws_bytes(256)];
-    __shared__ __attribute__((aligned(16))) uint8_t fws[kScanFinishWs];
-    const int NG = (a.E + 2 + 3) / 4;
-    const int g0 = blockIdx.x * kScanGroups;
-    scan_columns(a, g0, min(kScanGroups, NG - g0), ws, a.tot_counts, a.tot_stats);
-    __shared__ bool last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    if (threadIdx.x == 0) *a.ticket = 0u;
-    scan_finish_block(a, a.tot_counts, a.tot_stats, fws);
-}
-
-// The scan run by the router kernel's last workgroup: the column phase of
-// every column on this workgroup, totals in LDS, then the finish phase.
-__device__ __forceinline__ void scan_tail(const ScanArgs &a, uint8_t *lds) {
-    const int NG = (a.E + 2 + 3) / 4;
-    uint8_t *ws = lds;
-    int *tc = (int *)(lds + scan_ws_bytes(blockDim.x));
-    double *ts = (double *)(lds + scan_ws_bytes(blockDim.x) + 8 * (MOE_MAX_EXPERTS + 8));
-    uint8_t *fws = lds + scan_ws_bytes(blockDim.x) + 16 * (MOE_MAX_EXPERTS + 8);
-    scan_columns(a, 0, NG, ws, tc, ts);
-    __syncthreads();
-    scan_finish_block(a, tc, ts, fws);
-}
-
-// Scan, part 2: one block (the last of part 1).  Capacity clamp, offsets,
-// per-expert GEMM tile starts and the (expert, m0) tile list, the Switch and
-// z losses, the mean entropy and the AuxiliaryFreeLoss step, from the column
-// totals.
-__device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *tcnt, const double *tstat, uint8_t *ws) {
-#pragma clang fp contract(off)
-    int *cnt = (int *)ws;                       // [MOE_MAX_EXPERTS]
-    int *off = cnt + MOE_MAX_EXPERTS;           // [MOE_MAX_EXPERTS + 1]
-    int *tstart = off + MOE_MAX_EXPERTS + 1;    // [MOE_MAX_EXPERTS + 1]
-    float *fp = (float *)(tstart + MOE_MAX_EXPERTS + 1);  // [MOE_MAX_EXPERTS]
-    int &cap_s = *(int *)(fp + MOE_MAX_EXPERTS);
-    float &lsum_s = *(float *)(fp + MOE_MAX_EXPERTS + 1);
-    const int tid = threadIdx.x, nth = blockDim.x;
+    const bool writer = blk == 0;
     if (tid == 0) {
         int cap = INT_MAX;
         if (a.training && a.drop) {
@@ -1122,22 +978,61 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *
             const float cf = ceilf((a.capacity_factor * (float)a.T) / (float)a.E);
             cap = (cf >= 2147483647.0f) ? INT_MAX : (int)cf;
         }
-        cap_s = cap;
-        a.cap_out[0] = cap;
+        L.cap = cap;
     }
+    for (int e = tid; e < a.E; e += nth) L.base[e] = 0;
     __syncthreads();
+    {
+        // rank bases: thread (g, q) sums experts 4 g .. 4 g + 3 over its chunk
+        // of the route blocks before blk
+        const int ng = (a.E + 3) / 4;
+        const int C = max(1, nth / ng);
+        const int R = (blk + C - 1) / C;
+        const int g = tid % ng, q = tid / ng;
+        if (q < C && blk > 0) {
+            const int b0 = min(blk, q * R), b1 = min(blk, b0 + R);
+            int s[4] = {0, 0, 0, 0};
+#pragma unroll 4
+            for (int b = b0; b < b1; ++b) {
+                const int4 v = *(const int4 *)(a.blk_counts + (long long)b * a.ldc + 4 * g);
+                s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i < a.E && s[i]) atomicAdd(&L.base[4 * g + i], s[i]);
+        }
+    }
     const float total = (float)((long long)a.T * a.kl);
     for (int e = tid; e < a.E; e += nth) {
-        const int ce = min(tcnt[e], cap_s);
-        cnt[e] = ce;
+        const int ce = min(a.tot_cnt[e], L.cap);
+        L.cnt[e] = ce;
         // the terms f_e * P_e of the Switch loss (src/balancing/losses.jl:15-36)
         // over the a.Np probability rows; with shared experts of the layer the
         // ids are the shifted routed ids and expert e < lsh holds none of them
-        if (e < a.Np) {
+        if (writer && e < a.Np) {
             float f = (e < a.lsh) ? 0.0f : (float)ce;
             if (a.T * a.kl > 0) f = f / total;
-            const float P = (float)tstat[e] / (float)a.T;
-            fp[e] = f * P;
+            const float P = (float)((double)a.tot_p[e] / kPsumScale) / (float)a.T;
+            L.fp[e] = f * P;
+        }
+    }
+    if (writer && tid >= 64 && tid < 128) {
+        // the z and entropy sums over the route blocks: lane l takes rows
+        // l, l + 64, ... in order, then a fixed butterfly over the lanes
+        const int l = tid - 64;
+        double z = 0.0, hh = 0.0;
+        for (int b = l; b < a.nblk; b += 64) {
+            z += a.blk_zh[(long long)b * 2];
+            hh += a.blk_zh[(long long)b * 2 + 1];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            z = z + __shfl_xor(z, o);
+            hh = hh + __shfl_xor(hh, o);
+        }
+        if (l == 0) {
+            L.zh[0] = z;
+            L.zh[1] = hh;
         }
     }
     __syncthreads();
@@ -1145,7 +1040,7 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *
     // wave 0 (lane l holds experts 2 l and 2 l + 1; E <= 128)
     if (tid < 64) {
         const int e0 = 2 * tid, e1 = e0 + 1;
-        const int c0 = (e0 < a.E) ? cnt[e0] : 0, c1 = (e1 < a.E) ? cnt[e1] : 0;
+        const int c0 = (e0 < a.E) ? L.cnt[e0] : 0, c1 = (e1 < a.E) ? L.cnt[e1] : 0;
         const int n0 = (c0 + a.bm - 1) / a.bm, n1 = (c1 + a.bm - 1) / a.bm;
         int cs = c0 + c1, ns = n0 + n1;
 #pragma unroll
@@ -1158,38 +1053,41 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *
         }
         const int ce = cs - (c0 + c1), ne = ns - (n0 + n1);  // exclusive
         if (e0 <= a.E) {
-            off[e0] = ce;
-            tstart[e0] = ne;
+            L.off[e0] = ce;
+            L.tstart[e0] = ne;
         }
         if (e1 <= a.E) {
-            off[e1] = ce + c0;
-            tstart[e1] = ne + n0;
+            L.off[e1] = ce + c0;
+            L.tstart[e1] = ne + n0;
         }
         if (tid == 63) {  // the totals (also for E = 128, past the last pair)
-            off[a.E] = cs;
-            tstart[a.E] = ns;
+            L.off[a.E] = cs;
+            L.tstart[a.E] = ns;
         }
-        // the Switch-loss sum over the a.Np terms: in expert order up to 16
-        // experts (Julia's sequential sum), else a fixed tree (Julia's order
-        // for longer arrays is its SIMD reduction, not reproduced)
-        float part = 0.0f;
-        if (a.Np > 16) {
-            part = (e0 < a.Np) ? fp[e0] : 0.0f;
-            if (e1 < a.Np) part = part + fp[e1];
+        if (writer) {
+            // the Switch-loss sum over the a.Np terms: in expert order up to 16
+            // experts (Julia's sequential sum), else a fixed tree (Julia's order
+            // for longer arrays is its SIMD reduction, not reproduced)
+            float part = 0.0f;
+            if (a.Np > 16) {
+                part = (e0 < a.Np) ? L.fp[e0] : 0.0f;
+                if (e1 < a.Np) part = part + L.fp[e1];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) part = part + __shfl_xor(part, o);
-        } else if (tid == 0) {
-            part = fp[0];
-            for (int e = 1; e < a.Np; ++e) part = part + fp[e];
+                for (int o = 32; o > 0; o >>= 1) part = part + __shfl_xor(part, o);
+            } else if (tid == 0) {
+                part = L.fp[0];
+                for (int e = 1; e < a.Np; ++e) part = part + L.fp[e];
+            }
+            if (tid == 0) L.lsum = part;
         }
-        if (tid == 0) lsum_s = part;
     }
     __syncthreads();
+    if (!writer) return;
     if (tid == 0) {
-        const int ts = tstart[a.E];
-        a.num_tiles[0] = ts;
-        const double zs = tstat[a.E], hs = tstat[a.E + 1];
-        const float s = lsum_s;
+        a.cap_out[0] = L.cap;
+        a.num_tiles[0] = L.tstart[a.E];
+        const double zs = L.zh[0], hs = L.zh[1];
+        const float s = L.lsum;
         // AuxiliaryFreeLoss: complementary_weight * Switch(1.0f0) or 0.0f0
         // (src/balancing/auxiliary_free.jl:78-87)
         float sw;
@@ -1206,28 +1104,19 @@ __device__ __forceinline__ void scan_finish_block(const ScanArgs &a, const int *
         if (a.aux_free && a.training && a.aux_update) {
             // the kept entries of each expert are the counts after capacity
             long long kept = 0;
-            for (int e = 0; e < a.E; ++e) kept += cnt[e];
-            aux_free_step(cnt, kept, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
+            for (int e = 0; e < a.E; ++e) kept += L.cnt[e];
+            aux_free_step(L.cnt, kept, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
         }
     }
-    __syncthreads();
     for (int e = tid; e <= a.E; e += nth) {
-        a.offsets[e] = off[e];
-        a.tile_start[e] = tstart[e];
+        a.offsets[e] = L.off[e];
+        a.tile_start[e] = L.tstart[e];
     }
     for (int e = tid; e < a.E; e += nth) {
-        a.counts[e] = cnt[e];
-        const int nt = tstart[e + 1] - tstart[e];
-        for (int i = 0; i < nt; ++i) a.tiles[tstart[e] + i] = make_int2(e, i * a.bm);
+        a.counts[e] = L.cnt[e];
+        const int nt = L.tstart[e + 1] - L.tstart[e];
+        for (int i = 0; i < nt; ++i) a.tiles[L.tstart[e] + i] = make_int2(e, i * a.bm);
     }
-}
-
-hipError_t launch_scan(const ScanArgs &a, hipStream_t s) {
-    if (!a.ticket || a.E > MOE_MAX_EXPERTS || a.ldc % 4 || a.lds % 4 || a.ldc < a.E || a.lds < a.E + 2)
-        return hipErrorInvalidValue;
-    const int NG = (a.E + 2 + 3) / 4;
-    hipLaunchKernelGGL(scan_kernel, dim3((NG + kScanGroups - 1) / kScanGroups), dim3(256), 0, s, a);
-    return hipGetLastError();
 }
 
 // Element offset in xp of column col of row q: row-major (row stride ld_xp),
@@ -1264,17 +1153,14 @@ __device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int row, i
 }
 
 // ============================================================================
-// Permute: one wave per token.  Lanes < kt finalise the token's entries
-// (capacity drop + renormalisation, position), then the wave copies the
-// token's row into every position it owns, converting to the GEMM type.
+// Permute: one workgroup per route block (the scan first), then one wave per
+// token.  Lanes < kt finalise the token's entries (capacity drop +
+// renormalisation, position), then the wave copies the token's row into
+// every position it owns, converting to the GEMM type.
 // ============================================================================
-__global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
+__device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int lane, const ScanLds &L) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= a.T) return;
-    const int blk = t / a.rb;
-    const int cap = a.cap[0];
+    const int cap = L.cap;
     int e = 0, pos = -1, row = -1;  // position in expert order; xp row (tile image row when tiled)
     float g = 0.0f;
     if (lane < a.kt) {
@@ -1282,10 +1168,10 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
         e = a.idx[ent];
         g = a.gates[ent];
         if (e > 0 && e <= a.E) {
-            const int rk = a.rank_base[(long long)blk * a.ldc + (e - 1)] + a.rank[ent];
+            const int rk = L.base[e - 1] + a.rank[ent];
             if (rk < cap) {
-                pos = a.offsets[e - 1] + rk;
-                row = a.tiled ? a.tile_start[e - 1] * a.bm + rk : pos;
+                pos = L.off[e - 1] + rk;
+                row = a.tiled ? L.tstart[e - 1] * a.bm + rk : pos;
             } else {
                 e = 0;
                 g = 0.0f;
@@ -1373,17 +1259,21 @@ __global__ __launch_bounds__(256) void permute_kernel(PermuteArgs a) {
     }
 }
 
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
+    __shared__ ScanLds L;
+    scan_block(a.s, blockIdx.x, L);
+    const int lane = threadIdx.x & 63;
+    const int t1 = min(a.T, (blockIdx.x + 1) * a.rb);
+    for (int t = blockIdx.x * a.rb + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64) permute_token(a, t, lane, L);
+}
+
 // Permute for more slots per token than a wave has lanes (ExpertChoiceGating
 // with min(capacity, E) > 64; kt <= MOE_MAX_EXPERTS): lane l owns entries l
 // and l + 64; same finalisation as permute_kernel, then one row copy per kept
 // entry, element by element (most of these slots are empty).
-__global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
+__device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, int lane, const ScanLds &L) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= a.T) return;
-    const int blk = t / a.rb;
-    const int cap = a.cap[0];
+    const int cap = L.cap;
     int ee[2], pos[2], row[2];
     float g[2];
 #pragma unroll
@@ -1395,10 +1285,10 @@ __global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
             ee[c] = a.idx[ent];
             g[c] = a.gates[ent];
             if (ee[c] > 0 && ee[c] <= a.E) {
-                const int rk = a.rank_base[(long long)blk * a.ldc + (ee[c] - 1)] + a.rank[ent];
+                const int rk = L.base[ee[c] - 1] + a.rank[ent];
                 if (rk < cap) {
-                    pos[c] = a.offsets[ee[c] - 1] + rk;
-                    row[c] = a.tiled ? a.tile_start[ee[c] - 1] * a.bm + rk : pos[c];
+                    pos[c] = L.off[ee[c] - 1] + rk;
+                    row[c] = a.tiled ? L.tstart[ee[c] - 1] * a.bm + rk : pos[c];
                 } else {
                     ee[c] = 0;
                     g[c] = 0.0f;
@@ -1444,11 +1334,23 @@ __global__ __launch_bounds__(256) void permute_wide_kernel(PermuteArgs a) {
     }
 }
 
+__global__ __launch_bounds__(kPermThreads) void permute_wide_kernel(PermuteArgs a) {
+    __shared__ ScanLds L;
+    scan_block(a.s, blockIdx.x, L);
+    const int lane = threadIdx.x & 63;
+    const int t1 = min(a.T, (blockIdx.x + 1) * a.rb);
+    for (int t = blockIdx.x * a.rb + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
+        permute_wide_token(a, t, lane, L);
+}
+
 hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
-    if (a.kt > 2 * 64 || a.rb < 1) return hipErrorInvalidValue;
-    if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(permute_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
+    const int nblk = (a.T + a.rb - 1) / a.rb;
+    if (a.kt > 2 * 64 || a.rb < 1 || a.s.nblk != nblk || a.s.E > MOE_MAX_EXPERTS || a.s.ldc < a.s.E ||
+        a.s.ldc % 4)
+        return hipErrorInvalidValue;
+    if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3(nblk), dim3(kPermThreads), 0, s, a);
+    else hipLaunchKernelGGL(permute_kernel, dim3(nblk), dim3(kPermThreads), 0, s, a);
     return hipGetLastError();
 }
 
