@@ -81,6 +81,8 @@ struct moe_handle {
     double *blk_zh = nullptr;                 // [nblk][2] per route block z-loss / entropy sums
     int *tot_cnt2 = nullptr;                  // [2][E] expert counts of a call (two parities)
     unsigned long long *tot_p2 = nullptr;     // [2][E] probability sums of a call, fixed point
+    int *sup_cnt2 = nullptr;                  // [2][nsup_max][ldc] expert counts per super block
+    int nsup_max = 0;
     int *counts = nullptr, *offsets = nullptr, *cap = nullptr;
     int2 *tiles = nullptr;
     int *num_tiles = nullptr;
@@ -587,9 +589,12 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.ldc = h->ldc; ra.blk_zh = h->blk_zh;
     ra.tot_cnt = h->tot_cnt2 + (size_t)par * h->E; ra.tot_p = h->tot_p2 + (size_t)par * h->E;
     ra.clr_cnt = h->tot_cnt2 + (size_t)(par ^ 1) * h->E; ra.clr_p = h->tot_p2 + (size_t)(par ^ 1) * h->E;
+    ra.nsup_max = h->nsup_max;
+    ra.sup_cnt = h->sup_cnt2 + (size_t)par * h->nsup_max * h->ldc;
+    ra.clr_sup = h->sup_cnt2 + (size_t)(par ^ 1) * h->nsup_max * h->ldc;
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.ldc = h->ldc; sa.blk_zh = h->blk_zh;
-    sa.tot_cnt = ra.tot_cnt; sa.tot_p = ra.tot_p;
+    sa.tot_cnt = ra.tot_cnt; sa.tot_p = ra.tot_p; sa.sup_cnt = ra.sup_cnt;
     sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
     sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
@@ -613,13 +618,12 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         A.npass = 1;
         ra.out_mask = ec ? ROUTE_OUT_PROBS : (ROUTE_OUT_PROBS | ROUTE_OUT_GATING);
     }
-    // ExpertChoiceGating's rank kernel works on route blocks of kRouteBlock tokens
-    HIP_TRY(h, launch_router(A, ec ? kRouteBlock : 0, &h->rb, s));
+    HIP_TRY(h, launch_router(A, &h->rb, s));
     if (ec) {
         // the experts' choices give the slots, the stable ranks and the
         // per-block histogram
         HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
-                                        h->rank, h->blk_counts, h->ldc, ra.tot_cnt, s));
+                                        h->rank, h->blk_counts, h->ldc, ra.tot_cnt, ra.sup_cnt, h->rb, s));
     }
     // the scan runs in the permute kernel (its workgroups are the route blocks)
     sa.nblk = (T + h->rb - 1) / h->rb;
@@ -886,6 +890,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->blk_zh, sizeof(double) * (size_t)h->nblk_max * 2);
     A((void **)&h->tot_cnt2, sizeof(int) * 2 * E);
     A((void **)&h->tot_p2, sizeof(unsigned long long) * 2 * E);
+    h->nsup_max = (h->nblk_max + kSuper - 1) / kSuper;
+    A((void **)&h->sup_cnt2, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc);
     A((void **)&h->counts, sizeof(int) * E);
     A((void **)&h->offsets, sizeof(int) * (E + 1));
     A((void **)&h->cap, sizeof(int));
@@ -930,6 +936,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->tot_cnt2, sizeof(int) * 2 * E);
     Z(h->tot_p2, sizeof(unsigned long long) * 2 * E);
+    Z(h->sup_cnt2, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc);
     Z(h->aux_bias, sizeof(float) * h->Er);
     Z(h->aux_mom, sizeof(float) * h->Er);
     Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);

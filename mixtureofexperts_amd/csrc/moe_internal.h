@@ -8,10 +8,11 @@
 
 namespace moe {
 
-constexpr int kRouteBlock = 32;    // tokens per routing block of the ExpertChoiceGating kernels
 constexpr int kRtThreads = 512;    // threads per router_kernel workgroup (8 per token)
 constexpr int kRtMinBlock = 16;    // fewest tokens per router_kernel workgroup
-constexpr int kPermThreads = 1024; // threads per permute workgroup (one route block)
+constexpr int kPermThreads = 1024; // threads per permute workgroup: one wave per token
+constexpr int kPermTokens = kPermThreads / 64;  // tokens per permute workgroup (divides every route block)
+constexpr int kSuper = 16;         // route blocks per super block (rank bases: super rows, then block rows)
 constexpr double kPsumScale = 281474976710656.0;  // 2^48: fixed-point scale of the probability sums
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
@@ -108,6 +109,12 @@ struct RouteArgs {
     unsigned long long *tot_p;
     int *clr_cnt;
     unsigned long long *clr_p;
+    // expert counts per super block of kSuper route blocks [nsup][ldc]
+    // (integer atomics), this parity's and the other's (cleared: route block
+    // b takes the rows b, b + nblk, ... < nsup_max)
+    int *sup_cnt;
+    int *clr_sup;
+    int nsup_max;
 };
 
 // The scan of a routing call, run by every permute workgroup (its route
@@ -118,6 +125,7 @@ struct ScanArgs {
     int ldc;
     const double *blk_zh;   // [nblk][2]
     const int *tot_cnt;     // [E] entries per expert (before capacity)
+    const int *sup_cnt;     // [nsup][ldc] entries per expert of each super block
     const unsigned long long *tot_p;  // [Np] probability sums, fixed point
     int nblk, T, E, kt;   // E: experts of the histogram
     int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
@@ -145,7 +153,7 @@ struct ScanArgs {
 struct RtArgs {
     RouteArgs r;           // gating (r.out_mask: outputs of the single pass)
     RouterArgs g;          // logits GEMM (when the kernel computes the logits)
-    int TB;                // tokens per workgroup: 16, 32 or 64
+    int TB;                // tokens per workgroup: 16 (paired logits GEMM) or 64
     int KP, RB, dma;       // x staging: K columns per pass, LDS bytes per row, by global_load_lds
     int RW;                // LDS row stride of the logits / probability rows (floats)
     int off_L;             // LDS byte offset of the logits rows
@@ -160,7 +168,8 @@ struct PermuteArgs {
     int ct;                      // compute type of xp
     int *idx; float *gates;      // [T][kt] (rewritten under capacity)
     const int *rank;             // [T][kt] rank inside the route block and expert
-    int rb;                      // tokens per route block (one workgroup each)
+    int rb;                      // tokens per route block (a multiple of kPermTokens)
+    int tpw;                     // tokens per workgroup (set by launch_permute)
     ScanArgs s;                  // the scan (route-block rows and totals)
     int renorm;                  // capacity active: renormalise gates
     int *perm;                   // [T*kt]
@@ -260,9 +269,9 @@ struct DecodeArgs {
 // the router weight [D][Er_pad] fp32 -> the fused router's fragment image of
 // its three bf16 parts ((Dp / 32) * tiles per step KB, at most 3 * Ep * Dp * 2 B)
 hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp, uint16_t *img, hipStream_t s);
-// the routing call's router_kernel launch; tb_force > 0 fixes the tokens per
-// workgroup (else chosen here); *tb receives them (rows of the scan)
-hipError_t launch_router(RtArgs a, int tb_force, int *tb, hipStream_t s);
+// the routing call's router_kernel launch; *tb receives the tokens per
+// workgroup (route block) it chose
+hipError_t launch_router(RtArgs a, int *tb, hipStream_t s);
 // ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
 // gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
 // bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
@@ -270,8 +279,8 @@ hipError_t launch_router(RtArgs a, int tb_force, int *tb, hipStream_t s);
 // totals tot_cnt [E] (atomic adds)
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
                                 int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
-                                hipStream_t s);
-hipError_t launch_permute(const PermuteArgs &a, hipStream_t s);
+                                int *sup_cnt, int rb, hipStream_t s);
+hipError_t launch_permute(PermuteArgs a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 // compute_loss(::SwitchTransformerLoss) on device buffers in two launches
 // (per-block partial counts and probability sums, then their fold in block

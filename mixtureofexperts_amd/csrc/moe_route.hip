@@ -81,7 +81,7 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp
 
 // ============================================================================
 // The router kernel (router_kernel): one launch per routing call.  Workgroup
-// b of kRtThreads threads owns the TB = 16, 32 or 64 tokens [b TB, b TB + TB)
+// b of kRtThreads threads owns the TB = 16 or 64 tokens [b TB, b TB + TB)
 // (its route block) and
 //   1. computes their router logits on MFMA into LDS rows (or reads the
 //      caller's logits), plus the router bias;
@@ -187,20 +187,27 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
     constexpr int NPT = PAIRED ? 2 : 3;   // image tiles per expert tile and step
     constexpr int NP = XBF16 ? 1 : 3;     // activation parts
     constexpr int NACC = PAIRED ? 2 : 1;  // accumulator tiles per row tile
+    constexpr int RT = PAIRED ? 1 : 4;    // 16-token row tiles (the workgroup's TB = 16 RT tokens)
     constexpr int kRtSG = XBF16 ? 4 : 2;  // K steps per group of prefetched weight fragments
+    // weight groups in the register ring: all of a paired wave's 16 steps in
+    // flight at once for bf16 x; otherwise two groups ahead of the MFMAs
+    constexpr int NRING = (PAIRED && XBF16) ? 5 : (XBF16 || PAIRED ? 3 : 2);
+    // the next step's x fragments read during this step's MFMAs (bf16 x; the
+    // three parts of fp32 x over four row tiles would not fit the registers)
+    constexpr bool XPF = XBF16 || PAIRED;
     const RouterArgs &g = a.g;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int TB = a.TB, RT = TB >> 4, RB = a.RB, PPR = RB >> 4;
+    const int TB = RT * 16, RB = a.RB, PPR = RB >> 4;
     const int ET = PAIRED ? 1 : (g.Er + 15) >> 4;
     const int NTS = PAIRED ? 2 : 3 * ET;
     const int KG = 8 / ET;
     const int cg = w % ET, kg = w / ET;
     const bool mw = kg < KG;  // this wave runs MFMAs
 
-    rf32x4_t acc[4][NACC];
+    rf32x4_t acc[RT][NACC];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < RT; ++ti)
 #pragma unroll
         for (int j = 0; j < NACC; ++j) acc[ti][j] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -265,74 +272,96 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
                 }
             }
         };
+        // the x fragments (parts) of step st of the pass, every row tile
+        auto load_x = [&](int st, rbf16x8_t (&xa)[RT][NP]) __attribute__((always_inline)) {
+            const int u = st - (k0 >> 5);  // step inside the pass
+#pragma unroll
+            for (int ti = 0; ti < RT; ++ti) {
+                const int r = ti * 16 + l16;
+                const uint8_t *row = lds + r * RB;
+                if (XBF16) {
+                    xa[ti][0] = *(const rbf16x8_t *)(row + (((u * 4 + (lane >> 4)) ^ (r & 15)) << 4));
+                } else {
+                    const int u0 = u * 8 + (lane >> 4) * 2;
+                    const float4 f0 = *(const float4 *)(row + ((u0 ^ (r & 15)) << 4));
+                    const float4 f1 = *(const float4 *)(row + (((u0 + 1) ^ (r & 15)) << 4));
+                    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+                    uint16_t h0[8], h1[8], h2[8];
+#pragma unroll
+                    for (int m = 0; m < 8; ++m) {
+                        h0[m] = f32_to_bf16(v[m]);
+                        const float r1 = v[m] - bf16_to_f32(h0[m]);
+                        h1[m] = f32_to_bf16(r1);
+                        h2[m] = f32_to_bf16(r1 - bf16_to_f32(h1[m]));
+                    }
+                    __builtin_memcpy(&xa[ti][0], h0, 16);
+                    __builtin_memcpy(&xa[ti][NP > 1 ? 1 : 0], h1, 16);
+                    __builtin_memcpy(&xa[ti][NP > 2 ? 2 : 0], h2, 16);
+                }
+            }
+        };
+        // one group: the next step's x fragments are read while this step's
+        // MFMAs run; the MFMAs of a step go part by part over the row tiles,
+        // so consecutive ones write different accumulators
         auto mma = [&](int s0, const WF &wf) __attribute__((always_inline)) {
+            rbf16x8_t xc[RT][NP], xn[XPF ? RT : 1][NP];
+            if constexpr (XPF) load_x(min(s0, se - 1), xc);
 #pragma unroll
             for (int i = 0; i < kRtSG; ++i) {
-                const int st = s0 + i;
-                if (st >= se) break;
-                const int u = st - (k0 >> 5);  // step inside the pass
+                if (s0 + i >= se) break;
+                if constexpr (!XPF) load_x(s0 + i, xc);
+                else if (i + 1 < kRtSG) load_x(min(s0 + i + 1, se - 1), xn);
+                if constexpr (PAIRED) {
+                    // tile 0 (parts 0 | 1): every x part; tile 1 (part 2): x part 0
 #pragma unroll
-                for (int ti = 0; ti < 4; ++ti) {
-                    if (ti >= RT) break;
-                    const int r = ti * 16 + l16;
-                    const uint8_t *row = lds + r * RB;
-                    rbf16x8_t xa[NP];
-                    if (XBF16) {
-                        xa[0] = *(const rbf16x8_t *)(row + (((u * 4 + (lane >> 4)) ^ (r & 15)) << 4));
-                    } else {
-                        const int u0 = u * 8 + (lane >> 4) * 2;
-                        const float4 f0 = *(const float4 *)(row + ((u0 ^ (r & 15)) << 4));
-                        const float4 f1 = *(const float4 *)(row + (((u0 + 1) ^ (r & 15)) << 4));
-                        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-                        uint16_t h0[8], h1[8], h2[8];
+                    for (int xi = 0; xi < NP; ++xi)
 #pragma unroll
-                        for (int m = 0; m < 8; ++m) {
-                            h0[m] = f32_to_bf16(v[m]);
-                            const float r1 = v[m] - bf16_to_f32(h0[m]);
-                            h1[m] = f32_to_bf16(r1);
-                            h2[m] = f32_to_bf16(r1 - bf16_to_f32(h1[m]));
-                        }
-                        __builtin_memcpy(&xa[0], h0, 16);
-                        __builtin_memcpy(&xa[NP > 1 ? 1 : 0], h1, 16);
-                        __builtin_memcpy(&xa[NP > 2 ? 2 : 0], h2, 16);
-                    }
-                    if constexpr (PAIRED) {
-                        // tile 0 (parts 0 | 1): every x part; tile 1 (part 2): x part 0
+                        for (int ti = 0; ti < RT; ++ti)
+                            acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][0], acc[ti][0], 0, 0, 0);
 #pragma unroll
-                        for (int xi = 0; xi < NP; ++xi)
-                            acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wf[i][0], acc[ti][0], 0, 0, 0);
+                    for (int ti = 0; ti < RT; ++ti)
                         acc[ti][NACC - 1] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], wf[i][NPT - 1], acc[ti][NACC - 1], 0, 0, 0);
-                    } else {
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][0], wf[i][NPT - 1], acc[ti][NACC - 1], 0, 0, 0);
+                } else {
 #pragma unroll
-                        for (int p = 0; p < 3; ++p)
+                    for (int p = 0; p < 3; ++p)
 #pragma unroll
-                            for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
-                                acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[xi], wf[i][p < NPT ? p : 0],
+                        for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
+#pragma unroll
+                            for (int ti = 0; ti < RT; ++ti)
+                                acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][p < NPT ? p : 0],
                                                                                      acc[ti][0], 0, 0, 0);
+                }
+                if constexpr (XPF) {
+                    if (i + 1 < kRtSG) {
+#pragma unroll
+                        for (int ti = 0; ti < RT; ++ti)
+#pragma unroll
+                            for (int xi = 0; xi < NP; ++xi) xc[ti][xi] = xn[ti][xi];
                     }
                 }
             }
         };
-        // a ring of three weight groups: two in flight with the x tile, then
-        // each group's loads issued two groups ahead of its MFMAs
-        WF w0, w1, w2;
+        // the ring: NRING - 1 groups in flight with the x tile, then each
+        // group's loads issued NRING - 1 groups ahead of its MFMAs
+        WF wr[NRING];
         if (act) {
-            load_w(sb, w0);
-            if (sb + kRtSG < se) load_w(sb + kRtSG, w1);
+#pragma unroll
+            for (int j = 0; j + 1 < NRING; ++j)
+                if (sb + j * kRtSG < se) load_w(sb + j * kRtSG, wr[j]);
         }
         rt_wait_vm0();  // this wave's x pieces (and its first weight groups) have landed
         __syncthreads();
         if (act) {
-            for (int s0 = sb; s0 < se; s0 += 3 * kRtSG) {
-                if (s0 + 2 * kRtSG < se) load_w(s0 + 2 * kRtSG, w2);
-                mma(s0, w0);
-                if (s0 + kRtSG >= se) break;
-                if (s0 + 3 * kRtSG < se) load_w(s0 + 3 * kRtSG, w0);
-                mma(s0 + kRtSG, w1);
-                if (s0 + 2 * kRtSG >= se) break;
-                if (s0 + 4 * kRtSG < se) load_w(s0 + 4 * kRtSG, w1);
-                mma(s0 + 2 * kRtSG, w2);
+            for (int s0 = sb; s0 < se; s0 += NRING * kRtSG) {
+#pragma unroll
+                for (int j = 0; j < NRING; ++j) {
+                    const int sj = s0 + j * kRtSG;
+                    if (sj >= se) break;
+                    const int nx = sj + (NRING - 1) * kRtSG;
+                    if (nx < se) load_w(nx, wr[(j + NRING - 1) % NRING]);
+                    mma(sj, wr[j]);
+                }
             }
         }
         __syncthreads();  // the pass's x tile is consumed
@@ -344,8 +373,7 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
     float *P = (float *)lds;
     if (mw) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-            if (ti >= RT) break;
+        for (int ti = 0; ti < RT; ++ti) {
 #pragma unroll
             for (int j = 0; j < NACC; ++j) {
                 const int col = PAIRED ? j * 16 + l16 : cg * 16 + l16;
@@ -641,7 +669,10 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             int c = 0;
             for (int wd = 0; wd < TW; ++wd) c += __popc(emask[e * kRtMaskWords + wd]);
             a.blk_counts[(long long)blk * a.ldc + e] = c;
-            if (c) atomicAdd(&a.tot_cnt[e], c);
+            if (c) {
+                atomicAdd(&a.tot_cnt[e], c);
+                atomicAdd(&a.sup_cnt[(long long)(blk / kSuper) * a.ldc + e], c);
+            }
         }
         if (out_probs && e < E) {
             // per-row probability sums (Switch loss P_e): fp64 over the route
@@ -690,6 +721,8 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
             A.r.clr_p[e] = 0ull;
         }
     }
+    for (int s = blk; s < A.r.nsup_max; s += gridDim.x)
+        for (int e = threadIdx.x; e < A.r.ldc; e += kRtThreads) A.r.clr_sup[(long long)s * A.r.ldc + e] = 0;
     if constexpr (LG > 0) {
         rt_logits<LG == 1, PAIRED>(A, t0, rdyn, L);
     } else {
@@ -725,7 +758,7 @@ static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipS
     return hipGetLastError();
 }
 
-hipError_t launch_router(RtArgs A, int tb_force, int *tb, hipStream_t s) {
+hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     const RouteArgs &a = A.r;
     if (a.T <= 0) {
         *tb = kRtMinBlock;
@@ -739,14 +772,10 @@ hipError_t launch_router(RtArgs A, int tb_force, int *tb, hipStream_t s) {
     const bool paired = gemm && Er <= 8;
     const int ET = paired ? 1 : (Er + 15) / 16;
     // tokens per workgroup: 16 for the paired (few-expert) GEMM, whose x tile
-    // is widest; otherwise 64 / 32 / 16 while that leaves 256 workgroups;
-    // 64 without the GEMM
-    int TB;
-    if (tb_force > 0) TB = tb_force;
-    else if (!gemm) TB = 64;
-    else if (paired) TB = 16;
-    else TB = a.T >= 64 * 256 ? 64 : (a.T >= 32 * 256 ? 32 : 16);
-    if (TB != 16 && TB != 32 && TB != 64) return hipErrorInvalidValue;
+    // is widest; otherwise 64 (the weight image is read once per workgroup:
+    // the more tokens share it the better; 64 tokens fill the gating lanes)
+    // (the logits GEMM's row tiles are compile-time: 1 paired, 4 otherwise)
+    const int TB = gemm && paired ? 16 : 64;
     *tb = TB;
     A.TB = TB;
     A.RW = route_rw(Er);
@@ -771,7 +800,8 @@ hipError_t launch_router(RtArgs A, int tb_force, int *tb, hipStream_t s) {
     A.off_L = (int)((region0 + 1023) & ~(size_t)1023);
     const size_t lds = (size_t)A.off_L + rows;
     const int nblk = (a.T + TB - 1) / TB;
-    if (lds > lds_max || a.ldc < a.Eh || !a.tot_cnt || !a.tot_p || !a.clr_cnt || !a.clr_p || !a.blk_zh)
+    if (lds > lds_max || a.ldc < a.Eh || !a.tot_cnt || !a.tot_p || !a.clr_cnt || !a.clr_p || !a.blk_zh ||
+        !a.sup_cnt || !a.clr_sup || a.nsup_max * kSuper < nblk)
         return hipErrorInvalidValue;
     const int epl = route_epl(Er);
 #define MOE_RT(LG_, P_, EPL_) return launch_router_case<LG_, P_, EPL_>(A, nblk, lds, s)
@@ -883,7 +913,7 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
     }
 }
 
-// The bucketing inputs of the kept entries, per route block of kRouteBlock
+// The bucketing inputs of the kept entries, per route block of rb
 // tokens: thread e walks the block's tokens in order; a token holds expert e
 // in at most one slot, so the entry's rank among expert e's entries of the
 // block (token-then-slot order, the bucket loop's) is the count of earlier
@@ -891,11 +921,11 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
 __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
                                                                             int E, int kt, int *rank,
                                                                             int *blk_counts, int ldc,
-                                                                            int *tot_cnt) {
+                                                                            int *tot_cnt, int *sup_cnt, int rb) {
     const int e = threadIdx.x;
     if (e >= E) return;
-    const int t0 = blockIdx.x * kRouteBlock;
-    const int ntok = min(kRouteBlock, T - t0);
+    const int t0 = blockIdx.x * rb;
+    const int ntok = min(rb, T - t0);
     int c = 0;
     for (int i = 0; i < ntok; ++i) {
         const int sl = sel[(long long)(t0 + i) * E + e];
@@ -905,19 +935,22 @@ __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(con
         }
     }
     blk_counts[(long long)blockIdx.x * ldc + e] = c;
-    if (c) atomicAdd(&tot_cnt[e], c);
+    if (c) {
+        atomicAdd(&tot_cnt[e], c);
+        atomicAdd(&sup_cnt[(long long)(blockIdx.x / kSuper) * ldc + e], c);
+    }
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
                                 int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
-                                hipStream_t s) {
+                                int *sup_cnt, int rb, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255 || ldc < E) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
                        min(C, E), idx, gates);
-    hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + kRouteBlock - 1) / kRouteBlock), dim3(MOE_MAX_EXPERTS),
-                       0, s, sel, T, E, kt, rank, blk_counts, ldc, tot_cnt);
+    hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + rb - 1) / rb), dim3(MOE_MAX_EXPERTS), 0, s, sel, T, E,
+                       kt, rank, blk_counts, ldc, tot_cnt, sup_cnt, rb);
     return hipGetLastError();
 }
 
@@ -983,20 +1016,17 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
     for (int e = tid; e < a.E; e += nth) L.base[e] = 0;
     __syncthreads();
     {
-        // rank bases: thread (g, q) sums experts 4 g .. 4 g + 3 over its chunk
-        // of the route blocks before blk
+        // rank bases: the super blocks before blk's, then the route blocks
+        // of its own super block before it (at most 2 kSuper - 1 rows);
+        // thread (g, j) adds row j's experts 4 g .. 4 g + 3
         const int ng = (a.E + 3) / 4;
-        const int C = max(1, nth / ng);
-        const int R = (blk + C - 1) / C;
-        const int g = tid % ng, q = tid / ng;
-        if (q < C && blk > 0) {
-            const int b0 = min(blk, q * R), b1 = min(blk, b0 + R);
-            int s[4] = {0, 0, 0, 0};
-#pragma unroll 4
-            for (int b = b0; b < b1; ++b) {
-                const int4 v = *(const int4 *)(a.blk_counts + (long long)b * a.ldc + 4 * g);
-                s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
-            }
+        const int ns = blk / kSuper, nrow = ns + (blk - ns * kSuper);
+        for (int q = tid; q < ng * nrow; q += nth) {
+            const int g = q % ng, j = q / ng;
+            const int *src = (j < ns) ? a.sup_cnt + (long long)j * a.ldc
+                                      : a.blk_counts + (long long)(ns * kSuper + j - ns) * a.ldc;
+            const int4 v = *(const int4 *)(src + 4 * g);
+            const int s[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (4 * g + i < a.E && s[i]) atomicAdd(&L.base[4 * g + i], s[i]);
@@ -1153,8 +1183,8 @@ __device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int row, i
 }
 
 // ============================================================================
-// Permute: one workgroup per route block (the scan first), then one wave per
-// token.  Lanes < kt finalise the token's entries (capacity drop +
+// Permute: workgroups of kPermTokens tokens of one route block (its scan
+// first), one wave per token.  Lanes < kt finalise the token's entries (capacity drop +
 // renormalisation, position), then the wave copies the token's row into
 // every position it owns, converting to the GEMM type.
 // ============================================================================
@@ -1259,12 +1289,14 @@ __device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int l
     }
 }
 
+// Workgroup w takes the tpw tokens [w tpw, w tpw + tpw) of one route block,
+// a wave per token in turn, after that route block's scan.
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
     __shared__ ScanLds L;
-    scan_block(a.s, blockIdx.x, L);
-    const int lane = threadIdx.x & 63;
-    const int t1 = min(a.T, (blockIdx.x + 1) * a.rb);
-    for (int t = blockIdx.x * a.rb + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64) permute_token(a, t, lane, L);
+    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
+    const int t1 = min(a.T, (int)(blockIdx.x + 1) * a.tpw);
+    for (int t = blockIdx.x * a.tpw + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
+        permute_token(a, t, threadIdx.x & 63, L);
 }
 
 // Permute for more slots per token than a wave has lanes (ExpertChoiceGating
@@ -1336,21 +1368,26 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
 
 __global__ __launch_bounds__(kPermThreads) void permute_wide_kernel(PermuteArgs a) {
     __shared__ ScanLds L;
-    scan_block(a.s, blockIdx.x, L);
-    const int lane = threadIdx.x & 63;
-    const int t1 = min(a.T, (blockIdx.x + 1) * a.rb);
-    for (int t = blockIdx.x * a.rb + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
-        permute_wide_token(a, t, lane, L);
+    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
+    const int t1 = min(a.T, (int)(blockIdx.x + 1) * a.tpw);
+    for (int t = blockIdx.x * a.tpw + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
+        permute_wide_token(a, t, threadIdx.x & 63, L);
 }
 
-hipError_t launch_permute(const PermuteArgs &a, hipStream_t s) {
+hipError_t launch_permute(PermuteArgs a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + a.rb - 1) / a.rb;
-    if (a.kt > 2 * 64 || a.rb < 1 || a.s.nblk != nblk || a.s.E > MOE_MAX_EXPERTS || a.s.ldc < a.s.E ||
-        a.s.ldc % 4)
+    if (a.kt > 2 * 64 || a.rb < kPermTokens || a.rb % kPermTokens || a.s.nblk != nblk || a.s.E > MOE_MAX_EXPERTS ||
+        a.s.ldc < a.s.E || a.s.ldc % 4)
         return hipErrorInvalidValue;
-    if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3(nblk), dim3(kPermThreads), 0, s, a);
-    else hipLaunchKernelGGL(permute_kernel, dim3(nblk), dim3(kPermThreads), 0, s, a);
+    // tokens per workgroup: kPermTokens (one per wave) while that leaves at
+    // most 512 workgroups, else 2 or 4 per wave (dividing the route block):
+    // each workgroup runs its route block's scan first
+    a.tpw = kPermTokens;
+    while (a.tpw * 2 <= a.rb && a.tpw < 4 * kPermTokens && (a.T + a.tpw - 1) / a.tpw > 512) a.tpw *= 2;
+    const int nwg = (a.T + a.tpw - 1) / a.tpw;
+    if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else hipLaunchKernelGGL(permute_kernel, dim3(nwg), dim3(kPermThreads), 0, s, a);
     return hipGetLastError();
 }
 
