@@ -147,6 +147,18 @@ int moe_slots_per_token(const moe_handle *h);
  * NULL (the reference router has none; a bias is Dense(W, b)). */
 int moe_set_router(moe_handle *h, const float *weight, const float *bias);
 
+/* Router noise in training -- src/core/router.jl:32-41 (Router(...;
+ * noise_scale, use_noise_network)).  In training calls with noise_scale > 0
+ * the gate sees logits .+ randn .* noise_scale, or, with a noise network
+ * (noise_weight != NULL, memory [D][E_router] like the router weight),
+ * logits .+ noise_scale .* (randn .* softplus.(noise_weight' x)).  randn is
+ * the library's counter-based generator (seed, the handle's training-call
+ * number, token, router row), not Julia's stream.  The Switch loss and the
+ * statistics use the noisy probabilities; the z-loss the logits without
+ * noise (src/core/moe_layer.jl:117-121).  noise_scale = 0 turns the noise
+ * off.  A noise network needs 2 * E_router <= MOE_MAX_EXPERTS. */
+int moe_set_router_noise(moe_handle *h, float noise_scale, const float *noise_weight, uint64_t seed);
+
 /* Expert e (0-based) weights -- GatedExpert (src/experts/gated.jl:6-27):
  * w1 (H,D), w3 (H,D), w2 (D_out,H); StandardExpert (src/experts/standard.jl):
  * w1 (H,D), w2 (D_out,H), b1 (H), b2 (D_out), w3 NULL.

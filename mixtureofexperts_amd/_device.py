@@ -74,6 +74,13 @@ class DeviceLayer:
         b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
         _lib.check(_lib.lib().moe_set_router(self.h, _ptr(w), _ptr(b)), self.h)
 
+    def set_router_noise(self, noise_scale, noise_weight_mem_DE=None, seed=0):
+        """Router noise in training (router.jl:32-41); the noise network's
+        weight in the router weight's memory order [D][E_router], or None."""
+        w = None if noise_weight_mem_DE is None else np.ascontiguousarray(noise_weight_mem_DE, dtype=np.float32)
+        _lib.check(_lib.lib().moe_set_router_noise(self.h, float(noise_scale), _ptr(w), int(seed) & (2**64 - 1)),
+                   self.h)
+
     def set_expert(self, e, w1, w2, w3=None, b1=None, b2=None, *, src_dtype=_lib.MOE_F32,
                    layout=_lib.MOE_LAYOUT_LLAMA_IN_OUT, s1=None, s2=None, s3=None):
         """Matrices in memory order of ``layout`` (LLAMA_IN_OUT = [out][in],

@@ -49,6 +49,14 @@ struct moe_handle {
     // weights
     float *wr = nullptr, *br = nullptr;
     uint16_t *wsplit = nullptr;  // router weight's three bf16 parts as the fused router's fragment image
+    // router noise (moe_set_router_noise): scale, seed, training calls so far;
+    // with a noise network its weight [D][Er_pad] and the fragment image of
+    // the router and noise weights side by side ([W | Wn], 2 Er columns)
+    float noise_scale = 0.0f;
+    unsigned long long noise_seed = 0, noise_calls = 0;
+    float *wn = nullptr, *wrn = nullptr;
+    uint16_t *wsplit_n = nullptr;
+    bool noise_net = false;  // the noise network is set (its buffers stay allocated once made)
     int Ep16 = 0, Dp32 = 0;
     bool router_set = false, has_bias = false;
     std::vector<char> expert_set;
@@ -330,17 +338,6 @@ __global__ void convert_rows_kernel(const void *src, int src_bf16, int n, int D,
 
 // ---- convert_to_moe expert initialisation (src/llama2/conversion.jl:277-331) ----
 
-// Counter-based standard normal for (seed, stream, index): a splitmix64 hash
-// of the three gives two 24-bit uniforms in (0, 1), Box-Muller gives N(0, 1).
-__device__ inline float init_normal(unsigned long long seed, unsigned long long stream, unsigned long long i) {
-    unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (stream + 1) + 0xD1B54A32D192ED03ull * i;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    z ^= z >> 31;
-    const float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
-    const float u2 = ((float)(z & 0xFFFFFFull) + 0.5f) * (1.0f / 16777216.0f);
-    return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
-}
 
 // Expert e's matrix m (0 = w1, 1 = w2, 2 = w3) from the dense one, rows
 // [N][K] fp32 (K = the matrix's input features), per create_single_expert:
@@ -574,6 +571,18 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         rg.x = x_dev; rg.x_bf16 = x_bf16; rg.T = T; rg.D = h->D; rg.Er = h->Er; rg.Ep = h->Ep16; rg.Dp = h->Dp32;
         rg.ws = h->wsplit;
         ra.bias = h->has_bias ? h->br : nullptr;
+        if (training && h->noise_scale > 0.0f) {
+            // router noise (src/core/router.jl:32-41), one stream of the
+            // generator per training call
+            A.noise_scale = h->noise_scale;
+            A.noise_seed = h->noise_seed;
+            A.noise_call = h->noise_calls++;
+            if (h->noise_net) {
+                A.noise_net = 1;
+                rg.Er = 2 * h->Er;
+                rg.ws = h->wsplit_n;
+            }
+        }
     } else {
         ra.part = h->logits_in;  // the caller's logits
         ra.bias = nullptr;
@@ -965,6 +974,8 @@ int moe_destroy(moe_handle *h) {
     return MOE_OK;
 }
 
+static hipError_t build_noise_image(moe_handle *h);
+
 int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
     std::lock_guard<std::mutex> lk(h->mu);
@@ -984,10 +995,61 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
         HIP_TRY(h, hipMemcpyAsync(h->br, bias, sizeof(float) * h->Er, dev_b ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                   h->stream));
     HIP_TRY(h, launch_router_split(h->wr, h->D, h->Er, h->Er_pad, h->Dp32, h->wsplit, h->stream));
+    if (h->noise_net) HIP_TRY(h, build_noise_image(h));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     settle(h);
     h->has_bias = bias != nullptr;
     h->router_set = true;
+    return MOE_OK;
+}
+
+// [W | Wn] ([D][2 Er], rows padded to a multiple of 8) and its fragment image
+static hipError_t build_noise_image(moe_handle *h) {
+    const int Er2 = 2 * h->Er, Er2_pad = (int)round_up(Er2, 8);
+    hipError_t e = hipMemcpy2DAsync(h->wrn, sizeof(float) * Er2_pad, h->wr, sizeof(float) * h->Er_pad,
+                                    sizeof(float) * h->Er, h->D, hipMemcpyDeviceToDevice, h->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(h->wrn + h->Er, sizeof(float) * Er2_pad, h->wn, sizeof(float) * h->Er_pad,
+                             sizeof(float) * h->Er, h->D, hipMemcpyDeviceToDevice, h->stream);
+    if (e == hipSuccess) e = launch_router_split(h->wrn, h->D, Er2, Er2_pad, h->Dp32, h->wsplit_n, h->stream);
+    return e;
+}
+
+int moe_set_router_noise(moe_handle *h, float noise_scale, const float *noise_weight, uint64_t seed) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (!(noise_scale >= 0.0f) || !std::isfinite(noise_scale)) return fail(h, MOE_EINVAL, "noise_scale must be >= 0");
+    if (noise_weight && 2 * h->Er > MOE_MAX_EXPERTS)
+        return fail(h, MOE_EUNSUPPORTED, "a noise network needs 2 * router rows <= MOE_MAX_EXPERTS");
+    if (noise_weight && h->cfg.gate_kind != MOE_GATE_TOPK && h->cfg.gate_kind != MOE_GATE_SWITCH &&
+        h->cfg.gate_kind != MOE_GATE_SHARED && h->cfg.gate_kind != MOE_GATE_SOFT)
+        return fail(h, MOE_EUNSUPPORTED, "router noise: the gate's logits come from the router GEMM only");
+    const bool dev_w = noise_weight && is_device_ptr(noise_weight);
+    if (dev_w) HIP_TRY(h, hipDeviceSynchronize());
+    int r = join_stream(h, h->stream);
+    if (r != MOE_OK) return r;
+    if (noise_weight) {
+        if (!h->wn) {
+            const int Er2_pad = (int)round_up(2 * h->Er, 8);
+            r = dalloc(h, (void **)&h->wn, sizeof(float) * (size_t)h->D * h->Er_pad);
+            if (r == MOE_OK) r = dalloc(h, (void **)&h->wrn, sizeof(float) * (size_t)h->D * Er2_pad);
+            if (r == MOE_OK)
+                r = dalloc(h, (void **)&h->wsplit_n,
+                           sizeof(uint16_t) * 3 * round_up(2 * h->Er, 16) * (size_t)h->Dp32);
+            if (r != MOE_OK) return r;
+            HIP_TRY(h, hipMemsetAsync(h->wn, 0, sizeof(float) * (size_t)h->D * h->Er_pad, h->stream));
+        }
+        HIP_TRY(h, hipMemcpy2DAsync(h->wn, sizeof(float) * h->Er_pad, noise_weight, sizeof(float) * h->Er,
+                                    sizeof(float) * h->Er, h->D,
+                                    dev_w ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, h->stream));
+        HIP_TRY(h, build_noise_image(h));
+    }
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    settle(h);
+    h->noise_net = noise_weight != nullptr;
+    h->noise_scale = noise_scale;
+    h->noise_seed = seed;
+    h->noise_calls = 0;
     return MOE_OK;
 }
 

@@ -56,6 +56,18 @@ __host__ __device__ inline float fp8e4m3_to_f32(uint8_t b) {
     return (b & 0x80u) ? -v : v;
 }
 
+// Counter-based standard normal for (seed, stream, index): a splitmix64 hash
+// of the three gives two 24-bit uniforms in (0, 1), Box-Muller gives N(0, 1).
+__device__ inline float init_normal(unsigned long long seed, unsigned long long stream, unsigned long long i) {
+    unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (stream + 1) + 0xD1B54A32D192ED03ull * i;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = ((float)(z & 0xFFFFFFull) + 0.5f) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+
 // Julia `isless` total order as an unsigned key: every NaN is largest,
 // -0.0 < +0.0 (src/gating/topk.jl:35 partialsortperm, rev=true).
 __host__ __device__ inline uint32_t isless_key(float f) {
@@ -160,6 +172,14 @@ struct RtArgs {
     int npass;             // 2: AuxiliaryFreeLoss (probabilities pass, then gating on logits + aux_bias)
     const float *aux_bias; // [Er]
     int store_rows;        // write logits / probs [T][Er] to global memory
+    // router noise in training (src/core/router.jl:32-41): noise_scale > 0
+    // adds noise_scale * randn (noise_net: noise_scale * (randn *
+    // softplus(noise logits)), the noise logits in GEMM columns Er .. 2 Er - 1)
+    // to the logits the gate sees; randn = init_normal(noise_seed,
+    // noise_call, token * Er + expert)
+    float noise_scale;
+    int noise_net;
+    unsigned long long noise_seed, noise_call;
 };
 
 struct PermuteArgs {

@@ -395,7 +395,7 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
             return v;
         };
         float v = PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e);
-        if (bias) v = v + bias[e];
+        if (bias && e < a.r.Er) v = v + bias[e];  // (not on the noise network's columns)
         L[t * a.RW + e] = v;
     }
 }
@@ -439,9 +439,14 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     __syncthreads();  // a previous pass is done with emask and the rows
     for (int i = tid; i < a.Eh * kRtMaskWords; i += kRtThreads) emask[i] = 0u;
 
-    float v[EPL], pr[EPL];  // logits; exp terms, then probabilities (before the shared-gating scale)
+    const bool noise = A.noise_scale > 0.0f;
+    // z-loss from a softmax of its own: over all rows, unscaled, and on the
+    // logits without router noise (the reference's z-loss reruns the router
+    // with training=false, src/core/moe_layer.jl:117-121)
+    const bool zs_own = zsep || noise;
+    float v[EPL], vg[EPL], pr[EPL];  // logits; the logits the gate sees; exp terms, then probabilities
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) { v[j] = 0.0f; pr[j] = 0.0f; }
+    for (int j = 0; j < EPL; ++j) { v[j] = 0.0f; vg[j] = 0.0f; pr[j] = 0.0f; }
     float lse = 0.0f;
     double hs = 0.0;
     if (softmax) {
@@ -449,24 +454,38 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
             const bool ok = rvalid && i < E;
-            float x = ok ? L[ok ? rt * RW + i : 0] : 0.0f;
+            v[j] = ok ? L[ok ? rt * RW + i : 0] : 0.0f;
+            float x = v[j];
+            if (noise) {
+                // logits .+ randn .* noise_scale, or logits .+ noise_scale .*
+                // (randn .* softplus.(noise logits)) (router.jl:32-41)
+                const float r = init_normal(A.noise_seed, A.noise_call, (unsigned long long)t * E + (ok ? i : 0));
+                if (A.noise_net) {
+                    const float nl = ok ? L[ok ? rt * RW + E + i : 0] : 0.0f;
+                    const float sp = log1pf(expf(-fabsf(nl))) + fmaxf(nl, 0.0f);  // NNlib softplus
+                    x = x + A.noise_scale * (r * sp);
+                } else {
+                    x = x + r * A.noise_scale;
+                }
+            }
+            // AuxiliaryFreeLoss gating pass: (noisy) logits .+ bias
             if (xbias) x = ok ? x + xbias[ok ? i : 0] : x;
-            v[j] = x;
+            vg[j] = ok ? x : 0.0f;
         }
-        // ---- max (of the routed rows; zsep: also of all rows) ----
+        // ---- max (of the routed rows; zs_own: also of all rows) ----
         float m = -INFINITY, mz = -INFINITY;
         float sv[EPL];  // logits ./ lambda for SoftMoEGating (advanced.jl:18)
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
             const bool ok = rvalid && i < E;
-            sv[j] = soft ? v[j] / a.soft_lambda : v[j];
+            sv[j] = soft ? vg[j] / a.soft_lambda : vg[j];
             m = (ok && i >= ns && sv[j] > m) ? sv[j] : m;
             mz = (ok && v[j] > mz) ? v[j] : mz;
         }
         m = lanes8_max(m);
-        if (zsep) mz = lanes8_max(mz);
-        // ---- exp terms; zsep: the z-loss exponent sum over all rows ----
+        if (zs_own) mz = lanes8_max(mz);
+        // ---- exp terms; zs_own: the z-loss exponent sum over all rows ----
         float zs = 0.0f;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
@@ -475,7 +494,7 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             const float ex = (m == INFINITY) ? ((sv[j] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv[j] - m));
             pr[j] = okr ? ex : 0.0f;
         }
-        if (zsep) {
+        if (zs_own) {
 #pragma unroll
             for (int j = 0; j < EPL; ++j) {
                 const int i = base + j;
@@ -529,12 +548,12 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         hs = lanes8_sum(hs);
         // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
         // the log in Float32 as Julia takes it of the Float32 sum
-        lse = zsep ? mz + logf(zs) : m + logf(s);
+        lse = zs_own ? mz + logf(zs) : m + logf(s);
         if (A.store_rows && out_probs && rvalid) {
 #pragma unroll
             for (int j = 0; j < EPL; ++j)
                 if (base + j < E) {
-                    a.logits[t * E + base + j] = v[j];
+                    a.logits[t * E + base + j] = vg[j];
                     a.probs[t * E + base + j] = Pr[rt * RW + base + j];
                 }
         }
@@ -769,8 +788,10 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
         ((a.out_mask & ROUTE_OUT_GATING) && a.kt > MOE_MAX_TOPK) || (!gemm && !a.part))
         return hipErrorInvalidValue;
     const int Er = a.Er;
-    const bool paired = gemm && Er <= 8;
-    const int ET = paired ? 1 : (Er + 15) / 16;
+    // the GEMM's columns: the router logits, then (noise network) the noise logits
+    const int Eg = gemm ? A.g.Er : Er;
+    const bool paired = gemm && Eg <= 8;
+    const int ET = paired ? 1 : (Eg + 15) / 16;
     // tokens per workgroup: 16 for the paired (few-expert) GEMM, whose x tile
     // is widest; otherwise 64 (the weight image is read once per workgroup:
     // the more tokens share it the better; 64 tokens fill the gating lanes)
@@ -778,13 +799,14 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     const int TB = gemm && paired ? 16 : 64;
     *tb = TB;
     A.TB = TB;
-    A.RW = route_rw(Er);
+    A.RW = route_rw(Eg);
     const size_t rows = sizeof(float) * (size_t)TB * A.RW;
     const size_t lds_max = 150 * 1024;  // + the static emask / wred (9.2 KB) <= 160 KB
     size_t region0 = rows;
     if (gemm) {
         const RouterArgs &g = A.g;
-        if (g.Dp % 32 != 0 || g.Dp < g.D || g.Er != Er) return hipErrorInvalidValue;
+        if (g.Dp % 32 != 0 || g.Dp < g.D || g.Er != (A.noise_net ? 2 * Er : Er) || g.Er > MOE_MAX_EXPERTS)
+            return hipErrorInvalidValue;
         const int ESZ = g.x_bf16 ? 2 : 4;
         // x tile bytes per row: what LDS holds beside the logits rows, in 256 B units
         const size_t avail = lds_max - rows - 1024;

@@ -60,13 +60,16 @@ def create_moe_config(**kwargs):
 class Router:
     """Router -- src/core/router.jl:4-46: ``weight`` (E, input_dim) float32 as
     Flux Dense(in, E, bias=false) with its default glorot-uniform init
-    (:18); an optional ``bias`` (E,) makes it Dense(W, b)."""
+    (:18); an optional ``bias`` (E,) makes it Dense(W, b).  With
+    ``use_noise_network`` a second Dense(in, E, bias=false),
+    ``noise_weight`` (:20); ``noise_seed`` seeds the device generator of
+    the training noise (router.jl:32-41)."""
 
     def __init__(self, input_dim, num_experts, gate_type, *, noise_scale=0.0, use_noise_network=False,
-                 use_fp32=True, rng=None, weight=None, bias=None):
+                 use_fp32=True, rng=None, weight=None, bias=None, noise_weight=None, noise_seed=None):
         rng = np.random.default_rng() if rng is None else rng
+        a = np.sqrt(6.0 / (input_dim + num_experts))
         if weight is None:
-            a = np.sqrt(6.0 / (input_dim + num_experts))
             weight = rng.uniform(-a, a, size=(num_experts, input_dim)).astype(np.float32)
         self.weight = np.asarray(weight, dtype=np.float32)
         self.bias = None if bias is None else np.asarray(bias, dtype=np.float32)
@@ -74,6 +77,12 @@ class Router:
         self.noise_scale = float(noise_scale)
         self.use_noise_network = bool(use_noise_network)
         self.use_fp32 = bool(use_fp32)
+        if self.use_noise_network and noise_weight is None:
+            noise_weight = rng.uniform(-a, a, size=(num_experts, input_dim)).astype(np.float32)
+        self.noise_weight = None if noise_weight is None else np.asarray(noise_weight, dtype=np.float32)
+        if noise_seed is None:
+            noise_seed = int(rng.integers(0, 2**63)) if self.noise_scale > 0 else 0
+        self.noise_seed = int(noise_seed)
 
 
 def create_experts(config, rng=None):
@@ -116,8 +125,6 @@ class MoELayer:
     # ---- device state ----------------------------------------------------
     def _check_supported(self, training):
         c = self.config
-        if training and c.noise_scale > 0:
-            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "router noise in training has no device path")
         if training and c.expert_dropout > 0 and c.expert_type != "gated":
             raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "expert dropout in training has no device path")
 
@@ -141,6 +148,10 @@ class MoELayer:
         """(Re)build the device handle and upload router and expert weights."""
         self._dev = self._new_device()
         self._dev.set_router(np.ascontiguousarray(self.router.weight.T), self.router.bias)
+        if self.router.noise_scale > 0:
+            nw = self.router.noise_weight if self.router.use_noise_network else None
+            self._dev.set_router_noise(self.router.noise_scale,
+                                       None if nw is None else np.ascontiguousarray(nw.T), self.router.noise_seed)
         for e, ex in enumerate(self.experts):
             ex.upload(self._dev, e)
         return self._dev

@@ -264,7 +264,7 @@ def aux_free_update_bias(idx, bias, mom, lr, momentum):
 
 def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, expert_type="gated", act="silu",
                 alpha=0.01, z_weight=0.001, training=False, drop_tokens=False, capacity_factor=1.25,
-                router_bias=None, logits=None, aux_free=None, gate_param=None, given=None):
+                router_bias=None, logits=None, aux_free=None, gate_param=None, given=None, z_logits=None):
     """forward_standard + the z-loss of MoELayer's call (moe_layer.jl:107-156).
 
     x_TD: [T][D] float32.  router_w_ED: (E, D) Flux weight.  experts: list of
@@ -276,7 +276,10 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
     state of an AuxiliaryFreeLoss balance loss (dict bias, mom, lr, momentum,
     update_freq, counter, use_comp, cw), updated in place: the gating runs on
     logits .+ bias (:137-140) and the balance loss is its compute_loss
-    (src/balancing/auxiliary_free.jl:78-87).  Returns (out [T][Dout], loss,
+    (src/balancing/auxiliary_free.jl:78-87).  ``z_logits``: the logits of the
+    z-loss when they differ from the gate's (router noise in training: the
+    gate sees the noisy logits, the z-loss reruns the router with
+    training=false, moe_layer.jl:117-121).  Returns (out [T][Dout], loss,
     aux dict)."""
     x = np.asarray(x_TD, np.float32)
     T = x.shape[0]
@@ -339,7 +342,7 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
             sw = switch_loss(idx, probs, alpha)
         loss = sw
         if z_weight > 0:
-            zl = z_loss(logits, z_weight)
+            zl = z_loss(logits if z_logits is None else z_logits, z_weight)
             loss = np.float32(loss + zl)
     aux = dict(logits=logits, idx=idx, gates=gates, probs=probs, counts=counts, offsets=offsets, perm=perm,
                switch_loss=sw, z_loss=zl, mean_entropy=mean_entropy(probs))

@@ -118,9 +118,8 @@ def test_host_mirror_config_defaults(moe):
 def test_host_mirror_rejects_unsupported_before_device(moe):
     from mixtureofexperts_amd import _lib
 
-    layer = moe.MoELayer(moe.MoEConfig(input_dim=8, hidden_dim=16, output_dim=8, noise_scale=0.1))
     with pytest.raises(moe.MoeError):
-        layer(np.zeros((8, 4), np.float32), training=True)
+        moe.MoELayer(moe.MoEConfig(input_dim=8, hidden_dim=16, output_dim=8, use_cur=True))
     with pytest.raises(moe.MoeError):
         moe.gating.gate_spec(object(), 8)
     with pytest.raises(moe.MoeError):

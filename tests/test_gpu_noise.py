@@ -1,0 +1,103 @@
+"""Router noise in training (src/core/router.jl:32-41) on the GPU.
+
+The noise comes from the library's counter-based generator, not Julia's randn
+stream, so the draws are checked by their distribution: the difference of the
+training call's logits and the same layer's inference logits, divided by
+noise_scale (or by noise_scale .* softplus(noise logits) with a noise
+network), must look like N(0, 1).  Everything downstream of the noise is then
+checked exactly: the routing on the noisy logits is bit-exact against the
+oracle, the Switch loss and the statistics follow the noisy probabilities,
+and the z-loss the logits without noise (moe_layer.jl:117-121)."""
+import numpy as np
+import pytest
+
+from test_gpu_layer import TOL, Case, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def softplus(v):
+    v = np.asarray(v, np.float32)
+    return (np.log1p(np.exp(-np.abs(v))) + np.maximum(v, 0)).astype(np.float32)
+
+
+def check_normal(r, what):
+    r = np.asarray(r, np.float64).ravel()
+    n = r.size
+    assert abs(r.mean()) < 5.0 / np.sqrt(n), f"{what}: mean {r.mean():.4f}"
+    assert abs(r.std() - 1.0) < 5.0 * np.sqrt(0.5 / n) + 0.01, f"{what}: std {r.std():.4f}"
+    # tails of a standard normal: P(|r| > 2) = 4.55 %
+    frac = float(np.mean(np.abs(r) > 2.0))
+    assert abs(frac - 0.0455) < 0.01, f"{what}: P(|r|>2) {frac:.4f}"
+
+
+def routed_checks(case, res, out, loss, noisy, clean):
+    ref_out, ref_loss, aux = case.oracle.moe_forward(case.x, case.wr, case.ex, gate=case.gate, k=case.k,
+                                                     num_shared=case.ns, expert_type=case.expert_type,
+                                                     act=case.act, alpha=case.alpha, z_weight=case.z,
+                                                     training=True, logits=noisy, z_logits=clean)
+    assert np.array_equal(res["indices"], aux["idx"])
+    assert np.array_equal(res["gates"].view(np.uint32), aux["gates"].view(np.uint32))
+    assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32))
+    assert np.array_equal(res["counts"], aux["counts"])
+    n = int(aux["offsets"][-1])
+    assert np.array_equal(res["perm"][:n], aux["perm"])
+    assert rel_err(out, ref_out) <= TOL["f32"]
+    assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (loss, ref_loss)
+    assert abs(res["z_loss"] - aux["z_loss"]) <= 1e-5 * max(1.0, abs(float(aux["z_loss"])))
+    assert abs(res["mean_entropy"] - aux["mean_entropy"]) <= 1e-5 * max(1.0, abs(float(aux["mean_entropy"])))
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (40, 4)])
+def test_router_noise(moe, oracle, E, k):
+    case = Case(moe, oracle, T=2048, D=128, H=64, E=E, k=k, seed=21)
+    scale = 0.5
+    case.dev.set_router_noise(scale, None, seed=1234)
+    _, _, clean_res = case.run(training=False)
+    clean = clean_res["logits"]
+    out, loss, res = case.run(training=True)
+    noisy = res["logits"]
+    check_normal((noisy - clean) / np.float32(scale), f"noise E={E}")
+    routed_checks(case, res, out, loss, noisy, clean)
+    # a new draw per training call; inference calls stay noise-free
+    _, _, res2 = case.run(training=True)
+    assert not np.array_equal(res2["logits"], noisy)
+    _, _, clean2 = case.run(training=False)
+    assert np.array_equal(clean2["logits"], clean)
+    # the same seed gives the same draws from a fresh start
+    case.dev.set_router_noise(scale, None, seed=1234)
+    _, _, res3 = case.run(training=True)
+    assert np.array_equal(res3["logits"], noisy)
+    # noise_scale 0 turns it off
+    case.dev.set_router_noise(0.0, None, seed=1234)
+    _, _, res4 = case.run(training=True)
+    assert np.array_equal(res4["logits"], clean)
+
+
+@pytest.mark.parametrize("E", [4, 8, 24])
+def test_router_noise_network(moe, oracle, E):
+    case = Case(moe, oracle, T=2048, D=128, H=64, E=E, k=2, seed=22)
+    scale = 0.3
+    wn = (np.random.default_rng(5).standard_normal((E, case.D)) / np.sqrt(case.D)).astype(np.float32)
+    case.dev.set_router_noise(scale, np.ascontiguousarray(wn.T), seed=99)
+    _, _, clean_res = case.run(training=False)
+    clean = clean_res["logits"]
+    out, loss, res = case.run(training=True)
+    noisy = res["logits"]
+    sp = softplus(case.x @ wn.T)
+    check_normal((noisy - clean) / (np.float32(scale) * sp), f"noise network E={E}")
+    routed_checks(case, res, out, loss, noisy, clean)
+
+
+def test_layer_router_noise_python_api(moe):
+    cfg = moe.MoEConfig(num_experts=8, expert_type="gated", input_dim=64, hidden_dim=96, output_dim=64,
+                        gate_type=moe.TopKGating(2), noise_scale=0.2, use_noise_network=True, max_tokens=256)
+    layer = moe.MoELayer(cfg, rng=np.random.default_rng(3))
+    x = np.random.default_rng(4).standard_normal((64, 256)).astype(np.float32)
+    y0, l0 = layer(x, training=False)
+    y1, l1 = layer(x, training=True)
+    y2, l2 = layer(x, training=False)
+    assert np.array_equal(y0, y2) and l0 == 0.0 and l2 == 0.0
+    assert np.isfinite(l1) and l1 > 0
+    assert not np.array_equal(y0, y1)  # the noisy gate routes some tokens differently
+    layer.close()
