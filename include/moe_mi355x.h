@@ -159,6 +159,14 @@ int moe_set_router(moe_handle *h, const float *weight, const float *bias);
  * off.  A noise network needs 2 * E_router <= MOE_MAX_EXPERTS. */
 int moe_set_router_noise(moe_handle *h, float noise_scale, const float *noise_weight, uint64_t seed);
 
+/* StandardExpert's Dropout(p) in training -- src/experts/standard.jl:26,
+ * 49-51: in training calls each element of h = act(W1 x .+ b1) is kept,
+ * times Float32(1 / (1 - p)), with probability 1 - p (a uniform draw > p),
+ * else zeroed, before W2.  Draws: the library's counter-based generator
+ * (seed, the handle's training-call number, expert-ordered row, column),
+ * not Julia's stream.  p = 0 turns it off; StandardExpert handles only. */
+int moe_set_expert_dropout(moe_handle *h, float p, uint64_t seed);
+
 /* Expert e (0-based) weights -- GatedExpert (src/experts/gated.jl:6-27):
  * w1 (H,D), w3 (H,D), w2 (D_out,H); StandardExpert (src/experts/standard.jl):
  * w1 (H,D), w2 (D_out,H), b1 (H), b2 (D_out), w3 NULL.

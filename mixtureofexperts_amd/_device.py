@@ -81,6 +81,10 @@ class DeviceLayer:
         _lib.check(_lib.lib().moe_set_router_noise(self.h, float(noise_scale), _ptr(w), int(seed) & (2**64 - 1)),
                    self.h)
 
+    def set_expert_dropout(self, p, seed=0):
+        """StandardExpert's Dropout(p) in training (standard.jl:49-51)."""
+        _lib.check(_lib.lib().moe_set_expert_dropout(self.h, float(p), int(seed) & (2**64 - 1)), self.h)
+
     def set_expert(self, e, w1, w2, w3=None, b1=None, b2=None, *, src_dtype=_lib.MOE_F32,
                    layout=_lib.MOE_LAYOUT_LLAMA_IN_OUT, s1=None, s2=None, s3=None):
         """Matrices in memory order of ``layout`` (LLAMA_IN_OUT = [out][in],

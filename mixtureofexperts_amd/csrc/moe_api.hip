@@ -57,6 +57,9 @@ struct moe_handle {
     float *wn = nullptr, *wrn = nullptr;
     uint16_t *wsplit_n = nullptr;
     bool noise_net = false;  // the noise network is set (its buffers stay allocated once made)
+    // StandardExpert dropout in training (moe_set_expert_dropout)
+    float drop_p = 0.0f;
+    unsigned long long drop_seed = 0, drop_calls = 0;
     int Ep16 = 0, Dp32 = 0;
     bool router_set = false, has_bias = false;
     std::vector<char> expert_set;
@@ -641,8 +644,16 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     return MOE_OK;
 }
 
-static GemmArgs up_args(moe_handle *h, int mt_grid) {
+static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
     GemmArgs g{};
+    if (training && !h->gated && h->drop_p > 0.0f) {
+        // Dropout(p) on h in training (src/experts/standard.jl:49-51), one
+        // stream of the generator per call
+        g.drop_p = h->drop_p;
+        g.drop_scale = (float)(1.0 / (1.0 - (double)h->drop_p));
+        g.drop_seed = h->drop_seed;
+        g.drop_call = h->drop_calls++;
+    }
     g.A = h->xp; g.lda = h->D_pad;
     g.B0 = h->bf16_gemm ? h->w1t : h->w1;
     g.B1 = h->gated ? (h->bf16_gemm ? h->w3t : h->w3) : nullptr;
@@ -685,10 +696,11 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
 // The expert up GEMM (W1/W3 or W1 + activation) and the down GEMM (W2) over
 // mt_grid M tiles: the LDS-DMA kernel for bf16 and fp8 weights (bf16
 // activations), the register-staged fp32 kernel for fp32 weights.
-static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s) {
+static hipError_t launch_up(moe_handle *h, int mt_grid, hipStream_t s, bool training = false) {
     const int mode = h->gated ? MODE_GATED_UP : MODE_STD_UP;
-    if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, h->wt == WT_FP8, up_args(h, mt_grid), s);
-    return launch_grouped_gemm_f32(mode, up_args(h, mt_grid), s);
+    const GemmArgs g = up_args(h, mt_grid, training);
+    if (h->bf16_gemm) return launch_grouped_gemm_bf16(mode, h->bm, h->wt == WT_FP8, g, s);
+    return launch_grouped_gemm_f32(mode, g, s);
 }
 
 // y_f32: write y in fp32 also on the bf16-kernel path (moe_expert_forward
@@ -703,9 +715,9 @@ static hipError_t launch_down(moe_handle *h, int mt_grid, hipStream_t s, int ksp
     return launch_grouped_gemm_f32(MODE_DOWN, down_args(h, mt_grid, 1, true), s);
 }
 
-static int run_experts(moe_handle *h, int T, hipStream_t s) {
+static int run_experts(moe_handle *h, int T, int training, hipStream_t s) {
     const int mt = m_tiles_for(h, T);
-    HIP_TRY(h, launch_up(h, mt, s));
+    HIP_TRY(h, launch_up(h, mt, s, training != 0));
     HIP_TRY(h, launch_down(h, mt, s, down_ksplit(h)));
     return MOE_OK;
 }
@@ -750,7 +762,7 @@ static int forward_locked(moe_handle *h, const void *x_dev, int x_dtype, int T, 
     const int xb = x_dtype == MOE_BF16;
     r = run_routing(h, x_dev, xb, T, training, true, PERMUTE_ROWS, loss_dev, s);
     if (r != MOE_OK) return r;
-    r = run_experts(h, T, s);
+    r = run_experts(h, T, training, s);
     if (r != MOE_OK) return r;
     r = run_combine(h, T, out_dev, s);
     if (r != MOE_OK) return r;
@@ -975,6 +987,17 @@ int moe_destroy(moe_handle *h) {
 }
 
 static hipError_t build_noise_image(moe_handle *h);
+
+int moe_set_expert_dropout(moe_handle *h, float p, uint64_t seed) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (h->gated) return fail(h, MOE_EUNSUPPORTED, "dropout: StandardExpert only (GatedExpert has none)");
+    if (!(p >= 0.0f && p < 1.0f)) return fail(h, MOE_EINVAL, "dropout p must be in [0, 1)");
+    h->drop_p = p;
+    h->drop_seed = seed;
+    h->drop_calls = 0;
+    return MOE_OK;
+}
 
 int moe_set_router(moe_handle *h, const float *weight, const float *bias) {
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
@@ -1596,7 +1619,7 @@ int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream) {
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     r = join_stream(h, s);
     if (r != MOE_OK) return r;
-    HIP_TRY(h, launch_up(h, m_tiles_for(h, T), s));
+    HIP_TRY(h, launch_up(h, m_tiles_for(h, T), s, h->last_training != 0));
     return mark_stream(h, s);
 }
 

@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
                 if (MODE == MODE_GATED_UP) {
                     v = act_apply(g.act, acc[0][i][j][q]) * acc[NB - 1][i][j][q];
                 } else if (MODE == MODE_STD_UP) {
-                    v = act_apply(g.act, acc[0][i][j][q] + bias);
+                    v = dropout_h(g, arow0 + ml, n, act_apply(g.act, acc[0][i][j][q] + bias));
                 } else {
                     v = acc[0][i][j][q] + bias;
                 }

@@ -311,8 +311,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
                         for (int c = 0; c < 4; ++c) a[4 * g4 + c] = a[4 * g4 + c] * sc[c];
                     }
                     if constexpr (MODE == MODE_STD_UP) {
-                        put(ml, lc, act_fast<ACT>(a[4 * g4 + 0] + b4[0]), act_fast<ACT>(a[4 * g4 + 1] + b4[1]),
-                            act_fast<ACT>(a[4 * g4 + 2] + b4[2]), act_fast<ACT>(a[4 * g4 + 3] + b4[3]));
+                        float h4[4];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            h4[c] = dropout_h(g, jb.arow0 + ml, n + c, act_fast<ACT>(a[4 * g4 + c] + b4[c]));
+                        put(ml, lc, h4[0], h4[1], h4[2], h4[3]);
                     } else if (yb) {
                         put(ml, lc, a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1], a[4 * g4 + 2] + b4[2],
                             a[4 * g4 + 3] + b4[3]);

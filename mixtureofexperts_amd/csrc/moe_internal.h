@@ -56,16 +56,24 @@ __host__ __device__ inline float fp8e4m3_to_f32(uint8_t b) {
     return (b & 0x80u) ? -v : v;
 }
 
-// Counter-based standard normal for (seed, stream, index): a splitmix64 hash
-// of the three gives two 24-bit uniforms in (0, 1), Box-Muller gives N(0, 1).
-__device__ inline float init_normal(unsigned long long seed, unsigned long long stream, unsigned long long i) {
+// Counter-based generator: a splitmix64 hash of (seed, stream, index).
+__device__ inline unsigned long long rng_hash(unsigned long long seed, unsigned long long stream, unsigned long long i) {
     unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (stream + 1) + 0xD1B54A32D192ED03ull * i;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    z ^= z >> 31;
+    return z ^ (z >> 31);
+}
+// Standard normal for (seed, stream, index): the hash's two 24-bit uniforms
+// in (0, 1), Box-Muller gives N(0, 1).
+__device__ inline float init_normal(unsigned long long seed, unsigned long long stream, unsigned long long i) {
+    const unsigned long long z = rng_hash(seed, stream, i);
     const float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
     const float u2 = ((float)(z & 0xFFFFFFull) + 0.5f) * (1.0f / 16777216.0f);
     return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+// Uniform in (0, 1) for (seed, stream, index): the hash's top 24 bits.
+__device__ inline float init_uniform(unsigned long long seed, unsigned long long stream, unsigned long long i) {
+    return ((float)(rng_hash(seed, stream, i) >> 40) + 0.5f) * (1.0f / 16777216.0f);
 }
 
 // Julia `isless` total order as an unsigned key: every NaN is largest,
@@ -262,7 +270,21 @@ struct GemmArgs {
     float *split_ws;                     // partials of split tiles (MODE_DOWN, ksplit > 1)
     int act;
     int c_bf16;                          // MODE_DOWN: y in bf16 (else fp32)
+    // MODE_STD_UP in training: StandardExpert's Dropout(drop_p)
+    // (src/experts/standard.jl:49-51): element (row pos, column n) of h is
+    // kept, times drop_scale = Float32(1 / (1 - p)), when
+    // init_uniform(drop_seed, drop_call, pos N + n) > p, else 0
+    float drop_p, drop_scale;
+    unsigned long long drop_seed, drop_call;
 };
+
+__device__ inline float dropout_h(const GemmArgs &g, long long pos, int n, float v) {
+    if (g.drop_p > 0.0f) {
+        const float u = init_uniform(g.drop_seed, g.drop_call, (unsigned long long)pos * g.N + n);
+        v = (u > g.drop_p) ? v * g.drop_scale : 0.0f;
+    }
+    return v;
+}
 
 // Decode (moe_ffn_forward!, src/llama2/inference.jl:58-121): n tokens, each
 // routed and combined on its own, slots in order.

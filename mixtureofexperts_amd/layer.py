@@ -115,6 +115,7 @@ class MoELayer:
             noise_scale=config.noise_scale, use_noise_network=config.use_noise_network,
             use_fp32=config.use_fp32_router, rng=rng)
         self.balance_loss = config.balance_loss
+        self._drop_seed = int(rng.integers(0, 2**63)) if config.expert_dropout > 0 else 0
         self.training_stats = {
             "tokens_per_expert": np.zeros(config.num_experts, dtype=np.int64),
             "routing_entropy": [],
@@ -123,11 +124,6 @@ class MoELayer:
         self._dev = None
 
     # ---- device state ----------------------------------------------------
-    def _check_supported(self, training):
-        c = self.config
-        if training and c.expert_dropout > 0 and c.expert_type != "gated":
-            raise _lib.MoeError(_lib.MOE_EUNSUPPORTED, "expert dropout in training has no device path")
-
     def _new_device(self):
         """A device handle for this layer's configuration (no weights yet)."""
         c = self.config
@@ -154,6 +150,11 @@ class MoELayer:
                                        None if nw is None else np.ascontiguousarray(nw.T), self.router.noise_seed)
         for e, ex in enumerate(self.experts):
             ex.upload(self._dev, e)
+        p = max([getattr(ex, "dropout", 0.0) for ex in self.experts] + [0.0])
+        if p > 0 and self.config.expert_type != "gated":
+            # StandardExpert's Dropout(p) in training (standard.jl:49-51),
+            # the layer's experts share p (MoEConfig.expert_dropout)
+            self._dev.set_expert_dropout(p, self._drop_seed)
         return self._dev
 
     def close(self):
@@ -173,7 +174,6 @@ class MoELayer:
         x: (input_dim, T) float32, or uint16 bf16 bit patterns with
         ``x_dtype="bf16"``.  Returns (output (output_dim, T) float32,
         balance_loss float32[, training_stats])."""
-        self._check_supported(training)
         xa = np.asarray(x)
         if xa.ndim != 2 or xa.shape[0] != self.config.input_dim:
             raise _lib.MoeError(_lib.MOE_EINVAL, f"x must be ({self.config.input_dim}, T), got {xa.shape}")

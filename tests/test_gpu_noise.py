@@ -1,4 +1,5 @@
-"""Router noise in training (src/core/router.jl:32-41) on the GPU.
+"""Router noise (src/core/router.jl:32-41) and StandardExpert dropout
+(src/experts/standard.jl:49-51) in training, on the GPU.
 
 The noise comes from the library's counter-based generator, not Julia's randn
 stream, so the draws are checked by their distribution: the difference of the
@@ -100,4 +101,65 @@ def test_layer_router_noise_python_api(moe):
     assert np.array_equal(y0, y2) and l0 == 0.0 and l2 == 0.0
     assert np.isfinite(l1) and l1 > 0
     assert not np.array_equal(y0, y1)  # the noisy gate routes some tokens differently
+    layer.close()
+
+
+@pytest.mark.parametrize("wdtype", ["f32", "bf16"])
+def test_standard_expert_dropout(moe, oracle, wdtype):
+    """StandardExpert's Dropout(p) in training (src/experts/standard.jl:49-51):
+    with W1 = W2 = I, zero biases, the identity activation and k = 1 (gate
+    exactly 1) the layer output is dropout(x): every element is 0 or x *
+    Float32(1 / (1 - p)) (fp32: exactly; bf16: x and h rounded to bf16), the
+    zeros are a fraction p of the elements, and inference calls keep x."""
+    from mixtureofexperts_amd import _lib
+    from mixtureofexperts_amd._device import DeviceLayer, GateSpec
+
+    T, D, E, p = 512, 64, 4, 0.25
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    if wdtype == "bf16":
+        x = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(x))
+    wr = rng.standard_normal((E, D)).astype(np.float32)
+    eye = np.eye(D, dtype=np.float32)
+    wcode = {"f32": _lib.MOE_F32, "bf16": _lib.MOE_BF16}[wdtype]
+    dev = DeviceLayer(num_experts=E, expert_type=_lib.MOE_EXPERT_STANDARD, input_dim=D, hidden_dim=D, output_dim=D,
+                      activation=_lib.MOE_ACT_IDENTITY, gate=GateSpec(_lib.MOE_GATE_TOPK, 1, 0), weight_dtype=wcode,
+                      balance_alpha=0.01, z_loss_weight=0.001, capacity_factor=1.25, drop_tokens=False,
+                      max_tokens=T, num_shared_experts=0)
+    dev.set_router(np.ascontiguousarray(wr.T), None)
+    for e in range(E):
+        dev.set_expert(e, eye, eye, None, np.zeros(D, np.float32), np.zeros(D, np.float32), src_dtype=_lib.MOE_F32)
+    dev.set_expert_dropout(p, seed=77)
+    y_inf, _, _ = dev.forward(x, _lib.MOE_F32, False)
+    assert np.array_equal(y_inf, x)
+    y, _, _ = dev.forward(x, _lib.MOE_F32, True)
+    scale = np.float32(1.0 / (1.0 - p))
+    kept = (x * scale).astype(np.float32)
+    if wdtype == "bf16":
+        kept = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(kept))
+    zero = y == 0
+    assert np.array_equal(y[~zero], kept[~zero])
+    frac = float(zero.mean())
+    assert abs(frac - p) < 5 * np.sqrt(p * (1 - p) / zero.size), frac
+    # a new mask per training call, the same one from the same seed
+    y2, _, _ = dev.forward(x, _lib.MOE_F32, True)
+    assert not np.array_equal(y2 == 0, zero)
+    dev.set_expert_dropout(p, seed=77)
+    y3, _, _ = dev.forward(x, _lib.MOE_F32, True)
+    assert np.array_equal(y3, y)
+    dev.set_expert_dropout(0.0, seed=77)
+    y4, _, _ = dev.forward(x, _lib.MOE_F32, True)
+    assert np.array_equal(y4, x)
+    dev.close()
+
+
+def test_layer_expert_dropout_python_api(moe):
+    cfg = moe.MoEConfig(num_experts=4, expert_type="standard", input_dim=64, hidden_dim=128, output_dim=64,
+                        gate_type=moe.TopKGating(2), expert_dropout=0.3, max_tokens=128)
+    layer = moe.MoELayer(cfg, rng=np.random.default_rng(8))
+    x = np.random.default_rng(9).standard_normal((64, 128)).astype(np.float32)
+    y0, _ = layer(x, training=False)
+    y1, _ = layer(x, training=True)
+    y2, _ = layer(x, training=False)
+    assert np.array_equal(y0, y2) and not np.array_equal(y0, y1)
     layer.close()
