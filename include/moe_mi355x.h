@@ -351,6 +351,12 @@ int moe_stage_expert_up_async(moe_handle *h, int32_t T, void *stream);
 int moe_stage_expert_down_async(moe_handle *h, int32_t T, void *stream);
 int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stream);
 
+/* Per-token logsumexp of the last routing call's logits (the z-loss's
+ * lse_t = max + log(sum(exp(l - max))), src/balancing/losses.jl:111-114;
+ * with router noise, of the logits without noise) -> lse [T] float, host
+ * memory.  T must be that call's token count.  Blocking. */
+int moe_router_lse(moe_handle *h, int32_t T, float *lse);
+
 /* Copy the per-expert counts of the last call to host memory (int32 [E]). */
 int moe_read_counts(moe_handle *h, int32_t *counts);
 

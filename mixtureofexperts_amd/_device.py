@@ -81,6 +81,12 @@ class DeviceLayer:
         _lib.check(_lib.lib().moe_set_router_noise(self.h, float(noise_scale), _ptr(w), int(seed) & (2**64 - 1)),
                    self.h)
 
+    def router_lse(self, T):
+        """Per-token logsumexp of the last routing call's logits (float32 [T])."""
+        out = np.zeros(T, np.float32)
+        _lib.check(_lib.lib().moe_router_lse(self.h, int(T), out.ctypes.data), self.h)
+        return out
+
     def set_expert_dropout(self, p, seed=0):
         """StandardExpert's Dropout(p) in training (standard.jl:49-51)."""
         _lib.check(_lib.lib().moe_set_expert_dropout(self.h, float(p), int(seed) & (2**64 - 1)), self.h)

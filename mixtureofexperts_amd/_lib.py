@@ -35,7 +35,7 @@ MOE_MAX_EXPERTS = 128
 # every symbol the header declares (checked by the CPU test suite)
 EXPORTED_SYMBOLS = [
     "moe_create", "moe_destroy", "moe_last_error", "moe_abi_version",
-    "moe_router_outputs", "moe_slots_per_token", "moe_set_router", "moe_set_router_noise", "moe_set_expert_dropout", "moe_set_expert",
+    "moe_router_outputs", "moe_slots_per_token", "moe_set_router", "moe_set_router_noise", "moe_set_expert_dropout", "moe_router_lse", "moe_set_expert",
     "moe_compute_gates", "moe_route_from_logits", "moe_forward", "moe_expert_forward",
     "moe_forward_async", "moe_stage_router_async", "moe_stage_permute_async",
     "moe_stage_expert_up_async", "moe_stage_expert_down_async", "moe_stage_combine_async",
@@ -124,6 +124,7 @@ def lib():
     L.moe_set_router.argtypes = [vp, vp, vp]
     L.moe_set_router_noise.argtypes = [vp, ctypes.c_float, vp, ctypes.c_uint64]
     L.moe_set_expert_dropout.argtypes = [vp, ctypes.c_float, ctypes.c_uint64]
+    L.moe_router_lse.argtypes = [vp, i32, vp]
     L.moe_set_expert.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
     L.moe_compute_gates.argtypes = [vp, vp, i32, vp, vp, vp]
     L.moe_route_from_logits.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]

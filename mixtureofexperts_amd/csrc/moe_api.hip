@@ -82,6 +82,8 @@ struct moe_handle {
     int bm = kGemmBM;           // GEMM tile rows of this handle's kernels (scan granule)
     bool bf16_gemm = false;     // bf16 weights and activations: the LDS-DMA MFMA kernel
     float *logits = nullptr, *probs = nullptr, *gates = nullptr, *gate_sorted = nullptr;
+    float *lse = nullptr;          // [T] per-token logsumexp of the last routing call
+    int last_route_T = -1;         // T of the last routing call
     float *logits_in = nullptr;    // [T][Er] the caller's logits (routing from logits)
     int rb = kRtMinBlock;          // tokens per route block of the last routing call
     int ldc = 0;                   // row stride of blk_counts (E rounded up to 4)
@@ -599,6 +601,8 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     const int par = h->rpar;
     h->rpar ^= 1;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.ldc = h->ldc; ra.blk_zh = h->blk_zh;
+    ra.lse = h->lse;
+    h->last_route_T = T;
     ra.tot_cnt = h->tot_cnt2 + (size_t)par * h->E; ra.tot_p = h->tot_p2 + (size_t)par * h->E;
     ra.clr_cnt = h->tot_cnt2 + (size_t)(par ^ 1) * h->E; ra.clr_p = h->tot_p2 + (size_t)(par ^ 1) * h->E;
     ra.nsup_max = h->nsup_max;
@@ -903,6 +907,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->logits, sizeof(float) * T * h->Er);
     A((void **)&h->logits_in, sizeof(float) * T * h->Er);
     A((void **)&h->probs, sizeof(float) * T * h->Er);
+    A((void **)&h->lse, sizeof(float) * T);
     A((void **)&h->idx, sizeof(int) * nent);
     A((void **)&h->gates, sizeof(float) * nent);
     A((void **)&h->rank, sizeof(int) * nent);
@@ -987,6 +992,20 @@ int moe_destroy(moe_handle *h) {
 }
 
 static hipError_t build_noise_image(moe_handle *h);
+
+int moe_router_lse(moe_handle *h, int32_t T, float *lse) {
+    if (!h) return fail(nullptr, MOE_EINVAL, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (!lse) return fail(h, MOE_EINVAL, "null lse");
+    if (T != h->last_route_T || T < 1) return fail(h, MOE_EINVAL, "T must be the last routing call's token count");
+    hipStream_t s = h->stream;
+    int r = join_stream(h, s);
+    if (r != MOE_OK) return r;
+    HIP_TRY(h, hipMemcpyAsync(lse, h->lse, sizeof(float) * (size_t)T, hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    settle(h);
+    return MOE_OK;
+}
 
 int moe_set_expert_dropout(moe_handle *h, float p, uint64_t seed) {
     if (!h) return fail(nullptr, MOE_EINVAL, "null handle");

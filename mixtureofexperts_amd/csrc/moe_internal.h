@@ -115,6 +115,7 @@ struct RouteArgs {
     int given;             // idx / gates hold the caller's routing (no top-k); probs from
     int given_probs;       //   a.probs when given_probs, else 1/E
     float *probs;          // [T][E]
+    float *lse;            // [T] per-token logsumexp of the z-loss's logits (probabilities pass), or null
     int *idx;              // [T][kt]
     float *gates;          // [T][kt]
     int *rank;             // [T][kt] rank of the entry inside its block & expert

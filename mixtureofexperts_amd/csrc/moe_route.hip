@@ -661,6 +661,7 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     if (softmax && rvalid && rs == 0) {
         zterm = (double)(lse * lse);
         hterm = -hs;
+        if (out_probs && a.lse) a.lse[t] = lse;
     }
 #pragma unroll
     for (int o = 8; o < 64; o <<= 1) {

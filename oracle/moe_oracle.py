@@ -177,6 +177,16 @@ def z_loss(logits, beta):
     return np.float32(_lib().oracle_z_loss(lg.ctypes.data, T, E, np.float32(beta), None))
 
 
+def logsumexp_rows(logits):
+    """Per-token lse_t = m + log(sum(exp(l - m))) of the z-loss
+    (src/balancing/losses.jl:111-114), the same recipe as z_loss."""
+    lg = _c(logits, np.float32)
+    T, E = lg.shape
+    out = np.zeros(T, np.float32)
+    _lib().oracle_z_loss(lg.ctypes.data, T, E, np.float32(1.0), out.ctypes.data)
+    return out
+
+
 def mean_entropy(probs):
     p = _c(probs, np.float32)
     return np.float32(_lib().oracle_mean_entropy(p.ctypes.data, p.shape[0], p.shape[1]))

@@ -590,3 +590,20 @@ def test_random_layer_shapes(moe, oracle):
             check_case(c, TOL[wdtype])
         finally:
             c.dev.close()
+
+
+def test_router_lse(moe, oracle):
+    """Per-token logsumexp of the z-loss (src/balancing/losses.jl:111-114)
+    from moe_router_lse after a layer forward: within 2 ulp of the oracle's on
+    the GPU's logits, and its squares' mean times beta is the z-loss."""
+    case = Case(moe, oracle, T=1000, D=96, H=64, E=12, k=2, seed=41, z=0.01)
+    out, loss, res = case.run(training=True)
+    lse = case.dev.router_lse(case.T)
+    ref = oracle.logsumexp_rows(res["logits"])
+    assert np.all(np.abs(lse - ref) <= 2.5e-7 * np.maximum(1.0, np.abs(ref))), np.max(np.abs(lse - ref))
+    zl = np.float32(0.01) * np.float32(np.mean((lse.astype(np.float64)) ** 2))
+    assert abs(res["z_loss"] - zl) <= 1e-5 * max(1.0, abs(float(zl)))
+    from mixtureofexperts_amd import _lib
+
+    with pytest.raises(_lib.MoeError):
+        case.dev.router_lse(case.T - 1)

@@ -737,3 +737,21 @@ def test_decode_ffn_combines_in_slot_order(oracle):
     for j in order:
         expert = (expert + gates[0, j] * ys[j]).astype(np.float32)
     assert not np.array_equal(slot, expert)  # the case distinguishes the two orders
+
+
+def test_logsumexp_rows_closed_forms(oracle):
+    # zero logits: lse = ln E; a constant shift c: lse + c; one dominant
+    # logit: lse -> that logit; against a float64 restatement on random rows
+    E = 7
+    z = oracle.logsumexp_rows(np.zeros((3, E), np.float32))
+    assert np.allclose(z, np.log(E), rtol=2e-7)
+    rng = np.random.default_rng(0)
+    lg = rng.standard_normal((50, E)).astype(np.float32)
+    a = oracle.logsumexp_rows(lg)
+    b = oracle.logsumexp_rows((lg + np.float32(3.0)).astype(np.float32))
+    assert np.allclose(b, a + 3.0, rtol=1e-6, atol=1e-6)
+    ref = np.log(np.sum(np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True)), 1)) + lg.max(1)
+    assert np.allclose(a, ref, rtol=1e-6, atol=1e-6)
+    d = np.zeros((1, E), np.float32)
+    d[0, 2] = 200.0
+    assert oracle.logsumexp_rows(d)[0] == np.float32(200.0)
