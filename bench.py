@@ -9,7 +9,11 @@ and are resident in HBM before the timed region.
 One step = one MoE-layer forward over the 4096-token batch, issued as its five
 stages (router, permute, expert up GEMM, expert down GEMM, combine) with HIP
 events between them on the launch stream, so the per-kernel times come from
-the timed region itself.  Prints one JSON line.
+the timed region itself ("stages").  After the timed region each stage is
+also launched --stage-reps times back to back between two events
+("stages_steady": per launch, the stage's kernels plus the stream's gap
+between consecutive kernels, without the per-stage event's dispatch latency).
+Prints one JSON line.
 """
 import argparse
 import ctypes
@@ -295,6 +299,8 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=4096,
                     help="tokens of the workload the CPU baseline runs (default: all of the mixtral batch)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stage-reps", type=int, default=20,
+                    help="back-to-back launches per stage for the steady-state stage times")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the timed region, run one plain device copy of MIB MiB (fp32 multiply by 1, "
                          "read MIB and write MIB): the reference kernel that scales rocprofv3 FETCH_SIZE / "
@@ -361,6 +367,30 @@ def main():
     stage_ms = {n: float(np.mean([ev[j].elapsed_time(ev[j + 1]) for ev in events])) for j, n in enumerate(stage_names)}
     assert bool(torch.isfinite(wl["out"]).all()), "non-finite output"
 
+    # Steady-state stage times, after the timed region: each stage launched
+    # args.stage_reps times back to back between two events (every stage is
+    # idempotent on the handle's buffers), divided by the count.  Each launch
+    # then costs its kernels plus the stream's gap between consecutive
+    # kernels, as inside a forward; the per-stage events of the timed region
+    # add each stage's dispatch latency after an event on top of that.
+    stage_fns = [lambda: L.moe_stage_router_async(h, xp, xcode, T, 1, sp),
+                 lambda: L.moe_stage_permute_async(h, xp, xcode, T, sp),
+                 lambda: L.moe_stage_expert_up_async(h, T, sp),
+                 lambda: L.moe_stage_expert_down_async(h, T, sp),
+                 lambda: L.moe_stage_combine_async(h, T, op, sp)]
+    steady_ms = {}
+    reps = max(1, args.stage_reps)
+    for n, fn in zip(stage_names, stage_fns):
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _lib.check(fn(), h)
+        ea.record(stream)
+        for _ in range(reps):
+            _lib.check(fn(), h)
+        eb.record(stream)
+        torch.cuda.synchronize()
+        steady_ms[n] = ea.elapsed_time(eb) / reps
+    assert bool(torch.isfinite(wl["out"]).all()), "non-finite output"
+
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -416,6 +446,18 @@ def main():
             "expert_up": {"ms": round(stage_ms["expert_up"], 4), "TFLOP/s": round(up_tflops, 1)},
             "expert_down": {"ms": round(stage_ms["expert_down"], 4), "TFLOP/s": round(down_tflops, 1)},
             "combine": {"ms": round(stage_ms["combine"], 4), "GB/s": round(gbs(combine_bytes, stage_ms["combine"]), 1)},
+        },
+        "stages_steady": {
+            "reps": reps,
+            "router": {"ms": round(steady_ms["router"], 4), "GB/s": round(gbs(router_bytes, steady_ms["router"]), 1)},
+            "permute": {"ms": round(steady_ms["permute"], 4),
+                        "GB/s": round(gbs(permute_bytes, steady_ms["permute"]), 1)},
+            "expert_up": {"ms": round(steady_ms["expert_up"], 4),
+                          "TFLOP/s": round(up_flops / (steady_ms["expert_up"] * 1e-3) / 1e12, 1)},
+            "expert_down": {"ms": round(steady_ms["expert_down"], 4),
+                            "TFLOP/s": round(down_flops / (steady_ms["expert_down"] * 1e-3) / 1e12, 1)},
+            "combine": {"ms": round(steady_ms["combine"], 4),
+                        "GB/s": round(gbs(combine_bytes, steady_ms["combine"]), 1)},
         },
         "expert_counts": counts.tolist(),
     }
