@@ -231,6 +231,14 @@ __device__ __forceinline__ int b_frag_row(int j, int wn) {
     return (NB == 2) ? ((j & 1) * 128 + wn * (WN / 2) + (j >> 1) * 32) : (wn * WN + j * 32);
 }
 
+// Component c (a compile-time constant after unrolling) of a float4.
+__device__ __forceinline__ float f4_at(const float4 &v, int c) {
+    return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+}
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
 // ---- epilogue ---------------------------------------------------------------------
 // The MFMA computes the transposed block (weights are its A operand): lane l
 // holds token row l % 32 of the 32-row block and output columns 8 (q / 4) +
@@ -251,33 +259,40 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
     const int half = lane >> 5;
     const int r32 = lane & 31;
     const long long sofs = (long long)jb.e * g.s_stride;
-    auto scale4 = [&](const float *sp, int n, float *sc) {
-        if constexpr (WF8) {
-            const float4 v = *(const float4 *)(sp + sofs + n);
-            sc[0] = v.x; sc[1] = v.y; sc[2] = v.z; sc[3] = v.w;
-        } else {
-            sc[0] = sc[1] = sc[2] = sc[3] = 1.0f;
-        }
-    };
+    // The per-column vectors of the lane's column groups (weight scales, the
+    // bias) are loaded in batches ahead of the accumulator reads that use
+    // them: each load placed next to its use would wait out the round trip of
+    // the one before it.
     if constexpr (MODE == MODE_GATED_UP) {
         // h pad columns [N, Npad) come out as act(0) * 0 = 0 from the zero weight
         // pad rows, so the whole tile is stored (ldc = Npad).
+        constexpr int NG = (JN / 2) * 4;  // column groups of 4 h columns of the lane
+        float4 sg[NG], su[NG];
+        if constexpr (WF8) {
+#pragma unroll
+            for (int q = 0; q < NG; ++q) {
+                const int lc = wn * (WN / 2) + (q >> 2) * 32 + 8 * (q & 3) + 4 * half;
+                sg[q] = *(const float4 *)(g.s0 + sofs + jb.n0 + lc);
+                su[q] = *(const float4 *)(g.s1 + sofs + jb.n0 + lc);
+            }
+        }
 #pragma unroll
         for (int m = 0; m < JN / 2; ++m)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
+                const int q = m * 4 + g4;
                 const int lc = wn * (WN / 2) + m * 32 + 8 * g4 + 4 * half;
-                float sg[4], su[4];
-                scale4(g.s0, jb.n0 + lc, sg);
-                scale4(g.s1, jb.n0 + lc, su);
 #pragma unroll
                 for (int i = 0; i < IM; ++i) {
                     const int ml = row0 + i * 32 + r32;
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const float gt = WF8 ? acc[i][2 * m][4 * g4 + c] * sg[c] : acc[i][2 * m][4 * g4 + c];
-                        const float up = WF8 ? acc[i][2 * m + 1][4 * g4 + c] * su[c] : acc[i][2 * m + 1][4 * g4 + c];
+                        float gt = acc[i][2 * m][4 * g4 + c], up = acc[i][2 * m + 1][4 * g4 + c];
+                        if constexpr (WF8) {
+                            gt = gt * f4_at(sg[q], c);
+                            up = up * f4_at(su[q], c);
+                        }
                         v[c] = act_fast<ACT>(gt) * up;
                     }
                     put(ml, lc, v[0], v[1], v[2], v[3]);
@@ -286,60 +301,85 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
     } else {
         // MODE_STD_UP stores bf16 h (pads are act(b1 pad = 0) of zero rows: 0 for
         // silu, gelu, relu, identity); MODE_DOWN stores y with ldc = N, in bf16
-        // (c_bf16) or fp32.
+        // (c_bf16) or fp32.  The lane's column blocks in two parts (four with
+        // fp8 scales on 256-row tiles, whose accumulators leave fewer
+        // registers), each with one batch of vector loads.
         const bool vec4 = (MODE == MODE_STD_UP) || ((g.ldc & 3) == 0);
         const bool yb = (MODE == MODE_STD_UP) || (g.c_bf16 && jb.nks == 1);
+        const bool has_bias = g.bias && jb.ks == 0;  // split K: the bias belongs to one partial sum only
+        constexpr int JH = (WF8 && IM == 4) ? 1 : (JN + 1) / 2;  // column blocks per part
+        auto part = [&](auto H_, auto DROP_) {
+            constexpr int H = decltype(H_)::value;
+            constexpr bool DROP = decltype(DROP_)::value;
+            constexpr int J0 = H * JH, J1 = (J0 + JH < JN) ? J0 + JH : JN;
+            float4 bv[JH * 4], sc[JH * 4];
 #pragma unroll
-        for (int j = 0; j < JN; ++j)
+            for (int q = 0; q < (J1 - J0) * 4; ++q) {
+                const int n = jb.n0 + wn * WN + (J0 + (q >> 2)) * 32 + 8 * (q & 3) + 4 * half;
+                bv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (has_bias) bv[q] = *(const float4 *)(g.bias + sofs + n);
+                if constexpr (WF8) sc[q] = *(const float4 *)(g.s0 + sofs + n);
+            }
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                const int lc = wn * WN + j * 32 + 8 * g4 + 4 * half;
-                const int n = jb.n0 + lc;
-                float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g.bias && jb.ks == 0) {  // split K: the bias belongs to one partial sum only
-                    const float4 bv = *(const float4 *)(g.bias + sofs + n);
-                    b4[0] = bv.x; b4[1] = bv.y; b4[2] = bv.z; b4[3] = bv.w;
-                }
-                float sc[4];
-                scale4(g.s0, n, sc);
+            for (int j = J0; j < J1; ++j)
 #pragma unroll
-                for (int i = 0; i < IM; ++i) {
-                    const int ml = row0 + i * 32 + r32;
-                    f32x16_t a = acc[i][j];
-                    if constexpr (WF8) {
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int q = (j - J0) * 4 + g4;
+                    const int lc = wn * WN + j * 32 + 8 * g4 + 4 * half;
+                    const int n = jb.n0 + lc;
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) a[4 * g4 + c] = a[4 * g4 + c] * sc[c];
-                    }
-                    if constexpr (MODE == MODE_STD_UP) {
-                        float h4[4];
+                    for (int i = 0; i < IM; ++i) {
+                        const int ml = row0 + i * 32 + r32;
+                        float a[4];
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            h4[c] = dropout_h(g, jb.arow0 + ml, n + c, act_fast<ACT>(a[4 * g4 + c] + b4[c]));
-                        put(ml, lc, h4[0], h4[1], h4[2], h4[3]);
-                    } else if (yb) {
-                        put(ml, lc, a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1], a[4 * g4 + 2] + b4[2],
-                            a[4 * g4 + 3] + b4[3]);
-                    } else {
-                        if (ml >= jb.rows) continue;
-                        // fp32 y: K range 0 (or an unsplit tile) writes y; range
-                        // r >= 1 its partial block in split_ws (BM x 256, row
-                        // stride 256).  bf16 y: every range writes its block.
-                        const long long blk = g.c_bf16 ? (long long)jb.split_j * jb.nks + jb.ks
-                                                       : (long long)jb.split_j * (jb.nks - 1) + jb.ks - 1;
-                        float *crow = (jb.ks == 0 && !g.c_bf16)
-                                          ? (float *)g.C + (jb.arow0 + ml) * g.ldc
-                                          : g.split_ws + blk * (IM * 64) * 256 + (long long)ml * 256 - jb.n0;
-                        if (vec4 && n + 3 < g.N) {
-                            *(float4 *)(crow + n) = make_float4(a[4 * g4 + 0] + b4[0], a[4 * g4 + 1] + b4[1],
-                                                                a[4 * g4 + 2] + b4[2], a[4 * g4 + 3] + b4[3]);
+                        for (int c = 0; c < 4; ++c) {
+                            a[c] = acc[i][j][4 * g4 + c];
+                            if constexpr (WF8) a[c] = a[c] * f4_at(sc[q], c);
+                            a[c] = a[c] + f4_at(bv[q], c);
+                        }
+                        if constexpr (MODE == MODE_STD_UP) {
+                            float h4[4];
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                h4[c] = act_fast<ACT>(a[c]);
+                                if constexpr (DROP) h4[c] = dropout_h(g, jb.arow0 + ml, n + c, h4[c]);
+                            }
+                            put(ml, lc, h4[0], h4[1], h4[2], h4[3]);
+                        } else if (yb) {
+                            put(ml, lc, a[0], a[1], a[2], a[3]);
                         } else {
+                            if (ml >= jb.rows) continue;
+                            // fp32 y: K range 0 (or an unsplit tile) writes y; range
+                            // r >= 1 its partial block in split_ws (BM x 256, row
+                            // stride 256).  bf16 y: every range writes its block.
+                            const long long blk = g.c_bf16 ? (long long)jb.split_j * jb.nks + jb.ks
+                                                           : (long long)jb.split_j * (jb.nks - 1) + jb.ks - 1;
+                            float *crow = (jb.ks == 0 && !g.c_bf16)
+                                              ? (float *)g.C + (jb.arow0 + ml) * g.ldc
+                                              : g.split_ws + blk * (IM * 64) * 256 + (long long)ml * 256 - jb.n0;
+                            if (vec4 && n + 3 < g.N) {
+                                *(float4 *)(crow + n) = make_float4(a[0], a[1], a[2], a[3]);
+                            } else {
 #pragma unroll
-                            for (int c = 0; c < 4; ++c)
-                                if (n + c < g.N) crow[n + c] = a[4 * g4 + c] + b4[c];
+                                for (int c = 0; c < 4; ++c)
+                                    if (n + c < g.N) crow[n + c] = a[c];
+                            }
                         }
                     }
                 }
-            }
+        };
+        auto tile = [&](auto DROP_) {
+            part(ic<0>{}, DROP_);
+            if constexpr (JN > JH) part(ic<1>{}, DROP_);
+            if constexpr (JN > 2 * JH) part(ic<2>{}, DROP_);
+            if constexpr (JN > 3 * JH) part(ic<3>{}, DROP_);
+        };
+        if constexpr (MODE == MODE_STD_UP) {
+            if (g.drop_p > 0.0f) tile(std::true_type{});
+            else tile(std::false_type{});
+        } else {
+            tile(std::false_type{});
+        }
     }
 }
 
@@ -445,9 +485,6 @@ __device__ __forceinline__ void store_staged(const GemmArgs &g, const TileJob &j
         else if constexpr (J == 4) return (MOE_LDS_AS uint8_t *)slot4;                     \
         else return (MOE_LDS_AS uint8_t *)slot5;                                           \
     }
-
-template <int N>
-using ic = std::integral_constant<int, N>;
 
 // Prologue: this wave's NL loads of stages 0 .. NS-2 (clamped to the last
 // stage), stage s into slot s.
