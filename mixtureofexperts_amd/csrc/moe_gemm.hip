@@ -16,7 +16,8 @@
 //
 // Tile: 128 x 128 outputs per B matrix, 4 waves in a 2 x 2 layout, each wave
 // 64 x 64 = 2 x 2 blocks of v_mfma_f32_32x32x2_f32, four per 16-byte
-// fragment.  LDS rows of 128 B are XOR-swizzled in 16-byte chunks so both the
+// fragment (a tile of at most 32 rows: 1 x 4 waves of one 32 x 32 block; the
+// blocks past the tile's rows run no MFMAs).  LDS rows of 128 B are XOR-swizzled in 16-byte chunks so both the
 // stores and the fragment reads are bank-conflict free.
 #include "moe_internal.h"
 
@@ -70,8 +71,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = (wave & 1) * 64;
-    const int wn = (wave >> 1) * 64;
+    // Wave layout: 2 x 2 waves of 64 x 64 outputs; a tile of at most 32 rows
+    // (a small expert segment) runs 1 x 4 waves of 32 x 32, so that all four
+    // SIMDs share its MFMAs.
+    const bool skinny = rows <= 32;
+    const int wm = skinny ? 0 : (wave & 1) * 64;
+    const int wn = skinny ? wave * 32 : (wave >> 1) * 64;
+    const int nj = skinny ? 1 : 2;  // 32-column blocks of the wave
 
     const uint8_t *Ab = (const uint8_t *)g.A;
     const long long lda_b = g.lda * 4;
@@ -118,6 +124,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
     const int KT = g.K / BK;
     const int half = lane >> 5;
     const int r32 = lane & 31;
+    // 32-row blocks of this wave that hold rows of the tile (wave-uniform): an
+    // expert's last tile runs MFMAs only on those; the other accumulators stay
+    // 0 and their rows are not stored
+    const int nv = __builtin_amdgcn_readfirstlane(min(2, max(0, rows - wm + 31) >> 5));
     MOE_LOAD_TILES(0);
     for (int kt = 0; kt < KT; ++kt) {
         __syncthreads();
@@ -134,13 +144,14 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    bfr[b][j] = *(const f32x4_t *)(lds + (BM + b * BN) * ROWB + lds_off(wn + j * 32 + r32, chunk));
+                    if (j < nj) bfr[b][j] = *(const f32x4_t *)(lds + (BM + b * BN) * ROWB + lds_off(wn + j * 32 + r32, chunk));
 #pragma unroll
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
+                        if (i >= nv || j >= nj) continue;  // no row of the tile, or not the wave's
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].x, bfr[b][j].x, acc[b][i][j], 0, 0, 0);
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].y, bfr[b][j].y, acc[b][i][j], 0, 0, 0);
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].z, bfr[b][j].z, acc[b][i][j], 0, 0, 0);
@@ -156,6 +167,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
     const long long sofs = (long long)e * g.s_stride;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
+        if (j >= nj) continue;
         const int nl = wn + j * 32 + r32;
         const int n = n0 + nl;
         if (n >= g.N) continue;
