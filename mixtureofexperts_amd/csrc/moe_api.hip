@@ -92,9 +92,8 @@ struct moe_handle {
     bool keep_rows = false;        // the next routing call writes logits / probs to global memory
     int *idx = nullptr, *rank = nullptr, *blk_counts = nullptr;
     double *blk_zh = nullptr;                 // [nblk][2] per route block z-loss / entropy sums
-    int *tot_cnt2 = nullptr;                  // [2][E] expert counts of a call (two parities)
-    unsigned long long *tot_p2 = nullptr;     // [2][E] probability sums of a call, fixed point
-    int *sup_cnt2 = nullptr;                  // [2][nsup_max][ldc] expert counts per super block
+    int *sup_cnt2 = nullptr;                  // [2][nsup_max][ldc] expert counts per super block (two parities)
+    unsigned long long *sup_p2 = nullptr;     // [2][nsup_max][ldc] probability sums per super block, fixed point
     int nsup_max = 0;
     int *counts = nullptr, *offsets = nullptr, *cap = nullptr;
     int2 *tiles = nullptr;
@@ -596,21 +595,21 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     ra.gate_kind = h->cfg.gate_kind; ra.lsh = h->lsh;
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
-    // the call's totals buffers (parity rpar); the router's workgroup 0
-    // zeroes the other parity's for the next call
+    // the call's super-block totals (parity rpar); the router zeroes the
+    // other parity's for the next call
     const int par = h->rpar;
     h->rpar ^= 1;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.ldc = h->ldc; ra.blk_zh = h->blk_zh;
     ra.lse = h->lse;
     h->last_route_T = T;
-    ra.tot_cnt = h->tot_cnt2 + (size_t)par * h->E; ra.tot_p = h->tot_p2 + (size_t)par * h->E;
-    ra.clr_cnt = h->tot_cnt2 + (size_t)(par ^ 1) * h->E; ra.clr_p = h->tot_p2 + (size_t)(par ^ 1) * h->E;
     ra.nsup_max = h->nsup_max;
     ra.sup_cnt = h->sup_cnt2 + (size_t)par * h->nsup_max * h->ldc;
     ra.clr_sup = h->sup_cnt2 + (size_t)(par ^ 1) * h->nsup_max * h->ldc;
+    ra.sup_p = h->sup_p2 + (size_t)par * h->nsup_max * h->ldc;
+    ra.clr_supp = h->sup_p2 + (size_t)(par ^ 1) * h->nsup_max * h->ldc;
     ScanArgs sa{};
     sa.blk_counts = h->blk_counts; sa.ldc = h->ldc; sa.blk_zh = h->blk_zh;
-    sa.tot_cnt = ra.tot_cnt; sa.tot_p = ra.tot_p; sa.sup_cnt = ra.sup_cnt;
+    sa.sup_cnt = ra.sup_cnt; sa.sup_p = ra.sup_p;
     sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
     sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
@@ -639,10 +638,11 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         // the experts' choices give the slots, the stable ranks and the
         // per-block histogram
         HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
-                                        h->rank, h->blk_counts, h->ldc, ra.tot_cnt, ra.sup_cnt, h->rb, s));
+                                        h->rank, h->blk_counts, h->ldc, ra.sup_cnt, h->rb, s));
     }
     // the scan runs in the permute kernel (its workgroups are the route blocks)
     sa.nblk = (T + h->rb - 1) / h->rb;
+    sa.nsup = (sa.nblk + kSuper - 1) / kSuper;
     h->scan = sa;
     if (permute_mode != PERMUTE_NONE) return run_permute(h, x_dev, x_bf16, T, training, permute_mode, s);
     return MOE_OK;
@@ -914,10 +914,9 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->ldc = (int)((E + 3) / 4 * 4);
     A((void **)&h->blk_counts, sizeof(int) * (size_t)h->nblk_max * h->ldc);
     A((void **)&h->blk_zh, sizeof(double) * (size_t)h->nblk_max * 2);
-    A((void **)&h->tot_cnt2, sizeof(int) * 2 * E);
-    A((void **)&h->tot_p2, sizeof(unsigned long long) * 2 * E);
     h->nsup_max = (h->nblk_max + kSuper - 1) / kSuper;
     A((void **)&h->sup_cnt2, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc);
+    A((void **)&h->sup_p2, sizeof(unsigned long long) * 2 * (size_t)h->nsup_max * h->ldc);
     A((void **)&h->counts, sizeof(int) * E);
     A((void **)&h->offsets, sizeof(int) * (E + 1));
     A((void **)&h->cap, sizeof(int));
@@ -960,9 +959,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->s2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->b1, sizeof(float) * (size_t)h->E * h->H_pad);
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
-    Z(h->tot_cnt2, sizeof(int) * 2 * E);
-    Z(h->tot_p2, sizeof(unsigned long long) * 2 * E);
     Z(h->sup_cnt2, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc);
+    Z(h->sup_p2, sizeof(unsigned long long) * 2 * (size_t)h->nsup_max * h->ldc);
     Z(h->aux_bias, sizeof(float) * h->Er);
     Z(h->aux_mom, sizeof(float) * h->Er);
     Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);

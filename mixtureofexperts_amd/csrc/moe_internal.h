@@ -122,19 +122,17 @@ struct RouteArgs {
     int *blk_counts;       // [nblk][ldc]: entries per expert (columns < Eh)
     int ldc;               // row stride of blk_counts (Eh rounded up to 4)
     double *blk_zh;        // [nblk][2]: the route block's sums of lse^2 and of the entropy
-    // totals over the call's route blocks, by integer atomics (order-free, so
-    // deterministic): entries per expert [Eh], probability sums per router
-    // row [E] in fixed point (kPsumScale); the call's parity of two buffers,
-    // block 0 zeroes the other parity's for the next call
-    int *tot_cnt;
-    unsigned long long *tot_p;
-    int *clr_cnt;
-    unsigned long long *clr_p;
-    // expert counts per super block of kSuper route blocks [nsup][ldc]
-    // (integer atomics), this parity's and the other's (cleared: route block
-    // b takes the rows b, b + nblk, ... < nsup_max)
+    // totals per super block of kSuper route blocks, by integer atomics
+    // (order-free, so deterministic; kSuper route blocks per address instead
+    // of all of them): entries per expert sup_cnt [nsup][ldc] and probability
+    // sums per router row sup_p [nsup][ldc] in fixed point (kPsumScale).  The
+    // call's parity of two buffers, and the other parity's (cleared for the
+    // next call: route block b takes the rows b, b + nblk, ... < nsup_max).
+    // The permute's scan adds the rows.
     int *sup_cnt;
+    unsigned long long *sup_p;
     int *clr_sup;
+    unsigned long long *clr_supp;
     int nsup_max;
 };
 
@@ -145,9 +143,9 @@ struct ScanArgs {
     const int *blk_counts;  // [nblk][ldc]
     int ldc;
     const double *blk_zh;   // [nblk][2]
-    const int *tot_cnt;     // [E] entries per expert (before capacity)
-    const int *sup_cnt;     // [nsup][ldc] entries per expert of each super block
-    const unsigned long long *tot_p;  // [Np] probability sums, fixed point
+    const int *sup_cnt;     // [nsup][ldc] entries per expert of each super block (before capacity)
+    const unsigned long long *sup_p;  // [nsup][ldc] probability sums per router row, fixed point
+    int nsup;               // super blocks of the call: ceil(nblk / kSuper)
     int nblk, T, E, kt;   // E: experts of the histogram
     int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
     int training, drop, z_enabled;
@@ -319,10 +317,10 @@ hipError_t launch_router(RtArgs a, int *tb, hipStream_t s);
 // gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
 // bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
 // expert's entries in its route block), blk_counts [nblk][ldc] and the
-// totals tot_cnt [E] (atomic adds)
+// totals per super block sup_cnt [nsup][ldc] (atomic adds)
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
-                                int *sup_cnt, int rb, hipStream_t s);
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *sup_cnt,
+                                int rb, hipStream_t s);
 hipError_t launch_permute(PermuteArgs a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 // compute_loss(::SwitchTransformerLoss) on device buffers in two launches

@@ -689,20 +689,17 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             int c = 0;
             for (int wd = 0; wd < TW; ++wd) c += __popc(emask[e * kRtMaskWords + wd]);
             a.blk_counts[(long long)blk * a.ldc + e] = c;
-            if (c) {
-                atomicAdd(&a.tot_cnt[e], c);
-                atomicAdd(&a.sup_cnt[(long long)(blk / kSuper) * a.ldc + e], c);
-            }
+            if (c) atomicAdd(&a.sup_cnt[(long long)(blk / kSuper) * a.ldc + e], c);
         }
         if (out_probs && e < E) {
             // per-row probability sums (Switch loss P_e): fp64 over the route
-            // block's tokens in token order, added to the call's total in
-            // fixed point (scale 2^48, at most 2^54 per route block)
+            // block's tokens in token order, added to the super block's sum
+            // in fixed point (scale 2^48, at most 2^54 per route block)
             double ps = 0.0;
 #pragma unroll 8
             for (int i = 0; i < ntok; ++i) ps += (double)Pr[i * RW + e];
             const unsigned long long fx = __double2ull_rn(ps * kPsumScale);
-            if (fx) atomicAdd(&a.tot_p[e], fx);
+            if (fx) atomicAdd(&a.sup_p[(long long)(blk / kSuper) * a.ldc + e], fx);
         }
     }
     if (tid == 0 && out_probs) {
@@ -734,15 +731,12 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
     const int ntok = min(A.TB, A.r.T - t0);
     float *L = (float *)(rdyn + A.off_L);
     float *Pr = (float *)rdyn;  // over the staging region, free once the logits are in L
-    if (blk == 0) {
-        // the other parity's totals, last read by the previous call's permute
-        for (int e = threadIdx.x; e < A.r.Eh; e += kRtThreads) {
-            A.r.clr_cnt[e] = 0;
-            A.r.clr_p[e] = 0ull;
-        }
-    }
+    // the other parity's super-block totals, last read by the previous call's permute
     for (int s = blk; s < A.r.nsup_max; s += gridDim.x)
-        for (int e = threadIdx.x; e < A.r.ldc; e += kRtThreads) A.r.clr_sup[(long long)s * A.r.ldc + e] = 0;
+        for (int e = threadIdx.x; e < A.r.ldc; e += kRtThreads) {
+            A.r.clr_sup[(long long)s * A.r.ldc + e] = 0;
+            A.r.clr_supp[(long long)s * A.r.ldc + e] = 0ull;
+        }
     if constexpr (LG > 0) {
         rt_logits<LG == 1, PAIRED>(A, t0, rdyn, L);
     } else {
@@ -823,8 +817,8 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     A.off_L = (int)((region0 + 1023) & ~(size_t)1023);
     const size_t lds = (size_t)A.off_L + rows;
     const int nblk = (a.T + TB - 1) / TB;
-    if (lds > lds_max || a.ldc < a.Eh || !a.tot_cnt || !a.tot_p || !a.clr_cnt || !a.clr_p || !a.blk_zh ||
-        !a.sup_cnt || !a.clr_sup || a.nsup_max * kSuper < nblk)
+    if (lds > lds_max || a.ldc < a.Eh || !a.blk_zh || !a.sup_cnt || !a.sup_p || !a.clr_sup || !a.clr_supp ||
+        a.nsup_max * kSuper < nblk)
         return hipErrorInvalidValue;
     const int epl = route_epl(Er);
 #define MOE_RT(LG_, P_, EPL_) return launch_router_case<LG_, P_, EPL_>(A, nblk, lds, s)
@@ -944,7 +938,7 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
 __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
                                                                             int E, int kt, int *rank,
                                                                             int *blk_counts, int ldc,
-                                                                            int *tot_cnt, int *sup_cnt, int rb) {
+                                                                            int *sup_cnt, int rb) {
     const int e = threadIdx.x;
     if (e >= E) return;
     const int t0 = blockIdx.x * rb;
@@ -958,22 +952,19 @@ __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(con
         }
     }
     blk_counts[(long long)blockIdx.x * ldc + e] = c;
-    if (c) {
-        atomicAdd(&tot_cnt[e], c);
-        atomicAdd(&sup_cnt[(long long)(blockIdx.x / kSuper) * ldc + e], c);
-    }
+    if (c) atomicAdd(&sup_cnt[(long long)(blockIdx.x / kSuper) * ldc + e], c);
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *tot_cnt,
-                                int *sup_cnt, int rb, hipStream_t s) {
+                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *sup_cnt,
+                                int rb, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255 || ldc < E) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
                        min(C, E), idx, gates);
     hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + rb - 1) / rb), dim3(MOE_MAX_EXPERTS), 0, s, sel, T, E,
-                       kt, rank, blk_counts, ldc, tot_cnt, sup_cnt, rb);
+                       kt, rank, blk_counts, ldc, sup_cnt, rb);
     return hipGetLastError();
 }
 
@@ -1015,6 +1006,8 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
 struct ScanLds {
     int cnt[MOE_MAX_EXPERTS];
     int base[MOE_MAX_EXPERTS];
+    int tot[MOE_MAX_EXPERTS];                  // the call's entries per expert (before capacity)
+    unsigned long long ptot[MOE_MAX_EXPERTS];  // the call's probability sums (fixed point), workgroup 0
     int off[MOE_MAX_EXPERTS + 1];
     int tstart[MOE_MAX_EXPERTS + 1];
     float fp[MOE_MAX_EXPERTS];
@@ -1036,28 +1029,48 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
         }
         L.cap = cap;
     }
-    for (int e = tid; e < a.E; e += nth) L.base[e] = 0;
+    for (int e = tid; e < a.E; e += nth) {
+        L.base[e] = 0;
+        L.tot[e] = 0;
+        L.ptot[e] = 0ull;
+    }
     __syncthreads();
     {
         // rank bases: the super blocks before blk's, then the route blocks
-        // of its own super block before it (at most 2 kSuper - 1 rows);
-        // thread (g, j) adds row j's experts 4 g .. 4 g + 3
+        // of its own super block before it (at most 2 kSuper - 1 rows); the
+        // totals: every super block's row (workgroup 0 also the probability
+        // sums).  Thread (g, j) adds row j's experts 4 g .. 4 g + 3, all
+        // rows' loads in flight at once (integer LDS atomics: any order)
         const int ng = (a.E + 3) / 4;
         const int ns = blk / kSuper, nrow = ns + (blk - ns * kSuper);
-        for (int q = tid; q < ng * nrow; q += nth) {
+        const int nq = ng * (nrow + a.nsup * (writer ? 2 : 1));
+        for (int q = tid; q < nq; q += nth) {
             const int g = q % ng, j = q / ng;
-            const int *src = (j < ns) ? a.sup_cnt + (long long)j * a.ldc
-                                      : a.blk_counts + (long long)(ns * kSuper + j - ns) * a.ldc;
-            const int4 v = *(const int4 *)(src + 4 * g);
-            const int s[4] = {v.x, v.y, v.z, v.w};
+            if (j < nrow + a.nsup) {
+                const bool bj = j < nrow;
+                const int *src = !bj ? a.sup_cnt + (long long)(j - nrow) * a.ldc
+                                     : (j < ns) ? a.sup_cnt + (long long)j * a.ldc
+                                                : a.blk_counts + (long long)(ns * kSuper + j - ns) * a.ldc;
+                const int4 v = *(const int4 *)(src + 4 * g);
+                const int s[4] = {v.x, v.y, v.z, v.w};
+                int *dst = bj ? L.base : L.tot;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (4 * g + i < a.E && s[i]) atomicAdd(&L.base[4 * g + i], s[i]);
+                for (int i = 0; i < 4; ++i)
+                    if (4 * g + i < a.E && s[i]) atomicAdd(&dst[4 * g + i], s[i]);
+            } else {
+                const unsigned long long *src = a.sup_p + (long long)(j - nrow - a.nsup) * a.ldc + 4 * g;
+                const ulonglong2 v0 = *(const ulonglong2 *)src, v1 = *(const ulonglong2 *)(src + 2);
+                const unsigned long long s[4] = {v0.x, v0.y, v1.x, v1.y};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (4 * g + i < a.Np && s[i]) atomicAdd(&L.ptot[4 * g + i], s[i]);
+            }
         }
     }
     const float total = (float)((long long)a.T * a.kl);
+    __syncthreads();
     for (int e = tid; e < a.E; e += nth) {
-        const int ce = min(a.tot_cnt[e], L.cap);
+        const int ce = min(L.tot[e], L.cap);
         L.cnt[e] = ce;
         // the terms f_e * P_e of the Switch loss (src/balancing/losses.jl:15-36)
         // over the a.Np probability rows; with shared experts of the layer the
@@ -1065,7 +1078,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
         if (writer && e < a.Np) {
             float f = (e < a.lsh) ? 0.0f : (float)ce;
             if (a.T * a.kl > 0) f = f / total;
-            const float P = (float)((double)a.tot_p[e] / kPsumScale) / (float)a.T;
+            const float P = (float)((double)L.ptot[e] / kPsumScale) / (float)a.T;
             L.fp[e] = f * P;
         }
     }
