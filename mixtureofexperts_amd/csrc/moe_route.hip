@@ -1224,7 +1224,24 @@ __device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int row, i
 // renormalisation, position), then the wave copies the token's row into
 // every position it owns, converting to the GEMM type.
 // ============================================================================
-__device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int lane, const ScanLds &L) {
+// bf16 rows into the bf16 tile image: UB 16-byte chunks per lane per batch
+// (UB * 512 columns, the smallest power of two covering D up to 4096, so that
+// few lanes rewrite the row's last chunk), loaded together from clamped
+// in-row addresses, then stored to every position the token holds.
+__device__ __forceinline__ bool permute_bf16_rows(const PermuteArgs &a) {
+    return a.copy_rows && a.ct == CT_BF16 && a.x_bf16 && (a.D & 7) == 0;
+}
+template <int UB>
+__device__ __forceinline__ void load_row_chunk(const PermuteArgs &a, int t, int d0, int lane, u32x4_t (&v)[UB]) {
+    const uint16_t *__restrict__ src = (const uint16_t *)a.x + (long long)t * a.D;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) v[u] = *(const u32x4_t *)(src + min(d0 + u * 512 + lane * 8, a.D - 8));
+}
+
+// pre: the row's first batch, already loaded by the caller when have_pre
+template <int UB>
+__device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int lane, const ScanLds &L,
+                                              const u32x4_t (&pre)[UB], bool have_pre) {
 #pragma clang fp contract(off)
     const int cap = L.cap;
     int e = 0, pos = -1, row = -1;  // position in expert order; xp row (tile image row when tiled)
@@ -1263,17 +1280,16 @@ __device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int l
         }
     }
     if (!a.copy_rows) return;
-    if (a.ct == CT_BF16 && a.x_bf16 && (a.D & 7) == 0) {
-        // 8 bf16 per lane per chunk; the loads of 8 chunks (8 KB per wave) are
-        // issued together from clamped in-row addresses, then stored to every
-        // position the token holds.
-        const uint16_t *__restrict__ src = (const uint16_t *)a.x + (long long)t * a.D;
-        constexpr int U = 8;
-        for (int d0 = 0; d0 < a.D; d0 += 512 * U) {
-            u32x4_t v[U];
+    if (permute_bf16_rows(a)) {
+        for (int d0 = 0; d0 < a.D; d0 += 512 * UB) {
+            u32x4_t v[UB];
+            if (d0 == 0 && have_pre) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) v[u] = *(const u32x4_t *)(src + min(d0 + u * 512 + lane * 8, a.D - 8));
-            store_row_chunk<U>(a, row, d0, lane, v);
+                for (int u = 0; u < UB; ++u) v[u] = pre[u];
+            } else {
+                load_row_chunk<UB>(a, t, d0, lane, v);
+            }
+            store_row_chunk<UB>(a, row, d0, lane, v);
         }
         return;
     }
@@ -1326,13 +1342,21 @@ __device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int l
 }
 
 // Workgroup w takes the tpw tokens [w tpw, w tpw + tpw) of one route block,
-// a wave per token in turn, after that route block's scan.
+// a wave per token in turn, after that route block's scan.  Each wave loads
+// the first batch of its first token's row before the scan (the loads do not
+// depend on it), so their latency overlaps the scan's; up to 4 chunks per
+// lane (8 would hold 32 registers through the scan and spill).
+template <int UB>
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
     __shared__ ScanLds L;
-    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
+    const int lane = threadIdx.x & 63;
     const int t1 = min(a.T, (int)(blockIdx.x + 1) * a.tpw);
-    for (int t = blockIdx.x * a.tpw + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
-        permute_token(a, t, threadIdx.x & 63, L);
+    const int tf = blockIdx.x * a.tpw + (threadIdx.x >> 6);
+    u32x4_t pre[UB];
+    const bool have_pre = UB <= 4 && permute_bf16_rows(a) && tf < t1;
+    if (have_pre) load_row_chunk<UB>(a, tf, 0, lane, pre);
+    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
+    for (int t = tf; t < t1; t += kPermThreads / 64) permute_token<UB>(a, t, lane, L, pre, have_pre && t == tf);
 }
 
 // Permute for more slots per token than a wave has lanes (ExpertChoiceGating
@@ -1423,7 +1447,10 @@ hipError_t launch_permute(PermuteArgs a, hipStream_t s) {
     while (a.tpw * 2 <= a.rb && a.tpw < 4 * kPermTokens && (a.T + a.tpw - 1) / a.tpw > 512) a.tpw *= 2;
     const int nwg = (a.T + a.tpw - 1) / a.tpw;
     if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3(nwg), dim3(kPermThreads), 0, s, a);
-    else hipLaunchKernelGGL(permute_kernel, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D >= 4096) hipLaunchKernelGGL(permute_kernel<8>, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D >= 2048) hipLaunchKernelGGL(permute_kernel<4>, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D >= 1024) hipLaunchKernelGGL(permute_kernel<2>, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else hipLaunchKernelGGL(permute_kernel<1>, dim3(nwg), dim3(kPermThreads), 0, s, a);
     return hipGetLastError();
 }
 
