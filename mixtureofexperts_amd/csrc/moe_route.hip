@@ -757,7 +757,9 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
 }
 
 // experts per lane of a token's 8 (the gating's register blocks)
-static int route_epl(int E) { return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : 16))); }
+static int route_epl(int E) {
+    return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : (E <= 80 ? 10 : (E <= 96 ? 12 : 16)))));
+}
 
 template <int LG, int PAIRED, int EPL>
 static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipStream_t s) {
@@ -827,6 +829,8 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     case 2: MOE_RT(LG_, 0, 2);          \
     case 4: MOE_RT(LG_, 0, 4);          \
     case 8: MOE_RT(LG_, 0, 8);          \
+    case 10: MOE_RT(LG_, 0, 10);        \
+    case 12: MOE_RT(LG_, 0, 12);        \
     default: MOE_RT(LG_, 0, 16);        \
     }
     if (!gemm) {
