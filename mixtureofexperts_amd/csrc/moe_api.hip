@@ -99,6 +99,7 @@ struct moe_handle {
     int2 *tiles = nullptr;
     int *num_tiles = nullptr;
     int *tile_start = nullptr;
+    int *item_start = nullptr;  // [E+1] the up GEMM's paired work items (up_pairs)
     float *scalars = nullptr;
     int *perm = nullptr, *pos_of = nullptr;
     void *xp = nullptr, *hbuf = nullptr;
@@ -559,6 +560,14 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
 // (compute_logits) with an AuxiliaryFreeLoss gates on logits + its bias
 // (src/core/moe_layer.jl:137-140) in a second route pass and, when training,
 // counts one compute_loss call for the bias update (auxiliary_free.jl:36-40).
+// n-tiles of the up GEMM
+static int up_ntiles(const moe_handle *h) {
+    return h->bf16_gemm ? h->H_pad / (h->gated ? 128 : 256) : h->H_pad / kGemmBN;
+}
+// The bf16 up GEMM on 256-row tiles with an even n-tile count pairs an
+// expert's last M tile of at most 128 rows with two n-tiles (item_start).
+static bool up_pairs(const moe_handle *h) { return h->bf16_gemm && h->bm == 256 && up_ntiles(h) % 2 == 0; }
+
 static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
                        int permute_mode, float *loss_dev, hipStream_t s) {
     const bool aux = compute_logits && h->aux_free && !h->given;
@@ -615,6 +624,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
     sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets;
+    sa.item_start = up_pairs(h) ? h->item_start : nullptr; sa.pair_nt = up_ntiles(h);
     sa.cap_out = h->cap; sa.tiles = h->tiles; sa.num_tiles = h->num_tiles; sa.scalars = h->scalars;
     sa.loss_out = loss_dev;
     sa.aux_free = aux; sa.aux_use_comp = h->aux_use_comp; sa.aux_update = aux_update;
@@ -666,9 +676,10 @@ static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
     g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E; g.ksplit = 1; g.ncu = h->ncu;
+    g.item_start = up_pairs(h) ? h->item_start : nullptr;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
     // bf16 kernel: 128 h columns (gated, W1 and W3 rows) or 256 rows per tile
-    g.n_tiles = h->bf16_gemm ? h->H_pad / (h->gated ? 128 : 256) : h->H_pad / kGemmBN;
+    g.n_tiles = up_ntiles(h);
     return g;
 }
 
@@ -923,6 +934,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->tiles, sizeof(int2) * (size_t)h->max_tiles);
     A((void **)&h->num_tiles, sizeof(int));
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
+    A((void **)&h->item_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
     A((void **)&h->aux_bias, sizeof(float) * h->Er);
@@ -1486,6 +1498,14 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     for (int i = 0; i < nt; ++i) tl[i] = make_int2(expert, i * h->bm);
     std::vector<int> ts(h->E + 1, 0);
     for (int e = 0; e <= h->E; ++e) ts[e] = e > expert ? nt : 0;
+    // the up GEMM's work items (the device scan's rule): a last M tile of at
+    // most bm/2 rows covers two n-tiles in one item
+    std::vector<int> is(h->E + 1, 0);
+    if (up_pairs(h)) {
+        const int pnt = up_ntiles(h), f = n / h->bm, rr = n % h->bm;
+        const int items = (rr > 0 && 2 * rr <= h->bm) ? pnt * f + pnt / 2 : pnt * nt;
+        for (int e = 0; e <= h->E; ++e) is[e] = e > expert ? items : 0;
+    }
     void *xs = nullptr;
     HIP_TRY(h, hipMalloc(&xs, sizeof(float) * (size_t)n * h->D));
     hipError_t e = hipMemcpyAsync(xs, x, sizeof(float) * (size_t)n * h->D, hipMemcpyHostToDevice, s);
@@ -1495,6 +1515,8 @@ int moe_expert_forward(moe_handle *h, int32_t expert, const float *x, int32_t n,
     if (e == hipSuccess) e = hipMemcpyAsync(h->num_tiles, &nt, sizeof(int), hipMemcpyHostToDevice, s);
     if (e == hipSuccess)
         e = hipMemcpyAsync(h->tile_start, ts.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && up_pairs(h))
+        e = hipMemcpyAsync(h->item_start, is.data(), sizeof(int) * (h->E + 1), hipMemcpyHostToDevice, s);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(convert_rows_kernel, dim3(1024), dim3(256), 0, s, (const void *)xs, 0, n, h->D, h->ct,
                            h->xp, h->D_pad, h->bf16_gemm ? h->bm : 0);

@@ -126,6 +126,7 @@ struct TileJob {
     int n0;            // first B row of the tile (first h column in the gated mode)
     int split_j;       // split tiles: index among them (partials in split_ws)
     int mt;            // M tile (tile image block of the A operand and of h)
+    int pair;          // up GEMM: the expert's last M tile (at most BM / 2 rows) for n-tiles nt and nt + 1
     long long arow0;   // first A row (expert-ordered row of the tile's first row)
 };
 
@@ -133,8 +134,59 @@ struct TileJob {
 // ones (tail_split).  Each class is dealt to the 8 XCDs in contiguous ranges
 // (block L runs on XCD L mod 8): slots 0 .. pf-1 of an XCD take its whole
 // tiles, the next ps slots its split items, which are dispatched last.
+// With g.item_start (the up GEMM, NT even, 256-row tiles) an expert whose
+// last M tile holds r <= BM / 2 rows has, per pair of n-tiles (2 j, 2 j + 1),
+// the f full M tiles of n-tile 2 j, those of n-tile 2 j + 1, then one paired
+// item: its last M tile against both n-tiles (the other experts as above).
+// A paired item runs the MFMAs of a full tile, so every workgroup of a round
+// takes about as long as the others and the workgroups that share weight
+// tiles stay in step; item_start[e] = the items before expert e.
+template <int BM, int NB>
+__device__ __forceinline__ bool decode_job_pairs(const GemmArgs &g, TileJob &jb) {
+    const int NT = g.n_tiles;
+    const int W = g.item_start[g.E];
+    const int pf = (W + 7) >> 3;
+    const int L = blockIdx.x, x = L & 7, slot = L >> 3;
+    const int item = x * pf + slot;
+    if (slot >= pf || item >= W) return false;
+    int lo = 0, hi = g.E - 1;  // largest e with item_start[e] <= item (a non-empty expert)
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (g.item_start[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int c = g.counts[e];
+    const int f = c / BM, r = c - f * BM;
+    const int local = item - g.item_start[e];
+    int nt, m, pair = 0;
+    if (r > 0 && r <= BM / 2) {
+        const int gs = 2 * f + 1;
+        const int j = local / gs, q = local - j * gs;
+        if (q < f) { nt = 2 * j; m = q; }
+        else if (q < 2 * f) { nt = 2 * j + 1; m = q - f; }
+        else { nt = 2 * j; m = f; pair = 1; }
+    } else {
+        const int nte = f + (r > 0 ? 1 : 0);
+        nt = local / nte;
+        m = local - nt * nte;
+    }
+    const int m0 = m * BM;
+    jb.e = e;
+    jb.ks = 0;
+    jb.nks = 1;
+    jb.KT = g.K / 32;
+    jb.rows = min(BM, c - m0);
+    jb.arow0 = (long long)g.offsets[e] + m0;
+    jb.n0 = nt * (NB == 2 ? 128 : 256);
+    jb.split_j = 0;
+    jb.mt = g.tile_start[e] + m;
+    jb.pair = pair;
+    return true;
+}
+
 template <int BM, int NB>
 __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
+    if (g.item_start) return decode_job_pairs<BM, NB>(g, jb);
     const int NT = g.n_tiles;
     const int W = g.tile_start[g.E] * NT;
     const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
@@ -173,6 +225,7 @@ __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
     jb.n0 = nt * (NB == 2 ? 128 : 256);
     jb.split_j = tile - ts.nfull;
     jb.mt = t0 + m0 / BM;
+    jb.pair = 0;
     return true;
 }
 
@@ -194,19 +247,25 @@ __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
 // 32 (fp8) (gated: tile rows [0, 128) are W1 rows n0.., [128, 256) the same
 // W3 rows).  An expert's last M tile also holds rows past its valid ones;
 // their products land in rows that are never stored.
-template <int BM, int NB, int NWAVE, int LA, int LB, int WF8>
+// PAIR (a paired item): the first BM / 2 A rows of each image block, and 512
+// B-tile rows: those of n-tile nt (rows 0 .. 255 as above), then those of
+// n-tile nt + 1.
+template <int BM, int NB, int NWAVE, int LA, int LB, int WF8, bool PAIR>
 __device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, int w, int lane,
                                           const uint8_t *(&gsrc)[LA + LB], uint32_t (&ldst)[LA + LB]) {
     constexpr int ROWB = 64;
     constexpr int BROWB = WF8 ? 32 : 64;  // B bytes per row per stage
-    constexpr int A_BYTES = BM * ROWB;
+    constexpr int BMA = PAIR ? BM / 2 : BM;  // A rows staged
+    constexpr int A_IMG = BM * ROWB;         // image block of an M tile and K stage
+    constexpr int A_LDS = BMA * ROWB;
+    constexpr int BRW = PAIR ? 512 : 256;    // B-tile rows
     constexpr int RB = (NB == 2) ? 128 : 256;
     const long long KTT = g.K / 32;
     const long long s0 = (long long)jb.ks * jb.KT;  // first stage of the K range
-    const uint8_t *Ab = (const uint8_t *)g.A + ((long long)jb.mt * KTT + s0) * A_BYTES + lane * 16;
+    const uint8_t *Ab = (const uint8_t *)g.A + ((long long)jb.mt * KTT + s0) * A_IMG + lane * 16;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int r = w * (BM / NWAVE) + 16 * i;
+        const int r = w * (BMA / NWAVE) + 16 * i;
         gsrc[i] = Ab + (long long)r * ROWB;
         ldst[i] = r * ROWB;
     }
@@ -214,12 +273,13 @@ __device__ __forceinline__ void load_plan(const GemmArgs &g, const TileJob &jb, 
     const long long esz = WF8 ? 1 : 2;
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
-        const int t = w * (256 / NWAVE) + BR * i;  // first tile row of the load
-        const int r = (NB == 2) ? (t & 127) : t;   // row within the n block
-        const uint8_t *Bsrc = (NB == 2 && t >= 128) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
+        const int t = w * (BRW / NWAVE) + BR * i;  // first tile row of the load
+        const int hf = t >> 8, tt = t & 255;       // n-tile of the pair; row in its 256-row tile
+        const int r = (NB == 2) ? (tt & 127) : tt; // row within the n block
+        const uint8_t *Bsrc = (NB == 2 && tt >= 128) ? (const uint8_t *)g.B1 : (const uint8_t *)g.B0;
         gsrc[LA + i] = Bsrc + (long long)jb.e * g.b_stride * esz +
-                       ((long long)(jb.n0 / RB) * KTT + s0) * RB * BROWB + (long long)r * BROWB + lane * 16;
-        ldst[LA + i] = A_BYTES + t * BROWB;
+                       ((long long)(jb.n0 / RB + hf) * KTT + s0) * RB * BROWB + (long long)r * BROWB + lane * 16;
+        ldst[LA + i] = A_LDS + t * BROWB;
     }
 }
 
@@ -468,23 +528,46 @@ __device__ __forceinline__ void store_staged(const GemmArgs &g, const TileJob &j
     }
 }
 
-// LDS ring: one array per slot (slot index known at compile time everywhere).
-#define MOE_LDS_RING(STAGE, NS)                                                            \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot0[STAGE];                        \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot1[STAGE];                        \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot2[NS > 2 ? STAGE : 16];          \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot3[NS > 3 ? STAGE : 16];          \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot4[NS > 4 ? STAGE : 16];          \
-    __shared__ __attribute__((aligned(1024))) uint8_t slot5[NS > 5 ? STAGE : 16];          \
-    auto slot = [&](auto J_) -> MOE_LDS_AS uint8_t * {                                     \
-        constexpr int J = decltype(J_)::value;                                             \
-        if constexpr (J == 0) return (MOE_LDS_AS uint8_t *)slot0;                          \
-        else if constexpr (J == 1) return (MOE_LDS_AS uint8_t *)slot1;                     \
-        else if constexpr (J == 2) return (MOE_LDS_AS uint8_t *)slot2;                     \
-        else if constexpr (J == 3) return (MOE_LDS_AS uint8_t *)slot3;                     \
-        else if constexpr (J == 4) return (MOE_LDS_AS uint8_t *)slot4;                     \
-        else return (MOE_LDS_AS uint8_t *)slot5;                                           \
+// A paired item's staged tile (up GEMMs): staging rows hf BM / 2 + r hold row
+// r of n-tile nt + hf; each n-tile's rows go to the first BM / 2 rows of its
+// h image blocks (units as in store_staged, per n-tile).
+template <int MODE, int BM, int CH, typename RowAddr>
+__device__ __forceinline__ void store_staged_pair(const GemmArgs &g, const TileJob &jb, RowAddr row_addr) {
+    constexpr int U = 8;
+    constexpr int BMA = BM / 2;
+    constexpr int NUH = BMA * CH;                               // 16-byte units per n-tile
+    constexpr int NTW = (MODE == MODE_GATED_UP) ? 128 : 256;    // h columns per n-tile
+    const long long KTT = g.ldc / 32;
+#pragma unroll
+    for (int u0 = 0; u0 < 2 * NUH; u0 += 256 * U) {
+        u32x4_t v[U];
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const int u = u0 + q * 256 + (int)threadIdx.x;
+            const int hf = u / NUH, up = u - hf * NUH;
+            const int r = (up >> 2) % BMA;
+            const int ch = (up / (4 * BMA)) * 4 + ((up & 3) ^ ((r >> 2) & 3));
+            v[q] = *(const MOE_LDS_AS u32x4_t *)(row_addr(hf * BMA + r) + ((ch ^ (r & (CH - 1))) << 4));
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const int u = u0 + q * 256 + (int)threadIdx.x;
+            const int hf = u / NUH, up = u - hf * NUH;
+            uint8_t *base = (uint8_t *)g.C + ((long long)jb.mt * KTT + (jb.n0 + hf * NTW) / 32) * BM * 64;
+            *(u32x4_t *)(base + (long long)(up / (4 * BMA)) * BM * 64 + (up % (4 * BMA)) * 16) = v[q];
+        }
     }
+}
+
+// A sink that moves rows by a fixed offset (the paired item's second n-tile).
+template <typename Put>
+struct RowOffsetPut {
+    Put put;
+    int off;
+    __device__ __forceinline__ void operator()(int ml, int lc, float v0, float v1, float v2, float v3) const {
+        put(ml + off, lc, v0, v1, v2, v3);
+    }
+};
 
 // Prologue: this wave's NL loads of stages 0 .. NS-2 (clamped to the last
 // stage), stage s into slot s.
@@ -528,30 +611,48 @@ __device__ __forceinline__ void store_staged(const GemmArgs &g, const TileJob &j
 // OCC: workgroups per CU.  128-row tiles (small experts, weight-bandwidth
 // bound, or short K) run two per CU on a shorter ring, so one workgroup's
 // prologue and epilogue overlap the other's main loop.
-template <int MODE, int BM, int ACT, int WF8, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void grouped_gemm_bf16_kernel(
-    GemmArgs g) {
+//
+// The LDS ring: one array of RING bytes; slot J of a stage size STAGE at J
+// STAGE.  The staged epilogue reuses it as rows of CW bytes.
+template <int BM, int WF8, int OCC>
+struct RingShape {
+    static constexpr int STAGE = BM * 64 + 256 * (WF8 ? 32 : 64);
+    static constexpr int NS = (OCC == 2) ? (WF8 ? 4 : 3) : ((BM == 256 && !WF8) ? 4 : 6);
+    static constexpr int BYTES = NS * STAGE;
+};
+
+// One work item.  PAIR: a paired item (decode_job_pairs): 4 waves as 2 (n-tile
+// of the pair) x 2 (N), each over the item's BM / 2 rows; otherwise 2 (M) x 2
+// (N) over the BM rows of one n-tile.
+template <int MODE, int BM, int ACT, int WF8, int OCC, bool PAIR>
+__device__ __forceinline__ void tile_body(const GemmArgs &g, const TileJob &jb, uint8_t *ring_) {
     constexpr int NWAVE = 4;
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
     constexpr int ROWB = 64;             // bytes per LDS A row = 32 bf16 of K (one stage)
     constexpr int BROWB = WF8 ? 32 : 64; // bytes per LDS B row
-    constexpr int A_BYTES = BM * ROWB;
-    constexpr int STAGE = A_BYTES + 256 * BROWB;
+    constexpr int BMA = PAIR ? BM / 2 : BM;  // A rows staged per stage
+    constexpr int BRW = PAIR ? 512 : 256;    // B-tile rows per stage
+    constexpr int A_BYTES = BMA * ROWB;      // A bytes of a stage in LDS
+    constexpr int A_IMG = BM * ROWB;         // A image block stride (one K stage of an M tile)
+    constexpr int STAGE = A_BYTES + BRW * BROWB;
+    constexpr int RING = RingShape<BM, WF8, OCC>::BYTES;
     // LDS ring slots (<= 144 KB per CU)
-    constexpr int NS = (OCC == 2) ? (WF8 ? 4 : 3) : ((BM == 256 && !WF8) ? 4 : 6);
-    constexpr int WM = BM / 2;           // wave tile rows (2 waves along M)
+    constexpr int NS = PAIR ? RING / STAGE : RingShape<BM, WF8, OCC>::NS;
+    static_assert(NS >= 3 && NS <= 6, "ring depth");
+    constexpr int WM = BM / 2;           // wave tile rows (2 waves along M; PAIR: the item's BM / 2 rows)
     constexpr int WN = 128;              // wave tile columns (2 waves along N)
     constexpr int IM = WM / 32;          // 32-row blocks per wave
     constexpr int JN = WN / 32;          // 32-column blocks per wave
-    constexpr int LA = BM / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
-    constexpr int LB = 256 / ((WF8 ? 32 : 16) * NWAVE);  // B loads per wave per stage
+    constexpr int LA = BMA / (16 * NWAVE);  // A loads (16 rows each) per wave per stage
+    constexpr int LB = BRW / ((WF8 ? 32 : 16) * NWAVE);  // B loads per wave per stage
     constexpr int NL = LA + LB;          // 16-byte loads per lane per stage
     constexpr int NL0 = NL / 2;          // of which issued in a stage's first sub-step
-    static_assert(NS * STAGE * OCC <= 160 * 1024, "LDS");
-    MOE_LDS_RING(STAGE, NS);
+    static_assert(NS * STAGE <= RING && RING * OCC <= 160 * 1024, "LDS");
+    auto slot = [&](auto J_) -> MOE_LDS_AS uint8_t * {
+        constexpr int J = decltype(J_)::value;
+        return (MOE_LDS_AS uint8_t *)ring_ + (J < NS ? J : 0) * STAGE;
+    };
 
-    TileJob jb;
-    if (!decode_job<BM, NB>(g, jb)) return;
     const int KT = jb.KT;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -559,11 +660,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 
     const uint8_t *gsrc[NL];
     uint32_t ldst[NL];
-    load_plan<BM, NB, NWAVE, LA, LB, WF8>(g, jb, w, lane, gsrc, ldst);
+    load_plan<BM, NB, NWAVE, LA, LB, WF8, PAIR>(g, jb, w, lane, gsrc, ldst);
     // load i of stage kt into ring slot J
     auto dma = [&](auto J_, int kt, int i) {
         const uint32_t l = (uint32_t)(uintptr_t)(slot(J_) + ldst[i]);
-        lds_dma16(gsrc[i] + (long long)kt * (i < LA ? A_BYTES : (NB == 2 ? 128 : 256) * BROWB),
+        lds_dma16(gsrc[i] + (long long)kt * (i < LA ? A_IMG : (NB == 2 ? 128 : 256) * BROWB),
                   __builtin_amdgcn_readfirstlane(l));
     };
 
@@ -576,11 +677,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     // assignment of K values to (sub-step, lane half) shared by A and B works.
     const int half = lane >> 5;
     const int r32 = lane & 31;
-    const int a_frag = (wm * WM + r32) * ROWB;
+    const int a_frag = ((PAIR ? 0 : wm * WM) + r32) * ROWB;
     int b_frag[JN];
 #pragma unroll
     for (int j = 0; j < JN; ++j)
-        b_frag[j] = A_BYTES + (b_frag_row<NB, WN>(j, wn) + r32) * BROWB + (WF8 ? ((half ^ ((r32 >> 3) & 1)) << 4) : 0);
+        b_frag[j] = A_BYTES + ((PAIR ? wm * 256 : 0) + b_frag_row<NB, WN>(j, wn) + r32) * BROWB +
+                    (WF8 ? ((half ^ ((r32 >> 3) & 1)) << 4) : 0);
     int choff[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -683,7 +785,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         };
         MOE_STAGE_LOOP(NS, KT)
     };
-    const int nv = min(IM, (max(0, jb.rows - wm * WM) + 31) >> 5);  // wave-uniform
+    const int nv = min(IM, (max(0, jb.rows - (PAIR ? 0 : wm * WM)) + 31) >> 5);  // wave-uniform
     if (nv == IM) run(ic<IM>{});
     else if (nv == 0) run(ic<0>{});
     else if (nv == 1) run(ic<1>{});
@@ -693,33 +795,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     }
     wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
-    // bf16 outputs are staged in the (now idle) LDS ring, STAGE / CW rows per
-    // slot: h as its tile image; y rows when y is bf16, the tile not split and
-    // N, ldc multiples of 8 (whole 16-byte chunks).
+    // bf16 outputs are staged in the (now idle) LDS ring, rows of CW bytes:
+    // h as its tile image; y rows when y is bf16, the tile not split and N,
+    // ldc multiples of 8 (whole 16-byte chunks).  A paired item stages the
+    // rows of its n-tile nt + wm at rows wm BM / 2 ..
     constexpr int CW = (MODE == MODE_GATED_UP ? 128 : 256) * 2;  // output bytes per tile row
     constexpr int CH = CW / 16;
-    constexpr int RPS = STAGE / CW;
-    static_assert(RPS * NS >= BM, "LDS staging of the output tile");
+    static_assert(BM * CW <= RING, "LDS staging of the output tile");
     const bool staged = (MODE != MODE_DOWN) || (g.c_bf16 && jb.nks == 1 && ((g.N | g.ldc) & 7) == 0);
     if (staged) {
-        auto row_addr = [&](int r) -> MOE_LDS_AS uint8_t * {
-            const int q = r / RPS;
-            MOE_LDS_AS uint8_t *p = slot(ic<0>{});
-            p = (q == 1) ? slot(ic<1>{}) : p;
-            if constexpr (NS > 2) p = (q == 2) ? slot(ic<2 % NS>{}) : p;
-            if constexpr (NS > 3) p = (q == 3) ? slot(ic<3 % NS>{}) : p;
-            if constexpr (NS > 4) p = (q == 4) ? slot(ic<4 % NS>{}) : p;
-            if constexpr (NS > 5) p = (q == 5) ? slot(ic<5 % NS>{}) : p;
-            return p + (r - q * RPS) * CW;
-        };
+        auto row_addr = [&](int r) -> MOE_LDS_AS uint8_t * { return (MOE_LDS_AS uint8_t *)ring_ + r * CW; };
         __syncthreads();  // every wave's ring reads and loads are done
-        store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane,
-                                               StagePut<CH, decltype(row_addr)>{row_addr});
-        __syncthreads();
-        store_staged<MODE, BM, CH>(g, jb, row_addr);
+        if constexpr (PAIR) {
+            TileJob jw = jb;
+            jw.n0 = jb.n0 + wm * (NB == 2 ? 128 : 256);
+            using SP = StagePut<CH, decltype(row_addr)>;
+            store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jw, acc, 0, wn, lane,
+                                                   RowOffsetPut<SP>{SP{row_addr}, wm * BMA});
+            __syncthreads();
+            store_staged_pair<MODE, BM, CH>(g, jb, row_addr);
+        } else {
+            store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane,
+                                                   StagePut<CH, decltype(row_addr)>{row_addr});
+            __syncthreads();
+            store_staged<MODE, BM, CH>(g, jb, row_addr);
+        }
     } else if constexpr (MODE == MODE_DOWN) {
         store_tile<MODE, ACT, IM, JN, WN, WF8>(g, jb, acc, wm * WM, wn, lane, DirectPut{g, jb});
     }
+}
+
+template <int MODE, int BM, int ACT, int WF8, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void grouped_gemm_bf16_kernel(
+    GemmArgs g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[RingShape<BM, WF8, OCC>::BYTES];
+    TileJob jb;
+    if (!decode_job<BM, (MODE == MODE_GATED_UP) ? 2 : 1>(g, jb)) return;
+    if constexpr (MODE != MODE_DOWN && BM == 256) {
+        if (jb.pair) {
+            tile_body<MODE, BM, ACT, WF8, OCC, true>(g, jb, ring);
+            return;
+        }
+    }
+    tile_body<MODE, BM, ACT, WF8, OCC, false>(g, jb, ring);
 }
 
 // ============================================================================

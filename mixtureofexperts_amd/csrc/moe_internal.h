@@ -152,6 +152,8 @@ struct ScanArgs {
     float capacity_factor, alpha, beta;
     int bm;                // GEMM tile rows
     int *tile_start;       // [E+1] first M tile of each expert (sum of ceil(count / bm))
+    int *item_start;       // [E+1] or null: the up GEMM's paired work items before each expert (pair_nt n-tiles)
+    int pair_nt;
     int *counts;           // [E]   (after capacity)
     int *offsets;          // [E+1]
     int *cap_out;          // [1] capacity (INT_MAX when unused)
@@ -262,6 +264,7 @@ struct GemmArgs {
                                          // tile image (ldc = its K)
     const int2 *tiles; const int *num_tiles; const int *counts; const int *offsets;
     const int *tile_start;               // [E+1] (bf16 kernel work list)
+    const int *item_start;               // [E+1] or null: the up GEMM's paired items (256-row tiles, n_tiles even)
     int E;
     int m_tiles_grid; int n_tiles;
     int ksplit;                          // bf16 kernel: the most K ranges a tail tile may be split into (tail_split)

@@ -1182,6 +1182,28 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
         a.offsets[e] = L.off[e];
         a.tile_start[e] = L.tstart[e];
     }
+    if (a.item_start && tid < 64) {
+        // the up GEMM's work items per expert: pair_nt n-tiles times its M
+        // tiles, except that a last M tile of at most bm / 2 rows serves two
+        // n-tiles in one item (pair_nt even); exclusive prefix by wave 0
+        auto items = [&](int e) {
+            if (e >= a.E) return 0;
+            const int c = L.cnt[e], f = c / a.bm, r = c - f * a.bm;
+            return (r > 0 && 2 * r <= a.bm) ? a.pair_nt * f + a.pair_nt / 2 : a.pair_nt * (f + (r > 0 ? 1 : 0));
+        };
+        const int e0 = 2 * tid, e1 = e0 + 1;
+        const int n0 = items(e0), n1 = items(e1);
+        int ns = n0 + n1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int nu = __shfl_up(ns, o);
+            if (tid >= o) ns += nu;
+        }
+        const int ne = ns - (n0 + n1);
+        if (e0 <= a.E) a.item_start[e0] = ne;
+        if (e1 <= a.E) a.item_start[e1] = ne + n0;
+        if (tid == 63 && a.E == 128) a.item_start[128] = ns;
+    }
     for (int e = tid; e < a.E; e += nth) {
         a.counts[e] = L.cnt[e];
         const int nt = L.tstart[e + 1] - L.tstart[e];
