@@ -560,6 +560,10 @@ static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
 // (compute_logits) with an AuxiliaryFreeLoss gates on logits + its bias
 // (src/core/moe_layer.jl:137-140) in a second route pass and, when training,
 // counts one compute_loss call for the bias update (auxiliary_free.jl:36-40).
+// Workgroup slots of the bf16 GEMMs (their tail split plans its last round
+// over them): 128-row tiles run two workgroups per CU.
+static int gemm_slots(const moe_handle *h) { return h->bm == 128 ? 2 * h->ncu : h->ncu; }
+
 // n-tiles of the up GEMM
 static int up_ntiles(const moe_handle *h) {
     return h->bf16_gemm ? h->H_pad / (h->gated ? 128 : 256) : h->H_pad / kGemmBN;
@@ -675,8 +679,13 @@ static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
     g.s0 = h->s1; g.s1 = h->s3; g.bias = h->gated ? nullptr : h->b1; g.s_stride = h->H_pad;
     g.N = h->H; g.K = h->D_pad; g.C = h->hbuf; g.ldc = h->H_pad;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
-    g.tile_start = h->tile_start; g.E = h->E; g.ksplit = 1; g.ncu = h->ncu;
+    g.tile_start = h->tile_start; g.E = h->E;
     g.item_start = up_pairs(h) ? h->item_start : nullptr;
+    // bf16 kernel on 256-row tiles (one workgroup per CU, whose last round
+    // would leave most CUs idle for a whole tile): the tail split of that
+    // round, folded by fold_up_kernel
+    g.ksplit = (h->bf16_gemm && h->split_ws && h->bm == 256) ? kUpSplitMax : 1;
+    g.ncu = h->bf16_gemm ? gemm_slots(h) : h->ncu; g.split_ws = h->split_ws;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
     // bf16 kernel: 128 h columns (gated, W1 and W3 rows) or 256 rows per tile
     g.n_tiles = up_ntiles(h);
@@ -688,9 +697,6 @@ static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
 // and fold_split_kernel adds their partials to y in range order.
 static int down_ksplit(const moe_handle *h) { return h->bf16_gemm ? kDownSplitMax : 1; }
 
-// Workgroup slots of the bf16 down GEMM (the tail split plans its last
-// round over them): 128-row tiles run two workgroups per CU.
-static int down_slots(const moe_handle *h) { return h->bm == 128 ? 2 * h->ncu : h->ncu; }
 
 static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     GemmArgs g{};
@@ -700,7 +706,7 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->ld_y;
     g.c_bf16 = (h->bf16_gemm && !y_f32) ? 1 : 0;  // the bf16-kernel paths keep y in bf16
-    g.ksplit = ksplit; g.ncu = down_slots(h); g.split_ws = h->split_ws;
+    g.ksplit = ksplit; g.ncu = gemm_slots(h); g.split_ws = h->split_ws;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
@@ -949,9 +955,10 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     // spread over the HBM channels
     h->ld_y = h->bf16_gemm ? (int)round_up(h->Dout, 64) + 64 : h->Dout;
     A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->ld_y);
-    // tail split: fewer split tiles than down-GEMM slots, each with up to kDownSplitMax partial blocks of BM x 256
+    // tail split: at most gemm_slots partial blocks of BM x 256 floats
+    // (rem * S <= slots) for either GEMM
     if (h->bf16_gemm)
-        A((void **)&h->split_ws, sizeof(float) * (size_t)down_slots(h) * h->bm * 256 * kDownSplitMax);
+        A((void **)&h->split_ws, sizeof(float) * (size_t)gemm_slots(h) * h->bm * 256);
     if (r != MOE_OK) return cleanup(r);
     // Pads of the packed weights and of the activation rows must read as 0.
     hipError_t ze = hipSuccess;

@@ -130,102 +130,91 @@ struct TileJob {
     long long arow0;   // first A row (expert-ordered row of the tile's first row)
 };
 
-// Work items: the tiles that are not split, then the K ranges of the split
+// Work items: the items that are not split, then the K ranges of the split
 // ones (tail_split).  Each class is dealt to the 8 XCDs in contiguous ranges
 // (block L runs on XCD L mod 8): slots 0 .. pf-1 of an XCD take its whole
-// tiles, the next ps slots its split items, which are dispatched last.
-// With g.item_start (the up GEMM, NT even, 256-row tiles) an expert whose
-// last M tile holds r <= BM / 2 rows has, per pair of n-tiles (2 j, 2 j + 1),
-// the f full M tiles of n-tile 2 j, those of n-tile 2 j + 1, then one paired
-// item: its last M tile against both n-tiles (the other experts as above).
-// A paired item runs the MFMAs of a full tile, so every workgroup of a round
-// takes about as long as the others and the workgroups that share weight
-// tiles stay in step; item_start[e] = the items before expert e.
+// items, the next ps slots its split items, which are dispatched last.
+//
+// The plain list: tile t of W = tile_start[E] * NT, expert-major, then
+// n-tile, then m-tile.  With g.item_start (the up GEMM, NT even, 256-row
+// tiles) an expert whose last M tile holds r <= BM / 2 rows has, per pair of
+// n-tiles (2 j, 2 j + 1), the f full M tiles of n-tile 2 j, those of n-tile
+// 2 j + 1, then one paired item: its last M tile against both n-tiles (the
+// other experts as in the plain list); W = item_start[E].  A paired item runs
+// the MFMAs of a full tile, so every workgroup of a round takes about as long
+// as the others and the workgroups that share weight tiles stay in step.
+
+// Items of the work list.
+__device__ __forceinline__ int work_items(const GemmArgs &g) {
+    return g.item_start ? g.item_start[g.E] : g.tile_start[g.E] * g.n_tiles;
+}
+
+// Item -> tile (e, n0, rows, mt, pair); the K range fields are the caller's.
 template <int BM, int NB>
-__device__ __forceinline__ bool decode_job_pairs(const GemmArgs &g, TileJob &jb) {
+__device__ __forceinline__ void decode_item(const GemmArgs &g, int item, TileJob &jb) {
     const int NT = g.n_tiles;
-    const int W = g.item_start[g.E];
-    const int pf = (W + 7) >> 3;
-    const int L = blockIdx.x, x = L & 7, slot = L >> 3;
-    const int item = x * pf + slot;
-    if (slot >= pf || item >= W) return false;
-    int lo = 0, hi = g.E - 1;  // largest e with item_start[e] <= item (a non-empty expert)
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (g.item_start[mid] <= item) lo = mid; else hi = mid - 1;
+    int lo = 0, hi = g.E - 1;  // largest e whose first item is <= item (a non-empty expert)
+    if (g.item_start) {
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (g.item_start[mid] <= item) lo = mid; else hi = mid - 1;
+        }
+    } else {
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (g.tile_start[mid] * NT <= item) lo = mid; else hi = mid - 1;
+        }
     }
     const int e = lo;
     const int c = g.counts[e];
     const int f = c / BM, r = c - f * BM;
-    const int local = item - g.item_start[e];
     int nt, m, pair = 0;
-    if (r > 0 && r <= BM / 2) {
+    if (g.item_start && r > 0 && r <= BM / 2) {
+        const int local = item - g.item_start[e];
         const int gs = 2 * f + 1;
         const int j = local / gs, q = local - j * gs;
         if (q < f) { nt = 2 * j; m = q; }
         else if (q < 2 * f) { nt = 2 * j + 1; m = q - f; }
         else { nt = 2 * j; m = f; pair = 1; }
     } else {
-        const int nte = f + (r > 0 ? 1 : 0);
+        const int nte = f + (r > 0 ? 1 : 0);  // = tile_start[e + 1] - tile_start[e]
+        const int local = item - (g.item_start ? g.item_start[e] : g.tile_start[e] * NT);
         nt = local / nte;
         m = local - nt * nte;
     }
     const int m0 = m * BM;
     jb.e = e;
-    jb.ks = 0;
-    jb.nks = 1;
-    jb.KT = g.K / 32;
     jb.rows = min(BM, c - m0);
     jb.arow0 = (long long)g.offsets[e] + m0;
     jb.n0 = nt * (NB == 2 ? 128 : 256);
-    jb.split_j = 0;
     jb.mt = g.tile_start[e] + m;
     jb.pair = pair;
-    return true;
 }
 
 template <int BM, int NB>
 __device__ __forceinline__ bool decode_job(const GemmArgs &g, TileJob &jb) {
-    if (g.item_start) return decode_job_pairs<BM, NB>(g, jb);
-    const int NT = g.n_tiles;
-    const int W = g.tile_start[g.E] * NT;
+    const int W = work_items(g);
     const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
     const int nsi = (W - ts.nfull) * ts.S;  // split items
     const int pf = (ts.nfull + 7) >> 3, ps = (nsi + 7) >> 3;
     const int L = blockIdx.x, x = L & 7, slot = L >> 3;
-    int tile, ks = 0, nks = 1;
+    int item, ks = 0, nks = 1;
     if (slot < pf) {
-        tile = x * pf + slot;
-        if (tile >= ts.nfull) return false;
+        item = x * pf + slot;
+        if (item >= ts.nfull) return false;
     } else {
         if (slot - pf >= ps) return false;
         const int q = x * ps + (slot - pf);
         if (q >= nsi) return false;
-        tile = ts.nfull + q / ts.S;
+        item = ts.nfull + q / ts.S;
         ks = q - (q / ts.S) * ts.S;
         nks = ts.S;
     }
-    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT <= tile (a non-empty expert)
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (g.tile_start[mid] * NT <= tile) lo = mid; else hi = mid - 1;
-    }
-    const int e = lo;
-    const int t0 = g.tile_start[e];
-    const int nte = g.tile_start[e + 1] - t0;
-    const int local = tile - t0 * NT;  // within the expert: n-tile major, m-tile minor
-    const int nt = local / nte;
-    const int m0 = (local - nt * nte) * BM;
-    jb.e = e;
+    decode_item<BM, NB>(g, item, jb);
     jb.ks = ks;
     jb.nks = nks;
     jb.KT = g.K / 32 / nks;
-    jb.rows = min(BM, g.counts[e] - m0);
-    jb.arow0 = (long long)g.offsets[e] + m0;
-    jb.n0 = nt * (NB == 2 ? 128 : 256);
-    jb.split_j = tile - ts.nfull;
-    jb.mt = t0 + m0 / BM;
-    jb.pair = 0;
+    jb.split_j = item - ts.nfull;
     return true;
 }
 
@@ -621,10 +610,19 @@ struct RingShape {
     static constexpr int BYTES = NS * STAGE;
 };
 
-// One work item.  PAIR: a paired item (decode_job_pairs): 4 waves as 2 (n-tile
+// One work item.  SPLIT: a K range of a split up-GEMM tile, which stores its
+// partial sums (its own instantiation: the branch after the main loop would
+// keep registers live through it).  PAIR: a paired item (decode_item): 4
+// waves as 2 (n-tile
 // of the pair) x 2 (N), each over the item's BM / 2 rows; otherwise 2 (M) x 2
 // (N) over the BM rows of one n-tile.
-template <int MODE, int BM, int ACT, int WF8, int OCC, bool PAIR>
+template <int IM, int JN>
+__device__ __forceinline__ void store_partial(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN]);
+template <int MODE, int BM, int ACT, int WF8, int OCC, bool PAIR, int IM, int JN>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
+                                              uint8_t *ring_);
+
+template <int MODE, int BM, int ACT, int WF8, int OCC, bool PAIR, bool SPLIT = false>
 __device__ __forceinline__ void tile_body(const GemmArgs &g, const TileJob &jb, uint8_t *ring_) {
     constexpr int NWAVE = 4;
     constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
@@ -794,11 +792,47 @@ __device__ __forceinline__ void tile_body(const GemmArgs &g, const TileJob &jb, 
         else run(ic<3>{});
     }
     wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
+    if constexpr (SPLIT) {
+        // a K range of a split up-GEMM tile: its partial sums, for fold_up_kernel
+        store_partial<IM, JN>(g, jb, acc);
+        return;
+    }
+    tile_epilogue<MODE, BM, ACT, WF8, OCC, PAIR>(g, jb, acc, ring_);
+}
 
-    // bf16 outputs are staged in the (now idle) LDS ring, rows of CW bytes:
-    // h as its tile image; y rows when y is bf16, the tile not split and N,
-    // ldc multiples of 8 (whole 16-byte chunks).  A paired item stages the
-    // rows of its n-tile nt + wm at rows wm BM / 2 ..
+// Partial sums of one K range of a split up-GEMM tile, in fragment order:
+// block (split_j S + ks) of split_ws holds BM x 256 floats, thread t's
+// accumulator values (i, j, q) at float (((i JN + j) 4 + q / 4) 256 + t) 4 +
+// q % 4, so each wave writes and reads whole 1 KB runs.
+template <int IM, int JN>
+__device__ __forceinline__ void store_partial(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN]) {
+    float *ws = g.split_ws + ((long long)jb.split_j * jb.nks + jb.ks) * (IM * JN * 16 * 256) + threadIdx.x * 4;
+#pragma unroll
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int j = 0; j < JN; ++j)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+                *(float4 *)(ws + ((i * JN + j) * 4 + q4) * 1024) =
+                    make_float4(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1], acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
+}
+
+// The epilogue of a tile whose accumulators are complete.  bf16 outputs are
+// staged in the (idle) LDS ring, rows of CW bytes: h as its tile image; y
+// rows when y is bf16, the tile not split and N, ldc multiples of 8 (whole
+// 16-byte chunks).  A paired item stages the rows of its n-tile nt + wm at
+// rows wm BM / 2 ..
+template <int MODE, int BM, int ACT, int WF8, int OCC, bool PAIR, int IM, int JN>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs &g, const TileJob &jb, const f32x16_t (&acc)[IM][JN],
+                                              uint8_t *ring_) {
+    constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
+    constexpr int BMA = PAIR ? BM / 2 : BM;
+    constexpr int WM = BM / 2;
+    constexpr int WN = 128;
+    constexpr int RING = RingShape<BM, WF8, OCC>::BYTES;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w & 1, wn = w >> 1;
     constexpr int CW = (MODE == MODE_GATED_UP ? 128 : 256) * 2;  // output bytes per tile row
     constexpr int CH = CW / 16;
     static_assert(BM * CW <= RING, "LDS staging of the output tile");
@@ -831,6 +865,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     __shared__ __attribute__((aligned(1024))) uint8_t ring[RingShape<BM, WF8, OCC>::BYTES];
     TileJob jb;
     if (!decode_job<BM, (MODE == MODE_GATED_UP) ? 2 : 1>(g, jb)) return;
+    if constexpr (MODE != MODE_DOWN) {
+        if (jb.nks > 1) {
+            if constexpr (BM == 256) {
+                if (jb.pair) {
+                    tile_body<MODE, BM, ACT, WF8, OCC, true, true>(g, jb, ring);
+                    return;
+                }
+            }
+            tile_body<MODE, BM, ACT, WF8, OCC, false, true>(g, jb, ring);
+            return;
+        }
+    }
     if constexpr (MODE != MODE_DOWN && BM == 256) {
         if (jb.pair) {
             tile_body<MODE, BM, ACT, WF8, OCC, true>(g, jb, ring);
@@ -838,6 +884,91 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         }
     }
     tile_body<MODE, BM, ACT, WF8, OCC, false>(g, jb, ring);
+}
+
+// ============================================================================
+// Fold of the up GEMM's split tiles (tail_split).  Work unit (j, i, mo) of a
+// split tile j: for every thread t of the tile's workgroup, its accumulator
+// blocks [i][2 mo], [i][2 mo + 1] (a 32-row block and 64 B-tile columns of its
+// wave: one W1 | W3 column pair of the gated mode, two column blocks
+// otherwise).  Thread t of a fold workgroup sums those blocks' K-range
+// partials in range order (a fixed order, so results are deterministic) and
+// runs the tile's epilogue on them (fp8 scales, bias, activation, dropout),
+// storing its bf16 h values straight into the h tile image (ImagePut).
+// Workgroups stride over the units.
+// ============================================================================
+// Sink of h values into the h tile image: rows of 64 B per 32-wide K stage
+// block of BM rows, chunk c of row r at position c ^ ((r >> 2) & 3) (the
+// layout store_staged writes).  base: the image block of the tile's M tile
+// and of the stage of column n0.
+template <int BM>
+struct ImagePut {
+    uint8_t *base;
+    __device__ __forceinline__ void operator()(int ml, int lc, float v0, float v1, float v2, float v3) const {
+        const int p = ((lc >> 3) & 3) ^ ((ml >> 2) & 3);
+        uint8_t *a = base + ((long long)(lc >> 5) * BM + ml) * 64 + p * 16 + (lc & 4) * 2;
+        *(uint2 *)a = pack_bf16x4(v0, v1, v2, v3);
+    }
+};
+
+template <int MODE, int BM, int ACT, int WF8>
+__global__ __launch_bounds__(256) void fold_up_kernel(GemmArgs g) {
+    constexpr int NB = (MODE == MODE_GATED_UP) ? 2 : 1;
+    constexpr int IM = BM / 64, JN = 4;  // the accumulator blocks of tile_body's waves
+    constexpr int WN = 128;
+    constexpr long long BLK = IM * JN * 16 * 256;  // floats per partial block
+    const int W = work_items(g);
+    const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
+    if (ts.S < 2) return;
+    const int nunit = (W - ts.nfull) * IM * 2;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w & 1, wn = w >> 1;
+    const long long KTT = g.ldc / 32;  // h: K of the down GEMM = ldc
+    for (int u = blockIdx.x; u < nunit; u += gridDim.x) {
+        const int j = u / (IM * 2), i = (u >> 1) % IM, mo = u & 1;
+        // every partial of the unit in flight before the work-item decode
+        // (a chain of dependent loads) runs
+        const float *ws = g.split_ws + (long long)j * ts.S * BLK + t * 4;
+        float4 p[kUpSplitMax][8];
+#pragma unroll
+        for (int r = 0; r < kUpSplitMax; ++r)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (r < ts.S) p[r][q] = *(const float4 *)(ws + r * BLK + ((i * JN + 2 * mo) * 4 + q) * 1024);
+        TileJob jb;
+        decode_item<BM, NB>(g, ts.nfull + j, jb);
+        jb.ks = 0;
+        jb.nks = 1;
+        jb.KT = g.K / 32;
+        jb.split_j = j;
+        f32x16_t acc[1][2];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            float4 a = p[0][q];
+#pragma unroll
+            for (int r = 1; r < kUpSplitMax; ++r)
+                if (r < ts.S) {
+                    a.x = a.x + p[r][q].x; a.y = a.y + p[r][q].y; a.z = a.z + p[r][q].z; a.w = a.w + p[r][q].w;
+                }
+            acc[0][q >> 2][4 * (q & 3)] = a.x;
+            acc[0][q >> 2][4 * (q & 3) + 1] = a.y;
+            acc[0][q >> 2][4 * (q & 3) + 2] = a.z;
+            acc[0][q >> 2][4 * (q & 3) + 3] = a.w;
+        }
+        // the columns of these blocks: gated, h columns wn WN / 2 + 32 mo ..;
+        // otherwise B-tile columns wn WN + 64 mo ..; a paired item's wave wm
+        // holds n-tile nt + wm over the item's rows
+        TileJob jw = jb;
+        int row0;
+        if (jb.pair) {
+            jw.n0 += wm * (NB == 2 ? 128 : 256);
+            row0 = i * 32;
+        } else {
+            row0 = wm * (BM / 2) + i * 32;
+        }
+        jw.n0 += (NB == 2) ? wn * (WN / 2) + 32 * mo : wn * WN + 64 * mo;
+        ImagePut<BM> put{(uint8_t *)g.C + ((long long)jw.mt * KTT + jw.n0 / 32) * BM * 64};
+        store_tile<MODE, ACT, 1, 2, WN, WF8>(g, jw, acc, row0, 0, lane, put);
+    }
 }
 
 // ============================================================================
@@ -993,7 +1124,16 @@ static hipError_t launch_bf16(const GemmArgs &g, hipStream_t s) {
     // plans its last round over g.ncu = 2 slots per CU)
     constexpr int OCC = (BM == 128) ? 2 : 1;
     hipLaunchKernelGGL((grouped_gemm_bf16_kernel<MODE, BM, ACT, WF8, OCC>), dim3((unsigned)total), dim3(256), 0, s, g);
-    return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    // the up GEMM's split tiles (256-row tiles only) are folded in work units
+    // over g.ncu workgroups
+    if constexpr (MODE != MODE_DOWN && BM == 256) {
+        if (e == hipSuccess && g.ksplit > 1) {
+            hipLaunchKernelGGL((fold_up_kernel<MODE, BM, ACT, WF8>), dim3((unsigned)g.ncu), dim3(256), 0, s, g);
+            e = hipGetLastError();
+        }
+    }
+    return e;
 }
 
 template <int MODE, int BM, int WF8>
@@ -1012,8 +1152,9 @@ static hipError_t launch_bf16_act(const GemmArgs &g, hipStream_t s) {
 
 hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &g, hipStream_t s) {
     if (g.m_tiles_grid <= 0 || g.n_tiles <= 0) return hipSuccess;
-    // only the fp32 down GEMM writes partial sums
-    if (g.ksplit < 1 || (g.ksplit > 1 && (mode != MODE_DOWN || !g.split_ws || g.ncu < 1))) return hipErrorInvalidValue;
+    // split tiles write partial sums; the up GEMM splits 256-row tiles only
+    if (g.ksplit < 1 || (g.ksplit > 1 && (!g.split_ws || g.ncu < 1))) return hipErrorInvalidValue;
+    if (g.ksplit > 1 && mode != MODE_DOWN && bm != 256) return hipErrorInvalidValue;
     if (wfp8 && (!g.s0 || (mode == MODE_GATED_UP && !g.s1))) return hipErrorInvalidValue;
 #define MOE_BF16_CASE(M, B, F) \
     if (mode == M && bm == B && (wfp8 != 0) == (F != 0)) return launch_bf16_act<M, B, F>(g, s);

@@ -212,17 +212,19 @@ struct PermuteArgs {
     int tiled, bm, ktt;
 };
 
-// Tail split of the bf16 down GEMM.  W tiles run on ncu workgroup slots (one
-// per CU for 256-row tiles, two for 128-row tiles); the
-// rem = W mod ncu tiles of the last, partial round are each split into S K
-// ranges (the largest S <= smax with S dividing the K stages and rem * S <=
-// ncu), so that round is as long as 1/S of a tile.  Tiles are numbered
-// expert-major, then n-tile, then m-tile; tiles >= nfull are split.  K range
-// 0 of a split tile writes y, range r >= 1 writes its partial to split_ws
-// block j (S - 1) + r - 1 (j = tile - nfull; a block is BM x 256 fp32, row
-// stride 256); fold_split_kernel then adds them to y in range order.  With
-// a bf16 y every K range r of a split tile writes its partial to block
-// j S + r, and the fold rounds their sum once.
+// Tail split of the bf16 GEMMs.  W work items (tiles, or the up GEMM's
+// paired items) run on ncu workgroup slots (one per CU for 256-row tiles, two
+// for 128-row tiles); the rem = W mod ncu items of the last, partial round
+// are each split into S K ranges (the largest S <= smax with S dividing the K
+// stages and rem * S <= ncu), so that round is as long as 1/S of a tile.
+// Items are numbered expert-major, then n-tile, then m-tile; items >= nfull
+// are split.  Down GEMM: K range 0 of a split tile writes y, range r >= 1
+// writes its partial to split_ws block j (S - 1) + r - 1 (j = tile - nfull; a
+// block is BM x 256 fp32, row stride 256); fold_split_kernel then adds them
+// to y in range order.  With a bf16 y every K range r of a split tile writes
+// its partial to block j S + r, and the fold rounds their sum once.  Up GEMM:
+// every range writes block j S + r in fragment order, and fold_up_kernel
+// sums them and runs the epilogue.
 struct TailSplit {
     int nfull;   // tiles not split
     int S;       // K ranges of each split tile (1: none)
@@ -240,6 +242,10 @@ __host__ __device__ inline TailSplit tail_split(int W, int ncu, int smax, int st
     return t;
 }
 constexpr int kDownSplitMax = 4;
+// The up GEMM's tail split: K ranges of a split tile (its partials are BM x
+// 256 floats per range in fragment order; fold_up_kernel sums them and runs
+// the tile's epilogue).
+constexpr int kUpSplitMax = 4;
 
 struct CombineArgs {
     const void *y; int ld_y;     // [rows][ld_y], fp32 or (y_bf16) bf16
@@ -269,7 +275,7 @@ struct GemmArgs {
     int m_tiles_grid; int n_tiles;
     int ksplit;                          // bf16 kernel: the most K ranges a tail tile may be split into (tail_split)
     int ncu;                             // workgroup slots of one round (CUs x workgroups per CU)
-    float *split_ws;                     // partials of split tiles (MODE_DOWN, ksplit > 1)
+    float *split_ws;                     // partials of split tiles (ksplit > 1)
     int act;
     int c_bf16;                          // MODE_DOWN: y in bf16 (else fp32)
     // MODE_STD_UP in training: StandardExpert's Dropout(drop_p)
