@@ -927,32 +927,48 @@ __global__ __launch_bounds__(256) void fold_up_kernel(GemmArgs g) {
         const int j = u / (IM * 2), i = (u >> 1) % IM, mo = u & 1;
         // every partial of the unit in flight before the work-item decode
         // (a chain of dependent loads) runs
-        const float *ws = g.split_ws + (long long)j * ts.S * BLK + t * 4;
-        float4 p[kUpSplitMax][8];
+        const float *ws = g.split_ws + (long long)j * ts.S * BLK + ((i * JN + 2 * mo) * 4) * 1024 + t * 4;
+        constexpr int RB = 4;  // ranges whose loads are in flight together
+        float4 p[RB][8], a[8];
 #pragma unroll
-        for (int r = 0; r < kUpSplitMax; ++r)
+        for (int r = 0; r < RB; ++r)
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-                if (r < ts.S) p[r][q] = *(const float4 *)(ws + r * BLK + ((i * JN + 2 * mo) * 4 + q) * 1024);
+                if (r < ts.S) p[r][q] = *(const float4 *)(ws + r * BLK + q * 1024);
         TileJob jb;
         decode_item<BM, NB>(g, ts.nfull + j, jb);
         jb.ks = 0;
         jb.nks = 1;
         jb.KT = g.K / 32;
         jb.split_j = j;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) a[q] = p[0][q];
+        // ranges in order: a = ((p0 + p1) + p2) + ...
+#pragma unroll
+        for (int r0 = 0; r0 < kUpSplitMax; r0 += RB) {
+            if (r0 > 0) {
+#pragma unroll
+                for (int r = 0; r < RB; ++r)
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        if (r0 + r < ts.S) p[r][q] = *(const float4 *)(ws + (r0 + r) * BLK + q * 1024);
+            }
+#pragma unroll
+            for (int r = (r0 == 0 ? 1 : 0); r < RB; ++r)
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (r0 + r < ts.S) {
+                        a[q].x = a[q].x + p[r][q].x; a[q].y = a[q].y + p[r][q].y;
+                        a[q].z = a[q].z + p[r][q].z; a[q].w = a[q].w + p[r][q].w;
+                    }
+        }
         f32x16_t acc[1][2];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            float4 a = p[0][q];
-#pragma unroll
-            for (int r = 1; r < kUpSplitMax; ++r)
-                if (r < ts.S) {
-                    a.x = a.x + p[r][q].x; a.y = a.y + p[r][q].y; a.z = a.z + p[r][q].z; a.w = a.w + p[r][q].w;
-                }
-            acc[0][q >> 2][4 * (q & 3)] = a.x;
-            acc[0][q >> 2][4 * (q & 3) + 1] = a.y;
-            acc[0][q >> 2][4 * (q & 3) + 2] = a.z;
-            acc[0][q >> 2][4 * (q & 3) + 3] = a.w;
+            acc[0][q >> 2][4 * (q & 3)] = a[q].x;
+            acc[0][q >> 2][4 * (q & 3) + 1] = a[q].y;
+            acc[0][q >> 2][4 * (q & 3) + 2] = a[q].z;
+            acc[0][q >> 2][4 * (q & 3) + 3] = a[q].w;
         }
         // the columns of these blocks: gated, h columns wn WN / 2 + 32 mo ..;
         // otherwise B-tile columns wn WN + 64 mo ..; a paired item's wave wm

@@ -245,7 +245,7 @@ constexpr int kDownSplitMax = 4;
 // The up GEMM's tail split: K ranges of a split tile (its partials are BM x
 // 256 floats per range in fragment order; fold_up_kernel sums them and runs
 // the tile's epilogue).
-constexpr int kUpSplitMax = 4;
+constexpr int kUpSplitMax = 8;
 
 struct CombineArgs {
     const void *y; int ld_y;     // [rows][ld_y], fp32 or (y_bf16) bf16
