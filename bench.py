@@ -179,6 +179,18 @@ def up_kernel_name(cfg):
     return "grouped_gemm_kernel (expert up GEMM, {} weights)".format(cfg["w"])
 
 
+def up_algorithmic_bytes(cfg, rows):
+    """Algorithmic HBM bytes of one up-GEMM launch: every expert's W1 (and W3)
+    once, its fp8 row scales, the permuted x rows read and h written once
+    (bf16 on the bf16/fp8-weight paths, fp32 otherwise)."""
+    D, H, E = cfg["D"], cfg["H"], cfg["E"]
+    mats = 2 if cfg["etype"] == "gated" else 1
+    wb = {"f32": 4, "bf16": 2, "fp8": 1}[cfg["w"]]
+    ab = 4 if cfg["w"] == "f32" else 2
+    weights = E * mats * H * D * wb + (E * mats * H * 4 if cfg["w"] == "fp8" else 0)
+    return weights + rows * D * ab + rows * H * ab
+
+
 def measured_traffic(cfg):
     """HBM bytes per launch of the dominant kernel, from the committed
     rocprofv3 FETCH_SIZE + WRITE_SIZE summary (profiles/hbm_traffic.json),
@@ -438,6 +450,20 @@ def main():
     permute_bytes = T * D * xs + rows * D * xs
     combine_bytes = rows * D * xs + rows * 8 + T * D * 4
     gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
+    # the up GEMM's binding roofline: MFMA when its flops at peak take longer
+    # than its algorithmic bytes at HBM peak (Mixtral, DeepSeek), else HBM
+    # (Switch: 128 experts of ~128 rows, weight-bandwidth bound)
+    up_bytes = up_algorithmic_bytes(cfg, rows)
+    if up_flops / (peak * 1e12) >= up_bytes / (PEAK_HBM_GBS * 1e9):
+        roofline = {"bound": "mfma", "kernel": up_kernel_name(cfg), "launch_ms": round(up_ms, 4),
+                    "achieved": round(up_tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(up_tflops / peak, 4), "traffic": measured_traffic(cfg)}
+    else:
+        up_gbs = gbs(up_bytes, up_ms)
+        roofline = {"bound": "hbm", "kernel": up_kernel_name(cfg), "launch_ms": round(up_ms, 4),
+                    "achieved": round(up_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(up_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(cfg),
+                    "algorithmic_bytes": up_bytes}
     line = {
         "metric": METRIC,
         "value": round(tokens_s, 1),
@@ -455,9 +481,7 @@ def main():
                    "top_k": k, "shared_experts": cfg["ns"], "expert_type": cfg["etype"], "activation": cfg["act"],
                    "weights": cfg["w"], "output": "f32"},
         "tflops": round((up_flops + down_flops) / (ms_step * 1e-3) / 1e12, 2),
-        "roofline": {"bound": "mfma", "kernel": up_kernel_name(cfg), "launch_ms": round(up_ms, 4),
-                     "achieved": round(up_tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(up_tflops / peak, 4), "traffic": measured_traffic(cfg)},
+        "roofline": roofline,
         "stages": {
             "router": {"ms": round(stage_ms["router"], 4), "GB/s": round(gbs(router_bytes, stage_ms["router"]), 1)},
             "permute": {"ms": round(stage_ms["permute"], 4), "GB/s": round(gbs(permute_bytes, stage_ms["permute"]), 1)},
