@@ -100,11 +100,12 @@ struct moe_handle {
     int *num_tiles = nullptr;
     int *tile_start = nullptr;
     int *item_start = nullptr;  // [E+1] the up GEMM's paired work items (up_pairs)
+    long long split_cap = 0;    // floats of split_ws
     float *scalars = nullptr;
     int *perm = nullptr, *pos_of = nullptr;
     void *xp = nullptr, *hbuf = nullptr;
     float *y = nullptr;
-    float *split_ws = nullptr;  // down-GEMM tail split: partials of the split tiles
+    float *split_ws = nullptr;  // partial sums of the GEMMs' split tiles / K ranges
     int ncu = 256;              // compute units: workgroup slots of one GEMM round
     void *x_dev = nullptr;
     float *out_dev = nullptr;
@@ -685,7 +686,7 @@ static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
     // would leave most CUs idle for a whole tile): the tail split of that
     // round, folded by fold_up_kernel
     g.ksplit = (h->bf16_gemm && h->split_ws && h->bm == 256) ? kUpSplitMax : 1;
-    g.ncu = h->bf16_gemm ? gemm_slots(h) : h->ncu; g.split_ws = h->split_ws;
+    g.ncu = h->bf16_gemm ? gemm_slots(h) : h->ncu; g.split_ws = h->split_ws; g.split_cap = h->split_cap;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
     // bf16 kernel: 128 h columns (gated, W1 and W3 rows) or 256 rows per tile
     g.n_tiles = up_ntiles(h);
@@ -706,7 +707,8 @@ static GemmArgs down_args(moe_handle *h, int mt_grid, int ksplit, bool y_f32) {
     g.s0 = h->s2; g.s1 = nullptr; g.bias = h->gated ? nullptr : h->b2; g.s_stride = h->Dout_npad;
     g.N = h->Dout; g.K = h->H_pad; g.C = h->y; g.ldc = h->ld_y;
     g.c_bf16 = (h->bf16_gemm && !y_f32) ? 1 : 0;  // the bf16-kernel paths keep y in bf16
-    g.ksplit = ksplit; g.ncu = gemm_slots(h); g.split_ws = h->split_ws;
+    g.ksplit = ksplit; g.ncu = h->bf16_gemm ? gemm_slots(h) : h->ncu;
+    g.split_ws = h->split_ws; g.split_cap = h->split_cap;
     g.tiles = h->tiles; g.num_tiles = h->num_tiles; g.counts = h->counts; g.offsets = h->offsets;
     g.tile_start = h->tile_start; g.E = h->E;
     g.m_tiles_grid = mt_grid; g.act = h->cfg.activation;
@@ -956,9 +958,10 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->ld_y = h->bf16_gemm ? (int)round_up(h->Dout, 64) + 64 : h->Dout;
     A((void **)&h->y, sizeof(float) * (size_t)h->rows_max * h->ld_y);
     // tail split: at most gemm_slots partial blocks of BM x 256 floats
-    // (rem * S <= slots) for either GEMM
-    if (h->bf16_gemm)
-        A((void **)&h->split_ws, sizeof(float) * (size_t)gemm_slots(h) * h->bm * 256);
+    // (rem * S <= slots) for either GEMM; the fp32 kernel's K split of small
+    // tile grids: about two workgroups per CU of NB x 128 x 128 floats
+    h->split_cap = h->bf16_gemm ? (long long)gemm_slots(h) * h->bm * 256 : 2LL * h->ncu * kGemmBM * kGemmBN;
+    A((void **)&h->split_ws, sizeof(float) * (size_t)h->split_cap);
     if (r != MOE_OK) return cleanup(r);
     // Pads of the packed weights and of the activation rows must read as 0.
     hipError_t ze = hipSuccess;

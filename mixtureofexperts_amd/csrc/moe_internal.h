@@ -246,6 +246,8 @@ constexpr int kDownSplitMax = 4;
 // 256 floats per range in fragment order; fold_up_kernel sums them and runs
 // the tile's epilogue).
 constexpr int kUpSplitMax = 8;
+// The fp32 grouped GEMM's K split (small tile grids): at most this many ranges.
+constexpr int kF32SplitMax = 8;
 
 struct CombineArgs {
     const void *y; int ld_y;     // [rows][ld_y], fp32 or (y_bf16) bf16
@@ -276,6 +278,7 @@ struct GemmArgs {
     int ksplit;                          // bf16 kernel: the most K ranges a tail tile may be split into (tail_split)
     int ncu;                             // workgroup slots of one round (CUs x workgroups per CU)
     float *split_ws;                     // partials of split tiles (ksplit > 1)
+    long long split_cap;                 // fp32 kernel: floats of split_ws (its K split fits within)
     int act;
     int c_bf16;                          // MODE_DOWN: y in bf16 (else fp32)
     // MODE_STD_UP in training: StandardExpert's Dropout(drop_p)
