@@ -367,6 +367,25 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
         __syncthreads();  // the pass's x tile is consumed
     }
 
+    const float *bias = a.r.bias;
+    if (!PAIRED && KG == 1) {
+        // one K group: each logit is one wave's accumulator, written with the
+        // bias straight into its row (the values the partial-sum pass gives)
+        if (mw) {
+#pragma unroll
+            for (int ti = 0; ti < RT; ++ti) {
+                const int e = cg * 16 + l16;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int t = ti * 16 + (lane >> 4) * 4 + rr;
+                    float v = acc[ti][0][rr];
+                    if (bias && e < a.r.Er) v = v + bias[e];
+                    if (e < g.Er) L[t * a.RW + e] = v;
+                }
+            }
+        }
+        return;
+    }
     // accumulators -> LDS partials P[kg][t][col] (over the staging region),
     // col = image column of the expert tile (paired: 16 j + c)
     const int NCOL = PAIRED ? 32 : ET * 16;
@@ -386,7 +405,6 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
         }
     }
     __syncthreads();
-    const float *bias = a.r.bias;
     for (int q = tid; q < TB * g.Er; q += kRtThreads) {
         const int t = q / g.Er, e = q - t * g.Er;
         auto col_sum = [&](int col) __attribute__((always_inline)) {
