@@ -136,13 +136,16 @@ struct TileJob {
 // items, the next ps slots its split items, which are dispatched last.
 //
 // The plain list: tile t of W = tile_start[E] * NT, expert-major, then
-// n-tile, then m-tile.  With g.item_start (the up GEMM, NT even, 256-row
+// blocks of kMBlock M tiles, then n-tile, then M tile.  With g.item_start (the up GEMM, NT even, 256-row
 // tiles) an expert whose last M tile holds r <= BM / 2 rows has, per pair of
 // n-tiles (2 j, 2 j + 1), the f full M tiles of n-tile 2 j, those of n-tile
 // 2 j + 1, then one paired item: its last M tile against both n-tiles (the
 // other experts as in the plain list); W = item_start[E].  A paired item runs
 // the MFMAs of a full tile, so every workgroup of a round takes about as long
 // as the others and the workgroups that share weight tiles stay in step.
+
+// M tiles per block of the plain list's order.
+constexpr int kMBlock = 8;
 
 // Items of the work list.
 __device__ __forceinline__ int work_items(const GemmArgs &g) {
@@ -177,10 +180,22 @@ __device__ __forceinline__ void decode_item(const GemmArgs &g, int item, TileJob
         else if (q < 2 * f) { nt = 2 * j + 1; m = q - f; }
         else { nt = 2 * j; m = f; pair = 1; }
     } else {
+        // blocks of kMBlock M tiles: block-major, then n-tile, then M tile,
+        // so an expert of many M tiles re-reads neither its rows for every
+        // n-tile nor its weights for every M tile (the last block holds the
+        // remaining ml tiles)
         const int nte = f + (r > 0 ? 1 : 0);  // = tile_start[e + 1] - tile_start[e]
         const int local = item - (g.item_start ? g.item_start[e] : g.tile_start[e] * NT);
-        nt = local / nte;
-        m = local - nt * nte;
+        const int nfb = nte / kMBlock, infull = nfb * kMBlock * NT;
+        if (local < infull) {
+            const int b = local / (kMBlock * NT), q = local - b * (kMBlock * NT);
+            nt = q / kMBlock;
+            m = b * kMBlock + (q - nt * kMBlock);
+        } else {
+            const int ml = nte - nfb * kMBlock, q = local - infull;
+            nt = q / ml;
+            m = nfb * kMBlock + (q - nt * ml);
+        }
     }
     const int m0 = m * BM;
     jb.e = e;
@@ -994,28 +1009,19 @@ __global__ __launch_bounds__(256) void fold_up_kernel(GemmArgs g) {
 // 4 rows, with all their loads in flight (one batch: no store is followed by
 // a load in the same thread).
 // ============================================================================
-__global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g, int bm) {
+template <int BM>
+__global__ __launch_bounds__(256) void fold_split_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
-    const int NT = g.n_tiles;
-    const int W = g.tile_start[g.E] * NT;
+    constexpr int bm = BM;
+    const int W = work_items(g);
     const TailSplit ts = tail_split(W, g.ncu, g.ksplit, g.K / 32);
     const int j = blockIdx.x;
     if (ts.S < 2 || j >= W - ts.nfull) return;
-    const int tile = ts.nfull + j;
-    int lo = 0, hi = g.E - 1;  // largest e with tile_start[e] * NT <= tile (a non-empty expert)
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (g.tile_start[mid] * NT <= tile) lo = mid; else hi = mid - 1;
-    }
-    const int e = lo;
-    const int t0 = g.tile_start[e];
-    const int nte = g.tile_start[e + 1] - t0;
-    const int local = tile - t0 * NT;
-    const int nt = local / nte;
-    const int m0 = (local - nt * nte) * bm;
-    const int rows = min(bm, g.counts[e] - m0);
-    const long long arow0 = (long long)g.offsets[e] + m0;
-    const int n0 = nt * 256;
+    TileJob jb;
+    decode_item<BM, 1>(g, ts.nfull + j, jb);
+    const int rows = jb.rows;
+    const long long arow0 = jb.arow0;
+    const int n0 = jb.n0;
     const int c4 = (threadIdx.x & 63) * 4;
     const int n = n0 + c4;
     const bool vec4 = (g.ldc & 3) == 0 && n + 3 < g.N;
@@ -1127,7 +1133,12 @@ hipError_t launch_retile_weights(const void *src, void *dst, int Npad, int Kp, i
 
 hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s) {
     if (g.ksplit < 2 || g.ncu < 1 || g.m_tiles_grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fold_split_kernel, dim3(g.ncu, (bm + 15) / 16), dim3(256), 0, s, g, bm);
+    if (bm == 256)
+        hipLaunchKernelGGL(fold_split_kernel<256>, dim3(g.ncu, 16), dim3(256), 0, s, g);
+    else if (bm == 128)
+        hipLaunchKernelGGL(fold_split_kernel<128>, dim3(g.ncu, 8), dim3(256), 0, s, g);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
