@@ -18,8 +18,11 @@
  *    message.  Host-pointer entry points block until results are in host
  *    memory.  *_async entry points take device pointers and a hipStream_t
  *    (passed as void*, NULL = the handle's own stream) and only enqueue.
- *  - Calls on one handle are serialised by the library; distinct handles may
- *    be used from distinct threads.
+ *  - Calls on one handle are serialised by the library, across streams too
+ *    (a call on another stream than the previous async call's waits for that
+ *    call's work); distinct handles may be used from distinct threads.  The
+ *    stream of an async call must stay valid until the next call on the
+ *    handle, or moe_destroy, has returned.
  */
 #ifndef MOE_MI355X_H
 #define MOE_MI355X_H
