@@ -1529,7 +1529,7 @@ __device__ __forceinline__ float4 load_y4(const void *y, long long off) {
 template <int KT, bool BLEND, bool YB>
 __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
 #pragma clang fp contract(off)
-    constexpr int U = (KT >= 8) ? 2 : (KT >= 4 ? 4 : 8);
+    constexpr int U = (KT >= 8) ? 1 : (KT >= 4 ? 4 : 8);
     int ee[KT], pp[KT];
     float gg[KT];
 #pragma unroll
