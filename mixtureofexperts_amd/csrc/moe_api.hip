@@ -651,6 +651,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         A.npass = 1;
         ra.out_mask = ec ? ROUTE_OUT_PROBS : (ROUTE_OUT_PROBS | ROUTE_OUT_GATING);
     }
+    A.ncu = h->ncu;
     HIP_TRY(h, launch_router(A, &h->rb, s));
     if (ec) {
         // the experts' choices give the slots, the stable ranks and the

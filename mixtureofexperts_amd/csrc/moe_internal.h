@@ -174,7 +174,8 @@ struct ScanArgs {
 struct RtArgs {
     RouteArgs r;           // gating (r.out_mask: outputs of the single pass)
     RouterArgs g;          // logits GEMM (when the kernel computes the logits)
-    int TB;                // tokens per workgroup: 16 (paired logits GEMM) or 64
+    int TB;                // tokens per workgroup: 16 (paired logits GEMM), 32 or 64
+    int ncu;               // CUs (64-token workgroups fewer than this: 32-token ones)
     int KP, RB, dma;       // x staging: K columns per pass, LDS bytes per row, by global_load_lds
     int RW;                // LDS row stride of the logits / probability rows (floats)
     int off_L;             // LDS byte offset of the logits rows

@@ -180,14 +180,14 @@ __device__ __forceinline__ double lanes8_sum(double v) {
 // tile; D lane l: column l % 16, tokens 4 (l / 16) .. +4.  The accumulators
 // then go to LDS partials P[kg][t][col] and each logit is their sum in
 // K-group order (paired tiles: the three parts' columns added in part order).
-template <int XBF16, int PAIRED>
+template <int XBF16, int PAIRED, int RT>
 __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds, float *L) {
 #pragma clang fp contract(off)
     constexpr int ESZ = XBF16 ? 2 : 4;
     constexpr int NPT = PAIRED ? 2 : 3;   // image tiles per expert tile and step
     constexpr int NP = XBF16 ? 1 : 3;     // activation parts
     constexpr int NACC = PAIRED ? 2 : 1;  // accumulator tiles per row tile
-    constexpr int RT = PAIRED ? 1 : 4;    // 16-token row tiles (the workgroup's TB = 16 RT tokens)
+    // RT: 16-token row tiles (the workgroup's TB = 16 RT tokens)
     constexpr int kRtSG = XBF16 ? 4 : 2;  // K steps per group of prefetched weight fragments
     // weight groups in the register ring: all of a paired wave's 16 steps in
     // flight at once for bf16 x; otherwise two groups ahead of the MFMAs
@@ -739,7 +739,8 @@ __host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) 
 
 // LG: 0 = the caller's logits (r.part), 1 = logits GEMM on bf16 x, 2 = on fp32
 // x.  PAIRED: Er <= 8 (the paired weight tiles).  EPL: experts per lane.
-template <int LG, int PAIRED, int EPL>
+// RT: 16-token row tiles of the logits GEMM (TB = 16 RT).
+template <int LG, int PAIRED, int EPL, int RT>
 __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t rdyn[];
     __shared__ unsigned emask[MOE_MAX_EXPERTS * kRtMaskWords];
@@ -756,7 +757,7 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
             A.r.clr_supp[(long long)s * A.r.ldc + e] = 0ull;
         }
     if constexpr (LG > 0) {
-        rt_logits<LG == 1, PAIRED>(A, t0, rdyn, L);
+        rt_logits<LG == 1, PAIRED, RT>(A, t0, rdyn, L);
     } else {
         const int Er = A.r.Er;
         for (int q = threadIdx.x; q < ntok * Er; q += kRtThreads) {
@@ -779,9 +780,9 @@ static int route_epl(int E) {
     return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : (E <= 80 ? 10 : (E <= 96 ? 12 : 16)))));
 }
 
-template <int LG, int PAIRED, int EPL>
+template <int LG, int PAIRED, int EPL, int RT>
 static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipStream_t s) {
-    auto kern = router_kernel<LG, PAIRED, EPL>;
+    auto kern = router_kernel<LG, PAIRED, EPL, RT>;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [&] {
@@ -809,9 +810,12 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     const int ET = paired ? 1 : (Eg + 15) / 16;
     // tokens per workgroup: 16 for the paired (few-expert) GEMM, whose x tile
     // is widest; otherwise 64 (the weight image is read once per workgroup:
-    // the more tokens share it the better; 64 tokens fill the gating lanes)
-    // (the logits GEMM's row tiles are compile-time: 1 paired, 4 otherwise)
-    const int TB = gemm && paired ? 16 : 64;
+    // the more tokens share it the better; 64 tokens fill the gating lanes),
+    // or 32 when 64-token workgroups would leave CUs idle (their x tile then
+    // also takes fewer K passes) (the logits GEMM's row tiles are
+    // compile-time: 1, 2 or 4)
+    const bool half = gemm && !paired && A.ncu > 0 && (a.T + 63) / 64 < A.ncu;
+    const int TB = gemm && paired ? 16 : (half ? 32 : 64);
     *tb = TB;
     A.TB = TB;
     A.RW = route_rw(Eg);
@@ -841,26 +845,28 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
         a.nsup_max * kSuper < nblk)
         return hipErrorInvalidValue;
     const int epl = route_epl(Er);
-#define MOE_RT(LG_, P_, EPL_) return launch_router_case<LG_, P_, EPL_>(A, nblk, lds, s)
-#define MOE_RT_EPL(LG_)                 \
+#define MOE_RT(LG_, P_, EPL_, RT_) return launch_router_case<LG_, P_, EPL_, RT_>(A, nblk, lds, s)
+#define MOE_RT_EPL(LG_, RT_)            \
     switch (epl) {                      \
-    case 2: MOE_RT(LG_, 0, 2);          \
-    case 4: MOE_RT(LG_, 0, 4);          \
-    case 8: MOE_RT(LG_, 0, 8);          \
-    case 10: MOE_RT(LG_, 0, 10);        \
-    case 12: MOE_RT(LG_, 0, 12);        \
-    default: MOE_RT(LG_, 0, 16);        \
+    case 2: MOE_RT(LG_, 0, 2, RT_);     \
+    case 4: MOE_RT(LG_, 0, 4, RT_);     \
+    case 8: MOE_RT(LG_, 0, 8, RT_);     \
+    case 10: MOE_RT(LG_, 0, 10, RT_);   \
+    case 12: MOE_RT(LG_, 0, 12, RT_);   \
+    default: MOE_RT(LG_, 0, 16, RT_);   \
     }
     if (!gemm) {
-        if (epl == 1) MOE_RT(0, 0, 1);
-        MOE_RT_EPL(0)
+        if (epl == 1) MOE_RT(0, 0, 1, 4);
+        MOE_RT_EPL(0, 4)
     }
     if (A.g.x_bf16) {
-        if (paired) MOE_RT(1, 1, 1);
-        MOE_RT_EPL(1)
+        if (paired) MOE_RT(1, 1, 1, 1);
+        if (half) MOE_RT_EPL(1, 2)
+        MOE_RT_EPL(1, 4)
     }
-    if (paired) MOE_RT(2, 1, 1);
-    MOE_RT_EPL(2)
+    if (paired) MOE_RT(2, 1, 1, 1);
+    if (half) MOE_RT_EPL(2, 2)
+    MOE_RT_EPL(2, 4)
 #undef MOE_RT_EPL
 #undef MOE_RT
 }
