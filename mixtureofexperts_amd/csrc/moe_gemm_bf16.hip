@@ -18,11 +18,13 @@
 // the epilogue: s[n] * sum_k a[k] q[n][k] = sum_k a[k] (s[n] q[n][k]).
 //
 // Work list.  The device-side scan writes tile_start[e] = sum over e' < e of
-// ceil(count_e' / BM).  Work item id is ordered expert-major, then n-tile (and
-// K range), then m-tile, so consecutive items share one weight tile.
-// Workgroups are dealt round-robin to the 8 XCDs, so item ids are assigned in
-// contiguous per-XCD ranges: the blocks that share a weight tile and walk K in
-// step run behind the same L2.
+// ceil(count_e' / BM).  Work item id is ordered expert-major, then blocks of
+// kMBlock M tiles, then n-tile, then M tile (the up GEMM on 256-row tiles:
+// pairs of n-tiles with a paired last M tile; split items: K range), so
+// consecutive items share one weight tile and a block's rows serve its
+// n-tiles.  Workgroups are dealt round-robin to the 8 XCDs, so item ids are
+// assigned in contiguous per-XCD ranges: the blocks that share a weight tile
+// and walk K in step run behind the same L2.
 //
 // Block: 4 waves, one per SIMD, as 2 (M) x 2 (N); each wave owns a (BM/2) x 128
 // sub-tile and interleaves its MFMAs with the fragment reads of the next

@@ -218,8 +218,8 @@ struct PermuteArgs {
 // for 128-row tiles); the rem = W mod ncu items of the last, partial round
 // are each split into S K ranges (the largest S <= smax with S dividing the K
 // stages and rem * S <= ncu), so that round is as long as 1/S of a tile.
-// Items are numbered expert-major, then n-tile, then m-tile; items >= nfull
-// are split.  Down GEMM: K range 0 of a split tile writes y, range r >= 1
+// Items are numbered in the work list's order (expert-major); items >=
+// nfull are split.  Down GEMM: K range 0 of a split tile writes y, range r >= 1
 // writes its partial to split_ws block j (S - 1) + r - 1 (j = tile - nfull; a
 // block is BM x 256 fp32, row stride 256); fold_split_kernel then adds them
 // to y in range order.  With a bf16 y every K range r of a split tile writes
