@@ -318,6 +318,11 @@ def main():
                     help="after the timed region, run one plain device copy of MIB MiB (fp32 multiply by 1, "
                          "read MIB and write MIB): the reference kernel that scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings to bytes")
+    ap.add_argument("--copy-rates", default="", metavar="MB,MB,...",
+                    help="after the timed region, plain device copies moving each listed number of MB in "
+                         "total (half read, half written), 10 launches per size, each as an elementwise "
+                         "kernel (torch.mul by 1) and as the runtime's device-to-device copy; their kernel-"
+                         "trace durations are the copy rate the memory-bound stages are compared with")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -430,6 +435,20 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    if args.copy_rates:
+        for mb in [float(v) for v in args.copy_rates.split(",") if v]:
+            n = int(mb * 1e6 / 2) // 4  # fp32 elements per buffer
+            src = torch.ones(n, dtype=torch.float32, device="cuda")
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            for _ in range(10):
+                torch.mul(src, 1.0, out=dst)
+            for _ in range(10):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            print(f"copy rates: {mb} MB done ({n * 4} B per buffer)", file=sys.stderr, flush=True)
+            del src, dst
+
     ms_step = elapsed * 1000.0 / args.steps
     tokens_s = T * args.steps / elapsed
     kt = wl["kt"]
@@ -442,11 +461,13 @@ def main():
     down_tflops = down_flops / (stage_ms["expert_down"] * 1e-3) / 1e12
     xs = 2 if cfg["w"] != "f32" else 4
     # algorithmic HBM bytes of the memory-bound stages (per launch): read x,
-    # the router weight; write indices + gates, per-token logsumexp and probs;
-    # permute reads x and writes the k expert-ordered copies; combine reads the
-    # k expert outputs (bf16 on the bf16/fp8-weight paths, else fp32) with
-    # their (position, gate) and writes fp32 out
-    router_bytes = T * D * xs + E * D * 4 + T * kt * (4 + 4) + T * 4 + E * T * 4
+    # the router weight; write indices + gates and the per-token logsumexp
+    # (the [T][E] probabilities are written only when a caller asks for them,
+    # which the bench does not); permute reads x and writes the k
+    # expert-ordered copies; combine reads the k expert outputs (bf16 on the
+    # bf16/fp8-weight paths, else fp32) with their (position, gate) and
+    # writes fp32 out
+    router_bytes = T * D * xs + E * D * 4 + T * kt * (4 + 4) + T * 4
     permute_bytes = T * D * xs + rows * D * xs
     combine_bytes = rows * D * xs + rows * 8 + T * D * 4
     gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
@@ -492,6 +513,9 @@ def main():
         },
         "stages_steady": {
             "reps": reps,
+            "note": "cache-warm: each stage relaunched back to back on the same buffers, so its working set "
+                    "(33-340 MB) is largely served from the 256 MB Infinity Cache; launch-overhead evidence, "
+                    "not HBM bandwidth (the HBM figures are the kernel traces under profiles/)",
             "router": {"ms": round(steady_ms["router"], 4), "GB/s": round(gbs(router_bytes, steady_ms["router"]), 1)},
             "permute": {"ms": round(steady_ms["permute"], 4),
                         "GB/s": round(gbs(permute_bytes, steady_ms["permute"]), 1)},

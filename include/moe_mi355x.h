@@ -21,8 +21,11 @@
  *  - Calls on one handle are serialised by the library, across streams too
  *    (a call on another stream than the previous async call's waits for that
  *    call's work); distinct handles may be used from distinct threads.  The
- *    stream of an async call must stay valid until the next call on the
- *    handle, or moe_destroy, has returned.
+ *    async calls that complete a layer (moe_forward_async, moe_decode_async,
+ *    moe_stage_combine_async) mark their end with an event of the handle:
+ *    their stream may be destroyed as soon as they return.  The stream of
+ *    one of the other stage calls must stay valid until the next call on the
+ *    handle has returned.  moe_destroy never uses a caller's stream.
  */
 #ifndef MOE_MI355X_H
 #define MOE_MI355X_H
@@ -164,8 +167,9 @@ int moe_set_router_noise(moe_handle *h, float noise_scale, const float *noise_we
 
 /* StandardExpert's Dropout(p) in training -- src/experts/standard.jl:26,
  * 49-51: in training calls each element of h = act(W1 x .+ b1) is kept,
- * times Float32(1 / (1 - p)), with probability 1 - p (a uniform draw > p),
- * else zeroed, before W2.  Draws: the library's counter-based generator
+ * times 1 / (1 - p) in Float32 arithmetic (1 - p rounded, then the quotient,
+ * as NNlib's dropout computes it for a Float32 p), with probability 1 - p (a
+ * uniform draw > p), else zeroed, before W2.  Draws: the library's counter-based generator
  * (seed, the handle's training-call number, expert-ordered row, column),
  * not Julia's stream.  p = 0 turns it off; StandardExpert handles only. */
 int moe_set_expert_dropout(moe_handle *h, float p, uint64_t seed);

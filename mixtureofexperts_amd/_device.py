@@ -4,6 +4,7 @@ All array arguments are host numpy arrays in the ABI's token-major memory
 order (a Julia (D, T) matrix is passed as its (T, D) row-major memory).
 """
 import ctypes
+import sys
 from collections import namedtuple
 
 import numpy as np
@@ -63,6 +64,11 @@ class DeviceLayer:
             self.h = None
 
     def __del__(self):
+        # At interpreter shutdown the HIP runtime, torch's streams and this
+        # module's globals may already be torn down: the process is ending,
+        # its device memory goes with it, so no device call is made then.
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:

@@ -18,6 +18,13 @@ using namespace moe;
 namespace {
 thread_local std::string g_create_error;
 inline long long round_up(long long v, long long m) { return (v + m - 1) / m * m; }
+// Dropout's scale of the kept values, 1 / (1 - p), rounded as Float32
+// arithmetic rounds it: 1 - p, then the quotient (NNlib's dropout on a
+// Float32 p; src/experts/standard.jl:49-51).
+float drop_scale_f32(float p) {
+    volatile float q = 1.0f - p;  // one rounding, not fused into the division
+    return 1.0f / q;
+}
 }  // namespace
 
 struct moe_handle {
@@ -39,13 +46,19 @@ struct moe_handle {
     hipStream_t stream = nullptr;
     // Calls on one handle share its workspace and weights.  The last call
     // that enqueued work without waiting for it did so on last_stream
-    // (pending); a call on another stream first records `done` on
-    // last_stream (after that work) and makes its own stream wait for it.
-    // Nothing is recorded between calls on one stream: a marker between two
-    // kernels costs ~5 us of GPU time, at every stage boundary.
+    // (pending).  Calls that complete a layer (moe_forward_async,
+    // moe_decode_async, moe_stage_combine_async) record `done` on their
+    // stream after their work (done_rec): a later call on another stream
+    // only waits for it, and moe_destroy synchronises on it, so neither
+    // touches a caller stream that may be gone by then.  Between the other
+    // stage calls nothing is recorded (a marker between two kernels costs
+    // ~5 us of GPU time, at every stage boundary): a call on another stream
+    // first records `done` on last_stream, which the caller keeps valid
+    // until that next call.
     hipEvent_t done = nullptr;
     hipStream_t last_stream = nullptr;
     bool pending = false;
+    bool done_rec = false;
     std::mutex mu;
     std::string err;
 
@@ -158,22 +171,36 @@ static void free_all(moe_handle *h) {
 // another stream.
 static int join_stream(moe_handle *h, hipStream_t s) {
     if (h->pending && h->last_stream != s) {
-        hipError_t e = hipEventRecord(h->done, h->last_stream);
-        if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
+        hipError_t e = hipSuccess;
+        if (!h->done_rec) {
+            e = hipEventRecord(h->done, h->last_stream);
+            if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
+            h->done_rec = true;
+        }
         e = hipStreamWaitEvent(s, h->done, 0);
         if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipStreamWaitEvent: ") + hipGetErrorString(e));
     }
     return MOE_OK;
 }
-// After a call has enqueued its work on s (and not waited for it).
-static int mark_stream(moe_handle *h, hipStream_t s) {
+// After a call has enqueued its work on s (and not waited for it); a call
+// that completes a layer (record) marks its end with `done`.
+static int mark_stream(moe_handle *h, hipStream_t s, bool record = false) {
     h->last_stream = s;
     h->pending = true;
+    h->done_rec = false;
+    if (record) {
+        const hipError_t e = hipEventRecord(h->done, s);
+        if (e != hipSuccess) return fail(h, MOE_EHIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
+        h->done_rec = true;
+    }
     return MOE_OK;
 }
 // After a call that joined and then synchronised its stream: nothing of the
 // handle is in flight.
-static void settle(moe_handle *h) { h->pending = false; }
+static void settle(moe_handle *h) {
+    h->pending = false;
+    h->done_rec = false;
+}
 
 // ExpertChoiceGating capacity ceil(Int, T * capacity_factor / E) in Float32
 // (src/gating/expert_choice.jl:13), saturated at INT_MAX.
@@ -613,9 +640,10 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     ra.k = h->k; ra.ns = h->ns; ra.kt = h->kc; ra.probs = h->probs; ra.idx = h->idx; ra.gates = h->gates;
     ra.soft_lambda = h->cfg.gate_param; ra.given = h->given; ra.given_probs = h->given_probs;
     // the call's super-block totals (parity rpar); the router zeroes the
-    // other parity's for the next call
+    // other parity's for the next call.  rpar flips once the router kernel
+    // is launched: a call that fails before that leaves the next one on the
+    // same (still clear) parity.
     const int par = h->rpar;
-    h->rpar ^= 1;
     ra.rank = h->rank; ra.blk_counts = h->blk_counts; ra.ldc = h->ldc; ra.blk_zh = h->blk_zh;
     ra.lse = h->lse;
     h->last_route_T = T;
@@ -652,7 +680,18 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
         ra.out_mask = ec ? ROUTE_OUT_PROBS : (ROUTE_OUT_PROBS | ROUTE_OUT_GATING);
     }
     A.ncu = h->ncu;
-    HIP_TRY(h, launch_router(A, &h->rb, s));
+    {
+        const hipError_t e = launch_router(A, &h->rb, s);
+        if (e != hipSuccess) {
+            // whether the kernel ran is unknown (a launch error may come from
+            // earlier work): clear both parities' totals so that no later
+            // call adds onto stale counts
+            (void)hipMemsetAsync(h->sup_cnt2, 0, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc, s);
+            (void)hipMemsetAsync(h->sup_p2, 0, sizeof(unsigned long long) * 2 * (size_t)h->nsup_max * h->ldc, s);
+            return fail(h, MOE_EHIP, std::string("launch_router: ") + hipGetErrorString(e));
+        }
+    }
+    h->rpar = par ^ 1;
     if (ec) {
         // the experts' choices give the slots, the stable ranks and the
         // per-block histogram
@@ -673,7 +712,9 @@ static GemmArgs up_args(moe_handle *h, int mt_grid, bool training) {
         // Dropout(p) on h in training (src/experts/standard.jl:49-51), one
         // stream of the generator per call
         g.drop_p = h->drop_p;
-        g.drop_scale = (float)(1.0 / (1.0 - (double)h->drop_p));
+        // 1 / (1 - p) in Float32 arithmetic, as NNlib's dropout computes it
+        // for the Float32 p of StandardExpert's Dropout (two fp32 roundings)
+        g.drop_scale = drop_scale_f32(h->drop_p);
         g.drop_seed = h->drop_seed;
         g.drop_call = h->drop_calls++;
     }
@@ -1004,7 +1045,13 @@ int moe_destroy(moe_handle *h) {
     if (!h) return MOE_OK;
     {
         std::lock_guard<std::mutex> lk(h->mu);
-        if (h->pending && hipEventRecord(h->done, h->last_stream) == hipSuccess) (void)hipEventSynchronize(h->done);
+        // the handle's last work: up to `done` when a layer-completing call
+        // recorded it; after a bare stage call, everything on the device (its
+        // stream is not used here: it may be gone, e.g. from a finalizer)
+        if (h->pending) {
+            if (h->done_rec) (void)hipEventSynchronize(h->done);
+            else (void)hipDeviceSynchronize();
+        }
         if (h->stream) (void)hipStreamSynchronize(h->stream);
         free_all(h);
         if (h->done) (void)hipEventDestroy(h->done);
@@ -1618,7 +1665,7 @@ int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_d
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     r = join_stream(h, s);
     if (r == MOE_OK) r = decode_locked(h, xb_dev, n, out_dev, s);
-    if (r == MOE_OK) r = mark_stream(h, s);
+    if (r == MOE_OK) r = mark_stream(h, s, true);
     return r;
 }
 
@@ -1629,7 +1676,7 @@ int moe_forward_async(moe_handle *h, const void *x_dev, int32_t x_dtype, int32_t
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     int r = join_stream(h, s);
     if (r == MOE_OK) r = forward_locked(h, x_dev, x_dtype, T, training, out_dev, loss_dev, s);
-    if (r == MOE_OK) r = mark_stream(h, s);
+    if (r == MOE_OK) r = mark_stream(h, s, true);
     return r;
 }
 
@@ -1697,7 +1744,7 @@ int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stre
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     r = join_stream(h, s);
     if (r == MOE_OK) r = run_combine(h, T, out_dev, s);
-    if (r == MOE_OK) r = mark_stream(h, s);
+    if (r == MOE_OK) r = mark_stream(h, s, true);
     return r;
 }
 

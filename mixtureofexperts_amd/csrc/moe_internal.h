@@ -13,7 +13,12 @@ constexpr int kRtMinBlock = 16;    // fewest tokens per router_kernel workgroup
 constexpr int kPermThreads = 1024; // threads per permute workgroup: one wave per token
 constexpr int kPermTokens = kPermThreads / 64;  // tokens per permute workgroup (divides every route block)
 constexpr int kSuper = 16;         // route blocks per super block (rank bases: super rows, then block rows)
-constexpr double kPsumScale = 281474976710656.0;  // 2^48: fixed-point scale of the probability sums
+// Fixed-point scale of the per-expert probability sums (2^32).  A call's
+// total for one expert is at most T * 2^32 < 2^63 for every T the handle
+// accepts (max_tokens * slots <= INT_MAX / 2), so the unsigned 64-bit totals
+// cannot wrap; each route block's sum is rounded once, by at most 2^-33, far
+// below one fp32 ulp of the mean probability.
+constexpr double kPsumScale = 4294967296.0;
 constexpr int kGemmBM = 128;       // fp32 / fp8-weight grouped-GEMM tile rows (token rows)
 constexpr int kGemmBN = 128;       // fp32 / fp8-weight grouped-GEMM tile columns
 constexpr int kKPad = 64;          // K padding of packed weights and activation rows

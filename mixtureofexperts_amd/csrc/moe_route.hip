@@ -712,7 +712,7 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         if (out_probs && e < E) {
             // per-row probability sums (Switch loss P_e): fp64 over the route
             // block's tokens in token order, added to the super block's sum
-            // in fixed point (scale 2^48, at most 2^54 per route block)
+            // in fixed point (kPsumScale = 2^32, at most 2^38 per route block)
             double ps = 0.0;
 #pragma unroll 8
             for (int i = 0; i < ntok; ++i) ps += (double)Pr[i * RW + e];

@@ -122,6 +122,7 @@ class MoELayer:
             "capacity_overflow": 0,
         }
         self._dev = None
+        self._noise_error = None  # router noise the device refused (raised by training calls)
 
     # ---- device state ----------------------------------------------------
     def _new_device(self):
@@ -144,10 +145,19 @@ class MoELayer:
         """(Re)build the device handle and upload router and expert weights."""
         self._dev = self._new_device()
         self._dev.set_router(np.ascontiguousarray(self.router.weight.T), self.router.bias)
+        self._noise_error = None
         if self.router.noise_scale > 0:
             nw = self.router.noise_weight if self.router.use_noise_network else None
-            self._dev.set_router_noise(self.router.noise_scale,
-                                       None if nw is None else np.ascontiguousarray(nw.T), self.router.noise_seed)
+            try:
+                self._dev.set_router_noise(self.router.noise_scale,
+                                           None if nw is None else np.ascontiguousarray(nw.T), self.router.noise_seed)
+            except _lib.MoeError as err:
+                # the noise only enters training calls (router.jl:32): a
+                # router whose noise has no device path still runs inference,
+                # and its training calls raise this error
+                if err.status != _lib.MOE_EUNSUPPORTED:
+                    raise
+                self._noise_error = err
         for e, ex in enumerate(self.experts):
             ex.upload(self._dev, e)
         p = max([getattr(ex, "dropout", 0.0) for ex in self.experts] + [0.0])
@@ -187,6 +197,8 @@ class MoELayer:
             xt = np.ascontiguousarray(xa.T, dtype=np.float32)
             xcode = _lib.MOE_F32
         dev = self._dev if self._dev is not None else self.sync_weights()
+        if training and self._noise_error is not None:
+            raise self._noise_error
         aux_free = self.balance_loss if isinstance(self.balance_loss, AuxiliaryFreeLoss) else None
         if aux_free is not None:
             dev.set_aux_free(aux_free)

@@ -194,8 +194,9 @@ def test_stories42m_moe_decode_chain(moe, oracle):
     # against oracle.decode_ffn on the GPU's logits with the experts read back
     # from the device: routing and gates bit-exact, output within 1e-4; the
     # chain's final output also against the oracle run end to end on its own.
+    # 256 tokens: the decode length of BASELINE config 2.
     rng = np.random.default_rng(42)
-    dim, hid, E, n_tok = 512, 1376, 8, 48
+    dim, hid, E, n_tok = 512, 1376, 8, 256
     layers, host = [], []
     try:
         for li in range(3):
@@ -213,7 +214,7 @@ def test_stories42m_moe_decode_chain(moe, oracle):
         final = np.zeros((n_tok, dim), np.float32)
         usage = np.zeros((3, E), np.int64)
         for t in range(n_tok):
-            print(f"decode chain token {t}", flush=True) if t % 16 == 0 else None
+            print(f"decode chain token {t}", flush=True) if t % 64 == 0 else None
             v = x[t:t + 1]
             for li, layer in enumerate(layers):
                 out, logits, idx, gates = layer._dev.decode(np.ascontiguousarray(v))

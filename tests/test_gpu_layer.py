@@ -24,7 +24,7 @@ class Case:
 
     def __init__(self, moe, oracle, *, T, D, H, Dout=None, E, k, gate="topk", ns=0, expert_type="gated", act="silu",
                  wdtype="f32", xdtype="f32", seed=0, router_bias=None, alpha=0.01, z=0.001, drop=False, cf=1.25,
-                 max_tokens=None, wscale=None, lsh=0):
+                 max_tokens=None, wscale=None, lsh=0, init="he"):
         from mixtureofexperts_amd import _lib
         from mixtureofexperts_amd._device import DeviceLayer, GateSpec
 
@@ -43,14 +43,23 @@ class Case:
         else:
             self.x_dev = self.x = x
             self.xcode = _lib.MOE_F32
-        self.wr = (rng.standard_normal((E - lsh, D)) * (1.0 / np.sqrt(D))).astype(np.float32)
+        # init "he": experts ~ N(0, 2 / fan_in) as GatedExpert's randn * sqrt(2 / D)
+        # (src/experts/gated.jl:16-24), router 1 / sqrt(D); "glorot": Glorot
+        # normal, N(0, 2 / (fan_in + fan_out)) for every matrix
+        if init == "glorot":
+            s_r, s_in, s_h = np.sqrt(2.0 / (D + E - lsh)), np.sqrt(2.0 / (D + H)), np.sqrt(2.0 / (H + Dout))
+            s_w2 = s_h
+        else:
+            s_r = 1.0 / np.sqrt(D)
+            s_in = np.sqrt(2.0 / D) if wscale is None else wscale
+            s_h = np.sqrt(2.0 / H) if wscale is None else wscale
+            s_w2 = s_in if expert_type == "gated" else s_h
+        self.wr = (rng.standard_normal((E - lsh, D)) * s_r).astype(np.float32)
         self.rb = router_bias
-        s_in = np.sqrt(2.0 / D) if wscale is None else wscale
-        s_h = np.sqrt(2.0 / H) if wscale is None else wscale
         self.ex, dev_ex = [], []
         for _ in range(E):
             w1 = (rng.standard_normal((H, D)) * s_in).astype(np.float32)
-            w2 = (rng.standard_normal((Dout, H)) * (s_in if expert_type == "gated" else s_h)).astype(np.float32)
+            w2 = (rng.standard_normal((Dout, H)) * s_w2).astype(np.float32)
             w3 = (rng.standard_normal((H, D)) * s_in).astype(np.float32) if expert_type == "gated" else None
             b1 = (rng.standard_normal(H) * 0.1).astype(np.float32) if expert_type != "gated" else None
             b2 = (rng.standard_normal(Dout) * 0.1).astype(np.float32) if expert_type != "gated" else None
@@ -346,8 +355,9 @@ def test_host_routed_gates_layer(moe, oracle):
 
 def test_readme_config_fp32(moe, oracle):
     # README MoELayer, 8 gated silu experts, 512/2048/512,
-    # TopKGating(2), SwitchTransformerLoss(0.01), x randn(512, 32), fp32
-    c = Case(moe, oracle, T=32, D=512, H=2048, E=8, k=2, wdtype="f32", seed=1)
+    # TopKGating(2), SwitchTransformerLoss(0.01), x randn(512, 32), fp32,
+    # weights Glorot-normal from a fixed seed
+    c = Case(moe, oracle, T=32, D=512, H=2048, E=8, k=2, wdtype="f32", seed=1, init="glorot")
     check_case(c, TOL["f32"], training=True)
     check_case(c, TOL["f32"], training=False)
 
@@ -607,3 +617,43 @@ def test_router_lse(moe, oracle):
 
     with pytest.raises(_lib.MoeError):
         case.dev.router_lse(case.T - 1)
+
+
+@pytest.mark.parametrize("T", [65536, 131072])
+def test_switch_loss_large_batch(moe, oracle, T):
+    """The Switch loss at large batches (src/balancing/losses.jl:15-36,
+    src/core/moe_layer.jl:151): a router bias makes expert 1 dominant (mean
+    probability ~0.8), so at T = 131072 its per-call probability mass passes
+    2^16.  The fused loss (the router's fixed-point
+    probability sums, totalled in the permute's scan) and the mean entropy
+    are checked within 1e-5 against the oracle on the GPU's indices and
+    probabilities, and routing bit-exact through check_case."""
+    bias = np.zeros(8, np.float32)
+    bias[0] = 4.0
+    c = Case(moe, oracle, T=T, D=64, H=64, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=131, router_bias=bias)
+    try:
+        out, loss, res = c.run(training=True)
+        p_mean = float(res["probs"][:, 0].astype(np.float64).mean())
+        assert p_mean > 0.75, p_mean
+        if T > 65536:
+            assert p_mean * T > 65536  # the mass a 2^48 fixed-point total would wrap on
+        sw = oracle.switch_loss(res["indices"], res["probs"], c.alpha)
+        assert abs(res["switch_loss"] - sw) <= 1e-5 * max(1.0, abs(float(sw))), (res["switch_loss"], sw)
+        ent = oracle.mean_entropy(res["probs"])
+        assert abs(res["mean_entropy"] - ent) <= 1e-5 * max(1.0, abs(float(ent))), (res["mean_entropy"], ent)
+        check_case(c, TOL["bf16"])
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("E,ns", [(10, 1), (11, 3)])
+def test_shared_expert_gating_inexact_scales(moe, oracle, E, ns):
+    """A layer with SharedExpertGating(ns, TopKGating(2), E): the routed gate
+    scale 1 - ns/(ns + 2) (2/3, 2/5) and probability scale 1 - ns/E in
+    Float64 (src/gating/advanced.jl:95-105), bit-exact through check_case."""
+    c = Case(moe, oracle, T=1200, D=128, H=192, E=E, k=2, gate="shared", ns=ns, wdtype="bf16", xdtype="bf16",
+             seed=300 + E)
+    try:
+        check_case(c, TOL["bf16"])
+    finally:
+        c.dev.close()

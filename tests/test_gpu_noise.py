@@ -104,17 +104,19 @@ def test_layer_router_noise_python_api(moe):
     layer.close()
 
 
-@pytest.mark.parametrize("wdtype", ["f32", "bf16"])
-def test_standard_expert_dropout(moe, oracle, wdtype):
+@pytest.mark.parametrize("wdtype,p", [("f32", 0.25), ("bf16", 0.25), ("f32", 0.15)])
+def test_standard_expert_dropout(moe, oracle, wdtype, p):
     """StandardExpert's Dropout(p) in training (src/experts/standard.jl:49-51):
     with W1 = W2 = I, zero biases, the identity activation and k = 1 (gate
-    exactly 1) the layer output is dropout(x): every element is 0 or x *
-    Float32(1 / (1 - p)) (fp32: exactly; bf16: x and h rounded to bf16), the
-    zeros are a fraction p of the elements, and inference calls keep x."""
+    exactly 1) the layer output is dropout(x): every element is 0 or x times
+    the scale 1 / (1 - p) in Float32 arithmetic, as NNlib computes it for the
+    Float32 p (fp32: exactly; bf16: x and h rounded to bf16), the zeros are a
+    fraction p of the elements, and inference calls keep x.  At p = 0.15 that
+    scale is 1 ulp below Float32(1 / (1 - p)) computed in Float64."""
     from mixtureofexperts_amd import _lib
     from mixtureofexperts_amd._device import DeviceLayer, GateSpec
 
-    T, D, E, p = 512, 64, 4, 0.25
+    T, D, E = 512, 64, 4
     rng = np.random.default_rng(31)
     x = rng.standard_normal((T, D)).astype(np.float32)
     if wdtype == "bf16":
@@ -133,7 +135,10 @@ def test_standard_expert_dropout(moe, oracle, wdtype):
     y_inf, _, _ = dev.forward(x, _lib.MOE_F32, False)
     assert np.array_equal(y_inf, x)
     y, _, _ = dev.forward(x, _lib.MOE_F32, True)
-    scale = np.float32(1.0 / (1.0 - p))
+    p32 = np.float32(p)
+    scale = np.float32(1) / (np.float32(1) - p32)
+    if p == 0.15:
+        assert scale != np.float32(1.0 / (1.0 - float(p32)))  # the case tells the two roundings apart
     kept = (x * scale).astype(np.float32)
     if wdtype == "bf16":
         kept = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(kept))
@@ -163,3 +168,30 @@ def test_layer_expert_dropout_python_api(moe):
     y2, _ = layer(x, training=False)
     assert np.array_equal(y0, y2) and not np.array_equal(y0, y1)
     layer.close()
+
+
+def test_noise_network_many_experts_inference(moe):
+    """A noise network on a router of more than 64 outputs has no device path
+    (its noise logits would be GEMM columns E .. 2E - 1 past MOE_MAX_EXPERTS).
+    The noise only enters training calls (src/core/router.jl:32), so such a
+    layer still runs inference, bit-identical to the same layer without
+    noise; its training calls raise MOE_EUNSUPPORTED."""
+    from mixtureofexperts_amd import _lib
+
+    E, D, H, T = 128, 64, 128, 512
+    cfg = moe.MoEConfig(num_experts=E, expert_type="standard", input_dim=D, hidden_dim=H, output_dim=D,
+                        gate_type=moe.SwitchGating(), noise_scale=0.2, use_noise_network=True, max_tokens=T,
+                        weight_dtype="bf16")
+    noisy = moe.MoELayer(cfg, rng=np.random.default_rng(41))
+    plain_router = moe.Router(D, E, noisy.router.gate_type, weight=noisy.router.weight)
+    plain_cfg = moe.MoEConfig(**{**cfg.__dict__, "noise_scale": 0.0, "use_noise_network": False})
+    plain = moe.MoELayer(plain_cfg, experts=noisy.experts, router=plain_router)
+    x = np.random.default_rng(42).standard_normal((D, T)).astype(np.float32)
+    y0, l0 = noisy(x, training=False)
+    y1, l1 = plain(x, training=False)
+    assert np.array_equal(y0, y1) and l0 == l1 == 0.0
+    with pytest.raises(_lib.MoeError) as err:
+        noisy(x, training=True)
+    assert err.value.status == _lib.MOE_EUNSUPPORTED
+    noisy.close()
+    plain.close()

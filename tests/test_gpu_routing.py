@@ -283,3 +283,23 @@ def test_host_routed_gates(moe):
     idx, gates, _ = moe.compute_gates(moe.RandomGating(4, rng=np.random.default_rng(1)), np.zeros((6, 200), np.float32))
     assert idx.shape == (4, 200) and idx.min() >= 1 and idx.max() <= 6
     assert all(len(set(idx[:, i])) == 4 for i in range(200))
+
+
+@pytest.mark.parametrize("E,ns,k", [(10, 1, 2), (11, 3, 2)])
+def test_shared_gating_inexact_scales(moe, oracle, E, ns, k):
+    """SharedExpertGating(ns, TopKGating(k), E) with scales that are not
+    exact in binary: the routed gates times 1 - ns/total_k (2/3 for ns = 1,
+    2/5 for ns = 3) and the routed probabilities times 1 - ns/E (9/10, 8/11),
+    both computed in Float64 as Julia promotes `1.0f0 - Int/Int`
+    (src/gating/advanced.jl:95-105) and rounded once.  Bit-exact against the
+    oracle; the case also shows that a Float32 scale would round some gates
+    differently, so a Float32 restatement could not pass it."""
+    rng = np.random.default_rng(E * 10 + ns)
+    lg = rng.standard_normal((4096, E)).astype(np.float32)
+    check_route(moe, oracle, lg, "shared", k, ns)
+    # the case tells the Float64 scale from a Float32 one
+    _, g, _ = oracle.compute_gates_topk(lg[:, ns:], k)
+    s64 = 1.0 - ns / (ns + k)
+    f64 = (g.astype(np.float64) * s64).astype(np.float32)
+    f32 = g * np.float32(s64)
+    assert np.count_nonzero(f64 != f32) > 0
