@@ -262,6 +262,7 @@ struct CombineArgs {
     int T, D, kt;
     int lsh;                     // > 0: out = 0.5 * sum(y_shared / lsh) + 0.5 * routed
     float *out;                  // [T][D]
+    int u, nchunk;               // set by launch_combine: 4-column groups per lane, column chunks per token
 };
 
 struct GemmArgs {

@@ -1027,10 +1027,10 @@ __device__ inline void aux_free_step(const int *cnt, long long total, int E, flo
 // capacity, the expert counts after capacity (from the call's totals), their
 // offsets and GEMM tile starts (exclusive prefixes over the experts), and the
 // route block's rank bases (the counts of the route blocks before it, summed
-// with integer LDS atomics).  Workgroup 0 also writes the offsets, counts,
-// tile starts, the (expert, m0) GEMM tile list and the capacity, computes the
-// Switch and z losses and the mean entropy, and runs the AuxiliaryFreeLoss
-// step.  Ends with a barrier.
+// with integer LDS atomics).  The writer (workgroup 0) also writes the
+// offsets, counts, tile starts, the (expert, m0) GEMM tile
+// list and the capacity, computes the Switch and z losses and the mean
+// entropy, and runs the AuxiliaryFreeLoss step.  Ends with a barrier.
 struct ScanLds {
     int cnt[MOE_MAX_EXPERTS];
     int base[MOE_MAX_EXPERTS];
@@ -1044,10 +1044,9 @@ struct ScanLds {
     float lsum;
 };
 
-__device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &L) {
+__device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &L, bool writer) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x, nth = blockDim.x;
-    const bool writer = blk == 0;
     if (tid == 0) {
         int cap = INT_MAX;
         if (a.training && a.drop) {
@@ -1275,7 +1274,7 @@ __device__ __forceinline__ void store_row_chunk(const PermuteArgs &a, int row, i
 // every position it owns, converting to the GEMM type.
 // ============================================================================
 // bf16 rows into the bf16 tile image: UB 16-byte chunks per lane per batch
-// (UB * 512 columns, the smallest power of two covering D up to 4096, so that
+// (UB * 512 columns, the smallest power of two covering D up to 2048, so that
 // few lanes rewrite the row's last chunk), loaded together from clamped
 // in-row addresses, then stored to every position the token holds.
 __device__ __forceinline__ bool permute_bf16_rows(const PermuteArgs &a) {
@@ -1288,20 +1287,36 @@ __device__ __forceinline__ void load_row_chunk(const PermuteArgs &a, int t, int 
     for (int u = 0; u < UB; ++u) v[u] = *(const u32x4_t *)(src + min(d0 + u * 512 + lane * 8, a.D - 8));
 }
 
-// pre: the row's first batch, already loaded by the caller when have_pre
-template <int UB>
-__device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int lane, const ScanLds &L,
-                                              const u32x4_t (&pre)[UB], bool have_pre) {
+// The entry of lane j < kt of a token (its expert id, gate and rank inside
+// the route block), loaded ahead of the scan that gives its position.
+struct EntryMeta {
+    int e, rk;
+    float g;
+};
+__device__ __forceinline__ EntryMeta load_meta(const PermuteArgs &a, int t, int lane) {
+    EntryMeta m{0, 0, 0.0f};
+    if (t >= 0 && lane < a.kt) {
+        const long long ent = (long long)t * a.kt + lane;
+        m.e = a.idx[ent];
+        m.g = a.gates[ent];
+        m.rk = a.rank[ent];
+    }
+    return m;
+}
+
+// A token's entries after the scan: capacity drop and renormalisation,
+// positions (pos_of, perm, gate_sorted); returns the xp row of lane j's entry
+// j (< 0: none).
+__device__ __forceinline__ int permute_entries(const PermuteArgs &a, int t, int lane, const ScanLds &L, EntryMeta m) {
 #pragma clang fp contract(off)
     const int cap = L.cap;
     int e = 0, pos = -1, row = -1;  // position in expert order; xp row (tile image row when tiled)
     float g = 0.0f;
     if (lane < a.kt) {
-        const long long ent = (long long)t * a.kt + lane;
-        e = a.idx[ent];
-        g = a.gates[ent];
+        e = m.e;
+        g = m.g;
         if (e > 0 && e <= a.E) {
-            const int rk = L.base[e - 1] + a.rank[ent];
+            const int rk = L.base[e - 1] + m.rk;
             if (rk < cap) {
                 pos = L.off[e - 1] + rk;
                 row = a.tiled ? L.tstart[e - 1] * a.bm + rk : pos;
@@ -1329,17 +1344,27 @@ __device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int l
             a.gate_sorted[pos] = g;
         }
     }
-    if (!a.copy_rows) return;
+    return row;
+}
+
+// The token's row into every xp row it owns, converting to the GEMM type.
+// bf16 rows: `first` holds the row's first batch (loaded by the caller);
+// each further batch is loaded before the previous one is stored.
+template <int UB>
+__device__ __forceinline__ void permute_copy(const PermuteArgs &a, int t, int lane, int row,
+                                             const u32x4_t (&first)[UB]) {
     if (permute_bf16_rows(a)) {
-        for (int d0 = 0; d0 < a.D; d0 += 512 * UB) {
-            u32x4_t v[UB];
-            if (d0 == 0 && have_pre) {
+        u32x4_t cur[UB];
 #pragma unroll
-                for (int u = 0; u < UB; ++u) v[u] = pre[u];
-            } else {
-                load_row_chunk<UB>(a, t, d0, lane, v);
-            }
-            store_row_chunk<UB>(a, row, d0, lane, v);
+        for (int u = 0; u < UB; ++u) cur[u] = first[u];
+        for (int d0 = 0;; d0 += 512 * UB) {
+            const bool more = d0 + 512 * UB < a.D;
+            u32x4_t nx[UB];
+            if (more) load_row_chunk<UB>(a, t, d0 + 512 * UB, lane, nx);
+            store_row_chunk<UB>(a, row, d0, lane, cur);
+            if (!more) break;
+#pragma unroll
+            for (int u = 0; u < UB; ++u) cur[u] = nx[u];
         }
         return;
     }
@@ -1392,21 +1417,43 @@ __device__ __forceinline__ void permute_token(const PermuteArgs &a, int t, int l
 }
 
 // Workgroup w takes the tpw tokens [w tpw, w tpw + tpw) of one route block,
-// a wave per token in turn, after that route block's scan.  Each wave loads
-// the first batch of its first token's row before the scan (the loads do not
-// depend on it), so their latency overlaps the scan's; up to 4 chunks per
-// lane (8 would hold 32 registers through the scan and spill).
-template <int UB>
+// a wave per token in turn, after that route block's scan (workgroup 0 is
+// also the scan's writer: a workgroup of its own would not fit beside the
+// others and would run after them).  Each wave loads its first token's
+// entries and first row batch before the scan (they do not depend on it), so
+// their latency overlaps the scan's.  Batches are at most 4 chunks per lane
+// (2048 columns): a row of 8 chunks held through the scan exceeds the 128
+// registers of a 1024-thread workgroup.  Then the loads that the next stores
+// need are in flight before the current stores: rows of one batch (PIPE) the
+// next token's entries and first batch; longer rows (one token per wave at
+// the usual sizes) the row's next batch (permute_copy).
+template <int UB, bool PIPE>
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
+    static_assert(UB <= 4, "row batch held through the scan");
     __shared__ ScanLds L;
     const int lane = threadIdx.x & 63;
     const int t1 = min(a.T, (int)(blockIdx.x + 1) * a.tpw);
-    const int tf = blockIdx.x * a.tpw + (threadIdx.x >> 6);
-    u32x4_t pre[UB];
-    const bool have_pre = UB <= 4 && permute_bf16_rows(a) && tf < t1;
-    if (have_pre) load_row_chunk<UB>(a, tf, 0, lane, pre);
-    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
-    for (int t = tf; t < t1; t += kPermThreads / 64) permute_token<UB>(a, t, lane, L, pre, have_pre && t == tf);
+    int t = blockIdx.x * a.tpw + (threadIdx.x >> 6);
+    const bool rows16 = permute_bf16_rows(a);
+    EntryMeta m = load_meta(a, t < t1 ? t : -1, lane);
+    u32x4_t cur[UB];
+    if (rows16 && t < t1) load_row_chunk<UB>(a, t, 0, lane, cur);
+    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L, blockIdx.x == 0);
+    for (; t < t1; t += kPermThreads / 64) {
+        const int tn = t + kPermThreads / 64;
+        const EntryMeta mn = load_meta(a, tn < t1 ? tn : -1, lane);
+        u32x4_t nxt[PIPE ? UB : 1];
+        if (PIPE && rows16 && tn < t1) load_row_chunk<PIPE ? UB : 1>(a, tn, 0, lane, nxt);
+        const int row = permute_entries(a, t, lane, L, m);
+        if (a.copy_rows) permute_copy<UB>(a, t, lane, row, cur);
+        m = mn;
+        if constexpr (PIPE) {
+#pragma unroll
+            for (int u = 0; u < UB; ++u) cur[u] = nxt[u];
+        } else if (rows16 && tn < t1) {
+            load_row_chunk<UB>(a, tn, 0, lane, cur);
+        }
+    }
 }
 
 // Permute for more slots per token than a wave has lanes (ExpertChoiceGating
@@ -1478,7 +1525,7 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
 
 __global__ __launch_bounds__(kPermThreads) void permute_wide_kernel(PermuteArgs a) {
     __shared__ ScanLds L;
-    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L);
+    scan_block(a.s, (int)(((long long)blockIdx.x * a.tpw) / a.rb), L, blockIdx.x == 0);
     const int t1 = min(a.T, (int)(blockIdx.x + 1) * a.tpw);
     for (int t = blockIdx.x * a.tpw + (threadIdx.x >> 6); t < t1; t += kPermThreads / 64)
         permute_wide_token(a, t, threadIdx.x & 63, L);
@@ -1497,10 +1544,10 @@ hipError_t launch_permute(PermuteArgs a, hipStream_t s) {
     while (a.tpw * 2 <= a.rb && a.tpw < 4 * kPermTokens && (a.T + a.tpw - 1) / a.tpw > 512) a.tpw *= 2;
     const int nwg = (a.T + a.tpw - 1) / a.tpw;
     if (a.kt > 64) hipLaunchKernelGGL(permute_wide_kernel, dim3(nwg), dim3(kPermThreads), 0, s, a);
-    else if (a.D >= 4096) hipLaunchKernelGGL(permute_kernel<8>, dim3(nwg), dim3(kPermThreads), 0, s, a);
-    else if (a.D >= 2048) hipLaunchKernelGGL(permute_kernel<4>, dim3(nwg), dim3(kPermThreads), 0, s, a);
-    else if (a.D >= 1024) hipLaunchKernelGGL(permute_kernel<2>, dim3(nwg), dim3(kPermThreads), 0, s, a);
-    else hipLaunchKernelGGL(permute_kernel<1>, dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D > 2048) hipLaunchKernelGGL((permute_kernel<4, false>), dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D > 1024) hipLaunchKernelGGL((permute_kernel<4, true>), dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else if (a.D > 512) hipLaunchKernelGGL((permute_kernel<2, true>), dim3(nwg), dim3(kPermThreads), 0, s, a);
+    else hipLaunchKernelGGL((permute_kernel<1, true>), dim3(nwg), dim3(kPermThreads), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1518,33 +1565,108 @@ hipError_t launch_permute(PermuteArgs a, hipStream_t s) {
 // y is fp32, or bf16 (a.y_bf16) where the down GEMM ran on the bf16 kernel;
 // each term is widened to fp32 before it is scaled and summed.
 //
-// Fast path (every one of the token's KT entries kept, rows 16-byte
-// aligned): the entries are sorted by expert in registers, and all y loads of
-// a chunk of U groups of 4 per lane are issued before any is summed.
+// Fast path (every entry kept, rows 16-byte aligned): the entries are sorted
+// by expert in registers, then the token's columns are walked in chunks of
+// 256 u columns (lane l: columns 4 l .. 4 l + 3 of each group of 256), the
+// loads of chunk c + 1 issued before chunk c is summed and stored.  Every
+// wave then reads and writes at the same time: a wave that first loaded its
+// whole row and only then stored it would leave the HBM with a phase of
+// reads only, then a phase of writes only.  u = 8 / kt groups per chunk (at
+// least 1; lowered to the smallest power of two covering D), so a chunk is
+// kt u loads of 8 bytes (bf16 y) per lane.
 // ============================================================================
+__host__ __device__ constexpr int combine_umax(int kt) { return kt >= 8 ? 1 : 8 / kt; }
+
 template <bool YB>
-__device__ __forceinline__ float4 load_y4(const void *y, long long off) {
-    if (YB) {
-        const uint2 r = *(const uint2 *)((const uint16_t *)y + off);
-        return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
-                           __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+struct YRaw {
+    uint2 v;  // 4 bf16
+    __device__ __forceinline__ void load(const void *y, long long off) { v = *(const uint2 *)((const uint16_t *)y + off); }
+    __device__ __forceinline__ float4 f() const {
+        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
     }
-    return *(const float4 *)((const float *)y + off);
+};
+template <>
+struct YRaw<false> {
+    float4 v;
+    __device__ __forceinline__ void load(const void *y, long long off) { v = *(const float4 *)((const float *)y + off); }
+    __device__ __forceinline__ float4 f() const { return v; }
+};
+
+// pp / gg: positions and gates of the token's KT entries in expert order
+template <int KT, bool BLEND, bool YB>
+__device__ __forceinline__ void combine_fast(const CombineArgs &a, long long t, int lane, const int (&pp)[KT],
+                                             const float (&gg)[KT]) {
+#pragma clang fp contract(off)
+    constexpr int UM = combine_umax(KT);
+    const int cw = 256 * a.u;
+    YRaw<YB> cur[KT][UM], nxt[KT][UM];
+    auto load = [&](YRaw<YB>(&r)[KT][UM], int d0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KT; ++i)
+#pragma unroll
+            for (int u = 0; u < UM; ++u)
+                if (u < a.u) r[i][u].load(a.y, (long long)pp[i] * a.ld_y + min(d0 + u * 256 + lane * 4, a.D - 4));
+    };
+    float *__restrict__ o = a.out + t * a.D;
+    load(cur, 0);
+    for (int d0 = 0; d0 < a.D; d0 += cw) {
+        if (d0 + cw < a.D) load(nxt, d0 + cw);
+#pragma unroll
+        for (int u = 0; u < UM; ++u) {
+            if (u >= a.u) break;
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float4 sh = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int i = 0; i < KT; ++i) {
+                const float4 v = cur[i][u].f();
+                if (BLEND && i < a.lsh) {
+                    const float n = (float)a.lsh;
+                    sh.x = sh.x + v.x / n;
+                    sh.y = sh.y + v.y / n;
+                    sh.z = sh.z + v.z / n;
+                    sh.w = sh.w + v.w / n;
+                } else {
+                    const float g = gg[i];
+                    acc.x = acc.x + g * v.x;
+                    acc.y = acc.y + g * v.y;
+                    acc.z = acc.z + g * v.z;
+                    acc.w = acc.w + g * v.w;
+                }
+            }
+            if (BLEND) {
+                acc.x = 0.5f * sh.x + 0.5f * acc.x;
+                acc.y = 0.5f * sh.y + 0.5f * acc.y;
+                acc.z = 0.5f * sh.z + 0.5f * acc.z;
+                acc.w = 0.5f * sh.w + 0.5f * acc.w;
+            }
+            const int d = d0 + u * 256 + lane * 4;
+            if (d < a.D) *(float4 *)(o + d) = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < KT; ++i)
+#pragma unroll
+            for (int u = 0; u < UM; ++u) cur[i][u] = nxt[i][u];
+    }
 }
 
-template <int KT, bool BLEND, bool YB>
-__device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int lane) {
-#pragma clang fp contract(off)
-    constexpr int U = (KT >= 8) ? 1 : (KT >= 4 ? 4 : 8);
+// The token's entries (all KT slots), then the fast path when every one is
+// kept and the rows are 16-byte aligned.  Returns false otherwise.
+template <int KT, bool BLEND>
+__device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, long long t, int lane) {
+    if (a.kt != KT) return false;
     int ee[KT], pp[KT];
     float gg[KT];
+    bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-        const long long ent = (long long)t * KT + j;
+        const long long ent = t * KT + j;
         ee[j] = a.idx[ent];
         pp[j] = a.pos_of[ent];
         gg[j] = a.gates[ent];
+        all_kept = all_kept && pp[j] >= 0;
     }
+    if (!all_kept) return false;
     // stable sort by expert id (distinct ids; a fixed compare-exchange network)
 #pragma unroll
     for (int i = 0; i < KT; ++i)
@@ -1557,78 +1679,25 @@ __device__ __forceinline__ void combine_fast(const CombineArgs &a, int t, int la
             pp[j] = sw ? pp[j + 1] : p0; pp[j + 1] = sw ? p0 : pp[j + 1];
             gg[j] = sw ? gg[j + 1] : g0; gg[j + 1] = sw ? g0 : gg[j + 1];
         }
-    float *__restrict__ o = a.out + (long long)t * a.D;
-    for (int d0 = 0; d0 < a.D; d0 += 256 * U) {
-        float4 v[KT][U];
-#pragma unroll
-        for (int i = 0; i < KT; ++i)
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int d = min(d0 + u * 256 + lane * 4, a.D - 4);
-                v[i][u] = load_y4<YB>(a.y, (long long)pp[i] * a.ld_y + d);
-            }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float4 sh = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-            for (int i = 0; i < KT; ++i) {
-                if (BLEND && i < a.lsh) {
-                    const float n = (float)a.lsh;
-                    sh.x = sh.x + v[i][u].x / n;
-                    sh.y = sh.y + v[i][u].y / n;
-                    sh.z = sh.z + v[i][u].z / n;
-                    sh.w = sh.w + v[i][u].w / n;
-                } else {
-                    const float g = gg[i];
-                    acc.x = acc.x + g * v[i][u].x;
-                    acc.y = acc.y + g * v[i][u].y;
-                    acc.z = acc.z + g * v[i][u].z;
-                    acc.w = acc.w + g * v[i][u].w;
-                }
-            }
-            if (BLEND) {
-                acc.x = 0.5f * sh.x + 0.5f * acc.x;
-                acc.y = 0.5f * sh.y + 0.5f * acc.y;
-                acc.z = 0.5f * sh.z + 0.5f * acc.z;
-                acc.w = 0.5f * sh.w + 0.5f * acc.w;
-            }
-            const int d = d0 + u * 256 + lane * 4;
-            if (d < a.D) *(float4 *)(o + d) = acc;
-        }
-    }
-}
-
-template <int KT>
-__device__ __forceinline__ bool try_combine_fast(const CombineArgs &a, int t, int lane) {
-    if (a.kt != KT) return false;
-    if (a.y_bf16) combine_fast<KT, false, true>(a, t, lane);
-    else combine_fast<KT, false, false>(a, t, lane);
-    return true;
-}
-
-template <int KT>
-__device__ __forceinline__ bool try_combine_blend(const CombineArgs &a, int t, int lane) {
-    if (a.kt != KT) return false;
-    if (a.y_bf16) combine_fast<KT, true, true>(a, t, lane);
-    else combine_fast<KT, true, false>(a, t, lane);
+    if (a.y_bf16) combine_fast<KT, BLEND, true>(a, t, lane, pp, gg);
+    else combine_fast<KT, BLEND, false>(a, t, lane, pp, gg);
     return true;
 }
 
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const long long t = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
     if (a.kt > MOE_MAX_TOPK) {
         // more slots than a token's sort network holds: ExpertChoiceGating,
         // whose slots list the token's experts in ascending id order (empty
         // and dropped slots have no position), so slot order is expert order
-        float *o = a.out + (long long)t * a.D;
+        float *o = a.out + t * a.D;
         for (int d = lane; d < a.D; d += 64) {
             float acc = 0.0f;
             for (int j = 0; j < a.kt; ++j) {
-                const long long ent = (long long)t * a.kt + j;
+                const long long ent = t * a.kt + j;
                 const int p = a.pos_of[ent];
                 if (p < 0) continue;
                 const long long off = (long long)p * a.ld_y + d;
@@ -1639,24 +1708,20 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         }
         return;
     }
-    bool all_kept = (a.D & 3) == 0 && (a.ld_y & 3) == 0;
-    for (int j = 0; j < a.kt; ++j) all_kept = all_kept && a.pos_of[(long long)t * a.kt + j] >= 0;
-    if (all_kept) {
-        if (a.lsh > 0) {
-            if (try_combine_blend<2>(a, t, lane) || try_combine_blend<3>(a, t, lane) ||
-                try_combine_blend<4>(a, t, lane))
-                return;
-        } else if (try_combine_fast<2>(a, t, lane) || try_combine_fast<1>(a, t, lane) ||
-                   try_combine_fast<8>(a, t, lane) || try_combine_fast<4>(a, t, lane) ||
-                   try_combine_fast<6>(a, t, lane)) {
+    if (a.lsh > 0) {
+        if (try_combine_fast<2, true>(a, t, lane) || try_combine_fast<3, true>(a, t, lane) ||
+            try_combine_fast<4, true>(a, t, lane))
             return;
-        }
+    } else if (try_combine_fast<2, false>(a, t, lane) || try_combine_fast<1, false>(a, t, lane) ||
+               try_combine_fast<8, false>(a, t, lane) || try_combine_fast<4, false>(a, t, lane) ||
+               try_combine_fast<6, false>(a, t, lane)) {
+        return;
     }
     int ee[MOE_MAX_TOPK], pp[MOE_MAX_TOPK];
     float gg[MOE_MAX_TOPK];
     int n = 0;
     for (int j = 0; j < a.kt; ++j) {
-        const long long ent = (long long)t * a.kt + j;
+        const long long ent = t * a.kt + j;
         const int p = a.pos_of[ent];
         if (p < 0) continue;
         const int e = a.idx[ent];
@@ -1673,7 +1738,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         gg[i] = g;
         ++n;
     }
-    float *o = a.out + (long long)t * a.D;
+    float *o = a.out + t * a.D;
     for (int d = lane; d < a.D; d += 64) {
         float acc = 0.0f, sh = 0.0f;
         for (int i = 0; i < n; ++i) {
@@ -1687,9 +1752,16 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
 }
 
-hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
-    if (a.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
+hipError_t launch_combine(const CombineArgs &a0, hipStream_t s) {
+    if (a0.T <= 0) return hipSuccess;
+    CombineArgs a = a0;
+    // 256-column groups per chunk of the fast path: combine_umax(kt), lowered
+    // to the smallest power of two that covers D
+    const int groups = (a.D + 255) / 256;
+    a.u = combine_umax(std::min(a.kt, MOE_MAX_TOPK));
+    while (a.u > 1 && a.u / 2 >= groups) a.u /= 2;
+    a.nchunk = (a.D + 256 * a.u - 1) / (256 * a.u);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((a.T + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
