@@ -420,22 +420,31 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
 
 // ---- gating -------------------------------------------------------------------
 // One gating pass over the route block's tokens: lane rs of token rt = tid /
-// 8 holds the contiguous experts rs EPL .. +EPL of the token's row in
-// registers.  Logits: the LDS row L[rt] (plus xbias, the second pass's bias).
-// Per token: the max; exp terms e = (float)exp((double)(l - m)) (NNlib's
-// branch for m == +Inf); their fp32 sum in expert order (a chain through the
-// lanes: lane r adds its experts, in order, to lane r - 1's running sum,
-// passed on by DPP row_shr:1); probabilities e / s; the fp64 entropy terms
-// and the logsumexp.  Top-k: k rounds, each taking the largest (isless key,
-// then lower index) element below the previous round's, by a per-lane scan
-// and a 3-step DPP butterfly; the gates.  Then per entry (lane rs = slot
-// rs): its stable rank among the route block's entries of its expert (LDS
-// bitmask per expert, bit = entry), and the route block's histogram,
-// probability sums and loss terms.  Pr: LDS rows [TB][RW] for the output
-// probabilities.
+// 8 owns the contiguous experts rs EPL .. +EPL of the token's row.  Logits:
+// the LDS row L[rt] (plus xbias, the second pass's bias).  Per token: the
+// max; exp terms e = (float)exp((double)(l - m)) (NNlib's branch for m ==
+// +Inf); their fp32 sum in expert order (a chain through the lanes: lane r
+// adds its experts, in order, to lane r - 1's running sum, passed on by DPP
+// row_shr:1); probabilities e / s; the fp64 entropy terms and the
+// logsumexp.  Top-k: k rounds, each taking the largest (isless key, then
+// lower index) element below the previous round's, by a per-lane scan and a
+// 3-step DPP butterfly; the gates.  Then per entry (lane rs = slot rs): its
+// stable rank among the route block's entries of its expert (LDS bitmask per
+// expert, bit = entry), and the route block's histogram, probability sums
+// and loss terms.  Pr: LDS rows [TB][RW] for the output probabilities; G:
+// LDS rows [TB][RW], the gate's working row (its logits, then the exp terms,
+// then the probabilities).
+//
+// The per-expert work with long instruction sequences (fp64 exp, IEEE
+// division, the entropy log, the noise draws) runs in loops over the lane's
+// EPL experts through G, so that its code is executed EPL times from the
+// instruction cache instead of being laid out EPL times (up to 16: tens of KB
+// of straight-line code, fetched once per workgroup at L2 latency); only the
+// ordered chain sum and the top-k compares work on registers (pr).
 template <int EPL>
 __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const float *xbias, int blk, int t0, int ntok,
-                                        const float *L, float *Pr, unsigned *emask, double (*wred)[kRtThreads / 64]) {
+                                        const float *L, float *Pr, float *G, unsigned *emask,
+                                        double (*wred)[kRtThreads / 64]) {
 #pragma clang fp contract(off)
     const RouteArgs &a = A.r;
     const int RW = A.RW;
@@ -453,6 +462,7 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     const long long t = (long long)t0 + rt;
     const int ns = shared_gate ? a.ns : 0;  // rows before the routed ones
     const int base = rs * EPL;
+    const int row = rt * RW;
 
     __syncthreads();  // a previous pass is done with emask and the rows
     for (int i = tid; i < a.Eh * kRtMaskWords; i += kRtThreads) emask[i] = 0u;
@@ -462,24 +472,35 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     // logits without router noise (the reference's z-loss reruns the router
     // with training=false, src/core/moe_layer.jl:117-121)
     const bool zs_own = zsep || noise;
-    float v[EPL], vg[EPL], pr[EPL];  // logits; the logits the gate sees; exp terms, then probabilities
+    float pr[EPL];  // exp terms, then probabilities
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) { v[j] = 0.0f; vg[j] = 0.0f; pr[j] = 0.0f; }
+    for (int j = 0; j < EPL; ++j) pr[j] = 0.0f;
+    // G[row + i] into pr (the lane's experts in range)
+    auto load_pr = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const bool ok = rvalid && base + j < E;
+            pr[j] = ok ? G[ok ? row + base + j : 0] : 0.0f;
+        }
+    };
     float lse = 0.0f;
     double hs = 0.0;
     if (softmax) {
-#pragma unroll
+        // ---- the gate's logits (router noise, the aux bias) into G; the
+        // max of the routed rows (zs_own: also of all rows' plain logits) ----
+        float m = -INFINITY, mz = -INFINITY;
+#pragma unroll 4
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
             const bool ok = rvalid && i < E;
-            v[j] = ok ? L[ok ? rt * RW + i : 0] : 0.0f;
-            float x = v[j];
+            const float v = ok ? L[ok ? row + i : 0] : 0.0f;
+            float x = v;
             if (noise) {
                 // logits .+ randn .* noise_scale, or logits .+ noise_scale .*
                 // (randn .* softplus.(noise logits)) (router.jl:32-41)
                 const float r = init_normal(A.noise_seed, A.noise_call, (unsigned long long)t * E + (ok ? i : 0));
                 if (A.noise_net) {
-                    const float nl = ok ? L[ok ? rt * RW + E + i : 0] : 0.0f;
+                    const float nl = ok ? L[ok ? row + E + i : 0] : 0.0f;
                     const float sp = log1pf(expf(-fabsf(nl))) + fmaxf(nl, 0.0f);  // NNlib softplus
                     x = x + A.noise_scale * (r * sp);
                 } else {
@@ -488,38 +509,33 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             }
             // AuxiliaryFreeLoss gating pass: (noisy) logits .+ bias
             if (xbias) x = ok ? x + xbias[ok ? i : 0] : x;
-            vg[j] = ok ? x : 0.0f;
-        }
-        // ---- max (of the routed rows; zs_own: also of all rows) ----
-        float m = -INFINITY, mz = -INFINITY;
-        float sv[EPL];  // logits ./ lambda for SoftMoEGating (advanced.jl:18)
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const int i = base + j;
-            const bool ok = rvalid && i < E;
-            sv[j] = soft ? vg[j] / a.soft_lambda : vg[j];
-            m = (ok && i >= ns && sv[j] > m) ? sv[j] : m;
-            mz = (ok && v[j] > mz) ? v[j] : mz;
+            const float vg = ok ? x : 0.0f;
+            if (ok) {
+                G[row + i] = vg;
+                if (A.store_rows && out_probs) a.logits[t * E + i] = vg;
+            }
+            const float sv = soft ? vg / a.soft_lambda : vg;  // logits ./ lambda for SoftMoEGating (advanced.jl:18)
+            m = (ok && i >= ns && sv > m) ? sv : m;
+            mz = (ok && v > mz) ? v : mz;
         }
         m = lanes8_max(m);
         if (zs_own) mz = lanes8_max(mz);
-        // ---- exp terms; zs_own: the z-loss exponent sum over all rows ----
+        // ---- exp terms into G (0 for the shared rows); zs_own: the z-loss
+        // exponent sum over all rows ----
         float zs = 0.0f;
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
-            const bool okr = rvalid && i >= ns && i < E;
-            const float ex = (m == INFINITY) ? ((sv[j] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv[j] - m));
-            pr[j] = okr ? ex : 0.0f;
+            const bool ok = rvalid && i < E;
+            const bool okr = ok && i >= ns;
+            const float vg = ok ? G[ok ? row + i : 0] : 0.0f;
+            const float sv = soft ? vg / a.soft_lambda : vg;
+            const float ex = (m == INFINITY) ? ((sv == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(sv - m));
+            if (ok) G[row + i] = okr ? ex : 0.0f;
+            if (zs_own && ok) zs = zs + (float)exp((double)(L[row + i] - mz));
         }
-        if (zs_own) {
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) {
-                const int i = base + j;
-                if (rvalid && i < E) zs = zs + (float)exp((double)(v[j] - mz));
-            }
-            zs = lanes8_sum(zs);
-        }
+        if (zs_own) zs = lanes8_sum(zs);
+        load_pr();
         // ---- sum in expert order: a chain through the token's lanes ----
         float s;
         {
@@ -538,15 +554,15 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             // every lane of the token takes lane 7's total (swizzle: lane (i & 0x18) | 7)
             s = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0xF8));
         }
-        // ---- probabilities (outputs: shared gating's shared rows 1/E, routed
-        // rows p scaled by 1 - ns/E in Float64; the caller's gate: its
-        // probabilities or ones ./ E); entropy terms p log(p + 1e-8) with
-        // p + 1e-8 in Float64 as Julia promotes it, the log as the hardware
-        // log2 (v_log_f32, about 1 ulp) times ln 2 in fp32 (a statistic: the
-        // mean entropy is checked to 1e-5 relative) ----
+        // ---- probabilities (into G for the top-k; outputs: shared gating's
+        // shared rows 1/E, routed rows p scaled by 1 - ns/E in Float64; the
+        // caller's gate: its probabilities or ones ./ E); entropy terms p
+        // log(p + 1e-8) with p + 1e-8 in Float64 as Julia promotes it, the
+        // log as the hardware log2 (v_log_f32, about 1 ulp) times ln 2 in
+        // fp32 (a statistic: the mean entropy is checked to 1e-5 relative) ----
         const float invE = 1.0f / (float)E;
         const double pscale = 1.0 - (double)ns / (double)E;
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < EPL; ++j) {
             const int i = base + j;
             const bool ok = rvalid && i < E;
@@ -554,10 +570,14 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             if (a.given) {
                 pv = a.given_probs ? (ok ? a.probs[ok ? t * E + i : 0] : 0.0f) : invE;
             } else {
-                pr[j] = pr[j] / s;
-                pv = (i < ns) ? invE : (shared_gate ? (float)((double)pr[j] * pscale) : pr[j]);
+                const float p = (ok ? G[ok ? row + i : 0] : 0.0f) / s;
+                if (ok) G[row + i] = p;
+                pv = (i < ns) ? invE : (shared_gate ? (float)((double)p * pscale) : p);
             }
-            if (ok) Pr[rt * RW + i] = pv;
+            if (ok) {
+                Pr[row + i] = pv;
+                if (A.store_rows && out_probs) a.probs[t * E + i] = pv;
+            }
             const double pd = (double)pv;
             const float lg = __builtin_amdgcn_logf((float)(pd + 1e-8)) * 0.693147180559945309f;
             const double term = pd * (double)lg;
@@ -567,14 +587,7 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         // logsumexp (src/balancing/losses.jl:111-114) from the same exp recipe,
         // the log in Float32 as Julia takes it of the Float32 sum
         lse = zs_own ? mz + logf(zs) : m + logf(s);
-        if (A.store_rows && out_probs && rvalid) {
-#pragma unroll
-            for (int j = 0; j < EPL; ++j)
-                if (base + j < E) {
-                    a.logits[t * E + base + j] = vg[j];
-                    a.probs[t * E + base + j] = Pr[rt * RW + base + j];
-                }
-        }
+        if (!a.given) load_pr();
     }
 
     // ---- top-k and gates; the entry of this lane (slot rs of the token) ----
@@ -673,18 +686,29 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     __syncthreads();  // emask cleared
     if (has_ent) atomicOr(&emask[(my_e - 1) * kRtMaskWords + (ent >> 5)], 1u << (ent & 31));
     // route-block sums of the per-token loss terms (tokens rt: lane rs == 0),
-    // in a fixed order: within a wave by a butterfly over its 8 tokens, then
-    // the waves in order
+    // in a fixed order: within a wave its 8 tokens in order (read lane by
+    // lane: no LDS round trip per step), then the waves in order
     double zterm = 0.0, hterm = 0.0;
     if (softmax && rvalid && rs == 0) {
         zterm = (double)(lse * lse);
         hterm = -hs;
         if (out_probs && a.lse) a.lse[t] = lse;
     }
+    {
+        auto lane_d = [](double v, int l) __attribute__((always_inline)) {
+            const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+            const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l);
+            const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+            return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+        };
+        double zw = lane_d(zterm, 0), hw = lane_d(hterm, 0);
 #pragma unroll
-    for (int o = 8; o < 64; o <<= 1) {
-        zterm = zterm + __shfl_xor(zterm, o);
-        hterm = hterm + __shfl_xor(hterm, o);
+        for (int q = 1; q < 8; ++q) {
+            zw = zw + lane_d(zterm, 8 * q);
+            hw = hw + lane_d(hterm, 8 * q);
+        }
+        zterm = zw;
+        hterm = hw;
     }
     if (lane == 0) {
         wred[0][wv] = zterm;
@@ -749,7 +773,10 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
     const int t0 = blk * A.TB;
     const int ntok = min(A.TB, A.r.T - t0);
     float *L = (float *)(rdyn + A.off_L);
-    float *Pr = (float *)rdyn;  // over the staging region, free once the logits are in L
+    // over the staging region, free once the logits are in L: the output
+    // probability rows, then the gate's working rows
+    float *Pr = (float *)rdyn;
+    float *G = Pr + A.TB * A.RW;
     // the other parity's super-block totals, last read by the previous call's permute
     for (int s = blk; s < A.r.nsup_max; s += gridDim.x)
         for (int e = threadIdx.x; e < A.r.ldc; e += kRtThreads) {
@@ -768,10 +795,10 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
         }
     }
     if (A.npass == 2) {
-        rt_gate<EPL>(A, ROUTE_OUT_PROBS, nullptr, blk, t0, ntok, L, Pr, emask, wred);
-        rt_gate<EPL>(A, ROUTE_OUT_GATING, A.aux_bias, blk, t0, ntok, L, Pr, emask, wred);
+        rt_gate<EPL>(A, ROUTE_OUT_PROBS, nullptr, blk, t0, ntok, L, Pr, G, emask, wred);
+        rt_gate<EPL>(A, ROUTE_OUT_GATING, A.aux_bias, blk, t0, ntok, L, Pr, G, emask, wred);
     } else {
-        rt_gate<EPL>(A, A.r.out_mask, nullptr, blk, t0, ntok, L, Pr, emask, wred);
+        rt_gate<EPL>(A, A.r.out_mask, nullptr, blk, t0, ntok, L, Pr, G, emask, wred);
     }
 }
 
@@ -821,7 +848,7 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     A.RW = route_rw(Eg);
     const size_t rows = sizeof(float) * (size_t)TB * A.RW;
     const size_t lds_max = 150 * 1024;  // + the static emask / wred (9.2 KB) <= 160 KB
-    size_t region0 = rows;
+    size_t region0 = 2 * rows;  // the gating's Pr and G rows
     if (gemm) {
         const RouterArgs &g = A.g;
         if (g.Dp % 32 != 0 || g.Dp < g.D || g.Er != (A.noise_net ? 2 * Er : Er) || g.Er > MOE_MAX_EXPERTS)
