@@ -48,7 +48,8 @@ struct moe_handle {
     // that enqueued work without waiting for it did so on last_stream
     // (pending).  Calls that complete a layer (moe_forward_async,
     // moe_decode_async, moe_stage_combine_async) record `done` on their
-    // stream after their work (done_rec): a later call on another stream
+    // stream after their work (done_rec; moe_decode_async through its last
+    // kernel's completion signal): a later call on another stream
     // only waits for it, and moe_destroy synchronises on it, so neither
     // touches a caller stream that may be gone by then.  Between the other
     // stage calls nothing is recorded (a marker between two kernels costs
@@ -1617,7 +1618,8 @@ static int decode_check(moe_handle *h, int n) {
     return MOE_OK;
 }
 
-static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_dev, hipStream_t s) {
+static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_dev, hipStream_t s,
+                         hipEvent_t done = nullptr) {
     DecodeArgs a{};
     a.x = x_dev; a.D = h->D; a.n = n; a.kt = h->kt; a.k = h->k; a.E = h->Er; a.lsh = h->lsh;
     a.wr = h->wr; a.Er_pad = h->Er_pad; a.br = h->has_bias ? h->br : nullptr;
@@ -1627,7 +1629,7 @@ static int decode_locked(moe_handle *h, const float *x_dev, int n, float *out_de
     a.Dpad = h->D_pad; a.H = h->H; a.Hpad = h->H_pad; a.Dout = h->Dout;
     a.s1 = h->s1; a.s3 = h->s3; a.s2 = h->s2; a.Dout_npad = h->Dout_npad;
     a.h = (float *)h->hbuf; a.out = out_dev;
-    HIP_TRY(h, launch_decode_ffn(a, h->ncu, s));
+    HIP_TRY(h, launch_decode_ffn(a, h->ncu, s, done));
     h->last_T = -1;  // the routing buffers no longer describe a layer forward
     return MOE_OK;
 }
@@ -1664,8 +1666,11 @@ int moe_decode_async(moe_handle *h, const float *xb_dev, int32_t n, float *out_d
     if ((uintptr_t)xb_dev & 15) return fail(h, MOE_EINVAL, "xb_dev must be 16-byte aligned");
     hipStream_t s = stream ? (hipStream_t)stream : h->stream;
     r = join_stream(h, s);
-    if (r == MOE_OK) r = decode_locked(h, xb_dev, n, out_dev, s);
-    if (r == MOE_OK) r = mark_stream(h, s, true);
+    if (r == MOE_OK) r = decode_locked(h, xb_dev, n, out_dev, s, h->done);
+    if (r == MOE_OK) {
+        mark_stream(h, s);
+        h->done_rec = true;  // recorded by the last kernel's completion
+    }
     return r;
 }
 

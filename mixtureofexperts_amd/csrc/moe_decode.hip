@@ -20,6 +20,8 @@
 // and the 64 partial sums are added by a fixed butterfly, so every result is
 // deterministic.  All of a batch's loads are issued before its products
 // (clamped addresses, out-of-row chunks selected to zero).
+#include <hip/hip_ext.h>
+
 #include "moe_internal.h"
 
 namespace moe {
@@ -87,10 +89,10 @@ struct DecodeRouteLds {
 };
 
 // compute_gates of token t from the wave partials in L (see decode_route_block);
-// HI: E > 64, lane l also holds expert l + 64.
+// HI: E > 64, lane l also holds expert l + 64 (E <= 64: decode_gates64).
 template <bool HI>
 __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, int t, bool write,
-                                                           const DecodeRouteLds &L) {
+                                                           const DecodeRouteLds &L, float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, E = a.E;
     constexpr int NH = HI ? 2 : 1;
@@ -172,6 +174,7 @@ __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, 
             mye = e;
         }
     }
+    gate = lane < a.k ? myp / ssum : 0.0f;
     if (write) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
@@ -188,7 +191,94 @@ __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, 
         }
         if (lane < a.k) {
             a.idx[(long long)t * a.kt + a.lsh + lane] = a.lsh + mye + 1;
-            a.gates[(long long)t * a.kt + a.lsh + lane] = myp / ssum;
+            a.gates[(long long)t * a.kt + a.lsh + lane] = gate;
+        }
+    }
+    return packed;
+}
+
+// Wave maximum of v (unsigned or float compare), uniform: within each 16-lane
+// row by DPP steps, then the row results (rows past the first only when
+// `rows4`).  Maxima are exact, so the order of the steps does not matter.
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v, bool rows4) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));
+    uint32_t r = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    if (rows4) {
+        r = max(r, (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+        r = max(r, (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+        r = max(r, (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    }
+    return r;
+}
+__device__ __forceinline__ float wave_fmax(float v, bool rows4) {  // v never NaN
+    v = fmaxf(v, dpp_f<0xb1>(v));
+    v = fmaxf(v, dpp_f<0x4e>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    float r = readlane_f(v, 0);
+    if (rows4) r = fmaxf(fmaxf(r, readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+    return r;
+}
+
+// compute_gates for E <= 64, lane e holding expert e: the same recipe and
+// results as decode_gates, in fewer dependent steps.  The max (NaN ignored:
+// NaN lanes enter as -Inf, so all-NaN logits give -Inf as there) is a DPP
+// reduction; the sum runs in expert order over 8-lane groups, lanes past E
+// adding exact zeros; the k slots are k rounds of "largest isless key, lowest
+// expert among equal keys", the partialsortperm order that decode_gates
+// derives from ranks.
+__device__ __forceinline__ unsigned long long decode_gates64(const DecodeArgs &a, int t, bool write,
+                                                             const DecodeRouteLds &L, float &gate) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, E = a.E;
+    const bool valid = lane < E, rows4 = E > 16;
+    const int ec = min(lane, a.Er_pad - 1);
+    float lg = ((L.part[0][ec] + L.part[1][ec]) + L.part[2][ec]) + L.part[3][ec];
+    if (a.br) lg = lg + a.br[min(lane, E - 1)];
+    const float m = wave_fmax(valid && !__builtin_isnan(lg) ? lg : -INFINITY, rows4);
+    float ev = (m == INFINITY) ? ((lg == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(lg - m));
+    ev = valid ? ev : 0.0f;
+    float s = 0.0f;  // expert order: s + 0 == s for the lanes past E (s >= 0 or NaN)
+    for (int i0 = 0; i0 < E; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = readlane_f(ev, i0 + u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s = s + v[u];
+    }
+    const float p = ev / s;
+    uint32_t key = valid ? isless_key(p) : 0u;  // every float's key is > 0
+    float ssum = 0.0f, myp = 0.0f;
+    int mye = 0;
+    unsigned long long packed = 0ull;
+    for (int j = 0; j < a.k; ++j) {
+        const uint32_t mk = wave_umax(key, rows4);
+        const int e = __builtin_ctzll(__ballot(valid && key == mk));
+        const float pj = readlane_f(p, e);
+        ssum = (j == 0) ? pj : ssum + pj;  // slot order
+        packed |= (unsigned long long)e << (8 * j);
+        if (lane == e) key = 0u;  // taken
+        if (lane == j) {
+            myp = pj;
+            mye = e;
+        }
+    }
+    gate = lane < a.k ? myp / ssum : 0.0f;
+    if (write) {
+        if (valid) {
+            a.logits[(long long)t * E + lane] = lg;
+            a.probs[(long long)t * E + lane] = p;
+        }
+        if (lane < a.lsh) {
+            a.idx[(long long)t * a.kt + lane] = lane + 1;
+            a.gates[(long long)t * a.kt + lane] = 1.0f / (float)a.lsh;
+        }
+        if (lane < a.k) {
+            a.idx[(long long)t * a.kt + a.lsh + lane] = a.lsh + mye + 1;
+            a.gates[(long long)t * a.kt + a.lsh + lane] = gate;
         }
     }
     return packed;
@@ -206,9 +296,11 @@ __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, 
 // keys (partialsortperm(p, 1:k, rev=true)): the rank of expert i is the number
 // of experts before it in that order; the gates are p of the slots over their
 // sum in slot order.  Lane l holds experts l and, for E > 64, l + 64.
-// Returns the 0-based expert of slot j in bits [8 j, 8 j + 8) (uniform);
-// `write` (wave 0 of one block per token) stores logits, probs, indices, gates.
-__device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L) {
+// Returns the 0-based expert of routed slot j in bits [8 j, 8 j + 8)
+// (uniform), and in `gate` of lane j < k that slot's gate; `write` (wave 0 of
+// one block per token) stores logits, probs, indices, gates.
+__device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L,
+                                                 float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int E = a.E, Q = a.Er_pad >> 2;               // router row: Q float4 (Er_pad % 8 == 0)
@@ -266,25 +358,22 @@ __device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, boo
     if (c == 0 && q < Q) *(float4 *)&L.part[w][4 * q] = acc;
     __syncthreads();
 
-    return E > 64 ? decode_gates<true>(a, t, write, L) : decode_gates<false>(a, t, write, L);
+    return E > 64 ? decode_gates<true>(a, t, write, L, gate) : decode_gates64(a, t, write, L, gate);
 }
 
-// ---- up: block (token t, y) routes t, then its waves take units u = (slot,
-// row j) two at a time, u0 = 2 (y * 4 + wave), stepping 8 gridDim.y.  A unit
-// is the pair of dot products (W1_e row j) . x and (W3_e row j) . x over all
-// Hpad rows (pad rows have zero weights, so their h is 0 and the down products
-// may run over Hpad).
+// ---- up: the waves of token t take units u = (slot, row j) two at a time,
+// wave v of the token (v = y * 4 + wave of its block y) the units u0 = 2 v,
+// stepping 2 nv.  A unit is the pair of dot products (W1_e row j) . x and
+// (W3_e row j) . x over all Hpad rows (pad rows have zero weights, so their h
+// is 0 and the down products may run over Hpad).
 template <int WT>
-__global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_up_units(const DecodeArgs &a, int t, int v, int nv, unsigned long long sel) {
 #pragma clang fp contract(off)
-    __shared__ DecodeRouteLds L;
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const unsigned long long sel = decode_route_block(a, t, blockIdx.y == 0 && w == 0, L);
+    const int lane = threadIdx.x & 63;
     const int units = a.kt * a.Hpad;
     const int nch = a.D >> 2;  // 4-element chunks per row
     const float4 *x4 = (const float4 *)(a.x + (long long)t * a.D);
-    for (int u0 = (blockIdx.y * 4 + w) * 2; u0 < units; u0 += gridDim.y * 8) {
+    for (int u0 = 2 * v; u0 < units; u0 += 2 * nv) {
         const bool two = u0 + 1 < units;
         const int u1 = two ? u0 + 1 : u0;
         const int s0 = u0 / a.Hpad, j0 = u0 - s0 * a.Hpad;
@@ -335,6 +424,16 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
             if (two) a.h[hb + u1] = ok1 ? (g1 * (1.0f / (1.0f + expf(-g1)))) * q1 : 0.0f;
         }
     }
+}
+
+// block (token t, y) routes t, then runs its waves' units
+template <int WT>
+__global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
+    __shared__ DecodeRouteLds L;
+    const int w = threadIdx.x >> 6;
+    float gate;
+    const unsigned long long sel = decode_route_block(a, blockIdx.x, blockIdx.y == 0 && w == 0, L, gate);
+    decode_up_units<WT>(a, blockIdx.x, blockIdx.y * 4 + w, gridDim.y * 4, sel);
 }
 
 // ---- down: one wave per output row i of token t; slots two at a time, U
@@ -416,20 +515,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 }
 
 template <int WT>
-static hipError_t launch_decode_wt(const DecodeArgs &a, int ncu, hipStream_t s) {
+static hipError_t launch_decode_wt(const DecodeArgs &a, int ncu, hipStream_t s, hipEvent_t done) {
     const int tasks = (a.kt * a.Hpad + 1) / 2;                  // unit pairs per token
     const int gy = max(1, min((tasks + 3) / 4, max(1, 4 * ncu / a.n)));
     hipLaunchKernelGGL(decode_up_kernel<WT>, dim3(a.n, gy), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (a.Hpad <= 1024)
-        hipLaunchKernelGGL((decode_down_kernel<WT, 4>), dim3(a.n, a.Dout), dim3(64), 0, s, a);
-    else
-        hipLaunchKernelGGL((decode_down_kernel<WT, 8>), dim3(a.n, a.Dout), dim3(64), 0, s, a);
+    // `done` is recorded by the down kernel's own completion (no marker packet
+    // after it: that costs about 1 us of GPU time per call)
+    const dim3 grid(a.n, a.Dout), block(64);
+    if (a.Hpad <= 1024) hipExtLaunchKernelGGL((decode_down_kernel<WT, 4>), grid, block, 0, s, nullptr, done, 0, a);
+    else hipExtLaunchKernelGGL((decode_down_kernel<WT, 8>), grid, block, 0, s, nullptr, done, 0, a);
     return hipGetLastError();
 }
 
-hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s) {
+hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s, hipEvent_t done) {
     if (a.n <= 0) return hipSuccess;
     if (a.E < 1 || a.E + a.lsh > MOE_MAX_EXPERTS || a.k < 1 || a.k > a.E || a.lsh < 0 || a.kt != a.k + a.lsh ||
         a.kt > MOE_MAX_TOPK)
@@ -438,9 +538,9 @@ hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s) {
     if (a.D < 4 || (a.D & 3) || (a.Dpad & 3) || (a.Hpad & 3) || a.D > a.Dpad || a.H > a.Hpad) return hipErrorInvalidValue;
     if (((uintptr_t)a.x & 15) || ((uintptr_t)a.h & 15)) return hipErrorInvalidValue;
     switch (a.wt) {
-    case WT_F32: return launch_decode_wt<WT_F32>(a, ncu, s);
-    case WT_BF16: return launch_decode_wt<WT_BF16>(a, ncu, s);
-    default: return launch_decode_wt<WT_FP8>(a, ncu, s);
+    case WT_F32: return launch_decode_wt<WT_F32>(a, ncu, s, done);
+    case WT_BF16: return launch_decode_wt<WT_BF16>(a, ncu, s, done);
+    default: return launch_decode_wt<WT_FP8>(a, ncu, s, done);
     }
 }
 

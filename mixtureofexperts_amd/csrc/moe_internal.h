@@ -369,7 +369,8 @@ hipError_t launch_fold_split(int bm, const GemmArgs &g, hipStream_t s);
 // bf16 kernel's B tile image (RB-row blocks: 128 for gated W1 / W3, else 256)
 hipError_t launch_retile_weights(const void *src, void *dst, int Npad, int Kp, int esz, int RB, hipStream_t s);
 // decode: routing fused into the gated up products of each selected slot, then
-// the down products and the slot-order combine (two kernels)
-hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s);
+// the down products and the slot-order combine (two kernels); `done`, when not
+// null, is recorded at the end of the second
+hipError_t launch_decode_ffn(const DecodeArgs &a, int ncu, hipStream_t s, hipEvent_t done = nullptr);
 
 }  // namespace moe

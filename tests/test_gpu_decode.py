@@ -44,6 +44,31 @@ def test_decode_c2_fp32(moe, oracle, n):
         c.dev.close()
 
 
+@pytest.mark.parametrize("lsh,k", [(0, 2), (1, 2)])
+def test_decode_batch_and_single_calls_agree(moe, oracle, lsh, k):
+    # a call over 12 tokens and calls over 1 to 3 of them compute the same
+    # products in the same order: each token's output, logits, routing and
+    # gates are bitwise equal, over 30 calls in a row
+    E = 8 + lsh
+    c = Case(moe, oracle, T=12, D=512, H=1376, E=E, k=k, wdtype="f32", seed=31 + lsh, lsh=lsh, max_tokens=12)
+    try:
+        x = np.ascontiguousarray(c.x[:12])
+        print(f"decode n=12 lsh={lsh}", flush=True)
+        out12, l12, i12, g12 = c.dev.decode(x)
+        ref, ridx, _, _ = oracle.decode_ffn(x, c.wr, c.ex, k=k, logits=l12, num_shared=lsh)
+        assert np.array_equal(i12[:, lsh:] - lsh, ridx)
+        assert rel_err(out12, ref) <= TOL["f32"]
+        for rep in range(30):
+            n = 1 + rep % 3
+            t = (5 * rep) % (12 - n + 1)
+            o, lg, i, g = c.dev.decode(np.ascontiguousarray(x[t:t + n]))
+            assert np.array_equal(o.view(np.uint32), out12[t:t + n].view(np.uint32)), (rep, t, n)
+            assert np.array_equal(lg.view(np.uint32), l12[t:t + n].view(np.uint32)), (rep, t, n)
+            assert np.array_equal(i, i12[t:t + n]) and np.array_equal(g.view(np.uint32), g12[t:t + n].view(np.uint32))
+    finally:
+        c.dev.close()
+
+
 @pytest.mark.parametrize("wdtype", ["bf16", "fp8"])
 def test_decode_low_precision_weights(moe, oracle, wdtype):
     c = Case(moe, oracle, T=8, D=512, H=1376, E=8, k=2, wdtype=wdtype, seed=22)
@@ -70,6 +95,41 @@ def test_decode_many_experts(moe, oracle):
     c = Case(moe, oracle, T=5, D=128, H=96, E=96, k=4, wdtype="f32", seed=29, router_bias=rb)
     try:
         check_decode(c, oracle, 5, TOL["f32"])
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("E", [16, 40])
+def test_decode_tied_and_infinite_logits(moe, oracle, E):
+    # equal probabilities go to the lower expert first (partialsortperm with
+    # isless, rev=true): router rows 1, 3 and 7 are equal, so their logits tie
+    # bitwise; a +Inf bias on experts 5 and 9 makes p 1/2 there and 0
+    # elsewhere (the +Inf-maximum rule), so the third slot is a tie of zeros
+    # (expert 0).  Routing and gates bit-exact against the oracle on the GPU's
+    # logits; the output within the fp32 tolerance.
+    rb = np.zeros(E, np.float32)
+    c = Case(moe, oracle, T=6, D=64, H=128, E=E, k=3, wdtype="f32", seed=33, router_bias=rb, max_tokens=6)
+    try:
+        wr = c.wr.copy()
+        wr[3] = wr[1]
+        wr[7] = wr[1]
+        c.wr = wr
+        c.dev.set_router(np.ascontiguousarray(wr.T), rb)
+        x = np.ascontiguousarray(c.x[:6])
+        out, logits, idx, gates = c.dev.decode(x)
+        assert np.array_equal(logits[:, 3].view(np.uint32), logits[:, 1].view(np.uint32))
+        ref, ridx, rgates, _ = oracle.decode_ffn(x, wr, c.ex, k=3, logits=logits)
+        assert np.array_equal(idx, ridx) and np.array_equal(gates.view(np.uint32), rgates.view(np.uint32))
+        assert rel_err(out, ref) <= TOL["f32"]
+        rb_inf = rb.copy()
+        rb_inf[5] = rb_inf[9] = np.inf
+        c.dev.set_router(np.ascontiguousarray(wr.T), rb_inf)
+        out, logits, idx, gates = c.dev.decode(x)
+        ref, ridx, rgates, _ = oracle.decode_ffn(x, wr, c.ex, k=3, logits=logits)
+        assert np.array_equal(idx, ridx) and np.array_equal(gates.view(np.uint32), rgates.view(np.uint32))
+        assert np.array_equal(idx, np.tile(np.array([6, 10, 1], np.int32), (6, 1)))
+        assert np.array_equal(gates, np.tile(np.array([0.5, 0.5, 0.0], np.float32), (6, 1)))
+        assert rel_err(out, ref) <= TOL["f32"]
     finally:
         c.dev.close()
 
