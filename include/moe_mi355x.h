@@ -104,7 +104,8 @@ typedef struct {
     int32_t num_shared_experts; /* MoEConfig.num_shared_experts: experts 1..ns run on every
                                    token (forward_with_shared_experts,
                                    src/core/moe_layer.jl:158-185); the router then has
-                                   num_experts - ns outputs.  TopK / Switch gates only. */
+                                   num_experts - ns outputs, and any gate and balance loss
+                                   runs on those (the gate's ids shifted by ns). */
     float gate_param;           /* SoftMoEGating.lambda (SOFT), ExpertChoiceGating.capacity_factor
                                    (EXPERT_CHOICE); unused otherwise */
     int32_t reserved[5];        /* zero */
@@ -135,12 +136,13 @@ int moe_destroy(moe_handle *h);
 /* Last error message of h (or of the last failed moe_create when h is NULL). */
 const char *moe_last_error(const moe_handle *h);
 int moe_abi_version(void);
-/* Number of router outputs: E for TopK/Switch/Shared gating, E - ns with
- * num_shared_experts = ns > 0. */
+/* Number of router outputs: E, or E - ns with num_shared_experts = ns > 0. */
 int moe_router_outputs(const moe_handle *h);
-/* Slots per token: k, 1 (Switch) or num_shared + k (SharedExpertGating, or
- * num_shared_experts > 0: the ns shared slots first, with ids 1..ns, then the
- * routed slots with ids shifted by ns, as expert_indices .+= ns makes them). */
+/* Slots per token: k, 1 (Switch), num_shared + k (SharedExpertGating) or
+ * min(capacity at max_tokens, E) (ExpertChoiceGating); with
+ * num_shared_experts = ns > 0, ns more: the ns shared slots first, with ids
+ * 1..ns, then the gate's slots with ids shifted by ns, as expert_indices .+=
+ * ns makes them. */
 int moe_slots_per_token(const moe_handle *h);
 
 /* ---- weights (uploaded once, prepacked, device resident) --------------- */
@@ -195,12 +197,19 @@ int moe_set_expert(moe_handle *h, int32_t expert, int32_t layout, int32_t src_dt
  * update_counter += 1 and, when it is a multiple of update_freq, the bias
  * update of update_bias! (:36-69) runs on the device over the kept entries.
  * bias / bias_momentum: E_router floats (host), NULL = zeros.  enable = 0
- * restores the loss set at moe_create.  Not with num_shared_experts > 0. */
+ * restores the loss set at moe_create.  With num_shared_experts > 0 the layer
+ * runs forward_with_shared_experts (src/core/moe_layer.jl:158-185): the gate
+ * sees the plain logits (no bias), and the loss and update_bias! receive the
+ * gate's ids shifted by num_shared_experts, so bias / bias_momentum then hold
+ * num_experts floats (the shared experts' entries count no assignment, and an
+ * ExpertChoiceGating matrix's empty entries count as expert
+ * num_shared_experts, as the shifted zeros do there). */
 int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const float *bias_momentum,
                      float learning_rate, float momentum, int32_t update_freq, int64_t update_counter,
                      int32_t use_complementary_loss, float complementary_weight);
-/* Read back the AuxiliaryFreeLoss state (E_router floats each; any pointer
- * may be NULL).  Blocks until the handle's queued work has finished. */
+/* Read back the AuxiliaryFreeLoss state (E_router floats each, num_experts
+ * with num_shared_experts > 0; any pointer may be NULL).  Blocks until the
+ * handle's queued work has finished. */
 int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *update_counter);
 
 /* Expert initialisation strategies of convert_to_moe / create_single_expert
@@ -255,8 +264,10 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
  * is forward_with_shared_experts (src/core/moe_layer.jl:158-185): out =
  * 0.5 * sum_i(y_i / ns) + 0.5 * routed, the routed part combined as in
  * forward_standard over experts ns+1..E, no capacity constraint, and the
- * Switch loss over the E - ns router probabilities with the shifted routed
- * ids (ids above E - ns are not counted, src/balancing/losses.jl:22-26). */
+ * balance loss over the E - ns router probabilities with the gate's shifted
+ * ids (ids above E - ns are not counted, src/balancing/losses.jl:22-26; an
+ * ExpertChoiceGating matrix's empty entries become id ns and are counted
+ * when ns <= E - ns). */
 int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
                 float *out, float *loss, moe_forward_aux *aux);
 

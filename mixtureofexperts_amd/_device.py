@@ -50,6 +50,10 @@ class DeviceLayer:
         self.h = h
         self.router_outputs = _lib.lib().moe_router_outputs(h)
         self.slots = _lib.lib().moe_slots_per_token(h)
+        # AuxiliaryFreeLoss bias length: the router outputs, or all experts
+        # when the layer has shared experts (update_bias! then sees the ids
+        # shifted by num_shared_experts, up to num_experts)
+        self.aux_free_len = num_experts if num_shared_experts > 0 else self.router_outputs
 
     @classmethod
     def gating_only(cls, spec, E, T, capacity_factor=None):
@@ -114,8 +118,9 @@ class DeviceLayer:
         """Load an AuxiliaryFreeLoss's state and parameters into the handle."""
         bias = np.ascontiguousarray(loss.bias, dtype=np.float32)
         mom = np.ascontiguousarray(loss.bias_momentum, dtype=np.float32)
-        if bias.size != self.router_outputs or mom.size != self.router_outputs:
-            raise _lib.MoeError(_lib.MOE_EINVAL, "AuxiliaryFreeLoss.num_experts must equal the router outputs")
+        if bias.size != self.aux_free_len or mom.size != self.aux_free_len:
+            raise _lib.MoeError(_lib.MOE_EINVAL, "AuxiliaryFreeLoss.num_experts must equal the router outputs "
+                                "(num_experts with shared experts of the layer)")
         _lib.check(_lib.lib().moe_set_aux_free(self.h, 1, bias.ctypes.data, mom.ctypes.data, loss.learning_rate,
                                                loss.momentum, loss.update_freq, loss.update_counter,
                                                int(loss.use_complementary_loss), loss.complementary_weight),
@@ -123,8 +128,8 @@ class DeviceLayer:
 
     def get_aux_free(self, loss):
         """Copy the handle's AuxiliaryFreeLoss state back into ``loss``."""
-        bias = np.zeros(self.router_outputs, dtype=np.float32)
-        mom = np.zeros(self.router_outputs, dtype=np.float32)
+        bias = np.zeros(self.aux_free_len, dtype=np.float32)
+        mom = np.zeros(self.aux_free_len, dtype=np.float32)
         cnt = ctypes.c_int64(0)
         _lib.check(_lib.lib().moe_get_aux_free(self.h, bias.ctypes.data, mom.ctypes.data, ctypes.byref(cnt)),
                    self.h)

@@ -219,33 +219,28 @@ static int validate_config(const moe_config *c, std::string &why) {
     if (c->max_tokens < 1) { why = "max_tokens must be >= 1"; return 0; }
     if (c->drop_tokens && !(c->capacity_factor > 0.0f)) { why = "capacity_factor must be > 0"; return 0; }
     const int k = (c->gate_kind == MOE_GATE_SWITCH) ? 1 : c->top_k;
+    // the layer's shared experts (forward_with_shared_experts) run with any
+    // gate and loss; the router and its gate see the Er = num_experts - lsh
+    // routed experts (src/core/moe_layer.jl:47-50, 158-185)
     const int lsh = c->num_shared_experts;
     if (lsh < 0 || lsh >= c->num_experts) { why = "num_shared_experts must be in [0, num_experts)"; return 0; }
-    if (lsh > 0 && c->gate_kind == MOE_GATE_SHARED) {
-        why = "num_shared_experts > 0 with SharedExpertGating has no device path";
-        return 0;
-    }
-    if ((c->gate_kind == MOE_GATE_SOFT || c->gate_kind == MOE_GATE_EXPERT_CHOICE) && lsh > 0) {
-        why = "num_shared_experts > 0 needs TopKGating or SwitchGating";
-        return 0;
-    }
+    const int Er = c->num_experts - lsh;
     if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH || c->gate_kind == MOE_GATE_SOFT) {
-        if (k < 1 || k > c->num_experts - lsh) { why = "top_k must be in [1, num_experts - num_shared_experts]"; return 0; }
+        if (k < 1 || k > Er) { why = "top_k must be in [1, num_experts - num_shared_experts]"; return 0; }
         if (lsh + k > MOE_MAX_TOPK) { why = "num_shared_experts + top_k above MOE_MAX_TOPK (8)"; return 0; }
     } else if (c->gate_kind == MOE_GATE_EXPERT_CHOICE) {
         if (!(c->gate_param > 0.0f)) { why = "ExpertChoiceGating capacity_factor (gate_param) must be > 0"; return 0; }
     } else if (c->gate_kind == MOE_GATE_SHARED) {
         const int ns = c->gate_num_shared;
-        if (ns < 0 || ns >= c->num_experts) { why = "gate_num_shared must be in [0, num_experts)"; return 0; }
-        if (k < 1 || k > c->num_experts - ns) { why = "top_k must be in [1, num_experts - num_shared]"; return 0; }
-        if (ns + k > MOE_MAX_TOPK) { why = "num_shared + top_k above MOE_MAX_TOPK (8)"; return 0; }
+        if (ns < 0 || ns >= Er) { why = "gate_num_shared must be in [0, num_experts - num_shared_experts)"; return 0; }
+        if (k < 1 || k > Er - ns) { why = "top_k must be in [1, num_experts - num_shared_experts - num_shared]"; return 0; }
+        if (lsh + ns + k > MOE_MAX_TOPK) { why = "num_shared_experts + num_shared + top_k above MOE_MAX_TOPK (8)"; return 0; }
     } else {
         why = "unknown gate_kind";
         return 0;
     }
     const int slots = (c->gate_kind == MOE_GATE_EXPERT_CHOICE)
-                          ? (int)std::min<long long>(
-                                c->num_experts, expert_choice_capacity(c->max_tokens, c->gate_param, c->num_experts))
+                          ? lsh + (int)std::min<long long>(Er, expert_choice_capacity(c->max_tokens, c->gate_param, Er))
                           : k + lsh + (c->gate_kind == MOE_GATE_SHARED ? c->gate_num_shared : 0);
     const long long rows = (long long)c->max_tokens * slots;
     if (rows > INT_MAX / 2) { why = "max_tokens * slots too large"; return 0; }
@@ -575,6 +570,11 @@ enum { PERMUTE_NONE = 0, PERMUTE_INDEX = 1, PERMUTE_ROWS = 2 };
 // The capacity constraint runs in forward_standard only
 // (src/core/moe_layer.jl:142-147), not in forward_with_shared_experts.
 static bool drop_active(const moe_handle *h) { return h->cfg.drop_tokens && h->lsh == 0; }
+// AuxiliaryFreeLoss bias / momentum length: the router's experts, or, with
+// shared experts of the layer, all num_experts: update_bias! then receives
+// the gate's ids shifted by num_shared_experts (src/core/moe_layer.jl:172,
+// 182), up to num_experts, and indexes the bias with them
+static int aux_free_len(const moe_handle *h) { return h->lsh > 0 ? h->E : h->Er; }
 
 static int run_permute(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, int mode, hipStream_t s) {
     PermuteArgs pa{};
@@ -607,6 +607,10 @@ static bool up_pairs(const moe_handle *h) { return h->bf16_gemm && h->bm == 256 
 static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int training, bool compute_logits,
                        int permute_mode, float *loss_dev, hipStream_t s) {
     const bool aux = compute_logits && h->aux_free && !h->given;
+    // forward_standard gates on logits .+ bias (src/core/moe_layer.jl:137-140);
+    // forward_with_shared_experts gates on the plain logits and only hands the
+    // (shifted) ids to the loss (:168-182)
+    const bool aux_gate = aux && h->lsh == 0;
     const bool ec = h->cfg.gate_kind == MOE_GATE_EXPERT_CHOICE && !h->given;
     bool aux_update = false;
     if (aux && training) {
@@ -658,7 +662,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     sa.sup_cnt = ra.sup_cnt; sa.sup_p = ra.sup_p;
     sa.T = T; sa.E = h->E; sa.kt = h->kc;
     sa.training = training; sa.drop = drop_active(h); sa.z_enabled = h->cfg.z_loss_weight > 0.0f;
-    sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl;
+    sa.Np = h->Er; sa.lsh = h->lsh; sa.kl = h->kl; sa.ec_empty = (ec && h->lsh > 0) ? 1 : 0;
     sa.capacity_factor = h->cfg.capacity_factor; sa.alpha = h->cfg.balance_alpha; sa.beta = h->cfg.z_loss_weight;
     sa.bm = h->bm; sa.tile_start = h->tile_start; sa.counts = h->counts; sa.offsets = h->offsets;
     sa.item_start = up_pairs(h) ? h->item_start : nullptr; sa.pair_nt = up_ntiles(h);
@@ -671,7 +675,7 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     // ExpertChoiceGating kernels that read them
     A.store_rows = (h->keep_rows || ec || !compute_logits) ? 1 : 0;
     h->keep_rows = false;
-    if (aux) {
+    if (aux_gate) {
         // probabilities pass on the logits, gating pass on logits + the loss's bias
         A.npass = 2;
         A.aux_bias = h->aux_bias;
@@ -696,8 +700,8 @@ static int run_routing(moe_handle *h, const void *x_dev, int x_bf16, int T, int 
     if (ec) {
         // the experts' choices give the slots, the stable ranks and the
         // per-block histogram
-        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->E, h->kl, h->kc, h->ec_sel, h->idx, h->gates,
-                                        h->rank, h->blk_counts, h->ldc, ra.sup_cnt, h->rb, s));
+        HIP_TRY(h, launch_expert_choice(h->logits, h->probs, T, h->Er, h->lsh, h->kl, h->kc, h->ec_sel, h->idx,
+                                        h->gates, h->rank, h->blk_counts, h->ldc, ra.sup_cnt, h->rb, s));
     }
     // the scan runs in the permute kernel (its workgroups are the route blocks)
     sa.nblk = (T + h->rb - 1) / h->rb;
@@ -812,7 +816,7 @@ static int begin_call(moe_handle *h, int T) {
         // the call's min(capacity, E) <= kt = min(capacity at max_tokens, E)
         // slots are filled, the rest stay empty; the Switch loss counts all
         // capacity rows of the reference's (capacity, T) index matrix
-        h->kl = (int)expert_choice_capacity(T, h->cfg.gate_param, h->E);
+        h->kl = (int)expert_choice_capacity(T, h->cfg.gate_param, h->Er);
     }
     return MOE_OK;
 }
@@ -882,7 +886,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->k = (cfg->gate_kind == MOE_GATE_SWITCH || cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) ? 1 : cfg->top_k;
     h->ns = (cfg->gate_kind == MOE_GATE_SHARED) ? cfg->gate_num_shared : 0;
     h->kt = (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE)
-                ? (int)std::min<long long>(h->E, expert_choice_capacity(cfg->max_tokens, cfg->gate_param, h->E))
+                ? h->lsh + (int)std::min<long long>(h->Er, expert_choice_capacity(cfg->max_tokens, cfg->gate_param, h->Er))
                 : h->lsh + h->ns + h->k;
     h->kc = h->kt;
     h->kl = h->kt - h->lsh;
@@ -950,10 +954,11 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->ent_max = (long long)h->T_max * h->kt;
     h->rows_max = h->T_max * h->kt;
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) {
-        // each expert takes at most min(capacity, T) tokens
+        // each routed expert takes at most min(capacity, T) tokens; every
+        // token holds the lsh shared experts
         const long long cmax = std::min<long long>(
-            expert_choice_capacity(h->T_max, cfg->gate_param, h->E), h->T_max);
-        h->rows_max = (int)std::min<long long>(h->rows_max, (long long)h->E * cmax);
+            expert_choice_capacity(h->T_max, cfg->gate_param, h->Er), h->T_max);
+        h->rows_max = (int)std::min<long long>(h->rows_max, (long long)h->T_max * h->lsh + (long long)h->Er * cmax);
     }
     h->bf16_gemm = h->ct == CT_BF16 && (h->wt == WT_BF16 || h->wt == WT_FP8);
     // 256-row tiles for a few large experts (at most 16, averaging at least 384
@@ -991,8 +996,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->item_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
     if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
-    A((void **)&h->aux_bias, sizeof(float) * h->Er);
-    A((void **)&h->aux_mom, sizeof(float) * h->Er);
+    A((void **)&h->aux_bias, sizeof(float) * aux_free_len(h));
+    A((void **)&h->aux_mom, sizeof(float) * aux_free_len(h));
     A((void **)&h->perm, sizeof(int) * nent);
     A((void **)&h->pos_of, sizeof(int) * nent);
     A((void **)&h->gate_sorted, sizeof(float) * (size_t)h->rows_max);
@@ -1029,8 +1034,8 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     Z(h->b2, sizeof(float) * (size_t)h->E * h->Dout_npad);
     Z(h->sup_cnt2, sizeof(int) * 2 * (size_t)h->nsup_max * h->ldc);
     Z(h->sup_p2, sizeof(unsigned long long) * 2 * (size_t)h->nsup_max * h->ldc);
-    Z(h->aux_bias, sizeof(float) * h->Er);
-    Z(h->aux_mom, sizeof(float) * h->Er);
+    Z(h->aux_bias, sizeof(float) * aux_free_len(h));
+    Z(h->aux_mom, sizeof(float) * aux_free_len(h));
     Z(h->xp, asz * (size_t)h->act_rows * h->D_pad);
     Z(h->hbuf, asz * (size_t)h->act_rows * h->H_pad);
     if (ze == hipSuccess) ze = hipStreamSynchronize(h->stream);
@@ -1362,14 +1367,12 @@ int moe_set_aux_free(moe_handle *h, int32_t enable, const float *bias, const flo
         h->aux_free = false;
         return MOE_OK;
     }
-    if (h->lsh > 0)
-        return fail(h, MOE_EUNSUPPORTED, "AuxiliaryFreeLoss with num_shared_experts > 0 has no device path");
     if (update_freq < 1) return fail(h, MOE_EINVAL, "update_freq must be >= 1");
     if (update_counter < 0) return fail(h, MOE_EINVAL, "update_counter must be >= 0");
     hipStream_t s = h->stream;
     int r = join_stream(h, s);
     if (r != MOE_OK) return r;
-    const size_t bytes = sizeof(float) * h->Er;
+    const size_t bytes = sizeof(float) * aux_free_len(h);
     if (bias) HIP_TRY(h, hipMemcpyAsync(h->aux_bias, bias, bytes, hipMemcpyHostToDevice, s));
     else HIP_TRY(h, hipMemsetAsync(h->aux_bias, 0, bytes, s));
     if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(h->aux_mom, bias_momentum, bytes, hipMemcpyHostToDevice, s));
@@ -1392,7 +1395,7 @@ int moe_get_aux_free(moe_handle *h, float *bias, float *bias_momentum, int64_t *
     hipStream_t s = h->stream;
     int r = join_stream(h, s);
     if (r != MOE_OK) return r;
-    const size_t bytes = sizeof(float) * h->Er;
+    const size_t bytes = sizeof(float) * aux_free_len(h);
     if (bias) HIP_TRY(h, hipMemcpyAsync(bias, h->aux_bias, bytes, hipMemcpyDeviceToHost, s));
     if (bias_momentum) HIP_TRY(h, hipMemcpyAsync(bias_momentum, h->aux_mom, bytes, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));

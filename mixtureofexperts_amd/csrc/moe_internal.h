@@ -153,6 +153,8 @@ struct ScanArgs {
     int nsup;               // super blocks of the call: ceil(nblk / kSuper)
     int nblk, T, E, kt;   // E: experts of the histogram
     int Np, lsh, kl;      // Switch loss: probability rows N, shared experts of the layer, router slots per token
+    int ec_empty;          // ExpertChoiceGating with shared experts: the (kl, T) index matrix's empty
+                           // entries, shifted to id lsh, count as expert lsh (losses and update_bias!)
     int training, drop, z_enabled;
     float capacity_factor, alpha, beta;
     int bm;                // GEMM tile rows
@@ -171,7 +173,7 @@ struct ScanArgs {
     // update_bias! step of this call when aux_update (training only)
     int aux_free, aux_use_comp, aux_update;
     float aux_cw, aux_lr, aux_momentum;
-    float *aux_bias, *aux_mom;  // [E] device state
+    float *aux_bias, *aux_mom;  // [E] device state (the shared experts' entries, lsh > 0, count nothing)
 };
 
 // One router_kernel launch: logits (GEMM of g, or r.part), then one or two
@@ -332,14 +334,16 @@ hipError_t launch_router_split(const float *w, int D, int Er, int Er_pad, int Dp
 // the routing call's router_kernel launch; *tb receives the tokens per
 // workgroup (route block) it chose
 hipError_t launch_router(RtArgs a, int *tb, hipStream_t s);
-// ExpertChoiceGating on logits / probs [T][E]: sel [T][E] bytes (work), idx /
-// gates [T][kt] (kt >= min(C, E), the slots past min(C, E) empty), and the
-// bucketing inputs of the scan: rank [T][kt] (rank of each entry among its
-// expert's entries in its route block), blk_counts [nblk][ldc] and the
-// totals per super block sup_cnt [nsup][ldc] (atomic adds)
-hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *sup_cnt,
-                                int rb, hipStream_t s);
+// ExpertChoiceGating on logits / probs [T][E] of the E routed experts, after
+// the layer's lsh shared experts: sel [T][E] bytes (work), idx / gates
+// [T][kt] (kt >= lsh + min(C, E): the shared slots, then the routed ones, ids
+// shifted by lsh; the slots past lsh + min(C, E) empty), and the bucketing
+// inputs of the scan over the lsh + E experts: rank [T][kt] (rank of each
+// entry among its expert's entries in its route block), blk_counts
+// [nblk][ldc] and the totals per super block sup_cnt [nsup][ldc] (atomic adds)
+hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int lsh, int C, int kt,
+                                uint8_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
+                                int *sup_cnt, int rb, hipStream_t s);
 hipError_t launch_permute(PermuteArgs a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 // compute_loss(::SwitchTransformerLoss) on device buffers in two launches

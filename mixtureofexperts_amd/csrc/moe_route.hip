@@ -595,7 +595,8 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
     float my_g = 0.0f;
     if (out_gating && !a.given) {
         // routed slot this lane reports: rs minus the shared slots before it
-        const int jr = rs - (shared_gate ? ns : (soft ? 0 : a.lsh));
+        // (the layer's lsh shared experts, then SharedExpertGating's ns)
+        const int jr = rs - a.lsh - ns;
         uint64_t thr = ~0ull;
         float sg = 0.0f, sel_v = 0.0f;
         int sel_i = -1;
@@ -627,45 +628,45 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             sel_v = mine ? bv : sel_v;
         }
         const bool routed = jr >= 0 && jr < a.k;
+        if (a.lsh > 0 && rs < a.lsh) {
+            // forward_with_shared_experts: the layer's shared experts 1..lsh in
+            // slots 0..lsh-1 (their outputs are averaged, the gate is only
+            // reported); the gate's ids below are shifted by lsh
+            // (expert_indices .+= num_shared_experts, src/core/moe_layer.jl:172)
+            my_e = rs + 1;
+            my_g = 1.0f / (float)a.lsh;
+        }
         if (soft) {
             // SoftMoEGating: top-k of the scaled-softmax probabilities; the
             // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
             // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
+            // for the routed slot jr
             float pj = 0.0f;
-            const int src = (lane & ~7) | (rs / EPL);  // the lane holding expert rs (rs < 8)
+            const int jq = max(jr, 0);
+            const int src = (lane & ~7) | (jq / EPL);  // the lane holding expert jq (jq < k <= E)
 #pragma unroll
             for (int u = 0; u < EPL; ++u) {
                 const float wv2 = __shfl(pr[u], src);
-                pj = (u == rs % EPL) ? wv2 : pj;
+                pj = (u == jq % EPL) ? wv2 : pj;
             }
             if (routed) {
-                my_e = sel_i + 1;
+                my_e = sel_i + 1 + a.lsh;
                 my_g = pj;
             }
         } else if (shared_gate) {
-            // shared slots 0 .. ns-1 (gate 1/kt), then the routed top-k with
-            // gates scaled by 1 - ns/kt in Float64 (advanced.jl:80-108)
-            if (rs < ns) {
+            // the gate's shared slots (ids 1..ns, gate 1/kt of the gate's kt =
+            // ns + k), then the routed top-k with gates scaled by 1 - ns/kt
+            // in Float64 (advanced.jl:80-108)
+            const int kg = a.kt - a.lsh;
+            if (rs >= a.lsh && rs < a.lsh + ns) {
                 my_e = rs + 1;
-                my_g = 1.0f / (float)a.kt;
-            } else if (routed) {
-                my_e = sel_i + 1;
-                my_g = (float)((double)(sel_v / sg) * (1.0 - (double)ns / (double)a.kt));
-            }
-        } else if (a.lsh > 0) {
-            // forward_with_shared_experts: shared experts 1..lsh in slots
-            // 0..lsh-1 (their outputs are averaged, the gate is only
-            // reported), then the routed ids shifted by lsh (expert_indices
-            // .+= num_shared_experts, src/core/moe_layer.jl:172)
-            if (rs < a.lsh) {
-                my_e = rs + 1;
-                my_g = 1.0f / (float)a.lsh;
+                my_g = 1.0f / (float)kg;
             } else if (routed) {
                 my_e = sel_i + 1 + a.lsh;
-                my_g = sel_v / sg;
+                my_g = (float)((double)(sel_v / sg) * (1.0 - (double)ns / (double)kg));
             }
         } else if (routed) {
-            my_e = sel_i + 1;
+            my_e = sel_i + 1 + a.lsh;
             my_g = sel_v / sg;
         }
         if (!rvalid || (routed && sel_i < 0)) my_e = 0;
@@ -954,24 +955,32 @@ __global__ __launch_bounds__(256) void expert_choice_select_kernel(const float *
     }
 }
 
-// One thread per token: its slots hold the experts that took it in ascending
-// id order, at most kcap = min(C, E) of them (a later expert past the
-// capacity rows is left out, expert_choice.jl:40-50), gate = probability of
-// the expert for the token; the remaining slots of the kt are empty (id 0).
-// sel[t][e] becomes the slot + 1 of entry (t, e) (<= kcap <= 128), or 0 when
-// expert e did not take token t or the entry was left out.
+// One thread per token: with shared experts of the layer (lsh > 0) its
+// first lsh slots hold them (ids 1..lsh, gate 1/lsh reported); the next
+// slots hold the routed experts that took it in ascending id order, ids
+// shifted by lsh (src/core/moe_layer.jl:172), at most kcap = min(C, E) of
+// them (a later expert past the capacity rows is left out,
+// expert_choice.jl:40-50), gate = probability of the expert for the token;
+// the remaining slots of the kt are empty (id 0).  sel[t][e] becomes the
+// routed slot + 1 of entry (t, e) (<= kcap <= 128), or 0 when expert e did
+// not take token t or the entry was left out.
 __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__restrict__ sel,
                                                                      const float *__restrict__ probs, int T, int E,
-                                                                     int kt, int kcap, int *idx, float *gates) {
+                                                                     int kt, int kcap, int lsh, int *idx,
+                                                                     float *gates) {
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (t >= T) return;
+    for (int j = 0; j < lsh; ++j) {
+        idx[(long long)t * kt + j] = j + 1;
+        gates[(long long)t * kt + j] = 1.0f / (float)lsh;
+    }
     int c = 0;
     for (int e = 0; e < E; ++e) {
         const long long o = (long long)t * E + e;
         if (sel[o]) {
             if (c < kcap) {
-                idx[(long long)t * kt + c] = e + 1;
-                gates[(long long)t * kt + c] = probs[o];
+                idx[(long long)t * kt + lsh + c] = lsh + e + 1;
+                gates[(long long)t * kt + lsh + c] = probs[o];
                 sel[o] = (uint8_t)(c + 1);
             } else {
                 sel[o] = 0;
@@ -979,47 +988,54 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
             ++c;
         }
     }
-    for (int j = min(c, kcap); j < kt; ++j) {
+    for (int j = lsh + min(c, kcap); j < kt; ++j) {
         idx[(long long)t * kt + j] = 0;
         gates[(long long)t * kt + j] = 0.0f;
     }
 }
 
 // The bucketing inputs of the kept entries, per route block of rb
-// tokens: thread e walks the block's tokens in order; a token holds expert e
-// in at most one slot, so the entry's rank among expert e's entries of the
-// block (token-then-slot order, the bucket loop's) is the count of earlier
-// tokens that hold e.
+// tokens: thread e (of the lsh + E experts of the layer) walks the block's
+// tokens in order; a token holds expert e in at most one slot, so the
+// entry's rank among expert e's entries of the block (token-then-slot order,
+// the bucket loop's) is the count of earlier tokens that hold e.  A shared
+// expert e < lsh is held by every token, in slot e.
 __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
-                                                                            int E, int kt, int *rank,
+                                                                            int E, int kt, int lsh, int *rank,
                                                                             int *blk_counts, int ldc,
                                                                             int *sup_cnt, int rb) {
     const int e = threadIdx.x;
-    if (e >= E) return;
+    if (e >= lsh + E) return;
     const int t0 = blockIdx.x * rb;
     const int ntok = min(rb, T - t0);
     int c = 0;
-    for (int i = 0; i < ntok; ++i) {
-        const int sl = sel[(long long)(t0 + i) * E + e];
-        if (sl) {
-            rank[(long long)(t0 + i) * kt + sl - 1] = c;
-            ++c;
+    if (e < lsh) {
+        for (int i = 0; i < ntok; ++i) rank[(long long)(t0 + i) * kt + e] = i;
+        c = ntok;
+    } else {
+        for (int i = 0; i < ntok; ++i) {
+            const int sl = sel[(long long)(t0 + i) * E + (e - lsh)];
+            if (sl) {
+                rank[(long long)(t0 + i) * kt + lsh + sl - 1] = c;
+                ++c;
+            }
         }
     }
     blk_counts[(long long)blockIdx.x * ldc + e] = c;
     if (c) atomicAdd(&sup_cnt[(long long)(blockIdx.x / kSuper) * ldc + e], c);
 }
 
-hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int C, int kt, uint8_t *sel,
-                                int *idx, float *gates, int *rank, int *blk_counts, int ldc, int *sup_cnt,
-                                int rb, hipStream_t s) {
+hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int lsh, int C, int kt,
+                                uint8_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
+                                int *sup_cnt, int rb, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    if (E > MOE_MAX_EXPERTS || kt < min(C, E) || kt > 255 || ldc < E) return hipErrorInvalidValue;
+    if (lsh < 0 || lsh + E > MOE_MAX_EXPERTS || kt < lsh + min(C, E) || kt > 255 || ldc < lsh + E)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
-                       min(C, E), idx, gates);
+                       min(C, E), lsh, idx, gates);
     hipLaunchKernelGGL(expert_choice_rank_kernel, dim3((T + rb - 1) / rb), dim3(MOE_MAX_EXPERTS), 0, s, sel, T, E,
-                       kt, rank, blk_counts, ldc, sup_cnt, rb);
+                       kt, lsh, rank, blk_counts, ldc, sup_cnt, rb);
     return hipGetLastError();
 }
 
@@ -1033,13 +1049,19 @@ hipError_t launch_expert_choice(const float *logits, const float *probs, int T, 
 // counts Float32, target = total / E and the gradient in Float64, the
 // momentum stored as Float32 of a Float64 sum, the bias step in Float32, then
 // bias .-= mean(bias) with the Float32 sum taken in index order.
-__device__ inline void aux_free_step(const int *cnt, long long total, int E, float lr, float momentum,
-                                     float *bias, float *mom) {
+// With the layer's shared experts (lsh > 0) the indices are the gate's ids
+// shifted by lsh (forward_with_shared_experts, src/core/moe_layer.jl:172,
+// 182): the shared experts e < lsh hold none of them, except that `extra`
+// entries (an ExpertChoice matrix's empty entries, shifted to id lsh) count
+// for expert lsh - 1 (0-based).
+__device__ inline void aux_free_step(const int *cnt, int lsh, long long extra, long long total, int E, float lr,
+                                     float momentum, float *bias, float *mom) {
 #pragma clang fp contract(off)
     if (total <= 0) return;
     const double target = (double)total / (double)E;
     for (int e = 0; e < E; ++e) {
-        const double grad = ((double)(float)cnt[e] - target) / (double)total;
+        const long long ce = (e < lsh) ? (e == lsh - 1 ? extra : 0) : cnt[e];
+        const double grad = ((double)(float)ce - target) / (double)total;
         const float m = (float)((double)(momentum * mom[e]) + (double)(1.0f - momentum) * grad);
         mom[e] = m;
         bias[e] = bias[e] - lr * m;
@@ -1130,7 +1152,16 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
         // over the a.Np probability rows; with shared experts of the layer the
         // ids are the shifted routed ids and expert e < lsh holds none of them
         if (writer && e < a.Np) {
-            float f = (e < a.lsh) ? 0.0f : (float)ce;
+            float f = (float)ce;
+            if (e < a.lsh) {
+                // ExpertChoice's empty entries, shifted to id lsh (ec_empty)
+                long long empty = 0;
+                if (a.ec_empty && e == a.lsh - 1) {
+                    empty = (long long)a.T * a.kl;
+                    for (int r = a.lsh; r < a.E; ++r) empty -= L.tot[r];
+                }
+                f = (float)empty;
+            }
             if (a.T * a.kl > 0) f = f / total;
             const float P = (float)((double)L.ptot[e] / kPsumScale) / (float)a.T;
             L.fp[e] = f * P;
@@ -1222,10 +1253,13 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
         a.scalars[3] = (float)(hs / (double)a.T);
         if (a.loss_out) a.loss_out[0] = loss;
         if (a.aux_free && a.training && a.aux_update) {
-            // the kept entries of each expert are the counts after capacity
+            // the kept entries of each expert are the counts after capacity;
+            // with shared experts the loss's index matrix holds the routed
+            // entries (and ExpertChoice's empty ones, as id lsh)
             long long kept = 0;
-            for (int e = 0; e < a.E; ++e) kept += L.cnt[e];
-            aux_free_step(L.cnt, kept, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
+            for (int e = a.lsh; e < a.E; ++e) kept += L.cnt[e];
+            const long long empty = a.ec_empty ? (long long)a.T * a.kl - kept : 0;
+            aux_free_step(L.cnt, a.lsh, empty, kept + empty, a.E, a.aux_lr, a.aux_momentum, a.aux_bias, a.aux_mom);
         }
     }
     for (int e = tid; e <= a.E; e += nth) {
@@ -1719,18 +1753,21 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     if (a.kt > MOE_MAX_TOPK) {
         // more slots than a token's sort network holds: ExpertChoiceGating,
         // whose slots list the token's experts in ascending id order (empty
-        // and dropped slots have no position), so slot order is expert order
+        // and dropped slots have no position), so slot order is expert order;
+        // the layer's shared experts, if any, are slots 0..lsh-1 (ids 1..lsh)
         float *o = a.out + t * a.D;
         for (int d = lane; d < a.D; d += 64) {
-            float acc = 0.0f;
+            float acc = 0.0f, sh = 0.0f;
             for (int j = 0; j < a.kt; ++j) {
                 const long long ent = t * a.kt + j;
                 const int p = a.pos_of[ent];
                 if (p < 0) continue;
                 const long long off = (long long)p * a.ld_y + d;
                 const float v = a.y_bf16 ? bf16_to_f32(((const uint16_t *)a.y)[off]) : ((const float *)a.y)[off];
-                acc = acc + a.gates[ent] * v;
+                if (j < a.lsh) sh = sh + v / (float)a.lsh;
+                else acc = acc + a.gates[ent] * v;
             }
+            if (a.lsh > 0) acc = 0.5f * sh + 0.5f * acc;
             o[d] = acc;
         }
         return;
@@ -1916,7 +1953,7 @@ __global__ __launch_bounds__(256) void aux_free_update_kernel(const int *idx, lo
     }
     atomicAdd(&tot, mine);
     __syncthreads();
-    if (tid == 0) aux_free_step(cnt, (long long)tot, E, lr, momentum, bias, mom);
+    if (tid == 0) aux_free_step(cnt, 0, 0, (long long)tot, E, lr, momentum, bias, mom);
 }
 
 hipError_t launch_aux_free_update(const int *idx, long long n, int E, float lr, float momentum, float *bias,

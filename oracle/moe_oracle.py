@@ -360,18 +360,26 @@ def moe_forward(x_TD, router_w_ED, experts, *, gate="topk", k=2, num_shared=0, e
 
 
 def moe_forward_shared_experts(x_TD, router_w_ED, experts, num_shared, *, gate="topk", k=2, expert_type="gated",
-                               act="silu", alpha=0.01, z_weight=0.001, training=False, router_bias=None, logits=None):
+                               act="silu", alpha=0.01, z_weight=0.001, training=False, router_bias=None, logits=None,
+                               gate_param=None, gate_num_shared=0, aux_free=None):
     """forward_with_shared_experts + the z-loss of MoELayer's call
     (src/core/moe_layer.jl:107-128, 158-185), num_shared_experts = ns > 0.
 
     experts: all E experts, the first ns the shared ones; router_w_ED is the
     (E - ns, D) router.  shared = sum_i (y_i ./ ns) from zeros (:161-166);
-    the router's indices are shifted by ns (:172) and the routed experts run
-    through process_expert_forward! with the unshifted ids (:174-177);
-    output = 0.5f0 .* shared .+ 0.5f0 .* routed (:179-180); the Switch loss
-    takes the shifted indices and the (E - ns) router probabilities (:182),
-    so ids above E - ns are not counted (src/balancing/losses.jl:22-26); no
-    capacity constraint and no update_stats!.  Returns (out, loss, aux)."""
+    the router's gate (any of moe_forward's, with ``gate_param`` and
+    ``gate_num_shared`` for SharedExpertGating) runs on the plain logits (no
+    AuxiliaryFreeLoss bias: only forward_standard adds it, :137-140); its
+    indices are shifted by ns (:172), every entry, so an ExpertChoice
+    matrix's empty entries (0) become ns; the routed experts run through
+    process_expert_forward! with the unshifted ids (:174-177), empty entries
+    skipped; output = 0.5f0 .* shared .+ 0.5f0 .* routed (:179-180); the
+    balance loss takes the shifted indices and the (E - ns) router
+    probabilities (:182): the Switch loss counts ids 1..E - ns only
+    (src/balancing/losses.jl:22-26); an ``aux_free`` state (moe_forward's
+    dict, its bias over all E experts) is updated by update_bias! on the
+    shifted indices (src/balancing/auxiliary_free.jl:36-87).  No capacity
+    constraint and no update_stats!.  Returns (out, loss, aux)."""
     x = np.asarray(x_TD, np.float32)
     T = x.shape[0]
     ns = int(num_shared)
@@ -384,8 +392,9 @@ def moe_forward_shared_experts(x_TD, router_w_ED, experts, num_shared, *, gate="
         else:
             y = standard_expert(x, ex["w1"], ex["w2"], ex.get("b1"), ex.get("b2"), fn)
         shared = (shared + (y / np.float32(ns)).astype(np.float32)).astype(np.float32)
-    routed, _, ra = moe_forward(x, router_w_ED, experts[ns:], gate=gate, k=k, expert_type=expert_type, act=act,
-                                alpha=alpha, z_weight=0.0, training=False, router_bias=router_bias, logits=logits)
+    routed, _, ra = moe_forward(x, router_w_ED, experts[ns:], gate=gate, k=k, num_shared=gate_num_shared,
+                                expert_type=expert_type, act=act, alpha=alpha, z_weight=0.0, training=False,
+                                router_bias=router_bias, logits=logits, gate_param=gate_param)
     half = np.float32(0.5)
     out = ((half * shared).astype(np.float32) + (half * routed).astype(np.float32)).astype(np.float32)
     shifted = (ra["idx"] + ns).astype(np.int32)
@@ -393,13 +402,21 @@ def moe_forward_shared_experts(x_TD, router_w_ED, experts, num_shared, *, gate="
     sw = np.float32(0.0)
     zl = np.float32(0.0)
     if training:
-        sw = switch_loss(shifted, ra["probs"], alpha)
+        if aux_free is not None:
+            aux_free["counter"] += 1
+            if aux_free["counter"] % aux_free["update_freq"] == 0:
+                aux_free_update_bias(shifted, aux_free["bias"], aux_free["mom"], aux_free["lr"], aux_free["momentum"])
+            sw = np.float32(np.float32(aux_free["cw"]) * switch_loss(shifted, ra["probs"], 1.0)) \
+                if aux_free["use_comp"] else np.float32(0.0)
+        else:
+            sw = switch_loss(shifted, ra["probs"], alpha)
         loss = sw
         if z_weight > 0:
             zl = z_loss(ra["logits"], z_weight)
             loss = np.float32(loss + zl)
     aux = dict(logits=ra["logits"], idx=shifted, gates=ra["gates"], probs=ra["probs"], routed_idx=ra["idx"],
-               routed_counts=ra["counts"], shared=shared, routed=routed, switch_loss=sw, z_loss=zl)
+               routed_counts=ra["counts"], shared=shared, routed=routed, switch_loss=sw, z_loss=zl,
+               mean_entropy=ra["mean_entropy"])
     return out, loss, aux
 
 

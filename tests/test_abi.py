@@ -68,10 +68,13 @@ def _cfg(**kw):
     (dict(num_shared_experts=-1), "num_shared_experts"),
     (dict(num_shared_experts=7), "top_k"),
     (dict(num_shared_experts=2, top_k=7, num_experts=16), "MOE_MAX_TOPK"),
-    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1), "SharedExpertGating"),
+    # with the layer's shared experts the gate sees num_experts - num_shared_experts experts
+    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=6), "gate_num_shared"),
+    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1, top_k=6, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=3, top_k=4), "top_k"),
     (dict(gate_kind=4, gate_param=0.0), "capacity_factor"),
     (dict(gate_kind=3, top_k=9), "top_k"),
-    (dict(gate_kind=3, num_shared_experts=1), "TopKGating or SwitchGating"),
+    (dict(gate_kind=3, num_shared_experts=7), "top_k"),
 ])
 def test_create_rejects_bad_config(moe, bad, msg):
     from mixtureofexperts_amd import _lib
@@ -82,6 +85,27 @@ def test_create_rejects_bad_config(moe, bad, msg):
     assert rc == _lib.MOE_EINVAL
     assert h.value is None
     assert msg in L.moe_last_error(None).decode()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kw,slots,router_rows", [
+    (dict(num_shared_experts=1, gate_kind=3, top_k=2, gate_param=0.5), 3, 7),      # SoftMoEGating
+    (dict(num_shared_experts=2, gate_kind=4, gate_param=1.0), 2 + 6, 6),           # ExpertChoice: 2 + min(C=11, 6)
+    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1, top_k=2), 5, 6),  # SharedExpertGating
+])
+def test_create_accepts_shared_experts_with_every_gate(moe, kw, slots, router_rows):
+    # forward_with_shared_experts runs whatever gate the layer holds
+    # (src/core/moe_layer.jl:158-185): the shared slots plus the gate's
+    from mixtureofexperts_amd import _lib
+
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.moe_create(ctypes.byref(_cfg(**kw)), ctypes.byref(h)) == _lib.MOE_OK
+    try:
+        assert L.moe_slots_per_token(h) == slots
+        assert L.moe_router_outputs(h) == router_rows
+    finally:
+        L.moe_destroy(h)
 
 
 def test_null_handle_calls_fail_cleanly(moe):

@@ -24,7 +24,7 @@ class Case:
 
     def __init__(self, moe, oracle, *, T, D, H, Dout=None, E, k, gate="topk", ns=0, expert_type="gated", act="silu",
                  wdtype="f32", xdtype="f32", seed=0, router_bias=None, alpha=0.01, z=0.001, drop=False, cf=1.25,
-                 max_tokens=None, wscale=None, lsh=0, init="he"):
+                 max_tokens=None, wscale=None, lsh=0, init="he", gate_param=None):
         from mixtureofexperts_amd import _lib
         from mixtureofexperts_amd._device import DeviceLayer, GateSpec
 
@@ -78,8 +78,11 @@ class Case:
                 dev_ex.append(dict(src=_lib.MOE_F32, w=mats, s=[None] * 3))
             self.ex.append(dict(w1=ov[0], w2=ov[1], w3=ov[2], b1=b1, b2=b2))
             dev_ex[-1]["b"] = (b1, b2)
+        self.gate_param = gate_param
         spec = {"topk": GateSpec(_lib.MOE_GATE_TOPK, k, 0), "switch": GateSpec(_lib.MOE_GATE_SWITCH, 1, 0),
-                "shared": GateSpec(_lib.MOE_GATE_SHARED, k, ns)}[gate]
+                "shared": GateSpec(_lib.MOE_GATE_SHARED, k, ns),
+                "soft": GateSpec(_lib.MOE_GATE_SOFT, k, 0, gate_param or 0.0),
+                "expert_choice": GateSpec(_lib.MOE_GATE_EXPERT_CHOICE, 1, 0, gate_param or 0.0)}[gate]
         acts = {"silu": _lib.MOE_ACT_SILU, "gelu": _lib.MOE_ACT_GELU, "relu": _lib.MOE_ACT_RELU,
                 "identity": _lib.MOE_ACT_IDENTITY}
         wcode = {"f32": _lib.MOE_F32, "bf16": _lib.MOE_BF16, "fp8": _lib.MOE_FP8_E4M3}[wdtype]
@@ -135,21 +138,41 @@ def check_case(case, tol, training=True, T=None):
     return out, err
 
 
-def check_shared_experts_case(case, tol, training=True):
+def check_shared_experts_case(case, tol, training=True, aux_free=None):
     """forward_with_shared_experts (num_shared_experts = lsh > 0) against the
-    oracle on the GPU's router logits."""
+    oracle on the GPU's router logits; ``aux_free``: an AuxiliaryFreeLoss
+    state dict of the oracle's (bias over all E experts), loaded into the
+    handle first and compared after the call."""
+    import ctypes
+
+    from mixtureofexperts_amd import _lib
+
+    if aux_free is not None:
+        st = aux_free
+        _lib.check(_lib.lib().moe_set_aux_free(
+            case.dev.h, 1, st["bias"].ctypes.data, st["mom"].ctypes.data, st["lr"], st["momentum"],
+            st["update_freq"], st["counter"], int(st["use_comp"]), st["cw"]), case.dev.h)
     out, loss, res = case.run(training)
     T, lsh, k, E = case.T, case.lsh, case.k, case.E
     ref_logits = (case.x @ case.wr.T).astype(np.float32)
     assert np.max(np.abs(res["logits"] - ref_logits)) <= 1e-5 * max(1.0, np.max(np.abs(ref_logits)))
     ref_out, ref_loss, aux = case.oracle.moe_forward_shared_experts(
         case.x, case.wr, case.ex, lsh, gate=case.gate, k=k, expert_type=case.expert_type, act=case.act,
-        alpha=case.alpha, z_weight=case.z, training=training, logits=res["logits"])
-    # slots: the shared experts 1..lsh, then the shifted routed ids, bit-exact
-    assert res["indices"].shape == (T, lsh + k)
+        alpha=case.alpha, z_weight=case.z, training=training, logits=res["logits"], gate_param=case.gate_param,
+        gate_num_shared=case.ns, aux_free=aux_free)
+    # slots: the shared experts 1..lsh, then the gate's shifted ids, bit-exact
+    # (ExpertChoice: lsh + min(C, E - lsh) slots, empty ones 0 on the device
+    # where the oracle's shifted matrix holds lsh)
+    kg = aux["idx"].shape[1]
+    kd = res["indices"].shape[1] - lsh
+    n = min(kg, kd)
+    routed = np.where(aux["routed_idx"] > 0, aux["routed_idx"] + lsh, 0).astype(np.int32)
+    if case.gate != "expert_choice":
+        assert kd == kg
     assert np.array_equal(res["indices"][:, :lsh], np.tile(np.arange(1, lsh + 1, dtype=np.int32), (T, 1)))
-    assert np.array_equal(res["indices"][:, lsh:], aux["idx"])
-    assert np.array_equal(res["gates"][:, lsh:].view(np.uint32), aux["gates"].view(np.uint32))
+    assert np.array_equal(res["indices"][:, lsh:lsh + n], routed[:, :n])
+    assert np.all(routed[:, n:] == 0) and np.all(res["indices"][:, lsh + n:] == 0)
+    assert np.array_equal(res["gates"][:, lsh:lsh + n].view(np.uint32), aux["gates"][:, :n].view(np.uint32))
     assert np.array_equal(res["probs"].view(np.uint32), aux["probs"].view(np.uint32))
     assert np.array_equal(res["counts"][:lsh], np.full(lsh, T, np.int32))
     assert np.array_equal(res["counts"][lsh:], aux["routed_counts"])
@@ -160,7 +183,62 @@ def check_shared_experts_case(case, tol, training=True):
         assert abs(res["switch_loss"] - aux["switch_loss"]) <= 1e-5 * max(1.0, abs(float(aux["switch_loss"])))
     else:
         assert loss == 0.0
+    if aux_free is not None:
+        # update_bias! over the shifted ids, the same Float32 / Float64 steps
+        bias, mom, cnt = np.zeros(E, np.float32), np.zeros(E, np.float32), ctypes.c_int64(0)
+        _lib.check(_lib.lib().moe_get_aux_free(case.dev.h, bias.ctypes.data, mom.ctypes.data, ctypes.byref(cnt)),
+                   case.dev.h)
+        assert cnt.value == aux_free["counter"]
+        assert np.array_equal(bias.view(np.uint32), aux_free["bias"].view(np.uint32)), (bias, aux_free["bias"])
+        assert np.array_equal(mom.view(np.uint32), aux_free["mom"].view(np.uint32))
     return out, err
+
+
+@pytest.mark.parametrize("gate,lsh,k,ns,E,param,wdtype,T", [
+    ("soft", 1, 2, 0, 9, 0.5, "bf16", 500),              # SoftMoEGating: slot gate = p of expert `slot`
+    ("soft", 2, 3, 0, 8, 1.0, "f32", 300),
+    ("expert_choice", 1, 1, 0, 5, 1.0, "f32", 400),      # empty entries count as id lsh in the loss
+    ("expert_choice", 2, 1, 0, 10, 1.25, "bf16", 512),   # lsh + min(C, 8) = 10 slots per token
+    ("shared", 2, 2, 1, 9, None, "bf16", 500),           # SharedExpertGating(1, TopKGating(2), 7)
+    ("shared", 1, 3, 2, 12, None, "fp8", 400),
+])
+def test_shared_experts_with_every_gate(moe, oracle, gate, lsh, k, ns, E, param, wdtype, T):
+    # forward_with_shared_experts runs whatever gate the router holds
+    # (src/core/moe_layer.jl:158-185): the gate's ids shifted by lsh, the
+    # balance loss on the shifted ids, the output blended 0.5 / 0.5
+    c = Case(moe, oracle, T=T, D=128, H=192, E=E, k=k, gate=gate, ns=ns, wdtype=wdtype,
+             xdtype="bf16" if wdtype != "f32" else "f32", seed=90 + E, lsh=lsh, gate_param=param)
+    try:
+        check_shared_experts_case(c, TOL[wdtype], training=True)
+        check_shared_experts_case(c, TOL[wdtype], training=False)
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("gate,lsh,k,E,param,update_freq", [
+    ("topk", 1, 2, 7, None, 1),
+    ("topk", 2, 2, 8, None, 2),             # the second call updates
+    ("expert_choice", 1, 1, 5, 1.0, 1),     # empty entries count for bias index lsh - 1
+    ("switch", 3, 1, 9, None, 1),
+])
+def test_shared_experts_aux_free_loss(moe, oracle, gate, lsh, k, E, param, update_freq):
+    # AuxiliaryFreeLoss with shared experts: the gate sees the plain logits
+    # (the bias is not applied: a large bias on one expert does not move the
+    # routing), update_bias! and the complementary loss take the shifted ids,
+    # and the bias covers all E experts (src/core/moe_layer.jl:158-185,
+    # src/balancing/auxiliary_free.jl:36-87).  Three training calls; bias,
+    # momentum and counter bit-exact after each.
+    c = Case(moe, oracle, T=300, D=64, H=96, E=E, k=k, gate=gate, wdtype="f32", seed=95 + E, lsh=lsh,
+             gate_param=param)
+    try:
+        bias0 = np.zeros(E, np.float32)
+        bias0[lsh] = 50.0  # would win every token if the gate added it
+        st = dict(bias=bias0, mom=np.zeros(E, np.float32), lr=0.01, momentum=0.9, update_freq=update_freq,
+                  counter=0, use_comp=True, cw=0.001)
+        for _ in range(3):
+            check_shared_experts_case(c, TOL["f32"], training=True, aux_free=st)
+    finally:
+        c.dev.close()
 
 
 @pytest.mark.parametrize("lsh,k,E,gate,etype,act,wdtype,xdtype", [

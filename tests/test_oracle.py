@@ -515,6 +515,77 @@ def test_shared_experts_switch_loss_counts_shifted_ids(oracle):
     assert loss_z == np.float32(aux_z["switch_loss"] + aux_z["z_loss"])
 
 
+def test_shared_experts_expert_choice_empty_entries_count_as_id_ns(oracle):
+    # ExpertChoiceGating under shared experts: the (C, T) index matrix's empty
+    # entries are shifted to id ns like every other entry (:172), so the Switch
+    # loss counts them for expert ns when ns <= E - ns.  E = 5, ns = 1, four
+    # routed experts, T = 10, capacity_factor 1.0: C = ceil(10 / 4) = 3 rows,
+    # brute-force f over the shifted matrix against the probability means; the
+    # output ignores the empty entries (process_expert_forward! skips id 0).
+    rng = np.random.default_rng(27)
+    T, D, H, E, ns = 10, 8, 8, 5, 1
+    x, ex = _shared_case(rng, T, D, H, E)
+    wr = rng.standard_normal((E - ns, D)).astype(np.float32)
+    alpha = 0.01
+    out, loss, aux = oracle.moe_forward_shared_experts(x, wr, ex, ns, gate="expert_choice", gate_param=1.0,
+                                                       training=True, alpha=alpha, z_weight=0.0)
+    C, N = 3, E - ns
+    assert aux["idx"].shape == (T, C)
+    empty = int(np.sum(aux["routed_idx"] == 0))
+    assert empty > 0 and np.sum(aux["idx"] == ns) == empty
+    f = [sum(1 for t in range(T) for j in range(C) if aux["idx"][t, j] == e + 1) / (C * T) for e in range(N)]
+    assert f[ns - 1] == empty / (C * T)
+    P = [float(np.mean(aux["probs"][:, e].astype(np.float64))) for e in range(N)]
+    assert abs(float(loss) - alpha * N * sum(fe * pe for fe, pe in zip(f, P))) < 1e-7
+    # routed output = the forward_standard of the routed experts on the same gate
+    std, _, _ = oracle.moe_forward(x, wr, ex[ns:], gate="expert_choice", gate_param=1.0, logits=aux["logits"])
+    assert np.array_equal(aux["routed"], std)
+
+
+def test_shared_experts_aux_free_updates_over_shifted_ids(oracle):
+    # AuxiliaryFreeLoss under shared experts: the gate runs on the plain
+    # logits (no bias) and update_bias! counts the shifted ids over a bias of
+    # all E experts.  E = 3, ns = 1, k = 1, a router that sends every token to
+    # routed expert 1 (shifted id 2): counts (0, T, 0), target T / 3, so the
+    # gradient is (-1/3, 2/3, -1/3) and, from zero momentum, the bias moves by
+    # -lr (1 - m) grad (mean 0, so the centring step leaves it); the bias
+    # (0, -100, 100), which would send every token to id 3 if the gate saw
+    # it, does not change the routing.
+    rng = np.random.default_rng(28)
+    T, D, H, E, ns = 12, 8, 8, 3, 1
+    x, ex = _shared_case(rng, T, D, H, E)
+    lg = np.tile(np.array([[4.0, -4.0]], np.float32), (T, 1))
+    lr, m = 0.01, 0.9
+    b0 = np.array([0.0, -100.0, 100.0], np.float32)
+    st = dict(bias=b0.copy(), mom=np.zeros(3, np.float32), lr=lr, momentum=m, update_freq=1, counter=0,
+              use_comp=True, cw=0.001)
+    _, loss, aux = oracle.moe_forward_shared_experts(x, None, ex, ns, k=1, training=True, z_weight=0.0,
+                                                     logits=lg, aux_free=st)
+    assert np.all(aux["idx"] == 2)
+    g = np.array([-1.0 / 3.0, 2.0 / 3.0, -1.0 / 3.0])
+    assert np.allclose(st["bias"], b0 - lr * (1 - m) * g, rtol=0, atol=3e-5)
+    assert np.allclose(st["mom"], (1 - m) * g, rtol=0, atol=1e-7)
+    assert st["counter"] == 1
+    # complementary loss: cw * Switch(1) over the shifted ids (id 2 of N = 2)
+    p = oracle.softmax(lg)
+    assert abs(float(loss) - 0.001 * 1.0 * 2 * 1.0 * float(np.mean(p[:, 1].astype(np.float64)))) < 1e-9
+
+
+def test_shared_experts_with_shared_expert_gating(oracle):
+    # SharedExpertGating(g, TopKGating(k), E - ns) under the layer's ns shared
+    # experts: the gate's own shared ids 1..g and its routed ids are shifted
+    # by ns; the gate's slot gates are those of compute_gates_shared on the
+    # same logits (1/(g + k) and the scaled top-k)
+    rng = np.random.default_rng(29)
+    T, D, H, E, ns, g, k = 20, 8, 8, 9, 2, 1, 2
+    x, ex = _shared_case(rng, T, D, H, E)
+    wr = rng.standard_normal((E - ns, D)).astype(np.float32)
+    _, _, aux = oracle.moe_forward_shared_experts(x, wr, ex, ns, gate="shared", gate_num_shared=g, k=k)
+    i0, g0, _ = oracle.compute_gates_shared(aux["logits"], g, k)
+    assert np.array_equal(aux["idx"], i0 + ns) and np.array_equal(aux["gates"], g0)
+    assert np.all(aux["idx"][:, 0] == ns + 1)
+
+
 # ---- SoftMoEGating / ExpertChoiceGating ------------------------------------------
 
 def test_soft_gating_closed_forms(oracle):
