@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 #define MOE_ABI_VERSION 1
-#define MOE_MAX_TOPK 8        /* maximum slots per token of the top-k gates (shared + routed) */
+#define MOE_MAX_TOPK 16       /* maximum slots per token of the top-k gates (shared + routed) */
 #define MOE_MAX_EXPERTS 128   /* maximum experts seen by one router */
 
 typedef enum {

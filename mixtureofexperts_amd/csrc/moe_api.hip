@@ -227,14 +227,14 @@ static int validate_config(const moe_config *c, std::string &why) {
     const int Er = c->num_experts - lsh;
     if (c->gate_kind == MOE_GATE_TOPK || c->gate_kind == MOE_GATE_SWITCH || c->gate_kind == MOE_GATE_SOFT) {
         if (k < 1 || k > Er) { why = "top_k must be in [1, num_experts - num_shared_experts]"; return 0; }
-        if (lsh + k > MOE_MAX_TOPK) { why = "num_shared_experts + top_k above MOE_MAX_TOPK (8)"; return 0; }
+        if (lsh + k > MOE_MAX_TOPK) { why = "num_shared_experts + top_k above MOE_MAX_TOPK (16)"; return 0; }
     } else if (c->gate_kind == MOE_GATE_EXPERT_CHOICE) {
         if (!(c->gate_param > 0.0f)) { why = "ExpertChoiceGating capacity_factor (gate_param) must be > 0"; return 0; }
     } else if (c->gate_kind == MOE_GATE_SHARED) {
         const int ns = c->gate_num_shared;
         if (ns < 0 || ns >= Er) { why = "gate_num_shared must be in [0, num_experts - num_shared_experts)"; return 0; }
         if (k < 1 || k > Er - ns) { why = "top_k must be in [1, num_experts - num_shared_experts - num_shared]"; return 0; }
-        if (lsh + ns + k > MOE_MAX_TOPK) { why = "num_shared_experts + num_shared + top_k above MOE_MAX_TOPK (8)"; return 0; }
+        if (lsh + ns + k > MOE_MAX_TOPK) { why = "num_shared_experts + num_shared + top_k above MOE_MAX_TOPK (16)"; return 0; }
     } else {
         why = "unknown gate_kind";
         return 0;

@@ -88,10 +88,27 @@ struct DecodeRouteLds {
     __attribute__((aligned(16))) float part[4][MOE_MAX_EXPERTS];  // per-wave logit partials
 };
 
+// The routed slots' experts of one token (0-based), 16 bits each: slot j in
+// bits [16 (j % 4), +16) of word j / 4 (wave-uniform; k <= 16).
+struct DecodeSel {
+    unsigned long long w[4] = {0ull, 0ull, 0ull, 0ull};
+    __device__ __forceinline__ void set(int j, int e) {
+        const unsigned long long v = (unsigned long long)e << (16 * (j & 3));
+        if (j < 4) w[0] |= v;
+        else if (j < 8) w[1] |= v;
+        else if (j < 12) w[2] |= v;
+        else w[3] |= v;
+    }
+    __device__ __forceinline__ int get(int j) const {
+        const unsigned long long v = j < 4 ? w[0] : (j < 8 ? w[1] : (j < 12 ? w[2] : w[3]));
+        return (int)((v >> (16 * (j & 3))) & 0xffffu);
+    }
+};
+
 // compute_gates of token t from the wave partials in L (see decode_route_block);
 // HI: E > 64, lane l also holds expert l + 64 (E <= 64: decode_gates64).
 template <bool HI>
-__device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, int t, bool write,
+__device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bool write,
                                                            const DecodeRouteLds &L, float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, E = a.E;
@@ -161,14 +178,14 @@ __device__ __forceinline__ unsigned long long decode_gates(const DecodeArgs &a, 
 #undef MOE_LANE_OF
     float ssum = 0.0f, myp = 0.0f;
     int mye = 0;
-    unsigned long long packed = 0ull;
+    DecodeSel packed;
     for (int j = 0; j < a.k; ++j) {
         const unsigned long long b0 = __ballot(lane < E && rank[0] == j);
         const unsigned long long b1 = HI ? __ballot(lane + 64 < E && rank[NH - 1] == j) : 0ull;
         const int e = b0 ? __builtin_ctzll(b0) : 64 + __builtin_ctzll(b1);
         const float pj = readlane_f(HI && e >= 64 ? pv[NH - 1] : pv[0], e & 63);
         ssum = (j == 0) ? pj : ssum + pj;  // slot order
-        packed |= (unsigned long long)e << (8 * j);
+        packed.set(j, e);
         if (lane == j) {
             myp = pj;
             mye = e;
@@ -230,7 +247,7 @@ __device__ __forceinline__ float wave_fmax(float v, bool rows4) {  // v never Na
 // adding exact zeros; the k slots are k rounds of "largest isless key, lowest
 // expert among equal keys", the partialsortperm order that decode_gates
 // derives from ranks.
-__device__ __forceinline__ unsigned long long decode_gates64(const DecodeArgs &a, int t, bool write,
+__device__ __forceinline__ DecodeSel decode_gates64(const DecodeArgs &a, int t, bool write,
                                                              const DecodeRouteLds &L, float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, E = a.E;
@@ -253,13 +270,13 @@ __device__ __forceinline__ unsigned long long decode_gates64(const DecodeArgs &a
     uint32_t key = valid ? isless_key(p) : 0u;  // every float's key is > 0
     float ssum = 0.0f, myp = 0.0f;
     int mye = 0;
-    unsigned long long packed = 0ull;
+    DecodeSel packed;
     for (int j = 0; j < a.k; ++j) {
         const uint32_t mk = wave_umax(key, rows4);
         const int e = __builtin_ctzll(__ballot(valid && key == mk));
         const float pj = readlane_f(p, e);
         ssum = (j == 0) ? pj : ssum + pj;  // slot order
-        packed |= (unsigned long long)e << (8 * j);
+        packed.set(j, e);
         if (lane == e) key = 0u;  // taken
         if (lane == j) {
             myp = pj;
@@ -296,10 +313,10 @@ __device__ __forceinline__ unsigned long long decode_gates64(const DecodeArgs &a
 // keys (partialsortperm(p, 1:k, rev=true)): the rank of expert i is the number
 // of experts before it in that order; the gates are p of the slots over their
 // sum in slot order.  Lane l holds experts l and, for E > 64, l + 64.
-// Returns the 0-based expert of routed slot j in bits [8 j, 8 j + 8)
-// (uniform), and in `gate` of lane j < k that slot's gate; `write` (wave 0 of
+// Returns the 0-based experts of the routed slots (uniform), and in `gate`
+// of lane j < k that slot's gate; `write` (wave 0 of
 // one block per token) stores logits, probs, indices, gates.
-__device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L,
+__device__ DecodeSel decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L,
                                                  float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -367,7 +384,7 @@ __device__ unsigned long long decode_route_block(const DecodeArgs &a, int t, boo
 // (W3_e row j) . x over all Hpad rows (pad rows have zero weights, so their h
 // is 0 and the down products may run over Hpad).
 template <int WT>
-__device__ __forceinline__ void decode_up_units(const DecodeArgs &a, int t, int v, int nv, unsigned long long sel) {
+__device__ __forceinline__ void decode_up_units(const DecodeArgs &a, int t, int v, int nv, const DecodeSel &sel) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int units = a.kt * a.Hpad;
@@ -379,8 +396,8 @@ __device__ __forceinline__ void decode_up_units(const DecodeArgs &a, int t, int 
         const int s0 = u0 / a.Hpad, j0 = u0 - s0 * a.Hpad;
         const int s1 = u1 / a.Hpad, j1 = u1 - s1 * a.Hpad;
         // expert of a slot: shared s < lsh, else routed lsh + (slot s - lsh's pick)
-        const int e0 = s0 < a.lsh ? s0 : a.lsh + (int)((sel >> (8 * (s0 - a.lsh))) & 0xff);
-        const int e1 = s1 < a.lsh ? s1 : a.lsh + (int)((sel >> (8 * (s1 - a.lsh))) & 0xff);
+        const int e0 = s0 < a.lsh ? s0 : a.lsh + sel.get(s0 - a.lsh);
+        const int e1 = s1 < a.lsh ? s1 : a.lsh + sel.get(s1 - a.lsh);
         const bool ok0 = e0 >= 0 && e0 < a.E + a.lsh, ok1 = e1 >= 0 && e1 < a.E + a.lsh;
         const long long r0 = (long long)(ok0 ? e0 : 0) * a.w1_stride + (long long)j0 * a.Dpad;
         const long long r1 = (long long)(ok1 ? e1 : 0) * a.w1_stride + (long long)j1 * a.Dpad;
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a) {
     __shared__ DecodeRouteLds L;
     const int w = threadIdx.x >> 6;
     float gate;
-    const unsigned long long sel = decode_route_block(a, blockIdx.x, blockIdx.y == 0 && w == 0, L, gate);
+    const DecodeSel sel = decode_route_block(a, blockIdx.x, blockIdx.y == 0 && w == 0, L, gate);
     decode_up_units<WT>(a, blockIdx.x, blockIdx.y * 4 + w, gridDim.y * 4, sel);
 }
 

@@ -112,7 +112,7 @@ __device__ __forceinline__ void rt_dma16(const void *gaddr, uint32_t lds) {
 }
 __device__ __forceinline__ void rt_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-constexpr int kRtMaskWords = 16;  // rank bitmask words per expert: TB * kt <= 64 * 8 entries
+constexpr int kRtMaskWords = 16;  // rank bitmask words per expert: TB * kt <= 512 entries (TB <= 32 when kt > 8)
 
 // The partner lane of butterfly step 1, 2, 3 inside an 8-lane group, by DPP:
 // lane ^ 1, lane ^ 2 (quad permutations), then the mirrored lane of the other
@@ -590,16 +590,22 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         if (!a.given) load_pr();
     }
 
-    // ---- top-k and gates; the entry of this lane (slot rs of the token) ----
-    int my_e = 0;  // 1-based expert of entry (rt, rs), 0: none
-    float my_g = 0.0f;
+    // ---- top-k and gates; the entries of this lane: slots rs and rs + 8 of
+    // its token (kt <= 16 = 2 x 8 lanes) ----
+    constexpr int SPL = 2;
+    const int spl = a.kt > 8 ? 2 : 1;  // slot passes in use
+    int my_e[SPL] = {0, 0};            // 1-based expert of entry (rt, rs + 8 p), 0: none
+    float my_g[SPL] = {0.0f, 0.0f};
     if (out_gating && !a.given) {
-        // routed slot this lane reports: rs minus the shared slots before it
+        // routed slot of each pass: its slot minus the shared slots before it
         // (the layer's lsh shared experts, then SharedExpertGating's ns)
-        const int jr = rs - a.lsh - ns;
+        int jr[SPL];
+#pragma unroll
+        for (int p = 0; p < SPL; ++p) jr[p] = rs + 8 * p - a.lsh - ns;
         uint64_t thr = ~0ull;
-        float sg = 0.0f, sel_v = 0.0f;
-        int sel_i = -1;
+        float sg = 0.0f;
+        float sel_v[SPL] = {0.0f, 0.0f};
+        int sel_i[SPL] = {-1, -1};
 #pragma unroll 1
         for (int r = 0; r < a.k; ++r) {
             uint64_t best = 0ull;
@@ -623,69 +629,91 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
             }
             thr = best;
             sg = (r == 0) ? bv : sg + bv;  // gate sum in slot order
-            const bool mine = r == jr;
-            sel_i = mine ? (int)~(uint32_t)best : sel_i;
-            sel_v = mine ? bv : sel_v;
-        }
-        const bool routed = jr >= 0 && jr < a.k;
-        if (a.lsh > 0 && rs < a.lsh) {
-            // forward_with_shared_experts: the layer's shared experts 1..lsh in
-            // slots 0..lsh-1 (their outputs are averaged, the gate is only
-            // reported); the gate's ids below are shifted by lsh
-            // (expert_indices .+= num_shared_experts, src/core/moe_layer.jl:172)
-            my_e = rs + 1;
-            my_g = 1.0f / (float)a.lsh;
-        }
-        if (soft) {
-            // SoftMoEGating: top-k of the scaled-softmax probabilities; the
-            // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
-            // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
-            // for the routed slot jr
-            float pj = 0.0f;
-            const int jq = max(jr, 0);
-            const int src = (lane & ~7) | (jq / EPL);  // the lane holding expert jq (jq < k <= E)
 #pragma unroll
-            for (int u = 0; u < EPL; ++u) {
-                const float wv2 = __shfl(pr[u], src);
-                pj = (u == jq % EPL) ? wv2 : pj;
+            for (int p = 0; p < SPL; ++p) {
+                const bool mine = r == jr[p];
+                sel_i[p] = mine ? (int)~(uint32_t)best : sel_i[p];
+                sel_v[p] = mine ? bv : sel_v[p];
             }
-            if (routed) {
-                my_e = sel_i + 1 + a.lsh;
-                my_g = pj;
-            }
-        } else if (shared_gate) {
-            // the gate's shared slots (ids 1..ns, gate 1/kt of the gate's kt =
-            // ns + k), then the routed top-k with gates scaled by 1 - ns/kt
-            // in Float64 (advanced.jl:80-108)
-            const int kg = a.kt - a.lsh;
-            if (rs >= a.lsh && rs < a.lsh + ns) {
-                my_e = rs + 1;
-                my_g = 1.0f / (float)kg;
-            } else if (routed) {
-                my_e = sel_i + 1 + a.lsh;
-                my_g = (float)((double)(sel_v / sg) * (1.0 - (double)ns / (double)kg));
-            }
-        } else if (routed) {
-            my_e = sel_i + 1 + a.lsh;
-            my_g = sel_v / sg;
         }
-        if (!rvalid || (routed && sel_i < 0)) my_e = 0;
-    } else if (out_gating && rvalid && rs < a.kt) {
+#pragma unroll
+        for (int p = 0; p < SPL; ++p) {
+            if (p >= spl) break;
+            const int q = rs + 8 * p;  // the slot of this pass
+            const bool routed = jr[p] >= 0 && jr[p] < a.k;
+            if (a.lsh > 0 && q < a.lsh) {
+                // forward_with_shared_experts: the layer's shared experts 1..lsh in
+                // slots 0..lsh-1 (their outputs are averaged, the gate is only
+                // reported); the gate's ids below are shifted by lsh
+                // (expert_indices .+= num_shared_experts, src/core/moe_layer.jl:172)
+                my_e[p] = q + 1;
+                my_g[p] = 1.0f / (float)a.lsh;
+            }
+            if (soft) {
+                // SoftMoEGating: top-k of the scaled-softmax probabilities; the
+                // dispatch reads row `slot` of the (E, T) gate matrix, i.e. the
+                // probability of expert `slot` (advanced.jl:24-33, moe_layer.jl:200)
+                // for the routed slot jr
+                float pj = 0.0f;
+                const int jq = max(jr[p], 0);
+                const int src = (lane & ~7) | (jq / EPL);  // the lane holding expert jq (jq < k <= E)
+#pragma unroll
+                for (int u = 0; u < EPL; ++u) {
+                    const float wv2 = __shfl(pr[u], src);
+                    pj = (u == jq % EPL) ? wv2 : pj;
+                }
+                if (routed) {
+                    my_e[p] = sel_i[p] + 1 + a.lsh;
+                    my_g[p] = pj;
+                }
+            } else if (shared_gate) {
+                // the gate's shared slots (ids 1..ns, gate 1/kt of the gate's kt =
+                // ns + k), then the routed top-k with gates scaled by 1 - ns/kt
+                // in Float64 (advanced.jl:80-108)
+                const int kg = a.kt - a.lsh;
+                if (q >= a.lsh && q < a.lsh + ns) {
+                    my_e[p] = q + 1;
+                    my_g[p] = 1.0f / (float)kg;
+                } else if (routed) {
+                    my_e[p] = sel_i[p] + 1 + a.lsh;
+                    my_g[p] = (float)((double)(sel_v[p] / sg) * (1.0 - (double)ns / (double)kg));
+                }
+            } else if (routed) {
+                my_e[p] = sel_i[p] + 1 + a.lsh;
+                my_g[p] = sel_v[p] / sg;
+            }
+            if (!rvalid || (routed && sel_i[p] < 0)) my_e[p] = 0;
+        }
+    } else if (out_gating && rvalid) {
         // the caller's routing: ids outside 1..E are skipped, as the
         // dispatch's `expert_id > 0 && expert_id <= length(experts)` does
         // (src/core/moe_layer.jl:198)
-        const long long ent = t * a.kt + rs;
-        const int e = a.idx[ent];
-        my_e = (e >= 1 && e <= a.Eh) ? e : 0;
-        my_g = a.gates[ent];
+#pragma unroll
+        for (int p = 0; p < SPL; ++p) {
+            const int q = rs + 8 * p;
+            if (q < a.kt) {
+                const long long ent = t * a.kt + q;
+                const int e = a.idx[ent];
+                my_e[p] = (e >= 1 && e <= a.Eh) ? e : 0;
+                my_g[p] = a.gates[ent];
+            }
+        }
     }
 
     // ---- stable rank of each entry among the route block's entries of its
     // expert (entries in token-then-slot order, as the bucket loop visits them)
-    const int ent = rt * a.kt + rs;  // entry of this lane (rs < kt)
-    const bool has_ent = out_gating && rvalid && rs < a.kt && my_e > 0;
+    int ent[SPL];
+    bool has_ent[SPL];
+#pragma unroll
+    for (int p = 0; p < SPL; ++p) {
+        const int q = rs + 8 * p;
+        ent[p] = rt * a.kt + q;  // entry of this pass (q < kt)
+        has_ent[p] = out_gating && rvalid && q < a.kt && my_e[p] > 0;
+    }
     __syncthreads();  // emask cleared
-    if (has_ent) atomicOr(&emask[(my_e - 1) * kRtMaskWords + (ent >> 5)], 1u << (ent & 31));
+#pragma unroll
+    for (int p = 0; p < SPL; ++p)
+        if (has_ent[p]) atomicOr(&emask[(my_e[p] - 1) * kRtMaskWords + (ent[p] >> 5)], 1u << (ent[p] & 31));
     // route-block sums of the per-token loss terms (tokens rt: lane rs == 0),
     // in a fixed order: within a wave its 8 tokens in order (read lane by
     // lane: no LDS round trip per step), then the waves in order
@@ -716,15 +744,19 @@ __device__ __forceinline__ void rt_gate(const RtArgs &A, int out_mask, const flo
         wred[1][wv] = hterm;
     }
     __syncthreads();  // emask complete, wred and the probability rows written
-    if (has_ent) {
-        const unsigned *mk = &emask[(my_e - 1) * kRtMaskWords];
-        int rr = __popc(mk[ent >> 5] & ((1u << (ent & 31)) - 1u));
-        for (int wd = 0; wd < (ent >> 5); ++wd) rr += __popc(mk[wd]);
-        a.rank[t * a.kt + rs] = rr;
-    }
-    if (out_gating && rvalid && rs < a.kt) {
-        a.idx[t * a.kt + rs] = my_e;
-        a.gates[t * a.kt + rs] = my_g;
+#pragma unroll
+    for (int p = 0; p < SPL; ++p) {
+        const int q = rs + 8 * p;
+        if (has_ent[p]) {
+            const unsigned *mk = &emask[(my_e[p] - 1) * kRtMaskWords];
+            int rr = __popc(mk[ent[p] >> 5] & ((1u << (ent[p] & 31)) - 1u));
+            for (int wd = 0; wd < (ent[p] >> 5); ++wd) rr += __popc(mk[wd]);
+            a.rank[t * a.kt + q] = rr;
+        }
+        if (out_gating && rvalid && q < a.kt) {
+            a.idx[t * a.kt + q] = my_e[p];
+            a.gates[t * a.kt + q] = my_g[p];
+        }
     }
     const int TW = (ntok * a.kt + 31) >> 5;  // mask words in use
     for (int e = tid; e < a.Eh; e += kRtThreads) {
@@ -842,7 +874,10 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     // or 32 when 64-token workgroups would leave CUs idle (their x tile then
     // also takes fewer K passes) (the logits GEMM's row tiles are
     // compile-time: 1, 2 or 4)
-    const bool half = gemm && !paired && A.ncu > 0 && (a.T + 63) / 64 < A.ncu;
+    // more than 8 slots per token: 32-token workgroups at most (the rank
+    // bitmasks hold kRtMaskWords * 32 = 512 entries per expert)
+    const bool wide = (a.out_mask & ROUTE_OUT_GATING) && a.kt > 8;
+    const bool half = (gemm && !paired && A.ncu > 0 && (a.T + 63) / 64 < A.ncu) || wide;
     const int TB = gemm && paired ? 16 : (half ? 32 : 64);
     *tb = TB;
     A.TB = TB;
@@ -884,6 +919,7 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     default: MOE_RT(LG_, 0, 16, RT_);   \
     }
     if (!gemm) {
+        // (RT only shapes the logits GEMM, which this case does not run)
         if (epl == 1) MOE_RT(0, 0, 1, 4);
         MOE_RT_EPL(0, 4)
     }

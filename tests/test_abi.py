@@ -56,9 +56,9 @@ def _cfg(**kw):
     (dict(num_experts=129), "num_experts"),
     (dict(top_k=9), "top_k"),
     (dict(top_k=0), "top_k"),
-    (dict(top_k=9, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(top_k=17, num_experts=32), "MOE_MAX_TOPK"),
     (dict(gate_kind=2, gate_num_shared=8), "gate_num_shared"),
-    (dict(gate_kind=2, gate_num_shared=2, top_k=7, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(gate_kind=2, gate_num_shared=2, top_k=15, num_experts=32), "MOE_MAX_TOPK"),
     (dict(gate_kind=7), "gate_kind"),
     (dict(weight_dtype=5), "weight_dtype"),
     (dict(max_tokens=0), "max_tokens"),
@@ -67,10 +67,10 @@ def _cfg(**kw):
     (dict(num_shared_experts=8), "num_shared_experts"),
     (dict(num_shared_experts=-1), "num_shared_experts"),
     (dict(num_shared_experts=7), "top_k"),
-    (dict(num_shared_experts=2, top_k=7, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(num_shared_experts=2, top_k=15, num_experts=32), "MOE_MAX_TOPK"),
     # with the layer's shared experts the gate sees num_experts - num_shared_experts experts
     (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=6), "gate_num_shared"),
-    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1, top_k=6, num_experts=16), "MOE_MAX_TOPK"),
+    (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=1, top_k=14, num_experts=32), "MOE_MAX_TOPK"),
     (dict(num_shared_experts=2, gate_kind=2, gate_num_shared=3, top_k=4), "top_k"),
     (dict(gate_kind=4, gate_param=0.0), "capacity_factor"),
     (dict(gate_kind=3, top_k=9), "top_k"),

@@ -99,6 +99,30 @@ def test_decode_many_experts(moe, oracle):
         c.dev.close()
 
 
+@pytest.mark.parametrize("E,k,lsh", [(20, 12, 0), (96, 16, 0), (14, 10, 3)])
+def test_decode_more_than_8_slots(moe, oracle, E, k, lsh):
+    # up to MOE_MAX_TOPK = 16 slots per token (routed experts of slots 8..15
+    # in the upper words of the wave's slot list), E <= 64 and E > 64 gating,
+    # with and without the layer's shared experts
+    Et = E + lsh
+    c = Case(moe, oracle, T=6, D=256, H=200, E=Et, k=k, wdtype="f32", seed=60 + k, lsh=lsh, max_tokens=8)
+    try:
+        x = np.ascontiguousarray(c.x[:6])
+        print(f"decode E={E} k={k} lsh={lsh}", flush=True)
+        out, logits, idx, gates = c.dev.decode(x)
+        out2, _, _, _ = c.dev.decode(x)
+        assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+        assert idx.shape == (6, lsh + k)
+        ref, ridx, rgates, _ = oracle.decode_ffn(x, c.wr, c.ex, gate="topk", k=k, logits=logits, num_shared=lsh)
+        assert np.array_equal(idx[:, :lsh], np.tile(np.arange(1, lsh + 1, dtype=np.int32), (6, 1)))
+        assert np.array_equal(idx[:, lsh:] - lsh, ridx)
+        assert np.array_equal(gates[:, lsh:].view(np.uint32), rgates.view(np.uint32))
+        err = rel_err(out, ref)
+        assert err <= TOL["f32"], err
+    finally:
+        c.dev.close()
+
+
 @pytest.mark.parametrize("E", [16, 40])
 def test_decode_tied_and_infinite_logits(moe, oracle, E):
     # equal probabilities go to the lower expert first (partialsortperm with

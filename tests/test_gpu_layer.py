@@ -520,6 +520,41 @@ def test_over_64_routed_experts(moe, oracle, E, k, gate, ns):
         c.dev.close()
 
 
+@pytest.mark.parametrize("E,k,gate,ns,wdtype,drop", [
+    (16, 12, "topk", 0, "bf16", False),      # two slots per routing lane, 32-token route blocks
+    (24, 16, "topk", 0, "f32", False),       # MOE_MAX_TOPK slots
+    (96, 10, "topk", 0, "bf16", False),      # > 64 experts: sorted lists + butterfly merge, k > 8
+    (20, 9, "shared", 3, "fp8", False),      # SharedExpertGating: 3 + 9 = 12 slots
+    (16, 11, "topk", 0, "bf16", True),       # capacity drop and renormalisation over 11 slots
+])
+def test_more_than_8_slots(moe, oracle, E, k, gate, ns, wdtype, drop):
+    # TopKGating(k) with k up to MOE_MAX_TOPK = 16: routing bit-exact, the
+    # combine's general path (slots sorted by expert id) within tolerance
+    c = Case(moe, oracle, T=700, D=128, H=160, E=E, k=k, gate=gate, ns=ns, wdtype=wdtype,
+             xdtype="f32" if wdtype == "f32" else "bf16", seed=E * 7 + k, drop=drop, cf=1.0)
+    try:
+        check_case(c, TOL[wdtype])
+        check_case(c, TOL[wdtype], training=False)
+        check_case(c, TOL[wdtype], T=333)  # a partial last route block
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("gate,lsh,k,ns,E,param,wdtype", [
+    ("topk", 2, 10, 0, 14, None, "bf16"),    # forward_with_shared_experts: 12 slots
+    ("soft", 3, 8, 0, 12, 0.75, "f32"),      # 11 slots, SoftMoE gates
+    ("shared", 2, 9, 4, 17, None, "bf16"),   # 2 + 4 + 9 = 15 slots
+])
+def test_shared_experts_more_than_8_slots(moe, oracle, gate, lsh, k, ns, E, param, wdtype):
+    c = Case(moe, oracle, T=400, D=128, H=192, E=E, k=k, gate=gate, ns=ns, wdtype=wdtype,
+             xdtype="bf16" if wdtype != "f32" else "f32", seed=70 + E, lsh=lsh, gate_param=param)
+    try:
+        check_shared_experts_case(c, TOL[wdtype], training=True)
+        check_shared_experts_case(c, TOL[wdtype], training=False)
+    finally:
+        c.dev.close()
+
+
 def test_varying_batch_on_one_handle(moe, oracle):
     c = Case(moe, oracle, T=300, D=128, H=256, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=9)
     for T in (300, 1, 7, 129, 300):
