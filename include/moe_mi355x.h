@@ -38,7 +38,7 @@ extern "C" {
 
 #define MOE_ABI_VERSION 1
 #define MOE_MAX_TOPK 16       /* maximum slots per token of the top-k gates (shared + routed) */
-#define MOE_MAX_EXPERTS 128   /* maximum experts seen by one router */
+#define MOE_MAX_EXPERTS 512   /* maximum experts of a layer (shared + routed) */
 
 typedef enum {
     MOE_OK = 0,

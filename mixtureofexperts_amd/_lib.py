@@ -30,7 +30,7 @@ MOE_ACT_GELU, MOE_ACT_SILU, MOE_ACT_RELU, MOE_ACT_IDENTITY = 0, 1, 2, 3
 MOE_GATE_TOPK, MOE_GATE_SWITCH, MOE_GATE_SHARED, MOE_GATE_SOFT, MOE_GATE_EXPERT_CHOICE = 0, 1, 2, 3, 4
 MOE_INIT_COPY, MOE_INIT_PERTURB, MOE_INIT_SPLIT, MOE_INIT_RANDOM = 0, 1, 2, 3
 MOE_MAX_TOPK = 16
-MOE_MAX_EXPERTS = 128
+MOE_MAX_EXPERTS = 512
 
 # every symbol the header declares (checked by the CPU test suite)
 EXPORTED_SYMBOLS = [

@@ -38,7 +38,7 @@ struct moe_handle {
     // divides by (the router's index rows: kt - lsh, ExpertChoice's capacity)
     int kc = 0, kl = 0;
     bool given = false, given_probs = false;  // the current call routes on the caller's indices
-    uint8_t *ec_sel = nullptr;                // ExpertChoiceGating selections [T][E]
+    uint16_t *ec_sel = nullptr;               // ExpertChoiceGating selections [T][E] (slot + 1 <= 512)
     int D_pad = 0, H_pad = 0, Dout_npad = 0;
     int ct = CT_BF16, wt = WT_BF16;
     bool gated = true;
@@ -211,7 +211,7 @@ static long long expert_choice_capacity(int T, float cf, int E) {
 }
 
 static int validate_config(const moe_config *c, std::string &why) {
-    if (c->num_experts < 1 || c->num_experts > MOE_MAX_EXPERTS) { why = "num_experts out of range [1,128]"; return 0; }
+    if (c->num_experts < 1 || c->num_experts > MOE_MAX_EXPERTS) { why = "num_experts out of range [1, MOE_MAX_EXPERTS (512)]"; return 0; }
     if (c->input_dim < 1 || c->hidden_dim < 1 || c->output_dim < 1) { why = "dimensions must be positive"; return 0; }
     if (c->expert_type != MOE_EXPERT_GATED && c->expert_type != MOE_EXPERT_STANDARD) { why = "unknown expert_type"; return 0; }
     if (c->activation < MOE_ACT_GELU || c->activation > MOE_ACT_IDENTITY) { why = "unknown activation"; return 0; }
@@ -995,7 +995,7 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     A((void **)&h->tile_start, sizeof(int) * (E + 1));
     A((void **)&h->item_start, sizeof(int) * (E + 1));
     A((void **)&h->scalars, sizeof(float) * 8);
-    if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, T * E);
+    if (cfg->gate_kind == MOE_GATE_EXPERT_CHOICE) A((void **)&h->ec_sel, sizeof(uint16_t) * T * E);
     A((void **)&h->aux_bias, sizeof(float) * aux_free_len(h));
     A((void **)&h->aux_mom, sizeof(float) * aux_free_len(h));
     A((void **)&h->perm, sizeof(int) * nent);
@@ -1759,7 +1759,7 @@ int moe_stage_combine_async(moe_handle *h, int32_t T, float *out_dev, void *stre
 int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *probs, int32_t E, float alpha,
                     float *loss) {
     if (!loss || T < 0 || k < 1 || E < 1) return fail(nullptr, MOE_EINVAL, "bad switch-loss arguments");
-    if (E > MOE_MAX_EXPERTS) return fail(nullptr, MOE_EINVAL, "switch loss: E above MOE_MAX_EXPERTS (128)");
+    if (E > MOE_MAX_EXPERTS) return fail(nullptr, MOE_EINVAL, "switch loss: E above MOE_MAX_EXPERTS (512)");
     if ((long long)T * k > INT_MAX) return fail(nullptr, MOE_EINVAL, "switch loss: T * k too large");
     if (T > 0 && (!indices || !probs)) return fail(nullptr, MOE_EINVAL, "null indices or probs");
     if (T == 0) { *loss = NAN; return MOE_OK; }
@@ -1783,7 +1783,7 @@ int moe_switch_loss(const int32_t *indices, int32_t T, int32_t k, const float *p
 
 // ---- the allocation-free Switch loss -------------------------------------------
 // The largest partials launch_switch_loss writes: kSwitchLossMaxBlocks rows of
-// MOE_MAX_EXPERTS doubles and ints (96 KiB).
+// MOE_MAX_EXPERTS doubles and ints (384 KiB).
 constexpr size_t kSwitchLossScratchBytes =
     (size_t)kSwitchLossMaxBlocks * MOE_MAX_EXPERTS * (sizeof(double) + sizeof(int));
 static_assert(kSwitchLossScratchBytes == MOE_SWITCH_LOSS_SCRATCH_BYTES, "header and library agree");
@@ -1822,7 +1822,7 @@ int moe_switch_loss_noalloc(const int32_t *indices_dev, int32_t T, int32_t k, co
     if (!loss_dev || T < 0 || k < 1 || E < 1) return fail(nullptr, MOE_EINVAL, "bad switch-loss arguments");
     if (E > MOE_MAX_EXPERTS)
         return fail(nullptr, MOE_EINVAL,
-                    "moe_switch_loss_noalloc: E above MOE_MAX_EXPERTS (128), the limit of its scratch array");
+                    "moe_switch_loss_noalloc: E above MOE_MAX_EXPERTS (512), the limit of its scratch array");
     if ((long long)T * k > INT_MAX) return fail(nullptr, MOE_EINVAL, "switch loss: T * k too large");
     if (T > 0 && (!indices_dev || !probs_dev)) return fail(nullptr, MOE_EINVAL, "null indices or probs");
     if (switch_loss_scratch_bytes(T, E) > kSwitchLossScratchBytes)

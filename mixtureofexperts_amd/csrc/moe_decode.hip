@@ -105,14 +105,24 @@ struct DecodeSel {
     }
 };
 
+// v[i >> 6] for a wave-uniform i < 64 NH, without a dynamically indexed
+// register array
+template <int NH, typename V>
+__device__ __forceinline__ V part_of(const V (&v)[NH], int i) {
+    V r = v[0];
+#pragma unroll
+    for (int h = 1; h < NH; ++h) r = ((i >> 6) == h) ? v[h] : r;
+    return r;
+}
+
 // compute_gates of token t from the wave partials in L (see decode_route_block);
-// HI: E > 64, lane l also holds expert l + 64 (E <= 64: decode_gates64).
-template <bool HI>
+// E > 64: lane l holds experts l, l + 64, ..., l + 64 (NH - 1) (E <= 64:
+// decode_gates64).
+template <int NH>
 __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bool write,
                                                            const DecodeRouteLds &L, float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, E = a.E;
-    constexpr int NH = HI ? 2 : 1;
     float lg[NH], ev[NH], pv[NH];
     uint32_t key[NH];
 #pragma unroll
@@ -123,8 +133,8 @@ __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bo
         if (a.br) v = v + a.br[min(e, E - 1)];
         lg[h] = v;
     }
-    // lane i & 63 of half i >> 6
-#define MOE_LANE_OF(arr, i) (NH == 1 ? (arr)[0] : ((i) < 64 ? (arr)[0] : (arr)[NH - 1]))
+    // lane i & 63 of part i >> 6
+#define MOE_LANE_OF(arr, i) part_of<NH>(arr, i)
     float m = -INFINITY;                                // max, NaN ignored
     for (int i0 = 0; i0 < E; i0 += 8) {
         float v[8];
@@ -180,10 +190,16 @@ __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bo
     int mye = 0;
     DecodeSel packed;
     for (int j = 0; j < a.k; ++j) {
-        const unsigned long long b0 = __ballot(lane < E && rank[0] == j);
-        const unsigned long long b1 = HI ? __ballot(lane + 64 < E && rank[NH - 1] == j) : 0ull;
-        const int e = b0 ? __builtin_ctzll(b0) : 64 + __builtin_ctzll(b1);
-        const float pj = readlane_f(HI && e >= 64 ? pv[NH - 1] : pv[0], e & 63);
+        // the expert of rank j: the first part whose ballot holds it
+        int e = 0;
+        bool found = false;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const unsigned long long b = __ballot(lane + 64 * h < E && rank[h] == j);
+            e = (!found && b) ? 64 * h + __builtin_ctzll(b) : e;
+            found = found || b;
+        }
+        const float pj = readlane_f(part_of<NH>(pv, e), e & 63);
         ssum = (j == 0) ? pj : ssum + pj;  // slot order
         packed.set(j, e);
         if (lane == j) {
@@ -312,7 +328,7 @@ __device__ __forceinline__ DecodeSel decode_gates64(const DecodeArgs &a, int t, 
 // / sum; top-k by the isless key descending, lower index first among equal
 // keys (partialsortperm(p, 1:k, rev=true)): the rank of expert i is the number
 // of experts before it in that order; the gates are p of the slots over their
-// sum in slot order.  Lane l holds experts l and, for E > 64, l + 64.
+// sum in slot order.  Lane l holds experts l, l + 64, l + 128, ... < E.
 // Returns the 0-based experts of the routed slots (uniform), and in `gate`
 // of lane j < k that slot's gate; `write` (wave 0 of
 // one block per token) stores logits, probs, indices, gates.
@@ -322,60 +338,65 @@ __device__ DecodeSel decode_route_block(const DecodeArgs &a, int t, bool write, 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int E = a.E, Q = a.Er_pad >> 2;               // router row: Q float4 (Er_pad % 8 == 0)
     int QP = 1;
-    while (QP < Q) QP <<= 1;                            // Q <= 32
-    const int C = 64 / QP;                              // chunks per wave
-    const int q = lane / C, c = lane - q * C;
+    while (QP < Q) QP <<= 1;                            // Q <= MOE_MAX_EXPERTS / 4
+    const int C = QP >= 64 ? 1 : 64 / QP;               // chunks per wave
+    const int NQ = QP > 64 ? QP / 64 : 1;               // float4 columns per lane (lane, lane + 64, ...)
     const int CH = (a.D + 4 * C - 1) / (4 * C);
     const float *x = a.x + (long long)t * a.D;
     const float4 *wr4 = (const float4 *)a.wr;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    {
-        const int d0 = (w * C + c) * CH, d1 = min(a.D, d0 + CH);
-        const int qq = min(q, Q - 1);
-        for (int d = d0; d < d1; d += 4) {
-            float xv[4];
-            float4 wv[4];
+    for (int qi = 0; qi < NQ; ++qi) {
+        const int q = C == 1 ? lane + 64 * qi : lane / C, c = C == 1 ? 0 : lane - q * C;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        {
+            const int d0 = (w * C + c) * CH, d1 = min(a.D, d0 + CH);
+            const int qq = min(q, Q - 1);
+            for (int d = d0; d < d1; d += 4) {
+                float xv[4];
+                float4 wv[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int dd = min(d + u, d1 - 1);
-                xv[u] = x[dd];
-                wv[u] = wr4[(long long)dd * Q + qq];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (d + u < d1) {
-                    acc.x = acc.x + xv[u] * wv[u].x;
-                    acc.y = acc.y + xv[u] * wv[u].y;
-                    acc.z = acc.z + xv[u] * wv[u].z;
-                    acc.w = acc.w + xv[u] * wv[u].w;
+                for (int u = 0; u < 4; ++u) {
+                    const int dd = min(d + u, d1 - 1);
+                    xv[u] = x[dd];
+                    wv[u] = wr4[(long long)dd * Q + qq];
                 }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (d + u < d1) {
+                        acc.x = acc.x + xv[u] * wv[u].x;
+                        acc.y = acc.y + xv[u] * wv[u].y;
+                        acc.z = acc.z + xv[u] * wv[u].z;
+                        acc.w = acc.w + xv[u] * wv[u].w;
+                    }
+            }
         }
+        // groups of C contiguous lanes: every lane of a group ends with the same sum
+        if (C >= 2) {
+            acc.x = acc.x + dpp_f<0xb1>(acc.x); acc.y = acc.y + dpp_f<0xb1>(acc.y);
+            acc.z = acc.z + dpp_f<0xb1>(acc.z); acc.w = acc.w + dpp_f<0xb1>(acc.w);
+        }
+        if (C >= 4) {
+            acc.x = acc.x + dpp_f<0x4e>(acc.x); acc.y = acc.y + dpp_f<0x4e>(acc.y);
+            acc.z = acc.z + dpp_f<0x4e>(acc.z); acc.w = acc.w + dpp_f<0x4e>(acc.w);
+        }
+        if (C >= 8) {
+            acc.x = acc.x + dpp_f<0x141>(acc.x); acc.y = acc.y + dpp_f<0x141>(acc.y);
+            acc.z = acc.z + dpp_f<0x141>(acc.z); acc.w = acc.w + dpp_f<0x141>(acc.w);
+        }
+        if (C >= 16) {
+            acc.x = acc.x + dpp_f<0x140>(acc.x); acc.y = acc.y + dpp_f<0x140>(acc.y);
+            acc.z = acc.z + dpp_f<0x140>(acc.z); acc.w = acc.w + dpp_f<0x140>(acc.w);
+        }
+        for (int o = 16; o < C; o <<= 1) {
+            acc.x = acc.x + __shfl_xor(acc.x, o); acc.y = acc.y + __shfl_xor(acc.y, o);
+            acc.z = acc.z + __shfl_xor(acc.z, o); acc.w = acc.w + __shfl_xor(acc.w, o);
+        }
+        if (c == 0 && q < Q) *(float4 *)&L.part[w][4 * q] = acc;
     }
-    // groups of C contiguous lanes: every lane of a group ends with the same sum
-    if (C >= 2) {
-        acc.x = acc.x + dpp_f<0xb1>(acc.x); acc.y = acc.y + dpp_f<0xb1>(acc.y);
-        acc.z = acc.z + dpp_f<0xb1>(acc.z); acc.w = acc.w + dpp_f<0xb1>(acc.w);
-    }
-    if (C >= 4) {
-        acc.x = acc.x + dpp_f<0x4e>(acc.x); acc.y = acc.y + dpp_f<0x4e>(acc.y);
-        acc.z = acc.z + dpp_f<0x4e>(acc.z); acc.w = acc.w + dpp_f<0x4e>(acc.w);
-    }
-    if (C >= 8) {
-        acc.x = acc.x + dpp_f<0x141>(acc.x); acc.y = acc.y + dpp_f<0x141>(acc.y);
-        acc.z = acc.z + dpp_f<0x141>(acc.z); acc.w = acc.w + dpp_f<0x141>(acc.w);
-    }
-    if (C >= 16) {
-        acc.x = acc.x + dpp_f<0x140>(acc.x); acc.y = acc.y + dpp_f<0x140>(acc.y);
-        acc.z = acc.z + dpp_f<0x140>(acc.z); acc.w = acc.w + dpp_f<0x140>(acc.w);
-    }
-    for (int o = 16; o < C; o <<= 1) {
-        acc.x = acc.x + __shfl_xor(acc.x, o); acc.y = acc.y + __shfl_xor(acc.y, o);
-        acc.z = acc.z + __shfl_xor(acc.z, o); acc.w = acc.w + __shfl_xor(acc.w, o);
-    }
-    if (c == 0 && q < Q) *(float4 *)&L.part[w][4 * q] = acc;
     __syncthreads();
 
-    return E > 64 ? decode_gates<true>(a, t, write, L, gate) : decode_gates64(a, t, write, L, gate);
+    if (E > 256) return decode_gates<8>(a, t, write, L, gate);
+    if (E > 128) return decode_gates<4>(a, t, write, L, gate);
+    return E > 64 ? decode_gates<2>(a, t, write, L, gate) : decode_gates64(a, t, write, L, gate);
 }
 
 // ---- up: the waves of token t take units u = (slot, row j) two at a time,

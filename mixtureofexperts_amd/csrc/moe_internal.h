@@ -181,11 +181,12 @@ struct ScanArgs {
 struct RtArgs {
     RouteArgs r;           // gating (r.out_mask: outputs of the single pass)
     RouterArgs g;          // logits GEMM (when the kernel computes the logits)
-    int TB;                // tokens per workgroup: 16 (paired logits GEMM), 32 or 64
+    int TB;                // tokens per workgroup: 16 (paired logits GEMM, over 256 GEMM columns), 32 or 64
     int ncu;               // CUs (64-token workgroups fewer than this: 32-token ones)
     int KP, RB, dma;       // x staging: K columns per pass, LDS bytes per row, by global_load_lds
     int RW;                // LDS row stride of the logits / probability rows (floats)
     int off_L;             // LDS byte offset of the logits rows
+    int off_M;             // LDS byte offset of the rank bitmasks (Eh x kRtMaskWords words)
     int npass;             // 2: AuxiliaryFreeLoss (probabilities pass, then gating on logits + aux_bias)
     const float *aux_bias; // [Er]
     int store_rows;        // write logits / probs [T][Er] to global memory
@@ -342,7 +343,7 @@ hipError_t launch_router(RtArgs a, int *tb, hipStream_t s);
 // entry among its expert's entries in its route block), blk_counts
 // [nblk][ldc] and the totals per super block sup_cnt [nsup][ldc] (atomic adds)
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int lsh, int C, int kt,
-                                uint8_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
+                                uint16_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
                                 int *sup_cnt, int rb, hipStream_t s);
 hipError_t launch_permute(PermuteArgs a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);

@@ -180,6 +180,8 @@ __device__ __forceinline__ double lanes8_sum(double v) {
 // tile; D lane l: column l % 16, tokens 4 (l / 16) .. +4.  The accumulators
 // then go to LDS partials P[kg][t][col] and each logit is their sum in
 // K-group order (paired tiles: the three parts' columns added in part order).
+// More than 8 expert tiles (over 128 GEMM columns): column groups of 8 tiles
+// in turn, one tile per wave and one K group, x staged again for each group.
 template <int XBF16, int PAIRED, int RT>
 __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds, float *L) {
 #pragma clang fp contract(off)
@@ -199,223 +201,226 @@ __device__ __forceinline__ void rt_logits(const RtArgs &a, int t0, uint8_t *lds,
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int TB = RT * 16, RB = a.RB, PPR = RB >> 4;
-    const int ET = PAIRED ? 1 : (g.Er + 15) >> 4;
-    const int NTS = PAIRED ? 2 : 3 * ET;
-    const int KG = 8 / ET;
-    const int cg = w % ET, kg = w / ET;
-    const bool mw = kg < KG;  // this wave runs MFMAs
+    const int ETA = PAIRED ? 1 : (g.Er + 15) >> 4;  // expert tiles of the GEMM
+    const int NTS = PAIRED ? 2 : 3 * ETA;
+    for (int cgo = 0; cgo < ETA; cgo += 8) {  // column group: tiles cgo .. cgo + 7
+        const int ET = PAIRED ? 1 : min(ETA - cgo, 8);
+        const int KG = ETA > 8 ? 1 : 8 / ET;
+        const int cg = w % ET, kg = w / ET;
+        const bool mw = kg < KG;  // this wave runs MFMAs
 
-    rf32x4_t acc[RT][NACC];
+        rf32x4_t acc[RT][NACC];
 #pragma unroll
-    for (int ti = 0; ti < RT; ++ti)
+        for (int ti = 0; ti < RT; ++ti)
 #pragma unroll
-        for (int j = 0; j < NACC; ++j) acc[ti][j] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < NACC; ++j) acc[ti][j] = rf32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    using WF = rbf16x8_t[kRtSG][NPT];
-    for (int k0 = 0; k0 < g.Dp; k0 += a.KP) {
-        const int kp = min(a.KP, g.Dp - k0);
-        const int UPR = kp * ESZ / 16;  // data units per staged row
-        // ---- stage x[t0 .. t0 + TB)[k0 .. k0 + kp) (rows past T: row T - 1) ----
-        if (a.dma) {
-            const int NCH = TB * PPR / 64;  // 1 KB pieces of LDS
-            for (int c = w; c < NCH; c += kRtThreads / 64) {
-                const int p = c * 64 + lane;
-                const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
-                const long long t = min(t0 + r, g.T - 1);
-                const uint8_t *src = (const uint8_t *)g.x + (t * g.D + k0) * ESZ + (u < UPR ? u : 0) * 16;
-                rt_dma16(src, __builtin_amdgcn_readfirstlane(rt_lds_addr(lds + c * 1024)));
+        using WF = rbf16x8_t[kRtSG][NPT];
+        for (int k0 = 0; k0 < g.Dp; k0 += a.KP) {
+            const int kp = min(a.KP, g.Dp - k0);
+            const int UPR = kp * ESZ / 16;  // data units per staged row
+            // ---- stage x[t0 .. t0 + TB)[k0 .. k0 + kp) (rows past T: row T - 1) ----
+            if (a.dma) {
+                const int NCH = TB * PPR / 64;  // 1 KB pieces of LDS
+                for (int c = w; c < NCH; c += kRtThreads / 64) {
+                    const int p = c * 64 + lane;
+                    const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
+                    const long long t = min(t0 + r, g.T - 1);
+                    const uint8_t *src = (const uint8_t *)g.x + (t * g.D + k0) * ESZ + (u < UPR ? u : 0) * 16;
+                    rt_dma16(src, __builtin_amdgcn_readfirstlane(rt_lds_addr(lds + c * 1024)));
+                }
+            } else {
+                for (int p = tid; p < TB * PPR; p += kRtThreads) {
+                    const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
+                    const long long t = min(t0 + r, g.T - 1);
+                    uint32_t q[4] = {0u, 0u, 0u, 0u};
+                    if (u < UPR) {
+                        const int kb = k0 + u * (16 / ESZ);
+                        if (XBF16) {
+                            const uint16_t *row = (const uint16_t *)g.x + t * g.D;
+                            uint16_t hv[8];
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) hv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : (uint16_t)0;
+                            __builtin_memcpy(q, hv, 16);
+                        } else {
+                            const float *row = (const float *)g.x + t * g.D;
+                            float fv[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) fv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : 0.0f;
+                            __builtin_memcpy(q, fv, 16);
+                        }
+                    }
+                    *(u32x4_t *)(lds + p * 16) = u32x4_t{q[0], q[1], q[2], q[3]};
+                }
             }
-        } else {
-            for (int p = tid; p < TB * PPR; p += kRtThreads) {
-                const int r = p / PPR, pu = p - r * PPR, u = pu ^ (r & 15);
-                const long long t = min(t0 + r, g.T - 1);
-                uint32_t q[4] = {0u, 0u, 0u, 0u};
-                if (u < UPR) {
-                    const int kb = k0 + u * (16 / ESZ);
+            // ---- this wave's K steps of the pass: [sb, se) ----
+            const int sp = kp >> 5, spw = (sp + KG - 1) / KG;
+            const int sb = (k0 >> 5) + kg * spw, se = min((k0 >> 5) + sp, sb + spw);
+            const bool act = mw && sb < se;
+            auto load_w = [&](int s0, WF &wf) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < kRtSG; ++i) {
+                    const int st = min(s0 + i, se - 1);
+#pragma unroll
+                    for (int p = 0; p < NPT; ++p) {
+                        const int q = PAIRED ? p : 3 * (cgo + cg) + p;
+                        const rbf16x8_t *src = (const rbf16x8_t *)(g.ws + (((long long)st * NTS + q) * 64 + lane) * 8);
+                        if (PAIRED && p == 1) {
+                            // paired tile 1: columns 8..15 are zero in the image; those lanes skip the load
+                            rbf16x8_t z = {};
+                            if ((lane & 8) == 0) z = *src;
+                            wf[i][p] = z;
+                        } else {
+                            wf[i][p] = *src;
+                        }
+                    }
+                }
+            };
+            // the x fragments (parts) of step st of the pass, every row tile
+            auto load_x = [&](int st, rbf16x8_t (&xa)[RT][NP]) __attribute__((always_inline)) {
+                const int u = st - (k0 >> 5);  // step inside the pass
+#pragma unroll
+                for (int ti = 0; ti < RT; ++ti) {
+                    const int r = ti * 16 + l16;
+                    const uint8_t *row = lds + r * RB;
                     if (XBF16) {
-                        const uint16_t *row = (const uint16_t *)g.x + t * g.D;
-                        uint16_t hv[8];
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) hv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : (uint16_t)0;
-                        __builtin_memcpy(q, hv, 16);
+                        xa[ti][0] = *(const rbf16x8_t *)(row + (((u * 4 + (lane >> 4)) ^ (r & 15)) << 4));
                     } else {
-                        const float *row = (const float *)g.x + t * g.D;
-                        float fv[4];
+                        const int u0 = u * 8 + (lane >> 4) * 2;
+                        const float4 f0 = *(const float4 *)(row + ((u0 ^ (r & 15)) << 4));
+                        const float4 f1 = *(const float4 *)(row + (((u0 + 1) ^ (r & 15)) << 4));
+                        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+                        uint16_t h0[8], h1[8], h2[8];
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) fv[i] = (kb + i < g.D) ? row[min(kb + i, g.D - 1)] : 0.0f;
-                        __builtin_memcpy(q, fv, 16);
+                        for (int m = 0; m < 8; ++m) {
+                            h0[m] = f32_to_bf16(v[m]);
+                            const float r1 = v[m] - bf16_to_f32(h0[m]);
+                            h1[m] = f32_to_bf16(r1);
+                            h2[m] = f32_to_bf16(r1 - bf16_to_f32(h1[m]));
+                        }
+                        __builtin_memcpy(&xa[ti][0], h0, 16);
+                        __builtin_memcpy(&xa[ti][NP > 1 ? 1 : 0], h1, 16);
+                        __builtin_memcpy(&xa[ti][NP > 2 ? 2 : 0], h2, 16);
                     }
                 }
-                *(u32x4_t *)(lds + p * 16) = u32x4_t{q[0], q[1], q[2], q[3]};
-            }
-        }
-        // ---- this wave's K steps of the pass: [sb, se) ----
-        const int sp = kp >> 5, spw = (sp + KG - 1) / KG;
-        const int sb = (k0 >> 5) + kg * spw, se = min((k0 >> 5) + sp, sb + spw);
-        const bool act = mw && sb < se;
-        auto load_w = [&](int s0, WF &wf) __attribute__((always_inline)) {
+            };
+            // one group: the next step's x fragments are read while this step's
+            // MFMAs run; the MFMAs of a step go part by part over the row tiles,
+            // so consecutive ones write different accumulators
+            auto mma = [&](int s0, const WF &wf) __attribute__((always_inline)) {
+                rbf16x8_t xc[RT][NP], xn[XPF ? RT : 1][NP];
+                if constexpr (XPF) load_x(min(s0, se - 1), xc);
 #pragma unroll
-            for (int i = 0; i < kRtSG; ++i) {
-                const int st = min(s0 + i, se - 1);
+                for (int i = 0; i < kRtSG; ++i) {
+                    if (s0 + i >= se) break;
+                    if constexpr (!XPF) load_x(s0 + i, xc);
+                    else if (i + 1 < kRtSG) load_x(min(s0 + i + 1, se - 1), xn);
+                    if constexpr (PAIRED) {
+                        // tile 0 (parts 0 | 1): every x part; tile 1 (part 2): x part 0
 #pragma unroll
-                for (int p = 0; p < NPT; ++p) {
-                    const int q = PAIRED ? p : 3 * cg + p;
-                    const rbf16x8_t *src = (const rbf16x8_t *)(g.ws + (((long long)st * NTS + q) * 64 + lane) * 8);
-                    if (PAIRED && p == 1) {
-                        // paired tile 1: columns 8..15 are zero in the image; those lanes skip the load
-                        rbf16x8_t z = {};
-                        if ((lane & 8) == 0) z = *src;
-                        wf[i][p] = z;
-                    } else {
-                        wf[i][p] = *src;
-                    }
-                }
-            }
-        };
-        // the x fragments (parts) of step st of the pass, every row tile
-        auto load_x = [&](int st, rbf16x8_t (&xa)[RT][NP]) __attribute__((always_inline)) {
-            const int u = st - (k0 >> 5);  // step inside the pass
-#pragma unroll
-            for (int ti = 0; ti < RT; ++ti) {
-                const int r = ti * 16 + l16;
-                const uint8_t *row = lds + r * RB;
-                if (XBF16) {
-                    xa[ti][0] = *(const rbf16x8_t *)(row + (((u * 4 + (lane >> 4)) ^ (r & 15)) << 4));
-                } else {
-                    const int u0 = u * 8 + (lane >> 4) * 2;
-                    const float4 f0 = *(const float4 *)(row + ((u0 ^ (r & 15)) << 4));
-                    const float4 f1 = *(const float4 *)(row + (((u0 + 1) ^ (r & 15)) << 4));
-                    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-                    uint16_t h0[8], h1[8], h2[8];
-#pragma unroll
-                    for (int m = 0; m < 8; ++m) {
-                        h0[m] = f32_to_bf16(v[m]);
-                        const float r1 = v[m] - bf16_to_f32(h0[m]);
-                        h1[m] = f32_to_bf16(r1);
-                        h2[m] = f32_to_bf16(r1 - bf16_to_f32(h1[m]));
-                    }
-                    __builtin_memcpy(&xa[ti][0], h0, 16);
-                    __builtin_memcpy(&xa[ti][NP > 1 ? 1 : 0], h1, 16);
-                    __builtin_memcpy(&xa[ti][NP > 2 ? 2 : 0], h2, 16);
-                }
-            }
-        };
-        // one group: the next step's x fragments are read while this step's
-        // MFMAs run; the MFMAs of a step go part by part over the row tiles,
-        // so consecutive ones write different accumulators
-        auto mma = [&](int s0, const WF &wf) __attribute__((always_inline)) {
-            rbf16x8_t xc[RT][NP], xn[XPF ? RT : 1][NP];
-            if constexpr (XPF) load_x(min(s0, se - 1), xc);
-#pragma unroll
-            for (int i = 0; i < kRtSG; ++i) {
-                if (s0 + i >= se) break;
-                if constexpr (!XPF) load_x(s0 + i, xc);
-                else if (i + 1 < kRtSG) load_x(min(s0 + i + 1, se - 1), xn);
-                if constexpr (PAIRED) {
-                    // tile 0 (parts 0 | 1): every x part; tile 1 (part 2): x part 0
-#pragma unroll
-                    for (int xi = 0; xi < NP; ++xi)
-#pragma unroll
-                        for (int ti = 0; ti < RT; ++ti)
-                            acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][0], acc[ti][0], 0, 0, 0);
-#pragma unroll
-                    for (int ti = 0; ti < RT; ++ti)
-                        acc[ti][NACC - 1] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][0], wf[i][NPT - 1], acc[ti][NACC - 1], 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int p = 0; p < 3; ++p)
-#pragma unroll
-                        for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
+                        for (int xi = 0; xi < NP; ++xi)
 #pragma unroll
                             for (int ti = 0; ti < RT; ++ti)
-                                acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][p < NPT ? p : 0],
-                                                                                     acc[ti][0], 0, 0, 0);
-                }
-                if constexpr (XPF) {
-                    if (i + 1 < kRtSG) {
+                                acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][0], acc[ti][0], 0, 0, 0);
 #pragma unroll
                         for (int ti = 0; ti < RT; ++ti)
+                            acc[ti][NACC - 1] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][0], wf[i][NPT - 1], acc[ti][NACC - 1], 0, 0, 0);
+                    } else {
 #pragma unroll
-                            for (int xi = 0; xi < NP; ++xi) xc[ti][xi] = xn[ti][xi];
+                        for (int p = 0; p < 3; ++p)
+#pragma unroll
+                            for (int xi = 0; xi + p < 3 && xi < NP; ++xi)
+#pragma unroll
+                                for (int ti = 0; ti < RT; ++ti)
+                                    acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[ti][xi], wf[i][p < NPT ? p : 0],
+                                                                                         acc[ti][0], 0, 0, 0);
+                    }
+                    if constexpr (XPF) {
+                        if (i + 1 < kRtSG) {
+#pragma unroll
+                            for (int ti = 0; ti < RT; ++ti)
+#pragma unroll
+                                for (int xi = 0; xi < NP; ++xi) xc[ti][xi] = xn[ti][xi];
+                        }
+                    }
+                }
+            };
+            // the ring: NRING - 1 groups in flight with the x tile, then each
+            // group's loads issued NRING - 1 groups ahead of its MFMAs
+            WF wr[NRING];
+            if (act) {
+#pragma unroll
+                for (int j = 0; j + 1 < NRING; ++j)
+                    if (sb + j * kRtSG < se) load_w(sb + j * kRtSG, wr[j]);
+            }
+            rt_wait_vm0();  // this wave's x pieces (and its first weight groups) have landed
+            __syncthreads();
+            if (act) {
+                for (int s0 = sb; s0 < se; s0 += NRING * kRtSG) {
+#pragma unroll
+                    for (int j = 0; j < NRING; ++j) {
+                        const int sj = s0 + j * kRtSG;
+                        if (sj >= se) break;
+                        const int nx = sj + (NRING - 1) * kRtSG;
+                        if (nx < se) load_w(nx, wr[(j + NRING - 1) % NRING]);
+                        mma(sj, wr[j]);
                     }
                 }
             }
-        };
-        // the ring: NRING - 1 groups in flight with the x tile, then each
-        // group's loads issued NRING - 1 groups ahead of its MFMAs
-        WF wr[NRING];
-        if (act) {
-#pragma unroll
-            for (int j = 0; j + 1 < NRING; ++j)
-                if (sb + j * kRtSG < se) load_w(sb + j * kRtSG, wr[j]);
+            __syncthreads();  // the pass's x tile is consumed
         }
-        rt_wait_vm0();  // this wave's x pieces (and its first weight groups) have landed
-        __syncthreads();
-        if (act) {
-            for (int s0 = sb; s0 < se; s0 += NRING * kRtSG) {
+
+        const float *bias = a.r.bias;
+        if (!PAIRED && KG == 1) {
+            // one K group: each logit is one wave's accumulator, written with the
+            // bias straight into its row (the values the partial-sum pass gives)
+            if (mw) {
 #pragma unroll
-                for (int j = 0; j < NRING; ++j) {
-                    const int sj = s0 + j * kRtSG;
-                    if (sj >= se) break;
-                    const int nx = sj + (NRING - 1) * kRtSG;
-                    if (nx < se) load_w(nx, wr[(j + NRING - 1) % NRING]);
-                    mma(sj, wr[j]);
+                for (int ti = 0; ti < RT; ++ti) {
+                    const int e = (cgo + cg) * 16 + l16;
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int t = ti * 16 + (lane >> 4) * 4 + rr;
+                        float v = acc[ti][0][rr];
+                        if (bias && e < a.r.Er) v = v + bias[e];
+                        if (e < g.Er) L[t * a.RW + e] = v;
+                    }
                 }
             }
+            continue;  // the next column group (ETA > 8), else done
         }
-        __syncthreads();  // the pass's x tile is consumed
-    }
-
-    const float *bias = a.r.bias;
-    if (!PAIRED && KG == 1) {
-        // one K group: each logit is one wave's accumulator, written with the
-        // bias straight into its row (the values the partial-sum pass gives)
+        // accumulators -> LDS partials P[kg][t][col] (over the staging region),
+        // col = image column of the expert tile (paired: 16 j + c)
+        const int NCOL = PAIRED ? 32 : ET * 16;
+        float *P = (float *)lds;
         if (mw) {
 #pragma unroll
             for (int ti = 0; ti < RT; ++ti) {
-                const int e = cg * 16 + l16;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int t = ti * 16 + (lane >> 4) * 4 + rr;
-                    float v = acc[ti][0][rr];
-                    if (bias && e < a.r.Er) v = v + bias[e];
-                    if (e < g.Er) L[t * a.RW + e] = v;
+                for (int j = 0; j < NACC; ++j) {
+                    const int col = PAIRED ? j * 16 + l16 : cg * 16 + l16;
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int t = ti * 16 + (lane >> 4) * 4 + rr;
+                        P[(kg * TB + t) * NCOL + col] = acc[ti][j][rr];
+                    }
                 }
             }
         }
-        return;
-    }
-    // accumulators -> LDS partials P[kg][t][col] (over the staging region),
-    // col = image column of the expert tile (paired: 16 j + c)
-    const int NCOL = PAIRED ? 32 : ET * 16;
-    float *P = (float *)lds;
-    if (mw) {
-#pragma unroll
-        for (int ti = 0; ti < RT; ++ti) {
-#pragma unroll
-            for (int j = 0; j < NACC; ++j) {
-                const int col = PAIRED ? j * 16 + l16 : cg * 16 + l16;
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int t = ti * 16 + (lane >> 4) * 4 + rr;
-                    P[(kg * TB + t) * NCOL + col] = acc[ti][j][rr];
-                }
-            }
+        __syncthreads();
+        for (int q = tid; q < TB * g.Er; q += kRtThreads) {
+            const int t = q / g.Er, e = q - t * g.Er;
+            auto col_sum = [&](int col) __attribute__((always_inline)) {
+                float v = P[t * NCOL + col];
+                for (int k = 1; k < KG; ++k) v = v + P[(k * TB + t) * NCOL + col];
+                return v;
+            };
+            float v = PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e);
+            if (bias && e < a.r.Er) v = v + bias[e];  // (not on the noise network's columns)
+            L[t * a.RW + e] = v;
         }
-    }
-    __syncthreads();
-    for (int q = tid; q < TB * g.Er; q += kRtThreads) {
-        const int t = q / g.Er, e = q - t * g.Er;
-        auto col_sum = [&](int col) __attribute__((always_inline)) {
-            float v = P[t * NCOL + col];
-            for (int k = 1; k < KG; ++k) v = v + P[(k * TB + t) * NCOL + col];
-            return v;
-        };
-        float v = PAIRED ? (col_sum(e) + col_sum(8 + e)) + col_sum(16 + e) : col_sum(e);
-        if (bias && e < a.r.Er) v = v + bias[e];  // (not on the noise network's columns)
-        L[t * a.RW + e] = v;
-    }
+    }  // column groups (one when ETA <= 8: this path)
 }
 
 // ---- gating -------------------------------------------------------------------
@@ -800,12 +805,13 @@ __host__ __device__ inline int route_rw(int E) { return 4 * ((((E + 3) / 4 + 1) 
 template <int LG, int PAIRED, int EPL, int RT>
 __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t rdyn[];
-    __shared__ unsigned emask[MOE_MAX_EXPERTS * kRtMaskWords];
     __shared__ double wred[2][kRtThreads / 64];
     const int blk = blockIdx.x;
     const int t0 = blk * A.TB;
     const int ntok = min(A.TB, A.r.T - t0);
     float *L = (float *)(rdyn + A.off_L);
+    // the rank bitmasks, Eh x kRtMaskWords words after the logits rows
+    unsigned *emask = (unsigned *)(rdyn + A.off_M);
     // over the staging region, free once the logits are in L: the output
     // probability rows, then the gate's working rows
     float *Pr = (float *)rdyn;
@@ -837,8 +843,12 @@ __global__ __launch_bounds__(kRtThreads) void router_kernel(RtArgs A) {
 
 // experts per lane of a token's 8 (the gating's register blocks)
 static int route_epl(int E) {
-    return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : (E <= 80 ? 10 : (E <= 96 ? 12 : 16)))));
+    return E <= 8 ? 1 : (E <= 16 ? 2 : (E <= 32 ? 4 : (E <= 64 ? 8 : (E <= 80 ? 10 : (E <= 96 ? 12 :
+           (E <= 128 ? 16 : (E <= 256 ? 32 : 64)))))));
 }
+
+// dynamic LDS of a router workgroup (the static wred is 128 B of the 160 KB)
+constexpr size_t kRtLdsMax = 159 * 1024;
 
 template <int LG, int PAIRED, int EPL, int RT>
 static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipStream_t s) {
@@ -846,7 +856,7 @@ static hipError_t launch_router_case(const RtArgs &A, int nblk, size_t lds, hipS
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [&] {
-        attr = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        attr = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRtLdsMax);
     });
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kern, dim3(nblk), dim3(kRtThreads), lds, s, A);
@@ -875,15 +885,20 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     // also takes fewer K passes) (the logits GEMM's row tiles are
     // compile-time: 1, 2 or 4)
     // more than 8 slots per token: 32-token workgroups at most (the rank
-    // bitmasks hold kRtMaskWords * 32 = 512 entries per expert)
+    // bitmasks hold kRtMaskWords * 32 = 512 entries per expert); the three
+    // LDS rows of a token (logits, probabilities, gate) over 128 columns: 32
+    // tokens, over 256 columns: 16
     const bool wide = (a.out_mask & ROUTE_OUT_GATING) && a.kt > 8;
-    const bool half = (gemm && !paired && A.ncu > 0 && (a.T + 63) / 64 < A.ncu) || wide;
-    const int TB = gemm && paired ? 16 : (half ? 32 : 64);
+    const bool half = (gemm && !paired && A.ncu > 0 && (a.T + 63) / 64 < A.ncu) || wide || Eg > 128;
+    const int TB = (gemm && paired) || Eg > 256 ? 16 : (half ? 32 : 64);
     *tb = TB;
     A.TB = TB;
     A.RW = route_rw(Eg);
     const size_t rows = sizeof(float) * (size_t)TB * A.RW;
-    const size_t lds_max = 150 * 1024;  // + the static emask / wred (9.2 KB) <= 160 KB
+    const size_t mask_bytes = sizeof(unsigned) * (size_t)a.Eh * kRtMaskWords;
+    // the x tile, rows and partials within 150 KB (the bitmasks of up to 128
+    // experts beside them), less for more experts
+    const size_t lds_max = std::min<size_t>(150 * 1024, kRtLdsMax - mask_bytes);
     size_t region0 = 2 * rows;  // the gating's Pr and G rows
     if (gemm) {
         const RouterArgs &g = A.g;
@@ -897,14 +912,17 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
         A.KP = std::min(g.Dp, KPmax);
         A.RB = ((A.KP * ESZ + 255) / 256) * 256;
         A.dma = (g.D % 32 == 0) && (((uintptr_t)g.x & 15) == 0);
-        const int KG = 8 / ET;
+        // the partial sums of the K groups (one column group of at most 8
+        // tiles: more tiles write their logits directly)
+        const int KG = ET > 8 ? 0 : 8 / ET;
         const size_t part = sizeof(float) * (size_t)KG * TB * (paired ? 32 : ET * 16);
         region0 = std::max(region0, std::max((size_t)TB * A.RB, part));
     }
     A.off_L = (int)((region0 + 1023) & ~(size_t)1023);
-    const size_t lds = (size_t)A.off_L + rows;
+    A.off_M = (int)(A.off_L + rows);
+    const size_t lds = (size_t)A.off_M + mask_bytes;
     const int nblk = (a.T + TB - 1) / TB;
-    if (lds > lds_max || a.ldc < a.Eh || !a.blk_zh || !a.sup_cnt || !a.sup_p || !a.clr_sup || !a.clr_supp ||
+    if (lds > lds_max + mask_bytes || a.ldc < a.Eh || !a.blk_zh || !a.sup_cnt || !a.sup_p || !a.clr_sup || !a.clr_supp ||
         a.nsup_max * kSuper < nblk)
         return hipErrorInvalidValue;
     const int epl = route_epl(Er);
@@ -917,6 +935,23 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
     case 10: MOE_RT(LG_, 0, 10, RT_);   \
     case 12: MOE_RT(LG_, 0, 12, RT_);   \
     default: MOE_RT(LG_, 0, 16, RT_);   \
+    }
+    // over 128 router rows: 32 experts per lane on 32-token workgroups, over
+    // 256: 64 on 16-token ones (a noise network's GEMM columns can make the
+    // workgroups smaller than the gating needs: the TB they get is used)
+    if (epl == 64) {
+        if (!gemm) MOE_RT(0, 0, 64, 4);
+        if (A.g.x_bf16) MOE_RT(1, 0, 64, 1);
+        MOE_RT(2, 0, 64, 1);
+    }
+    if (epl == 32) {
+        if (!gemm) MOE_RT(0, 0, 32, 4);
+        if (TB == 16) {
+            if (A.g.x_bf16) MOE_RT(1, 0, 32, 1);
+            MOE_RT(2, 0, 32, 1);
+        }
+        if (A.g.x_bf16) MOE_RT(1, 0, 32, 2);
+        MOE_RT(2, 0, 32, 2);
     }
     if (!gemm) {
         // (RT only shapes the logits GEMM, which this case does not run)
@@ -944,7 +979,7 @@ hipError_t launch_router(RtArgs A, int *tb, hipStream_t s) {
 // C-th largest key K and how many tokens of key K to take; the tokens of key
 // > K and the first of key == K in token order are marked in sel[t][e].
 __global__ __launch_bounds__(256) void expert_choice_select_kernel(const float *__restrict__ logits, int T, int E,
-                                                                   int C, uint8_t *__restrict__ sel) {
+                                                                   int C, uint16_t *__restrict__ sel) {
     __shared__ unsigned hist[256];
     __shared__ unsigned s_prefix, s_rem;
     __shared__ unsigned wties[4];
@@ -998,9 +1033,9 @@ __global__ __launch_bounds__(256) void expert_choice_select_kernel(const float *
 // them (a later expert past the capacity rows is left out,
 // expert_choice.jl:40-50), gate = probability of the expert for the token;
 // the remaining slots of the kt are empty (id 0).  sel[t][e] becomes the
-// routed slot + 1 of entry (t, e) (<= kcap <= 128), or 0 when expert e did
+// routed slot + 1 of entry (t, e) (<= kcap <= MOE_MAX_EXPERTS), or 0 when expert e did
 // not take token t or the entry was left out.
-__global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__restrict__ sel,
+__global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint16_t *__restrict__ sel,
                                                                      const float *__restrict__ probs, int T, int E,
                                                                      int kt, int kcap, int lsh, int *idx,
                                                                      float *gates) {
@@ -1017,7 +1052,7 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
             if (c < kcap) {
                 idx[(long long)t * kt + lsh + c] = lsh + e + 1;
                 gates[(long long)t * kt + lsh + c] = probs[o];
-                sel[o] = (uint8_t)(c + 1);
+                sel[o] = (uint16_t)(c + 1);
             } else {
                 sel[o] = 0;
             }
@@ -1036,7 +1071,7 @@ __global__ __launch_bounds__(256) void expert_choice_assemble_kernel(uint8_t *__
 // entry's rank among expert e's entries of the block (token-then-slot order,
 // the bucket loop's) is the count of earlier tokens that hold e.  A shared
 // expert e < lsh is held by every token, in slot e.
-__global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint8_t *__restrict__ sel, int T,
+__global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(const uint16_t *__restrict__ sel, int T,
                                                                             int E, int kt, int lsh, int *rank,
                                                                             int *blk_counts, int ldc,
                                                                             int *sup_cnt, int rb) {
@@ -1062,10 +1097,10 @@ __global__ __launch_bounds__(MOE_MAX_EXPERTS) void expert_choice_rank_kernel(con
 }
 
 hipError_t launch_expert_choice(const float *logits, const float *probs, int T, int E, int lsh, int C, int kt,
-                                uint8_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
+                                uint16_t *sel, int *idx, float *gates, int *rank, int *blk_counts, int ldc,
                                 int *sup_cnt, int rb, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    if (lsh < 0 || lsh + E > MOE_MAX_EXPERTS || kt < lsh + min(C, E) || kt > 255 || ldc < lsh + E)
+    if (lsh < 0 || lsh + E > MOE_MAX_EXPERTS || kt < lsh + min(C, E) || kt > MOE_MAX_EXPERTS || ldc < lsh + E)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(expert_choice_select_kernel, dim3(E), dim3(256), 0, s, logits, T, E, C, sel);
     hipLaunchKernelGGL(expert_choice_assemble_kernel, dim3((T + 255) / 256), dim3(256), 0, s, sel, probs, T, E, kt,
@@ -1116,6 +1151,8 @@ __device__ inline void aux_free_step(const int *cnt, int lsh, long long extra, l
 // offsets, counts, tile starts, the (expert, m0) GEMM tile
 // list and the capacity, computes the Switch and z losses and the mean
 // entropy, and runs the AuxiliaryFreeLoss step.  Ends with a barrier.
+constexpr int kScanPerLane = MOE_MAX_EXPERTS / 64;  // experts per lane of the scan's prefix wave
+
 struct ScanLds {
     int cnt[MOE_MAX_EXPERTS];
     int base[MOE_MAX_EXPERTS];
@@ -1224,12 +1261,19 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
     }
     __syncthreads();
     // offsets and GEMM tile starts: exclusive prefixes over the experts by
-    // wave 0 (lane l holds experts 2 l and 2 l + 1; E <= 128)
+    // wave 0 (lane l holds the kScanPerLane experts from kScanPerLane l)
     if (tid < 64) {
-        const int e0 = 2 * tid, e1 = e0 + 1;
-        const int c0 = (e0 < a.E) ? L.cnt[e0] : 0, c1 = (e1 < a.E) ? L.cnt[e1] : 0;
-        const int n0 = (c0 + a.bm - 1) / a.bm, n1 = (c1 + a.bm - 1) / a.bm;
-        int cs = c0 + c1, ns = n0 + n1;
+        const int eb = kScanPerLane * tid;
+        int c[kScanPerLane], n[kScanPerLane];
+        int cs = 0, ns = 0;
+#pragma unroll
+        for (int i = 0; i < kScanPerLane; ++i) {
+            c[i] = (eb + i < a.E) ? L.cnt[eb + i] : 0;
+            n[i] = (c[i] + a.bm - 1) / a.bm;
+            cs += c[i];
+            ns += n[i];
+        }
+        const int cl = cs, nl = ns;  // the lane's own sums
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int cu = __shfl_up(cs, o), nu = __shfl_up(ns, o);
@@ -1238,27 +1282,35 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
                 ns += nu;
             }
         }
-        const int ce = cs - (c0 + c1), ne = ns - (n0 + n1);  // exclusive
-        if (e0 <= a.E) {
-            L.off[e0] = ce;
-            L.tstart[e0] = ne;
+        int ce = cs - cl, ne = ns - nl;  // exclusive
+#pragma unroll
+        for (int i = 0; i < kScanPerLane; ++i) {
+            if (eb + i <= a.E) {
+                L.off[eb + i] = ce;
+                L.tstart[eb + i] = ne;
+            }
+            ce += c[i];
+            ne += n[i];
         }
-        if (e1 <= a.E) {
-            L.off[e1] = ce + c0;
-            L.tstart[e1] = ne + n0;
-        }
-        if (tid == 63) {  // the totals (also for E = 128, past the last pair)
+        if (tid == 63 && a.E == MOE_MAX_EXPERTS) {  // the totals, past the last lane's experts
             L.off[a.E] = cs;
             L.tstart[a.E] = ns;
         }
         if (writer) {
             // the Switch-loss sum over the a.Np terms: in expert order up to 16
-            // experts (Julia's sequential sum), else a fixed tree (Julia's order
-            // for longer arrays is its SIMD reduction, not reproduced)
+            // experts (Julia's sequential sum), else a fixed tree: lane l adds
+            // the pairs (2 l, 2 l + 1) of each 128 experts in turn, then a
+            // butterfly over the lanes (Julia's order for longer arrays is its
+            // SIMD reduction, not reproduced)
             float part = 0.0f;
             if (a.Np > 16) {
-                part = (e0 < a.Np) ? L.fp[e0] : 0.0f;
-                if (e1 < a.Np) part = part + L.fp[e1];
+#pragma unroll
+                for (int q = 0; q < MOE_MAX_EXPERTS / 128; ++q) {
+                    const int e0 = 128 * q + 2 * tid, e1 = e0 + 1;
+                    float pq = (e0 < a.Np) ? L.fp[e0] : 0.0f;
+                    if (e1 < a.Np) pq = pq + L.fp[e1];
+                    part = (q == 0) ? pq : part + pq;
+                }
 #pragma unroll
                 for (int o = 32; o > 0; o >>= 1) part = part + __shfl_xor(part, o);
             } else if (tid == 0) {
@@ -1311,18 +1363,27 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
             const int c = L.cnt[e], f = c / a.bm, r = c - f * a.bm;
             return (r > 0 && 2 * r <= a.bm) ? a.pair_nt * f + a.pair_nt / 2 : a.pair_nt * (f + (r > 0 ? 1 : 0));
         };
-        const int e0 = 2 * tid, e1 = e0 + 1;
-        const int n0 = items(e0), n1 = items(e1);
-        int ns = n0 + n1;
+        const int eb = kScanPerLane * tid;
+        int n[kScanPerLane];
+        int ns = 0;
+#pragma unroll
+        for (int i = 0; i < kScanPerLane; ++i) {
+            n[i] = items(eb + i);
+            ns += n[i];
+        }
+        const int nl = ns;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int nu = __shfl_up(ns, o);
             if (tid >= o) ns += nu;
         }
-        const int ne = ns - (n0 + n1);
-        if (e0 <= a.E) a.item_start[e0] = ne;
-        if (e1 <= a.E) a.item_start[e1] = ne + n0;
-        if (tid == 63 && a.E == 128) a.item_start[128] = ns;
+        int ne = ns - nl;
+#pragma unroll
+        for (int i = 0; i < kScanPerLane; ++i) {
+            if (eb + i <= a.E) a.item_start[eb + i] = ne;
+            ne += n[i];
+        }
+        if (tid == 63 && a.E == MOE_MAX_EXPERTS) a.item_start[a.E] = ns;
     }
     for (int e = tid; e < a.E; e += nth) {
         a.counts[e] = L.cnt[e];
@@ -1554,16 +1615,29 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
 }
 
 // Permute for more slots per token than a wave has lanes (ExpertChoiceGating
-// with min(capacity, E) > 64; kt <= MOE_MAX_EXPERTS): lane l owns entries l
-// and l + 64; same finalisation as permute_kernel, then one row copy per kept
-// entry, element by element (most of these slots are empty).
+// with min(capacity, E) > 64; kt <= MOE_MAX_EXPERTS): lane l owns entries l,
+// l + 64, ... (kWideEnt of them); same finalisation as permute_kernel, then
+// one row copy per kept entry, element by element (most of these slots are
+// empty).
+constexpr int kWideEnt = MOE_MAX_EXPERTS / 64;
+
+// v[c] for a wave-uniform c < kWideEnt, without a dynamically indexed
+// register array
+template <typename V>
+__device__ __forceinline__ V wide_pick(const V (&v)[kWideEnt], int c) {
+    V r = v[0];
+#pragma unroll
+    for (int i = 1; i < kWideEnt; ++i) r = (c == i) ? v[i] : r;
+    return r;
+}
+
 __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, int lane, const ScanLds &L) {
 #pragma clang fp contract(off)
     const int cap = L.cap;
-    int ee[2], pos[2], row[2];
-    float g[2];
+    int ee[kWideEnt], pos[kWideEnt], row[kWideEnt];
+    float g[kWideEnt];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < kWideEnt; ++c) {
         const int j = lane + 64 * c;
         ee[c] = 0; pos[c] = -1; row[c] = -1; g[c] = 0.0f;
         if (j < a.kt) {
@@ -1585,14 +1659,14 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
     if (a.renorm) {
         // gate_sum over the slots in slot order; divide when > 0
         float sum = __shfl(g[0], 0);
-        for (int j = 1; j < a.kt; ++j) sum = sum + __shfl(g[j >> 6], j & 63);
+        for (int j = 1; j < a.kt; ++j) sum = sum + __shfl(wide_pick(g, j >> 6), j & 63);
         if (sum > 0.0f) {
-            g[0] = g[0] / sum;
-            g[1] = g[1] / sum;
+#pragma unroll
+            for (int c = 0; c < kWideEnt; ++c) g[c] = g[c] / sum;
         }
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < kWideEnt; ++c) {
         const int j = lane + 64 * c;
         if (j < a.kt) {
             const long long ent = (long long)t * a.kt + j;
@@ -1609,7 +1683,7 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
     }
     if (!a.copy_rows) return;
     for (int j = 0; j < a.kt; ++j) {
-        const int p = __shfl(row[j >> 6], j & 63);
+        const int p = __shfl(wide_pick(row, j >> 6), j & 63);
         if (p < 0) continue;
         for (int d = lane; d < a.D; d += 64) {
             const float v = a.x_bf16 ? bf16_to_f32(((const uint16_t *)a.x)[(long long)t * a.D + d])
@@ -1631,7 +1705,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_wide_kernel(PermuteArgs 
 hipError_t launch_permute(PermuteArgs a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     const int nblk = (a.T + a.rb - 1) / a.rb;
-    if (a.kt > 2 * 64 || a.rb < kPermTokens || a.rb % kPermTokens || a.s.nblk != nblk || a.s.E > MOE_MAX_EXPERTS ||
+    if (a.kt > kWideEnt * 64 || a.rb < kPermTokens || a.rb % kPermTokens || a.s.nblk != nblk || a.s.E > MOE_MAX_EXPERTS ||
         a.s.ldc < a.s.E || a.s.ldc % 4)
         return hipErrorInvalidValue;
     // tokens per workgroup: kPermTokens (one per wave) while that leaves at

@@ -72,21 +72,22 @@ void oracle_softmax(const float *logits, int64_t T, int E, float *probs)
 
 /* ---- top-k with renormalisation -----------------------------------------
  * src/gating/topk.jl:33-41: partialsortperm(probs[:,t], 1:k, rev=true),
- * then gates = p_sel ./ sum(p_sel) (sum sequential in slot order for k < 16,
- * Julia's short-array reduction). */
-static void topk_row(const float *p, int E, int k, int32_t *idx, float *g)
+ * then gates = p_sel ./ sum(p_sel), the sum sequential in slot order: Julia's
+ * short-array loop for k < 16; for k = 16 its mapreduce_impl adds a1 + a2 and
+ * then the other 14 in an @simd loop, too short for a vectorised body (the
+ * scalar remainder runs them in order).  `taken`: E bytes of scratch. */
+static void topk_row(const float *p, int E, int k, int32_t *idx, float *g, uint8_t *taken)
 {
-    uint64_t taken_lo = 0, taken_hi = 0; /* E <= 128 */
+    memset(taken, 0, (size_t)E);
     for (int j = 0; j < k; ++j) {
         int best = -1;
         uint32_t bk = 0;
         for (int i = 0; i < E; ++i) {
-            int taken = (i < 64) ? (int)((taken_lo >> i) & 1u) : (int)((taken_hi >> (i - 64)) & 1u);
-            if (taken) continue;
+            if (taken[i]) continue;
             uint32_t key = isless_key(p[i]);
             if (best < 0 || key > bk) { best = i; bk = key; } /* strict > : lower index wins ties */
         }
-        if (best < 64) taken_lo |= 1ull << best; else taken_hi |= 1ull << (best - 64);
+        taken[best] = 1;
         idx[j] = best + 1;
     }
     float s = p[idx[0] - 1];
@@ -99,11 +100,14 @@ static void topk_row(const float *p, int E, int k, int32_t *idx, float *g)
 int oracle_compute_gates_topk(const float *logits, int64_t T, int E, int k,
                               int32_t *idx, float *gates, float *probs)
 {
-    if (E < 1 || E > 128 || k < 1 || k > E) return -1;
+    if (E < 1 || k < 1 || k > E) return -1;
+    uint8_t *taken = (uint8_t *)malloc((size_t)E);
+    if (!taken) return -2;
     for (int64_t t = 0; t < T; ++t) {
         softmax_row(logits + t * E, E, probs + t * E);
-        topk_row(probs + t * E, E, k, idx + t * k, gates + t * k);
+        topk_row(probs + t * E, E, k, idx + t * k, gates + t * k, taken);
     }
+    free(taken);
     return 0;
 }
 
@@ -114,19 +118,23 @@ int oracle_compute_gates_shared(const float *logits, int64_t T, int E, int ns, i
                                 int32_t *idx, float *gates, float *probs)
 {
     int Er = E - ns;
-    if (ns < 0 || Er < 1 || Er > 128 || k < 1 || k > Er) return -1;
+    if (ns < 0 || Er < 1 || k < 1 || k > Er) return -1;
     int tk = ns + k;
     float *pr = (float *)malloc(sizeof(float) * (size_t)Er);
-    int32_t ri[128];
-    float rg[128];
-    if (!pr) return -2;
+    int32_t *ri = (int32_t *)malloc(sizeof(int32_t) * (size_t)k);
+    float *rg = (float *)malloc(sizeof(float) * (size_t)k);
+    uint8_t *taken = (uint8_t *)malloc((size_t)Er);
+    if (!pr || !ri || !rg || !taken) {
+        free(pr); free(ri); free(rg); free(taken);
+        return -2;
+    }
     const double routed_gate_scale = 1.0 - (double)ns / (double)tk; /* 1.0f0 - Int/Int -> Float64 */
     const double routed_prob_scale = 1.0 - (double)ns / (double)E;
     const float shared_gate = 1.0f / (float)tk;
     const float shared_prob = 1.0f / (float)E;
     for (int64_t t = 0; t < T; ++t) {
         softmax_row(logits + t * E + ns, Er, pr);
-        topk_row(pr, Er, k, ri, rg);
+        topk_row(pr, Er, k, ri, rg, taken);
         for (int j = 0; j < ns; ++j) {
             idx[t * tk + j] = j + 1;
             gates[t * tk + j] = shared_gate;
@@ -138,7 +146,7 @@ int oracle_compute_gates_shared(const float *logits, int64_t T, int E, int ns, i
         for (int i = 0; i < ns; ++i) probs[t * E + i] = shared_prob;
         for (int i = 0; i < Er; ++i) probs[t * E + ns + i] = (float)((double)pr[i] * routed_prob_scale);
     }
-    free(pr);
+    free(pr); free(ri); free(rg); free(taken);
     return 0;
 }
 

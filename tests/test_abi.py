@@ -53,7 +53,7 @@ def _cfg(**kw):
 
 @pytest.mark.parametrize("bad,msg", [
     (dict(num_experts=0), "num_experts"),
-    (dict(num_experts=129), "num_experts"),
+    (dict(num_experts=513), "num_experts"),
     (dict(top_k=9), "top_k"),
     (dict(top_k=0), "top_k"),
     (dict(top_k=17, num_experts=32), "MOE_MAX_TOPK"),

@@ -99,11 +99,12 @@ def test_decode_many_experts(moe, oracle):
         c.dev.close()
 
 
-@pytest.mark.parametrize("E,k,lsh", [(20, 12, 0), (96, 16, 0), (14, 10, 3)])
+@pytest.mark.parametrize("E,k,lsh", [(20, 12, 0), (96, 16, 0), (14, 10, 3), (200, 8, 0), (384, 8, 1), (512, 6, 0)])
 def test_decode_more_than_8_slots(moe, oracle, E, k, lsh):
     # up to MOE_MAX_TOPK = 16 slots per token (routed experts of slots 8..15
-    # in the upper words of the wave's slot list), E <= 64 and E > 64 gating,
-    # with and without the layer's shared experts
+    # in the upper words of the wave's slot list), E <= 64 and E > 64 gating
+    # (up to 512 experts: 8 per lane), with and without the layer's shared
+    # experts
     Et = E + lsh
     c = Case(moe, oracle, T=6, D=256, H=200, E=Et, k=k, wdtype="f32", seed=60 + k, lsh=lsh, max_tokens=8)
     try:

@@ -220,6 +220,7 @@ def test_shared_experts_with_every_gate(moe, oracle, gate, lsh, k, ns, E, param,
     ("topk", 2, 2, 8, None, 2),             # the second call updates
     ("expert_choice", 1, 1, 5, 1.0, 1),     # empty entries count for bias index lsh - 1
     ("switch", 3, 1, 9, None, 1),
+    ("topk", 1, 4, 300, None, 1),           # bias over 300 experts
 ])
 def test_shared_experts_aux_free_loss(moe, oracle, gate, lsh, k, E, param, update_freq):
     # AuxiliaryFreeLoss with shared experts: the gate sees the plain logits
@@ -354,7 +355,10 @@ def test_aux_free_python_api(moe, oracle):
                                                       # more than 8 slots per token: min(capacity, E) = 16, 64, 86
                                                       ("expert_choice", 1.25, 16, 0, "bf16", 4096),
                                                       ("expert_choice", 1.25, 64, 0, "bf16", 4096),
-                                                      ("expert_choice", 4.0, 96, 0, "f32", 2048)])
+                                                      ("expert_choice", 4.0, 96, 0, "f32", 2048),
+                                                      # over 128 experts; 134 slots per token (wide permute)
+                                                      ("soft", 0.9, 300, 5, "bf16", 600),
+                                                      ("expert_choice", 100.0, 300, 0, "bf16", 400)])
 def test_soft_and_expert_choice_layer(moe, oracle, gate, param, E, k, wdtype, T):
     # the layer forward with SoftMoEGating / ExpertChoiceGating against the
     # oracle on the GPU's logits: routing bit-exact, output and loss in tolerance
@@ -551,6 +555,35 @@ def test_shared_experts_more_than_8_slots(moe, oracle, gate, lsh, k, ns, E, para
     try:
         check_shared_experts_case(c, TOL[wdtype], training=True)
         check_shared_experts_case(c, TOL[wdtype], training=False)
+    finally:
+        c.dev.close()
+
+
+@pytest.mark.parametrize("E,k,gate,ns,lsh,wdtype,T", [
+    (129, 4, "topk", 0, 0, "bf16", 900),     # 32 experts per gating lane, two logits column groups
+    (256, 8, "topk", 0, 0, "bf16", 1500),    # DeepSeek-V3's routed expert count
+    (300, 6, "shared", 2, 0, "fp8", 700),
+    (512, 1, "switch", 0, 0, "bf16", 1200),  # MOE_MAX_EXPERTS: 16-token route blocks, 64 experts per lane
+    (160, 3, "topk", 0, 0, "f32", 500),      # fp32 x: the six-term logits GEMM over 10 tiles
+    (385, 8, "topk", 0, 1, "bf16", 800),     # 384 routed + 1 shared expert of the layer
+])
+def test_over_128_experts(moe, oracle, E, k, gate, ns, lsh, wdtype, T):
+    # more experts than a 128-row router: the logits GEMM in column groups of
+    # 128, the gating with 32 or 64 experts per lane on 32- or 16-token route
+    # blocks, the scan's prefix over up to 512 experts; routing bit-exact,
+    # output and losses within tolerance
+    rng = np.random.default_rng(E + k)
+    bias = (rng.standard_normal(E - lsh) * 0.5).astype(np.float32) if lsh == 0 else None
+    c = Case(moe, oracle, T=T, D=128, H=96, E=E, k=k, gate=gate, ns=ns, wdtype=wdtype,
+             xdtype="f32" if wdtype == "f32" else "bf16", seed=E * 3 + k, router_bias=bias, lsh=lsh)
+    try:
+        if lsh:
+            check_shared_experts_case(c, TOL[wdtype], training=True)
+            check_shared_experts_case(c, TOL[wdtype], training=False)
+        else:
+            check_case(c, TOL[wdtype])
+            check_case(c, TOL[wdtype], training=False)
+            check_case(c, TOL[wdtype], T=T // 3 + 1)
     finally:
         c.dev.close()
 

@@ -63,7 +63,7 @@ def test_topk_random_logits(moe, oracle, T, E, k):
     check_route(moe, oracle, logits, "topk", k)
 
 
-@pytest.mark.parametrize("E", [65, 96, 128])
+@pytest.mark.parametrize("E", [65, 96, 128, 129, 256, 300, 512])
 @pytest.mark.parametrize("k", [2, 3, 6, 8])
 def test_topk_over_64_experts(moe, oracle, E, k):
     # more than 64 routed experts with k >= 2: each of a token's 8 lanes keeps
@@ -85,7 +85,7 @@ def test_topk_over_64_experts(moe, oracle, E, k):
     check_route(moe, oracle, lg, "topk", k)
 
 
-@pytest.mark.parametrize("E,ns,k", [(100, 2, 6), (128, 1, 7), (67, 2, 2)])
+@pytest.mark.parametrize("E,ns,k", [(100, 2, 6), (128, 1, 7), (67, 2, 2), (257, 1, 8), (385, 1, 8)])
 def test_shared_gating_over_64_routed(moe, oracle, E, ns, k):
     rng = np.random.default_rng(E + ns + k)
     lg = rng.standard_normal((2500, E)).astype(np.float32)
@@ -194,7 +194,7 @@ def test_routing_is_deterministic(moe, oracle):
 
 
 @pytest.mark.parametrize("T,E,k,lam", [(2048, 8, 2, 0.7), (1000, 64, 6, 2.0), (77, 5, 3, -1.5), (1500, 128, 4, 0.9),
-                                       (600, 96, 8, 1.0)])
+                                       (600, 96, 8, 1.0), (700, 300, 6, 1.3), (300, 512, 12, 0.8)])
 def test_soft_moe_gating(moe, oracle, T, E, k, lam):
     # SoftMoEGating: top-k of softmax(logits ./ lambda), the gate matrix is the
     # probabilities (the dispatch reads the probability of expert `slot`)
@@ -210,7 +210,8 @@ def test_soft_moe_gating(moe, oracle, T, E, k, lam):
 
 @pytest.mark.parametrize("T,E,cf,ties", [(4096, 8, 1.25, False), (64, 16, 1.0, True), (300, 8, 0.25, True),
                                          (33, 6, 3.0, True), (4096, 16, 1.25, False), (4096, 64, 1.25, False),
-                                         (1000, 64, 2.0, True), (2048, 128, 6.0, False)])
+                                         (1000, 64, 2.0, True), (2048, 128, 6.0, False), (2048, 256, 6.0, False),
+                                         (500, 512, 3.0, True)])
 def test_expert_choice_gating(moe, oracle, T, E, cf, ties):
     # ExpertChoiceGating: the (capacity, T) indices / gates bit-exact
     rng = np.random.default_rng(T * E)
@@ -233,7 +234,9 @@ def test_expert_choice_many_slots_bucketing(moe, oracle):
     assert np.array_equal(idx[:, :16], np.tile(np.arange(1, 17)[:, None], (1, 16)))
     assert np.all(idx[:, 16:] == 0)
     rng = np.random.default_rng(77)
-    for T, E, cf in ((64, 16, 4.0), (4096, 64, 1.25), (500, 128, 40.0)):
+    # (500, 300, 150.0): 250 slots per token, (300, 512, 600.0): 352 (a lane
+    # of the wide permute owns 4 and 6 of them)
+    for T, E, cf in ((64, 16, 4.0), (4096, 64, 1.25), (500, 128, 40.0), (500, 300, 150.0), (300, 512, 600.0)):
         lg = rng.standard_normal((T, E)).astype(np.float32)
         g = moe.ExpertChoiceGating(cf)
         print(f"expert choice bucketing T={T} E={E} cf={cf}", flush=True)

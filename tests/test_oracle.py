@@ -64,6 +64,30 @@ def test_topk_brute_force(oracle):
             assert sorted(float(p[t, i]) for i in best) == sorted(float(p[t, i - 1]) for i in idx[t])
 
 
+def test_topk_many_experts_and_slots_sorted_order(oracle):
+    # up to 512 experts and 16 slots: the k-pass selection equals the head of
+    # a stable sort by (isless desc, index asc) (numpy lexsort), with ties;
+    # the gates are p / (sequential slot-order sum), and SharedExpertGating's
+    # routed slots are the same top-k over rows ns+1..E
+    rng = np.random.default_rng(12)
+    for E, k in ((129, 16), (300, 9), (512, 16), (512, 1)):
+        for ties in (False, True):
+            lg = (rng.integers(-2, 3, size=(40, E)) if ties else rng.standard_normal((40, E))).astype(np.float32)
+            idx, g, p = oracle.compute_gates_topk(lg, k)
+            keys = np.array([[isless_sort_key(float(v)) for v in row] for row in p])
+            for t in range(40):
+                order = np.lexsort((np.arange(E), -keys[t][:, 1], -keys[t][:, 0]))
+                assert np.array_equal(idx[t] - 1, order[:k])
+                sel = p[t, idx[t] - 1]
+                s = sel[0]
+                for v in sel[1:]:
+                    s = np.float32(s + v)
+                assert np.array_equal(g[t], (sel / s).astype(np.float32))
+            si, sg, sp = oracle.compute_gates_shared(lg, 1, min(k, E - 1))
+            ri, _, _ = oracle.compute_gates_topk(lg[:, 1:], min(k, E - 1))
+            assert np.array_equal(si[:, 1:], ri + 1) and np.all(si[:, 0] == 1)
+
+
 def test_softmax_matches_float64(oracle):
     # independent restatement: float64 softmax; oracle within 2 ulp-ish
     rng = np.random.default_rng(3)

@@ -52,7 +52,7 @@ def test_switch_loss_noalloc_limits(moe):
     L = _lib.lib()
     out = torch.zeros(1, dtype=torch.float32, device="cuda")
     # more experts than the scratch array holds: a clear error, nothing launched
-    st = L.moe_switch_loss_noalloc(None, 4, 1, None, 129, ctypes.c_float(0.01), out.data_ptr(), None)
+    st = L.moe_switch_loss_noalloc(None, 4, 1, None, 513, ctypes.c_float(0.01), out.data_ptr(), None)
     assert st == _lib.MOE_EINVAL
     assert "MOE_MAX_EXPERTS" in L.moe_last_error(None).decode()
     # an empty batch: the NaN of a mean over no tokens, as moe_switch_loss returns
