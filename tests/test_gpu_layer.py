@@ -588,6 +588,35 @@ def test_over_128_experts(moe, oracle, E, k, gate, ns, lsh, wdtype, T):
         c.dev.close()
 
 
+@pytest.mark.parametrize("E,kd,wdtype,T", [(300, 12, "bf16", 500), (40, 16, "f32", 300), (512, 3, "bf16", 700)])
+def test_forward_routed_many_experts_and_slots(moe, oracle, E, kd, wdtype, T):
+    # moe_forward_routed (the caller's indices and gates, as HashGating /
+    # RandomGating hand them over) with up to 512 experts and 16 slots per
+    # token; some slots empty (id 0, skipped as the dispatch's expert_id > 0
+    # check does, src/core/moe_layer.jl:198); the Switch loss on 1/E
+    # probabilities
+    # (the handle's routing buffers hold max_tokens * 2 slots: room for T * kd)
+    c = Case(moe, oracle, T=T, D=128, H=96, E=E, k=2, wdtype=wdtype, xdtype="f32" if wdtype == "f32" else "bf16",
+             seed=E + kd, max_tokens=T * kd // 2)
+    try:
+        rng = np.random.default_rng(E * kd)
+        idx = np.stack([rng.choice(E, kd, replace=False) + 1 for _ in range(T)]).astype(np.int32)
+        idx[::17, kd // 2] = 0
+        gates = rng.random((T, kd)).astype(np.float32)
+        print(f"forward_routed E={E} kd={kd}", flush=True)
+        out, loss, res = c.dev.forward_routed(np.ascontiguousarray(c.x_dev), c.xcode, True, idx, gates, want_aux=True)
+        ref, ref_loss, aux = oracle.moe_forward(c.x, c.wr, c.ex, k=kd, training=True, logits=res["logits"],
+                                                given=(idx, gates, None), alpha=c.alpha, z_weight=c.z)
+        assert np.array_equal(res["indices"], idx) and np.array_equal(res["gates"].view(np.uint32), gates.view(np.uint32))
+        assert np.array_equal(res["counts"], aux["counts"]) and np.array_equal(res["offsets"], aux["offsets"])
+        n = int(aux["offsets"][-1])
+        assert np.array_equal(res["perm"][:n], aux["perm"])
+        assert rel_err(out, ref) <= TOL[wdtype]
+        assert abs(loss - ref_loss) <= 1e-5 * max(1.0, abs(float(ref_loss))), (loss, ref_loss)
+    finally:
+        c.dev.close()
+
+
 def test_varying_batch_on_one_handle(moe, oracle):
     c = Case(moe, oracle, T=300, D=128, H=256, E=8, k=2, wdtype="bf16", xdtype="bf16", seed=9)
     for T in (300, 1, 7, 129, 300):
