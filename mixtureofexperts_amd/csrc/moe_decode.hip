@@ -105,19 +105,12 @@ struct DecodeSel {
     }
 };
 
-// v[i >> 6] for a wave-uniform i < 64 NH, without a dynamically indexed
-// register array
-template <int NH, typename V>
-__device__ __forceinline__ V part_of(const V (&v)[NH], int i) {
-    V r = v[0];
-#pragma unroll
-    for (int h = 1; h < NH; ++h) r = ((i >> 6) == h) ? v[h] : r;
-    return r;
-}
-
 // compute_gates of token t from the wave partials in L (see decode_route_block);
 // E > 64: lane l holds experts l, l + 64, ..., l + 64 (NH - 1) (E <= 64:
-// decode_gates64).
+// decode_gates64).  The per-expert passes walk part h = 0 .. NH - 1, then its
+// lanes, i.e. the experts in ascending order; every register array is read
+// with compile-time indices only (a part picked at run time would be a
+// private-memory array).
 template <int NH>
 __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bool write,
                                                            const DecodeRouteLds &L, float &gate) {
@@ -133,32 +126,32 @@ __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bo
         if (a.br) v = v + a.br[min(e, E - 1)];
         lg[h] = v;
     }
-    // lane i & 63 of part i >> 6
-#define MOE_LANE_OF(arr, i) part_of<NH>(arr, i)
     float m = -INFINITY;                                // max, NaN ignored
-    for (int i0 = 0; i0 < E; i0 += 8) {
-        float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = min(i0 + u, E - 1);
-            v[u] = readlane_f(MOE_LANE_OF(lg, i), i & 63);
+    for (int h = 0; h < NH; ++h) {
+        const int nh = min(64, E - 64 * h);             // experts of part h (<= 0: none)
+        for (int i0 = 0; i0 < nh; i0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = readlane_f(lg[h], min(i0 + u, nh - 1));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) m = (i0 + u < nh) ? fmaxf(m, v[u]) : m;
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) m = (i0 + u < E) ? fmaxf(m, v[u]) : m;
     }
 #pragma unroll
     for (int h = 0; h < NH; ++h)
         ev[h] = (m == INFINITY) ? ((lg[h] == INFINITY) ? 1.0f : 0.0f) : (float)exp((double)(lg[h] - m));
     float s = 0.0f;                                     // expert order
-    for (int i0 = 0; i0 < E; i0 += 8) {
-        float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = min(i0 + u, E - 1);
-            v[u] = readlane_f(MOE_LANE_OF(ev, i), i & 63);
+    for (int h = 0; h < NH; ++h) {
+        const int nh = min(64, E - 64 * h);
+        for (int i0 = 0; i0 < nh; i0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = readlane_f(ev[h], min(i0 + u, nh - 1));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = (i0 + u < nh) ? s + v[u] : s;
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) s = (i0 + u < E) ? s + v[u] : s;
     }
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -168,24 +161,24 @@ __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bo
     int rank[NH];
 #pragma unroll
     for (int h = 0; h < NH; ++h) rank[h] = 0;
-    for (int i0 = 0; i0 < E; i0 += 8) {
-        uint32_t kv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = min(i0 + u, E - 1);
-            kv[u] = (uint32_t)__builtin_amdgcn_readlane((int)MOE_LANE_OF(key, i), i & 63);
-        }
+    for (int h2 = 0; h2 < NH; ++h2) {
+        const int nh = min(64, E - 64 * h2);
+        for (int i0 = 0; i0 < nh; i0 += 8) {
+            uint32_t kv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = i0 + u;
+            for (int u = 0; u < 8; ++u) kv[u] = (uint32_t)__builtin_amdgcn_readlane((int)key[h2], min(i0 + u, nh - 1));
 #pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const int e = lane + 64 * h;
-                rank[h] += (i < E && (kv[u] > key[h] || (kv[u] == key[h] && i < e))) ? 1 : 0;
+            for (int u = 0; u < 8; ++u) {
+                const int i = 64 * h2 + i0 + u;
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const int e = lane + 64 * h;
+                    rank[h] += (i0 + u < nh && (kv[u] > key[h] || (kv[u] == key[h] && i < e))) ? 1 : 0;
+                }
             }
         }
     }
-#undef MOE_LANE_OF
     float ssum = 0.0f, myp = 0.0f;
     int mye = 0;
     DecodeSel packed;
@@ -199,7 +192,12 @@ __device__ __forceinline__ DecodeSel decode_gates(const DecodeArgs &a, int t, bo
             e = (!found && b) ? 64 * h + __builtin_ctzll(b) : e;
             found = found || b;
         }
-        const float pj = readlane_f(part_of<NH>(pv, e), e & 63);
+        float pj = 0.0f;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float c = readlane_f(pv[h], e & 63);
+            pj = ((e >> 6) == h) ? c : pj;
+        }
         ssum = (j == 0) ? pj : ssum + pj;  // slot order
         packed.set(j, e);
         if (lane == j) {
@@ -332,7 +330,7 @@ __device__ __forceinline__ DecodeSel decode_gates64(const DecodeArgs &a, int t, 
 // Returns the 0-based experts of the routed slots (uniform), and in `gate`
 // of lane j < k that slot's gate; `write` (wave 0 of
 // one block per token) stores logits, probs, indices, gates.
-__device__ DecodeSel decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L,
+__device__ __forceinline__ DecodeSel decode_route_block(const DecodeArgs &a, int t, bool write, DecodeRouteLds &L,
                                                  float &gate) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;

@@ -1151,8 +1151,6 @@ __device__ inline void aux_free_step(const int *cnt, int lsh, long long extra, l
 // offsets, counts, tile starts, the (expert, m0) GEMM tile
 // list and the capacity, computes the Switch and z losses and the mean
 // entropy, and runs the AuxiliaryFreeLoss step.  Ends with a barrier.
-constexpr int kScanPerLane = MOE_MAX_EXPERTS / 64;  // experts per lane of the scan's prefix wave
-
 struct ScanLds {
     int cnt[MOE_MAX_EXPERTS];
     int base[MOE_MAX_EXPERTS];
@@ -1261,40 +1259,32 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
     }
     __syncthreads();
     // offsets and GEMM tile starts: exclusive prefixes over the experts by
-    // wave 0 (lane l holds the kScanPerLane experts from kScanPerLane l)
+    // wave 0, in groups of 64 experts (lane l: expert g0 + l of group g0)
     if (tid < 64) {
-        const int eb = kScanPerLane * tid;
-        int c[kScanPerLane], n[kScanPerLane];
-        int cs = 0, ns = 0;
+        int cbase = 0, nbase = 0;  // totals of the groups before
+        for (int g0 = 0; g0 < a.E; g0 += 64) {
+            const int e = g0 + tid;
+            const int c = (e < a.E) ? L.cnt[e] : 0;
+            const int n = (c + a.bm - 1) / a.bm;
+            int cs = c, ns = n;
 #pragma unroll
-        for (int i = 0; i < kScanPerLane; ++i) {
-            c[i] = (eb + i < a.E) ? L.cnt[eb + i] : 0;
-            n[i] = (c[i] + a.bm - 1) / a.bm;
-            cs += c[i];
-            ns += n[i];
-        }
-        const int cl = cs, nl = ns;  // the lane's own sums
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int cu = __shfl_up(cs, o), nu = __shfl_up(ns, o);
-            if (tid >= o) {
-                cs += cu;
-                ns += nu;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int cu = __shfl_up(cs, o), nu = __shfl_up(ns, o);
+                if (tid >= o) {
+                    cs += cu;
+                    ns += nu;
+                }
             }
-        }
-        int ce = cs - cl, ne = ns - nl;  // exclusive
-#pragma unroll
-        for (int i = 0; i < kScanPerLane; ++i) {
-            if (eb + i <= a.E) {
-                L.off[eb + i] = ce;
-                L.tstart[eb + i] = ne;
+            if (e <= a.E) {  // (e == E: the totals)
+                L.off[e] = cbase + cs - c;
+                L.tstart[e] = nbase + ns - n;
             }
-            ce += c[i];
-            ne += n[i];
+            cbase += __shfl(cs, 63);
+            nbase += __shfl(ns, 63);
         }
-        if (tid == 63 && a.E == MOE_MAX_EXPERTS) {  // the totals, past the last lane's experts
-            L.off[a.E] = cs;
-            L.tstart[a.E] = ns;
+        if (tid == 0 && (a.E & 63) == 0) {  // the totals, past the last group's lanes
+            L.off[a.E] = cbase;
+            L.tstart[a.E] = nbase;
         }
         if (writer) {
             // the Switch-loss sum over the a.Np terms: in expert order up to 16
@@ -1363,27 +1353,20 @@ __device__ __forceinline__ void scan_block(const ScanArgs &a, int blk, ScanLds &
             const int c = L.cnt[e], f = c / a.bm, r = c - f * a.bm;
             return (r > 0 && 2 * r <= a.bm) ? a.pair_nt * f + a.pair_nt / 2 : a.pair_nt * (f + (r > 0 ? 1 : 0));
         };
-        const int eb = kScanPerLane * tid;
-        int n[kScanPerLane];
-        int ns = 0;
+        int nbase = 0;
+        for (int g0 = 0; g0 < a.E; g0 += 64) {
+            const int e = g0 + tid;
+            const int n = items(e);
+            int ns = n;
 #pragma unroll
-        for (int i = 0; i < kScanPerLane; ++i) {
-            n[i] = items(eb + i);
-            ns += n[i];
+            for (int o = 1; o < 64; o <<= 1) {
+                const int nu = __shfl_up(ns, o);
+                if (tid >= o) ns += nu;
+            }
+            if (e <= a.E) a.item_start[e] = nbase + ns - n;
+            nbase += __shfl(ns, 63);
         }
-        const int nl = ns;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int nu = __shfl_up(ns, o);
-            if (tid >= o) ns += nu;
-        }
-        int ne = ns - nl;
-#pragma unroll
-        for (int i = 0; i < kScanPerLane; ++i) {
-            if (eb + i <= a.E) a.item_start[eb + i] = ne;
-            ne += n[i];
-        }
-        if (tid == 63 && a.E == MOE_MAX_EXPERTS) a.item_start[a.E] = ns;
+        if (tid == 0 && (a.E & 63) == 0) a.item_start[a.E] = nbase;
     }
     for (int e = tid; e < a.E; e += nth) {
         a.counts[e] = L.cnt[e];
