@@ -38,6 +38,16 @@ DEVICE_ONLY_FLAGS = [
 ]
 
 
+# The device pass reports each kernel's resources (registers, LDS, private
+# "scratch" memory per lane); build_library writes them to RESOURCES_PATH.
+# A kernel with scratch keeps a register array in memory (a runtime index
+# into it, or spills): the kernels here are written to need none.
+RESOURCES_PATH = os.path.join(PKG_DIR, "kernel_resources.json")
+_RESOURCE_FIELDS = {"TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch",
+                    "Occupancy [waves/SIMD]": "occupancy", "VGPRs Spill": "vgpr_spill",
+                    "LDS Size [bytes/block]": "lds"}
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -45,6 +55,28 @@ def _run(cmd, verbose):
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode}): {' '.join(cmd)}")
+    return res
+
+
+def parse_resource_remarks(text):
+    """{kernel symbol: {sgprs, vgprs, agprs, scratch, occupancy, lds}} from the
+    compiler's kernel-resource-usage remarks."""
+    import re
+
+    out, name = {}, None
+    for line in text.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            out[name] = {}
+            continue
+        if name is None:
+            continue
+        for label, key in _RESOURCE_FIELDS.items():
+            m = re.search(r"remark:\s+" + re.escape(label) + r": (\d+)", line)
+            if m:
+                out[name][key] = int(m.group(1))
+    return out
 
 
 def build_library(verbose: bool = False) -> str:
@@ -61,18 +93,27 @@ def build_library(verbose: bool = False) -> str:
         bundle = os.path.join(tmpdir, stem + ".hipfb")
         obj = os.path.join(tmpdir, stem + ".o")
         cuid = f"-cuid=moe_{stem}"
-        _run([HIPCC, *HIP_FLAGS, *DEVICE_ONLY_FLAGS, *incs, cuid, "--cuda-device-only", "-c", path, "-o", bundle],
-             verbose)
+        dev = _run([HIPCC, *HIP_FLAGS, *DEVICE_ONLY_FLAGS, *incs, cuid, "--cuda-device-only",
+                    "-Rpass-analysis=kernel-resource-usage", "-c", path, "-o", bundle], verbose)
         _run([HIPCC, *HIP_FLAGS, *incs, cuid, "--cuda-host-only", "-Xclang", "-fcuda-include-gpubinary", "-Xclang",
               bundle, "-c", path, "-o", obj], verbose)
-        return obj
+        return obj, parse_resource_remarks(dev.stderr)
+
+    import json
 
     with tempfile.TemporaryDirectory(prefix="moe_build_") as tmpdir:
         with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-            objs = [f.result() for f in [pool.submit(compile_one, s, tmpdir) for s in SOURCES]]
+            done = [f.result() for f in [pool.submit(compile_one, s, tmpdir) for s in SOURCES]]
+        objs = [o for o, _ in done]
         tmp = LIB_PATH + ".tmp"
         _run([HIPCC, f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)
+    resources = {src: res for src, (_, res) in zip(SOURCES, done)}
+    with open(RESOURCES_PATH, "w") as f:
+        json.dump(resources, f, indent=1, sort_keys=True)
+    scratch = [k for r in resources.values() for k, v in r.items() if v.get("scratch", 0) > 0]
+    if scratch:
+        sys.stderr.write("warning: kernels with private (scratch) memory: " + ", ".join(scratch) + "\n")
     return LIB_PATH
 
 

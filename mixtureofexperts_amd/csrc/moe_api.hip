@@ -963,8 +963,11 @@ int moe_create(const moe_config *cfg, moe_handle **out) {
     h->bf16_gemm = h->ct == CT_BF16 && (h->wt == WT_BF16 || h->wt == WT_FP8);
     // 256-row tiles for a few large experts (at most 16, averaging at least 384
     // rows at max_tokens); 128-row tiles, two workgroups per CU, for many or
-    // small ones (fine-grained MoE layers: skewed counts, short K)
-    h->bm = (h->bf16_gemm && h->E <= 16 && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
+    // small ones (fine-grained MoE layers: skewed counts, short K), and for
+    // standard experts with fp8 weights (on 256-row tiles their up GEMM's
+    // accumulators, fp8 stage bytes and epilogue scales exceed the registers)
+    const bool fp8_std = h->wt == WT_FP8 && !h->gated;
+    h->bm = (h->bf16_gemm && !fp8_std && h->E <= 16 && (long long)h->rows_max >= 384LL * h->E) ? 256 : kGemmBM;
     h->max_tiles = h->rows_max / h->bm + h->E + 1;
     // bf16 kernel: xp and h are A tile images of up to max_tiles M tiles
     h->act_rows = h->bf16_gemm ? (long long)h->max_tiles * h->bm : h->rows_max;

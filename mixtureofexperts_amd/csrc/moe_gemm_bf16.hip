@@ -373,7 +373,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const TileJob &jb,
         const bool vec4 = (MODE == MODE_STD_UP) || ((g.ldc & 3) == 0);
         const bool yb = (MODE == MODE_STD_UP) || (g.c_bf16 && jb.nks == 1);
         const bool has_bias = g.bias && jb.ks == 0;  // split K: the bias belongs to one partial sum only
-        constexpr int JH = (WF8 && IM == 4) ? 1 : (JN + 1) / 2;  // column blocks per part
+        constexpr int JH = ((WF8 || MODE == MODE_STD_UP) && IM == 4) ? 1 : (JN + 1) / 2;  // column blocks per part
         auto part = [&](auto H_, auto DROP_) {
             constexpr int H = decltype(H_)::value;
             constexpr bool DROP = decltype(DROP_)::value;
@@ -1194,8 +1194,7 @@ hipError_t launch_grouped_gemm_bf16(int mode, int bm, int wfp8, const GemmArgs &
     MOE_BF16_CASE(MODE_STD_UP, 128, 0)
     MOE_BF16_CASE(MODE_DOWN, 128, 0)
     MOE_BF16_CASE(MODE_GATED_UP, 256, 1)
-    MOE_BF16_CASE(MODE_STD_UP, 256, 1)
-    MOE_BF16_CASE(MODE_DOWN, 256, 1)
+    MOE_BF16_CASE(MODE_DOWN, 256, 1)  // (standard experts with fp8 weights take 128-row tiles)
     MOE_BF16_CASE(MODE_GATED_UP, 128, 1)
     MOE_BF16_CASE(MODE_STD_UP, 128, 1)
     MOE_BF16_CASE(MODE_DOWN, 128, 1)

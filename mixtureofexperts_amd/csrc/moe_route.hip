@@ -1604,16 +1604,6 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteArgs a) {
 // empty).
 constexpr int kWideEnt = MOE_MAX_EXPERTS / 64;
 
-// v[c] for a wave-uniform c < kWideEnt, without a dynamically indexed
-// register array
-template <typename V>
-__device__ __forceinline__ V wide_pick(const V (&v)[kWideEnt], int c) {
-    V r = v[0];
-#pragma unroll
-    for (int i = 1; i < kWideEnt; ++i) r = (c == i) ? v[i] : r;
-    return r;
-}
-
 __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, int lane, const ScanLds &L) {
 #pragma clang fp contract(off)
     const int cap = L.cap;
@@ -1639,10 +1629,17 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
             }
         }
     }
+    // (slot 64 c + l is lane l's entry c: the loops over slots run c-major
+    // with c a compile-time index, so no register array is indexed at run time)
     if (a.renorm) {
         // gate_sum over the slots in slot order; divide when > 0
-        float sum = __shfl(g[0], 0);
-        for (int j = 1; j < a.kt; ++j) sum = sum + __shfl(wide_pick(g, j >> 6), j & 63);
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kWideEnt; ++c)
+            for (int l = 0; l < 64 && 64 * c + l < a.kt; ++l) {
+                const float v = __shfl(g[c], l);
+                sum = (c == 0 && l == 0) ? v : sum + v;
+            }
         if (sum > 0.0f) {
 #pragma unroll
             for (int c = 0; c < kWideEnt; ++c) g[c] = g[c] / sum;
@@ -1665,16 +1662,18 @@ __device__ __forceinline__ void permute_wide_token(const PermuteArgs &a, int t, 
         }
     }
     if (!a.copy_rows) return;
-    for (int j = 0; j < a.kt; ++j) {
-        const int p = __shfl(wide_pick(row, j >> 6), j & 63);
-        if (p < 0) continue;
-        for (int d = lane; d < a.D; d += 64) {
-            const float v = a.x_bf16 ? bf16_to_f32(((const uint16_t *)a.x)[(long long)t * a.D + d])
-                                     : ((const float *)a.x)[(long long)t * a.D + d];
-            if (a.ct == CT_BF16) ((uint16_t *)a.xp)[xp_index(a, p, d)] = f32_to_bf16(v);
-            else ((float *)a.xp)[(long long)p * a.ld_xp + d] = v;
+#pragma unroll
+    for (int c = 0; c < kWideEnt; ++c)
+        for (int l = 0; l < 64 && 64 * c + l < a.kt; ++l) {
+            const int p = __shfl(row[c], l);
+            if (p < 0) continue;
+            for (int d = lane; d < a.D; d += 64) {
+                const float v = a.x_bf16 ? bf16_to_f32(((const uint16_t *)a.x)[(long long)t * a.D + d])
+                                         : ((const float *)a.x)[(long long)t * a.D + d];
+                if (a.ct == CT_BF16) ((uint16_t *)a.xp)[xp_index(a, p, d)] = f32_to_bf16(v);
+                else ((float *)a.xp)[(long long)p * a.ld_xp + d] = v;
+            }
         }
-    }
 }
 
 __global__ __launch_bounds__(kPermThreads) void permute_wide_kernel(PermuteArgs a) {

@@ -468,8 +468,9 @@ def test_mixtral_shape_scaled(moe, oracle):
 ])
 def test_256_row_tiles(moe, oracle, E, k, etype, act, wdtype):
     # at most 16 experts averaging >= 384 rows: the 256-row tile kernels (one
-    # workgroup per CU); a skewed router bias gives partial last tiles, and
-    # D = 320 leaves y rows past the last 256-column block (cut at N)
+    # workgroup per CU; standard experts with fp8 weights stay on 128-row
+    # tiles); a skewed router bias gives partial last tiles, and D = 320
+    # leaves y rows past the last 256-column block (cut at N)
     rng = np.random.default_rng(70 + E)
     bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
     c = Case(moe, oracle, T=1600, D=320, H=384, E=E, k=k, gate="switch" if k == 1 else "topk", expert_type=etype,
