@@ -277,15 +277,18 @@ def test_shared_experts_python_api(moe, oracle):
     layer.close()
 
 
-@pytest.mark.parametrize("freq,use_comp,drop,wdtype", [(1, True, False, "f32"), (2, False, True, "bf16")])
-def test_aux_free_loss_layer(moe, oracle, freq, use_comp, drop, wdtype):
+@pytest.mark.parametrize("freq,use_comp,drop,wdtype,E,k", [
+    (1, True, False, "f32", 8, 2), (2, False, True, "bf16", 8, 2),
+    (1, True, False, "bf16", 24, 10),   # more than 8 slots: 32-token route blocks in both gating passes
+    (1, False, True, "bf16", 300, 6),   # over 256 router rows: 16-token route blocks
+])
+def test_aux_free_loss_layer(moe, oracle, freq, use_comp, drop, wdtype, E, k):
     # AuxiliaryFreeLoss as the balance loss: gating on logits + bias, the bias
     # state after every call bit-exact against the oracle's update_bias!
     # restatement, inference calls leave it alone
     rng = np.random.default_rng(50 + freq)
-    E = 8
-    c = Case(moe, oracle, T=600, D=128, H=192, E=E, k=2, wdtype=wdtype, xdtype=wdtype, seed=50 + freq, drop=drop,
-             cf=1.0)
+    c = Case(moe, oracle, T=600, D=128, H=192 if E <= 64 else 64, E=E, k=k, wdtype=wdtype, xdtype=wdtype,
+             seed=50 + freq + E, drop=drop, cf=1.0)
     lossfn = moe.AuxiliaryFreeLoss(E, learning_rate=0.05, update_freq=freq, use_complementary_loss=use_comp)
     lossfn.bias = (rng.standard_normal(E) * 0.5).astype(np.float32)
     st = dict(bias=lossfn.bias.copy(), mom=np.zeros(E, np.float32), lr=0.05, momentum=0.9, update_freq=freq,
@@ -294,7 +297,7 @@ def test_aux_free_loss_layer(moe, oracle, freq, use_comp, drop, wdtype):
         c.dev.set_aux_free(lossfn)
         out, loss, res = c.run(training)
         c.dev.get_aux_free(lossfn)
-        ref_out, ref_loss, aux = oracle.moe_forward(c.x, c.wr, c.ex, k=2, training=training, drop_tokens=drop,
+        ref_out, ref_loss, aux = oracle.moe_forward(c.x, c.wr, c.ex, k=k, training=training, drop_tokens=drop,
                                                     capacity_factor=1.0, z_weight=c.z, logits=res["logits"],
                                                     aux_free=st)
         assert np.array_equal(res["indices"], aux["idx"]), step
@@ -567,6 +570,7 @@ def test_shared_experts_more_than_8_slots(moe, oracle, gate, lsh, k, ns, E, para
     (512, 1, "switch", 0, 0, "bf16", 1200),  # MOE_MAX_EXPERTS: 16-token route blocks, 64 experts per lane
     (160, 3, "topk", 0, 0, "f32", 500),      # fp32 x: the six-term logits GEMM over 10 tiles
     (385, 8, "topk", 0, 1, "bf16", 800),     # 384 routed + 1 shared expert of the layer
+    (300, 4, "topk", 0, 0, "f32", 400),      # fp32 x over 256 router rows: 16-token route blocks
 ])
 def test_over_128_experts(moe, oracle, E, k, gate, ns, lsh, wdtype, T):
     # more experts than a 128-row router: the logits GEMM in column groups of

@@ -75,9 +75,12 @@ def test_router_noise(moe, oracle, E, k):
     assert np.array_equal(res4["logits"], clean)
 
 
-@pytest.mark.parametrize("E", [4, 8, 24, 100, 200])
-def test_router_noise_network(moe, oracle, E):
-    case = Case(moe, oracle, T=2048, D=128, H=64, E=E, k=2, seed=22)
+@pytest.mark.parametrize("E,xdtype", [(4, "f32"), (8, "f32"), (24, "f32"), (100, "f32"), (200, "f32"),
+                                      (150, "bf16")])
+def test_router_noise_network(moe, oracle, E, xdtype):
+    # (100: 200 GEMM columns, 32-token route blocks; 150 and 200: over 256
+    # columns, 16-token route blocks, on bf16 and fp32 x)
+    case = Case(moe, oracle, T=2048, D=128, H=64, E=E, k=2, seed=22, xdtype=xdtype)
     scale = 0.3
     wn = (np.random.default_rng(5).standard_normal((E, case.D)) / np.sqrt(case.D)).astype(np.float32)
     case.dev.set_router_noise(scale, np.ascontiguousarray(wn.T), seed=99)
