@@ -108,7 +108,7 @@ class Case:
         return self.oracle.moe_forward(self.x[:T], self.wr, self.ex, gate=self.gate, k=self.k, num_shared=self.ns,
                                        expert_type=self.expert_type, act=self.act, alpha=self.alpha,
                                        z_weight=self.z, training=training, drop_tokens=self.drop,
-                                       capacity_factor=self.cf, logits=logits)
+                                       capacity_factor=self.cf, logits=logits, gate_param=self.gate_param)
 
 
 def check_case(case, tol, training=True, T=None):
@@ -778,6 +778,37 @@ def test_random_layer_shapes(moe, oracle):
                  expert_type=etype, act=act, wdtype=wdtype, xdtype="bf16", seed=900 + case, router_bias=bias)
         try:
             check_case(c, TOL[wdtype])
+        finally:
+            c.dev.close()
+
+
+def test_random_wide_layers(moe, oracle):
+    # seeded layers over the wide ranges: 9..512 experts, up to 16 slots per
+    # token, every device gate, the layer's shared experts, fp32 / bf16 / fp8
+    # weights, capacity drop; routing bit-exact, output within tolerance
+    rng = np.random.default_rng(4243)
+    for case in range(12):
+        E = int(rng.choice([9, 24, 70, 129, 200, 300, 512]))
+        gate = str(rng.choice(["topk", "shared", "soft", "switch"]))
+        lsh = int(rng.integers(0, 3)) if case % 3 == 0 else 0
+        Er = E - lsh
+        ns = int(rng.integers(1, 4)) if gate == "shared" else 0
+        kmax = min(16 - lsh - ns, Er - ns)
+        k = 1 if gate == "switch" else (kmax if case % 4 == 2 else int(rng.integers(1, kmax + 1)))
+        wdtype = str(rng.choice(["f32", "bf16", "fp8"]))
+        T = int(rng.integers(40, 900))
+        drop = bool(rng.random() < 0.4) and lsh == 0
+        param = float(rng.choice([0.6, 1.0, 1.7])) if gate == "soft" else None
+        bias = (rng.standard_normal(Er) * 0.5).astype(np.float32) if lsh == 0 else None
+        print(f"wide case {case}: E={E} gate={gate} k={k} ns={ns} lsh={lsh} w={wdtype} T={T} drop={drop}", flush=True)
+        c = Case(moe, oracle, T=T, D=64, H=64, E=E, k=k, gate=gate, ns=ns, wdtype=wdtype,
+                 xdtype="f32" if wdtype == "f32" else "bf16", seed=4242 + case, router_bias=bias, lsh=lsh,
+                 drop=drop, cf=1.0, gate_param=param)
+        try:
+            if lsh:
+                check_shared_experts_case(c, TOL[wdtype], training=True)
+            else:
+                check_case(c, TOL[wdtype], training=bool(case % 2 == 0))
         finally:
             c.dev.close()
 
