@@ -1,4 +1,5 @@
-"""CPU check of the Julia binding in INTEGRATION.md against the C header.
+"""CPU check of the Julia binding a maintainer adds (the ```julia block of the
+integration guide at the repository root, DOC) against the C header.
 
 Every ``ccall((:moe_..., LIB), Ret, (ArgTypes...), args...)`` in the Julia
 block must name a function include/moe_mi355x.h declares, with the same
@@ -72,7 +73,7 @@ def _match(s, i):
 def julia_block():
     text = open(DOC).read()
     m = re.search(r"```julia\n(.*?)```", text, flags=re.S)
-    assert m, "no Julia block in INTEGRATION.md"
+    assert m, "no Julia block in the integration guide"
     return m.group(1)
 
 
@@ -156,7 +157,7 @@ def test_ccall_matches_header(call):
 def test_every_entry_point_has_a_binding():
     bound = {c[0] for c in julia_ccalls()}
     missing = sorted(set(header_decls()) - bound)
-    assert not missing, f"no ccall in INTEGRATION.md for {missing}"
+    assert not missing, f"no ccall in the integration guide for {missing}"
 
 
 @pytest.mark.parametrize("jname,cname", [("MoeConfigC", "moe_config"), ("MoeForwardAux", "moe_forward_aux")])
