@@ -46,6 +46,24 @@ CASES = [
     # shared gates 1/4 = 0.25
     dict(name="shared_2_plus_top2", logits=[[9.0, 9.0, 0.0, 4.0, 4.0, 1.0]], k=2, num_shared=2,
          indices=[[1, 2, 4, 5]], gates=[[0.25, 0.25, 0.25, 0.25]]),
+    # 256 equal logits: p = exp(0)/256 = 2^-8 exactly; the first 16 experts;
+    # their sum 16 * 2^-8 = 2^-4 is exact, so every gate is 2^-8 / 2^-4 = 1/16
+    dict(name="all_equal_E256_k16", logits=[[0.0] * 256], k=16, indices=[list(range(1, 17))],
+         gates=[[0.0625] * 16], probs=[[0.00390625] * 256]),
+    # 512 equal logits: p = 2^-9; the first 9 experts; the partial sums j * 2^-9
+    # are exact, so a gate is 2^-9 / (9 * 2^-9) = Float32(1/9) (one rounding)
+    dict(name="all_equal_E512_k9", logits=[[0.0] * 512], k=9, indices=[list(range(1, 10))],
+         gates=[[0.1111111119389534] * 9]),
+    # 300 strictly increasing logits 0, 1, ..., 299: the top 16 are experts
+    # 300, 299, ..., 285 in that order
+    dict(name="descending_pick_E300_k16", logits=[[float(i) for i in range(300)]], k=16,
+         indices=[list(range(300, 284, -1))]),
+    # SharedExpertGating(1, TopKGating(8), 257) on equal routed logits: the
+    # routed rows 2..257 all have p = 2^-8, the first 8 of them (ids 2..9) with
+    # gate 1/8 exactly, times 1 - 1/9 in Float64 = Float32(1/9); the shared
+    # expert's gate 1.0f0 / 9 = Float32(1/9) as well
+    dict(name="shared_1_plus_top8_E257", logits=[[5.0] + [0.0] * 256], k=8, num_shared=1,
+         indices=[list(range(1, 10))], gates=[[0.1111111119389534] * 9]),
     # several tokens at once, each its own case
     dict(name="multi_token", logits=[[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 1.0], [1.0, 1.0, 1.0]], k=1,
          indices=[[1], [2], [3], [1]], gates=[[1.0], [1.0], [1.0], [1.0]]),
