@@ -14,7 +14,8 @@ import numpy as np
 from . import _lib
 from ._device import DeviceLayer
 from .activations import activation_code, gelu
-from .balancing import AuxiliaryFreeLoss, LoadBalancingLoss, SwitchTransformerLoss, balance_alpha, update_bias
+from .balancing import (AuxiliaryFreeLoss, LoadBalancingLoss, NoBalancingLoss, SwitchTransformerLoss, balance_alpha,
+                        update_bias)
 from .experts import GatedExpert, StandardExpert
 from .gating import HOST_ROUTED_GATES, GatingMechanism, TopKGating, gate_spec
 
@@ -190,6 +191,8 @@ class MoELayer:
         T = xa.shape[1]
         if T > self.config.max_tokens:
             raise _lib.MoeError(_lib.MOE_EINVAL, f"batch of {T} tokens exceeds max_tokens={self.config.max_tokens}")
+        if T == 0:
+            return self._forward_empty(training, return_stats)
         if x_dtype == "bf16":
             xt = np.ascontiguousarray(xa.T, dtype=np.uint16)
             xcode = _lib.MOE_BF16
@@ -220,6 +223,38 @@ class MoELayer:
             self.training_stats["routing_entropy"].append(np.float32(res["mean_entropy"]))
         output = out.T
         loss = np.float32(loss)
+        if return_stats:
+            return output, loss, self.training_stats
+        return output, loss
+
+
+    def _forward_empty(self, training, return_stats):
+        """A batch of no tokens, x of shape (input_dim, 0): what the reference's
+        forward computes on empty arrays (src/core/moe_layer.jl:107-185), with
+        no device work.  The output is (output_dim, 0).  The loss is 0 in
+        inference.  In training it is the balance loss over no entries: the
+        Switch loss divides zero counts by zero assignments (NaN,
+        losses.jl:15-36); NoBalancingLoss gives 0; AuxiliaryFreeLoss counts
+        the call in update_bias! and leaves the bias alone (no assignments,
+        auxiliary_free.jl:36-55), then gives 0, or NaN with the complementary
+        Switch term (:73-83).  A positive z_loss_weight adds the z-loss, a
+        mean over no tokens (NaN, losses.jl:103-109).  forward_standard's
+        statistics gain no counts and a NaN mean entropy (:250-264)."""
+        c = self.config
+        balance_alpha(self.balance_loss)  # a loss with no device path raises as in a non-empty call
+        loss = np.float32(0.0)
+        if training:
+            bl = self.balance_loss
+            if isinstance(bl, AuxiliaryFreeLoss):
+                bl.update_counter += 1
+                loss = np.float32(np.nan) if bl.use_complementary_loss else np.float32(0.0)
+            elif not isinstance(bl, NoBalancingLoss):
+                loss = np.float32(np.nan)
+            if c.z_loss_weight > 0:
+                loss = np.float32(np.nan)
+        if c.num_shared_experts == 0:
+            self.training_stats["routing_entropy"].append(np.float32(np.nan))
+        output = np.zeros((c.output_dim, 0), dtype=np.float32)
         if return_stats:
             return output, loss, self.training_stats
         return output, loss

@@ -150,6 +150,45 @@ def test_host_mirror_rejects_unsupported_before_device(moe):
         moe.activations.activation_code(lambda v: v)
 
 
+def test_layer_empty_batch(moe):
+    # x of shape (input_dim, 0): the reference's forward on empty arrays
+    # (src/core/moe_layer.jl:107-185) -- an empty output, loss 0 in inference;
+    # in training the Switch loss's 0 / 0 and the z-loss's mean over no tokens
+    # are NaN.  No device work: the layer never builds its handle.
+    def layer(**kw):
+        cfg = dict(num_experts=4, expert_type="gated", input_dim=16, hidden_dim=32, output_dim=8,
+                   activation=moe.silu, gate_type=moe.TopKGating(2))
+        cfg.update(kw)
+        return moe.MoELayer(moe.MoEConfig(**cfg), rng=np.random.default_rng(0))
+
+    x = np.zeros((16, 0), np.float32)
+    lay = layer()
+    out, loss = lay(x)
+    assert out.shape == (8, 0) and out.dtype == np.float32 and loss == np.float32(0.0)
+    out, loss, stats = lay(x, training=True, return_stats=True)
+    assert out.shape == (8, 0) and np.isnan(loss)
+    assert stats["tokens_per_expert"].sum() == 0
+    assert len(stats["routing_entropy"]) == 2 and all(np.isnan(v) for v in stats["routing_entropy"])
+    assert lay._dev is None
+    # no balance loss and no z-loss: 0; the z-loss alone: NaN
+    assert layer(balance_loss=moe.NoBalancingLoss(), z_loss_weight=0.0)(x, training=True)[1] == np.float32(0.0)
+    assert np.isnan(layer(balance_loss=moe.NoBalancingLoss(), z_loss_weight=0.001)(x, training=True)[1])
+    # AuxiliaryFreeLoss: update_bias! counts the call, the bias stays (no assignments)
+    aux = moe.AuxiliaryFreeLoss(4, bias_init=0.25, use_complementary_loss=False)
+    lay = layer(balance_loss=aux, z_loss_weight=0.0)
+    assert lay(x, training=True)[1] == np.float32(0.0) and aux.update_counter == 1
+    assert np.array_equal(aux.bias, np.full(4, 0.25, np.float32)) and not aux.bias_momentum.any()
+    assert lay(x)[1] == np.float32(0.0) and aux.update_counter == 1  # inference: no compute_loss
+    aux_c = moe.AuxiliaryFreeLoss(4, use_complementary_loss=True)
+    assert np.isnan(layer(balance_loss=aux_c, z_loss_weight=0.0)(x, training=True)[1])
+    # forward_with_shared_experts updates no statistics
+    lay = layer(num_shared_experts=1)
+    out, loss, stats = lay(x, training=True, return_stats=True)
+    assert out.shape == (8, 0) and np.isnan(loss) and stats["routing_entropy"] == []
+    with pytest.raises(moe.MoeError):
+        lay(np.zeros((15, 0), np.float32))
+
+
 def test_gate_spec_mapping(moe):
     from mixtureofexperts_amd import _lib
 
