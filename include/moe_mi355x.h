@@ -267,7 +267,7 @@ int moe_route_from_logits(moe_handle *h, const float *logits, int32_t T, int32_t
  * balance loss over the E - ns router probabilities with the gate's shifted
  * ids (ids above E - ns are not counted, src/balancing/losses.jl:22-26; an
  * ExpertChoiceGating matrix's empty entries become id ns and are counted
- * when ns <= E - ns). */
+ * when ns <= E - ns).  1 <= T <= max_tokens, else MOE_EINVAL. */
 int moe_forward(moe_handle *h, const void *x, int32_t x_dtype, int32_t T, int32_t training,
                 float *out, float *loss, moe_forward_aux *aux);
 
